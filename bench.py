@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X hot path for sile's tile kernels, on one GPU.
+
+Measures the BASELINE metric: bf16 GEMM and causal flash-attention forward in
+TFLOP/s (fraction of MI355X dense MFMA peak) and fp16 row softmax in GB/s
+(fraction of HBM peak).  All inputs are synthetic, drawn from the seeded
+recipes of the configurations, and resident in HBM before timing starts.
+
+The JSON line's `value` is the bf16 GEMM M=N=K=8192 throughput (the metric's
+first quantity and the workload named in `config.workload`); every other
+measured kernel is listed under `components` with its own roofline.  A step is
+one launch of the kernel; per-launch durations come from HIP events recorded
+on the launch stream around each launch, and the K timed steps are bracketed
+by a device synchronisation on both sides.
+
+`cpu_baseline` times the CPU oracle (a restatement of sile's CPU backend loop
+nest, compiled like the reference's generated C) on a bounded sample of the
+same GEMM workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
+                       [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from sile_amd import _abi as hip  # noqa: E402
+
+METRIC = ("bf16 GEMM & flash-attn fwd TFLOP/s (% MI355X MFMA peak), softmax GB/s, 1 GPU")
+
+# Published MI355X peaks (dense): bf16/fp16 MFMA 2.5 PFLOP/s, fp8 5.0 PFLOP/s, HBM3E 8 TB/s.
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0}
+PEAK_HBM_GBS = 8000.0
+
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- input recipes
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits with round-to-nearest-even (numpy, no oracle)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+def normal(seed, shape, scale=1.0):
+    g = np.random.default_rng(seed)
+    out = np.empty(shape, np.float32)
+    flat = out.reshape(-1)
+    step = 1 << 24
+    for i in range(0, flat.size, step):
+        flat[i:i + step] = g.standard_normal(min(step, flat.size - i), dtype=np.float32)
+    if scale != 1.0:
+        out *= np.float32(scale)
+    return out
+
+
+# ---------------------------------------------------------------- timing
+
+def time_launches(launch, steps, warmup, stream, rotate=1):
+    """Runs `launch(i)` warmup + steps times; returns per-launch event times (ms)
+    of the timed steps and the wall time of the timed region (s)."""
+    for i in range(warmup):
+        launch(i % rotate)
+    hip.synchronize()
+    evs = [(hip.Event(), hip.Event()) for _ in range(steps)]
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record(stream)
+        launch(i % rotate)
+        evs[i][1].record(stream)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    ms = [a.elapsed_ms(b) for a, b in evs]
+    for a, b in evs:
+        a.close()
+        b.close()
+    return np.array(ms), wall
+
+
+def load_traffic():
+    if os.path.exists(PROFILE_TRAFFIC):
+        with open(PROFILE_TRAFFIC) as f:
+            return json.load(f)
+    return {}
+
+
+def roofline_obj(bound, achieved, peak, unit, traffic):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------- workloads
+
+def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
+    m = n = k = size
+    log(f"[bench] {name}: generating inputs")
+    if kind == "fp8":
+        from oracle import cpuref  # quantisation recipe only (inputs), not measured
+        a = normal(9, (m, k))
+        b = normal(10, (n, k))
+        sa = float(np.float32(np.abs(a).max() / 448.0))
+        sb = float(np.float32(np.abs(b).max() / 448.0))
+        a_bits, b_bits = cpuref.e4m3_encode(a, sa), cpuref.e4m3_encode(b, sb)
+        t, c_t = hip.F8E4M3, hip.BF16
+    else:
+        a_bits = bf16_bits(normal(4, (m, k), 1 / np.sqrt(k)))
+        b_bits = bf16_bits(normal(5, (n, k), 1 / np.sqrt(k)))
+        sa = sb = 1.0
+        t, c_t = hip.BF16, hip.BF16
+    da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
+    del a_bits, b_bits
+    dc = hip.DeviceBuffer(m * n * 2)
+
+    def launch(_):
+        hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+                 dc.ptr, n, sa, sb, 0, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    ms, wall = time_launches(launch, steps, warmup, stream)
+    flop = 2.0 * m * n * k
+    med = float(np.median(ms))
+    tflops = flop / (med * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[kind]
+    res = {
+        "name": name, "value": round(tflops, 2), "unit": "TFLOP/s", "ms_median": round(med, 4),
+        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "flop": flop,
+        "roofline": roofline_obj("mfma", tflops, peak, "TFLOP/s", traffic.get(name)),
+    }
+    for buf in (da, db, dc):
+        buf.close()
+    return res
+
+
+def bench_attention(name, s, steps, warmup, stream, traffic):
+    b, h, d = 4, 32, 128
+    log(f"[bench] {name}: generating inputs")
+    bufs = []
+    for seed in (6, 7, 8):
+        x = normal(seed, (b, h, s, d)).astype(np.float16)
+        bufs.append(hip.DeviceBuffer.from_array(x.view(np.uint16)))
+        del x
+    do = hip.DeviceBuffer(b * h * s * d * 2)
+    scale = 1.0 / np.sqrt(d)
+
+    def launch(_):
+        hip.flash_attn_fwd(hip.F16, b, h, s, d, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, do.ptr,
+                           scale, True, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    ms, wall = time_launches(launch, steps, warmup, stream)
+    # unmasked (query, key) pairs only: 2 GEMMs x 2 flop x D per pair
+    flop = 4.0 * d * b * h * s * (s + 1) / 2
+    med = float(np.median(ms))
+    tflops = flop / (med * 1e-3) / 1e12
+    res = {
+        "name": name, "value": round(tflops, 2), "unit": "TFLOP/s", "ms_median": round(med, 4),
+        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "flop": flop,
+        "flop_convention": "4*D*B*H*S*(S+1)/2 (causal pairs only)",
+        "roofline": roofline_obj("mfma", tflops, PEAK_TFLOPS["f16"], "TFLOP/s", traffic.get(name)),
+    }
+    for buf in bufs + [do]:
+        buf.close()
+    return res
+
+
+def bench_softmax(name, steps, warmup, stream, traffic):
+    rows = cols = 8192
+    log(f"[bench] {name}: generating inputs")
+    x = normal(3, (rows, cols), 2.0).astype(np.float16)
+    # 4 input/output pairs = 1 GiB, four times the 256 MiB Infinity Cache, so
+    # every timed launch reads its input from HBM
+    rotate = 4
+    xs = [hip.DeviceBuffer.from_array(x.view(np.uint16)) for _ in range(rotate)]
+    ys = [hip.DeviceBuffer(rows * cols * 2) for _ in range(rotate)]
+    del x
+
+    def launch(i):
+        hip.softmax_rows(hip.F16, hip.F16, rows, cols, xs[i].ptr, cols, ys[i].ptr, cols, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    ms, wall = time_launches(launch, steps, warmup, stream, rotate=rotate)
+    nbytes = 4.0 * rows * cols  # read 2 B + write 2 B per element
+    med = float(np.median(ms))
+    gbs = nbytes / (med * 1e-3) / 1e9
+    res = {
+        "name": name, "value": round(gbs, 1), "unit": "GB/s", "ms_median": round(med, 4),
+        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "bytes": nbytes,
+        "roofline": roofline_obj("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic.get(name)),
+    }
+    for buf in xs + ys:
+        buf.close()
+    return res
+
+
+def cpu_baseline(budget_rows_step=8):
+    """CPU oracle on a deterministic sample of the bf16 GEMM 8192^3 workload:
+    every `budget_rows_step`-th 256-row tile of C (all 8192 columns, full K),
+    inputs up-cast from the same bf16 data."""
+    from oracle import cpuref
+
+    m = n = k = 8192
+    log("[bench] cpu baseline: generating inputs")
+    a = cpuref.f32_from_bf16(bf16_bits(normal(4, (m, k), 1 / np.sqrt(k))))
+    b = cpuref.f32_from_bf16(bf16_bits(normal(5, (n, k), 1 / np.sqrt(k))))
+    c = np.zeros((m, n), np.float32)
+    tiles = (m // 256 + budget_rows_step - 1) // budget_rows_step
+    rows = tiles * 256
+    log(f"[bench] cpu baseline: {rows} rows x {n} cols x {k} k on {cpuref.num_threads()} threads")
+    t0 = time.perf_counter()
+    cpuref.gemm_nt(a, b, bm=256, row_tile_step=budget_rows_step, out=c)
+    dt = time.perf_counter() - t0
+    flop = 2.0 * rows * n * k
+    return {
+        "value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cpuref.num_threads(),
+        "kind": "port",
+        "sample": (f"bf16 GEMM 8192^3 on up-cast fp32 inputs, every {budget_rows_step}th "
+                   f"256-row tile of C ({rows} of {m} rows, all columns, full K): {flop:.3e} "
+                   f"flop in {dt:.2f} s; oracle = canonical-matmul loop nest, gcc -O2 -fopenmp"),
+        "seconds": round(dt, 3),
+    }
+
+
+ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
+       "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", nargs="*", default=None, choices=ALL)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    hip.init(0)
+    info = hip.device_info(0)
+    log(f"[bench] device {info['name']} {info['gcn_arch']} CUs={info['compute_units']} "
+        f"clock={info['clock_khz'] / 1e3:.0f} MHz")
+    stream = hip.Stream()
+    traffic = load_traffic()
+    names = args.only or ALL
+    results = {}
+    for name in names:
+        if name.startswith("gemm_"):
+            kind = "fp8" if "fp8" in name else "bf16"
+            results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,
+                                       args.warmup, stream, traffic)
+        elif name.startswith("flash_attn"):
+            results[name] = bench_attention(name, int(name.split("_s")[-1]), args.steps,
+                                            args.warmup, stream, traffic)
+        else:
+            results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic)
+        r = results[name]
+        log(f"[bench] {name}: {r['value']} {r['unit']} ({r['ms_median']} ms, "
+            f"{100 * r['roofline']['frac']:.1f}% of peak)")
+
+    head = results.get("gemm_bf16_8192") or next(iter(results.values()))
+    cpu = None
+    if not args.no_cpu_baseline and head["name"] == "gemm_bf16_8192":
+        cpu = cpu_baseline()
+        log(f"[bench] cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_median"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if "bf16" in head["name"] else ("fp8" if "fp8" in head["name"] else "f16"),
+        "data": "synthetic (seeded recipes of BASELINE configs; inputs resident in HBM)",
+        "config": {
+            "workload": {
+                "gemm_bf16_8192": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 acc, bf16 out",
+            }.get(head["name"], head["name"]),
+            "parallelism": "single GPU",
+        },
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "components": {k: v for k, v in results.items()},
+        "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["compute_units"]},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,215 @@
+/*
+ * sile_hip.h -- C ABI of libsile_hip.so, the MI355X (gfx950) execution path
+ * for sile's tile kernels.
+ *
+ * Plain C: pointers, sizes and status codes only.  Every entry point returns
+ * an int status (SILE_OK = 0); on failure sile_hip_last_error() gives the
+ * message.  This is the surface a Rust `HipBackend` in crates/sile-backend
+ * binds through FFI, beside the CPU and Metal runtimes
+ * (crates/sile-backend/src/cpu/mod.rs:14-145, crates/sile-backend/src/metal/mod.rs:11-172).
+ *
+ * Device pointers are HBM addresses from sile_hip_malloc.  Streams are HIP
+ * streams (NULL = the device's default stream).  The sile_hip_kernel_* entry
+ * points keep the reference's apply() contract and return after the work has
+ * completed; the op entry points (sile_hip_gemm, sile_hip_softmax_rows,
+ * sile_hip_reduce_rows, sile_hip_flash_attn_fwd) only enqueue on the stream.
+ */
+#ifndef SILE_HIP_H
+#define SILE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1..5 map 1:1 onto sile_core::Error
+ * (crates/sile-core/src/error.rs:1-13); SILE_ERR_RUNTIME is a HIP runtime
+ * failure after validation (a Rust binding reports it as Error::Compile with
+ * the message, the variant the reference uses for backend failures,
+ * crates/sile-backend/src/cpu/mod.rs:86-102). */
+enum {
+  SILE_OK = 0,
+  SILE_ERR_INVALID_DEVICE = 1,      /* Error::InvalidDevice: bad ordinal / SILE_DEVICE value */
+  SILE_ERR_UNSUPPORTED_BACKEND = 2, /* Error::UnsupportedBackend: no GPU, unsupported dtype/layout */
+  SILE_ERR_COMPILE = 3,             /* Error::Compile: code object load or symbol lookup failed */
+  SILE_ERR_IO = 4,                  /* Error::Io */
+  SILE_ERR_SHAPE = 5,               /* Error::Shape: bad or non-divisible shape, grid not set */
+  SILE_ERR_RUNTIME = 6              /* HIP runtime error during copy / launch / sync */
+};
+
+/* Element types.  The reference knows only f32 (crates/sile-hir/src/types.rs:11-14,
+ * crates/sile-core/src/kernel.rs:8-14); the 16-bit and fp8 types are additive. */
+typedef enum {
+  SILE_F32 = 0,
+  SILE_F16 = 1,
+  SILE_BF16 = 2,
+  SILE_F8E4M3 = 3 /* OCP e4m3fn: finite, max 448 */
+} sile_dtype;
+
+/* Matrix layouts of sile_hip_gemm operands. */
+typedef enum {
+  SILE_ROW_MAJOR = 0, /* element (i, j) at p[i * ld + j] */
+  SILE_COL_MAJOR = 1  /* element (i, j) at p[j * ld + i] */
+} sile_layout;
+
+/* Row reduce ops: TileIrOp::ReduceMax / ReduceSum (crates/sile-tile-ir/src/ir.rs:128-262). */
+typedef enum { SILE_REDUCE_MAX = 0, SILE_REDUCE_SUM = 1 } sile_reduce_op;
+
+typedef void *sile_hip_stream;   /* hipStream_t */
+typedef void *sile_hip_event;    /* hipEvent_t */
+typedef void *sile_hip_module;   /* hipModule_t */
+typedef void *sile_hip_function; /* hipFunction_t */
+
+typedef struct {
+  char name[256];
+  char gcn_arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t clock_khz;       /* peak engine clock */
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width;
+  int64_t total_global_mem;
+  int64_t l2_cache_bytes;
+  int64_t lds_per_block;
+} sile_hip_device_props;
+
+/* ---- device ------------------------------------------------------------ */
+
+/* Selects device `ordinal` for this thread and loads the gfx950 code objects
+ * on it (hipModuleLoadData).  Replaces Device::default()/create_stream for the
+ * HIP arm (crates/sile-core/src/device.rs:15-50): no GPU -> UNSUPPORTED_BACKEND,
+ * bad ordinal -> INVALID_DEVICE, code object rejected -> COMPILE. */
+int sile_hip_init(int ordinal);
+int sile_hip_device_count(int *count);
+int sile_hip_device_info(int ordinal, sile_hip_device_props *out);
+int sile_hip_device_synchronize(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char *sile_hip_last_error(void);
+/* Library version string. */
+const char *sile_hip_version(void);
+
+/* ---- HBM memory (the reference only has host Vec<f32> tensors,
+ *      crates/sile/src/tensor.rs:27-132; these make them device-resident) -- */
+int sile_hip_malloc(void **ptr, size_t bytes);
+int sile_hip_free(void *ptr);
+int sile_hip_memcpy_htod(void *dst, const void *src, size_t bytes);
+int sile_hip_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int sile_hip_memcpy_dtod(void *dst, const void *src, size_t bytes);
+int sile_hip_memset(void *dst, int value, size_t bytes);
+
+/* ---- streams and events (Stream is a device tag with a no-op synchronize in
+ *      the reference, crates/sile-core/src/stream.rs:3-20) ----------------- */
+int sile_hip_stream_create(sile_hip_stream *out);
+int sile_hip_stream_destroy(sile_hip_stream stream);
+int sile_hip_stream_synchronize(sile_hip_stream stream);
+int sile_hip_event_create(sile_hip_event *out);
+int sile_hip_event_destroy(sile_hip_event event);
+int sile_hip_event_record(sile_hip_event event, sile_hip_stream stream);
+int sile_hip_event_synchronize(sile_hip_event event);
+int sile_hip_event_elapsed_ms(float *ms, sile_hip_event start, sile_hip_event stop);
+
+/* ---- code objects and the generic tile launch --------------------------- */
+
+/* Loads a gfx950 code object (ELF) image: hipModuleLoadData.  Replaces the
+ * compile + dlopen step of CpuBackend::execute_compiled_source
+ * (crates/sile-backend/src/cpu/mod.rs:56-102); failure -> SILE_ERR_COMPILE. */
+int sile_hip_module_load(const void *image, size_t bytes, sile_hip_module *out);
+int sile_hip_module_unload(sile_hip_module module);
+/* hipModuleGetFunction; a missing symbol -> SILE_ERR_COMPILE (the reference's
+ * missing dlsym, crates/sile-backend/src/cpu/mod.rs:96-102). */
+int sile_hip_module_get(sile_hip_module module, const char *name, sile_hip_function *out);
+
+/* Launches `fn` with sile's kernel-wrapper convention
+ * (crates/sile-backend/src/cpu/codegen.rs:433-555, called as in
+ * crates/sile-backend/src/cpu/mod.rs:104-128): one workgroup of
+ * `threads_per_program` threads per program, grid[0]*grid[1]*grid[2]
+ * programs.  The kernel receives (void **buffers, int64_t num_programs,
+ * const int64_t *shapes, int64_t num_shapes) where `buffers` and `shapes` are
+ * device copies of the host arrays given here (buffers in kernel-param order,
+ * shapes = every arg's dims concatenated).  The kernel applies the
+ * `pid < total_tiles` guard itself.  Synchronous, like apply(). */
+int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t num_buffers,
+                          const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],
+                          uint32_t threads_per_program, sile_hip_stream stream);
+
+/* ---- the DSL kernels on the hot path, with the sile_kernel_<name> ABI ----
+ * Same arguments as the generated `void sile_kernel_<name>(void **buffers,
+ * int64_t num_threadgroups, int64_t threads_per_group, const int64_t *shapes,
+ * int64_t num_shapes)` (crates/sile-backend/src/cpu/codegen.rs:448-454), plus
+ * the kernel's const generics, plus a stream.  `buffers` holds DEVICE
+ * pointers; `shapes` is a HOST array.  num_threadgroups = grid.x*grid.y*grid.z;
+ * threads_per_group must be 1 (LLVM-IR mode, crates/sile-backend/src/cpu/mod.rs:109-120).
+ * Each program runs as one workgroup; programs with pid >= total_tiles do
+ * nothing.  Synchronous. */
+
+/* matmul<BM,BN,BK> of crates/sile/tests/backend_matmul.rs:3-19:
+ * buffers {a, b, c} f32; shapes = shape(a) ++ shape(b) ++ shape(c) (6 values).
+ * Bit-identical to the CPU backend (canonical matmul order,
+ * crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444). */
+int sile_hip_kernel_matmul(void *const *buffers, int64_t num_threadgroups,
+                           int64_t threads_per_group, const int64_t *shapes, int64_t num_shapes,
+                           int64_t bm, int64_t bn, int64_t bk, sile_hip_stream stream);
+
+/* softmax<BM,BN> of crates/sile/tests/backend_softmax.rs:3-15:
+ * buffers {x, y} f32; shapes = shape(x) ++ shape(y) (4 values). */
+int sile_hip_kernel_softmax(void *const *buffers, int64_t num_threadgroups,
+                            int64_t threads_per_group, const int64_t *shapes, int64_t num_shapes,
+                            int64_t bm, int64_t bn, sile_hip_stream stream);
+
+/* parallel_reduce<TILE> of crates/sile/examples/parallel_reduce.rs:3-9
+ * (test crates/sile/tests/backend_parallel_reduce.rs:3-9): buffers {a, out} f32;
+ * shapes = shape(a) ++ shape(out) (2 values).  out[0] += tile sums atomically.
+ * `partials` (device, may be NULL) receives each program's tile sum. */
+int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgroups,
+                                    int64_t threads_per_group, const int64_t *shapes,
+                                    int64_t num_shapes, int64_t tile, float *partials,
+                                    sile_hip_stream stream);
+
+/* ---- op entry points (asynchronous on `stream`) ------------------------- */
+
+/* C[M,N] = (scale_a * scale_b) * A . B, fp32 accumulation; the tile op MmaF of
+ * the canonical matmul (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444,
+ * crates/sile-tile-ir/src/ir.rs:128-262).  k runs over K' = (K / bk) * bk
+ * (bk <= 0: K' = K), the reference's K truncation.
+ * Supported:
+ *   f32  x f32  -> f32 : any shape/layout of B, A row-major; exact canonical order
+ *                        (bit-identical to the CPU backend).
+ *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
+ *                        A row-major, B column-major, M and N multiples of 256,
+ *                        K' a multiple of 64 (16-bit) or 128 (fp8), leading
+ *                        dimensions multiples of 16 bytes; MFMA path.
+ * Anything else -> SILE_ERR_UNSUPPORTED_BACKEND or SILE_ERR_SHAPE. */
+int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
+                  int64_t k, const void *a, int64_t lda, sile_layout a_layout, const void *b,
+                  int64_t ldb, sile_layout b_layout, void *c, int64_t ldc, float scale_a,
+                  float scale_b, int64_t bk, sile_hip_stream stream);
+
+/* Row softmax of a [rows, cols] matrix: y = exp(x - max) / sum(exp(x - max))
+ * per row with fp32 max/exp/sum (the softmax DSL kernel with BN = cols,
+ * crates/sile/tests/backend_softmax.rs:3-15).  in/out dtypes: f16->f16,
+ * bf16->bf16, f32->f32, f16->f32. */
+int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows, int64_t cols,
+                          const void *x, int64_t ldx, void *y, int64_t ldy,
+                          sile_hip_stream stream);
+
+/* out[r] = max_c x[r][c] or sum_c x[r][c] in fp32 (ReduceMax/ReduceSum along
+ * axis 1, crates/sile-tile-ir/src/passes/lowering/tile_compute/reduce.rs:10-112).
+ * in: f32, f16, bf16.  `out` is fp32 [rows]. */
+int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, int64_t cols,
+                         const void *x, int64_t ldx, float *out, sile_hip_stream stream);
+
+/* Flash-attention forward, O = softmax(Q K^T * scale [+ causal mask]) V with
+ * fp32 online-softmax state.  Q, K, V, O are [B, H, S, D] contiguous, f16 or
+ * bf16; D = 128; S a multiple of 128.  No reference counterpart: sile's DSL
+ * cannot express attention (no mask/iota/transpose); built from the Tile IR
+ * ops MmaF, ReduceMax, Exp, ReduceSum (crates/sile-tile-ir/src/ir.rs:128-262). */
+int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                            int64_t head_dim, const void *q, const void *k, const void *v,
+                            void *o, float scale, int causal, sile_hip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SILE_HIP_H */

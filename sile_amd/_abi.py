@@ -1,0 +1,306 @@
+"""ctypes binding of libsile_hip.so (the C ABI declared in include/sile_hip.h).
+
+This is the Python caller of the drop-in boundary: tests, bench.py and the
+Python mirror of sile's launch API (sile_amd.api) go through it.  There is no
+fallback: if the library is missing, loading raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libsile_hip.so")
+
+# Status codes (include/sile_hip.h) and the sile_core::Error variant each maps
+# to (crates/sile-core/src/error.rs:1-13).
+SILE_OK = 0
+STATUS_NAMES = {
+    1: "InvalidDevice",
+    2: "UnsupportedBackend",
+    3: "Compile",
+    4: "Io",
+    5: "Shape",
+    6: "Runtime",
+}
+
+F32, F16, BF16, F8E4M3 = 0, 1, 2, 3
+ROW_MAJOR, COL_MAJOR = 0, 1
+REDUCE_MAX, REDUCE_SUM = 0, 1
+
+_DTYPE_BYTES = {F32: 4, F16: 2, BF16: 2, F8E4M3: 1}
+
+
+class SileError(RuntimeError):
+    """A failed libsile_hip call: `kind` is the sile_core::Error variant name."""
+
+    def __init__(self, status: int, message: str, call: str):
+        self.status = status
+        self.kind = STATUS_NAMES.get(status, f"status{status}")
+        super().__init__(f"{call}: {self.kind}: {message}")
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+
+class DeviceProps(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("gcn_arch", ctypes.c_char * 64),
+        ("compute_units", ctypes.c_int32),
+        ("clock_khz", ctypes.c_int32),
+        ("memory_clock_khz", ctypes.c_int32),
+        ("memory_bus_width", ctypes.c_int32),
+        ("total_global_mem", ctypes.c_int64),
+        ("l2_cache_bytes", ctypes.c_int64),
+        ("lds_per_block", ctypes.c_int64),
+    ]
+
+
+# name -> argtypes (every function returns int status unless listed in _RESTYPE)
+SIGNATURES = {
+    "sile_hip_init": [_I32],
+    "sile_hip_device_count": [ctypes.POINTER(_I32)],
+    "sile_hip_device_info": [_I32, ctypes.POINTER(DeviceProps)],
+    "sile_hip_device_synchronize": [],
+    "sile_hip_last_error": [],
+    "sile_hip_version": [],
+    "sile_hip_malloc": [ctypes.POINTER(_P), _SZ],
+    "sile_hip_free": [_P],
+    "sile_hip_memcpy_htod": [_P, _P, _SZ],
+    "sile_hip_memcpy_dtoh": [_P, _P, _SZ],
+    "sile_hip_memcpy_dtod": [_P, _P, _SZ],
+    "sile_hip_memset": [_P, _I32, _SZ],
+    "sile_hip_stream_create": [ctypes.POINTER(_P)],
+    "sile_hip_stream_destroy": [_P],
+    "sile_hip_stream_synchronize": [_P],
+    "sile_hip_event_create": [ctypes.POINTER(_P)],
+    "sile_hip_event_destroy": [_P],
+    "sile_hip_event_record": [_P, _P],
+    "sile_hip_event_synchronize": [_P],
+    "sile_hip_event_elapsed_ms": [ctypes.POINTER(_F32), _P, _P],
+    "sile_hip_module_load": [_P, _SZ, ctypes.POINTER(_P)],
+    "sile_hip_module_unload": [_P],
+    "sile_hip_module_get": [_P, ctypes.c_char_p, ctypes.POINTER(_P)],
+    "sile_hip_launch_tiles": [_P, _P, _I64, _P, _I64, _P, ctypes.c_uint32, _P],
+    "sile_hip_kernel_matmul": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "sile_hip_kernel_softmax": [_P, _I64, _I64, _P, _I64, _I64, _I64, _P],
+    "sile_hip_kernel_parallel_reduce": [_P, _I64, _I64, _P, _I64, _I64, _P, _P],
+    "sile_hip_gemm": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32, _P,
+                      _I64, _F32, _F32, _I64, _P],
+    "sile_hip_softmax_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _I64, _P],
+    "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
+    "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
+}
+_RESTYPE = {"sile_hip_last_error": ctypes.c_char_p, "sile_hip_version": ctypes.c_char_p}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libsile_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m sile_amd.build` "
+                "(the HIP path has no fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().sile_hip_last_error().decode()
+
+
+def call(name: str, *args) -> None:
+    """Calls a status-returning entry point; raises SileError on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != SILE_OK:
+        raise SileError(rc, last_error(), name)
+
+
+def status(name: str, *args) -> int:
+    """Calls an entry point and returns its raw status (for error-path tests)."""
+    return getattr(lib(), name)(*args)
+
+
+# ---------------------------------------------------------------------------
+# device, memory, streams, events
+# ---------------------------------------------------------------------------
+
+def init(ordinal: int = 0) -> None:
+    call("sile_hip_init", ordinal)
+
+
+def device_count() -> int:
+    n = _I32(0)
+    call("sile_hip_device_count", ctypes.byref(n))
+    return n.value
+
+
+def device_info(ordinal: int = 0) -> dict:
+    p = DeviceProps()
+    call("sile_hip_device_info", ordinal, ctypes.byref(p))
+    return {
+        "name": p.name.decode(), "gcn_arch": p.gcn_arch.decode(),
+        "compute_units": p.compute_units, "clock_khz": p.clock_khz,
+        "memory_clock_khz": p.memory_clock_khz, "memory_bus_width": p.memory_bus_width,
+        "total_global_mem": p.total_global_mem, "l2_cache_bytes": p.l2_cache_bytes,
+        "lds_per_block": p.lds_per_block,
+    }
+
+
+def synchronize() -> None:
+    call("sile_hip_device_synchronize")
+
+
+class DeviceBuffer:
+    """An HBM allocation from sile_hip_malloc, freed on close()/GC."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _P()
+        call("sile_hip_malloc", ctypes.byref(p), self.nbytes)
+        self.ptr = p.value or 0
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        call("sile_hip_memcpy_htod", self.ptr, arr.ctypes.data, arr.nbytes)
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        call("sile_hip_memcpy_dtoh", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def fill_bytes(self, value: int) -> None:
+        call("sile_hip_memset", self.ptr, value, self.nbytes)
+
+    def close(self) -> None:
+        if self.ptr and _lib is not None:
+            call("sile_hip_free", self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        p = _P()
+        call("sile_hip_stream_create", ctypes.byref(p))
+        self.handle = p.value
+
+    def synchronize(self) -> None:
+        call("sile_hip_stream_synchronize", self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            call("sile_hip_stream_destroy", self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        p = _P()
+        call("sile_hip_event_create", ctypes.byref(p))
+        self.handle = p.value
+
+    def record(self, stream: "Stream | None" = None) -> None:
+        call("sile_hip_event_record", self.handle, stream.handle if stream else None)
+
+    def synchronize(self) -> None:
+        call("sile_hip_event_synchronize", self.handle)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _F32(0.0)
+        call("sile_hip_event_elapsed_ms", ctypes.byref(ms), self.handle, end.handle)
+        return float(ms.value)
+
+    def close(self) -> None:
+        if self.handle:
+            call("sile_hip_event_destroy", self.handle)
+            self.handle = None
+
+
+def _sh(stream) -> "int | None":
+    return None if stream is None else stream.handle
+
+
+def _ptr_array(ptrs):
+    return (ctypes.c_void_p * len(ptrs))(*ptrs)
+
+
+def _i64_array(vals):
+    return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+# ---------------------------------------------------------------------------
+# DSL kernels with the sile_kernel_<name> ABI
+# ---------------------------------------------------------------------------
+
+def kernel_matmul(bufs, num_threadgroups, shapes, bm, bn, bk, stream=None, threads_per_group=1):
+    call("sile_hip_kernel_matmul", _ptr_array(bufs), num_threadgroups, threads_per_group,
+         _i64_array(shapes), len(shapes), bm, bn, bk, _sh(stream))
+
+
+def kernel_softmax(bufs, num_threadgroups, shapes, bm, bn, stream=None, threads_per_group=1):
+    call("sile_hip_kernel_softmax", _ptr_array(bufs), num_threadgroups, threads_per_group,
+         _i64_array(shapes), len(shapes), bm, bn, _sh(stream))
+
+
+def kernel_parallel_reduce(bufs, num_threadgroups, shapes, tile, partials=0, stream=None,
+                           threads_per_group=1):
+    call("sile_hip_kernel_parallel_reduce", _ptr_array(bufs), num_threadgroups,
+         threads_per_group, _i64_array(shapes), len(shapes), tile, partials or None, _sh(stream))
+
+
+# ---------------------------------------------------------------------------
+# op entry points (asynchronous on the stream)
+# ---------------------------------------------------------------------------
+
+def gemm(a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout, c, ldc,
+         scale_a=1.0, scale_b=1.0, bk=0, stream=None):
+    call("sile_hip_gemm", a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout,
+         c, ldc, scale_a, scale_b, bk, _sh(stream))
+
+
+def softmax_rows(in_type, out_type, rows, cols, x, ldx, y, ldy, stream=None):
+    call("sile_hip_softmax_rows", in_type, out_type, rows, cols, x, ldx, y, ldy, _sh(stream))
+
+
+def reduce_rows(op, in_type, rows, cols, x, ldx, out, stream=None):
+    call("sile_hip_reduce_rows", op, in_type, rows, cols, x, ldx, out, _sh(stream))
+
+
+def flash_attn_fwd(dtype, batch, heads, seq_len, head_dim, q, k, v, o, scale, causal=True,
+                   stream=None):
+    call("sile_hip_flash_attn_fwd", dtype, batch, heads, seq_len, head_dim, q, k, v, o, scale,
+         1 if causal else 0, _sh(stream))
+
+
+def dtype_bytes(t: int) -> int:
+    return _DTYPE_BYTES[t]

@@ -1,0 +1,105 @@
+// Device-side helpers shared by the gfx950 kernels of libsile_hip.
+//
+// Everything here is written for CDNA4 (gfx950, wave64): vector types for the
+// MFMA operands, round-to-nearest-even conversions to the 16-bit types, and
+// wave-wide all-reductions built from DPP row permutes plus one cross-row
+// exchange each for the 16- and 32-lane steps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SILE_DEV __device__ __forceinline__
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+namespace sile {
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+SILE_DEV uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+SILE_DEV float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+SILE_DEV uint16_t bf16_rne(float f) {
+  uint32_t u = f32_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+SILE_DEV float bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+// fp32 -> fp16 bits (hardware conversion, round to nearest even).
+SILE_DEV uint16_t f16_rne(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+SILE_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Packs two fp32 into one dword of two 16-bit values (lo in bits 0..15).
+SILE_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)bf16_rne(lo) | ((uint32_t)bf16_rne(hi) << 16);
+}
+SILE_DEV uint32_t pack_f16x2(float lo, float hi) {
+  f16x2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ---- wave-wide all-reductions (DPP within 16-lane rows, then 2 exchanges) ----
+template <int kCtrl>
+SILE_DEV float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+// DPP controls: quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1] (xor 2),
+// row_half_mirror (lane i <-> 7-i in each 8), row_mirror (i <-> 15-i in each 16).
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// ds_swizzle bit mode: and_mask 0x1f, xor_mask 0x10 -> lane ^ 16 within 32.
+SILE_DEV float swizzle_xor16(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+SILE_DEV float xor32(float v) {
+  return __builtin_bit_cast(float, __shfl_xor(__builtin_bit_cast(int, v), 32));
+}
+
+SILE_DEV float fmax_ordered(float a, float b) { return (b > a) ? b : a; }
+
+SILE_DEV float wave_max(float v) {
+  v = fmax_ordered(v, dpp<kDppXor1>(v));
+  v = fmax_ordered(v, dpp<kDppXor2>(v));
+  v = fmax_ordered(v, dpp<kDppHalfMirror>(v));
+  v = fmax_ordered(v, dpp<kDppMirror>(v));
+  v = fmax_ordered(v, swizzle_xor16(v));
+  v = fmax_ordered(v, xor32(v));
+  return v;
+}
+
+SILE_DEV float wave_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  v += swizzle_xor16(v);
+  v += xor32(v);
+  return v;
+}
+
+// 2^x on the transcendental unit (v_exp_f32).
+SILE_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace sile

@@ -1,0 +1,157 @@
+// gfx950 kernels for sile's DSL example kernels, run with the reference's
+// program semantics: one workgroup per program, program ids decoded from the
+// workgroup index exactly as the generated CPU wrapper decodes its OpenMP
+// loop index (crates/sile-backend/src/cpu/codegen.rs:517-551):
+//   pid < total_tiles, gid0 = pid / tiles_n, gid1 = pid % tiles_n.
+// Element type is f32 only, as in the reference (crates/sile-hir/src/types.rs:11-14).
+#include "common.h"
+
+using namespace sile;
+
+struct MatmulTileArgs {
+  int64_t lda, ldb, ldc;  // shape(a)[1], shape(b)[1], shape(c)[1]
+  int64_t bm, bn, bk;     // const generics of the DSL kernel
+  int64_t tiles_n;        // shape(c)[1] / BN
+  int64_t total;          // (shape(c)[0] / BM) * tiles_n
+};
+
+// Canonical matmul program (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444):
+// every cell sums a[.]*b[.] from 0.0f in increasing k with a separate rounding
+// for the product and for the add, over k < (lda / BK) * BK.  Threads own
+// cells; each cell keeps the reference's sequential order, so results are
+// bit-identical to the CPU backend's.
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_matmul_f32(const float* __restrict__ a,
+                                                                       const float* __restrict__ b,
+                                                                       float* __restrict__ c,
+                                                                       MatmulTileArgs args) {
+#pragma clang fp contract(off)
+  const int64_t pid = blockIdx.x;
+  if (pid >= args.total) return;
+  const int64_t gid0 = pid / args.tiles_n, gid1 = pid % args.tiles_n;
+  const int64_t kp = (args.lda / args.bk) * args.bk;
+  const int64_t row0 = gid0 * args.bm, col0 = gid1 * args.bn;
+  const int64_t cells = args.bm * args.bn;
+  for (int64_t cell = threadIdx.x; cell < cells; cell += blockDim.x) {
+    const int64_t r = cell / args.bn, cc = cell % args.bn;
+    const float* ap = a + row0 * args.lda + r * args.lda;
+    const float* bp = b + col0 + cc;
+    float s = 0.0f;
+    for (int64_t k = 0; k < kp; ++k) {
+      float p = ap[k] * bp[0];
+      s = s + p;
+      bp += args.ldb;
+    }
+    c[row0 * args.ldc + col0 + r * args.ldc + cc] = s;
+  }
+}
+
+struct SoftmaxTileArgs {
+  int64_t ldx, ldy;  // shape(x)[1], shape(y)[1]
+  int64_t bm, bn;
+  int64_t tiles_n, total;
+};
+
+// Softmax DSL program (crates/sile/tests/backend_softmax.rs:3-15): for each of
+// the BM rows of the [BM, BN] tile at (gid0, gid1): m = row max, e = exp(x - m),
+// s = sum(e), y = e / s.  One wave per row; the max is order-independent, the
+// sum is a wave tree (the reference sums left to right; the results agree
+// within fp32 rounding of the sum, not bit for bit, and exp is the device's).
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_softmax_f32(const float* __restrict__ x,
+                                                                        float* __restrict__ y,
+                                                                        SoftmaxTileArgs args) {
+  const int64_t pid = blockIdx.x;
+  if (pid >= args.total) return;
+  const int64_t gid0 = pid / args.tiles_n, gid1 = pid % args.tiles_n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  for (int64_t r = wave; r < args.bm; r += nwaves) {
+    const float* xr = x + (gid0 * args.bm) * args.ldx + gid1 * args.bn + r * args.ldx;
+    float* yr = y + (gid0 * args.bm) * args.ldy + gid1 * args.bn + r * args.ldy;
+    float m = -__builtin_inff();
+    for (int64_t c = lane; c < args.bn; c += 64) m = fmax_ordered(m, xr[c]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int64_t c = lane; c < args.bn; c += 64) s += exp2_fast((xr[c] - m) * kLog2e);
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+    for (int64_t c = lane; c < args.bn; c += 64) yr[c] = exp2_fast((xr[c] - m) * kLog2e) * inv;
+  }
+}
+
+struct ReduceTileArgs {
+  int64_t tile;   // TILE const generic
+  int64_t total;  // shape(a)[0] (wrapper fallback: no tile store to infer from)
+};
+
+// parallel_reduce program (crates/sile/examples/parallel_reduce.rs:3-9): the
+// tile a[pid*TILE, pid*TILE+TILE) is summed in the fused load+reduce vec4
+// order (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:80-113,
+// 1182-1256): chunk sums ((v0+v1)+v2)+v3 added in chunk order to an
+// accumulator that starts at 0.0f (TILE > 16) or at chunk 0 (TILE <= 16), then
+// the scalar tail in order.  Lanes form the chunk sums in parallel; lane 0
+// folds them in order, so the per-program partial is bit-identical to the CPU
+// backend's.  Programs then add their partial to out[0] atomically; the order
+// across programs is unspecified there as here.
+extern "C" __global__ __launch_bounds__(64) void sile_dsl_parallel_reduce_f32(
+    const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
+    ReduceTileArgs args) {
+#pragma clang fp contract(off)
+  __shared__ float chunk_sums[64];
+  const int64_t pid = blockIdx.x;
+  if (pid >= args.total) return;
+  const int lane = threadIdx.x;
+  const float* t = a + pid * args.tile;
+  const int64_t chunks = args.tile / 4;
+  float acc = 0.0f;
+  int64_t first = 0;
+  if (args.tile <= 16 && chunks > 0) {
+    acc = ((t[0] + t[1]) + t[2]) + t[3];
+    first = 1;
+  }
+  for (int64_t base = first; base < chunks; base += 64) {
+    const int64_t ci = base + lane;
+    if (ci < chunks) {
+      const float* p = t + 4 * ci;
+      chunk_sums[lane] = ((p[0] + p[1]) + p[2]) + p[3];
+    }
+    __syncthreads();
+    if (lane == 0) {
+      const int64_t n = (chunks - base) < 64 ? (chunks - base) : 64;
+      for (int64_t i = 0; i < n; ++i) acc = acc + chunk_sums[i];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    if (args.tile < 4) {
+      // extent < 4 takes the plain sequential fold from element 0 (reduce.rs:32-112)
+      acc = t[0];
+      for (int64_t i = 1; i < args.tile; ++i) acc = acc + t[i];
+    } else {
+      for (int64_t i = chunks * 4; i < args.tile; ++i) acc = acc + t[i];
+    }
+    if (partials) partials[pid] = acc;
+    atomicAdd(out, acc);
+  }
+}
+
+// vec_add of crates/sile/tests/backend_vec_add.rs:3-9 (outside the hot path),
+// written against the generic tile-launch convention of sile_hip_launch_tiles:
+// (buffers, num_programs, shapes, num_shapes) with buffers = {a, b, c} and
+// shapes = shape(a) ++ shape(b) ++ shape(c).  The output is rank 1, so
+// total_tiles = shape(c)[0] and gid0 = pid (crates/sile-backend/src/cpu/codegen.rs:409-431,
+// 517-531); the [4] tile of program pid starts at pid * 4 (rank-1 addressing,
+// crates/sile-tile-ir/src/passes/lowering/tile_memory.rs:175-188).  Elements past
+// shape(c)[0] are skipped (the CPU backend has no such guard).
+extern "C" __global__ __launch_bounds__(64) void sile_tiles_vec_add4(void** buffers,
+                                                                     int64_t num_programs,
+                                                                     const int64_t* shapes,
+                                                                     int64_t num_shapes) {
+  const int64_t pid = blockIdx.x;
+  if (num_shapes < 3 || pid >= num_programs) return;
+  const int64_t total = shapes[2];
+  if (pid >= total) return;
+  const float* a = static_cast<const float*>(buffers[0]);
+  const float* b = static_cast<const float*>(buffers[1]);
+  float* c = static_cast<float*>(buffers[2]);
+  const int64_t i = pid * 4 + threadIdx.x;
+  if (threadIdx.x < 4 && i < shapes[0] && i < shapes[1] && i < shapes[2]) c[i] = a[i] + b[i];
+}

@@ -1,0 +1,250 @@
+// MFMA GEMM for gfx950:  C[M,N] = alpha * A[M,K] . B[K,N]
+//   A row-major ([M,K], K contiguous), B column-major (stored [N,K], K
+//   contiguous), fp32 accumulation in MFMA accumulators, output bf16 / fp16 /
+//   fp32 with round-to-nearest-even.  alpha carries the per-tensor scales of
+//   the fp8 path (scale_a * scale_b) and is 1 otherwise.
+//
+// This is the tile op `MmaF` of the canonical matmul
+// (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444) on the
+// matrix cores; k runs over K' = (K / bk) * bk as there, which the host
+// resolves before launch.
+//
+// Block tile 256 x 256, k-step 128 bytes per row (64 elements of a 16-bit type,
+// 128 of fp8), 256 threads = 4 waves in a 2 x 2 arrangement, each wave owning a
+// 128 x 128 sub-tile = 8 x 8 MFMA 16x16 blocks (256 fp32 accumulators per lane).
+//   * global -> registers with 128-bit loads, registers -> LDS (double-buffered,
+//     2 stages x 64 KiB), one barrier per k-step; the next k-step's global loads
+//     are in flight while the matrix cores work on the current one;
+//   * LDS rows are 128 bytes = 8 chunks of 16 bytes; chunk c of row r is stored
+//     at chunk position c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, which makes
+//     the 16-lane fragment reads (16 rows, one chunk column) and the tile
+//     writes (8 lanes per row) hit distinct banks;
+//   * the MFMA is issued with the B fragment as the first operand, so the
+//     accumulator of a lane holds 4 consecutive n of one output row and the
+//     epilogue writes 8-byte (16-bit C) or 16-byte (fp32 C) vectors;
+//   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
+//     remapped so the workgroups resident on one XCD cover a compact group of
+//     tiles (8 tile-rows x 4 tile-cols at a time) and share A / B panels in
+//     that XCD's L2.
+#include "common.h"
+
+using namespace sile;
+
+namespace {
+
+constexpr int kBM = 256, kBN = 256;
+constexpr int kRowBytes = 128;                       // bytes of one tile row per k-step
+constexpr int kTileBytes = kBM * kRowBytes;          // 32 KiB per operand per stage
+constexpr int kStageBytes = 2 * kTileBytes;          // A + B
+constexpr int kThreads = 256;
+constexpr int kLoadsPerThread = kTileBytes / 16 / kThreads;  // 8 x 16-byte chunks per operand
+
+enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
+enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
+
+SILE_DEV int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <int kKind>
+struct Mfma;
+template <>
+struct Mfma<kBF16> {
+  static constexpr int kElemBytes = 2;
+  static constexpr int kSubSteps = 2;  // 16x16x32: one 16-byte chunk per lane, 4 chunks per step
+  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<kF16> {
+  static constexpr int kElemBytes = 2;
+  static constexpr int kSubSteps = 2;
+  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<kFP8> {
+  static constexpr int kElemBytes = 1;
+  static constexpr int kSubSteps = 1;  // 16x16x128: two 16-byte chunks per lane, 8 chunks per step
+  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
+    const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
+                      (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
+    const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                      (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+    // cbsz = blgp = 0: both operands OCP e4m3; scales 0 select the unscaled MFMA.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+  }
+};
+
+template <int kOut>
+SILE_DEV void store_c4(void* C, int64_t idx, f32x4 v) {
+  if constexpr (kOut == kOutF32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx) = v;
+  } else if constexpr (kOut == kOutBF16) {
+    u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx) = w;
+  } else {
+    u32x2 w = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx) = w;
+  }
+}
+
+struct GemmArgs {
+  int64_t lda, ldb, ldc;  // in elements
+  int32_t tiles_m, tiles_n, k_steps;
+  float alpha;
+};
+
+template <int kKind, int kOut>
+__device__ __forceinline__ void gemm_nt_body(const uint8_t* __restrict__ A,
+                                             const uint8_t* __restrict__ B, void* __restrict__ C,
+                                             const GemmArgs& g, uint8_t* smem) {
+  using M = Mfma<kKind>;
+  constexpr int kEB = M::kElemBytes;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- XCD-aware tile order ----
+  const int num_tiles = g.tiles_m * g.tiles_n;
+  const int bid = blockIdx.x;
+  int lin = bid;
+  if ((num_tiles & 7) == 0) lin = (bid & 7) * (num_tiles >> 3) + (bid >> 3);
+  constexpr int kGroupM = 8;
+  const int group_size = kGroupM * g.tiles_n;
+  const int group = lin / group_size;
+  const int first_m = group * kGroupM;
+  const int rows_in_group = min(g.tiles_m - first_m, kGroupM);
+  const int in_group = lin - group * group_size;
+  const int tile_m = first_m + in_group % rows_in_group;
+  const int tile_n = in_group / rows_in_group;
+
+  // ---- global load addressing: thread t moves chunk (t & 7) of rows (t >> 3) + 32 i ----
+  const int ld_row = tid >> 3, ld_chunk = tid & 7;
+  const int64_t a_row_stride = g.lda * kEB, b_row_stride = g.ldb * kEB;
+  const uint8_t* a_src = A + ((int64_t)tile_m * kBM + ld_row) * a_row_stride + ld_chunk * 16;
+  const uint8_t* b_src = B + ((int64_t)tile_n * kBN + ld_row) * b_row_stride + ld_chunk * 16;
+  const int64_t a_step32 = 32 * a_row_stride, b_step32 = 32 * b_row_stride;
+  const int st_off = ld_row * kRowBytes + ((ld_chunk ^ swz(ld_row)) << 4);  // + 32*i rows: same swz
+
+  // ---- fragment read addressing ----
+  const int fr_row = lane & 15, fr_q = lane >> 4;
+  const int fr_swz = swz(fr_row);
+  const int a_frag_base = (wm * 128 + fr_row) * kRowBytes;
+  const int b_frag_base = kTileBytes + (wn * 128 + fr_row) * kRowBytes;
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
+  auto global_load = [&](int ks) {
+    const int64_t koff = (int64_t)ks * kRowBytes;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      ra[i] = *reinterpret_cast<const u32x4*>(a_src + i * a_step32 + koff);
+      rb[i] = *reinterpret_cast<const u32x4*>(b_src + i * b_step32 + koff);
+    }
+  };
+  auto lds_store = [&](int stage) {
+    uint8_t* base = smem + stage * kStageBytes + st_off;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      *reinterpret_cast<u32x4*>(base + i * 32 * kRowBytes) = ra[i];
+      *reinterpret_cast<u32x4*>(base + kTileBytes + i * 32 * kRowBytes) = rb[i];
+    }
+  };
+
+  global_load(0);
+  lds_store(0);
+  __syncthreads();
+
+  for (int ks = 0; ks < g.k_steps; ++ks) {
+    const int stage = ks & 1;
+    if (ks + 1 < g.k_steps) global_load(ks + 1);
+    const uint8_t* sbase = smem + stage * kStageBytes;
+#pragma unroll
+    for (int sub = 0; sub < M::kSubSteps; ++sub) {
+      constexpr int kChunksPerLane = 2 / M::kSubSteps;  // 1 (16-bit) or 2 (fp8)
+      u32x4 af[8][kChunksPerLane], bf[8][kChunksPerLane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int h = 0; h < kChunksPerLane; ++h) {
+          const int chunk = sub * 4 + fr_q * kChunksPerLane + h;
+          const int off = ((chunk ^ fr_swz) << 4);
+          af[i][h] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 16 * kRowBytes + off);
+          bf[i][h] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 16 * kRowBytes + off);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = M::run(bf[i], af[j], acc[i][j]);
+    }
+    if (ks + 1 < g.k_steps) lds_store(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds C[m][n .. n+3] for each (i = n block, j = m block) ----
+  const int64_t m_base = (int64_t)tile_m * kBM + wm * 128 + (lane & 15);
+  const int64_t n_base = (int64_t)tile_n * kBN + wn * 128 + (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      f32x4 v = acc[i][j];
+      if (g.alpha != 1.0f) v *= g.alpha;
+      store_c4<kOut>(C, (m_base + j * 16) * g.ldc + n_base + i * 16, v);
+    }
+}
+
+}  // namespace
+
+#define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                      \
+  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
+                                                            void* C, GemmArgs g) {             \
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];                    \
+    gemm_nt_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), C, \
+                            g, smem);                                                          \
+  }
+
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
+
+// fp32 GEMM on any shape in the canonical matmul's exact order: one thread per
+// cell, s = s + a*b from 0.0f over k < kp with separate roundings (no FMA).
+// A row-major [M,K]; B either row-major [K,N] (b_col_major = 0, the reference
+// layout) or column-major (stored [N,K]).
+extern "C" __global__ __launch_bounds__(256) void sile_gemm_f32_exact(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int64_t M,
+    int64_t N, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc, int32_t b_col_major) {
+#pragma clang fp contract(off)
+  const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x & 15);
+  const int64_t m = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
+  if (m >= M || n >= N) return;
+  const float* ap = A + m * lda;
+  float s = 0.0f;
+  if (b_col_major) {
+    const float* bp = B + n * ldb;
+    for (int64_t k = 0; k < kp; ++k) {
+      float p = ap[k] * bp[k];
+      s = s + p;
+    }
+  } else {
+    const float* bp = B + n;
+    for (int64_t k = 0; k < kp; ++k) {
+      float p = ap[k] * bp[k * ldb];
+      s = s + p;
+    }
+  }
+  C[m * ldc + n] = s;
+}

@@ -1,0 +1,215 @@
+// Row softmax and row reduce for gfx950 (HBM-bound).
+//
+// Semantics follow the softmax DSL kernel (crates/sile/tests/backend_softmax.rs:3-15)
+// with BN equal to the row width, i.e. a row softmax, and the reduce ops
+// ReduceMax / ReduceSum (crates/sile-tile-ir/src/ir.rs:128-262):
+//   m = max_c x[c]; e[c] = exp(x[c] - m); s = sum_c e[c]; y[c] = e[c] / s
+// with fp32 max, exp and sum for every input type.
+//
+// Fast path: one wave per row with the whole row held in registers, so x is
+// read from HBM once and y written once (4 bytes per fp16 element in total).
+// Each lane owns kChunks chunks of 8 consecutive elements; chunk j of lane l
+// starts at column (j * 64 + l) * 8, so every load/store instruction of the
+// wave moves one contiguous span (1 KiB for 16-bit types) with 128-bit
+// accesses.  The max and the sum are wave all-reductions over DPP row permutes
+// (common.h).  exp(x - m) is evaluated as 2^((x - m) * log2 e) on v_exp_f32.
+// Rows are assigned four per 256-thread workgroup.
+#include "common.h"
+
+using namespace sile;
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+template <int kT>
+struct Elem;
+template <>
+struct Elem<kF32> {
+  using Storage = float;
+  SILE_DEV static void load8(const float* p, float v[8]) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+    v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+  }
+  SILE_DEV static void store8(float* p, const float v[8]) {
+    f32x4 a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+  SILE_DEV static float load1(const float* p) { return *p; }
+  SILE_DEV static void store1(float* p, float v) { *p = v; }
+};
+template <>
+struct Elem<kF16> {
+  using Storage = uint16_t;
+  SILE_DEV static void load8(const uint16_t* p, float v[8]) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 h = __builtin_bit_cast(f16x2, w[i]);
+      v[2 * i] = (float)h[0];
+      v[2 * i + 1] = (float)h[1];
+    }
+  }
+  SILE_DEV static void store8(uint16_t* p, const float v[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_f16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = w;
+  }
+  SILE_DEV static float load1(const uint16_t* p) { return f16_to_f32(*p); }
+  SILE_DEV static void store1(uint16_t* p, float v) { *p = f16_rne(v); }
+};
+template <>
+struct Elem<kBF16> {
+  using Storage = uint16_t;
+  SILE_DEV static void load8(const uint16_t* p, float v[8]) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bits_f32(w[i] << 16);
+      v[2 * i + 1] = bits_f32(w[i] & 0xffff0000u);
+    }
+  }
+  SILE_DEV static void store8(uint16_t* p, const float v[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = w;
+  }
+  SILE_DEV static float load1(const uint16_t* p) { return bf16_to_f32(*p); }
+  SILE_DEV static void store1(uint16_t* p, float v) { *p = bf16_rne(v); }
+};
+
+// ---- register-resident row softmax: cols == kChunks * 512 ----
+template <int kIn, int kOut, int kChunks>
+__device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Storage* __restrict__ xr,
+                                                 typename Elem<kOut>::Storage* __restrict__ yr,
+                                                 int lane) {
+  float v[kChunks][8];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) Elem<kIn>::load8(xr + (j * 64 + lane) * 8, v[j]);
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmax_ordered(m, v[j][i]);
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[j][i] = exp2_fast((v[j][i] - m) * kLog2e);
+      s += v[j][i];
+    }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[j][i] *= inv;
+    Elem<kOut>::store8(yr + (j * 64 + lane) * 8, v[j]);
+  }
+}
+
+template <int kIn, int kOut, int kChunks>
+__device__ __forceinline__ void softmax_rows_regs_kernel(const void* x, void* y, int64_t rows,
+                                                         int64_t ldx, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  softmax_row_regs<kIn, kOut, kChunks>(static_cast<const TI*>(x) + row * ldx,
+                                       static_cast<TO*>(y) + row * ldy, lane);
+}
+
+// ---- any width: three passes over the row (L2-resident after the first) ----
+template <int kIn, int kOut>
+__device__ __forceinline__ void softmax_rows_generic_kernel(const void* x, void* y, int64_t rows,
+                                                            int64_t cols, int64_t ldx,
+                                                            int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  TO* yr = static_cast<TO*>(y) + row * ldy;
+  float m = -__builtin_inff();
+  for (int64_t c = lane; c < cols; c += 64) m = fmax_ordered(m, Elem<kIn>::load1(xr + c));
+  m = wave_max(m);
+  float s = 0.0f;
+  for (int64_t c = lane; c < cols; c += 64) s += exp2_fast((Elem<kIn>::load1(xr + c) - m) * kLog2e);
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  for (int64_t c = lane; c < cols; c += 64)
+    Elem<kOut>::store1(yr + c, exp2_fast((Elem<kIn>::load1(xr + c) - m) * kLog2e) * inv);
+}
+
+#define SILE_SOFTMAX_REGS(NAME, IN, OUT, CH)                                                 \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows, \
+                                                         int64_t ldx, int64_t ldy) {         \
+    softmax_rows_regs_kernel<IN, OUT, CH>(x, y, rows, ldx, ldy);                             \
+  }
+#define SILE_SOFTMAX_WIDTHS(TAG, IN, OUT)                      \
+  SILE_SOFTMAX_REGS(sile_softmax_rows_##TAG##_c1, IN, OUT, 1)   \
+  SILE_SOFTMAX_REGS(sile_softmax_rows_##TAG##_c2, IN, OUT, 2)   \
+  SILE_SOFTMAX_REGS(sile_softmax_rows_##TAG##_c4, IN, OUT, 4)   \
+  SILE_SOFTMAX_REGS(sile_softmax_rows_##TAG##_c8, IN, OUT, 8)   \
+  SILE_SOFTMAX_REGS(sile_softmax_rows_##TAG##_c16, IN, OUT, 16) \
+  extern "C" __global__ __launch_bounds__(256) void sile_softmax_rows_##TAG##_any(          \
+      const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy) {      \
+    softmax_rows_generic_kernel<IN, OUT>(x, y, rows, cols, ldx, ldy);                      \
+  }
+
+SILE_SOFTMAX_WIDTHS(f16_f16, kF16, kF16)
+SILE_SOFTMAX_WIDTHS(bf16_bf16, kBF16, kBF16)
+SILE_SOFTMAX_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_WIDTHS(f16_f32, kF16, kF32)
+
+// ---- row reduce (ReduceMax / ReduceSum along axis 1), fp32 result ----
+// op 0 = max (order-independent, so identical to the reference's fold),
+// op 1 = sum (wave tree; the reference folds left to right).
+template <int kIn>
+__device__ __forceinline__ void reduce_rows_kernel(int op, int vec, const void* x, float* out,
+                                                   int64_t rows, int64_t cols, int64_t ldx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  const int64_t vec_cols = vec ? (cols & ~(int64_t)7) : 0;
+  float acc = op == 0 ? -__builtin_inff() : 0.0f;
+  int64_t c = (int64_t)lane * 8;
+  for (; c < vec_cols; c += 512) {
+    float v[8];
+    Elem<kIn>::load8(xr + c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+  }
+  for (int64_t cc = vec_cols + lane; cc < cols; cc += 64) {
+    const float v = Elem<kIn>::load1(xr + cc);
+    acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
+  }
+  acc = op == 0 ? wave_max(acc) : wave_sum(acc);
+  if (lane == 0) out[row] = acc;
+}
+
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_f32(int op, int vec, const void* x,
+                                                                       float* out, int64_t rows,
+                                                                       int64_t cols, int64_t ldx) {
+  reduce_rows_kernel<kF32>(op, vec, x, out, rows, cols, ldx);
+}
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_f16(int op, int vec, const void* x,
+                                                                       float* out, int64_t rows,
+                                                                       int64_t cols, int64_t ldx) {
+  reduce_rows_kernel<kF16>(op, vec, x, out, rows, cols, ldx);
+}
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_bf16(int op, int vec, const void* x,
+                                                                        float* out, int64_t rows,
+                                                                        int64_t cols,
+                                                                        int64_t ldx) {
+  reduce_rows_kernel<kBF16>(op, vec, x, out, rows, cols, ldx);
+}

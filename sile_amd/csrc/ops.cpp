@@ -1,0 +1,341 @@
+// Op entry points of libsile_hip: argument validation on the host, then one
+// launch of the matching gfx950 kernel.  Every shape the kernels index with is
+// checked here first, so a launch never addresses memory outside the buffers
+// the caller described.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+
+#include "runtime_internal.h"
+
+using namespace sile_rt;
+
+namespace {
+
+// Kernel argument blocks; layouts match the structs in kernels/*.hip.
+struct MatmulTileArgs {
+  int64_t lda, ldb, ldc, bm, bn, bk, tiles_n, total;
+};
+struct SoftmaxTileArgs {
+  int64_t ldx, ldy, bm, bn, tiles_n, total;
+};
+struct ReduceTileArgs {
+  int64_t tile, total;
+};
+struct GemmArgs {
+  int64_t lda, ldb, ldc;
+  int32_t tiles_m, tiles_n, k_steps;
+  float alpha;
+};
+
+const char* dtype_name(int t) {
+  switch (t) {
+    case SILE_F32: return "f32";
+    case SILE_F16: return "f16";
+    case SILE_BF16: return "bf16";
+    case SILE_F8E4M3: return "f8e4m3";
+    default: return "?";
+  }
+}
+
+size_t dtype_bytes(int t) {
+  switch (t) {
+    case SILE_F32: return 4;
+    case SILE_F16:
+    case SILE_BF16: return 2;
+    case SILE_F8E4M3: return 1;
+    default: return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Programs that execute a body: min(num_threadgroups * threads_per_group, total),
+// since programs with pid >= total_tiles are skipped by the wrapper guard
+// (crates/sile-backend/src/cpu/codegen.rs:517-531).
+int programs_to_run(int64_t num_threadgroups, int64_t threads_per_group, int64_t total,
+                    int64_t* out) {
+  if (num_threadgroups < 0 || threads_per_group < 1)
+    return fail(SILE_ERR_SHAPE, "num_threadgroups %lld / threads_per_group %lld invalid",
+                (long long)num_threadgroups, (long long)threads_per_group);
+  const int64_t launched = num_threadgroups * threads_per_group;
+  *out = std::max<int64_t>(0, std::min(launched, total));
+  if (*out > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many programs");
+  return SILE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// DSL kernels (sile_kernel_<name> ABI)
+// ---------------------------------------------------------------------------
+
+int sile_hip_kernel_matmul(void* const* buffers, int64_t num_threadgroups,
+                           int64_t threads_per_group, const int64_t* shapes, int64_t num_shapes,
+                           int64_t bm, int64_t bn, int64_t bk, sile_hip_stream stream) {
+  if (!buffers || !shapes || num_shapes != 6)
+    return fail(SILE_ERR_SHAPE, "matmul expects 3 buffers and 6 shape values (got %lld)",
+                (long long)num_shapes);
+  if (bm <= 0 || bn <= 0 || bk <= 0) return fail(SILE_ERR_SHAPE, "BM, BN, BK must be positive");
+  const int64_t a0 = shapes[0], a1 = shapes[1], b0 = shapes[2], b1 = shapes[3], c0 = shapes[4],
+                c1 = shapes[5];
+  if (a0 < 0 || a1 < 0 || b0 < 0 || b1 < 0 || c0 < 0 || c1 < 0)
+    return fail(SILE_ERR_SHAPE, "negative extent");
+  MatmulTileArgs t{a1, b1, c1, bm, bn, bk, c1 / bn, 0};
+  t.total = (c0 / bm) * t.tiles_n;
+  int64_t run = 0;
+  int rc = programs_to_run(num_threadgroups, threads_per_group, t.total, &run);
+  if (rc != SILE_OK) return rc;
+  if (run == 0) return ok();
+  // Extents the programs touch: rows of a/c up to the last program's row tile,
+  // columns of b/c up to the last column tile any program reaches.
+  const int64_t kp = (a1 / bk) * bk;
+  const int64_t rows_needed = ((run - 1) / t.tiles_n + 1) * bm;
+  const int64_t cols_needed = std::min<int64_t>(run, t.tiles_n) * bn;
+  if (a0 < rows_needed || b0 < kp || b1 < cols_needed || c0 < rows_needed || c1 < cols_needed)
+    return fail(SILE_ERR_SHAPE,
+                "matmul shapes a[%lld,%lld] b[%lld,%lld] c[%lld,%lld] do not cover the tiles of "
+                "%lld programs (BM=%lld BN=%lld BK=%lld)",
+                (long long)a0, (long long)a1, (long long)b0, (long long)b1, (long long)c0,
+                (long long)c1, (long long)run, (long long)bm, (long long)bn, (long long)bk);
+  const void* a = buffers[0];
+  const void* b = buffers[1];
+  void* c = buffers[2];
+  void* params[] = {&a, &b, &c, &t};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch(Module::kDsl, "sile_dsl_matmul_f32", dim3((unsigned)run), dim3(256), params, s);
+  if (rc != SILE_OK) return rc;
+  SILE_HIP_CHECK(hipStreamSynchronize(s));
+  return ok();
+}
+
+int sile_hip_kernel_softmax(void* const* buffers, int64_t num_threadgroups,
+                            int64_t threads_per_group, const int64_t* shapes, int64_t num_shapes,
+                            int64_t bm, int64_t bn, sile_hip_stream stream) {
+  if (!buffers || !shapes || num_shapes != 4)
+    return fail(SILE_ERR_SHAPE, "softmax expects 2 buffers and 4 shape values (got %lld)",
+                (long long)num_shapes);
+  if (bm <= 0 || bn <= 0) return fail(SILE_ERR_SHAPE, "BM, BN must be positive");
+  const int64_t x0 = shapes[0], x1 = shapes[1], y0 = shapes[2], y1 = shapes[3];
+  if (x0 < 0 || x1 < 0 || y0 < 0 || y1 < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  SoftmaxTileArgs t{x1, y1, bm, bn, y1 / bn, 0};
+  t.total = (y0 / bm) * t.tiles_n;
+  int64_t run = 0;
+  int rc = programs_to_run(num_threadgroups, threads_per_group, t.total, &run);
+  if (rc != SILE_OK) return rc;
+  if (run == 0) return ok();
+  const int64_t rows_needed = ((run - 1) / t.tiles_n + 1) * bm;
+  const int64_t cols_needed = std::min<int64_t>(run, t.tiles_n) * bn;
+  if (x0 < rows_needed || x1 < cols_needed || y0 < rows_needed || y1 < cols_needed)
+    return fail(SILE_ERR_SHAPE,
+                "softmax shapes x[%lld,%lld] y[%lld,%lld] do not cover the tiles of %lld "
+                "programs (BM=%lld BN=%lld)",
+                (long long)x0, (long long)x1, (long long)y0, (long long)y1, (long long)run,
+                (long long)bm, (long long)bn);
+  const void* x = buffers[0];
+  void* y = buffers[1];
+  void* params[] = {&x, &y, &t};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch(Module::kDsl, "sile_dsl_softmax_f32", dim3((unsigned)run), dim3(256), params, s);
+  if (rc != SILE_OK) return rc;
+  SILE_HIP_CHECK(hipStreamSynchronize(s));
+  return ok();
+}
+
+int sile_hip_kernel_parallel_reduce(void* const* buffers, int64_t num_threadgroups,
+                                    int64_t threads_per_group, const int64_t* shapes,
+                                    int64_t num_shapes, int64_t tile, float* partials,
+                                    sile_hip_stream stream) {
+  if (!buffers || !shapes || num_shapes != 2)
+    return fail(SILE_ERR_SHAPE, "parallel_reduce expects 2 buffers and 2 shape values (got %lld)",
+                (long long)num_shapes);
+  if (tile <= 0) return fail(SILE_ERR_SHAPE, "TILE must be positive");
+  const int64_t len = shapes[0], out_len = shapes[1];
+  if (len < 0 || out_len < 1) return fail(SILE_ERR_SHAPE, "out must hold at least one element");
+  // No tile store to infer a plan from: total = shape(first buffer)[0]
+  // (crates/sile-backend/src/cpu/codegen.rs:479-503).
+  ReduceTileArgs t{tile, len};
+  int64_t run = 0;
+  int rc = programs_to_run(num_threadgroups, threads_per_group, t.total, &run);
+  if (rc != SILE_OK) return rc;
+  if (run == 0) return ok();
+  if (run > len / tile)
+    return fail(SILE_ERR_SHAPE, "%lld programs of TILE=%lld read past a[%lld]", (long long)run,
+                (long long)tile, (long long)len);
+  const void* a = buffers[0];
+  void* out = buffers[1];
+  void* params[] = {&a, &out, &partials, &t};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32", dim3((unsigned)run), dim3(64), params,
+              s);
+  if (rc != SILE_OK) return rc;
+  SILE_HIP_CHECK(hipStreamSynchronize(s));
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------
+
+int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
+                  int64_t k, const void* a, int64_t lda, sile_layout a_layout, const void* b,
+                  int64_t ldb, sile_layout b_layout, void* c, int64_t ldc, float scale_a,
+                  float scale_b, int64_t bk, sile_hip_stream stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(SILE_ERR_SHAPE, "negative GEMM extent");
+  const int64_t kp = bk > 0 ? (k / bk) * bk : k;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m == 0 || n == 0) return ok();
+  if (!a || !b || !c) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (a_layout != SILE_ROW_MAJOR)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "A must be row-major");
+
+  if (a_type == SILE_F32 && b_type == SILE_F32 && c_type == SILE_F32) {
+    const bool bcol = b_layout == SILE_COL_MAJOR;
+    if (lda < k || ldc < n || (bcol ? ldb < k : ldb < n))
+      return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
+    int32_t bc = bcol ? 1 : 0;
+    void* params[] = {&a, &b, &c, &m, &n, (void*)&kp, &lda, &ldb, &ldc, &bc};
+    const int64_t gx = (n + 15) / 16, gy = (m + 15) / 16;
+    if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
+    int rc = launch(Module::kGemm, "sile_gemm_f32_exact", dim3((unsigned)gx, (unsigned)gy),
+                    dim3(256), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+
+  const char* name = nullptr;
+  int64_t kstep = 64;
+  if (a_type == SILE_BF16 && b_type == SILE_BF16) {
+    name = c_type == SILE_BF16 ? "sile_gemm_nt_bf16_bf16"
+           : c_type == SILE_F32 ? "sile_gemm_nt_bf16_f32" : nullptr;
+  } else if (a_type == SILE_F16 && b_type == SILE_F16) {
+    name = c_type == SILE_F16 ? "sile_gemm_nt_f16_f16"
+           : c_type == SILE_F32 ? "sile_gemm_nt_f16_f32" : nullptr;
+  } else if (a_type == SILE_F8E4M3 && b_type == SILE_F8E4M3) {
+    name = c_type == SILE_BF16 ? "sile_gemm_nt_fp8_bf16"
+           : c_type == SILE_F32 ? "sile_gemm_nt_fp8_f32" : nullptr;
+    kstep = 128;
+  }
+  if (!name)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "GEMM %s x %s -> %s not supported",
+                dtype_name(a_type), dtype_name(b_type), dtype_name(c_type));
+  if (b_layout != SILE_COL_MAJOR)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "%s GEMM needs B column-major (K contiguous)",
+                dtype_name(a_type));
+  if (m % 256 || n % 256 || kp % kstep || kp == 0)
+    return fail(SILE_ERR_SHAPE,
+                "%s GEMM needs M, N multiples of 256 and K' multiple of %lld (M=%lld N=%lld K'=%lld)",
+                dtype_name(a_type), (long long)kstep, (long long)m, (long long)n, (long long)kp);
+  const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
+  if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
+  if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
+      !aligned16(c))
+    return fail(SILE_ERR_SHAPE, "operands and leading dimensions must be 16-byte aligned");
+  if ((m / 256) * (n / 256) > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
+  GemmArgs g{lda, ldb, ldc, (int32_t)(m / 256), (int32_t)(n / 256), (int32_t)(kp / kstep),
+             scale_a * scale_b};
+  void* params[] = {&a, &b, &c, &g};
+  int rc = launch(Module::kGemm, name, dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), params,
+                  s);
+  return rc == SILE_OK ? ok() : rc;
+}
+
+// ---------------------------------------------------------------------------
+// Row softmax / row reduce
+// ---------------------------------------------------------------------------
+
+int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows, int64_t cols,
+                          const void* x, int64_t ldx, void* y, int64_t ldy,
+                          sile_hip_stream stream) {
+  const char* tag = nullptr;
+  if (in_type == SILE_F16 && out_type == SILE_F16) tag = "f16_f16";
+  else if (in_type == SILE_BF16 && out_type == SILE_BF16) tag = "bf16_bf16";
+  else if (in_type == SILE_F32 && out_type == SILE_F32) tag = "f32_f32";
+  else if (in_type == SILE_F16 && out_type == SILE_F32) tag = "f16_f32";
+  if (!tag)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "softmax %s -> %s not supported",
+                dtype_name(in_type), dtype_name(out_type));
+  if (rows < 0 || cols < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (rows == 0) return ok();
+  if (cols == 0) return fail(SILE_ERR_SHAPE, "softmax over an empty row");
+  if (!x || !y) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldx < cols || ldy < cols) return fail(SILE_ERR_SHAPE, "leading dimension smaller than cols");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+  const bool vec_ok = ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y);
+  int chunks = 0;
+  if (vec_ok) {
+    for (int c : {1, 2, 4, 8, 16})
+      if (cols == (int64_t)c * 512) chunks = c;
+  }
+  char name[64];
+  int rc;
+  if (chunks) {
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_c%d", tag, chunks);
+    void* params[] = {&x, &y, &rows, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
+  } else {
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_any", tag);
+    void* params[] = {&x, &y, &rows, &cols, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
+  }
+  return rc == SILE_OK ? ok() : rc;
+}
+
+int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, int64_t cols,
+                         const void* x, int64_t ldx, float* out, sile_hip_stream stream) {
+  const char* name = in_type == SILE_F32    ? "sile_reduce_rows_f32"
+                     : in_type == SILE_F16  ? "sile_reduce_rows_f16"
+                     : in_type == SILE_BF16 ? "sile_reduce_rows_bf16"
+                                            : nullptr;
+  if (!name)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "reduce over %s not supported", dtype_name(in_type));
+  if (op != SILE_REDUCE_MAX && op != SILE_REDUCE_SUM)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "unknown reduce op %d", (int)op);
+  if (rows < 0 || cols < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (rows == 0) return ok();
+  if (cols == 0) return fail(SILE_ERR_SHAPE, "reduce over an empty row");
+  if (!x || !out) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldx < cols) return fail(SILE_ERR_SHAPE, "leading dimension smaller than cols");
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+  int iop = (int)op;
+  // The 128-bit path needs every row start 16-byte aligned; otherwise the
+  // kernel runs its scalar loop only.
+  int vec = aligned16(x) && (ldx * (int64_t)dtype_bytes(in_type)) % 16 == 0 ? 1 : 0;
+  void* params[] = {&iop, &vec, &x, &out, &rows, &cols, &ldx};
+  int rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params,
+                  static_cast<hipStream_t>(stream));
+  return rc == SILE_OK ? ok() : rc;
+}
+
+// ---------------------------------------------------------------------------
+// Attention
+// ---------------------------------------------------------------------------
+
+int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                            int64_t head_dim, const void* q, const void* k, const void* v,
+                            void* o, float scale, int causal, sile_hip_stream stream) {
+  if (dtype != SILE_F16 && dtype != SILE_BF16)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "attention over %s not supported", dtype_name(dtype));
+  if (batch < 0 || heads < 0 || seq_len < 0 || head_dim <= 0)
+    return fail(SILE_ERR_SHAPE, "invalid attention shape");
+  if (batch == 0 || heads == 0 || seq_len == 0) return ok();
+  if (!q || !k || !v || !o) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (head_dim > 256) return fail(SILE_ERR_UNSUPPORTED_BACKEND, "head_dim > 256 not supported");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int64_t bh = batch * heads;
+  const int64_t rows = bh * seq_len;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "attention too large");
+  const char* name = dtype == SILE_F16 ? "sile_attn_fwd_rowwise_f16" : "sile_attn_fwd_rowwise_bf16";
+  void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &bh, &seq_len, &head_dim, &scale, &causal};
+  int rc = launch(Module::kAttention, name, dim3((unsigned)blocks), dim3(256), params, s);
+  return rc == SILE_OK ? ok() : rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,357 @@
+// libsile_hip runtime: device selection, HBM memory, streams/events, code
+// object loading and kernel launch behind the C ABI of include/sile_hip.h.
+//
+// The library carries its gfx950 code objects inside its own image (the
+// build assembles them in with .incbin) and loads them with hipModuleLoadData
+// on first use of a device; kernels are launched with hipModuleLaunchKernel.
+// This replaces the reference CPU backend's per-launch `cc` compile and
+// dlopen (crates/sile-backend/src/cpu/mod.rs:48-134): compilation happens
+// once, at library build time.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "runtime_internal.h"
+
+// ---- embedded code objects -------------------------------------------------
+// SILE_CO_DIR is the build directory holding <name>.hsaco (raw ELF for gfx950).
+#ifndef SILE_CO_DIR
+#error "SILE_CO_DIR must name the directory of the built code objects"
+#endif
+
+#define SILE_EMBED(sym, file)                                           \
+  __asm__(".section .rodata." #sym ",\"a\",@progbits\n"                 \
+          ".p2align 12\n"                                               \
+          ".global " #sym "_begin\n" #sym "_begin:\n"                   \
+          ".incbin \"" SILE_CO_DIR "/" file "\"\n"                      \
+          ".global " #sym "_end\n" #sym "_end:\n"                       \
+          ".previous\n");                                               \
+  extern "C" const unsigned char sym##_begin[];                         \
+  extern "C" const unsigned char sym##_end[];
+
+SILE_EMBED(sile_co_dsl, "dsl.hsaco")
+SILE_EMBED(sile_co_softmax, "softmax.hsaco")
+SILE_EMBED(sile_co_gemm, "gemm.hsaco")
+SILE_EMBED(sile_co_attention, "attention.hsaco")
+
+namespace sile_rt {
+namespace {
+
+struct Image {
+  const unsigned char* begin;
+  const unsigned char* end;
+  const char* name;
+};
+
+const Image kImages[static_cast<int>(Module::kCount)] = {
+    {sile_co_dsl_begin, sile_co_dsl_end, "dsl"},
+    {sile_co_softmax_begin, sile_co_softmax_end, "softmax"},
+    {sile_co_gemm_begin, sile_co_gemm_end, "gemm"},
+    {sile_co_attention_begin, sile_co_attention_end, "attention"},
+};
+
+struct DeviceState {
+  hipModule_t modules[static_cast<int>(Module::kCount)] = {};
+  std::map<std::string, hipFunction_t> functions;
+};
+
+std::mutex g_mu;
+std::map<int, DeviceState> g_devices;
+thread_local std::string t_last_error;
+
+}  // namespace
+
+int fail(int status, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  t_last_error = buf;
+  return status;
+}
+
+int ok() {
+  t_last_error.clear();
+  return SILE_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SILE_ERR_RUNTIME, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+static int load_device_locked(int dev, DeviceState** out) {
+  auto it = g_devices.find(dev);
+  if (it != g_devices.end()) {
+    *out = &it->second;
+    return SILE_OK;
+  }
+  DeviceState st;
+  for (int i = 0; i < static_cast<int>(Module::kCount); ++i) {
+    hipError_t e = hipModuleLoadData(&st.modules[i], kImages[i].begin);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipModuleUnload(st.modules[j]);
+      return fail(SILE_ERR_COMPILE, "hipModuleLoadData(%s code object, %zu bytes) on device %d: %s",
+                  kImages[i].name, (size_t)(kImages[i].end - kImages[i].begin), dev,
+                  hipGetErrorString(e));
+    }
+  }
+  auto res = g_devices.emplace(dev, std::move(st));
+  *out = &res.first->second;
+  return SILE_OK;
+}
+
+int ensure_device() {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "no HIP device visible");
+  int dev = 0;
+  SILE_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* st = nullptr;
+  return load_device_locked(dev, &st);
+}
+
+int get_function(Module m, const char* name, hipFunction_t* out) {
+  int dev = 0;
+  SILE_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* st = nullptr;
+  int rc = load_device_locked(dev, &st);
+  if (rc != SILE_OK) return rc;
+  auto it = st->functions.find(name);
+  if (it != st->functions.end()) {
+    *out = it->second;
+    return SILE_OK;
+  }
+  hipFunction_t f = nullptr;
+  hipError_t e = hipModuleGetFunction(&f, st->modules[static_cast<int>(m)], name);
+  if (e != hipSuccess)
+    return fail(SILE_ERR_COMPILE, "kernel %s not found in the %s code object: %s", name,
+                kImages[static_cast<int>(m)].name, hipGetErrorString(e));
+  st->functions.emplace(name, f);
+  *out = f;
+  return SILE_OK;
+}
+
+int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
+           size_t dynamic_lds) {
+  hipFunction_t f = nullptr;
+  int rc = get_function(m, name, &f);
+  if (rc != SILE_OK) return rc;
+  hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                       (unsigned)dynamic_lds, stream, params, nullptr);
+  if (e != hipSuccess) return hip_fail(e, name);
+  return SILE_OK;
+}
+
+}  // namespace sile_rt
+
+using namespace sile_rt;
+
+extern "C" {
+
+const char* sile_hip_last_error(void) { return t_last_error.c_str(); }
+
+const char* sile_hip_version(void) { return "sile_hip 0.1 (gfx950)"; }
+
+int sile_hip_device_count(int* count) {
+  if (!count) return fail(SILE_ERR_SHAPE, "count is NULL");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return ok();
+}
+
+int sile_hip_init(int ordinal) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "no HIP device visible");
+  if (ordinal < 0 || ordinal >= count)
+    return fail(SILE_ERR_INVALID_DEVICE, "device ordinal %d out of range [0, %d)", ordinal, count);
+  SILE_HIP_CHECK(hipSetDevice(ordinal));
+  int rc = ensure_device();
+  if (rc != SILE_OK) return rc;
+  return ok();
+}
+
+int sile_hip_device_info(int ordinal, sile_hip_device_props* out) {
+  if (!out) return fail(SILE_ERR_SHAPE, "out is NULL");
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "no HIP device visible");
+  if (ordinal < 0 || ordinal >= count)
+    return fail(SILE_ERR_INVALID_DEVICE, "device ordinal %d out of range [0, %d)", ordinal, count);
+  hipDeviceProp_t p;
+  SILE_HIP_CHECK(hipGetDeviceProperties(&p, ordinal));
+  memset(out, 0, sizeof *out);
+  snprintf(out->name, sizeof out->name, "%s", p.name);
+  snprintf(out->gcn_arch, sizeof out->gcn_arch, "%s", p.gcnArchName);
+  out->compute_units = p.multiProcessorCount;
+  out->clock_khz = p.clockRate;
+  out->memory_clock_khz = p.memoryClockRate;
+  out->memory_bus_width = p.memoryBusWidth;
+  out->total_global_mem = (int64_t)p.totalGlobalMem;
+  out->l2_cache_bytes = p.l2CacheSize;
+  out->lds_per_block = (int64_t)p.sharedMemPerBlock;
+  return ok();
+}
+
+int sile_hip_device_synchronize(void) {
+  SILE_HIP_CHECK(hipDeviceSynchronize());
+  return ok();
+}
+
+int sile_hip_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(SILE_ERR_SHAPE, "ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return ok();
+  SILE_HIP_CHECK(hipMalloc(ptr, bytes));
+  return ok();
+}
+
+int sile_hip_free(void* ptr) {
+  if (ptr) SILE_HIP_CHECK(hipFree(ptr));
+  return ok();
+}
+
+int sile_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  if (bytes) SILE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return ok();
+}
+
+int sile_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  if (bytes) SILE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return ok();
+}
+
+int sile_hip_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+  if (bytes) SILE_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  return ok();
+}
+
+int sile_hip_memset(void* dst, int value, size_t bytes) {
+  if (bytes) SILE_HIP_CHECK(hipMemset(dst, value, bytes));
+  return ok();
+}
+
+int sile_hip_stream_create(sile_hip_stream* out) {
+  if (!out) return fail(SILE_ERR_SHAPE, "out is NULL");
+  hipStream_t s = nullptr;
+  SILE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = s;
+  return ok();
+}
+
+int sile_hip_stream_destroy(sile_hip_stream stream) {
+  if (stream) SILE_HIP_CHECK(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int sile_hip_stream_synchronize(sile_hip_stream stream) {
+  SILE_HIP_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int sile_hip_event_create(sile_hip_event* out) {
+  if (!out) return fail(SILE_ERR_SHAPE, "out is NULL");
+  hipEvent_t e = nullptr;
+  SILE_HIP_CHECK(hipEventCreate(&e));
+  *out = e;
+  return ok();
+}
+
+int sile_hip_event_destroy(sile_hip_event event) {
+  if (event) SILE_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return ok();
+}
+
+int sile_hip_event_record(sile_hip_event event, sile_hip_stream stream) {
+  SILE_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int sile_hip_event_synchronize(sile_hip_event event) {
+  SILE_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  return ok();
+}
+
+int sile_hip_event_elapsed_ms(float* ms, sile_hip_event start, sile_hip_event stop) {
+  if (!ms) return fail(SILE_ERR_SHAPE, "ms is NULL");
+  SILE_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                     static_cast<hipEvent_t>(stop)));
+  return ok();
+}
+
+int sile_hip_module_load(const void* image, size_t bytes, sile_hip_module* out) {
+  if (!image || !out || bytes < 4) return fail(SILE_ERR_COMPILE, "empty code object image");
+  int rc = ensure_device();
+  if (rc != SILE_OK) return rc;
+  hipModule_t m = nullptr;
+  hipError_t e = hipModuleLoadData(&m, image);
+  if (e != hipSuccess)
+    return fail(SILE_ERR_COMPILE, "hipModuleLoadData(%zu bytes): %s", bytes, hipGetErrorString(e));
+  *out = m;
+  return ok();
+}
+
+int sile_hip_module_unload(sile_hip_module module) {
+  if (module) SILE_HIP_CHECK(hipModuleUnload(static_cast<hipModule_t>(module)));
+  return ok();
+}
+
+int sile_hip_module_get(sile_hip_module module, const char* name, sile_hip_function* out) {
+  if (!module || !name || !out) return fail(SILE_ERR_COMPILE, "module, name or out is NULL");
+  hipFunction_t f = nullptr;
+  hipError_t e = hipModuleGetFunction(&f, static_cast<hipModule_t>(module), name);
+  if (e != hipSuccess)
+    return fail(SILE_ERR_COMPILE, "symbol %s not found: %s", name, hipGetErrorString(e));
+  *out = f;
+  return ok();
+}
+
+int sile_hip_launch_tiles(sile_hip_function fn, void* const* buffers, int64_t num_buffers,
+                          const int64_t* shapes, int64_t num_shapes, const uint32_t grid[3],
+                          uint32_t threads_per_program, sile_hip_stream stream) {
+  if (!fn) return fail(SILE_ERR_COMPILE, "function is NULL");
+  if (!grid) return fail(SILE_ERR_SHAPE, "grid not set");
+  if (num_buffers < 0 || num_shapes < 0 || (num_buffers && !buffers) || (num_shapes && !shapes))
+    return fail(SILE_ERR_SHAPE, "buffers/shapes arrays do not match their counts");
+  if (threads_per_program == 0 || threads_per_program > 1024)
+    return fail(SILE_ERR_SHAPE, "threads_per_program %u not in [1, 1024]", threads_per_program);
+  const int64_t programs = (int64_t)grid[0] * grid[1] * grid[2];
+  if (programs == 0) return ok();
+  if (programs > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many programs (%lld)", (long long)programs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Device copies of the pointer and shape tables, as the Metal runtime binds a
+  // shapes buffer after the args (crates/sile-backend/src/metal/mod.rs:131-144).
+  const size_t buf_bytes = (size_t)num_buffers * sizeof(void*);
+  const size_t shp_bytes = (size_t)num_shapes * sizeof(int64_t);
+  void* table = nullptr;
+  SILE_HIP_CHECK(hipMalloc(&table, buf_bytes + shp_bytes + 16));
+  std::vector<unsigned char> host(buf_bytes + shp_bytes + 16);
+  if (buf_bytes) memcpy(host.data(), buffers, buf_bytes);
+  if (shp_bytes) memcpy(host.data() + buf_bytes, shapes, shp_bytes);
+  hipError_t e = hipMemcpyAsync(table, host.data(), buf_bytes + shp_bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) {
+    void* dev_buffers = table;
+    void* dev_shapes = static_cast<unsigned char*>(table) + buf_bytes;
+    int64_t np = programs, ns = num_shapes;
+    void* params[] = {&dev_buffers, &np, &dev_shapes, &ns};
+    e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), (unsigned)programs, 1, 1,
+                              threads_per_program, 1, 1, 0, s, params, nullptr);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  hipError_t e2 = hipFree(table);
+  if (e != hipSuccess) return hip_fail(e, "sile_hip_launch_tiles");
+  if (e2 != hipSuccess) return hip_fail(e2, "hipFree");
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,41 @@
+// Internal interface between the runtime (runtime.cpp) and the op entry
+// points (ops.cpp) of libsile_hip.so.  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/sile_hip.h"
+
+namespace sile_rt {
+
+// Records `msg` as this thread's last error and returns `status`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the last error and returns SILE_OK.
+int ok();
+// Maps a HIP error to SILE_ERR_RUNTIME with the call site in the message.
+int hip_fail(hipError_t e, const char* what);
+
+#define SILE_HIP_CHECK(expr)                                     \
+  do {                                                           \
+    hipError_t _e = (expr);                                      \
+    if (_e != hipSuccess) return ::sile_rt::hip_fail(_e, #expr); \
+  } while (0)
+
+// The gfx950 code objects built into the library.
+enum class Module : int { kDsl = 0, kSoftmax = 1, kGemm = 2, kAttention = 3, kCount = 4 };
+
+// Makes sure the current device is initialised and its code objects are
+// loaded; returns a status.
+int ensure_device();
+// Looks up `name` in the given embedded module on the current device.
+int get_function(Module m, const char* name, hipFunction_t* out);
+// hipModuleLaunchKernel with kernelParams.
+int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
+           size_t dynamic_lds = 0);
+
+}  // namespace sile_rt

@@ -1,0 +1,68 @@
+"""GPU parity of sile_hip_flash_attn_fwd against the CPU oracle's naive fp32
+attention on the same 16-bit inputs.  Tolerance: |g - r| <= 2e-2 + 1e-2 |r|
+(the north star's bound for 16-bit outputs)."""
+import numpy as np
+import pytest
+
+from oracle import cpuref
+from tests.helpers import assert_close, bf16_round, f16_round, rng, say
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _inputs(b, h, s, d, dt, seed=6):
+    out = []
+    for i in range(3):
+        x = rng(seed + i).normal(size=(b, h, s, d)).astype(np.float32)
+        out.append(f16_round(x) if dt == "f16" else bf16_round(x))
+    return out
+
+
+def _run(hip, dt, b, h, s, d, qkv_bits, causal, scale):
+    t = hip.F16 if dt == "f16" else hip.BF16
+    bufs = [hip.DeviceBuffer.from_array(x) for x in qkv_bits]
+    do = hip.DeviceBuffer(b * h * s * d * 2)
+    do.fill_bytes(0xFF)
+    hip.flash_attn_fwd(t, b, h, s, d, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, do.ptr, scale, causal)
+    hip.synchronize()
+    bits = do.download(np.uint16, (b, h, s, d))
+    return bits.view(np.float16).astype(np.float32) if dt == "f16" else cpuref.f32_from_bf16(bits)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 3, 384, 128), (1, 1, 256, 64)])
+def test_attention_small(hip, dt, causal, b, h, s, d):
+    say(f"attention {dt} causal={causal} B={b} H={h} S={s} D={d}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, dt)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
+    qf, kf, vf = (x[1] for x in qkv)
+    for bi in range(b):
+        for hi in range(h):
+            ref = cpuref.attention_fwd(qf[bi, hi], kf[bi, hi], vf[bi, hi], scale, causal=causal)
+            assert_close(got[bi, hi], ref, atol=ATOL, rtol=RTOL, what=f"attn b{bi} h{hi}")
+
+
+@pytest.mark.parametrize("s", [4096])
+def test_attention_config4_sampled(hip, s):
+    """BASELINE config 4 shape family (B=4 reduced to 1 batch here, H=32, D=128,
+    causal, scale 1/sqrt(128)); two heads checked on the first, last and every
+    16th query block of 128 rows."""
+    b, h, d = 1, 32, 128
+    say(f"attention f16 causal B={b} H={h} S={s} D={d} sampled")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, "f16")
+    got = _run(hip, "f16", b, h, s, d, [x[0] for x in qkv], True, scale)
+    qf, kf, vf = (x[1] for x in qkv)
+    blocks = sorted(set(list(range(0, s // 128, 16)) + [s // 128 - 1]))
+    for hi in (0, h - 1):
+        ref = np.zeros((s, d), np.float32)
+        for blk in blocks:
+            cpuref.attention_fwd(qf[0, hi], kf[0, hi], vf[0, hi], scale, True, blk * 128,
+                                 blk * 128 + 128, out=ref)
+            sl = slice(blk * 128, blk * 128 + 128)
+            assert_close(got[0, hi, sl], ref[sl], atol=ATOL, rtol=RTOL, what=f"h{hi} blk{blk}")
+    assert np.isfinite(got).all()

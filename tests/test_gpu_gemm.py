@@ -1,0 +1,140 @@
+"""GPU parity of sile_hip_gemm against the CPU oracle's canonical matmul on the
+(de)quantised fp32 inputs.
+
+Tolerances: the north star's 2e-2 absolute / 1e-2 relative bound for bf16,
+fp16 and fp8 outputs, applied per element as |g - r| <= 2e-2 + 1e-2 |r|;
+the f32 path is bit-exact (canonical order).
+"""
+import numpy as np
+import pytest
+
+from oracle import cpuref
+from tests.helpers import assert_close, bf16_round, f16_round, fp8_quantise, rng, say
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _to_f32(hip, buf, c_type, m, n):
+    if c_type == 0:
+        return buf.download(np.float32, (m, n))
+    bits = buf.download(np.uint16, (m, n))
+    if c_type == hip.BF16:
+        return cpuref.f32_from_bf16(bits)
+    return bits.view(np.float16).astype(np.float32)
+
+
+def _run(hip, a_t, c_t, a_bits, b_bits, m, n, k, scale_a=1.0, scale_b=1.0, bk=0):
+    da = hip.DeviceBuffer.from_array(a_bits)
+    db = hip.DeviceBuffer.from_array(b_bits)
+    cbytes = 4 if c_t == hip.F32 else 2
+    dc = hip.DeviceBuffer(m * n * cbytes)
+    dc.fill_bytes(0xFF)  # NaN pattern: any cell the kernel skips is caught
+    hip.gemm(a_t, a_t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+             dc.ptr, n, scale_a, scale_b, bk)
+    hip.synchronize()
+    return _to_f32(hip, dc, c_t, m, n)
+
+
+SHAPES = [(256, 256, 64), (512, 256, 128), (768, 1024, 320), (2048, 2048, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_bf16_gemm(hip, m, n, k, out):
+    say(f"gemm bf16 {m}x{n}x{k} -> {out}")
+    a = (rng(4).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(5).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    a_bits, a_f = bf16_round(a)
+    b_bits, b_f = bf16_round(bt)
+    c_t = hip.BF16 if out == "bf16" else hip.F32
+    got = _run(hip, hip.BF16, c_t, a_bits, b_bits, m, n, k)
+    ref = cpuref.gemm_nt(a_f, b_f)
+    if out == "f32":
+        assert_close(got, ref, atol=1e-4, rtol=1e-4, what="bf16 gemm f32 out")
+    else:
+        assert_close(got, ref, atol=ATOL, rtol=RTOL, what="bf16 gemm")
+        # and the bf16 output is the rounding of an fp32 value close to ref
+        assert np.mean(np.abs(got - ref)) < 4e-3
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES[:3])
+def test_f16_gemm(hip, m, n, k):
+    say(f"gemm f16 {m}x{n}x{k}")
+    a = (rng(14).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(15).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    a_bits, a_f = f16_round(a)
+    b_bits, b_f = f16_round(bt)
+    got = _run(hip, hip.F16, hip.F16, a_bits, b_bits, m, n, k)
+    assert_close(got, cpuref.gemm_nt(a_f, b_f), atol=ATOL, rtol=RTOL, what="f16 gemm")
+
+
+def test_gemm_k_truncation(hip):
+    """bk = 96 on K = 320: k runs over (320 // 96) * 96 = 288 (not a multiple of
+    the 64-element k-step, so the MFMA path must refuse) and bk = 64 on K = 320
+    with K' = 320; bk = 128 -> K' = 256."""
+    say("gemm bf16 K truncation")
+    m = n = 256
+    k = 320
+    a = (rng(6).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(7).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    a_bits, a_f = bf16_round(a)
+    b_bits, b_f = bf16_round(bt)
+    got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=128)
+    assert_close(got, cpuref.gemm_nt(a_f, b_f, bk=128), atol=1e-4, rtol=1e-4, what="K'=256")
+    with pytest.raises(hip.SileError) as e:
+        _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=96)
+    assert e.value.kind == "Shape"
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 512), (2048, 2048, 2048)])
+def test_fp8_gemm(hip, m, n, k):
+    say(f"gemm fp8 {m}x{n}x{k}")
+    a = rng(9).normal(size=(m, k)).astype(np.float32)
+    bt = rng(10).normal(size=(n, k)).astype(np.float32)
+    qa, sa, a_deq = fp8_quantise(a)
+    qb, sb, b_deq = fp8_quantise(bt)
+    got = _run(hip, hip.F8E4M3, hip.BF16, qa, qb, m, n, k, sa, sb)
+    ref = cpuref.gemm_nt(a_deq, b_deq)
+    # fp8 GEMM outputs grow like sqrt(K) here (unit-variance inputs): the
+    # relative part of the bound dominates
+    assert_close(got, ref, atol=ATOL, rtol=RTOL, what="fp8 gemm")
+
+
+def test_f32_gemm_exact(hip):
+    say("gemm f32 exact 200x300x150 (both B layouts)")
+    m, n, k = 200, 300, 150
+    a = rng(1).uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = rng(2).uniform(-1, 1, size=(k, n)).astype(np.float32)
+    da, dbr = hip.DeviceBuffer.from_array(a), hip.DeviceBuffer.from_array(b)
+    dbc = hip.DeviceBuffer.from_array(np.ascontiguousarray(b.T))
+    dc = hip.DeviceBuffer(m * n * 4)
+    ref = cpuref.gemm_nt(a, np.ascontiguousarray(b.T), bk=0)
+    hip.gemm(hip.F32, hip.F32, hip.F32, m, n, k, da.ptr, k, hip.ROW_MAJOR, dbr.ptr, n,
+             hip.ROW_MAJOR, dc.ptr, n)
+    hip.synchronize()
+    np.testing.assert_array_equal(dc.download(np.float32, (m, n)), ref)
+    hip.gemm(hip.F32, hip.F32, hip.F32, m, n, k, da.ptr, k, hip.ROW_MAJOR, dbc.ptr, k,
+             hip.COL_MAJOR, dc.ptr, n)
+    hip.synchronize()
+    np.testing.assert_array_equal(dc.download(np.float32, (m, n)), ref)
+
+
+@pytest.mark.parametrize("size", [4096])
+def test_bf16_gemm_config3_sampled(hip, size):
+    """BASELINE config 3 at 4096^3: every 4th 256-row tile checked against the
+    oracle, every element of those tiles."""
+    say(f"gemm bf16 {size}^3 sampled")
+    m = n = k = size
+    a = (rng(4).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(5).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    a_bits, a_f = bf16_round(a)
+    b_bits, b_f = bf16_round(bt)
+    got = _run(hip, hip.BF16, hip.BF16, a_bits, b_bits, m, n, k)
+    ref = np.full((m, n), np.nan, np.float32)
+    cpuref.gemm_nt(a_f, b_f, bm=256, row_tile_step=4, out=ref)
+    rows = ~np.isnan(ref[:, 0])
+    assert rows.sum() == 4 * 256
+    assert_close(got[rows], ref[rows], atol=ATOL, rtol=RTOL, what="bf16 4096 sampled")
+    assert np.isfinite(got).all()

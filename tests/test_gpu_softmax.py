@@ -1,0 +1,125 @@
+"""GPU parity of sile_hip_softmax_rows and sile_hip_reduce_rows against the CPU
+oracle on the up-cast fp32 inputs.
+
+softmax tolerance: |g - r| <= 1e-6 + 1e-2 |r| per element for 16-bit outputs
+(the north star's 1e-2 relative bound; the absolute part is lowered from 2e-2
+to 1e-6 because every softmax output is below 2e-2 at these widths, which
+would make a 2e-2 bound vacuous), 1e-4 relative for fp32 outputs.
+"""
+import numpy as np
+import pytest
+
+from oracle import cpuref
+from tests.helpers import assert_close, bf16_round, f16_round, rng, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _softmax_gpu(hip, x_bits, in_t, out_t, rows, cols, ldx=None, ldy=None):
+    ldx = ldx or cols
+    ldy = ldy or cols
+    dx = hip.DeviceBuffer.from_array(x_bits)
+    ob = 4 if out_t == hip.F32 else 2
+    dy = hip.DeviceBuffer(rows * ldy * ob)
+    dy.fill_bytes(0)
+    hip.softmax_rows(in_t, out_t, rows, cols, dx.ptr, ldx, dy.ptr, ldy)
+    hip.synchronize()
+    if out_t == hip.F32:
+        y = dy.download(np.float32, (rows, ldy))
+    elif out_t == hip.F16:
+        y = dy.download(np.uint16, (rows, ldy)).view(np.float16).astype(np.float32)
+    else:
+        y = cpuref.f32_from_bf16(dy.download(np.uint16, (rows, ldy)))
+    return y[:, :cols]
+
+
+def test_softmax_f16_config2_full(hip):
+    """[8192, 8192] fp16, N(0, 4) seed 3, every element checked."""
+    say("softmax f16 8192x8192")
+    x = (rng(3).normal(size=(8192, 8192)) * 2.0).astype(np.float32)
+    xb, xf = f16_round(x)
+    got = _softmax_gpu(hip, xb, hip.F16, hip.F16, 8192, 8192)
+    ref = cpuref.softmax_rows(xf)
+    assert_close(got, ref, atol=1e-6, rtol=1e-2, what="softmax f16 8192")
+    assert np.all(np.abs(got.astype(np.float64).sum(axis=1) - 1.0) < 5e-3)
+    np.testing.assert_array_equal(got.argmax(axis=1), ref.argmax(axis=1))
+
+
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 100, 3000, 1])
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32", "f16_f32"])
+def test_softmax_widths_and_types(hip, cols, dt):
+    rows = 37
+    say(f"softmax {dt} {rows}x{cols}")
+    x = (rng(cols).normal(size=(rows, cols)) * 2.0).astype(np.float32)
+    if dt == "f16":
+        xb, xf = f16_round(x)
+        in_t = out_t = hip.F16
+    elif dt == "bf16":
+        xb, xf = bf16_round(x)
+        in_t = out_t = hip.BF16
+    elif dt == "f16_f32":
+        xb, xf = f16_round(x)
+        in_t, out_t = hip.F16, hip.F32
+    else:
+        xb = xf = x
+        in_t = out_t = hip.F32
+    got = _softmax_gpu(hip, xb, in_t, out_t, rows, cols)
+    ref = cpuref.softmax_rows(xf)
+    if out_t == hip.F32:
+        assert_close(got, ref, atol=1e-30, rtol=1e-4, what=f"softmax {dt}")
+    else:
+        rtol = 1e-2
+        assert_close(got, ref, atol=1e-6, rtol=rtol, what=f"softmax {dt}")
+
+
+def test_softmax_padded_rows(hip):
+    say("softmax f16 padded leading dimensions")
+    rows, cols = 20, 1024
+    x = (rng(8).normal(size=(rows, cols + 24)) * 2).astype(np.float32)
+    xb, xf = f16_round(x)
+    got = _softmax_gpu(hip, xb, hip.F16, hip.F16, rows, cols, ldx=cols + 24, ldy=cols + 8)
+    assert_close(got, cpuref.softmax_rows(np.ascontiguousarray(xf[:, :cols])), atol=1e-6,
+                 rtol=1e-2, what="padded")
+
+
+def test_softmax_extremes(hip):
+    say("softmax f32 extremes")
+    x = np.zeros((4, 512), np.float32)
+    x[1] = 7.0                      # constant row -> exactly 1/512
+    x[2, 17] = 80.0                 # one dominant entry
+    x[3] = np.linspace(-60, 60, 512)
+    got = _softmax_gpu(hip, x, hip.F32, hip.F32, 4, 512)
+    ref = cpuref.softmax_rows(x)
+    np.testing.assert_array_equal(got[1], np.float32(1 / 512))
+    assert got[2, 17] == pytest.approx(1.0, rel=1e-6)
+    assert_close(got, ref, atol=1e-30, rtol=1e-4, what="extremes")
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("cols", [8192, 1000, 13])
+def test_reduce_rows(hip, dt, cols):
+    rows = 41
+    say(f"reduce_rows {dt} {rows}x{cols}")
+    x = rng(cols + 1).normal(size=(rows, cols)).astype(np.float32) * 3
+    if dt == "f16":
+        xb, xf = f16_round(x)
+        t = hip.F16
+    elif dt == "bf16":
+        xb, xf = bf16_round(x)
+        t = hip.BF16
+    else:
+        xb = xf = x
+        t = hip.F32
+    dx = hip.DeviceBuffer.from_array(xb)
+    dout = hip.DeviceBuffer(rows * 4)
+    hip.reduce_rows(hip.REDUCE_MAX, t, rows, cols, dx.ptr, cols, dout.ptr)
+    hip.synchronize()
+    # max is order-independent: bit-identical to the reference's fold
+    np.testing.assert_array_equal(dout.download(np.float32, (rows,)),
+                                  cpuref.reduce_rows(xf, cpuref.REDUCE_MAX))
+    hip.reduce_rows(hip.REDUCE_SUM, t, rows, cols, dx.ptr, cols, dout.ptr)
+    hip.synchronize()
+    ref = cpuref.reduce_rows(xf, cpuref.REDUCE_SUM)
+    scale = np.abs(xf).sum(axis=1)
+    got = dout.download(np.float32, (rows,))
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale), np.max(np.abs(got - ref) / scale)

@@ -1,0 +1,342 @@
+"""Pins the CPU oracle (oracle/sile_cpuref.c) before it is trusted as the checker.
+
+Each check is chosen so that a plausible mistake in the restatement (a dropped
+K truncation, a transposed operand, a wrong program-id decode, FMA
+contraction, a reordered sum, a wrong rounding mode) fails at least one of:
+  * the reference's own literal fixtures (tests/golden/reference_fixtures.json),
+  * closed forms (exact integer GEMMs, constant-row softmax, n(n+1)/2),
+  * brute force / float64 recomputation on small inputs,
+  * order-sensitivity probes showing the exact-order claims are not vacuous.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import cpuref
+from tests.helpers import assert_close, rng
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_fixtures.json")
+
+
+@pytest.fixture(scope="module")
+def fixtures():
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+# ---------------------------------------------------------------- matmul (a1, a3)
+
+def test_matmul_reference_fixture(fixtures):
+    fx = fixtures["matmul_4x4"]
+    a = np.array(fx["a"]["data"], np.float32).reshape(fx["a"]["shape"])
+    b = np.array(fx["b"]["data"], np.float32).reshape(fx["b"]["shape"])
+    c = np.array(fx["c_init"]["data"], np.float32).reshape(fx["c_init"]["shape"])
+    cpuref.kernel_matmul(a, b, c, fx["grid"], fx["bm"], fx["bn"], fx["bk"])
+    np.testing.assert_array_equal(c.ravel(), np.array(fx["expected"], np.float32))
+
+
+def test_matmul_program_decode_and_guard():
+    # grid smaller than the tile count: only pids 0..1 run -> tiles (0,0), (0,1)
+    a = np.arange(16, dtype=np.float32).reshape(4, 4)
+    b = np.eye(4, dtype=np.float32)
+    c = np.full((4, 4), -7.0, np.float32)
+    cpuref.kernel_matmul(a, b, c, (2, 1, 1), 2, 2, 2)
+    np.testing.assert_array_equal(c[:2], a[:2])
+    np.testing.assert_array_equal(c[2:], -7.0)
+    # grid larger than the tile count: extra programs are skipped
+    c = np.zeros((4, 4), np.float32)
+    cpuref.kernel_matmul(a, b, c, (100, 1, 1), 2, 2, 2)
+    np.testing.assert_array_equal(c, a)
+    # tile count truncates: c[5,5] with BM=BN=2 covers rows/cols 0..3 only
+    c = np.full((5, 5), 3.0, np.float32)
+    a5 = np.ones((5, 4), np.float32)
+    b5 = np.ones((4, 5), np.float32)
+    cpuref.kernel_matmul(a5, b5, c, (4, 1, 1), 2, 2, 2)
+    np.testing.assert_array_equal(c[:4, :4], 4.0)
+    np.testing.assert_array_equal(c[4, :], 3.0)
+    np.testing.assert_array_equal(c[:, 4], 3.0)
+    assert cpuref.total_tiles([5, 5], 2, 2) == 4
+    assert cpuref.total_tiles([7], 1, 3) == 7
+
+
+def test_matmul_k_truncation():
+    # K = 5, BK = 2 -> k runs over 0..3 only (canonical_matmul.rs:58-73)
+    a = rng(11).integers(-3, 4, size=(4, 5)).astype(np.float32)
+    b = rng(12).integers(-3, 4, size=(5, 4)).astype(np.float32)
+    c = np.zeros((4, 4), np.float32)
+    cpuref.kernel_matmul(a, b, c, (4, 1, 1), 2, 2, 2)
+    np.testing.assert_array_equal(c, a[:, :4] @ b[:4, :])
+    assert not np.array_equal(c, a @ b)
+
+
+def test_matmul_integer_closed_form():
+    # integer data: every partial sum is an exact fp32 integer, so any order gives a @ b
+    a = rng(1).integers(-8, 9, size=(64, 96)).astype(np.float32)
+    b = rng(2).integers(-8, 9, size=(96, 32)).astype(np.float32)
+    c = np.zeros((64, 32), np.float32)
+    cpuref.kernel_matmul(a, b, c, (64 // 16 * 32 // 8, 1, 1), 16, 8, 32)
+    np.testing.assert_array_equal(c, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+def _sequential_f32_gemm(a, b):
+    """Independent numpy statement of the canonical order: a fp32 running sum
+    over k, each step rounding the product and then the add."""
+    s = np.zeros((a.shape[0], b.shape[1]), np.float32)
+    for k in range(a.shape[1]):
+        p = (a[:, k:k + 1] * b[k:k + 1, :]).astype(np.float32)
+        s = (s + p).astype(np.float32)
+    return s
+
+
+def test_matmul_exact_order_random():
+    a = rng(1).uniform(-1, 1, size=(64, 128)).astype(np.float32)
+    b = rng(2).uniform(-1, 1, size=(128, 64)).astype(np.float32)
+    c = np.zeros((64, 64), np.float32)
+    cpuref.kernel_matmul(a, b, c, (4, 1, 1), 32, 32, 32)
+    ref = _sequential_f32_gemm(a, b)
+    np.testing.assert_array_equal(c, ref)
+    # the order is observable: a float64 sum rounded once, or an FMA chain,
+    # differs in the last bits for random data (so the equality above pins it)
+    f64 = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    assert not np.array_equal(c, f64)
+    fma = np.zeros_like(ref)
+    for k in range(a.shape[1]):
+        fma = (fma.astype(np.float64) + a[:, k:k + 1].astype(np.float64) * b[k:k + 1, :]).astype(np.float32)
+    assert not np.array_equal(c, fma)
+    assert_close(c, f64, atol=1e-5, rtol=1e-4, what="fp64 sanity")
+
+
+def test_gemm_nt_matches_kernel_matmul():
+    a = rng(3).uniform(-1, 1, size=(96, 160)).astype(np.float32)
+    b = rng(4).uniform(-1, 1, size=(160, 64)).astype(np.float32)
+    c = np.zeros((96, 64), np.float32)
+    cpuref.kernel_matmul(a, b, c, (1000, 1, 1), 32, 32, 32)
+    c2 = cpuref.gemm_nt(a, np.ascontiguousarray(b.T), bk=32)
+    np.testing.assert_array_equal(c, c2)
+    # sampling: every 2nd row tile of 32 rows
+    c3 = np.full((96, 64), np.nan, np.float32)
+    cpuref.gemm_nt(a, np.ascontiguousarray(b.T), bk=32, bm=32, row_tile_step=2, out=c3)
+    np.testing.assert_array_equal(c3[0:32], c[0:32])
+    np.testing.assert_array_equal(c3[64:96], c[64:96])
+    assert np.isnan(c3[32:64]).all()
+
+
+# ---------------------------------------------------------------- reduce (a4, a5, a8)
+
+def test_reduce_rows_max_and_sequential_sum():
+    x = rng(5).normal(size=(33, 77)).astype(np.float32)
+    np.testing.assert_array_equal(cpuref.reduce_rows(x, cpuref.REDUCE_MAX), x.max(axis=1))
+    seq = np.add.accumulate(x, axis=1, dtype=np.float32)[:, -1]  # left fold from element 0
+    np.testing.assert_array_equal(cpuref.reduce_rows(x, cpuref.REDUCE_SUM), seq)
+
+
+def _vec4_fold(row, unrolled):
+    chunks = len(row) // 4
+    f = np.float32
+    acc = f(0.0)
+    start = 0
+    if unrolled:
+        acc = f(f(f(row[0] + row[1]) + row[2]) + row[3])
+        start = 1
+    for i in range(start, chunks):
+        v = row[4 * i:4 * i + 4]
+        acc = f(acc + f(f(f(v[0] + v[1]) + v[2]) + v[3]))
+    for j in range(chunks * 4, len(row)):
+        acc = f(acc + row[j])
+    return acc
+
+
+@pytest.mark.parametrize("cols", [4, 7, 16, 17, 1000, 1003])
+def test_reduce_rows_vec4_order(cols):
+    x = rng(cols).normal(size=(4, cols)).astype(np.float32) * np.float32(1e3)
+    got = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
+    ref = np.array([_vec4_fold(r, cols <= 16) for r in x], np.float32)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_vec4_order_is_observable():
+    x = rng(9).normal(size=(64, 1000)).astype(np.float32) * np.float32(1e3)
+    v = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
+    s = cpuref.reduce_rows(x, cpuref.REDUCE_SUM)
+    assert not np.array_equal(v, s)
+
+
+def test_parallel_reduce_reference_fixtures(fixtures):
+    fx = fixtures["parallel_reduce_ones"]
+    a = np.full(fx["a"]["shape"], fx["a"]["fill"], np.float32)
+    out = np.zeros(1, np.float32)
+    cpuref.kernel_parallel_reduce(a, out, fx["grid"], fx["tile"])
+    assert abs(out[0] - fx["expected"]) < fx["tolerance_abs"]
+    fx = fixtures["parallel_reduce_arange"]
+    n = fx["a"]["shape"][0]
+    a = np.arange(fx["a"]["arange_from"], fx["a"]["arange_from"] + n, dtype=np.float32)
+    out = np.zeros(1, np.float32)
+    cpuref.kernel_parallel_reduce(a, out, fx["grid"], fx["tile"])
+    assert abs(out[0] - fx["expected"]) <= fx["tolerance_rel"] * fx["expected"]
+    assert fx["expected"] == n * (n + 1) / 2
+
+
+def test_parallel_reduce_partials_order():
+    a = rng(13).normal(size=3000).astype(np.float32)
+    parts = cpuref.parallel_reduce_partials(a, 3, 1000)
+    ref = np.array([_vec4_fold(a[i * 1000:(i + 1) * 1000], False) for i in range(3)], np.float32)
+    np.testing.assert_array_equal(parts, ref)
+    small = cpuref.parallel_reduce_partials(a[:24], 2, 12)  # TILE <= 16: unrolled start
+    ref = np.array([_vec4_fold(a[i * 12:(i + 1) * 12], True) for i in range(2)], np.float32)
+    np.testing.assert_array_equal(small, ref)
+    tiny = cpuref.parallel_reduce_partials(a[:6], 2, 3)  # TILE < 4: plain fold
+    np.testing.assert_array_equal(tiny, np.add.accumulate(a[:6].reshape(2, 3), axis=1, dtype=np.float32)[:, -1])
+
+
+# ---------------------------------------------------------------- softmax (a6, a7)
+
+def test_softmax_reference_fixture(fixtures):
+    fx = fixtures["softmax_4x8"]
+    x = np.array(fx["x"]["data"], np.float32).reshape(fx["x"]["shape"])
+    y = np.zeros_like(x)
+    cpuref.kernel_softmax(x, y, fx["grid"], fx["bm"], fx["bn"])
+    assert np.all(np.abs(y.sum(axis=1) - fx["expected_row_sum"]) < fx["tolerance_abs"])
+    # every row is 0..7 shifted, so every row is the same softmax
+    np.testing.assert_array_equal(y, np.tile(y[0], (4, 1)))
+
+
+def test_softmax_closed_forms():
+    x = np.full((3, 64), 5.25, np.float32)
+    y = cpuref.softmax_rows(x)
+    np.testing.assert_array_equal(y, np.float32(1.0 / 64))
+    # one dominant entry: exp(-inf-like) underflows to 0, the max gets exactly 1
+    x = np.zeros((1, 16), np.float32)
+    x[0, 5] = 200.0
+    y = cpuref.softmax_rows(x)
+    assert y[0, 5] == 1.0 and np.all(np.delete(y[0], 5) == 0.0)
+
+
+def test_softmax_fp64_and_tile_semantics():
+    x = (rng(3).normal(size=(8, 256)) * 2).astype(np.float32)
+    y = cpuref.softmax_rows(x)
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    assert_close(y, e / e.sum(axis=1, keepdims=True), atol=1e-9, rtol=1e-5, what="fp64")
+    # shift invariance is exact up to fp32 rounding of x - m
+    y2 = cpuref.softmax_rows(x + np.float32(3.0))
+    assert_close(y2, y, atol=1e-9, rtol=1e-5, what="shift")
+    # the DSL kernel over [BM, BN] tiles: with BN < row width each tile is
+    # normalised on its own, as the reference program does
+    yt = np.zeros_like(x)
+    cpuref.kernel_softmax(x, yt, (8 * 2, 1, 1), 1, 128)
+    np.testing.assert_array_equal(yt[:, :128], cpuref.softmax_rows(x[:, :128]))
+    np.testing.assert_array_equal(yt[:, 128:], cpuref.softmax_rows(x[:, 128:]))
+
+
+# ---------------------------------------------------------------- attention (a9)
+
+def _attn_fp64(q, k, v, scale, causal):
+    q, k, v = (t.astype(np.float64) for t in (q, k, v))
+    s = q @ k.T * scale
+    if causal:
+        s = np.where(np.tril(np.ones_like(s, dtype=bool)), s, -np.inf)
+    s = s - s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    return (p @ v) / p.sum(axis=1, keepdims=True)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_fp64(causal):
+    q, k, v = (rng(20 + i).normal(size=(96, 32)).astype(np.float32) for i in range(3))
+    o = cpuref.attention_fwd(q, k, v, 1 / np.sqrt(32), causal=causal)
+    assert_close(o, _attn_fp64(q, k, v, 1 / np.sqrt(32), causal), atol=1e-5, rtol=1e-4, what="attn")
+
+
+def test_attention_closed_forms():
+    s, d = 64, 16
+    q, k = (rng(30 + i).normal(size=(s, d)).astype(np.float32) for i in range(2))
+    # constant V rows -> every output row is that constant (weights sum to 1)
+    v = np.tile(rng(32).normal(size=(1, d)).astype(np.float32), (s, 1))
+    o = cpuref.attention_fwd(q, k, v, 0.25, causal=True)
+    assert_close(o, v, atol=1e-6, rtol=1e-6, what="const V")
+    # query 0 sees only key 0: p = exp(0) = 1, l = 1, so o[0] = v[0] exactly
+    v = rng(33).normal(size=(s, d)).astype(np.float32)
+    o = cpuref.attention_fwd(q, k, v, 0.25, causal=True)
+    np.testing.assert_array_equal(o[0], v[0])
+    # zero keys -> uniform weights over the visible prefix: o[i] = mean(v[0..i])
+    o = cpuref.attention_fwd(q, np.zeros_like(k), v, 0.25, causal=True)
+    means = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, s + 1)[:, None]
+    assert_close(o, means, atol=1e-6, rtol=1e-5, what="uniform")
+    # causality: keys/values after row i do not change row i
+    k2, v2 = k.copy(), v.copy()
+    k2[40:] = 100.0
+    v2[40:] = -100.0
+    o2 = cpuref.attention_fwd(q, k2, v2, 0.25, causal=True)
+    np.testing.assert_array_equal(o2[:40], cpuref.attention_fwd(q, k, v, 0.25)[:40])
+    # row sampling computes exactly the requested rows
+    part = cpuref.attention_fwd(q, k, v, 0.25, q_begin=10, q_end=20)
+    full = cpuref.attention_fwd(q, k, v, 0.25)
+    np.testing.assert_array_equal(part[10:20], full[10:20])
+    assert np.all(part[:10] == 0) and np.all(part[20:] == 0)
+
+
+# ---------------------------------------------------------------- number formats
+
+def _e4m3_table():
+    vals = []
+    for code in range(256):
+        s, e, m = code >> 7, (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            vals.append(np.nan)
+            continue
+        mag = m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+        vals.append(-mag if s else mag)
+    return np.array(vals)
+
+
+def test_e4m3_decode_table():
+    table = _e4m3_table()
+    got = cpuref.e4m3_decode(np.arange(256, dtype=np.uint8))
+    finite = ~np.isnan(table)
+    np.testing.assert_array_equal(got[finite], table[finite].astype(np.float32))
+    assert np.isnan(got[0x7F]) and np.isnan(got[0xFF])
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and got[0x08] == 2.0 ** -6 and got[0x38] == 1.0
+
+
+def test_e4m3_encode_round_trip_and_rne():
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    vals = cpuref.e4m3_decode(codes)
+    back = cpuref.e4m3_encode(vals)
+    np.testing.assert_array_equal(back, codes)
+    # brute-force nearest-even against the table for random values
+    table = _e4m3_table()
+    pos = np.array([c for c in range(0, 0x7F)])  # positive finite codes, ascending value
+    x = np.abs(rng(40).normal(size=20000) * 60).astype(np.float32)
+    x = np.concatenate([x, ((table[pos][1:] + table[pos][:-1]) / 2).astype(np.float32)])  # exact midpoints
+    got = cpuref.e4m3_encode(x)
+    for xi, gi in zip(x, got):
+        if xi >= 448:
+            assert gi == 0x7E
+            continue
+        d = np.abs(table[pos] - xi)
+        best = np.flatnonzero(d == d.min())
+        want = best[0] if len(best) == 1 else best[np.argmin(pos[best] & 1)]  # tie -> even mantissa
+        assert gi == pos[want], (xi, gi, pos[want])
+    assert cpuref.e4m3_encode(np.array([1e6, -1e6], np.float32)).tolist() == [0x7E, 0xFE]
+    # the division form q = rne_sat(x / s) is used for the per-tensor scale
+    assert cpuref.e4m3_encode(np.array([3.0], np.float32), 0.5)[0] == cpuref.e4m3_encode(np.array([6.0], np.float32))[0]
+
+
+def test_bf16_rne():
+    x = rng(41).normal(size=50000).astype(np.float32)
+    x = np.concatenate([x, np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -0.0, np.inf], np.float32)])
+    got = cpuref.bf16_from_f32(x)
+    bits = x.view(np.uint32).astype(np.uint64)
+    lo = (bits >> 16).astype(np.uint64)
+    with np.errstate(invalid="ignore"):
+        cand_lo = (lo << 16).astype(np.uint32).view(np.float32).astype(np.float64)
+        cand_hi = ((lo + 1) << 16).astype(np.uint32).view(np.float32).astype(np.float64)
+        xd = x.astype(np.float64)
+        d_lo, d_hi = np.abs(xd - cand_lo), np.abs(cand_hi - xd)
+    want = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, lo + 1, np.where(lo % 2 == 0, lo, lo + 1)))
+    finite = np.isfinite(x)
+    np.testing.assert_array_equal(got[finite], want[finite].astype(np.uint16))
+    assert got[-1] == 0x7F80 and got[-2] == 0x8000
+    assert got[-4] == 0x3F80 and got[-3] == 0x3F82  # ties to even
