@@ -27,7 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-KERNELS = ["dsl", "softmax", "gemm", "attention"]
+KERNELS = ["dsl", "softmax", "gemm", "attention", "flash_attn"]
 HOST_SOURCES = ["runtime.cpp", "ops.cpp"]
 
 # Device code: gfx950 only; packed-fp32 instructions disabled (the compiler

@@ -1,0 +1,323 @@
+// Flash-attention forward on the gfx950 matrix cores, head_dim 128.
+//
+//   O = softmax(Q K^T * scale [+ causal mask]) V     Q, K, V, O: [B*H, S, 128] 16-bit
+//
+// sile's DSL has no attention kernel (no mask, iota or transpose); this is
+// the composition of its tile ops MmaF, ReduceMax, Exp, ReduceSum and the
+// softmax Map (crates/sile-tile-ir/src/ir.rs:128-262) fused into one pass
+// with an fp32 online softmax (running max m, running sum l, rescaled
+// accumulator), so S and P never leave registers.
+//
+// Work split: a workgroup of 4 waves owns a block of 4 * kQT * 32 queries of
+// one (batch, head); each wave owns kQT * 32 of them.  The workgroup walks the
+// keys in blocks of kNK, staged through LDS (double-buffered: the next block's
+// global loads are in flight while the matrix cores work on the current one).
+//
+// Orientation of the two products (v_mfma_f32_32x32x16_{f16,bf16}):
+//   * S^T = K . Q^T : the A operand is K (rows = keys, k = d, read from LDS),
+//     the B operand Q^T (k = d, cols = queries, kept in registers for the
+//     whole kernel).  The accumulator of lane l holds 16 keys of ONE query
+//     (l % 32), so the online-softmax max and sum are in-register folds plus
+//     one exchange with lane l ^ 32 for the max.
+//   * O^T = V^T . P^T : the A operand is V^T (rows = d, k = keys), the B
+//     operand P^T straight from the S^T accumulators converted to 16 bits.
+//     The output accumulator of lane l again holds one query (l % 32), so the
+//     rescale by exp(m_old - m_new) is a per-lane scalar.
+//   32x32 accumulator layout: register i of lane l is row 8*(i/4) + 4*(l/32) + i%4,
+//   column l % 32.  A/B operand: lane l supplies row/column l % 32 and 8
+//   consecutive k slots of k-group l / 32.
+//   P's 8 values for k-group g of a 16-key chunk are the keys
+//   {4g..4g+3, 8+4g..8+4g+3} of that chunk (accumulator rows).  V^T is
+//   therefore stored in LDS with bits 2 and 3 of the key index swapped inside
+//   every 16-key chunk, so that k-group g reads its 8 keys as one 16-byte
+//   vector.  V is transposed while it is written to LDS (4 keys x 1 d packed
+//   per 8-byte store).
+//
+// LDS layout per stage: K [kNK][256 B] with 16-byte chunk c of row r at
+// c ^ (r & 15); V^T [128][kNK * 2 B] with chunk c of row d at c ^ swz8(d).
+// Both make the fragment reads (one row per lane) conflict-free.
+//
+// Launch order: workgroups are dispatched round-robin over the 8 XCDs, so
+// workgroup i runs on XCD i % 8.  Head h is pinned to XCD h % 8 and its query
+// blocks are issued together (largest causal block first), so the K/V stream
+// of a head is shared in one XCD's L2 by all of its query blocks.
+#include "common.h"
+
+using namespace sile;
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kRowB = kD * 2;  // bytes of one K row
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+template <bool kBF16>
+SILE_DEV f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (kBF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <bool kBF16>
+SILE_DEV uint32_t pack2(float lo, float hi) {
+  return kBF16 ? pack_bf16x2(lo, hi) : pack_f16x2(lo, hi);
+}
+
+SILE_DEV int swz8(int d) { return (d ^ (d >> 3)) & 7; }
+// bits 2 and 3 of a key index swapped
+SILE_DEV int kperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+struct AttnArgs {
+  int64_t seq;          // S
+  int32_t bh;           // B * H
+  int32_t q_blocks;     // S / kBQ
+  float scale_log2;     // softmax scale * log2(e)
+  int32_t causal;
+  int32_t xcd_map;      // 1: head-per-XCD launch order (bh % 8 == 0)
+};
+
+template <bool kBF16, int kQT, int kNK>
+__device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
+                                              const uint16_t* __restrict__ K,
+                                              const uint16_t* __restrict__ V,
+                                              uint16_t* __restrict__ O, const AttnArgs& a,
+                                              uint8_t* smem) {
+  constexpr int kBQ = kWaves * kQT * 32;
+  constexpr int kKT = kNK / 32;                     // 32-key tiles per block
+  constexpr int kKBytes = kNK * kRowB;              // K stage bytes
+  constexpr int kVRowB = kNK * 2;                   // V^T row bytes
+  constexpr int kStageB = 2 * kKBytes;              // K + V^T (same size)
+  constexpr int kKLoads = kNK * 16 / kThreads;      // 16-byte K chunks per thread
+  constexpr int kVItems = kNK * 4 / kThreads;       // (4 keys x 8 d) items per thread
+  static_assert(kKLoads >= 1 && kVItems >= 1, "block too small for the workgroup");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+
+  // ---- which (head, query block) ----
+  int bh, qb;
+  const int bid = blockIdx.x;
+  if (a.xcd_map) {
+    const int xcd = bid & 7, idx = bid >> 3;
+    bh = ((idx / a.q_blocks) << 3) + xcd;
+    qb = idx % a.q_blocks;
+  } else {
+    bh = bid % a.bh;
+    qb = bid / a.bh;
+  }
+  if (a.causal) qb = a.q_blocks - 1 - qb;  // largest causal blocks first
+  const int64_t S = a.seq;
+  const int64_t head_off = (int64_t)bh * S * kD;
+  const uint16_t* Qh = Q + head_off;
+  const uint8_t* Kh = reinterpret_cast<const uint8_t*>(K + head_off);
+  const uint8_t* Vh = reinterpret_cast<const uint8_t*>(V + head_off);
+  const int q0 = qb * kBQ;
+  const int wq0 = q0 + wave * kQT * 32;  // first query of this wave
+
+  // ---- Q^T fragments: lane holds query wq0 + 32 qt + l32, d = 16 kk + 8 g + [0, 8) ----
+  u32x4 qf[kQT][8];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    const uint16_t* qrow = Qh + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
+  }
+
+  // ---- K / V global -> register staging ----
+  // K: thread moves chunk (tid & 15) of rows (tid >> 4) + 16 i.
+  // V: item (key group kg = 4 keys, d chunk dc = 8 d): dc = tid & 15, kg = (tid >> 4) + 16 i.
+  const int k_chunk = tid & 15, k_row = tid >> 4;
+  u32x4 kreg[kKLoads];
+  u32x4 vreg[kVItems][4];
+  auto global_load = [&](int kb) {
+    const uint8_t* kp = Kh + (int64_t)kb * kRowB;
+    const uint8_t* vp = Vh + (int64_t)kb * kRowB;
+#pragma unroll
+    for (int i = 0; i < kKLoads; ++i)
+      kreg[i] = *reinterpret_cast<const u32x4*>(kp + (k_row + 16 * i) * kRowB + k_chunk * 16);
+#pragma unroll
+    for (int i = 0; i < kVItems; ++i) {
+      const int kg = k_row + 16 * i;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vreg[i][r] = *reinterpret_cast<const u32x4*>(vp + (4 * kg + r) * kRowB + k_chunk * 16);
+    }
+  };
+  auto lds_store = [&](int stage) {
+    uint8_t* ks = smem + stage * kStageB;
+    uint8_t* vs = ks + kKBytes;
+#pragma unroll
+    for (int i = 0; i < kKLoads; ++i) {
+      const int row = k_row + 16 * i;
+      *reinterpret_cast<u32x4*>(ks + row * kRowB + ((k_chunk ^ (row & 15)) << 4)) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kVItems; ++i) {
+      const int kg = k_row + 16 * i;
+      const int kp = kperm(4 * kg);          // 4 keys stay contiguous
+      const int chunk = kp >> 3, half = (kp >> 2) & 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * k_chunk + e;
+        const int w = e >> 1, sh = (e & 1) * 16;
+        const uint32_t v0 = (vreg[i][0][w] >> sh) & 0xffffu, v1 = (vreg[i][1][w] >> sh) & 0xffffu;
+        const uint32_t v2 = (vreg[i][2][w] >> sh) & 0xffffu, v3 = (vreg[i][3][w] >> sh) & 0xffffu;
+        const u32x2 pk = {v0 | (v1 << 16), v2 | (v3 << 16)};
+        *reinterpret_cast<u32x2*>(vs + d * kVRowB + ((chunk ^ swz8(d)) << 4) + 8 * half) = pk;
+      }
+    }
+  };
+
+  f32x16 oacc[kQT][4];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
+  float m_run[kQT], l_run[kQT];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    m_run[qt] = -__builtin_inff();
+    l_run[qt] = 0.0f;
+  }
+
+  const int nblocks = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
+  const float c = a.scale_log2;
+
+  global_load(0);
+  lds_store(0);
+  __syncthreads();
+
+  for (int jb = 0; jb < nblocks; ++jb) {
+    const int stage = jb & 1;
+    const int kb = jb * kNK;
+    if (jb + 1 < nblocks) global_load(kb + kNK);
+    const bool active = !a.causal || kb <= wq0 + kQT * 32 - 1;
+    if (active) {
+      const uint8_t* ks = smem + stage * kStageB;
+      const uint8_t* vs = ks + kKBytes;
+      // ---- S^T = K . Q^T ----
+      f32x16 sacc[kKT][kQT];
+#pragma unroll
+      for (int t = 0; t < kKT; ++t)
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[t][qt][i] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < kKT; ++t) {
+        const int row = 32 * t + l32;
+        const uint8_t* krow = ks + row * kRowB;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + (((2 * kk + g) ^ (row & 15)) << 4));
+#pragma unroll
+          for (int qt = 0; qt < kQT; ++qt) sacc[t][qt] = mma32<kBF16>(kf, qf[qt][kk], sacc[t][qt]);
+        }
+      }
+      // ---- causal mask on the diagonal blocks ----
+      if (a.causal && kb + kNK - 1 > wq0) {
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          const int q = wq0 + 32 * qt + l32;
+#pragma unroll
+          for (int t = 0; t < kKT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int key = kb + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
+              if (key > q) sacc[t][qt][i] = -__builtin_inff();
+            }
+        }
+      }
+      // ---- online softmax ----
+      u32x4 pf[kQT][kKT * 2];
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < kKT; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmax_ordered(mx, sacc[t][qt][i]);
+        mx = fmax_ordered(mx, xor32(mx));
+        const float m_new = fmax_ordered(m_run[qt], mx);
+        const float mc = m_new * c;
+        const float alpha = exp2_fast(m_run[qt] * c - mc);
+        m_run[qt] = m_new;
+        float rs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kKT; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float p = exp2_fast(__builtin_fmaf(sacc[t][qt][i], c, -mc));
+            sacc[t][qt][i] = p;
+            rs += p;
+          }
+        l_run[qt] = l_run[qt] * alpha + rs;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha;
+#pragma unroll
+        for (int t = 0; t < kKT; ++t)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              w[j] = pack2<kBF16>(sacc[t][qt][8 * h + 2 * j], sacc[t][qt][8 * h + 2 * j + 1]);
+            pf[qt][2 * t + h] = w;
+          }
+      }
+      // ---- O^T += V^T . P^T ----
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int d = 32 * dt + l32;
+        const uint8_t* vrow = vs + d * kVRowB;
+#pragma unroll
+        for (int cc = 0; cc < kKT * 2; ++cc) {
+          const u32x4 vf =
+              *reinterpret_cast<const u32x4*>(vrow + (((2 * cc + g) ^ swz8(d)) << 4));
+#pragma unroll
+          for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oacc[qt][dt]);
+        }
+      }
+    }
+    if (jb + 1 < nblocks) lds_store(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    const float l = l_run[qt] + xor32(l_run[qt]);
+    const float inv = 1.0f / l;
+    const int q = wq0 + 32 * qt + l32;
+    uint16_t* orow = O + head_off + (int64_t)q * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 32 * dt + 8 * r + 4 * g;
+        const f32x16& acc = oacc[qt][dt];
+        const u32x2 w = {pack2<kBF16>(acc[4 * r] * inv, acc[4 * r + 1] * inv),
+                         pack2<kBF16>(acc[4 * r + 2] * inv, acc[4 * r + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+  }
+}
+
+}  // namespace
+
+#define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
+  extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \
+      const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * NK * kRowB];                 \
+    attn_fwd_body<BF, QT, NK>(Q, K, V, O, a, smem);                                           \
+  }
+
+SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k64, false, 1, 64)
+SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q2_k64, false, 2, 64)
+SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k64, true, 1, 64)

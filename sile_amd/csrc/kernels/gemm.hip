@@ -16,7 +16,9 @@
 //     2 stages x 64 KiB), one barrier per k-step; the next k-step's global loads
 //     are in flight while the matrix cores work on the current one;
 //   * LDS rows are 128 bytes = 8 chunks of 16 bytes; chunk c of row r is stored
-//     at chunk position c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, which makes
+//     at chunk position c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1), a function
+//     of r mod 16 only (the loaders' rows differ by multiples of 32 and the
+//     fragment readers' by multiples of 16, so each side needs one value), which makes
 //     the 16-lane fragment reads (16 rows, one chunk column) and the tile
 //     writes (8 lanes per row) hit distinct banks;
 //   * the MFMA is issued with the B fragment as the first operand, so the
@@ -42,7 +44,7 @@ constexpr int kLoadsPerThread = kTileBytes / 16 / kThreads;  // 8 x 16-byte chun
 enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
 enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
 
-SILE_DEV int swz(int r) { return (r ^ (r >> 3)) & 7; }
+SILE_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 template <int kKind>
 struct Mfma;
@@ -127,7 +129,7 @@ __device__ __forceinline__ void gemm_nt_body(const uint8_t* __restrict__ A,
   const uint8_t* a_src = A + ((int64_t)tile_m * kBM + ld_row) * a_row_stride + ld_chunk * 16;
   const uint8_t* b_src = B + ((int64_t)tile_n * kBN + ld_row) * b_row_stride + ld_chunk * 16;
   const int64_t a_step32 = 32 * a_row_stride, b_step32 = 32 * b_row_stride;
-  const int st_off = ld_row * kRowBytes + ((ld_chunk ^ swz(ld_row)) << 4);  // + 32*i rows: same swz
+  const int st_off = ld_row * kRowBytes + ((ld_chunk ^ swz(ld_row)) << 4);  // rows + 32 i: same r mod 16
 
   // ---- fragment read addressing ----
   const int fr_row = lane & 15, fr_q = lane >> 4;

@@ -46,7 +46,10 @@ struct Elem<kF16> {
     const u32x4 w = *reinterpret_cast<const u32x4*>(p);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const f16x2 h = __builtin_bit_cast(f16x2, w[i]);
+      // copy the element out first: hipcc's __builtin_bit_cast of an
+      // ext_vector element reads element 0 whatever the index
+      const uint32_t u = w[i];
+      const f16x2 h = __builtin_bit_cast(f16x2, u);
       v[2 * i] = (float)h[0];
       v[2 * i + 1] = (float)h[1];
     }

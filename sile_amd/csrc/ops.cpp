@@ -6,6 +6,8 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "runtime_internal.h"
@@ -329,6 +331,35 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (head_dim > 256) return fail(SILE_ERR_UNSUPPORTED_BACKEND, "head_dim > 256 not supported");
   hipStream_t s = static_cast<hipStream_t>(stream);
   int64_t bh = batch * heads;
+  if (bh > 0x7fffffffLL / std::max<int64_t>(seq_len, 1))
+    return fail(SILE_ERR_SHAPE, "attention too large");
+
+  // MFMA flash kernel: head_dim 128, S a multiple of the query block, 16-byte
+  // aligned operands.  kQT = 2 (256-query blocks) for f16 when S allows it.
+  if (head_dim == 128 && seq_len % 128 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+      aligned16(o)) {
+    int qt = 1;
+    if (dtype == SILE_F16 && seq_len % 256 == 0) {
+      const char* e = getenv("SILE_HIP_FA_QT");  // tile-variant override (tuning, tests)
+      qt = (e && atoi(e) == 2) ? 2 : 1;
+    }
+    const int64_t bq = 128 * qt;
+    struct {
+      int64_t seq;
+      int32_t bh, q_blocks;
+      float scale_log2;
+      int32_t causal, xcd_map;
+    } fa{seq_len, (int32_t)bh, (int32_t)(seq_len / bq), scale * 1.4426950408889634f,
+         causal ? 1 : 0, (bh % 8 == 0) ? 1 : 0};
+    const int64_t blocks = bh * (seq_len / bq);
+    char name[64];
+    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q%d_k64",
+             dtype == SILE_F16 ? "f16" : "bf16", qt);
+    void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
+    int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(256), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+
   const int64_t rows = bh * seq_len;
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "attention too large");

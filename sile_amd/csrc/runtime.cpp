@@ -39,6 +39,7 @@ SILE_EMBED(sile_co_dsl, "dsl.hsaco")
 SILE_EMBED(sile_co_softmax, "softmax.hsaco")
 SILE_EMBED(sile_co_gemm, "gemm.hsaco")
 SILE_EMBED(sile_co_attention, "attention.hsaco")
+SILE_EMBED(sile_co_flash_attn, "flash_attn.hsaco")
 
 namespace sile_rt {
 namespace {
@@ -54,6 +55,7 @@ const Image kImages[static_cast<int>(Module::kCount)] = {
     {sile_co_softmax_begin, sile_co_softmax_end, "softmax"},
     {sile_co_gemm_begin, sile_co_gemm_end, "gemm"},
     {sile_co_attention_begin, sile_co_attention_end, "attention"},
+    {sile_co_flash_attn_begin, sile_co_flash_attn_end, "flash_attn"},
 };
 
 struct DeviceState {

@@ -27,7 +27,14 @@ int hip_fail(hipError_t e, const char* what);
   } while (0)
 
 // The gfx950 code objects built into the library.
-enum class Module : int { kDsl = 0, kSoftmax = 1, kGemm = 2, kAttention = 3, kCount = 4 };
+enum class Module : int {
+  kDsl = 0,
+  kSoftmax = 1,
+  kGemm = 2,
+  kAttention = 3,
+  kFlashAttn = 4,
+  kCount = 5
+};
 
 // Makes sure the current device is initialised and its code objects are
 // loaded; returns a status.

@@ -66,3 +66,40 @@ def test_attention_config4_sampled(hip, s):
             sl = slice(blk * 128, blk * 128 + 128)
             assert_close(got[0, hi, sl], ref[sl], atol=ATOL, rtol=RTOL, what=f"h{hi} blk{blk}")
     assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("qt", ["1", "2"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_variants_xcd_order(hip, monkeypatch, qt, causal):
+    """MFMA flash kernel on B*H = 8 heads (head-per-XCD launch order) for both
+    query-tile variants (128- and 256-query blocks); every head and query is
+    compared with the fp32 oracle."""
+    monkeypatch.setenv("SILE_HIP_FA_QT", qt)
+    b, h, s, d = 2, 4, 512, 128
+    say(f"flash f16 qt={qt} causal={causal} B={b} H={h} S={s}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, "f16", seed=21)
+    got = _run(hip, "f16", b, h, s, d, [x[0] for x in qkv], causal, scale)
+    qf, kf, vf = (x[1] for x in qkv)
+    for bi in range(b):
+        for hi in range(h):
+            ref = cpuref.attention_fwd(qf[bi, hi], kf[bi, hi], vf[bi, hi], scale, causal=causal)
+            assert_close(got[bi, hi], ref, atol=ATOL, rtol=RTOL, what=f"attn b{bi} h{hi}")
+
+
+def test_flash_causal_row_independence(hip):
+    """Causality: changing keys/values after position p leaves rows <= p unchanged."""
+    b, h, s, d = 1, 8, 256, 128
+    say("flash causal independence")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, "f16", seed=31)
+    bits = [x[0].copy() for x in qkv]
+    first = _run(hip, "f16", b, h, s, d, bits, True, scale)
+    p = 150
+    r = rng(99)
+    for t in (1, 2):
+        bits[t][:, :, p + 1:] = r.integers(0x3000, 0x3c00, size=bits[t][:, :, p + 1:].shape,
+                                           dtype=np.uint16)
+    second = _run(hip, "f16", b, h, s, d, bits, True, scale)
+    assert np.array_equal(first[:, :, :p + 1], second[:, :, :p + 1])
+    assert not np.array_equal(first[:, :, p + 1:], second[:, :, p + 1:])
