@@ -71,25 +71,38 @@ def normal(seed, shape, scale=1.0):
 # ---------------------------------------------------------------- timing
 
 def time_launches(launch, steps, warmup, stream, rotate=1):
-    """Runs `launch(i)` warmup + steps times; returns per-launch event times (ms)
-    of the timed steps and the wall time of the timed region (s)."""
+    """Runs `launch(i)` warmup + steps times on `stream`; returns the duration
+    in ms of the timed region, measured with HIP events recorded on `stream`
+    before the first and after the last timed launch.  The launches run
+    back to back, so region / steps is the kernel's average launch duration
+    (events around every launch would add their own overhead to a 50 us
+    kernel).  The timed region is bracketed by a device synchronisation on
+    both sides."""
     for i in range(warmup):
         launch(i % rotate)
     hip.synchronize()
-    evs = [(hip.Event(), hip.Event()) for _ in range(steps)]
-    hip.synchronize()
-    t0 = time.perf_counter()
+    r0, r1 = hip.Event(), hip.Event()
+    r0.record(stream)
     for i in range(steps):
-        evs[i][0].record(stream)
         launch(i % rotate)
-        evs[i][1].record(stream)
+    r1.record(stream)
     hip.synchronize()
-    wall = time.perf_counter() - t0
-    ms = [a.elapsed_ms(b) for a, b in evs]
-    for a, b in evs:
-        a.close()
-        b.close()
-    return np.array(ms), wall
+    region_ms = r0.elapsed_ms(r1)
+    r0.close()
+    r1.close()
+    return region_ms
+
+
+def summarise(name, work, unit_scale, unit, region_ms, steps, bound, peak, traffic):
+    """value: work per step over the timed region; roofline.achieved: the
+    algorithmic work of one launch over the average launch duration (the same
+    quantity here, since a step is one launch)."""
+    per_step = region_ms / steps
+    value = work / (per_step * 1e-3) / unit_scale
+    return {
+        "name": name, "value": round(value, 2), "unit": unit, "ms_per_step": round(per_step, 4),
+        "roofline": roofline_obj(bound, value, peak, unit, traffic),
+    }
 
 
 def load_traffic():
@@ -110,12 +123,15 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
     m = n = k = size
     log(f"[bench] {name}: generating inputs")
     if kind == "fp8":
-        from oracle import cpuref  # quantisation recipe only (inputs), not measured
+        # per-tensor e4m3fn quantisation of the seeded inputs (the input
+        # recipe of the fp8 configuration; not part of the timed work)
+        from oracle import cpuref
         a = normal(9, (m, k))
         b = normal(10, (n, k))
         sa = float(np.float32(np.abs(a).max() / 448.0))
         sb = float(np.float32(np.abs(b).max() / 448.0))
         a_bits, b_bits = cpuref.e4m3_encode(a, sa), cpuref.e4m3_encode(b, sb)
+        del a, b
         t, c_t = hip.F8E4M3, hip.BF16
     else:
         a_bits = bf16_bits(normal(4, (m, k), 1 / np.sqrt(k)))
@@ -131,16 +147,11 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
                  dc.ptr, n, sa, sb, 0, stream)
 
     log(f"[bench] {name}: timing {steps} steps")
-    ms, wall = time_launches(launch, steps, warmup, stream)
+    region = time_launches(launch, steps, warmup, stream)
     flop = 2.0 * m * n * k
-    med = float(np.median(ms))
-    tflops = flop / (med * 1e-3) / 1e12
-    peak = PEAK_TFLOPS[kind]
-    res = {
-        "name": name, "value": round(tflops, 2), "unit": "TFLOP/s", "ms_median": round(med, 4),
-        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "flop": flop,
-        "roofline": roofline_obj("mfma", tflops, peak, "TFLOP/s", traffic.get(name)),
-    }
+    res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "mfma", PEAK_TFLOPS[kind],
+                    traffic.get(name))
+    res["flop_per_launch"] = flop
     for buf in (da, db, dc):
         buf.close()
     return res
@@ -162,17 +173,13 @@ def bench_attention(name, s, steps, warmup, stream, traffic):
                            scale, True, stream)
 
     log(f"[bench] {name}: timing {steps} steps")
-    ms, wall = time_launches(launch, steps, warmup, stream)
-    # unmasked (query, key) pairs only: 2 GEMMs x 2 flop x D per pair
+    region = time_launches(launch, steps, warmup, stream)
+    # unmasked (query, key) pairs only: 2 products x 2 flop x D per pair
     flop = 4.0 * d * b * h * s * (s + 1) / 2
-    med = float(np.median(ms))
-    tflops = flop / (med * 1e-3) / 1e12
-    res = {
-        "name": name, "value": round(tflops, 2), "unit": "TFLOP/s", "ms_median": round(med, 4),
-        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "flop": flop,
-        "flop_convention": "4*D*B*H*S*(S+1)/2 (causal pairs only)",
-        "roofline": roofline_obj("mfma", tflops, PEAK_TFLOPS["f16"], "TFLOP/s", traffic.get(name)),
-    }
+    res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "mfma", PEAK_TFLOPS["f16"],
+                    traffic.get(name))
+    res["flop_per_launch"] = flop
+    res["flop_convention"] = "4*D*B*H*S*(S+1)/2 (causal pairs only)"
     for buf in bufs + [do]:
         buf.close()
     return res
@@ -193,23 +200,44 @@ def bench_softmax(name, steps, warmup, stream, traffic):
         hip.softmax_rows(hip.F16, hip.F16, rows, cols, xs[i].ptr, cols, ys[i].ptr, cols, stream)
 
     log(f"[bench] {name}: timing {steps} steps")
-    ms, wall = time_launches(launch, steps, warmup, stream, rotate=rotate)
+    region = time_launches(launch, steps, warmup, stream, rotate=rotate)
     nbytes = 4.0 * rows * cols  # read 2 B + write 2 B per element
-    med = float(np.median(ms))
-    gbs = nbytes / (med * 1e-3) / 1e9
-    res = {
-        "name": name, "value": round(gbs, 1), "unit": "GB/s", "ms_median": round(med, 4),
-        "ms_mean": round(float(ms.mean()), 4), "wall_s": round(wall, 4), "bytes": nbytes,
-        "roofline": roofline_obj("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic.get(name)),
-    }
+    res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS,
+                    traffic.get(name))
+    res["bytes_per_launch"] = nbytes
     for buf in xs + ys:
         buf.close()
     return res
 
 
-def cpu_baseline(budget_rows_step=8):
+def bench_copy_calibration(name, steps, warmup):
+    """A plain device-to-device copy of COPY_BYTES (the HIP runtime's blit
+    kernel behind sile_hip_memcpy_dtod).  Run under rocprofv3 --pmc it gives
+    the FETCH_SIZE / WRITE_SIZE that a kernel moving exactly COPY_BYTES each
+    way reports, the scale used to turn the other kernels' counters into
+    bytes."""
+    src, dst = hip.DeviceBuffer(COPY_BYTES), hip.DeviceBuffer(COPY_BYTES)
+    src.fill_bytes(1)
+    for _ in range(warmup):
+        hip.call("sile_hip_memcpy_dtod", dst.ptr, src.ptr, COPY_BYTES)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        hip.call("sile_hip_memcpy_dtod", dst.ptr, src.ptr, COPY_BYTES)
+    hip.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    src.close()
+    dst.close()
+    return {"name": name, "value": round(2 * COPY_BYTES / dt / 1e9, 1), "unit": "GB/s",
+            "ms_per_step": round(dt * 1e3, 4), "bytes_each_way": COPY_BYTES}
+
+
+COPY_BYTES = 512 << 20
+
+
+def cpu_baseline(row_tile_step=1):
     """CPU oracle on a deterministic sample of the bf16 GEMM 8192^3 workload:
-    every `budget_rows_step`-th 256-row tile of C (all 8192 columns, full K),
+    every `row_tile_step`-th 256-row tile of C (all 8192 columns, full K),
     inputs up-cast from the same bf16 data."""
     from oracle import cpuref
 
@@ -218,25 +246,69 @@ def cpu_baseline(budget_rows_step=8):
     a = cpuref.f32_from_bf16(bf16_bits(normal(4, (m, k), 1 / np.sqrt(k))))
     b = cpuref.f32_from_bf16(bf16_bits(normal(5, (n, k), 1 / np.sqrt(k))))
     c = np.zeros((m, n), np.float32)
-    tiles = (m // 256 + budget_rows_step - 1) // budget_rows_step
+    tiles = (m // 256 + row_tile_step - 1) // row_tile_step
     rows = tiles * 256
     log(f"[bench] cpu baseline: {rows} rows x {n} cols x {k} k on {cpuref.num_threads()} threads")
     t0 = time.perf_counter()
-    cpuref.gemm_nt(a, b, bm=256, row_tile_step=budget_rows_step, out=c)
+    cpuref.gemm_nt(a, b, bm=256, row_tile_step=row_tile_step, out=c)
     dt = time.perf_counter() - t0
     flop = 2.0 * rows * n * k
     return {
         "value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cpuref.num_threads(),
         "kind": "port",
-        "sample": (f"bf16 GEMM 8192^3 on up-cast fp32 inputs, every {budget_rows_step}th "
-                   f"256-row tile of C ({rows} of {m} rows, all columns, full K): {flop:.3e} "
-                   f"flop in {dt:.2f} s; oracle = canonical-matmul loop nest, gcc -O2 -fopenmp"),
+        "sample": ((f"every {row_tile_step}th 256-row tile of C ({rows} of {m} rows, all "
+                    "columns, full K)" if row_tile_step > 1 else "the whole GEMM")
+                   + f" of bf16 GEMM 8192^3 on up-cast fp32 inputs: {flop:.3e} flop in {dt:.2f} s;"
+                   " oracle = canonical-matmul loop nest (sequential fp32 mul-then-add per cell),"
+                   " gcc -O2 -fopenmp"),
         "seconds": round(dt, 3),
     }
 
 
+# ---------------------------------------------------------------- PMC traffic
+
+def traffic_from_pmc(root):
+    """Builds profiles/traffic.json from rocprofv3 --pmc runs of this script,
+    one per workload and counter: ROOT/pmc_fetch_<name>/ (FETCH_SIZE) and
+    ROOT/pmc_write_<name>/ (WRITE_SIZE), <name> being a workload of ALL or
+    copy_calibration.  The mean per-dispatch KiB of the workload's kernel is
+    scaled by what the same counter reads for the copy calibration (COPY_BYTES
+    each way): bytes = KiB * COPY_BYTES / copy_KiB."""
+    import csv
+    import glob
+
+    def mean_kib(d, counter, want):
+        vals = []
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    if row.get("Counter_Name") == counter and want(row["Kernel_Name"]):
+                        vals.append(float(row["Counter_Value"]))
+        return sum(vals) / len(vals) if vals else None
+
+    def is_copy(k):
+        return "copyBuffer" in k
+
+    cf = mean_kib(os.path.join(root, "pmc_fetch_copy_calibration"), "FETCH_SIZE", is_copy)
+    cw = mean_kib(os.path.join(root, "pmc_write_copy_calibration"), "WRITE_SIZE", is_copy)
+    if not cf or not cw:
+        raise SystemExit("no copy-calibration dispatches found under " + root)
+    sf, sw = COPY_BYTES / (cf * 1024), COPY_BYTES / (cw * 1024)
+    out = {"_scale": {"fetch": round(sf, 4), "write": round(sw, 4), "copy_bytes": COPY_BYTES,
+                      "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1)}}
+    for name in ALL:
+        def is_sile(k):
+            return k.startswith("sile_")
+        f = mean_kib(os.path.join(root, "pmc_fetch_" + name), "FETCH_SIZE", is_sile)
+        w = mean_kib(os.path.join(root, "pmc_write_" + name), "WRITE_SIZE", is_sile)
+        if f is not None and w is not None:
+            out[name] = round(f * 1024 * sf + w * 1024 * sw)
+    return out
+
+
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
+EXTRA = ["copy_calibration"]
 
 
 def main():
@@ -244,12 +316,21 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", nargs="*", default=None, choices=ALL)
+    ap.add_argument("--only", nargs="*", default=None, choices=ALL + EXTRA)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-from", metavar="PMC_ROOT",
+                    help="write profiles/traffic.json from rocprofv3 --pmc runs and exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        t = traffic_from_pmc(args.traffic_from)
+        os.makedirs(os.path.dirname(PROFILE_TRAFFIC), exist_ok=True)
+        with open(PROFILE_TRAFFIC, "w") as f:
+            json.dump(t, f, indent=1, sort_keys=True)
+        print(json.dumps(t))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one MI355X: this build has no multi-GPU path, so --gpus N "
+              "with N > 1 is not supported (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     hip.init(0)
@@ -261,7 +342,9 @@ def main():
     names = args.only or ALL
     results = {}
     for name in names:
-        if name.startswith("gemm_"):
+        if name == "copy_calibration":
+            results[name] = bench_copy_calibration(name, args.steps, args.warmup)
+        elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
             results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,
                                        args.warmup, stream, traffic)
@@ -271,14 +354,18 @@ def main():
         else:
             results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic)
         r = results[name]
-        log(f"[bench] {name}: {r['value']} {r['unit']} ({r['ms_median']} ms, "
-            f"{100 * r['roofline']['frac']:.1f}% of peak)")
+        frac = r.get("roofline", {}).get("frac")
+        log(f"[bench] {name}: {r['value']} {r['unit']} ({r['ms_per_step']} ms/step"
+            + (f", {100 * frac:.1f}% of peak)" if frac is not None else ")"))
 
     head = results.get("gemm_bf16_8192") or next(iter(results.values()))
     cpu = None
     if not args.no_cpu_baseline and head["name"] == "gemm_bf16_8192":
         cpu = cpu_baseline()
         log(f"[bench] cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+    workloads = {
+        "gemm_bf16_8192": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 acc, bf16 out",
+    }
     line = {
         "metric": METRIC,
         "value": head["value"],
@@ -286,21 +373,17 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["ms_median"],
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16" if "bf16" in head["name"] else ("fp8" if "fp8" in head["name"] else "f16"),
-        "data": "synthetic (seeded recipes of BASELINE configs; inputs resident in HBM)",
-        "config": {
-            "workload": {
-                "gemm_bf16_8192": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 acc, bf16 out",
-            }.get(head["name"], head["name"]),
-            "parallelism": "single GPU",
-        },
-        "roofline": head["roofline"],
+        "data": "synthetic (seeded recipes of the BASELINE configs; inputs resident in HBM)",
+        "config": {"workload": workloads.get(head["name"], head["name"]),
+                   "parallelism": "single GPU"},
+        "roofline": head.get("roofline"),
         "cpu_baseline": cpu,
-        "components": {k: v for k, v in results.items()},
+        "components": results,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["compute_units"]},
     }
     print(json.dumps(line), flush=True)
