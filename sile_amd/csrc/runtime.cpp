@@ -142,6 +142,18 @@ int get_function(Module m, const char* name, hipFunction_t* out) {
   return SILE_OK;
 }
 
+int resident_blocks(Module m, const char* name, int block_threads, int64_t* out) {
+  hipFunction_t f = nullptr;
+  int rc = get_function(m, name, &f);
+  if (rc != SILE_OK) return rc;
+  int dev = 0, cus = 0, per_cu = 0;
+  SILE_HIP_CHECK(hipGetDevice(&dev));
+  SILE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  SILE_HIP_CHECK(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, block_threads, 0));
+  *out = (int64_t)cus * (per_cu > 0 ? per_cu : 1);
+  return SILE_OK;
+}
+
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds) {
   hipFunction_t f = nullptr;

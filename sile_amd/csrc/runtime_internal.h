@@ -41,6 +41,9 @@ enum class Module : int {
 int ensure_device();
 // Looks up `name` in the given embedded module on the current device.
 int get_function(Module m, const char* name, hipFunction_t* out);
+// Number of workgroups of `block_threads` threads of kernel `name` that fit on
+// the whole current device at once (CUs x resident workgroups per CU).
+int resident_blocks(Module m, const char* name, int block_threads, int64_t* out);
 // hipModuleLaunchKernel with kernelParams.
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds = 0);

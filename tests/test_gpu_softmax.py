@@ -123,3 +123,16 @@ def test_reduce_rows(hip, dt, cols):
     scale = np.abs(xf).sum(axis=1)
     got = dout.download(np.float32, (rows,))
     assert np.all(np.abs(got - ref) <= 1e-5 * scale), np.max(np.abs(got - ref) / scale)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("rows,cols", [(5001, 4096), (3, 8192), (16411, 8192)])
+def test_softmax_many_ragged_rows(hip, dt, rows, cols):
+    """Many rows, row counts that are not a multiple of the 4 rows of a
+    workgroup, and fewer rows than a workgroup: every row written exactly once."""
+    say(f"softmax rows {dt} {rows}x{cols}")
+    x = (rng(rows + cols).normal(size=(rows, cols)) * 2.0).astype(np.float32)
+    xb, xf = f16_round(x) if dt == "f16" else bf16_round(x)
+    t = hip.F16 if dt == "f16" else hip.BF16
+    got = _softmax_gpu(hip, xb, t, t, rows, cols)
+    assert_close(got, cpuref.softmax_rows(xf), atol=1e-6, rtol=1e-2, what=f"softmax {dt}")
