@@ -51,6 +51,7 @@ constexpr int kD = 128;
 constexpr int kRowB = kD * 2;  // bytes of one K row
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
 
 template <bool kBF16>
 SILE_DEV f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -235,6 +236,10 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
         }
       }
       // ---- online softmax ----
+      // The running max m only moves when some lane's block max exceeds it
+      // by more than kRescaleLog2 (in log2 units); otherwise exponents are
+      // taken against the stale m, so p <= 2^kRescaleLog2 and the rescale of
+      // O and l (a pass over all accumulators) is skipped for the block.
       u32x4 pf[kQT][kKT * 2];
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
@@ -242,12 +247,18 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 #pragma unroll
         for (int t = 0; t < kKT; ++t)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmax_ordered(mx, sacc[t][qt][i]);
-        mx = fmax_ordered(mx, xor32(mx));
-        const float m_new = fmax_ordered(m_run[qt], mx);
-        const float mc = m_new * c;
-        const float alpha = exp2_fast(m_run[qt] * c - mc);
-        m_run[qt] = m_new;
+          for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, sacc[t][qt][i]);
+        mx = __builtin_fmaxf(mx, xor32(mx));
+        const bool grow = (mx - m_run[qt]) * c > kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = __builtin_fmaxf(m_run[qt], mx);
+          const float alpha = exp2_fast((m_run[qt] - m_new) * c);
+          m_run[qt] = m_new;
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha;
+        }
+        const float mc = m_run[qt] * c;
         float rs = 0.0f;
 #pragma unroll
         for (int t = 0; t < kKT; ++t)
@@ -257,9 +268,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
             sacc[t][qt][i] = p;
             rs += p;
           }
-        l_run[qt] = l_run[qt] * alpha + rs;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha;
+        l_run[qt] += rs;
 #pragma unroll
         for (int t = 0; t < kKT; ++t)
 #pragma unroll
@@ -310,6 +319,287 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 }
 
 }  // namespace
+
+// ===========================================================================
+// Pipelined kernel (S a multiple of 256): 64 queries per wave, 32-key blocks.
+//
+// Iteration j of the key loop issues, as one scheduling region,
+//   * on the matrix cores: S_{j+1} = K_{j+1} . Q^T  and  O^T += V_{j-1}^T . P_{j-1}
+//   * on the VALU: the online softmax of S_j (mask, max, exp, row sum) -> P_j
+// so the softmax of one block runs while the matrix cores work on its
+// neighbours; the lazy O rescale (rare) follows the MFMAs.  K and V tiles go
+// from HBM straight into LDS (buffer_load_dwordx4 ... lds), double-buffered:
+// iteration j loads K_{j+2} and V_j.
+//
+// V is kept in LDS in its natural [key][d] layout and read with
+// ds_read_b64_tr_b16: in each 16-lane group, result slot j of lane i is
+// 16-bit element (i & 3) of the 8 bytes addressed by lane 4 j + (i >> 2).
+// Lane i of a group addresses V[k0 + (i >> 2)][d0 + 4 (i & 3) .. + 4], so it
+// receives V[k0 .. k0 + 3][d0 + i]: four consecutive keys of one d, i.e. four
+// k slots of the V^T A operand.  Two such reads (k0 = 16 cc + 4 g and
+// 16 cc + 8 + 4 g for k-group g = lane / 32) give the 8 slots whose keys are
+// exactly those P's accumulator rows hold for that k-group.
+//
+// LDS per stage: K [32][256 B], chunk c of row r at c ^ (r & 15);
+//                V [32][256 B], chunk c of row r at c ^ 4 (r & 3).
+// ===========================================================================
+namespace v2 {
+
+constexpr int kQT = 2, kNK = 32, kBQ = kWaves * kQT * 32;  // 256 queries per workgroup
+constexpr int kTileB = kNK * kRowB;                          // 8 KiB
+constexpr int kStageB = 2 * kTileB;                          // K + V
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
+
+template <bool kBF16>
+SILE_DEV float pair_sum(uint32_t pk, float acc) {
+  if constexpr (kBF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__bf16 __attribute__((ext_vector_type(2))), pk),
+                                           __builtin_bit_cast(__bf16 __attribute__((ext_vector_type(2))), 0x3f803f80u),
+                                           acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk), f16x2{(_Float16)1.0f, (_Float16)1.0f}, acc,
+                                  false);
+}
+
+template <bool kBF16>
+__device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
+                                            const uint16_t* __restrict__ K,
+                                            const uint16_t* __restrict__ V,
+                                            uint16_t* __restrict__ O, const AttnArgs& a,
+                                            uint8_t* smem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+
+  int bh, qb;
+  const int bid = blockIdx.x;
+  if (a.xcd_map) {
+    const int xcd = bid & 7, idx = bid >> 3;
+    bh = ((idx / a.q_blocks) << 3) + xcd;
+    qb = idx % a.q_blocks;
+  } else {
+    bh = bid % a.bh;
+    qb = bid / a.bh;
+  }
+  if (a.causal) qb = a.q_blocks - 1 - qb;
+  const int64_t S = a.seq;
+  const int64_t head_off = (int64_t)bh * S * kD;
+  const int q0 = qb * kBQ;
+  const int wq0 = q0 + wave * kQT * 32;
+
+  // ---- Q^T fragments (B operand of S^T = K . Q^T) ----
+  u32x4 qf[kQT][8];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    const uint16_t* qrow = Q + head_off + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
+  }
+
+  // ---- LDS-DMA addressing: wave w's instruction i fills rows 16 i + 4 w + (lane >> 4) ----
+  const int dma_row = 4 * wave + (lane >> 4), dma_pos = lane & 15;
+  const int k_voff = dma_row * kRowB + ((dma_pos ^ (dma_row & 15)) << 4);
+  const int v_voff = dma_row * kRowB + ((dma_pos ^ (4 * (dma_row & 3))) << 4);
+  const int kv_bytes = (int)(S * kRowB);
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(K + head_off), (short)0, kv_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(V + head_off), (short)0, kv_bytes, 0x00020000);
+  auto dma_k = [&](int blk, int stage) {
+    uint8_t* base = smem + stage * kStageB + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * 4096), 16, k_voff,
+                                               (blk * kNK + 16 * i) * kRowB, 0, 0);
+  };
+  auto dma_v = [&](int blk, int stage) {
+    uint8_t* base = smem + stage * kStageB + kTileB + wave * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * 4096), 16, v_voff,
+                                               (blk * kNK + 16 * i) * kRowB, 0, 0);
+  };
+
+  // ---- fragment reads ----
+  const int kf_off = l32 * kRowB;
+  const int kf_swz = l32 & 15;
+  auto s_block = [&](int stage, f32x16 (&sacc)[kQT]) {
+    const uint8_t* ks = smem + stage * kStageB + kf_off;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[qt][i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (((2 * kk + g) ^ kf_swz) << 4));
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) sacc[qt] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt]);
+    }
+  };
+  // V^T fragment for d-tile dt, key chunk cc: two transposing reads
+  const int tr_i = lane & 15, tr_s = (lane >> 4) & 1;
+  auto v_frag = [&](const uint8_t* vs, int dt, int cc) {
+    u32x4 out;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int key = 16 * cc + 8 * hh + 4 * g + (tr_i >> 2);
+      const int d = 32 * dt + 16 * tr_s + 4 * (tr_i & 3);
+      const int chunk = d >> 3;
+      const int off = key * kRowB + ((chunk ^ (4 * (key & 3))) << 4) + 8 * (tr_i & 1);
+      const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(vs + off));
+      const u32x2 w = __builtin_bit_cast(u32x2, v);
+      out[2 * hh] = w[0];
+      out[2 * hh + 1] = w[1];
+    }
+    return out;
+  };
+  auto pv_block = [&](int stage, const u32x4 (&pf)[kQT][2], f32x16 (&oacc)[kQT][4]) {
+    const uint8_t* vs = smem + stage * kStageB + kTileB;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const u32x4 vf = v_frag(vs, dt, cc);
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oacc[qt][dt]);
+      }
+  };
+
+  f32x16 oacc[kQT][4];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
+  float m_run[kQT], l_run[kQT], alpha[kQT];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    m_run[qt] = -__builtin_inff();
+    l_run[qt] = 0.0f;
+    alpha[qt] = 1.0f;
+  }
+  u32x4 pprev[kQT][2];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) pprev[qt][0] = pprev[qt][1] = u32x4{0u, 0u, 0u, 0u};
+
+  const int nb = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
+  const int last = nb - 1;
+  const float c = a.scale_log2;
+
+  // prologue: K_0, K_1 (clamped) and a finite V tile for the empty PV_{-1}
+  dma_k(0, 0);
+  dma_k(min(1, last), 1);
+  dma_v(0, 1);
+  __syncthreads();
+  f32x16 scur[kQT];
+  s_block(0, scur);
+  __syncthreads();
+
+  for (int j = 0; j < nb; ++j) {
+    const int s = j & 1;
+    dma_k(min(j + 2, last), s);
+    dma_v(j, s);
+    // matrix cores: S_{j+1} and PV_{j-1}
+    f32x16 snext[kQT];
+    s_block(s ^ 1, snext);
+    pv_block(s ^ 1, pprev, oacc);
+    // VALU: online softmax of S_j -> P_j
+    const int kb = j * kNK;
+    if (a.causal && kb + kNK - 1 > wq0) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        const int q = wq0 + 32 * qt + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + 8 * (i >> 2) + 4 * g + (i & 3);
+          if (key > q) scur[qt][i] = -__builtin_inff();
+        }
+      }
+    }
+    bool grow_any = false;
+    float mx[kQT];
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      float m = scur[qt][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][i]);
+      mx[qt] = __builtin_fmaxf(m, xor32(m));
+      grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
+    }
+    if (grow_any) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        const float m_new = __builtin_fmaxf(m_run[qt], mx[qt]);
+        alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
+        m_run[qt] = m_new;
+        l_run[qt] *= alpha[qt];
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      const float mc = m_run[qt] * c;
+      float rs = l_run[qt];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 w;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float p0 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj], c, -mc));
+          const float p1 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj + 1], c, -mc));
+          w[jj] = pack2<kBF16>(p0, p1);
+          rs = pair_sum<kBF16>(w[jj], rs);
+        }
+        pprev[qt][h] = w;
+      }
+      l_run[qt] = rs;
+    }
+    // lazy rescale of O (after PV_{j-1}, before PV_j)
+    if (grow_any) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha[qt];
+    }
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) scur[qt] = snext[qt];
+    __syncthreads();
+  }
+  // PV of the last block
+  pv_block(last & 1, pprev, oacc);
+
+  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    const float l = l_run[qt] + xor32(l_run[qt]);
+    const float inv = 1.0f / l;
+    const int q = wq0 + 32 * qt + l32;
+    uint16_t* orow = O + head_off + (int64_t)q * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 32 * dt + 8 * r + 4 * g;
+        const f32x16& acc = oacc[qt][dt];
+        const u32x2 w = {pack2<kBF16>(acc[4 * r] * inv, acc[4 * r + 1] * inv),
+                         pack2<kBF16>(acc[4 * r + 2] * inv, acc[4 * r + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+  }
+}
+
+}  // namespace v2
+
+#define SILE_FA_V2_KERNEL(NAME, BF)                                                           \
+  extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \
+      const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * v2::kStageB];                  \
+    v2::attn_fwd_v2<BF>(Q, K, V, O, a, smem);                                                 \
+  }
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true)
 
 #define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 
 #include "runtime_internal.h"
 
@@ -334,16 +335,18 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (bh > 0x7fffffffLL / std::max<int64_t>(seq_len, 1))
     return fail(SILE_ERR_SHAPE, "attention too large");
 
-  // MFMA flash kernel: head_dim 128, S a multiple of the query block, 16-byte
-  // aligned operands.  kQT = 2 (256-query blocks) for f16 when S allows it.
+  // MFMA flash kernels: head_dim 128, 16-byte aligned operands.
+  //   v2 (pipelined, 256-query blocks): S a multiple of 256;
+  //   q1 / q2 (128- / 256-query blocks): S a multiple of 128 / 256.
+  // SILE_HIP_FA_KERNEL=v2|q1|q2 overrides the choice (tuning, tests).
   if (head_dim == 128 && seq_len % 128 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
       aligned16(o)) {
-    int qt = 1;
-    if (dtype == SILE_F16 && seq_len % 256 == 0) {
-      const char* e = getenv("SILE_HIP_FA_QT");  // tile-variant override (tuning, tests)
-      qt = (e && atoi(e) == 2) ? 2 : 1;
-    }
-    const int64_t bq = 128 * qt;
+    const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
+    const char* env = getenv("SILE_HIP_FA_KERNEL");
+    std::string variant = env ? env : "v2";
+    if (variant != "v2" && variant != "q1" && variant != "q2") variant = "v2";
+    if (seq_len % 256 != 0 || (variant == "q2" && dtype != SILE_F16)) variant = "q1";
+    const int64_t bq = variant == "q1" ? 128 : 256;
     struct {
       int64_t seq;
       int32_t bh, q_blocks;
@@ -353,8 +356,10 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
          causal ? 1 : 0, (bh % 8 == 0) ? 1 : 0};
     const int64_t blocks = bh * (seq_len / bq);
     char name[64];
-    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q%d_k64",
-             dtype == SILE_F16 ? "f16" : "bf16", qt);
+    if (variant == "v2")
+      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2", dt);
+    else
+      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s_k64", dt, variant.c_str());
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(256), params, s);
     return rc == SILE_OK ? ok() : rc;

@@ -68,18 +68,19 @@ def test_attention_config4_sampled(hip, s):
     assert np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("qt", ["1", "2"])
+@pytest.mark.parametrize("variant", ["v2", "q1", "q2"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_flash_variants_xcd_order(hip, monkeypatch, qt, causal):
-    """MFMA flash kernel on B*H = 8 heads (head-per-XCD launch order) for both
-    query-tile variants (128- and 256-query blocks); every head and query is
+def test_flash_variants_xcd_order(hip, monkeypatch, variant, dt, causal):
+    """Each MFMA flash kernel (pipelined v2, 128- and 256-query-block q1 / q2)
+    on B*H = 8 heads (head-per-XCD launch order); every head and query is
     compared with the fp32 oracle."""
-    monkeypatch.setenv("SILE_HIP_FA_QT", qt)
+    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
     b, h, s, d = 2, 4, 512, 128
-    say(f"flash f16 qt={qt} causal={causal} B={b} H={h} S={s}")
+    say(f"flash {dt} {variant} causal={causal} B={b} H={h} S={s}")
     scale = 1.0 / np.sqrt(d)
-    qkv = _inputs(b, h, s, d, "f16", seed=21)
-    got = _run(hip, "f16", b, h, s, d, [x[0] for x in qkv], causal, scale)
+    qkv = _inputs(b, h, s, d, dt, seed=21)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
     qf, kf, vf = (x[1] for x in qkv)
     for bi in range(b):
         for hi in range(h):
