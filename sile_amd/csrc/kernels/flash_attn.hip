@@ -41,6 +41,8 @@
 // workgroup i runs on XCD i % 8.  Head h is pinned to XCD h % 8 and its query
 // blocks are issued together (largest causal block first), so the K/V stream
 // of a head is shared in one XCD's L2 by all of its query blocks.
+#include <type_traits>
+
 #include "common.h"
 
 using namespace sile;
@@ -345,9 +347,10 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 // ===========================================================================
 namespace v2 {
 
-constexpr int kQT = 2, kNK = 32, kBQ = kWaves * kQT * 32;  // 256 queries per workgroup
+constexpr int kNK = 32;                                      // keys per block
 constexpr int kTileB = kNK * kRowB;                          // 8 KiB
 constexpr int kStageB = 2 * kTileB;                          // K + V
+constexpr int kStages = 2;                                   // K_b, V_b in stage b & 1
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -364,12 +367,17 @@ SILE_DEV float pair_sum(uint32_t pk, float acc) {
                                   false);
 }
 
-template <bool kBF16>
+// kQT 32-query tiles per wave, kW waves per workgroup: kW * kQT * 32 queries
+// per workgroup (256 for both instantiations).
+template <bool kBF16, int kQT, int kW>
 __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
                                             uint16_t* __restrict__ O, const AttnArgs& a,
                                             uint8_t* smem) {
+  constexpr int kBQ = kW * kQT * 32;
+  constexpr int kDmaPerWave = 8 / kW;  // 1 KiB DMA instructions per wave per 8 KiB tile
+  static_assert(kDmaPerWave >= 1 && 8 % kW == 0, "8 KiB tiles in 1 KiB slices");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
 
@@ -398,7 +406,8 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
   }
 
-  // ---- LDS-DMA addressing: wave w's instruction i fills rows 16 i + 4 w + (lane >> 4) ----
+  // ---- LDS-DMA addressing: wave w's instruction i fills rows 4 (w + kW i) + (lane >> 4) ----
+  // (the swizzles depend on row & 15 and row & 3, the same for every i)
   const int dma_row = 4 * wave + (lane >> 4), dma_pos = lane & 15;
   const int k_voff = dma_row * kRowB + ((dma_pos ^ (dma_row & 15)) << 4);
   const int v_voff = dma_row * kRowB + ((dma_pos ^ (4 * (dma_row & 3))) << 4);
@@ -410,16 +419,16 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   auto dma_k = [&](int blk, int stage) {
     uint8_t* base = smem + stage * kStageB + wave * 1024;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * 4096), 16, k_voff,
-                                               (blk * kNK + 16 * i) * kRowB, 0, 0);
+    for (int i = 0; i < kDmaPerWave; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
+                                               k_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
   };
   auto dma_v = [&](int blk, int stage) {
     uint8_t* base = smem + stage * kStageB + kTileB + wave * 1024;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * 4096), 16, v_voff,
-                                               (blk * kNK + 16 * i) * kRowB, 0, 0);
+    for (int i = 0; i < kDmaPerWave; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
+                                               v_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
   };
 
   // ---- fragment reads ----
@@ -467,6 +476,28 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       }
   };
 
+  // S_{j+1} over the 8 d-steps and PV_{j-1} over (d-tile, key chunk), one
+  // step of each at a time: PV (dt, cc) runs at step dt + 4 cc
+  auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT], const u32x4 (&pf)[kQT][2],
+                       f32x16 (&oa)[kQT][4]) {
+    const uint8_t* ks = smem + kstage * kStageB + kf_off;
+    const uint8_t* vs = smem + vstage * kStageB + kTileB;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[qt][i] = 0.0f;
+#pragma unroll
+    for (int step = 0; step < 8; ++step) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (((2 * step + g) ^ kf_swz) << 4));
+      const int dt = step & 3, cc = step >> 2;
+      const u32x4 vf = v_frag(vs, dt, cc);
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) sacc[qt] = mma32<kBF16>(kf, qf[qt][step], sacc[qt]);
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
+    }
+  };
+
   f32x16 oacc[kQT][4];
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt)
@@ -489,34 +520,46 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   const int last = nb - 1;
   const float c = a.scale_log2;
 
-  // prologue: K_0, K_1 (clamped) and a finite V tile for the empty PV_{-1}
+  // Stages: iteration j reads K_{j+1} and V_{j-1} (stage (j + 1) & 1) and loads
+  // K_{j+2} and V_j into stage j & 1, whose previous contents were read in
+  // iteration j - 1; the barrier closing iteration j waits for those loads.
+  // The key loop is unrolled by two so that stage indices and the roles of
+  // the two S and P register sets are compile-time constants (nb is even:
+  // S is a multiple of 256 and blocks hold 32 keys).
+  // Prologue: K_0, K_1 and a finite V tile in stage 1 for the empty PV_{-1}
+  // (its P is zero).
   dma_k(0, 0);
   dma_k(min(1, last), 1);
   dma_v(0, 1);
   __syncthreads();
-  f32x16 scur[kQT];
-  s_block(0, scur);
+  f32x16 sa[kQT], sb[kQT];
+  u32x4 pb[kQT][2];
+  s_block(0, sa);
   __syncthreads();
 
-  for (int j = 0; j < nb; ++j) {
-    const int s = j & 1;
-    dma_k(min(j + 2, last), s);
-    dma_v(j, s);
-    // matrix cores: S_{j+1} and PV_{j-1}
-    f32x16 snext[kQT];
-    s_block(s ^ 1, snext);
-    pv_block(s ^ 1, pprev, oacc);
+  // One iteration: everything up to the optional O rescale is one basic block,
+  // so the scheduler interleaves the softmax VALU work of block j with the
+  // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
+  // code, needed only on the workgroup's diagonal.
+  auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT],
+                       f32x16 (&snext)[kQT], const u32x4 (&pprev)[kQT][2],
+                       u32x4 (&pnew)[kQT][2]) {
+    constexpr int kS = decltype(stage_c)::value;
+    constexpr bool kMasked = decltype(masked)::value;
+    dma_k(min(j + 2, last), kS);
+    dma_v(j, kS);
+    // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
+    // consecutive MFMAs never accumulate into the same registers
+    mma_block(kS ^ 1, kS ^ 1, snext, pprev, oacc);
     // VALU: online softmax of S_j -> P_j
-    const int kb = j * kNK;
-    if (a.causal && kb + kNK - 1 > wq0) {
+    if constexpr (kMasked) {
+      const int kb = j * kNK;
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
-        const int q = wq0 + 32 * qt + l32;
+        const int q = wq0 + 32 * qt + l32 - kb - 4 * g;  // key offset limit for this lane
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + 8 * (i >> 2) + 4 * g + (i & 3);
-          if (key > q) scur[qt][i] = -__builtin_inff();
-        }
+        for (int i = 0; i < 16; ++i)
+          scur[qt][i] = (8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][i];
       }
     }
     bool grow_any = false;
@@ -529,19 +572,13 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       mx[qt] = __builtin_fmaxf(m, xor32(m));
       grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
     }
-    if (grow_any) {
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        const float m_new = __builtin_fmaxf(m_run[qt], mx[qt]);
-        alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
-        m_run[qt] = m_new;
-        l_run[qt] *= alpha[qt];
-      }
-    }
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      const float mc = m_run[qt] * c;
-      float rs = l_run[qt];
+      const float m_new = grow_any ? __builtin_fmaxf(m_run[qt], mx[qt]) : m_run[qt];
+      alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
+      m_run[qt] = m_new;
+      const float mc = m_new * c;
+      float rs = l_run[qt] * alpha[qt];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         u32x4 w;
@@ -549,26 +586,46 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
         for (int jj = 0; jj < 4; ++jj) {
           const float p0 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj], c, -mc));
           const float p1 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj + 1], c, -mc));
-          w[jj] = pack2<kBF16>(p0, p1);
-          rs = pair_sum<kBF16>(w[jj], rs);
+          const uint32_t pk = pack2<kBF16>(p0, p1);
+          w[jj] = pk;
+          rs = pair_sum<kBF16>(pk, rs);
         }
-        pprev[qt][h] = w;
+        pnew[qt][h] = w;
       }
       l_run[qt] = rs;
     }
-    // lazy rescale of O (after PV_{j-1}, before PV_j)
+    // keep the softmax in this region, beside the MFMAs (the compiler would
+    // otherwise sink it below the rescale branch)
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      asm volatile("" : "+v"(pnew[qt][0]), "+v"(pnew[qt][1]), "+v"(l_run[qt]));
+    }
+    // lazy rescale of O (after PV_{j-1}, before PV_j); the empty asm keeps the
+    // compiler from turning the branch into an unconditional multiply
     if (grow_any) {
+      asm volatile("");
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha[qt];
     }
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) scur[qt] = snext[qt];
     __syncthreads();
+  };
+  // blocks left of the workgroup's diagonal need no mask
+  const int j_diag = a.causal ? q0 / kNK : nb;
+  using Z = std::integral_constant<int, 0>;
+  using One = std::integral_constant<int, 1>;
+  int j = 0;
+  for (; j < j_diag; j += 2) {
+    iteration(j, Z{}, std::false_type{}, sa, sb, pprev, pb);
+    iteration(j + 1, One{}, std::false_type{}, sb, sa, pb, pprev);
   }
-  // PV of the last block
-  pv_block(last & 1, pprev, oacc);
+  for (; j < nb; j += 2) {
+    iteration(j, Z{}, std::true_type{}, sa, sb, pprev, pb);
+    iteration(j + 1, One{}, std::true_type{}, sb, sa, pb, pprev);
+  }
+  // PV of the last block (nb is even: P_{nb-1} is in pprev, V_{nb-1} in stage 1)
+  pv_block(1, pprev, oacc);
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l ----
 #pragma unroll
@@ -592,14 +649,17 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 
 }  // namespace v2
 
-#define SILE_FA_V2_KERNEL(NAME, BF)                                                           \
-  extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \
+#define SILE_FA_V2_KERNEL(NAME, BF, QT, W)                                                    \
+  extern "C" __global__ __launch_bounds__(W * 64, 1) void NAME(                               \
       const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * v2::kStageB];                  \
-    v2::attn_fwd_v2<BF>(Q, K, V, O, a, smem);                                                 \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::kStages * v2::kStageB];        \
+    v2::attn_fwd_v2<BF, QT, W>(Q, K, V, O, a, smem);                                          \
   }
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true)
+// 4 waves x 64 queries (one wave per SIMD) and 8 waves x 32 queries (two per SIMD)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false, 2, 4)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true, 2, 4)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8)
 
 #define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \

@@ -68,11 +68,11 @@ def test_attention_config4_sampled(hip, s):
     assert np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("variant", ["v2", "q1", "q2"])
+@pytest.mark.parametrize("variant", ["v2", "v2w8", "q1", "q2"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_variants_xcd_order(hip, monkeypatch, variant, dt, causal):
-    """Each MFMA flash kernel (pipelined v2, 128- and 256-query-block q1 / q2)
+    """Each MFMA flash kernel (pipelined v2 with 4 or 8 waves, q1 / q2)
     on B*H = 8 heads (head-per-XCD launch order); every head and query is
     compared with the fp32 oracle."""
     monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
