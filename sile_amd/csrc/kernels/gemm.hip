@@ -28,6 +28,8 @@
 //     remapped so the workgroups resident on one XCD cover a compact group of
 //     tiles (8 tile-rows x 4 tile-cols at a time) and share A / B panels in
 //     that XCD's L2.
+#include <type_traits>
+
 #include "common.h"
 
 using namespace sile;
@@ -205,41 +207,6 @@ __device__ __forceinline__ void gemm_nt_body(const uint8_t* __restrict__ A,
     }
 }
 
-// ---------------------------------------------------------------------------
-// 16-bit operands (bf16, f16): v_mfma_f32_32x32x16, software-pipelined.
-//
-// Same 256 x 256 tile, LDS layout and swizzle as gemm_nt_body; each wave owns
-// a 128 x 128 sub-tile = 4 x 4 blocks of 32 x 32 (16 fp32 accumulators per
-// lane per block).  A 64-element k-step is four 16-element sub-steps; their
-// fragments (4 A + 4 B 16-byte vectors per lane) alternate between two
-// register sets F0 / F1, and the single barrier of a k-step sits before its
-// last sub-step:
-//
-//   sub 0: MFMA(F0) | LDS reads of sub 1 -> F1
-//   sub 1: MFMA(F1) | LDS reads of sub 2 -> F0
-//   sub 2: MFMA(F0) | LDS reads of sub 3 -> F1
-//   barrier          (every read of this stage is done; the next stage's tile
-//                     has landed)
-//   sub 3: MFMA(F1) | tile loads of k-step ks + 2 into this stage
-//                   | LDS reads of sub 0 of the next stage -> F0
-//
-// so neither LDS nor global latency sits between two groups of MFMAs; the
-// interleaving is pinned with sched_group_barrier.
-//
-// Fragments: for a 32 x 32 x 16 MFMA lane l supplies row l % 32 of its block
-// and the 8 k of k-group l / 32, i.e. 16-byte chunk 2 sub + l / 32 of the
-// 128-byte k-step row.  The MFMA is issued with the B fragment first, so
-// accumulator register r of lane l is C[m = l % 32][n = 8 (r / 4) + 4 (l / 32)
-// + r % 4] of its block: 4 consecutive n per store.
-//
-// Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
-// instruction of a wave fills 1 KiB of LDS, lane l writing bytes
-// [16 l, 16 l + 16) of it, i.e. 8 tile rows of 128 bytes.  Each lane therefore
-// fetches the global chunk that belongs at its LDS slot under the swizzle:
-// slot (row r, position p) holds logical chunk p ^ swz(r).  Wave w's
-// instruction i fills rows 8 (4 i + w) .. + 7.  The buffer resources cover
-// the tile's 256-row A and B panels, so a load past a panel returns zero.
-// ---------------------------------------------------------------------------
 namespace sched {
 constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 }
@@ -256,11 +223,49 @@ SILE_DEV f32x16 mma32x32(u32x4 a, u32x4 b, f32x16 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// 16-bit operands (bf16, f16): 32-element k-steps through 4 LDS stages.
+//
+// 256 x 256 output tile per workgroup of 4 waves (2 x 2), 128 x 128 per wave
+// as 4 x 4 blocks of v_mfma_f32_32x32x16 (256 fp32 accumulators per lane).  A
+// k-step is 32 elements: two 16-element sub-steps whose fragments (4 A + 4 B
+// 16-byte vectors per lane: row l % 32 of a block, chunk 2 sub + l / 32 of the
+// 64-byte k-step row) alternate between register sets F0 / F1.  The MFMA is
+// issued with the B fragment first, so accumulator register r of lane l is
+// C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
+//
+// Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
+// instruction of a wave fills 1 KiB of LDS, lane l writing bytes
+// [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
+// at its LDS slot under the swizzle.  The buffer resources cover the tile's
+// 256-row A and B panels (loads past a panel return zero).  An LDS stage holds
+// one k-step (rows of 64 bytes, 32 KiB for A + B) and there are 4 stages.
+// Iteration ks:
+//   * tile loads (LDS-DMA) of k-step ks + 3 into the stage of k-step ks - 1,
+//     spread over the whole iteration;
+//   * sub-step 0: MFMA(F0) | reads of F1 (k-step ks, elements 16..31);
+//   * sub-step 1: MFMA(F1) | reads of F0 (k-step ks + 1, elements 0..15);
+//   * barrier: s_waitcnt vmcnt(this iteration's loads) + s_barrier, i.e. it
+//     waits only for the loads issued one iteration earlier.
+// The loop is unrolled by 4 so every LDS stage offset is a constant.
+// Rows of 64 bytes hold 4 chunks; chunk c of row r sits at c ^ swz4(r),
+// swz4(r) = ((r >> 1) ^ (r >> 3)) & 3, conflict-free for the 32-row fragment
+// reads with either 32 or 64 LDS banks.
+// ---------------------------------------------------------------------------
+namespace k32 {
+constexpr int kRowB = 64;                        // bytes of a tile row per k-step
+constexpr int kTileB = 256 * kRowB;              // 16 KiB per operand
+constexpr int kStageB = 2 * kTileB;              // A + B
+constexpr int kStages = 4;
+SILE_DEV int swz4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+}  // namespace k32
+
 template <int kKind, int kOut>
 __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
-                                               const uint8_t* __restrict__ B,
-                                               void* __restrict__ C, const GemmArgs& g,
-                                               uint8_t* smem) {
+                                                const uint8_t* __restrict__ B,
+                                                void* __restrict__ C, const GemmArgs& g,
+                                                uint8_t* smem) {
+  using namespace k32;
   static_assert(kKind == kBF16 || kKind == kF16, "16-bit operand types only");
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -280,21 +285,21 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
   const int tile_m = first_m + in_group % rows_in_group;
   const int tile_n = in_group / rows_in_group;
 
-  // ---- buffer resources over the tile's A and B panels (256 rows each) ----
-  const int a_rs = (int)(g.lda * 2), b_rs = (int)(g.ldb * 2);  // row strides in bytes
+  const int a_rs = (int)(g.lda * 2), b_rs = (int)(g.ldb * 2);
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A + (int64_t)tile_m * kBM * a_rs), (short)0, kBM * a_rs, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(B + (int64_t)tile_n * kBN * b_rs), (short)0, kBN * b_rs, 0x00020000);
-  // lane's LDS slot: row 8 (4 i + wave) + (lane >> 3), position lane & 7
-  const int dma_row = 8 * wave + (lane >> 3);
-  const int dma_chunk = (lane & 7) ^ swz(dma_row);  // swz(row + 32 i) == swz(row)
+  // DMA: one instruction fills 1 KiB = 16 rows of 64 bytes; wave w's
+  // instruction i fills rows 16 (4 i + w) + (lane >> 2), position lane & 3.
+  const int dma_row = 16 * wave + (lane >> 2);
+  const int dma_chunk = (lane & 3) ^ swz4(dma_row);  // swz4(row + 64 i) == swz4(row)
   const int a_voff = dma_row * a_rs + dma_chunk * 16, b_voff = dma_row * b_rs + dma_chunk * 16;
 
   const int fr_row = lane & 31, fr_g = lane >> 5;
-  const int fr_swz = swz(fr_row);  // rows of a fragment read differ by multiples of 32
-  const int a_frag_base = (wm * 128 + fr_row) * kRowBytes;
-  const int b_frag_base = kTileBytes + (wn * 128 + fr_row) * kRowBytes;
+  const int fr_swz = swz4(fr_row);  // fragment rows differ by multiples of 32
+  const int a_frag_base = (wm * 128 + fr_row) * kRowB;
+  const int b_frag_base = kTileB + (wn * 128 + fr_row) * kRowB;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -307,24 +312,25 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
   u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
   const int last = g.k_steps - 1;
 
-  auto dload = [&](int ks, int stage) {
-    const int koff = ks * kRowBytes;
-    uint8_t* base = smem + stage * kStageBytes + wave * 1024;
+  // half h (0, 1) of k-step ks's tile loads: instructions 2 h, 2 h + 1 per operand
+  auto dload = [&](int ks, int stage, int h) {
+    const int koff = ks * kRowB;
+    uint8_t* base = smem + stage * kStageB + wave * 1024;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 2 * h; i < 2 * h + 2; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + i * 4096), 16, a_voff,
-                                               i * 32 * a_rs + koff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kTileBytes + i * 4096),
-                                               16, b_voff, i * 32 * b_rs + koff, 0, 0);
+                                               i * 64 * a_rs + koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kTileB + i * 4096),
+                                               16, b_voff, i * 64 * b_rs + koff, 0, 0);
     }
   };
   auto fread = [&](int stage, int sub, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const uint8_t* sbase = smem + stage * kStageBytes;
+    const uint8_t* sbase = smem + stage * kStageB;
     const int off = ((2 * sub + fr_g) ^ fr_swz) << 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fa[i] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 32 * kRowBytes + off);
-      fb[i] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowBytes + off);
+      fa[i] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 32 * kRowB + off);
+      fb[i] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowB + off);
     }
   };
   auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
@@ -333,58 +339,72 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mma32x32<kKind>(fb[i], fa[j], acc[i][j]);
   };
-  // 16 MFMAs with the 8 LDS reads of the next sub-step spread between them
-#define SILE_GEMM16_INTERLEAVE_READS(ID)                              \
-  _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) {                  \
-    __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, ID);        \
-    __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 1, ID);      \
-  }                                                                   \
-  __builtin_amdgcn_sched_barrier(0);
-
-  dload(0, 0);
-  dload(min(1, last), 1);
-  __syncthreads();
-  fread(0, 0, fa0, fb0);
-
-  // k-step ks: stage s = ks & 1.  The tile loaded after the barrier is k-step
-  // ks + 2, clamped to the last one (the final iterations reload a tile into
-  // a stage that is not read again, so that every iteration has one shape).
-  for (int ks = 0; ks < last; ++ks) {
-    const int s = ks & 1;
-    fread(s, 1, fa1, fb1);
+  // iteration ks in stage kS = ks % 4 (compile-time)
+  auto iteration = [&](int ks, auto stage_c) {
+    constexpr int kS = decltype(stage_c)::value;
+    constexpr int kNext = (kS + 1) % kStages, kLoad = (kS + 3) % kStages;
+    const int lk = min(ks + 3, last);
+    dload(lk, kLoad, 0);
+    fread(kS, 1, fa1, fb1);
     mma(fa0, fb0);
-    SILE_GEMM16_INTERLEAVE_READS(0)
-    fread(s, 2, fa0, fb0);
-    mma(fa1, fb1);
-    SILE_GEMM16_INTERLEAVE_READS(1)
-    fread(s, 3, fa1, fb1);
-    mma(fa0, fb0);
-    SILE_GEMM16_INTERLEAVE_READS(2)
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-    dload(min(ks + 2, last), s);
-    fread(s ^ 1, 0, fa0, fb0);
-    mma(fa1, fb1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 3);
-      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 2, 3);
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 3);
-      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 1, 3);
+    for (int i_ = 0; i_ < 4; ++i_) {
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+    dload(lk, kLoad, 1);
+    fread(kNext, 0, fa0, fb0);
+    mma(fa1, fb1);
+#pragma unroll
+    for (int i_ = 0; i_ < 4; ++i_) {
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 1, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this iteration's 8 tile loads may stay in flight; LDS reads complete
+    __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // prologue: k-steps 0..2 (clamped) in stages 0..2
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    dload(min(p, last), p, 0);
+    dload(min(p, last), p, 1);
   }
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // prologue tiles landed (own loads)
+  __builtin_amdgcn_s_barrier();
+  fread(0, 0, fa0, fb0);
+
+  // iterations 0 .. last - 1 (F0 of k-step last is read by iteration last - 1)
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  int ks = 0;
+  for (; ks + 4 <= last; ks += 4) {
+    iteration(ks, S0{});
+    iteration(ks + 1, S1{});
+    iteration(ks + 2, S2{});
+    iteration(ks + 3, S3{});
+  }
+  if (ks < last) { iteration(ks, S0{}); ++ks; }
+  if (ks < last) { iteration(ks, S1{}); ++ks; }
+  if (ks < last) { iteration(ks, S2{}); ++ks; }
+  // k-step last: its stage is last % 4
   {
-    const int s = last & 1;
-    fread(s, 1, fa1, fb1);
-    mma(fa0, fb0);
-    fread(s, 2, fa0, fb0);
-    mma(fa1, fb1);
-    fread(s, 3, fa1, fb1);
+    const int sl = last & 3;
+    fread(sl, 1, fa1, fb1);
     mma(fa0, fb0);
     mma(fa1, fb1);
   }
-#undef SILE_GEMM16_INTERLEAVE_READS
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // no DMA left in flight at exit
 
   // ---- epilogue ----
   const int64_t m_base = (int64_t)tile_m * kBM + wm * 128 + (lane & 31);
@@ -404,20 +424,23 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
 
 }  // namespace
 
-#define SILE_GEMM_KERNEL(NAME, BODY, KIND, OUT)                                                \
+#define SILE_GEMM_KERNEL(NAME, BODY, KIND, OUT, LDS)                                           \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
                                                             void* C, GemmArgs g) {             \
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageBytes];                    \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS];                              \
     BODY<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), C, g,     \
                     smem);                                                                     \
   }
 
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, gemm16_nt_body, kBF16, kOutBF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, gemm16_nt_body, kBF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, gemm16_nt_body, kF16, kOutF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, gemm16_nt_body, kF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, gemm_nt_body, kFP8, kOutBF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, gemm_nt_body, kFP8, kOutF32)
+// 16-bit kernels: k-steps of 32 elements; fp8 kernels: k-steps of 128 elements
+#define SILE_LDS16 (k32::kStages * k32::kStageB)
+#define SILE_LDS8 (2 * kStageBytes)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, gemm16_nt_body, kBF16, kOutBF16, SILE_LDS16)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, gemm16_nt_body, kBF16, kOutF32, SILE_LDS16)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, gemm16_nt_body, kF16, kOutF16, SILE_LDS16)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, gemm16_nt_body, kF16, kOutF32, SILE_LDS16)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, gemm_nt_body, kFP8, kOutBF16, SILE_LDS8)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, gemm_nt_body, kFP8, kOutF32, SILE_LDS8)
 
 // fp32 GEMM on any shape in the canonical matmul's exact order: one thread per
 // cell, s = s + a*b from 0.0f over k < kp with separate roundings (no FMA).

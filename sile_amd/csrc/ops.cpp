@@ -210,7 +210,7 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   }
 
   const char* name = nullptr;
-  int64_t kstep = 64;
+  int64_t kstep = 32;  // elements per k-step: 32 for 16-bit operands, 128 for fp8
   if (a_type == SILE_BF16 && b_type == SILE_BF16) {
     name = c_type == SILE_BF16 ? "sile_gemm_nt_bf16_bf16"
            : c_type == SILE_F32 ? "sile_gemm_nt_bf16_f32" : nullptr;

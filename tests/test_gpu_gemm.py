@@ -37,7 +37,8 @@ def _run(hip, a_t, c_t, a_bits, b_bits, m, n, k, scale_a=1.0, scale_b=1.0, bk=0)
     return _to_f32(hip, dc, c_t, m, n)
 
 
-SHAPES = [(256, 256, 64), (512, 256, 128), (768, 1024, 320), (2048, 2048, 1024)]
+SHAPES = [(256, 256, 64), (512, 256, 128), (768, 1024, 320), (2048, 2048, 1024), (256, 512, 32),
+          (512, 512, 96)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
@@ -71,9 +72,9 @@ def test_f16_gemm(hip, m, n, k):
 
 
 def test_gemm_k_truncation(hip):
-    """bk = 96 on K = 320: k runs over (320 // 96) * 96 = 288 (not a multiple of
-    the 64-element k-step, so the MFMA path must refuse) and bk = 64 on K = 320
-    with K' = 320; bk = 128 -> K' = 256."""
+    """The reference's K truncation K' = (K // bk) * bk on K = 320: bk = 128 ->
+    K' = 256, bk = 96 -> K' = 288 (both multiples of the 32-element k-step of
+    the 16-bit kernels), bk = 70 -> K' = 280, which the MFMA path refuses."""
     say("gemm bf16 K truncation")
     m = n = 256
     k = 320
@@ -81,10 +82,12 @@ def test_gemm_k_truncation(hip):
     bt = (rng(7).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
     a_bits, a_f = bf16_round(a)
     b_bits, b_f = bf16_round(bt)
-    got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=128)
-    assert_close(got, cpuref.gemm_nt(a_f, b_f, bk=128), atol=1e-4, rtol=1e-4, what="K'=256")
+    for bk in (128, 96):
+        got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=bk)
+        assert_close(got, cpuref.gemm_nt(a_f, b_f, bk=bk), atol=1e-4, rtol=1e-4,
+                     what=f"K'={(k // bk) * bk}")
     with pytest.raises(hip.SileError) as e:
-        _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=96)
+        _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=70)
     assert e.value.kind == "Shape"
 
 
