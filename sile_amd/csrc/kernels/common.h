@@ -15,6 +15,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -30,12 +31,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 SILE_DEV uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 SILE_DEV float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16 bits, round to nearest even (hardware v_cvt_pk_bf16_f32);
+// NaN stays a quiet NaN.
 SILE_DEV uint16_t bf16_rne(float f) {
-  uint32_t u = f32_bits(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
 }
 SILE_DEV float bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
 
@@ -48,7 +48,8 @@ SILE_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float1
 
 // Packs two fp32 into one dword of two 16-bit values (lo in bits 0..15).
 SILE_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)bf16_rne(lo) | ((uint32_t)bf16_rne(hi) << 16);
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 SILE_DEV uint32_t pack_f16x2(float lo, float hi) {
   f16x2 v = {(_Float16)lo, (_Float16)hi};
@@ -73,11 +74,33 @@ SILE_DEV float swizzle_xor16(float v) {
   return __builtin_bit_cast(float,
                             __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
-SILE_DEV float xor32(float v) {
-  return __builtin_bit_cast(float, __shfl_xor(__builtin_bit_cast(int, v), 32));
+// v_permlane32_swap on two copies of v: the upper half of one trades places
+// with the lower half of the other, leaving v's lower half (lo) and upper half
+// (hi) each broadcast to all 64 lanes.  Lane l then holds v[l % 32] and
+// v[32 + l % 32], i.e. v of lanes l and l ^ 32.  (Each result is copied to a
+// scalar before the bit cast: bit-casting a vector element directly reads
+// element 0 with this compiler.)
+SILE_DEV void half_swap(float v, float& lo, float& hi) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned a = r[0], b = r[1];
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
 }
 
 SILE_DEV float fmax_ordered(float a, float b) { return (b > a) ? b : a; }
+
+// max and sum of v over lanes l and l ^ 32 (the same value in both lanes)
+SILE_DEV float pair32_max(float v) {
+  float lo, hi;
+  half_swap(v, lo, hi);
+  return fmax_ordered(lo, hi);
+}
+SILE_DEV float pair32_sum(float v) {
+  float lo, hi;
+  half_swap(v, lo, hi);
+  return lo + hi;
+}
 
 SILE_DEV float wave_max(float v) {
   v = fmax_ordered(v, dpp<kDppXor1>(v));
@@ -85,8 +108,7 @@ SILE_DEV float wave_max(float v) {
   v = fmax_ordered(v, dpp<kDppHalfMirror>(v));
   v = fmax_ordered(v, dpp<kDppMirror>(v));
   v = fmax_ordered(v, swizzle_xor16(v));
-  v = fmax_ordered(v, xor32(v));
-  return v;
+  return pair32_max(v);
 }
 
 SILE_DEV float wave_sum(float v) {
@@ -95,8 +117,12 @@ SILE_DEV float wave_sum(float v) {
   v += dpp<kDppHalfMirror>(v);
   v += dpp<kDppMirror>(v);
   v += swizzle_xor16(v);
-  v += xor32(v);
-  return v;
+  return pair32_sum(v);
+}
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier masks.
+namespace sched {
+constexpr int kValu = 0x002, kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 }
 
 // 2^x on the transcendental unit (v_exp_f32).

@@ -250,7 +250,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
         for (int t = 0; t < kKT; ++t)
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, sacc[t][qt][i]);
-        mx = __builtin_fmaxf(mx, xor32(mx));
+        mx = pair32_max(mx);
         const bool grow = (mx - m_run[qt]) * c > kRescaleLog2;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float m_new = __builtin_fmaxf(m_run[qt], mx);
@@ -303,7 +303,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
   // ---- epilogue: O[q][d] = O^T[d][q] / l ----
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    const float l = l_run[qt] + xor32(l_run[qt]);
+    const float l = pair32_sum(l_run[qt]);
     const float inv = 1.0f / l;
     const int q = wq0 + 32 * qt + l32;
     uint16_t* orow = O + head_off + (int64_t)q * kD;
@@ -347,11 +347,6 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 // ===========================================================================
 namespace v2 {
 
-constexpr int kNK = 32;                                      // keys per block
-constexpr int kTileB = kNK * kRowB;                          // 8 KiB
-constexpr int kStageB = 2 * kTileB;                          // K + V
-constexpr int kStages = 2;                                   // K_b, V_b in stage b & 1
-
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
@@ -367,17 +362,26 @@ SILE_DEV float pair_sum(uint32_t pk, float acc) {
                                   false);
 }
 
+// LDS bytes of the two stages (K and V tiles of kNK keys each)
+template <int kNK>
+constexpr int lds_bytes() { return 2 * 2 * kNK * kRowB; }
+
 // kQT 32-query tiles per wave, kW waves per workgroup: kW * kQT * 32 queries
-// per workgroup (256 for both instantiations).
-template <bool kBF16, int kQT, int kW>
+// per workgroup (256 for every instantiation); kNK keys per block (32 or 64),
+// i.e. kST = kNK / 32 S tiles of 32 keys x 32 queries per query tile.
+template <bool kBF16, int kQT, int kW, int kNK, int kSched>
 __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
                                             uint16_t* __restrict__ O, const AttnArgs& a,
                                             uint8_t* smem) {
   constexpr int kBQ = kW * kQT * 32;
-  constexpr int kDmaPerWave = 8 / kW;  // 1 KiB DMA instructions per wave per 8 KiB tile
-  static_assert(kDmaPerWave >= 1 && 8 % kW == 0, "8 KiB tiles in 1 KiB slices");
+  constexpr int kST = kNK / 32;
+  constexpr int kTileB = kNK * kRowB;    // one K or V tile
+  constexpr int kStageB = 2 * kTileB;    // K + V
+  constexpr int kDmaPerWave = kTileB / 1024 / kW;  // 1 KiB DMA instructions per wave per tile
+  static_assert(kNK % 32 == 0 && kDmaPerWave >= 1 && (kTileB / 1024) % kW == 0,
+                "tiles in 1 KiB slices, evenly over the waves");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
 
@@ -432,22 +436,30 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   };
 
   // ---- fragment reads ----
+  // K fragment of S tile st, d-step kk: row 32 st + l32 (row & 15 == l32 & 15)
   const int kf_off = l32 * kRowB;
   const int kf_swz = l32 & 15;
-  auto s_block = [&](int stage, f32x16 (&sacc)[kQT]) {
+  auto k_frag = [&](const uint8_t* ks, int st, int kk) {
+    return *reinterpret_cast<const u32x4*>(ks + 32 * st * kRowB + (((2 * kk + g) ^ kf_swz) << 4));
+  };
+  auto s_block = [&](int stage, f32x16 (&sacc)[kQT][kST]) {
     const uint8_t* ks = smem + stage * kStageB + kf_off;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[qt][i] = 0.0f;
+      for (int st = 0; st < kST; ++st)
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (((2 * kk + g) ^ kf_swz) << 4));
+        for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
 #pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) sacc[qt] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt]);
-    }
+    for (int st = 0; st < kST; ++st)
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const u32x4 kf = k_frag(ks, st, kk);
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
+      }
   };
-  // V^T fragment for d-tile dt, key chunk cc: two transposing reads
+  // V^T fragment for d-tile dt, 16-key chunk cc: two transposing reads
   const int tr_i = lane & 15, tr_s = (lane >> 4) & 1;
   auto v_frag = [&](const uint8_t* vs, int dt, int cc) {
     u32x4 out;
@@ -464,35 +476,39 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     }
     return out;
   };
-  auto pv_block = [&](int stage, const u32x4 (&pf)[kQT][2], f32x16 (&oacc)[kQT][4]) {
+  auto pv_block = [&](int stage, const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oacc)[kQT][4]) {
     const uint8_t* vs = smem + stage * kStageB + kTileB;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
+      for (int cc = 0; cc < 2 * kST; ++cc) {
         const u32x4 vf = v_frag(vs, dt, cc);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oacc[qt][dt]);
       }
   };
 
-  // S_{j+1} over the 8 d-steps and PV_{j-1} over (d-tile, key chunk), one
-  // step of each at a time: PV (dt, cc) runs at step dt + 4 cc
-  auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT], const u32x4 (&pf)[kQT][2],
-                       f32x16 (&oa)[kQT][4]) {
+  // S_{j+1} over (S tile, d-step) and PV_{j-1} over (d-tile, key chunk), one
+  // step of each at a time: S step (st, kk) runs at step 8 st + kk, PV
+  // (dt, cc) at step dt + 4 cc
+  auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT][kST],
+                       const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oa)[kQT][4]) {
     const uint8_t* ks = smem + kstage * kStageB + kf_off;
     const uint8_t* vs = smem + vstage * kStageB + kTileB;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[qt][i] = 0.0f;
+      for (int st = 0; st < kST; ++st)
 #pragma unroll
-    for (int step = 0; step < 8; ++step) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (((2 * step + g) ^ kf_swz) << 4));
+        for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
+#pragma unroll
+    for (int step = 0; step < 8 * kST; ++step) {
+      const int st = step >> 3, kk = step & 7;
+      const u32x4 kf = k_frag(ks, st, kk);
       const int dt = step & 3, cc = step >> 2;
       const u32x4 vf = v_frag(vs, dt, cc);
 #pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) sacc[qt] = mma32<kBF16>(kf, qf[qt][step], sacc[qt]);
+      for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
     }
@@ -512,9 +528,11 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     l_run[qt] = 0.0f;
     alpha[qt] = 1.0f;
   }
-  u32x4 pprev[kQT][2];
+  u32x4 pprev[kQT][2 * kST];
 #pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) pprev[qt][0] = pprev[qt][1] = u32x4{0u, 0u, 0u, 0u};
+  for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+    for (int cc = 0; cc < 2 * kST; ++cc) pprev[qt][cc] = u32x4{0u, 0u, 0u, 0u};
 
   const int nb = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
   const int last = nb - 1;
@@ -525,15 +543,15 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   // iteration j - 1; the barrier closing iteration j waits for those loads.
   // The key loop is unrolled by two so that stage indices and the roles of
   // the two S and P register sets are compile-time constants (nb is even:
-  // S is a multiple of 256 and blocks hold 32 keys).
+  // S is a multiple of 256 and blocks hold at most 64 keys).
   // Prologue: K_0, K_1 and a finite V tile in stage 1 for the empty PV_{-1}
   // (its P is zero).
   dma_k(0, 0);
   dma_k(min(1, last), 1);
   dma_v(0, 1);
   __syncthreads();
-  f32x16 sa[kQT], sb[kQT];
-  u32x4 pb[kQT][2];
+  f32x16 sa[kQT][kST], sb[kQT][kST];
+  u32x4 pb[kQT][2 * kST];
   s_block(0, sa);
   __syncthreads();
 
@@ -541,9 +559,9 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   // so the scheduler interleaves the softmax VALU work of block j with the
   // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
   // code, needed only on the workgroup's diagonal.
-  auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT],
-                       f32x16 (&snext)[kQT], const u32x4 (&pprev)[kQT][2],
-                       u32x4 (&pnew)[kQT][2]) {
+  auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT][kST],
+                       f32x16 (&snext)[kQT][kST], const u32x4 (&pprev)[kQT][2 * kST],
+                       u32x4 (&pnew)[kQT][2 * kST]) {
     constexpr int kS = decltype(stage_c)::value;
     constexpr bool kMasked = decltype(masked)::value;
     dma_k(min(j + 2, last), kS);
@@ -558,18 +576,23 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       for (int qt = 0; qt < kQT; ++qt) {
         const int q = wq0 + 32 * qt + l32 - kb - 4 * g;  // key offset limit for this lane
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          scur[qt][i] = (8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][i];
+        for (int st = 0; st < kST; ++st)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            scur[qt][st][i] =
+                (32 * st + 8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][st][i];
       }
     }
     bool grow_any = false;
     float mx[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      float m = scur[qt][0];
+      float m = scur[qt][0][0];
 #pragma unroll
-      for (int i = 1; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][i]);
-      mx[qt] = __builtin_fmaxf(m, xor32(m));
+      for (int st = 0; st < kST; ++st)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][st][i]);
+      mx[qt] = pair32_max(m);
       grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
     }
 #pragma unroll
@@ -580,25 +603,45 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       const float mc = m_new * c;
       float rs = l_run[qt] * alpha[qt];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        u32x4 w;
+      for (int st = 0; st < kST; ++st)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const float p0 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj], c, -mc));
-          const float p1 = exp2_fast(__builtin_fmaf(scur[qt][8 * h + 2 * jj + 1], c, -mc));
-          const uint32_t pk = pack2<kBF16>(p0, p1);
-          w[jj] = pk;
-          rs = pair_sum<kBF16>(pk, rs);
+        for (int h = 0; h < 2; ++h) {
+          u32x4 w;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const float p0 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj], c, -mc));
+            const float p1 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj + 1], c, -mc));
+            const uint32_t pk = pack2<kBF16>(p0, p1);
+            w[jj] = pk;
+            rs = pair_sum<kBF16>(pk, rs);
+          }
+          pnew[qt][2 * st + h] = w;
         }
-        pnew[qt][h] = w;
-      }
       l_run[qt] = rs;
     }
     // keep the softmax in this region, beside the MFMAs (the compiler would
     // otherwise sink it below the rescale branch)
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      asm volatile("" : "+v"(pnew[qt][0]), "+v"(pnew[qt][1]), "+v"(l_run[qt]));
+#pragma unroll
+      for (int cc = 0; cc < 2 * kST; ++cc) asm volatile("" : "+v"(pnew[qt][cc]));
+      asm volatile("" : "+v"(l_run[qt]));
+    }
+    if constexpr (kSched > 0) {
+      // issue order: the DMA, the first fragments, then per MFMA step the
+      // fragments kSched steps ahead between the two MFMAs and a share of the
+      // softmax VALU after each
+      constexpr int kSteps = 8 * kST;
+      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 2 * kDmaPerWave, 0);
+      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3 * kSched, 0);
+#pragma unroll
+      for (int step = 0; step < kSteps; ++step) {
+        __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
+        if (step + kSched < kSteps) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
+      }
     }
     // lazy rescale of O (after PV_{j-1}, before PV_j); the empty asm keeps the
     // compiler from turning the branch into an unconditional multiply
@@ -630,7 +673,7 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   // ---- epilogue: O[q][d] = O^T[d][q] / l ----
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    const float l = l_run[qt] + xor32(l_run[qt]);
+    const float l = pair32_sum(l_run[qt]);
     const float inv = 1.0f / l;
     const int q = wq0 + 32 * qt + l32;
     uint16_t* orow = O + head_off + (int64_t)q * kD;
@@ -649,17 +692,21 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 
 }  // namespace v2
 
-#define SILE_FA_V2_KERNEL(NAME, BF, QT, W)                                                    \
+#define SILE_FA_V2_KERNEL(NAME, BF, QT, W, NK, SCHED)                                         \
   extern "C" __global__ __launch_bounds__(W * 64, 1) void NAME(                               \
       const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::kStages * v2::kStageB];        \
-    v2::attn_fwd_v2<BF, QT, W>(Q, K, V, O, a, smem);                                          \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::lds_bytes<NK>()];              \
+    v2::attn_fwd_v2<BF, QT, W, NK, SCHED>(Q, K, V, O, a, smem);                               \
   }
-// 4 waves x 64 queries (one wave per SIMD) and 8 waves x 32 queries (two per SIMD)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false, 2, 4)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true, 2, 4)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8)
+// 4 waves x 64 queries (one wave per SIMD) and 8 waves x 32 queries (two per
+// SIMD) over 32-key blocks; 8 waves x 32 queries over 64-key blocks with the
+// issue order fixed (the default)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false, 2, 4, 32, 0)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true, 2, 4, 32, 0)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 0)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32, 0)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2k64, false, 1, 8, 64, 1)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2k64, true, 1, 8, 64, 1)
 
 #define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \

@@ -207,10 +207,6 @@ __device__ __forceinline__ void gemm_nt_body(const uint8_t* __restrict__ A,
     }
 }
 
-namespace sched {
-constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
-}
-
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int kKind>

@@ -68,7 +68,7 @@ def test_attention_config4_sampled(hip, s):
     assert np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("variant", ["v2", "v2w8", "q1", "q2"])
+@pytest.mark.parametrize("variant", ["v2", "v2w8", "v2k64", "q1", "q2"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_variants_xcd_order(hip, monkeypatch, variant, dt, causal):
