@@ -40,6 +40,7 @@ METRIC = ("bf16 GEMM & flash-attn fwd TFLOP/s (% MI355X MFMA peak), softmax GB/s
 # Published MI355X peaks (dense): bf16/fp16 MFMA 2.5 PFLOP/s, fp8 5.0 PFLOP/s, HBM3E 8 TB/s.
 PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0}
 PEAK_HBM_GBS = 8000.0
+SETTLE_S = 0.5  # untimed load before each workload's warmup (clock ramp-up)
 
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -77,7 +78,19 @@ def time_launches(launch, steps, warmup, stream, rotate=1):
     back to back, so region / steps is the kernel's average launch duration
     (events around every launch would add their own overhead to a 50 us
     kernel).  The timed region is bracketed by a device synchronisation on
-    both sides."""
+    both sides.
+
+    Before the warmup launches the workload runs untimed for SETTLE_S
+    seconds: after the seconds of host-side input generation the GPU starts
+    at idle clocks and takes a few hundred ms of load to reach its steady
+    clock (5 warmup launches of the 8192^3 GEMM under-report it by ~8%)."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(8):
+            launch(i % rotate)
+            i += 1
+        hip.synchronize()
     for i in range(warmup):
         launch(i % rotate)
     hip.synchronize()

@@ -220,48 +220,48 @@ SILE_DEV f32x16 mma32x32(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit operands (bf16, f16): 32-element k-steps through 4 LDS stages.
+// 16-bit operands (bf16, f16): 64-element k-steps through 2 LDS stages.
 //
 // 256 x 256 output tile per workgroup of 4 waves (2 x 2), 128 x 128 per wave
-// as 4 x 4 blocks of v_mfma_f32_32x32x16 (256 fp32 accumulators per lane).  A
-// k-step is 32 elements: two 16-element sub-steps whose fragments (4 A + 4 B
-// 16-byte vectors per lane: row l % 32 of a block, chunk 2 sub + l / 32 of the
-// 64-byte k-step row) alternate between register sets F0 / F1.  The MFMA is
-// issued with the B fragment first, so accumulator register r of lane l is
-// C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
+// as 4 x 4 blocks of v_mfma_f32_32x32x16 (256 fp32 accumulators per lane).
+// The MFMA is issued with the B fragment first, so accumulator register r of
+// lane l is C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
 //
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
 // instruction of a wave fills 1 KiB of LDS, lane l writing bytes
 // [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
 // at its LDS slot under the swizzle.  The buffer resources cover the tile's
-// 256-row A and B panels (loads past a panel return zero).  An LDS stage holds
-// one k-step (rows of 64 bytes, 32 KiB for A + B) and there are 4 stages.
-// Iteration ks:
-//   * tile loads (LDS-DMA) of k-step ks + 3 into the stage of k-step ks - 1,
-//     spread over the whole iteration;
-//   * sub-step 0: MFMA(F0) | reads of F1 (k-step ks, elements 16..31);
-//   * sub-step 1: MFMA(F1) | reads of F0 (k-step ks + 1, elements 0..15);
-//   * barrier: s_waitcnt vmcnt(this iteration's loads) + s_barrier, i.e. it
-//     waits only for the loads issued one iteration earlier.
-// The loop is unrolled by 4 so every LDS stage offset is a constant.
-// Rows of 64 bytes hold 4 chunks; chunk c of row r sits at c ^ swz4(r),
-// swz4(r) = ((r >> 1) ^ (r >> 3)) & 3, conflict-free for the 32-row fragment
-// reads with either 32 or 64 LDS banks.
+// 256-row A and B panels (loads past a panel return zero).  A k-step is 64
+// elements: rows of 128 bytes, so one instruction fetches 8 whole 128-byte
+// lines.  Rows hold 8 chunks of 16 bytes; chunk c of row r sits at
+// c ^ ((r >> 1) & 7), conflict-free for the 32-row fragment reads.  A stage
+// (64 KiB) holds one k-step of A and B; there are 2.
+//
+// A k-step is 4 sub-steps of 16 elements whose fragments (4 A + 4 B 16-byte
+// vectors per lane: row l % 32 of a block, chunk 2 sub + l / 32 of the row)
+// alternate between register sets X (even sub-steps) and Y (odd).
+// Iteration ks (stage ks & 1), after the barrier that published k-step ks:
+//   reads X(ks, 0) | tile loads of k-step ks + 1 into the other stage
+//     (spread over the first half) | MFMA of Y(ks - 1, 3), second half
+//   MFMA X(0) | reads Y(1);  MFMA Y(1) | reads X(2);  MFMA X(2) | reads Y(3)
+//   MFMA Y(3), first half;  s_waitcnt (loads landed, reads done) + s_barrier
+// so the fragment reads after each barrier are covered by 8 MFMAs of the
+// previous k-step.  k_steps counts 32-element steps: an odd count ends with a
+// half k-step (sub-steps 2 and 3 multiply zero fragments).
 // ---------------------------------------------------------------------------
-namespace k32 {
-constexpr int kRowB = 64;                        // bytes of a tile row per k-step
-constexpr int kTileB = 256 * kRowB;              // 16 KiB per operand
+namespace k64 {
+constexpr int kRowB = 128;                       // bytes of a tile row per k-step
+constexpr int kTileB = 256 * kRowB;              // 32 KiB per operand
 constexpr int kStageB = 2 * kTileB;              // A + B
-constexpr int kStages = 4;
-SILE_DEV int swz4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-}  // namespace k32
+constexpr int kStages = 2;
+}  // namespace k64
 
 template <int kKind, int kOut>
-__device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
+__device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
                                                 const uint8_t* __restrict__ B,
                                                 void* __restrict__ C, const GemmArgs& g,
                                                 uint8_t* smem) {
-  using namespace k32;
+  using namespace k64;
   static_assert(kKind == kBF16 || kKind == kF16, "16-bit operand types only");
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -286,14 +286,16 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
       (void*)(A + (int64_t)tile_m * kBM * a_rs), (short)0, kBM * a_rs, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(B + (int64_t)tile_n * kBN * b_rs), (short)0, kBN * b_rs, 0x00020000);
-  // DMA: one instruction fills 1 KiB = 16 rows of 64 bytes; wave w's
-  // instruction i fills rows 16 (4 i + w) + (lane >> 2), position lane & 3.
-  const int dma_row = 16 * wave + (lane >> 2);
-  const int dma_chunk = (lane & 3) ^ swz4(dma_row);  // swz4(row + 64 i) == swz4(row)
+  // DMA: one instruction fills 1 KiB = 8 rows of 128 bytes; wave w's
+  // instruction i (0..7) fills rows 8 (4 i + w) + (lane >> 3), position
+  // lane & 7, whose chunk is (lane & 7) ^ ((row >> 1) & 7) with
+  // (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3) for every i.
+  const int dma_row = 8 * wave + (lane >> 3);
+  const int dma_chunk = (lane & 7) ^ (((wave & 1) << 2) | ((lane >> 4) & 3));
   const int a_voff = dma_row * a_rs + dma_chunk * 16, b_voff = dma_row * b_rs + dma_chunk * 16;
 
   const int fr_row = lane & 31, fr_g = lane >> 5;
-  const int fr_swz = swz4(fr_row);  // fragment rows differ by multiples of 32
+  const int fr_swz = (fr_row >> 1) & 7;  // fragment rows differ by multiples of 32
   const int a_frag_base = (wm * 128 + fr_row) * kRowB;
   const int b_frag_base = kTileB + (wn * 128 + fr_row) * kRowB;
 
@@ -305,19 +307,20 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
-  const int last = g.k_steps - 1;
+  u32x4 xa[4], xb[4], ya[4], yb[4];
+  const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
+  const bool half_last = (g.k_steps & 1) != 0;
 
-  // half h (0, 1) of k-step ks's tile loads: instructions 2 h, 2 h + 1 per operand
-  auto dload = [&](int ks, int stage, int h) {
+  // tile loads of k-step ks into stage: instructions [i0, i1) per operand
+  auto dload = [&](int ks, int stage, int i0, int i1) {
     const int koff = ks * kRowB;
     uint8_t* base = smem + stage * kStageB + wave * 1024;
 #pragma unroll
-    for (int i = 2 * h; i < 2 * h + 2; ++i) {
+    for (int i = i0; i < i1; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + i * 4096), 16, a_voff,
-                                               i * 64 * a_rs + koff, 0, 0);
+                                               i * 32 * a_rs + koff, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kTileB + i * 4096),
-                                               16, b_voff, i * 64 * b_rs + koff, 0, 0);
+                                               16, b_voff, i * 32 * b_rs + koff, 0, 0);
     }
   };
   auto fread = [&](int stage, int sub, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
@@ -329,78 +332,98 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
       fb[i] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowB + off);
     }
   };
-  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
+  // MFMAs of one sub-step on accumulator rows [i0, i1) (B-fragment index)
+  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4], int i0, int i1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = i0; i < i1; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mma32x32<kKind>(fb[i], fa[j], acc[i][j]);
   };
-  // iteration ks in stage kS = ks % 4 (compile-time)
-  auto iteration = [&](int ks, auto stage_c) {
-    constexpr int kS = decltype(stage_c)::value;
-    constexpr int kNext = (kS + 1) % kStages, kLoad = (kS + 3) % kStages;
-    const int lk = min(ks + 3, last);
-    dload(lk, kLoad, 0);
-    fread(kS, 1, fa1, fb1);
-    mma(fa0, fb0);
+  // issue order of a phase of kM MFMAs with kD fragment reads and kV loads
+  auto order = [&](auto m_c, auto d_c, auto v_c) {
+    constexpr int kM = decltype(m_c)::value, kD = decltype(d_c)::value,
+                  kV = decltype(v_c)::value;
 #pragma unroll
-    for (int i_ = 0; i_ < 4; ++i_) {
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 1, 0);
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, kM / 8, 0);
+      if constexpr (kD > 0) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, kD / 4, 0);
+      __builtin_amdgcn_sched_group_barrier(sched::kMfma, kM / 8, 0);
+      if constexpr (kV > 0) __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, kV / 4, 0);
     }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  using I16 = std::integral_constant<int, 16>;
+
+  // One k-step in stage st (a compile-time constant in the main loop, a
+  // runtime value in the final k-step).  kFinal: no next k-step (no loads, no
+  // barrier; a half k-step when half_last).
+  auto iteration = [&](int ks, auto stage_c, auto final_c) {
+    constexpr bool kFinal = decltype(final_c)::value;
+    const int st = stage_c;
+    // X(ks, 0), loads of ks + 1 (first half), Y(ks - 1, 3) second half
+    fread(st, 0, xa, xb);
+    if constexpr (!kFinal) dload(ks + 1, st ^ 1, 0, 4);
+    mma(ya, yb, 2, 4);
+    __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 8, 0);
+    order(I8{}, I0{}, std::integral_constant<int, kFinal ? 0 : 8>{});
     __builtin_amdgcn_sched_barrier(0);
-    dload(lk, kLoad, 1);
-    fread(kNext, 0, fa0, fb0);
-    mma(fa1, fb1);
+    // MFMA X(0) | reads Y(1) | loads of ks + 1 (second half)
+    if constexpr (!kFinal) dload(ks + 1, st ^ 1, 4, 8);
+    fread(st, 1, ya, yb);
+    mma(xa, xb, 0, 4);
+    order(I16{}, I8{}, std::integral_constant<int, kFinal ? 0 : 8>{});
+    __builtin_amdgcn_sched_barrier(0);
+    // MFMA Y(1) | reads X(2)
+    fread(st, 2, xa, xb);
+    mma(ya, yb, 0, 4);
+    order(I16{}, I8{}, I0{});
+    __builtin_amdgcn_sched_barrier(0);
+    // a half final k-step: sub-steps 2 and 3 multiply zeros (the LDS bytes
+    // past the last 32 elements hold whatever followed them in memory)
+    if constexpr (kFinal) {
 #pragma unroll
-    for (int i_ = 0; i_ < 4; ++i_) {
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 1, 1);
+      for (int i = 0; i < 4; ++i) xa[i] = half_last ? u32x4{0u, 0u, 0u, 0u} : xa[i];
     }
+    // MFMA X(2) | reads Y(3)
+    fread(st, 3, ya, yb);
+    if constexpr (kFinal) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ya[i] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[i];
+    }
+    mma(xa, xb, 0, 4);
+    order(I16{}, I8{}, I0{});
     __builtin_amdgcn_sched_barrier(0);
-    // this iteration's 8 tile loads may stay in flight; LDS reads complete
-    __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));
+    if constexpr (kFinal) {
+      mma(ya, yb, 0, 4);
+      return;
+    }
+    // MFMA Y(3), first half; then every load of ks + 1 landed and every read done
+    mma(ya, yb, 0, 2);
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: k-steps 0..2 (clamped) in stages 0..2
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    dload(min(p, last), p, 0);
-    dload(min(p, last), p, 1);
-  }
-  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // prologue tiles landed (own loads)
-  __builtin_amdgcn_s_barrier();
-  fread(0, 0, fa0, fb0);
-
-  // iterations 0 .. last - 1 (F0 of k-step last is read by iteration last - 1)
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  using S3 = std::integral_constant<int, 3>;
+  // prologue: k-step 0 into stage 0; Y(-1, 3) is zero
+  dload(0, 0, 0, 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ya[i] = yb[i] = u32x4{0u, 0u, 0u, 0u};
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // own loads landed
+  __builtin_amdgcn_s_barrier();
   int ks = 0;
-  for (; ks + 4 <= last; ks += 4) {
-    iteration(ks, S0{});
-    iteration(ks + 1, S1{});
-    iteration(ks + 2, S2{});
-    iteration(ks + 3, S3{});
+  for (; ks + 2 <= last; ks += 2) {
+    iteration(ks, S0{}, std::false_type{});
+    iteration(ks + 1, S1{}, std::false_type{});
   }
-  if (ks < last) { iteration(ks, S0{}); ++ks; }
-  if (ks < last) { iteration(ks, S1{}); ++ks; }
-  if (ks < last) { iteration(ks, S2{}); ++ks; }
-  // k-step last: its stage is last % 4
-  {
-    const int sl = last & 3;
-    fread(sl, 1, fa1, fb1);
-    mma(fa0, fb0);
-    mma(fa1, fb1);
+  if (ks < last) {
+    iteration(ks, S0{}, std::false_type{});
+    ++ks;
   }
-  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // no DMA left in flight at exit
+  iteration(ks, ks & 1, std::true_type{});
 
   // ---- epilogue ----
   const int64_t m_base = (int64_t)tile_m * kBM + wm * 128 + (lane & 31);
@@ -427,14 +450,21 @@ __device__ __forceinline__ void gemm16_nt_body(const uint8_t* __restrict__ A,
     BODY<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), C, g,     \
                     smem);                                                                     \
   }
+#define SILE_GEMM16_KERNEL(NAME, KIND, OUT)                                                   \
+  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
+                                                            void* C, GemmArgs g) {             \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[k64::kStages * k64::kStageB];      \
+    gemm16_k64_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), \
+                               C, g, smem);                                                    \
+  }
 
-// 16-bit kernels: k-steps of 32 elements; fp8 kernels: k-steps of 128 elements
-#define SILE_LDS16 (k32::kStages * k32::kStageB)
+// 16-bit kernels: k_steps counts 32-element steps (64-element k-steps, an odd
+// count ending in a half step); fp8 kernels: k-steps of 128 elements
 #define SILE_LDS8 (2 * kStageBytes)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, gemm16_nt_body, kBF16, kOutBF16, SILE_LDS16)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, gemm16_nt_body, kBF16, kOutF32, SILE_LDS16)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, gemm16_nt_body, kF16, kOutF16, SILE_LDS16)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, gemm16_nt_body, kF16, kOutF32, SILE_LDS16)
+SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
+SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
+SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, gemm_nt_body, kFP8, kOutBF16, SILE_LDS8)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, gemm_nt_body, kFP8, kOutF32, SILE_LDS8)
 
