@@ -7,27 +7,9 @@
 // This is the tile op `MmaF` of the canonical matmul
 // (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444) on the
 // matrix cores; k runs over K' = (K / bk) * bk as there, which the host
-// resolves before launch.
-//
-// Block tile 256 x 256, k-step 128 bytes per row (64 elements of a 16-bit type,
-// 128 of fp8), 256 threads = 4 waves in a 2 x 2 arrangement, each wave owning a
-// 128 x 128 sub-tile = 8 x 8 MFMA 16x16 blocks (256 fp32 accumulators per lane).
-//   * global -> registers with 128-bit loads, registers -> LDS (double-buffered,
-//     2 stages x 64 KiB), one barrier per k-step; the next k-step's global loads
-//     are in flight while the matrix cores work on the current one;
-//   * LDS rows are 128 bytes = 8 chunks of 16 bytes; chunk c of row r is stored
-//     at chunk position c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1), a function
-//     of r mod 16 only (the loaders' rows differ by multiples of 32 and the
-//     fragment readers' by multiples of 16, so each side needs one value), which makes
-//     the 16-lane fragment reads (16 rows, one chunk column) and the tile
-//     writes (8 lanes per row) hit distinct banks;
-//   * the MFMA is issued with the B fragment as the first operand, so the
-//     accumulator of a lane holds 4 consecutive n of one output row and the
-//     epilogue writes 8-byte (16-bit C) or 16-byte (fp32 C) vectors;
-//   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
-//     remapped so the workgroups resident on one XCD cover a compact group of
-//     tiles (8 tile-rows x 4 tile-cols at a time) and share A / B panels in
-//     that XCD's L2.
+// resolves before launch.  One body (gemm_k64_body) serves bf16, f16 and fp8
+// e4m3 operands; its design is described above it.  sile_gemm_f32_exact is the
+// fp32 path in the canonical order (bit-identical to the CPU backend).
 #include <type_traits>
 
 #include "common.h"
@@ -37,50 +19,9 @@ using namespace sile;
 namespace {
 
 constexpr int kBM = 256, kBN = 256;
-constexpr int kRowBytes = 128;                       // bytes of one tile row per k-step
-constexpr int kTileBytes = kBM * kRowBytes;          // 32 KiB per operand per stage
-constexpr int kStageBytes = 2 * kTileBytes;          // A + B
-constexpr int kThreads = 256;
-constexpr int kLoadsPerThread = kTileBytes / 16 / kThreads;  // 8 x 16-byte chunks per operand
 
 enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
 enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
-
-SILE_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-template <int kKind>
-struct Mfma;
-template <>
-struct Mfma<kBF16> {
-  static constexpr int kElemBytes = 2;
-  static constexpr int kSubSteps = 2;  // 16x16x32: one 16-byte chunk per lane, 4 chunks per step
-  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
-                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<kF16> {
-  static constexpr int kElemBytes = 2;
-  static constexpr int kSubSteps = 2;
-  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a[0]),
-                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<kFP8> {
-  static constexpr int kElemBytes = 1;
-  static constexpr int kSubSteps = 1;  // 16x16x128: two 16-byte chunks per lane, 8 chunks per step
-  SILE_DEV static f32x4 run(const u32x4* a, const u32x4* b, f32x4 c) {
-    const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
-                      (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
-    const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
-                      (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
-    // cbsz = blgp = 0: both operands OCP e4m3; scales 0 select the unscaled MFMA.
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
-  }
-};
 
 template <int kOut>
 SILE_DEV void store_c4(void* C, int64_t idx, f32x4 v) {
@@ -101,153 +42,60 @@ struct GemmArgs {
   float alpha;
 };
 
-template <int kKind, int kOut>
-__device__ __forceinline__ void gemm_nt_body(const uint8_t* __restrict__ A,
-                                             const uint8_t* __restrict__ B, void* __restrict__ C,
-                                             const GemmArgs& g, uint8_t* smem) {
-  using M = Mfma<kKind>;
-  constexpr int kEB = M::kElemBytes;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // ---- XCD-aware tile order ----
-  const int num_tiles = g.tiles_m * g.tiles_n;
-  const int bid = blockIdx.x;
-  int lin = bid;
-  if ((num_tiles & 7) == 0) lin = (bid & 7) * (num_tiles >> 3) + (bid >> 3);
-  constexpr int kGroupM = 8;
-  const int group_size = kGroupM * g.tiles_n;
-  const int group = lin / group_size;
-  const int first_m = group * kGroupM;
-  const int rows_in_group = min(g.tiles_m - first_m, kGroupM);
-  const int in_group = lin - group * group_size;
-  const int tile_m = first_m + in_group % rows_in_group;
-  const int tile_n = in_group / rows_in_group;
-
-  // ---- global load addressing: thread t moves chunk (t & 7) of rows (t >> 3) + 32 i ----
-  const int ld_row = tid >> 3, ld_chunk = tid & 7;
-  const int64_t a_row_stride = g.lda * kEB, b_row_stride = g.ldb * kEB;
-  const uint8_t* a_src = A + ((int64_t)tile_m * kBM + ld_row) * a_row_stride + ld_chunk * 16;
-  const uint8_t* b_src = B + ((int64_t)tile_n * kBN + ld_row) * b_row_stride + ld_chunk * 16;
-  const int64_t a_step32 = 32 * a_row_stride, b_step32 = 32 * b_row_stride;
-  const int st_off = ld_row * kRowBytes + ((ld_chunk ^ swz(ld_row)) << 4);  // rows + 32 i: same r mod 16
-
-  // ---- fragment read addressing ----
-  const int fr_row = lane & 15, fr_q = lane >> 4;
-  const int fr_swz = swz(fr_row);
-  const int a_frag_base = (wm * 128 + fr_row) * kRowBytes;
-  const int b_frag_base = kTileBytes + (wn * 128 + fr_row) * kRowBytes;
-
-  f32x4 acc[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  u32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
-  auto global_load = [&](int ks) {
-    const int64_t koff = (int64_t)ks * kRowBytes;
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(a_src + i * a_step32 + koff);
-      rb[i] = *reinterpret_cast<const u32x4*>(b_src + i * b_step32 + koff);
-    }
-  };
-  auto lds_store = [&](int stage) {
-    uint8_t* base = smem + stage * kStageBytes + st_off;
-#pragma unroll
-    for (int i = 0; i < kLoadsPerThread; ++i) {
-      *reinterpret_cast<u32x4*>(base + i * 32 * kRowBytes) = ra[i];
-      *reinterpret_cast<u32x4*>(base + kTileBytes + i * 32 * kRowBytes) = rb[i];
-    }
-  };
-
-  global_load(0);
-  lds_store(0);
-  __syncthreads();
-
-  for (int ks = 0; ks < g.k_steps; ++ks) {
-    const int stage = ks & 1;
-    if (ks + 1 < g.k_steps) global_load(ks + 1);
-    const uint8_t* sbase = smem + stage * kStageBytes;
-#pragma unroll
-    for (int sub = 0; sub < M::kSubSteps; ++sub) {
-      constexpr int kChunksPerLane = 2 / M::kSubSteps;  // 1 (16-bit) or 2 (fp8)
-      u32x4 af[8][kChunksPerLane], bf[8][kChunksPerLane];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-#pragma unroll
-        for (int h = 0; h < kChunksPerLane; ++h) {
-          const int chunk = sub * 4 + fr_q * kChunksPerLane + h;
-          const int off = ((chunk ^ fr_swz) << 4);
-          af[i][h] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 16 * kRowBytes + off);
-          bf[i][h] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 16 * kRowBytes + off);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = M::run(bf[i], af[j], acc[i][j]);
-    }
-    if (ks + 1 < g.k_steps) lds_store(stage ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane holds C[m][n .. n+3] for each (i = n block, j = m block) ----
-  const int64_t m_base = (int64_t)tile_m * kBM + wm * 128 + (lane & 15);
-  const int64_t n_base = (int64_t)tile_n * kBN + wn * 128 + (lane >> 4) * 4;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      f32x4 v = acc[i][j];
-      if (g.alpha != 1.0f) v *= g.alpha;
-      store_c4<kOut>(C, (m_base + j * 16) * g.ldc + n_base + i * 16, v);
-    }
-}
-
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// One 32 x 32 output block: v_mfma_f32_32x32x16_{bf16,f16} on one 16-byte
+// chunk per lane, or v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3, zero scale
+// operands: the unscaled instruction) on two.
 template <int kKind>
-SILE_DEV f32x16 mma32x32(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (kKind == kBF16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+SILE_DEV f32x16 mma32x32(const u32x4* a, const u32x4* b, f32x16 c) {
+  if constexpr (kKind == kBF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  } else if constexpr (kKind == kF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  } else {
+    const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
+                      (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
+    const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                      (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit operands (bf16, f16): 64-element k-steps through 2 LDS stages.
+// bf16, f16 and fp8 e4m3 operands: 128-byte k-steps through 2 LDS stages.
 //
 // 256 x 256 output tile per workgroup of 4 waves (2 x 2), 128 x 128 per wave
-// as 4 x 4 blocks of v_mfma_f32_32x32x16 (256 fp32 accumulators per lane).
-// The MFMA is issued with the B fragment first, so accumulator register r of
-// lane l is C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
+// as 4 x 4 blocks of v_mfma_f32_32x32x16_{bf16,f16} or
+// v_mfma_f32_32x32x64_f8f6f4 (256 fp32 accumulators per lane).  The MFMA is
+// issued with the B fragment first, so accumulator register r of lane l is
+// C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
 //
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
 // instruction of a wave fills 1 KiB of LDS, lane l writing bytes
 // [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
 // at its LDS slot under the swizzle.  The buffer resources cover the tile's
-// 256-row A and B panels (loads past a panel return zero).  A k-step is 64
-// elements: rows of 128 bytes, so one instruction fetches 8 whole 128-byte
-// lines.  Rows hold 8 chunks of 16 bytes; chunk c of row r sits at
-// c ^ ((r >> 1) & 7), conflict-free for the 32-row fragment reads.  A stage
-// (64 KiB) holds one k-step of A and B; there are 2.
+// 256-row A and B panels (loads past a panel return zero).  A k-step is 128
+// bytes of each row (64 16-bit or 128 fp8 elements), so one instruction
+// fetches 8 whole 128-byte lines.  Rows hold 8 chunks of 16 bytes; chunk c of
+// row r sits at c ^ ((r >> 1) & 7), conflict-free for the 32-row fragment
+// reads.  A stage (64 KiB) holds one k-step of A and B; there are 2.
 //
-// A k-step is 4 sub-steps of 16 elements whose fragments (4 A + 4 B 16-byte
-// vectors per lane: row l % 32 of a block, chunk 2 sub + l / 32 of the row)
-// alternate between register sets X (even sub-steps) and Y (odd).
-// Iteration ks (stage ks & 1), after the barrier that published k-step ks:
+// A k-step is kSubs sub-steps of one MFMA depth (4 of 16 elements for 16-bit
+// operands, 2 of 64 for fp8) whose fragments (4 A + 4 B blocks per lane: row
+// l % 32 of a block, the kCh 16-byte chunks kCh (2 sub + l / 32) + h of the
+// row, kCh = 1 for 16-bit and 2 for fp8) alternate between register sets X
+// (even sub-steps) and Y (odd).  Iteration ks (stage ks & 1), after the
+// barrier that published k-step ks:
 //   reads X(ks, 0) | tile loads of k-step ks + 1 into the other stage
-//     (spread over the first half) | MFMA of Y(ks - 1, 3), second half
-//   MFMA X(0) | reads Y(1);  MFMA Y(1) | reads X(2);  MFMA X(2) | reads Y(3)
-//   MFMA Y(3), first half;  s_waitcnt (loads landed, reads done) + s_barrier
+//     (spread over the first half) | MFMA of Y(ks - 1, last), second half
+//   MFMA X(0) | reads Y(1);  MFMA Y(1) | reads X(2);  ...
+//   MFMA Y(last), first half;  s_waitcnt (loads landed, reads done) + s_barrier
 // so the fragment reads after each barrier are covered by 8 MFMAs of the
-// previous k-step.  k_steps counts 32-element steps: an odd count ends with a
-// half k-step (sub-steps 2 and 3 multiply zero fragments).
+// previous k-step.  k_steps counts half k-steps (64 bytes of a row): an odd
+// count ends with a half k-step whose second half multiplies zero fragments.
 // ---------------------------------------------------------------------------
 namespace k64 {
 constexpr int kRowB = 128;                       // bytes of a tile row per k-step
@@ -257,17 +105,20 @@ constexpr int kStages = 2;
 }  // namespace k64
 
 template <int kKind, int kOut>
-__device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
+__device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
                                                 const uint8_t* __restrict__ B,
                                                 void* __restrict__ C, const GemmArgs& g,
                                                 uint8_t* smem) {
   using namespace k64;
-  static_assert(kKind == kBF16 || kKind == kF16, "16-bit operand types only");
+  constexpr int kEB = kKind == kFP8 ? 1 : 2;   // bytes per element
+  constexpr int kCh = kKind == kFP8 ? 2 : 1;   // 16-byte chunks per lane per MFMA
+  constexpr int kSubs = 4 / kCh;               // MFMA depths per 128-byte k-step
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- XCD-aware tile order (as gemm_nt_body) ----
+  // ---- XCD-aware tile order: workgroups go round-robin to the 8 XCDs; each
+  // XCD gets a contiguous range of tiles, grouped 8 tile-rows at a time ----
   const int num_tiles = g.tiles_m * g.tiles_n;
   const int bid = blockIdx.x;
   int lin = bid;
@@ -281,7 +132,7 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
   const int tile_m = first_m + in_group % rows_in_group;
   const int tile_n = in_group / rows_in_group;
 
-  const int a_rs = (int)(g.lda * 2), b_rs = (int)(g.ldb * 2);
+  const int a_rs = (int)(g.lda * kEB), b_rs = (int)(g.ldb * kEB);
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A + (int64_t)tile_m * kBM * a_rs), (short)0, kBM * a_rs, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -307,7 +158,7 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  u32x4 xa[4], xb[4], ya[4], yb[4];
+  u32x4 xa[4][kCh], xb[4][kCh], ya[4][kCh], yb[4][kCh];
   const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
   const bool half_last = (g.k_steps & 1) != 0;
 
@@ -323,17 +174,20 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
                                                16, b_voff, i * 32 * b_rs + koff, 0, 0);
     }
   };
-  auto fread = [&](int stage, int sub, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+  auto fread = [&](int stage, int sub, u32x4 (&fa)[4][kCh], u32x4 (&fb)[4][kCh]) {
     const uint8_t* sbase = smem + stage * kStageB;
-    const int off = ((2 * sub + fr_g) ^ fr_swz) << 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[i] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 32 * kRowB + off);
-      fb[i] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowB + off);
+    for (int h = 0; h < kCh; ++h) {
+      const int off = ((kCh * (2 * sub + fr_g) + h) ^ fr_swz) << 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i][h] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 32 * kRowB + off);
+        fb[i][h] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowB + off);
+      }
     }
   };
   // MFMAs of one sub-step on accumulator rows [i0, i1) (B-fragment index)
-  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4], int i0, int i1) {
+  auto mma = [&](const u32x4 (&fa)[4][kCh], const u32x4 (&fb)[4][kCh], int i0, int i1) {
 #pragma unroll
     for (int i = i0; i < i1; ++i)
 #pragma unroll
@@ -352,9 +206,9 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
     }
   };
   using I0 = std::integral_constant<int, 0>;
-  using I4 = std::integral_constant<int, 4>;
   using I8 = std::integral_constant<int, 8>;
   using I16 = std::integral_constant<int, 16>;
+  using IR = std::integral_constant<int, 8 * kCh>;  // fragment reads per sub-step
 
   // One k-step in stage st (a compile-time constant in the main loop, a
   // runtime value in the final k-step).  kFinal: no next k-step (no loads, no
@@ -362,45 +216,49 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
   auto iteration = [&](int ks, auto stage_c, auto final_c) {
     constexpr bool kFinal = decltype(final_c)::value;
     const int st = stage_c;
-    // X(ks, 0), loads of ks + 1 (first half), Y(ks - 1, 3) second half
+    // X(ks, 0), loads of ks + 1 (first half), Y(ks - 1, last) second half
     fread(st, 0, xa, xb);
     if constexpr (!kFinal) dload(ks + 1, st ^ 1, 0, 4);
     mma(ya, yb, 2, 4);
-    __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 8 * kCh, 0);
     order(I8{}, I0{}, std::integral_constant<int, kFinal ? 0 : 8>{});
     __builtin_amdgcn_sched_barrier(0);
-    // MFMA X(0) | reads Y(1) | loads of ks + 1 (second half)
-    if constexpr (!kFinal) dload(ks + 1, st ^ 1, 4, 8);
-    fread(st, 1, ya, yb);
-    mma(xa, xb, 0, 4);
-    order(I16{}, I8{}, std::integral_constant<int, kFinal ? 0 : 8>{});
-    __builtin_amdgcn_sched_barrier(0);
-    // MFMA Y(1) | reads X(2)
-    fread(st, 2, xa, xb);
-    mma(ya, yb, 0, 4);
-    order(I16{}, I8{}, I0{});
-    __builtin_amdgcn_sched_barrier(0);
-    // a half final k-step: sub-steps 2 and 3 multiply zeros (the LDS bytes
-    // past the last 32 elements hold whatever followed them in memory)
-    if constexpr (kFinal) {
+    // sub-steps 1 .. kSubs - 1: MFMA of sub - 1 | reads of sub (| the second
+    // half of the loads with sub 1).  A half final k-step multiplies zeros in
+    // its second half (the LDS bytes past the last half k-step hold whatever
+    // followed it in memory).
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xa[i] = half_last ? u32x4{0u, 0u, 0u, 0u} : xa[i];
-    }
-    // MFMA X(2) | reads Y(3)
-    fread(st, 3, ya, yb);
-    if constexpr (kFinal) {
+    for (int sub = 1; sub < kSubs; ++sub) {
+      auto& ra = (sub & 1) ? ya : xa;
+      auto& rb = (sub & 1) ? yb : xb;
+      const auto& pa = (sub & 1) ? xa : ya;
+      const auto& pb = (sub & 1) ? xb : yb;
+      if (sub == 1 && !kFinal) dload(ks + 1, st ^ 1, 4, 8);
+      fread(st, sub, ra, rb);
+      if (kFinal && sub >= kSubs / 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ya[i] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[i];
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int h = 0; h < kCh; ++h) {
+            ra[i][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : ra[i][h];
+            rb[i][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : rb[i][h];
+          }
+      }
+      mma(pa, pb, 0, 4);
+      if (sub == 1 && !kFinal)
+        order(I16{}, IR{}, I8{});
+      else
+        order(I16{}, IR{}, I0{});
+      __builtin_amdgcn_sched_barrier(0);
     }
-    mma(xa, xb, 0, 4);
-    order(I16{}, I8{}, I0{});
-    __builtin_amdgcn_sched_barrier(0);
     if constexpr (kFinal) {
       mma(ya, yb, 0, 4);
       return;
     }
-    // MFMA Y(3), first half; then every load of ks + 1 landed and every read done
+    // MFMA Y(last), first half (kept above the wait); then every load of
+    // ks + 1 landed and every read done
     mma(ya, yb, 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -411,7 +269,9 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
   // prologue: k-step 0 into stage 0; Y(-1, 3) is zero
   dload(0, 0, 0, 8);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ya[i] = yb[i] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h = 0; h < kCh; ++h) ya[i][h] = yb[i][h] = u32x4{0u, 0u, 0u, 0u};
   __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // own loads landed
   __builtin_amdgcn_s_barrier();
   int ks = 0;
@@ -443,30 +303,21 @@ __device__ __forceinline__ void gemm16_k64_body(const uint8_t* __restrict__ A,
 
 }  // namespace
 
-#define SILE_GEMM_KERNEL(NAME, BODY, KIND, OUT, LDS)                                           \
-  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
-                                                            void* C, GemmArgs g) {             \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS];                              \
-    BODY<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), C, g,     \
-                    smem);                                                                     \
-  }
-#define SILE_GEMM16_KERNEL(NAME, KIND, OUT)                                                   \
+#define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                     \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
                                                             void* C, GemmArgs g) {             \
     __shared__ __attribute__((aligned(1024))) uint8_t smem[k64::kStages * k64::kStageB];      \
-    gemm16_k64_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), \
-                               C, g, smem);                                                    \
+    gemm_k64_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),   \
+                             C, g, smem);                                                      \
   }
 
-// 16-bit kernels: k_steps counts 32-element steps (64-element k-steps, an odd
-// count ending in a half step); fp8 kernels: k-steps of 128 elements
-#define SILE_LDS8 (2 * kStageBytes)
-SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
-SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
-SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
-SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, gemm_nt_body, kFP8, kOutBF16, SILE_LDS8)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, gemm_nt_body, kFP8, kOutF32, SILE_LDS8)
+// k_steps counts half k-steps: 32 elements (16-bit) or 64 (fp8)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 
 // fp32 GEMM on any shape in the canonical matmul's exact order: one thread per
 // cell, s = s + a*b from 0.0f over k < kp with separate roundings (no FMA).

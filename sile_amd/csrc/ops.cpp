@@ -210,7 +210,7 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   }
 
   const char* name = nullptr;
-  int64_t kstep = 32;  // elements per k-step: 32 for 16-bit operands, 128 for fp8
+  int64_t kstep = 32;  // elements per half k-step (64 bytes of a row): 32 16-bit, 64 fp8
   if (a_type == SILE_BF16 && b_type == SILE_BF16) {
     name = c_type == SILE_BF16 ? "sile_gemm_nt_bf16_bf16"
            : c_type == SILE_F32 ? "sile_gemm_nt_bf16_f32" : nullptr;
@@ -220,7 +220,7 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   } else if (a_type == SILE_F8E4M3 && b_type == SILE_F8E4M3) {
     name = c_type == SILE_BF16 ? "sile_gemm_nt_fp8_bf16"
            : c_type == SILE_F32 ? "sile_gemm_nt_fp8_f32" : nullptr;
-    kstep = 128;
+    kstep = 64;
   }
   if (!name)
     return fail(SILE_ERR_UNSUPPORTED_BACKEND, "GEMM %s x %s -> %s not supported",

@@ -91,18 +91,56 @@ def test_gemm_k_truncation(hip):
     assert e.value.kind == "Shape"
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 512), (2048, 2048, 2048)])
-def test_fp8_gemm(hip, m, n, k):
-    say(f"gemm fp8 {m}x{n}x{k}")
+@pytest.mark.parametrize("m,n,k,out", [(256, 256, 128, "bf16"), (512, 768, 512, "bf16"),
+                                       (2048, 2048, 2048, "bf16"), (256, 512, 320, "bf16"),
+                                       (512, 256, 64, "f32"), (768, 512, 448, "f32")])
+def test_fp8_gemm(hip, m, n, k, out):
+    """K' = 320, 64 and 448 end in a half k-step (64 of 128 fp8 elements)."""
+    say(f"gemm fp8 {m}x{n}x{k} -> {out}")
     a = rng(9).normal(size=(m, k)).astype(np.float32)
     bt = rng(10).normal(size=(n, k)).astype(np.float32)
     qa, sa, a_deq = fp8_quantise(a)
     qb, sb, b_deq = fp8_quantise(bt)
-    got = _run(hip, hip.F8E4M3, hip.BF16, qa, qb, m, n, k, sa, sb)
+    c_t = hip.BF16 if out == "bf16" else hip.F32
+    got = _run(hip, hip.F8E4M3, c_t, qa, qb, m, n, k, sa, sb)
     ref = cpuref.gemm_nt(a_deq, b_deq)
     # fp8 GEMM outputs grow like sqrt(K) here (unit-variance inputs): the
-    # relative part of the bound dominates
-    assert_close(got, ref, atol=ATOL, rtol=RTOL, what="fp8 gemm")
+    # relative part of the bound dominates.  The fp8 MFMAs do not sum their
+    # products in full fp32 precision (about 2e-3 absolute from the exact sum
+    # at K = 256, with either instruction shape), so an fp32 output gets the
+    # same north-star bound as a bf16 one.
+    assert_close(got, ref, atol=ATOL, rtol=RTOL, what=f"fp8 gemm {out} out")
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+def test_truncated_k_ignores_nonfinite_tail(hip, kind):
+    """K' = (K / bk) * bk stops inside a k-step: the columns past K' (here NaN
+    and Inf) reach LDS with the last k-step but must not touch the result."""
+    m, n, k = 256, 512, 192
+    bk = 96 if kind == "bf16" else 64
+    kp = (k // bk) * bk
+    say(f"gemm {kind} K={k} bk={bk} (K'={kp}) with a non-finite tail")
+    a = rng(11).normal(size=(m, k)).astype(np.float32)
+    bt = rng(12).normal(size=(n, k)).astype(np.float32)
+    if kind == "bf16":
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        a_bits, a_f = bf16_round(a)
+        b_bits, b_f = bf16_round(bt)
+        a_bits[:, kp:] = 0x7FC0          # NaN
+        b_bits[:, kp:] = 0x7F80          # +Inf
+        got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=bk)
+        ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+        assert_close(got, ref, atol=1e-4, rtol=1e-4, what="bf16 truncated K")
+    else:
+        qa, sa, a_deq = fp8_quantise(a)
+        qb, sb, b_deq = fp8_quantise(bt)
+        qa[:, kp:] = 0x7F                # e4m3fn NaN
+        qb[:, kp:] = 0xFF
+        got = _run(hip, hip.F8E4M3, hip.F32, qa, qb, m, n, k, sa, sb, bk=bk)
+        ref = cpuref.gemm_nt(a_deq[:, :kp], b_deq[:, :kp])
+        assert_close(got, ref, atol=ATOL, rtol=RTOL, what="fp8 truncated K")
+    assert np.isfinite(got).all()
 
 
 def test_f32_gemm_exact(hip):
