@@ -62,8 +62,8 @@ NULL = None
     ((_abi.F16, _abi.BF16, _abi.F32, 256, 256, 64), 2),
     # MFMA path with non-multiple-of-256 M -> Shape
     ((_abi.BF16, _abi.BF16, _abi.BF16, 100, 256, 64), 5),
-    # fp8 K' not a multiple of 128 -> Shape
-    ((_abi.F8E4M3, _abi.F8E4M3, _abi.BF16, 256, 256, 64), 5),
+    # fp8 K' not a multiple of 64 -> Shape
+    ((_abi.F8E4M3, _abi.F8E4M3, _abi.BF16, 256, 256, 96), 5),
 ])
 def test_gemm_host_validation(args, code):
     a_t, b_t, c_t, m, n, k = args
