@@ -9,9 +9,9 @@ recipes of the configurations, and resident in HBM before timing starts.
 The JSON line's `value` is the bf16 GEMM M=N=K=8192 throughput (the metric's
 first quantity and the workload named in `config.workload`); every other
 measured kernel is listed under `components` with its own roofline.  A step is
-one launch of the kernel; per-launch durations come from HIP events recorded
-on the launch stream around each launch, and the K timed steps are bracketed
-by a device synchronisation on both sides.
+one launch of the kernel; the K timed steps run back to back between two HIP
+events recorded on the launch stream, bracketed by a device synchronisation on
+both sides, after an untimed clock-settle period and the W warmup steps.
 
 `cpu_baseline` times the CPU oracle (a restatement of sile's CPU backend loop
 nest, compiled like the reference's generated C) on a bounded sample of the
@@ -223,6 +223,36 @@ def bench_softmax(name, steps, warmup, stream, traffic):
     return res
 
 
+def bench_llir_vec_add(name, steps, warmup):
+    """vec_add<TILE=4> generated from LLIR (tests/golden/llir/vec_add.llir) by
+    sile_hip_llir_compile and run through sile_hip_launch_llir, which is
+    synchronous like the reference's apply(): each step is one whole call
+    (table upload, launch, wait).  c = a + b over 64M fp32 elements, 12 bytes
+    of HBM traffic per element."""
+    n = 64 << 20
+    with open(os.path.join(ROOT, "tests", "golden", "llir", "vec_add.llir")) as f:
+        kern = hip.LlirKernel(f.read(), (2, 1, 4))
+    a = hip.DeviceBuffer(n * 4)
+    b = hip.DeviceBuffer(n * 4)
+    c = hip.DeviceBuffer(n * 4)
+    a.fill_bytes(0)
+    b.fill_bytes(0)
+    ptrs, shapes, grid = [a.ptr, b.ptr, c.ptr], [n, n, n], (n // 4, 1, 1)
+    for _ in range(warmup):
+        kern(ptrs, shapes, grid)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        kern(ptrs, shapes, grid)
+    dt = (time.perf_counter() - t0) / steps
+    nbytes = 12.0 * n
+    res = summarise(name, nbytes, 1e9, "GB/s", dt * 1e3 * steps, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    for buf in (a, b, c):
+        buf.close()
+    kern.close()
+    return res
+
+
 def bench_copy_calibration(name, steps, warmup):
     """A plain device-to-device copy of COPY_BYTES (the HIP runtime's blit
     kernel behind sile_hip_memcpy_dtod).  Run under rocprofv3 --pmc it gives
@@ -321,7 +351,7 @@ def traffic_from_pmc(root):
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
-EXTRA = ["copy_calibration"]
+EXTRA = ["copy_calibration", "llir_vec_add"]
 
 
 def main():
@@ -357,6 +387,8 @@ def main():
     for name in names:
         if name == "copy_calibration":
             results[name] = bench_copy_calibration(name, args.steps, args.warmup)
+        elif name == "llir_vec_add":
+            results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
             results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,

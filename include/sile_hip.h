@@ -133,6 +133,44 @@ int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t nu
                           const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],
                           uint32_t threads_per_program, sile_hip_stream stream);
 
+/* ---- generic code generation for LLIR (sile_llvm_ir::Function) ----
+ * `llir_text` is a function in the reference's printed LLIR form
+ * (format_llvm_ir, crates/sile-llvm-ir/src/print.rs:6-57).  It is translated
+ * to HIP C++ following the CPU backend's C codegen
+ * (crates/sile-backend/src/cpu/codegen.rs, crates/sile-backend/src/emit.rs:112-177):
+ * a per-program body sile_llvm_ir_<name> and a wrapper sile_kernel_<name>
+ * with the (buffers, num_programs, shapes, num_shapes) ABI that derives the
+ * tile count and pid -> (gid0, gid1) decode as the CPU wrapper does
+ * (crates/sile-backend/src/cpu/codegen.rs:409-555).  The tile plan is given
+ * by the caller: the output parameter's index and the tile's rows and cols,
+ * the result of crates/sile-backend/src/emit.rs:241-296 infer_tile_plan;
+ * plan_output_param < 0 selects the CPU wrapper's fallbacks.  This is the
+ * codegen half of CodegenTarget / BackendArtifact
+ * (crates/sile-backend/src/lib.rs:11-26) for a HIP target. */
+
+/* Writes the generated HIP source (NUL-terminated) into out[out_capacity];
+ * *out_len receives its length.  Parse errors -> SILE_ERR_COMPILE.  Needs no
+ * GPU. */
+int sile_hip_llir_to_hip(const char *llir_text, int64_t plan_output_param, int64_t plan_rows,
+                         int64_t plan_cols, char *out, size_t out_capacity, size_t *out_len);
+/* Translates and compiles for gfx950 with hiprtc (as the CPU backend runs cc
+ * on every launch, crates/sile-backend/src/cpu/mod.rs:48-134).  *code_out is a
+ * malloc'd code object of *code_bytes bytes for sile_hip_module_load (free it
+ * with sile_hip_llir_free_code); kernel_name receives "sile_kernel_<name>".
+ * Compiler errors -> SILE_ERR_COMPILE with the log and the source.  Needs no
+ * GPU. */
+int sile_hip_llir_compile(const char *llir_text, int64_t plan_output_param, int64_t plan_rows,
+                          int64_t plan_cols, void **code_out, size_t *code_bytes,
+                          char *kernel_name, size_t name_capacity);
+void sile_hip_llir_free_code(void *code);
+/* Launches a generated sile_kernel_<name>: grid[0]*grid[1]*grid[2] programs,
+ * one per lane, 64 per workgroup (the CPU backend runs one program per
+ * thread, crates/sile-backend/src/cpu/codegen.rs:517-551).  Arguments as
+ * sile_hip_launch_tiles.  Synchronous. */
+int sile_hip_launch_llir(sile_hip_function fn, void *const *buffers, int64_t num_buffers,
+                         const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],
+                         sile_hip_stream stream);
+
 /* ---- the DSL kernels on the hot path, with the sile_kernel_<name> ABI ----
  * Same arguments as the generated `void sile_kernel_<name>(void **buffers,
  * int64_t num_threadgroups, int64_t threads_per_group, const int64_t *shapes,

@@ -89,6 +89,11 @@ SIGNATURES = {
     "sile_hip_module_unload": [_P],
     "sile_hip_module_get": [_P, ctypes.c_char_p, ctypes.POINTER(_P)],
     "sile_hip_launch_tiles": [_P, _P, _I64, _P, _I64, _P, ctypes.c_uint32, _P],
+    "sile_hip_llir_to_hip": [ctypes.c_char_p, _I64, _I64, _I64, _P, _SZ, ctypes.POINTER(_SZ)],
+    "sile_hip_llir_compile": [ctypes.c_char_p, _I64, _I64, _I64, ctypes.POINTER(_P),
+                              ctypes.POINTER(_SZ), _P, _SZ],
+    "sile_hip_llir_free_code": [_P],
+    "sile_hip_launch_llir": [_P, _P, _I64, _P, _I64, _P, _P],
     "sile_hip_kernel_matmul": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "sile_hip_kernel_softmax": [_P, _I64, _I64, _P, _I64, _I64, _I64, _P],
     "sile_hip_kernel_parallel_reduce": [_P, _I64, _I64, _P, _I64, _I64, _P, _P],
@@ -98,7 +103,8 @@ SIGNATURES = {
     "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
     "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
 }
-_RESTYPE = {"sile_hip_last_error": ctypes.c_char_p, "sile_hip_version": ctypes.c_char_p}
+_RESTYPE = {"sile_hip_last_error": ctypes.c_char_p, "sile_hip_version": ctypes.c_char_p,
+            "sile_hip_llir_free_code": None}
 
 _lib = None
 
@@ -276,6 +282,59 @@ def kernel_parallel_reduce(bufs, num_threadgroups, shapes, tile, partials=0, str
                            threads_per_group=1):
     call("sile_hip_kernel_parallel_reduce", _ptr_array(bufs), num_threadgroups,
          threads_per_group, _i64_array(shapes), len(shapes), tile, partials or None, _sh(stream))
+
+
+# ---------------------------------------------------------------------------
+# generic code generation for LLIR text
+# ---------------------------------------------------------------------------
+
+def _plan(plan):
+    """(output_param, rows, cols) or None (the CPU wrapper's fallbacks)."""
+    return (-1, 0, 0) if plan is None else tuple(int(x) for x in plan)
+
+
+def llir_to_hip(text: str, plan=None) -> str:
+    """The HIP C++ that sile_hip_llir_compile builds from `text`."""
+    p = _plan(plan)
+    n = _SZ(0)
+    call("sile_hip_llir_to_hip", text.encode(), *p, None, 0, ctypes.byref(n))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    call("sile_hip_llir_to_hip", text.encode(), *p, ctypes.cast(buf, _P), n.value + 1, None)
+    return buf.value.decode()
+
+
+def llir_compile(text: str, plan=None) -> "tuple[bytes, str]":
+    """gfx950 code object and kernel name for `text` (hiprtc; no GPU needed)."""
+    p = _plan(plan)
+    code, size = _P(), _SZ(0)
+    name = ctypes.create_string_buffer(256)
+    call("sile_hip_llir_compile", text.encode(), *p, ctypes.byref(code), ctypes.byref(size),
+         ctypes.cast(name, _P), 256)
+    try:
+        image = ctypes.string_at(code.value, size.value)
+    finally:
+        lib().sile_hip_llir_free_code(code)
+    return image, name.value.decode()
+
+
+class LlirKernel:
+    """A kernel generated from LLIR text, loaded on the current device."""
+
+    def __init__(self, text: str, plan=None):
+        self.image, self.name = llir_compile(text, plan)
+        self.module, self.fn = _P(), _P()
+        call("sile_hip_module_load", self.image, len(self.image), ctypes.byref(self.module))
+        call("sile_hip_module_get", self.module, self.name.encode(), ctypes.byref(self.fn))
+
+    def __call__(self, bufs, shapes, grid, stream=None):
+        g = (ctypes.c_uint32 * 3)(*grid)
+        call("sile_hip_launch_llir", self.fn, _ptr_array(bufs), len(bufs), _i64_array(shapes),
+             len(shapes), g, _sh(stream))
+
+    def close(self):
+        if self.module.value and _lib is not None:
+            call("sile_hip_module_unload", self.module)
+            self.module = _P()
 
 
 # ---------------------------------------------------------------------------

@@ -28,7 +28,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 KERNELS = ["dsl", "softmax", "gemm", "attention", "flash_attn"]
-HOST_SOURCES = ["runtime.cpp", "ops.cpp"]
+HOST_SOURCES = ["runtime.cpp", "ops.cpp", "llir.cpp"]
 
 # Device code: gfx950 only; packed-fp32 instructions disabled (the compiler
 # would otherwise form v_pk_{add,mul,fma}_f32 from scalar float code).
@@ -77,7 +77,7 @@ def build(verbose: bool = True) -> str:
     with open(vscript, "w") as f:
         f.write("{\n  global: sile_hip_*;\n  local: *;\n};\n")
     tmp = LIB + ".tmp"
-    _run(["g++", "-shared", "-o", tmp, *objs, f"-L{ROCM}/lib", "-lamdhip64",
+    _run(["g++", "-shared", "-o", tmp, *objs, f"-L{ROCM}/lib", "-lamdhip64", "-lhiprtc",
           f"-Wl,-rpath,{ROCM}/lib", "-Wl,--no-undefined", f"-Wl,--version-script={vscript}"])
     os.replace(tmp, LIB)
     if verbose:

@@ -1,0 +1,1012 @@
+// Generic HIP code generation for sile's LLVM-like IR (LLIR).
+//
+// Input: a function in the printed LLIR form of the reference
+// (crates/sile-llvm-ir/src/print.rs:6-57 `format_llvm_ir`, data model
+// crates/sile-llvm-ir/src/ir.rs:1-279).  Output: HIP C++ with the per-program
+// body `sile_llvm_ir_<name>` and a launch wrapper `sile_kernel_<name>`, compiled
+// for gfx950 at run time with hiprtc, as the CPU backend compiles its
+// generated C on every launch (crates/sile-backend/src/cpu/mod.rs:48-134).
+//
+// Semantics follow the CPU backend's C codegen
+// (crates/sile-backend/src/cpu/codegen.rs, crates/sile-backend/src/emit.rs:112-177):
+//   * every value is a local declared at the top; block parameters are locals
+//     assigned on the branch into the block;
+//   * bin / cmp / select / load / store / cast / gep lower to the C operators
+//     (`&(base[i][j])` for a gep, plain assignment for a cast);
+//   * block ids are the program's tile coordinates (gid0, gid1, gid2), thread
+//     ids are 0 and barriers do nothing (one program = one thread);
+//   * exp is expf, atomic add is an atomic float add, vec.load / vec.reduce.add
+//     are 4-wide loads and ((v0 + v1) + v2) + v3.
+// Control flow is emitted as labels and gotos (the reference's structured
+// for/if emitter produces the same execution order).  The launch wrapper
+// derives the number of tiles and the pid -> (gid0, gid1) decode from the
+// tile plan of the output parameter, as the CPU wrapper does
+// (crates/sile-backend/src/cpu/codegen.rs:409-555); the plan itself is an
+// input here (the reference computes it with `infer_tile_plan`,
+// crates/sile-backend/src/emit.rs:241-296, which a HIP backend in that crate
+// calls before handing the text over).  Programs are laid out one per lane,
+// 64 per workgroup.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cctype>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "runtime_internal.h"
+
+using sile_rt::fail;
+using sile_rt::ok;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// data model (the subset of ir.rs the printed form carries)
+// ---------------------------------------------------------------------------
+enum class TK { Void, I1, I32, I64, F16, F32, F64, Ptr, Vec, Arr };
+
+struct Type {
+  TK k = TK::Void;
+  int addr = 0;                // Ptr: address space number
+  std::shared_ptr<Type> elem;  // Ptr pointee (may be null: unknown), Vec / Arr element
+  int64_t len = 0;             // Vec / Arr length
+};
+
+Type scalar(TK k) {
+  Type t;
+  t.k = k;
+  return t;
+}
+Type ptr_to(const Type& pointee, int addr) {
+  Type t;
+  t.k = TK::Ptr;
+  t.addr = addr;
+  t.elem = std::make_shared<Type>(pointee);
+  return t;
+}
+
+struct Operand {
+  bool is_value = false;
+  std::string name;  // value name (without %) or the constant's text
+  enum { kInt, kFloat, kBool } ck = kInt;
+};
+
+struct Inst {
+  std::string result;  // empty: no result
+  Type ty;             // result type
+  std::string op;      // alloca gep load store atomic memcpy bin cmp cast select call intr
+  std::string sub;     // bin / cmp / cast mnemonic, intrinsic kind, callee
+  int dim = 0;         // intrinsic dim / vector length
+  std::vector<Operand> args;
+  Type aux;            // gep source element type, alloca type
+};
+
+struct Term {
+  std::string kind;  // br condbr switch ret
+  Operand cond;
+  std::string t, f;  // targets
+  std::vector<Operand> targs, fargs;
+  std::vector<std::pair<std::string, std::string>> cases;  // (literal, target)
+};
+
+struct Block {
+  std::string name;
+  std::vector<std::pair<std::string, Type>> params;
+  std::vector<Inst> insts;
+  Term term;
+};
+
+struct Param {
+  std::string name;
+  Type ty;
+  int rank = -1, shape_offset = -1;  // ABI (rank < 0: none)
+};
+
+struct Function {
+  std::string name;
+  std::vector<Param> params;
+  std::vector<Block> blocks;
+};
+
+struct ParseError {
+  std::string msg;
+};
+
+[[noreturn]] void perr(int line, const std::string& msg) {
+  throw ParseError{"LLIR line " + std::to_string(line) + ": " + msg};
+}
+
+std::string trim(const std::string& s) {
+  size_t a = 0, b = s.size();
+  while (a < b && isspace((unsigned char)s[a])) ++a;
+  while (b > a && isspace((unsigned char)s[b - 1])) --b;
+  return s.substr(a, b - a);
+}
+
+bool starts_with(const std::string& s, const std::string& p) {
+  return s.compare(0, p.size(), p) == 0;
+}
+
+// Splits on commas that are not inside <...>, [...] or (...).
+std::vector<std::string> split_top(const std::string& s, char sep = ',') {
+  std::vector<std::string> out;
+  int depth = 0;
+  std::string cur;
+  for (char c : s) {
+    if (c == '<' || c == '[' || c == '(') ++depth;
+    if (c == '>' || c == ']' || c == ')') --depth;
+    if (c == sep && depth == 0) {
+      out.push_back(trim(cur));
+      cur.clear();
+    } else {
+      cur += c;
+    }
+  }
+  if (!trim(cur).empty()) out.push_back(trim(cur));
+  return out;
+}
+
+// ---- types: i1 i32 i64 f16 f32 f64 void ptr "ptr addrspace(N)" <N x T> [N x T]
+struct Cursor {
+  const std::string& s;
+  size_t i;
+  int line;
+  void ws() {
+    while (i < s.size() && isspace((unsigned char)s[i])) ++i;
+  }
+  bool eat(const std::string& p) {
+    ws();
+    if (s.compare(i, p.size(), p) == 0) {
+      i += p.size();
+      return true;
+    }
+    return false;
+  }
+  void expect(const std::string& p) {
+    if (!eat(p)) perr(line, "expected '" + p + "' in: " + s);
+  }
+  std::string word() {  // [A-Za-z0-9_.$-]+
+    ws();
+    size_t a = i;
+    while (i < s.size() && (isalnum((unsigned char)s[i]) || s[i] == '_' || s[i] == '.' ||
+                            s[i] == '$' || s[i] == '-'))
+      ++i;
+    if (a == i) perr(line, "expected a word at column " + std::to_string(a) + " in: " + s);
+    return s.substr(a, i - a);
+  }
+  int64_t integer() {
+    ws();
+    size_t a = i;
+    if (i < s.size() && s[i] == '-') ++i;
+    while (i < s.size() && isdigit((unsigned char)s[i])) ++i;
+    if (a == i) perr(line, "expected an integer in: " + s);
+    return std::stoll(s.substr(a, i - a));
+  }
+  Type type() {
+    ws();
+    if (eat("<")) {
+      Type t;
+      t.k = TK::Vec;
+      t.len = integer();
+      expect("x");
+      t.elem = std::make_shared<Type>(type());
+      expect(">");
+      return t;
+    }
+    if (eat("[")) {
+      Type t;
+      t.k = TK::Arr;
+      t.len = integer();
+      expect("x");
+      t.elem = std::make_shared<Type>(type());
+      expect("]");
+      return t;
+    }
+    const std::string w = word();
+    if (w == "void") return scalar(TK::Void);
+    if (w == "i1") return scalar(TK::I1);
+    if (w == "i32") return scalar(TK::I32);
+    if (w == "i64") return scalar(TK::I64);
+    if (w == "f16") return scalar(TK::F16);
+    if (w == "f32") return scalar(TK::F32);
+    if (w == "f64") return scalar(TK::F64);
+    if (w == "ptr") {
+      Type t;
+      t.k = TK::Ptr;
+      size_t save = i;
+      if (eat("addrspace(")) {
+        t.addr = (int)integer();
+        expect(")");
+      } else {
+        i = save;
+      }
+      return t;
+    }
+    perr(line, "unknown type '" + w + "' in: " + s);
+  }
+  Operand operand() {
+    ws();
+    Operand o;
+    if (eat("%")) {
+      o.is_value = true;
+      o.name = word();
+      return o;
+    }
+    const std::string w = word();
+    o.name = w;
+    if (w == "true" || w == "false") {
+      o.ck = Operand::kBool;
+    } else if (w.find_first_of(".eE") != std::string::npos || w == "inf" || w == "-inf" ||
+               w == "NaN") {
+      o.ck = Operand::kFloat;
+    } else {
+      o.ck = Operand::kInt;
+    }
+    return o;
+  }
+  // "TYPE operand"
+  std::pair<Type, Operand> typed_operand() {
+    Type t = type();
+    Operand o = operand();
+    return {t, o};
+  }
+  bool done() {
+    ws();
+    return i >= s.size();
+  }
+};
+
+struct Parser {
+  Function fn;
+  std::map<std::string, Type> types;  // value name -> type
+
+  const Type* type_of(const Operand& o) {
+    if (!o.is_value) return nullptr;
+    auto it = types.find(o.name);
+    return it == types.end() ? nullptr : &it->second;
+  }
+
+  void define_value(const std::string& name, const Type& t, int line) {
+    if (name.empty()) return;
+    if (types.count(name)) perr(line, "value %" + name + " defined twice");
+    types[name] = t;
+  }
+
+  static std::string strip_metadata(const std::string& body) {
+    // a trailing " [parallel, unroll=4, ...]" (crates/sile-llvm-ir/src/print.rs:262-274)
+    if (body.empty() || body.back() != ']') return body;
+    const size_t open = body.rfind(" [");
+    if (open == std::string::npos) return body;
+    const std::string inner = body.substr(open + 2, body.size() - open - 3);
+    static const char* kw[] = {"parallel", "reduction", "vectorize_width=", "unroll=",
+                               "align=",   "noalias",   "readonly",         "writeonly"};
+    for (const std::string& item : split_top(inner)) {
+      bool known = false;
+      for (const char* k : kw) known |= starts_with(item, k);
+      if (!known) return body;  // part of the instruction (an array type)
+    }
+    return body.substr(0, open);
+  }
+
+  std::vector<Operand> arg_list(const std::string& s, int line) {
+    std::vector<Operand> out;
+    for (const std::string& a : split_top(s)) {
+      Cursor c{a, 0, line};
+      out.push_back(c.operand());
+    }
+    return out;
+  }
+
+  // " ; args(a, b)" style suffixes of a terminator
+  std::map<std::string, std::vector<Operand>> branch_suffixes(std::string& text, int line) {
+    std::map<std::string, std::vector<Operand>> out;
+    size_t pos;
+    while ((pos = text.rfind(" ; ")) != std::string::npos) {
+      std::string suf = trim(text.substr(pos + 3));
+      text = text.substr(0, pos);
+      const size_t lp = suf.find('(');
+      if (lp == std::string::npos || suf.back() != ')') perr(line, "bad branch arguments: " + suf);
+      out[suf.substr(0, lp)] = arg_list(suf.substr(lp + 1, suf.size() - lp - 2), line);
+    }
+    return out;
+  }
+
+  Inst parse_inst(const std::string& raw, int line) {
+    Inst in;
+    std::string body = raw;
+    if (starts_with(body, "%")) {
+      const size_t eq = body.find(" = ");
+      if (eq == std::string::npos) perr(line, "expected ' = ' in: " + raw);
+      in.result = body.substr(1, eq - 1);
+      body = body.substr(eq + 3);
+    }
+    body = strip_metadata(body);
+    Cursor c{body, 0, line};
+    const std::string op = c.word();
+    if (op == "alloca") {
+      in.op = "alloca";
+      in.aux = c.type();
+      c.expect(",");
+      c.expect("addrspace(");
+      const int as = (int)c.integer();
+      c.expect(")");
+      in.ty = ptr_to(in.aux, as);
+    } else if (op == "getelementptr") {
+      in.op = "gep";
+      in.aux = c.type();
+      c.expect(",");
+      auto [bt, base] = c.typed_operand();
+      in.args.push_back(base);
+      while (c.eat(",")) {
+        c.type();  // i64
+        in.args.push_back(c.operand());
+      }
+      // result: pointer to the source element type indexed by all but the
+      // first index (C array indexing), in the base's address space
+      Type pointee = in.aux;
+      for (size_t k = 2; k < in.args.size(); ++k) {
+        if (pointee.k != TK::Arr) perr(line, "gep indexes past the array levels: " + raw);
+        pointee = *pointee.elem;
+      }
+      in.ty = ptr_to(pointee, bt.addr);
+    } else if (op == "load") {
+      in.op = "load";
+      in.ty = c.type();
+      c.expect(",");
+      in.args.push_back(c.typed_operand().second);
+    } else if (op == "store") {
+      in.op = "store";
+      c.type();
+      in.args.push_back(c.operand());  // value
+      c.expect(",");
+      in.args.insert(in.args.begin(), c.typed_operand().second);  // [ptr, value]
+    } else if (op == "atomicrmw") {
+      in.op = "atomic";
+      in.sub = c.word();  // fadd / add
+      in.args.push_back(c.typed_operand().second);
+      c.expect(",");
+      auto [vt, v] = c.typed_operand();
+      in.args.push_back(v);
+      in.ty = vt;
+    } else if (op == "fadd" || op == "fsub" || op == "fmul" || op == "fdiv" || op == "add" ||
+               op == "sub" || op == "mul" || op == "sdiv" || op == "and" || op == "or") {
+      in.op = "bin";
+      in.sub = op;
+      in.args.push_back(c.operand());
+      c.expect(",");
+      in.args.push_back(c.operand());
+      const Type* t0 = type_of(in.args[0]);
+      const Type* t1 = type_of(in.args[1]);
+      if (t0) in.ty = *t0;
+      else if (t1) in.ty = *t1;
+      else in.ty = scalar(op[0] == 'f' ? TK::F32 : TK::I64);
+    } else if (op == "icmp" || op == "fcmp") {
+      in.op = "cmp";
+      in.sub = c.word();
+      in.args.push_back(c.operand());
+      c.expect(",");
+      in.args.push_back(c.operand());
+      in.ty = scalar(TK::I1);
+    } else if (op == "bitcast" || op == "sext" || op == "zext" || op == "trunc" ||
+               op == "sitofp" || op == "fptosi") {
+      in.op = "cast";
+      in.sub = op;
+      in.args.push_back(c.operand());
+      c.expect("to");
+      in.ty = c.type();
+    } else if (op == "select") {
+      in.op = "select";
+      c.type();  // i1
+      in.args.push_back(c.operand());
+      c.expect(",");
+      auto [tt, a] = c.typed_operand();
+      c.expect(",");
+      auto [ft, b] = c.typed_operand();
+      in.args.push_back(a);
+      in.args.push_back(b);
+      const Type* ta = type_of(a);
+      const Type* tb = type_of(b);
+      in.ty = ta ? *ta : tb ? *tb : tt;
+    } else if (op == "call") {
+      Type rt = c.type();
+      c.expect("@");
+      const std::string callee = c.word();
+      c.expect("(");
+      const size_t close = body.rfind(')');
+      if (close == std::string::npos || close < c.i) perr(line, "unterminated call: " + raw);
+      std::vector<Operand> args;
+      for (const std::string& a : split_top(body.substr(c.i, close - c.i))) {
+        Cursor ac{a, 0, line};
+        args.push_back(ac.typed_operand().second);
+      }
+      in.ty = rt;
+      in.args = args;
+      if (starts_with(callee, "llvm.nvvm.tid.") || starts_with(callee, "llvm.nvvm.ctaid.")) {
+        in.op = "intr";
+        in.sub = starts_with(callee, "llvm.nvvm.tid.") ? "tid" : "ctaid";
+        const char d = callee.back();
+        in.dim = d == 'y' ? 1 : d == 'z' ? 2 : 0;
+        in.ty = scalar(TK::I64);
+      } else if (callee == "llvm.nvvm.barrier0") {
+        in.op = "intr";
+        in.sub = "barrier";
+      } else if (starts_with(callee, "llvm.exp.")) {
+        in.op = "intr";
+        in.sub = "exp";
+      } else if (starts_with(callee, "llvm.vec.load.")) {
+        in.op = "intr";
+        in.sub = "vload";
+        in.dim = std::stoi(callee.substr(strlen("llvm.vec.load.")));
+      } else if (starts_with(callee, "llvm.vec.store.")) {
+        in.op = "intr";
+        in.sub = "vstore";
+        in.dim = std::stoi(callee.substr(strlen("llvm.vec.store.")));
+      } else if (callee == "llvm.vec.reduce.add") {
+        in.op = "intr";
+        in.sub = "vreduce";
+      } else if (callee == "llvm.memcpy.inline") {
+        in.op = "memcpy";
+        if (in.args.size() < 3) perr(line, "memcpy needs dst, src, size: " + raw);
+        in.args.resize(3);
+      } else {
+        in.op = "call";
+        in.sub = callee;
+      }
+    } else {
+      perr(line, "unknown instruction '" + op + "'");
+    }
+    define_value(in.result, in.ty, line);
+    return in;
+  }
+
+  Term parse_term(const std::string& raw, int line) {
+    Term t;
+    std::string text = raw;
+    if (starts_with(text, "ret")) {
+      t.kind = "ret";
+      return t;
+    }
+    if (starts_with(text, "switch")) {
+      t.kind = "switch";
+      Cursor c{text, 0, line};
+      c.word();
+      c.type();
+      t.cond = c.operand();
+      c.expect(",");
+      c.expect("label");
+      c.expect("%");
+      t.t = c.word();  // default
+      c.expect("[");
+      while (!c.eat("]")) {
+        const std::string lit = std::to_string(c.integer());
+        c.expect(",");
+        c.expect("label");
+        c.expect("%");
+        t.cases.push_back({lit, c.word()});
+      }
+      return t;
+    }
+    if (!starts_with(text, "br")) perr(line, "expected a terminator: " + raw);
+    auto suffix = branch_suffixes(text, line);
+    Cursor c{text, 0, line};
+    c.word();  // br
+    if (c.eat("label")) {
+      t.kind = "br";
+      c.expect("%");
+      t.t = c.word();
+      t.targs = suffix["args"];
+    } else {
+      t.kind = "condbr";
+      c.type();  // i1
+      t.cond = c.operand();
+      c.expect(",");
+      c.expect("label");
+      c.expect("%");
+      t.t = c.word();
+      c.expect(",");
+      c.expect("label");
+      c.expect("%");
+      t.f = c.word();
+      t.targs = suffix["true_args"];
+      t.fargs = suffix["false_args"];
+    }
+    return t;
+  }
+
+  static bool is_terminator(const std::string& s) {
+    return starts_with(s, "br ") || starts_with(s, "switch ") || starts_with(s, "ret");
+  }
+
+  void parse(const std::string& text) {
+    std::istringstream in(text);
+    std::string raw;
+    int line = 0;
+    bool in_fn = false, closed = false;
+    Block* cur = nullptr;
+    std::map<std::string, Param*> by_name;
+    while (std::getline(in, raw)) {
+      ++line;
+      const std::string s = trim(raw);
+      if (s.empty()) continue;
+      if (!in_fn) {
+        if (starts_with(s, ";")) continue;  // comments before the function
+        if (!starts_with(s, "define ")) perr(line, "expected 'define'");
+        Cursor c{s, 0, line};
+        c.word();
+        c.type();  // void
+        c.expect("@");
+        fn.name = c.word();
+        c.expect("(");
+        const size_t close = s.rfind(')');
+        if (close == std::string::npos || s.back() != '{') perr(line, "bad function header");
+        for (const std::string& p : split_top(s.substr(c.i, close - c.i))) {
+          Cursor pc{p, 0, line};
+          Param prm;
+          prm.ty = pc.type();
+          pc.expect("%");
+          prm.name = pc.word();
+          fn.params.push_back(prm);
+        }
+        for (auto& p : fn.params) by_name[p.name] = &p;
+        register_params();
+        in_fn = true;
+        continue;
+      }
+      if (s == "}") {
+        closed = true;
+        break;
+      }
+      if (starts_with(s, "; sile.param %")) {
+        // "; sile.param %a [rank=2, shape_offset=0, elem=f32]"
+        Cursor c{s, strlen("; sile.param %"), line};
+        const std::string name = c.word();
+        auto it = by_name.find(name);
+        if (it == by_name.end()) perr(line, "sile.param for an unknown parameter %" + name);
+        c.expect("[");
+        const size_t close = s.rfind(']');
+        for (const std::string& kv : split_top(s.substr(c.i, close - c.i))) {
+          const size_t eq = kv.find('=');
+          if (eq == std::string::npos) continue;
+          const std::string k = trim(kv.substr(0, eq)), v = trim(kv.substr(eq + 1));
+          if (k == "rank") it->second->rank = std::stoi(v);
+          else if (k == "shape_offset") it->second->shape_offset = std::stoi(v);
+          else if (k == "elem") {
+            Cursor tc{v, 0, line};
+            it->second->ty.elem = std::make_shared<Type>(tc.type());
+          }
+        }
+        types[name] = it->second->ty;
+        continue;
+      }
+      if (raw.size() && !isspace((unsigned char)raw[0]) && s.back() == ':') {
+        fn.blocks.push_back(Block{});
+        cur = &fn.blocks.back();
+        cur->name = s.substr(0, s.size() - 1);
+        continue;
+      }
+      if (!cur) perr(line, "instruction outside a block");
+      if (starts_with(s, "; args(")) {
+        // "; args(%k: i64, %acc: f32)"
+        const std::string inner = s.substr(strlen("; args("), s.size() - strlen("; args(") - 1);
+        for (const std::string& p : split_top(inner)) {
+          Cursor pc{p, 0, line};
+          pc.expect("%");
+          const std::string name = pc.word();
+          pc.expect(":");
+          Type t = pc.type();
+          cur->params.push_back({name, t});
+          define_value(name, t, line);
+        }
+        continue;
+      }
+      if (starts_with(s, ";")) continue;  // other comments
+      if (is_terminator(s)) {
+        cur->term = parse_term(s, line);
+        continue;
+      }
+      cur->insts.push_back(parse_inst(s, line));
+    }
+    if (!closed) perr(line, "missing closing '}'");
+    if (fn.blocks.empty()) perr(line, "function has no blocks");
+    for (const Block& b : fn.blocks)
+      if (b.term.kind.empty()) perr(line, "block " + b.name + " has no terminator");
+  }
+
+  // register the parameters' types before the body is parsed
+  void register_params() {
+    for (const Param& p : fn.params) types[p.name] = p.ty;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// HIP emitter
+// ---------------------------------------------------------------------------
+std::string c_scalar(const Type& t) {
+  switch (t.k) {
+    case TK::I1: return "bool";
+    case TK::I32: return "int";
+    case TK::I64: return "long long";
+    case TK::F16: return "unsigned short";  // as the C backend (codegen.rs:674)
+    case TK::F32: return "float";
+    case TK::F64: return "double";
+    case TK::Vec: return "llir_float4";
+    default: return "void";
+  }
+}
+
+// base element type and array dims of a (possibly nested) array type
+void array_shape(const Type& t, Type& base, std::vector<int64_t>& dims) {
+  const Type* cur = &t;
+  while (cur->k == TK::Arr) {
+    dims.push_back(cur->len);
+    cur = cur->elem.get();
+  }
+  base = *cur;
+}
+
+// declaration of `name` with type t
+std::string c_decl(const Type& t, const std::string& name) {
+  if (t.k == TK::Ptr) {
+    if (!t.elem) return "float* " + name;  // untyped pointer: the CPU wrapper's float*
+    Type base;
+    std::vector<int64_t> dims;
+    array_shape(*t.elem, base, dims);
+    if (dims.empty()) return c_scalar(base) + "* " + name;
+    std::string d;
+    for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
+    return c_scalar(base) + " (*" + name + ")" + d;
+  }
+  return c_scalar(t) + " " + name;
+}
+
+std::string ident(const std::string& name) {
+  std::string out = "v_";
+  for (char c : name) out += (isalnum((unsigned char)c) || c == '_') ? c : '_';
+  return out;
+}
+
+struct Emitter {
+  const Function& fn;
+  const std::map<std::string, Type>& types;
+  std::ostringstream o;
+
+  std::string opnd(const Operand& x) {
+    if (x.is_value) return ident(x.name);
+    if (x.ck == Operand::kBool) return x.name;
+    if (x.ck == Operand::kFloat) {
+      if (x.name == "inf") return "__builtin_inff()";
+      if (x.name == "-inf") return "(-__builtin_inff())";
+      if (x.name == "NaN") return "__builtin_nanf(\"\")";
+      return "(" + x.name + "f)";  // the decimal text as a float literal (emit.rs:104-110)
+    }
+    return "(" + x.name + "LL)";
+  }
+
+  static const char* bin_sym(const std::string& m) {
+    if (m == "fadd" || m == "add") return "+";
+    if (m == "fsub" || m == "sub") return "-";
+    if (m == "fmul" || m == "mul") return "*";
+    if (m == "fdiv" || m == "sdiv") return "/";
+    if (m == "and") return "&";
+    return "|";
+  }
+  static const char* cmp_sym(const std::string& p) {
+    if (p == "eq") return "==";
+    if (p == "ne") return "!=";
+    if (p == "slt" || p == "olt") return "<";
+    if (p == "sle" || p == "ole") return "<=";
+    if (p == "sgt" || p == "ogt") return ">";
+    return ">=";
+  }
+
+  void inst(const Inst& in) {
+    const std::string r = in.result.empty() ? "" : ident(in.result);
+    const auto& a = in.args;
+    if (in.op == "alloca") return;  // storage declared at the top
+    if (in.op == "gep") {
+      o << "  " << r << " = &(" << opnd(a[0]);
+      for (size_t k = 1; k < a.size(); ++k) o << "[" << opnd(a[k]) << "]";
+      o << ");\n";
+    } else if (in.op == "load") {
+      o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
+    } else if (in.op == "store") {
+      o << "  *(" << opnd(a[0]) << ") = " << opnd(a[1]) << ";\n";
+    } else if (in.op == "atomic") {
+      o << "  " << (r.empty() ? "" : r + " = ") << "atomicAdd(" << opnd(a[0]) << ", " << opnd(a[1])
+        << ");\n";
+    } else if (in.op == "memcpy") {
+      o << "  __builtin_memcpy(" << opnd(a[0]) << ", " << opnd(a[1]) << ", " << opnd(a[2])
+        << ");\n";
+    } else if (in.op == "bin") {
+      o << "  " << r << " = " << opnd(a[0]) << " " << bin_sym(in.sub) << " " << opnd(a[1])
+        << ";\n";
+    } else if (in.op == "cmp") {
+      o << "  " << r << " = " << opnd(a[0]) << " " << cmp_sym(in.sub) << " " << opnd(a[1])
+        << ";\n";
+    } else if (in.op == "cast") {
+      o << "  " << r << " = " << opnd(a[0]) << ";\n";
+    } else if (in.op == "select") {
+      o << "  " << r << " = (" << opnd(a[0]) << ") ? (" << opnd(a[1]) << ") : (" << opnd(a[2])
+        << ");\n";
+    } else if (in.op == "call") {
+      o << "  " << (r.empty() ? "" : r + " = ") << in.sub << "(";
+      for (size_t k = 0; k < a.size(); ++k) o << (k ? ", " : "") << opnd(a[k]);
+      o << ");\n";
+    } else if (in.op == "intr") {
+      if (in.sub == "tid") o << "  " << r << " = 0;\n";
+      else if (in.sub == "ctaid") o << "  " << r << " = sile_gid_" << in.dim << ";\n";
+      else if (in.sub == "barrier") o << "  (void)0;\n";
+      else if (in.sub == "exp") o << "  " << r << " = expf(" << opnd(a[0]) << ");\n";
+      else if (in.sub == "vload")
+        o << "  " << r << " = llir_vec_load_" << in.dim << "(" << opnd(a[0]) << ", " << opnd(a[1])
+          << ");\n";
+      else if (in.sub == "vstore")
+        o << "  llir_vec_store_" << in.dim << "(" << opnd(a[0]) << ", " << opnd(a[1]) << ", "
+          << opnd(a[2]) << ");\n";
+      else if (in.sub == "vreduce")
+        o << "  " << r << " = llir_vec_reduce_add(" << opnd(a[0]) << ");\n";
+    }
+  }
+
+  // parallel assignment of branch arguments, then the jump
+  void jump(const std::string& target, const std::vector<Operand>& args) {
+    const Block* b = nullptr;
+    for (const Block& x : fn.blocks)
+      if (x.name == target) b = &x;
+    if (!b) throw ParseError{"branch to unknown block %" + target};
+    if (args.size() != b->params.size())
+      throw ParseError{"branch to %" + target + " passes " + std::to_string(args.size()) +
+                       " arguments for " + std::to_string(b->params.size()) + " parameters"};
+    if (!args.empty()) {
+      o << "  {\n";
+      for (size_t k = 0; k < args.size(); ++k)
+        o << "    " << c_decl(b->params[k].second, "t" + std::to_string(k)) << " = "
+          << opnd(args[k]) << ";\n";
+      for (size_t k = 0; k < args.size(); ++k)
+        o << "    " << ident(b->params[k].first) << " = t" << k << ";\n";
+      o << "  }\n";
+    }
+    o << "  goto L_" << ident(target) << ";\n";
+  }
+
+  void term(const Term& t) {
+    if (t.kind == "ret") {
+      o << "  return;\n";
+    } else if (t.kind == "br") {
+      jump(t.t, t.targs);
+    } else if (t.kind == "condbr") {
+      o << "  if (" << opnd(t.cond) << ") {\n";
+      jump(t.t, t.targs);
+      o << "  } else {\n";
+      jump(t.f, t.fargs);
+      o << "  }\n";
+    } else if (t.kind == "switch") {
+      o << "  switch (" << opnd(t.cond) << ") {\n";
+      for (auto& c : t.cases) o << "    case " << c.first << "LL: goto L_" << ident(c.second) << ";\n";
+      o << "    default: goto L_" << ident(t.t) << ";\n  }\n";
+    }
+  }
+
+  bool is_shapes(const Param& p) const { return p.name == "__sile_shapes"; }
+
+  void body() {
+    o << "__device__ static void sile_llvm_ir_" << fn.name << "(";
+    for (size_t k = 0; k < fn.params.size(); ++k) {
+      const Param& p = fn.params[k];
+      o << (k ? ", " : "") << (is_shapes(p) ? "long long* " + ident(p.name) : c_decl(p.ty, ident(p.name)));
+    }
+    o << ", long long sile_gid_0, long long sile_gid_1, long long sile_gid_2) {\n";
+    o << "  (void)sile_gid_0; (void)sile_gid_1; (void)sile_gid_2;\n";
+    // declarations: block parameters, instruction results, alloca storage
+    for (const Block& b : fn.blocks) {
+      for (auto& p : b.params) o << "  " << c_decl(p.second, ident(p.first)) << ";\n";
+      for (const Inst& in : b.insts) {
+        if (in.result.empty()) continue;
+        if (in.op == "alloca") {
+          Type base;
+          std::vector<int64_t> dims;
+          array_shape(in.aux, base, dims);
+          std::string d;
+          for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
+          if (dims.empty()) d = "[1]";
+          o << "  " << c_scalar(base) << " " << ident(in.result) << "_storage" << d << ";\n";
+          if (dims.empty())
+            o << "  " << c_scalar(base) << "* " << ident(in.result) << " = " << ident(in.result)
+              << "_storage;\n";
+          else
+            o << "  " << c_decl(in.ty, ident(in.result)) << " = &" << ident(in.result)
+              << "_storage;\n";
+        } else {
+          o << "  " << c_decl(in.ty, ident(in.result)) << ";\n";
+        }
+      }
+    }
+    for (const Block& b : fn.blocks) {
+      o << "L_" << ident(b.name) << ":;\n";
+      for (const Inst& in : b.insts) inst(in);
+      term(b.term);
+    }
+    o << "}\n\n";
+  }
+
+  // the CPU backend's launch wrapper (crates/sile-backend/src/cpu/codegen.rs:409-555)
+  void wrapper(int64_t plan_out, int64_t rows, int64_t cols) {
+    const Param* out_param = nullptr;
+    if (plan_out >= 0) {
+      if (plan_out >= (int64_t)fn.params.size() || fn.params[plan_out].rank < 0)
+        throw ParseError{"tile plan names parameter " + std::to_string(plan_out) +
+                         ", which has no shape ABI"};
+      out_param = &fn.params[plan_out];
+    }
+    const Param* last_buf = nullptr;
+    const Param* first_buf = nullptr;
+    for (const Param& p : fn.params) {
+      if (is_shapes(p)) continue;
+      if (!first_buf) first_buf = &p;
+      last_buf = &p;
+    }
+    o << "extern \"C\" __global__ __launch_bounds__(64) void sile_kernel_" << fn.name
+      << "(void** buffers, long long num_programs, const long long* shapes, long long num_shapes) {\n";
+    o << "  const long long sile_pid = (long long)blockIdx.x * 64 + threadIdx.x;\n";
+    o << "  if (sile_pid >= num_programs) return;\n";
+    o << "  (void)num_shapes;\n";
+    // buffers in parameter order, each bound as its parameter's pointer type
+    int bi = 0;
+    for (const Param& p : fn.params) {
+      if (is_shapes(p)) continue;
+      o << "  " << c_decl(p.ty, ident(p.name)) << " = (" << c_decl(p.ty, "") << ")buffers["
+        << bi++ << "];\n";
+    }
+    auto tile_count = [&](const Param& abi_param, int64_t r, int64_t c) {
+      if (abi_param.rank == 1) {
+        o << "  const long long sile_total_tiles = shapes[" << abi_param.shape_offset << "];\n";
+        o << "  const long long sile_tiles_n = 1;\n";
+      } else {
+        o << "  const long long sile_tiles_n = shapes[" << abi_param.shape_offset + 1 << "] / " << c
+          << ";\n";
+        o << "  const long long sile_total_tiles = (shapes[" << abi_param.shape_offset << "] / " << r
+          << ") * sile_tiles_n;\n";
+      }
+    };
+    int output_rank = 1;
+    if (out_param) {
+      tile_count(*out_param, rows, cols);
+      output_rank = out_param->rank;
+    } else if (last_buf && last_buf->rank >= 0) {
+      output_rank = last_buf->rank;
+      if (last_buf->rank == 1) {
+        const Param& fb = (first_buf && first_buf->rank >= 0) ? *first_buf : *last_buf;
+        o << "  const long long sile_total_tiles = shapes[" << fb.shape_offset << "];\n";
+        o << "  const long long sile_tiles_n = 1;\n";
+      } else {
+        tile_count(*last_buf, 32, 16);
+      }
+    } else {
+      const Param* fp = fn.params.empty() ? nullptr : &fn.params[0];
+      if (fp && !is_shapes(*fp) && fp->rank >= 0)
+        o << "  const long long sile_total_tiles = shapes[" << fp->shape_offset << "];\n";
+      else
+        o << "  const long long sile_total_tiles = num_programs;\n";
+      o << "  const long long sile_tiles_n = 1;\n";
+      output_rank = last_buf && last_buf->rank >= 0 ? last_buf->rank : 1;
+    }
+    o << "  if (sile_pid < sile_total_tiles) {\n";
+    if (output_rank <= 1)
+      o << "    const long long g0 = sile_pid, g1 = 0;\n";
+    else
+      o << "    const long long g0 = sile_pid / sile_tiles_n, g1 = sile_pid % sile_tiles_n;\n";
+    o << "    (void)sile_tiles_n;\n";
+    o << "    sile_llvm_ir_" << fn.name << "(";
+    for (size_t k = 0; k < fn.params.size(); ++k)
+      o << (k ? ", " : "") << (is_shapes(fn.params[k]) ? "(long long*)shapes" : ident(fn.params[k].name));
+    o << ", g0, g1, 0);\n  }\n}\n";
+  }
+
+  std::string emit(int64_t plan_out, int64_t rows, int64_t cols) {
+    o << "// generated from sile LLIR function @" << fn.name << " for gfx950\n";
+    o << "struct llir_float4 { float v[4]; };\n";
+    o << "__device__ static inline llir_float4 llir_vec_load_4(const float* p, long long off) {\n"
+         "  llir_float4 r; r.v[0] = p[off]; r.v[1] = p[off + 1]; r.v[2] = p[off + 2]; "
+         "r.v[3] = p[off + 3]; return r;\n}\n";
+    o << "__device__ static inline void llir_vec_store_4(float* p, long long off, llir_float4 v) {\n"
+         "  p[off] = v.v[0]; p[off + 1] = v.v[1]; p[off + 2] = v.v[2]; p[off + 3] = v.v[3];\n}\n";
+    o << "__device__ static inline float llir_vec_reduce_add(llir_float4 v) {\n"
+         "  return v.v[0] + v.v[1] + v.v[2] + v.v[3];\n}\n\n";
+    body();
+    wrapper(plan_out, rows, cols);
+    return o.str();
+  }
+};
+
+// parse + emit; returns a status and fills `src` / the last error
+int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::string& src,
+           std::string& name) {
+  if (!text) return fail(SILE_ERR_SHAPE, "LLIR text is NULL");
+  if (plan_out >= 0 && (rows <= 0 || cols <= 0))
+    return fail(SILE_ERR_SHAPE, "tile plan needs positive rows and cols");
+  try {
+    Parser p;
+    p.parse(std::string(text));
+    Emitter e{p.fn, p.types, {}};
+    src = e.emit(plan_out, rows, cols);
+    name = "sile_kernel_" + p.fn.name;
+  } catch (const ParseError& e) {
+    return fail(SILE_ERR_COMPILE, "%s", e.msg.c_str());
+  } catch (const std::exception& e) {
+    return fail(SILE_ERR_COMPILE, "LLIR: %s", e.what());
+  }
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int sile_hip_llir_to_hip(const char* llir_text, int64_t plan_output_param, int64_t plan_rows,
+                         int64_t plan_cols, char* out, size_t out_capacity, size_t* out_len) {
+  std::string src, name;
+  int rc = to_hip(llir_text, plan_output_param, plan_rows, plan_cols, src, name);
+  if (rc != SILE_OK) return rc;
+  if (out_len) *out_len = src.size();
+  if (out && out_capacity) {
+    const size_t n = std::min(out_capacity - 1, src.size());
+    memcpy(out, src.data(), n);
+    out[n] = 0;
+    if (n < src.size()) return fail(SILE_ERR_SHAPE, "output buffer too small (%zu bytes needed)", src.size() + 1);
+  }
+  return ok();
+}
+
+int sile_hip_llir_compile(const char* llir_text, int64_t plan_output_param, int64_t plan_rows,
+                          int64_t plan_cols, void** code_out, size_t* code_bytes,
+                          char* kernel_name, size_t name_capacity) {
+  std::string src, name;
+  int rc = to_hip(llir_text, plan_output_param, plan_rows, plan_cols, src, name);
+  if (rc != SILE_OK) return rc;
+  if (!code_out || !code_bytes) return fail(SILE_ERR_SHAPE, "NULL output pointer");
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "sile_llir.hip", 0, nullptr, nullptr) !=
+      HIPRTC_SUCCESS)
+    return fail(SILE_ERR_COMPILE, "hiprtcCreateProgram failed");
+  // -ffp-contract=off: the CPU backend's C is compiled without contraction
+  // (crates/sile-backend/src/cpu/mod.rs:83, no -march, no FMA)
+  const char* opts[] = {"--offload-arch=gfx950", "-O3",     "-ffp-contract=off", "-Xclang",
+                        "-target-feature",       "-Xclang", "-packed-fp32-ops"};
+  const hiprtcResult r = hiprtcCompileProgram(prog, 7, opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t ls = 0;
+    hiprtcGetProgramLogSize(prog, &ls);
+    std::string log(ls + 1, '\0');
+    hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return fail(SILE_ERR_COMPILE, "hiprtc: %s\n%s\n--- generated source ---\n%s",
+                hiprtcGetErrorString(r), log.c_str(), src.c_str());
+  }
+  size_t cs = 0;
+  hiprtcGetCodeSize(prog, &cs);
+  void* code = malloc(cs);
+  if (!code) {
+    hiprtcDestroyProgram(&prog);
+    return fail(SILE_ERR_RUNTIME, "out of host memory");
+  }
+  hiprtcGetCode(prog, static_cast<char*>(code));
+  hiprtcDestroyProgram(&prog);
+  *code_out = code;
+  *code_bytes = cs;
+  if (kernel_name && name_capacity) {
+    const size_t n = std::min(name_capacity - 1, name.size());
+    memcpy(kernel_name, name.data(), n);
+    kernel_name[n] = 0;
+  }
+  return ok();
+}
+
+void sile_hip_llir_free_code(void* code) { free(code); }
+
+}  // extern "C"

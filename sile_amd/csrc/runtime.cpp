@@ -330,19 +330,16 @@ int sile_hip_module_get(sile_hip_module module, const char* name, sile_hip_funct
   return ok();
 }
 
-int sile_hip_launch_tiles(sile_hip_function fn, void* const* buffers, int64_t num_buffers,
-                          const int64_t* shapes, int64_t num_shapes, const uint32_t grid[3],
-                          uint32_t threads_per_program, sile_hip_stream stream) {
-  if (!fn) return fail(SILE_ERR_COMPILE, "function is NULL");
-  if (!grid) return fail(SILE_ERR_SHAPE, "grid not set");
-  if (num_buffers < 0 || num_shapes < 0 || (num_buffers && !buffers) || (num_shapes && !shapes))
-    return fail(SILE_ERR_SHAPE, "buffers/shapes arrays do not match their counts");
-  if (threads_per_program == 0 || threads_per_program > 1024)
-    return fail(SILE_ERR_SHAPE, "threads_per_program %u not in [1, 1024]", threads_per_program);
-  const int64_t programs = (int64_t)grid[0] * grid[1] * grid[2];
-  if (programs == 0) return ok();
-  if (programs > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many programs (%lld)", (long long)programs);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+}  // extern "C"
+
+namespace {
+
+// Uploads the buffer-pointer and shape tables, launches `fn` over `workgroups`
+// workgroups of `threads` threads with (buffers, programs, shapes, num_shapes)
+// and waits for it.
+int launch_with_tables(hipFunction_t fn, void* const* buffers, int64_t num_buffers,
+                       const int64_t* shapes, int64_t num_shapes, int64_t programs,
+                       int64_t workgroups, uint32_t threads, hipStream_t s) {
   // Device copies of the pointer and shape tables, as the Metal runtime binds a
   // shapes buffer after the args (crates/sile-backend/src/metal/mod.rs:131-144).
   const size_t buf_bytes = (size_t)num_buffers * sizeof(void*);
@@ -358,14 +355,56 @@ int sile_hip_launch_tiles(sile_hip_function fn, void* const* buffers, int64_t nu
     void* dev_shapes = static_cast<unsigned char*>(table) + buf_bytes;
     int64_t np = programs, ns = num_shapes;
     void* params[] = {&dev_buffers, &np, &dev_shapes, &ns};
-    e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), (unsigned)programs, 1, 1,
-                              threads_per_program, 1, 1, 0, s, params, nullptr);
+    e = hipModuleLaunchKernel(fn, (unsigned)workgroups, 1, 1, threads, 1, 1, 0, s, params, nullptr);
   }
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   hipError_t e2 = hipFree(table);
-  if (e != hipSuccess) return hip_fail(e, "sile_hip_launch_tiles");
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
   if (e2 != hipSuccess) return hip_fail(e2, "hipFree");
   return ok();
+}
+
+int check_launch_args(sile_hip_function fn, void* const* buffers, int64_t num_buffers,
+                      const int64_t* shapes, int64_t num_shapes, const uint32_t grid[3],
+                      int64_t* programs) {
+  if (!fn) return fail(SILE_ERR_COMPILE, "function is NULL");
+  if (!grid) return fail(SILE_ERR_SHAPE, "grid not set");
+  if (num_buffers < 0 || num_shapes < 0 || (num_buffers && !buffers) || (num_shapes && !shapes))
+    return fail(SILE_ERR_SHAPE, "buffers/shapes arrays do not match their counts");
+  *programs = (int64_t)grid[0] * grid[1] * grid[2];
+  if (*programs > 0x7fffffffLL)
+    return fail(SILE_ERR_SHAPE, "too many programs (%lld)", (long long)*programs);
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int sile_hip_launch_tiles(sile_hip_function fn, void* const* buffers, int64_t num_buffers,
+                          const int64_t* shapes, int64_t num_shapes, const uint32_t grid[3],
+                          uint32_t threads_per_program, sile_hip_stream stream) {
+  int64_t programs = 0;
+  int rc = check_launch_args(fn, buffers, num_buffers, shapes, num_shapes, grid, &programs);
+  if (rc != SILE_OK) return rc;
+  if (threads_per_program == 0 || threads_per_program > 1024)
+    return fail(SILE_ERR_SHAPE, "threads_per_program %u not in [1, 1024]", threads_per_program);
+  if (programs == 0) return ok();
+  return launch_with_tables(static_cast<hipFunction_t>(fn), buffers, num_buffers, shapes,
+                            num_shapes, programs, programs, threads_per_program,
+                            static_cast<hipStream_t>(stream));
+}
+
+int sile_hip_launch_llir(sile_hip_function fn, void* const* buffers, int64_t num_buffers,
+                         const int64_t* shapes, int64_t num_shapes, const uint32_t grid[3],
+                         sile_hip_stream stream) {
+  int64_t programs = 0;
+  int rc = check_launch_args(fn, buffers, num_buffers, shapes, num_shapes, grid, &programs);
+  if (rc != SILE_OK) return rc;
+  if (programs == 0) return ok();
+  return launch_with_tables(static_cast<hipFunction_t>(fn), buffers, num_buffers, shapes,
+                            num_shapes, programs, (programs + 63) / 64, 64,
+                            static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

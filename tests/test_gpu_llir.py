@@ -1,0 +1,100 @@
+"""GPU runs of kernels generated from LLIR (tests/golden/llir/, hand-written in
+the reference's printed form) through sile_hip_llir_compile + module_load +
+sile_hip_launch_llir, against the reference's fixtures and the CPU oracle.
+vec_add, relu and matmul are bit-exact (the matmul in the canonical order,
+compiled without contraction); softmax is within 1e-6 relative of the oracle
+(device expf against the host's), parallel_reduce within float rounding of
+the atomic order."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import cpuref
+from tests.helpers import assert_close, rng, say
+from tests.test_llir import PLANS, text
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_fixtures.json")
+
+
+@pytest.fixture(scope="module")
+def fixtures():
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module")
+def kernels(hip):
+    ks = {name: hip.LlirKernel(text(name), plan) for name, plan in PLANS.items()}
+    yield ks
+    for k in ks.values():
+        k.close()
+
+
+def _run(hip, kern, arrays, grid):
+    bufs = [hip.DeviceBuffer.from_array(a) for a in arrays]
+    shapes = [d for a in arrays for d in a.shape]
+    kern([b.ptr for b in bufs], shapes, grid)
+    return [b.download(a.dtype, a.shape) for b, a in zip(bufs, arrays)]
+
+
+def test_vec_add(hip, kernels, fixtures):
+    fx = fixtures["vec_add"]
+    say("llir vec_add fixture and 4096 random")
+    a = np.full(16, fx["a_fill"], np.float32)
+    b = np.full(16, fx["b_fill"], np.float32)
+    c = _run(hip, kernels["vec_add"], [a, b, np.zeros(16, np.float32)], (4, 1, 1))[2]
+    np.testing.assert_array_equal(c, fx["expected_fill"])
+    a, b = rng(1).normal(size=4096).astype(np.float32), rng(2).normal(size=4096).astype(np.float32)
+    c = _run(hip, kernels["vec_add"], [a, b, np.zeros(4096, np.float32)], (1024, 1, 1))[2]
+    np.testing.assert_array_equal(c, a + b)
+
+
+def test_relu(hip, kernels, fixtures):
+    fx = fixtures["relu_8"]
+    say("llir relu fixture")
+    x = _run(hip, kernels["relu"], [np.array(fx["x"], np.float32)], (1, 1, 1))[0]
+    np.testing.assert_array_equal(x, np.array(fx["expected"], np.float32))
+
+
+def test_matmul(hip, kernels, fixtures):
+    fx = fixtures["matmul_4x4"]
+    say("llir matmul 4x4 fixture and 64x40x48 bit-exact")
+    a = np.array(fx["a"]["data"], np.float32).reshape(fx["a"]["shape"])
+    b = np.array(fx["b"]["data"], np.float32).reshape(fx["b"]["shape"])
+    c = _run(hip, kernels["matmul"], [a, b, np.zeros((4, 4), np.float32)], (4, 1, 1))[2]
+    np.testing.assert_array_equal(c.ravel(), np.array(fx["expected"], np.float32))
+    a = rng(3).uniform(-1, 1, size=(64, 41)).astype(np.float32)   # K' = 40 (BK = 2)
+    b = rng(4).uniform(-1, 1, size=(41, 48)).astype(np.float32)
+    grid = (32 * 24, 1, 1)
+    got = _run(hip, kernels["matmul"], [a, b, np.zeros((64, 48), np.float32)], grid)[2]
+    ref = np.zeros((64, 48), np.float32)
+    cpuref.kernel_matmul(a, b, ref, grid, 2, 2, 2)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_softmax(hip, kernels, fixtures):
+    fx = fixtures["softmax_4x8"]
+    say("llir softmax fixture and [64, 8] random")
+    x = np.array(fx["x"]["data"], np.float32).reshape(fx["x"]["shape"])
+    y = _run(hip, kernels["softmax"], [x, np.zeros_like(x)], tuple(fx["grid"]))[1]
+    np.testing.assert_allclose(y.sum(axis=1), fx["expected_row_sum"], atol=fx["tolerance_abs"])
+    x = rng(5).normal(scale=2.0, size=(64, 8)).astype(np.float32)
+    y = _run(hip, kernels["softmax"], [x, np.zeros_like(x)], (32, 1, 1))[1]
+    ref = np.zeros_like(x)
+    cpuref.kernel_softmax(x, ref, (32, 1, 1), 2, 8)
+    assert_close(y, ref, atol=1e-7, rtol=1e-6, what="llir softmax")
+
+
+def test_parallel_reduce(hip, kernels):
+    say("llir parallel_reduce: 100000 ones and 1600 random")
+    x = np.ones(100000, np.float32)
+    out = _run(hip, kernels["parallel_reduce"], [x, np.zeros(1, np.float32)], (6250, 1, 1))[1]
+    assert out[0] == 100000.0
+    x = rng(6).uniform(0, 1, size=1600).astype(np.float32)
+    out = _run(hip, kernels["parallel_reduce"], [x, np.zeros(1, np.float32)], (100, 1, 1))[1]
+    parts = cpuref.parallel_reduce_partials(x, 100, 16)
+    assert_close(out[0], parts.astype(np.float64).sum(), atol=1e-3, rtol=1e-5, what="llir reduce")
