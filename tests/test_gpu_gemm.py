@@ -143,6 +143,44 @@ def test_truncated_k_ignores_nonfinite_tail(hip, kind):
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+def test_padded_leading_dimensions(hip, kind):
+    """A, B and C inside larger row pitches (lda > K, ldb > K, ldc > N): the
+    padding is never read into the result and never written."""
+    m, n, k = 512, 256, 320
+    lda, ldb, ldc = k + 64, k + 128, n + 64
+    say(f"gemm {kind} {m}x{n}x{k} lda={lda} ldb={ldb} ldc={ldc}")
+    a = rng(13).normal(size=(m, k)).astype(np.float32)
+    bt = rng(14).normal(size=(n, k)).astype(np.float32)
+    if kind == "bf16":
+        a /= np.sqrt(k)
+        bt /= np.sqrt(k)
+        qa, a_f = bf16_round(a)
+        qb, b_f = bf16_round(bt)
+        t, sa, sb, pad = hip.BF16, 1.0, 1.0, 0x7FC0   # NaN in the padding
+        ref = cpuref.gemm_nt(a_f, b_f)
+    else:
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t, pad = hip.F8E4M3, 0x7F
+        ref = cpuref.gemm_nt(a_f, b_f)
+    ap = np.full((m, lda), pad, qa.dtype)
+    ap[:, :k] = qa
+    bp = np.full((n, ldb), pad, qb.dtype)
+    bp[:, :k] = qb
+    da, db = hip.DeviceBuffer.from_array(ap), hip.DeviceBuffer.from_array(bp)
+    dc = hip.DeviceBuffer(m * ldc * 4)
+    dc.fill_bytes(0xFF)
+    hip.gemm(t, t, hip.F32, m, n, k, da.ptr, lda, hip.ROW_MAJOR, db.ptr, ldb, hip.COL_MAJOR,
+             dc.ptr, ldc, sa, sb)
+    hip.synchronize()
+    got = dc.download(np.float32, (m, ldc))
+    tol = (1e-4, 1e-4) if kind == "bf16" else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} padded")
+    # the columns past N keep the 0xFF fill
+    assert (got[:, n:].view(np.uint32) == 0xFFFFFFFF).all()
+
+
 def test_f32_gemm_exact(hip):
     say("gemm f32 exact 200x300x150 (both B layouts)")
     m, n, k = 200, 300, 150
