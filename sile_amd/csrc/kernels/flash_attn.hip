@@ -699,8 +699,8 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     v2::attn_fwd_v2<BF, QT, W, NK, SCHED>(Q, K, V, O, a, smem);                               \
   }
 // 4 waves x 64 queries (one wave per SIMD) and 8 waves x 32 queries (two per
-// SIMD) over 32-key blocks; 8 waves x 32 queries over 64-key blocks with the
-// issue order fixed (the default)
+// SIMD, the default) over 32-key blocks; 8 waves x 32 queries over 64-key
+// blocks with the issue order fixed
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false, 2, 4, 32, 0)
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true, 2, 4, 32, 0)
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 0)

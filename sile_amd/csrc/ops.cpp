@@ -336,17 +336,17 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     return fail(SILE_ERR_SHAPE, "attention too large");
 
   // MFMA flash kernels: head_dim 128, 16-byte aligned operands.
-  //   v2k64 (default) / v2w8 / v2 (pipelined, 256-query blocks, 8 waves x 32
-  //   queries or 4 waves x 64 queries, 64- or 32-key blocks): S a multiple of 256;
+  //   v2w8 (default) / v2k64 / v2 (pipelined, 256-query blocks, 8 waves x 32
+  //   queries or 4 waves x 64 queries, 32- or 64-key blocks): S a multiple of 256;
   //   q1 / q2 (128- / 256-query blocks): S a multiple of 128 / 256.
   // SILE_HIP_FA_KERNEL=v2|v2w8|v2k64|q1|q2 overrides the choice (tuning, tests).
   if (head_dim == 128 && seq_len % 128 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
       aligned16(o)) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
     const char* env = getenv("SILE_HIP_FA_KERNEL");
-    std::string variant = env ? env : "v2k64";
+    std::string variant = env ? env : "v2w8";
     const bool pipelined = variant == "v2" || variant == "v2w8" || variant == "v2k64";
-    if (!pipelined && variant != "q1" && variant != "q2") variant = "v2k64";
+    if (!pipelined && variant != "q1" && variant != "q2") variant = "v2w8";
     if (seq_len % 256 != 0 || (variant == "q2" && dtype != SILE_F16)) variant = "q1";
     const int64_t bq = variant == "q1" ? 128 : 256;
     struct {
