@@ -10,10 +10,10 @@
 // read from HBM once and y written once (4 bytes per fp16 element in total).
 // The 128-bit loads and stores are non-temporal (streaming data, no reuse):
 // measured 5.4 TB/s on [8192, 8192] fp16, the rate of a plain device copy.
-// Each lane owns kChunks chunks of 8 consecutive elements; chunk j of lane l
-// starts at column (j * 64 + l) * 8, so every load/store instruction of the
-// wave moves one contiguous span (1 KiB for 16-bit types) with 128-bit
-// accesses.  The max and the sum are wave all-reductions over DPP row permutes
+// Each lane owns kChunks chunks of E consecutive elements (E = 8 for 16-bit
+// inputs, 4 for fp32, one 128-bit access); chunk j of lane l starts at column
+// (j * 64 + l) * E, so every load instruction of the wave reads one
+// contiguous KiB of the row.  The max and the sum are wave all-reductions over DPP row permutes
 // (common.h).  exp(x - m) is evaluated as 2^((x - m) * log2 e) on v_exp_f32.
 // Rows are assigned four per 256-thread workgroup.
 #include "common.h"
@@ -37,6 +37,14 @@ struct Elem<kF32> {
     f32x4 a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
     __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
     __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(p + 4));
+  }
+  SILE_DEV static void load4(const float* p, float v[4]) {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  }
+  SILE_DEV static void store4(float* p, const float v[4]) {
+    f32x4 a = {v[0], v[1], v[2], v[3]};
+    __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
   }
   SILE_DEV static float load1(const float* p) { return *p; }
   SILE_DEV static void store1(float* p, float v) { *p = v; }
@@ -86,25 +94,49 @@ struct Elem<kBF16> {
   SILE_DEV static void store1(uint16_t* p, float v) { *p = bf16_rne(v); }
 };
 
-// ---- register-resident row softmax: cols == kChunks * 512 ----
+// Elements per lane chunk: one 16-byte access of the input, so that each
+// load instruction of the wave reads 1 KiB of contiguous row.  fp32 -> fp32
+// uses 4; the 16-bit inputs use 8.
+template <int kIn, int kOut>
+constexpr int chunk_elems() {
+  return kIn == kF32 && kOut == kF32 ? 4 : 8;
+}
+
+template <int kT, int kE>
+SILE_DEV void load_chunk(const typename Elem<kT>::Storage* p, float* v) {
+  if constexpr (kE == 4)
+    Elem<kT>::load4(p, v);
+  else
+    Elem<kT>::load8(p, v);
+}
+template <int kT, int kE>
+SILE_DEV void store_chunk(typename Elem<kT>::Storage* p, const float* v) {
+  if constexpr (kE == 4)
+    Elem<kT>::store4(p, v);
+  else
+    Elem<kT>::store8(p, v);
+}
+
+// ---- register-resident row softmax: cols == kChunks * 64 * chunk_elems ----
 template <int kIn, int kOut, int kChunks>
 __device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Storage* __restrict__ xr,
                                                  typename Elem<kOut>::Storage* __restrict__ yr,
                                                  int lane) {
-  float v[kChunks][8];
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  float v[kChunks][kE];
 #pragma unroll
-  for (int j = 0; j < kChunks; ++j) Elem<kIn>::load8(xr + (j * 64 + lane) * 8, v[j]);
+  for (int j = 0; j < kChunks; ++j) load_chunk<kIn, kE>(xr + (j * 64 + lane) * kE, v[j]);
   float m = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < kChunks; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmax_ordered(m, v[j][i]);
+    for (int i = 0; i < kE; ++i) m = fmax_ordered(m, v[j][i]);
   m = wave_max(m);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < kChunks; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kE; ++i) {
       v[j][i] = exp2_fast((v[j][i] - m) * kLog2e);
       s += v[j][i];
     }
@@ -113,9 +145,82 @@ __device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Stora
 #pragma unroll
   for (int j = 0; j < kChunks; ++j) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[j][i] *= inv;
-    Elem<kOut>::store8(yr + (j * 64 + lane) * 8, v[j]);
+    for (int i = 0; i < kE; ++i) v[j][i] *= inv;
+    store_chunk<kOut, kE>(yr + (j * 64 + lane) * kE, v[j]);
   }
+}
+
+// ---- 16-bit row softmax holding the row packed: cols == kChunks * 512 ----
+// The row stays in registers as raw 16-bit pairs (4 VGPRs per chunk instead of
+// 8), and exp(x - m) is evaluated twice (for the sum, then for the output),
+// so a wave needs about half the registers of softmax_row_regs and more waves
+// (more bytes of row in flight) fit on a SIMD.
+template <int kT>
+SILE_DEV void unpack8(const u32x4& w, float v[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = w[i];
+    if constexpr (kT == kF16) {
+      const f16x2 h = __builtin_bit_cast(f16x2, u);
+      v[2 * i] = (float)h[0];
+      v[2 * i + 1] = (float)h[1];
+    } else {
+      v[2 * i] = bits_f32(u << 16);
+      v[2 * i + 1] = bits_f32(u & 0xffff0000u);
+    }
+  }
+}
+
+template <int kT, int kChunks>
+__device__ __forceinline__ void softmax_row_packed(const uint16_t* __restrict__ xr,
+                                                   uint16_t* __restrict__ yr, int lane) {
+  u32x4 w[kChunks];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+    w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + (j * 64 + lane) * 8));
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    float v[8];
+    unpack8<kT>(w[j], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmax_ordered(m, v[i]);
+  }
+  m = wave_max(m);
+  // Opaque to the optimiser: without it the conversions of the first pass are
+  // kept alive for the later ones, which is the register cost this kernel avoids.
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) asm volatile("" : "+v"(w[j]));
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    float v[8];
+    unpack8<kT>(w[j], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += exp2_fast((v[i] - m) * kLog2e);
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) asm volatile("" : "+v"(w[j]));
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    float v[8];
+    unpack8<kT>(w[j], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = exp2_fast((v[i] - m) * kLog2e) * inv;
+    Elem<kT>::store8(yr + (j * 64 + lane) * 8, v);
+  }
+}
+
+template <int kT, int kChunks>
+__device__ __forceinline__ void softmax_rows_packed_kernel(const void* x, void* y, int64_t rows,
+                                                           int64_t ldx, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  softmax_row_packed<kT, kChunks>(static_cast<const uint16_t*>(x) + row * ldx,
+                                  static_cast<uint16_t*>(y) + row * ldy, lane);
 }
 
 template <int kIn, int kOut, int kChunks>
@@ -172,7 +277,18 @@ __device__ __forceinline__ void softmax_rows_generic_kernel(const void* x, void*
 SILE_SOFTMAX_WIDTHS(f16_f16, kF16, kF16)
 SILE_SOFTMAX_WIDTHS(bf16_bf16, kBF16, kBF16)
 SILE_SOFTMAX_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_REGS(sile_softmax_rows_f32_f32_c32, kF32, kF32, 32)
 SILE_SOFTMAX_WIDTHS(f16_f32, kF16, kF32)
+
+#define SILE_SOFTMAX_PACKED(NAME, T, CH)                                                     \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows, \
+                                                         int64_t ldx, int64_t ldy) {         \
+    softmax_rows_packed_kernel<T, CH>(x, y, rows, ldx, ldy);                                 \
+  }
+SILE_SOFTMAX_PACKED(sile_softmax_rows_f16_f16_p8, kF16, 8)
+SILE_SOFTMAX_PACKED(sile_softmax_rows_f16_f16_p16, kF16, 16)
+SILE_SOFTMAX_PACKED(sile_softmax_rows_bf16_bf16_p8, kBF16, 8)
+SILE_SOFTMAX_PACKED(sile_softmax_rows_bf16_bf16_p16, kBF16, 16)
 
 // ---- row reduce (ReduceMax / ReduceSum along axis 1), fp32 result ----
 // op 0 = max (order-independent, so identical to the reference's fold),
@@ -185,14 +301,15 @@ __device__ __forceinline__ void reduce_rows_kernel(int op, int vec, const void* 
   if (row >= rows) return;
   using TI = typename Elem<kIn>::Storage;
   const TI* xr = static_cast<const TI*>(x) + row * ldx;
-  const int64_t vec_cols = vec ? (cols & ~(int64_t)7) : 0;
+  constexpr int kE = chunk_elems<kIn, kF32>();  // one 16-byte load per lane
+  const int64_t vec_cols = vec ? (cols & ~(int64_t)(kE - 1)) : 0;
   float acc = op == 0 ? -__builtin_inff() : 0.0f;
-  int64_t c = (int64_t)lane * 8;
-  for (; c < vec_cols; c += 512) {
-    float v[8];
-    Elem<kIn>::load8(xr + c, v);
+  int64_t c = (int64_t)lane * kE;
+  for (; c + kE <= vec_cols; c += 64 * kE) {
+    float v[kE];
+    load_chunk<kIn, kE>(xr + c, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
   }
   for (int64_t cc = vec_cols + lane; cc < cols; cc += 64) {
     const float v = Elem<kIn>::load1(xr + cc);

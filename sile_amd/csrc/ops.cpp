@@ -269,15 +269,29 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
-  const bool vec_ok = ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y);
+  // register-resident kernels: a row of chunks * 64 lanes * E elements, E = 4
+  // for fp32 -> fp32 (one 16-byte access per lane and chunk), 8 otherwise
+  const bool f32_rows = in_type == SILE_F32 && out_type == SILE_F32;
+  const int64_t elems = f32_rows ? 4 : 8;
+  const int64_t ib = dtype_bytes(in_type), ob = dtype_bytes(out_type);
+  const bool vec_ok = (ldx * ib) % 16 == 0 && (ldy * ob) % 16 == 0 && aligned16(x) && aligned16(y);
   int chunks = 0;
   if (vec_ok) {
-    for (int c : {1, 2, 4, 8, 16})
-      if (cols == (int64_t)c * 512) chunks = c;
+    for (int c : {1, 2, 4, 8, 16, 32})
+      if (cols == (int64_t)c * 64 * elems && (c < 32 || f32_rows)) chunks = c;
   }
   char name[64];
   int rc;
-  if (chunks) {
+  // 16-bit rows of 4096 / 8192: the packed-row kernel (see softmax.hip) unless
+  // SILE_HIP_SOFTMAX_PACKED=0
+  const char* pk = getenv("SILE_HIP_SOFTMAX_PACKED");
+  const bool packed = (chunks == 8 || chunks == 16) && !(pk && pk[0] == '0') &&
+                      (!strcmp(tag, "f16_f16") || !strcmp(tag, "bf16_bf16"));
+  if (packed) {
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_p%d", tag, chunks);
+    void* params[] = {&x, &y, &rows, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
+  } else if (chunks) {
     snprintf(name, sizeof name, "sile_softmax_rows_%s_c%d", tag, chunks);
     void* params[] = {&x, &y, &rows, &ldx, &ldy};
     rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
