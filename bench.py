@@ -253,6 +253,45 @@ def bench_llir_vec_add(name, steps, warmup):
     return res
 
 
+def bench_tile_ir_softmax(name, steps, warmup):
+    """softmax<BM=4, BN=8192> over f32 [8192, 8192] given as printed Tile IR:
+    routed once by sile_hip_tile_ir_route (to the row softmax kernel), then
+    each step is one synchronous sile_hip_tile_ir_launch, like the reference's
+    apply().  8 bytes of HBM traffic per element (read 4, write 4); two
+    input/output pairs (1 GiB) rotate so every call reads from HBM."""
+    from tests import tile_ir_text
+    rows = cols = 8192
+    bm = 4
+    text = tile_ir_text.softmax(bm, cols)
+    shapes, programs = [rows, cols, rows, cols], rows // bm
+    route = hip.tile_ir_route(text, shapes, programs)
+    if route.kind != hip.ROUTE_SOFTMAX_ROWS:
+        raise RuntimeError(f"softmax routed to {route.name}: {route.reason}")
+    log(f"[bench] {name}: generating inputs")
+    x = normal(3, (rows, cols), 2.0)
+    rotate = 2
+    xs = [hip.DeviceBuffer.from_array(x) for _ in range(rotate)]
+    ys = [hip.DeviceBuffer(rows * cols * 4) for _ in range(rotate)]
+    del x
+
+    def call(i):
+        hip.tile_ir_launch(route, [xs[i].ptr, ys[i].ptr], shapes, programs)
+
+    for i in range(warmup):
+        call(i % rotate)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        call(i % rotate)
+    dt = (time.perf_counter() - t0) / steps
+    nbytes = 8.0 * rows * cols
+    res = summarise(name, nbytes, 1e9, "GB/s", dt * 1e3 * steps, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    res["route"] = route.name
+    for buf in xs + ys:
+        buf.close()
+    return res
+
+
 def bench_copy_calibration(name, steps, warmup):
     """A plain device-to-device copy of COPY_BYTES (the HIP runtime's blit
     kernel behind sile_hip_memcpy_dtod).  Run under rocprofv3 --pmc it gives
@@ -351,7 +390,7 @@ def traffic_from_pmc(root):
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
-EXTRA = ["copy_calibration", "llir_vec_add"]
+EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192"]
 
 
 def main():
@@ -389,6 +428,8 @@ def main():
             results[name] = bench_copy_calibration(name, args.steps, args.warmup)
         elif name == "llir_vec_add":
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
+        elif name == "tile_ir_softmax_f32_8192":
+            results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
             results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,

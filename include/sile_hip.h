@@ -246,6 +246,55 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
                             int64_t head_dim, const void *q, const void *k, const void *v,
                             void *o, float scale, int causal, sile_hip_stream stream);
 
+/* ---- pattern router: Tile IR -> hand-written kernels ---------------------
+ * Generalises the reference's canonical-matmul detector
+ * (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:446-666) to
+ * the other tile patterns of the hot path.  The input is a kernel in the
+ * printed Tile IR form (format_tile_ir, crates/sile-tile-ir/src/print.rs:5-354)
+ * after or before the default Tile IR passes
+ * (crates/sile-tile-ir/src/passes/mod.rs:31-42), which
+ * crates/sile/src/compiler.rs compile_kernel_to_llvm_ir returns beside the
+ * LLIR.  A HipBackend calls the router first and lowers to LLIR
+ * (sile_hip_llir_compile) only on SILE_ROUTE_NONE. */
+typedef enum {
+  SILE_ROUTE_NONE = 0,          /* no hand-written kernel: use the LLIR code generation */
+  SILE_ROUTE_MATMUL = 1,        /* canonical matmul -> sile_hip_kernel_matmul (bit-identical) */
+  SILE_ROUTE_SOFTMAX_ROWS = 2,  /* softmax chain, one tile per row band -> sile_hip_softmax_rows */
+  SILE_ROUTE_SOFTMAX_TILES = 3, /* softmax chain, other tilings -> sile_hip_kernel_softmax */
+  SILE_ROUTE_REDUCE_ROWS = 4,   /* load + reduce(axis 1) + store -> sile_hip_reduce_rows */
+  SILE_ROUTE_ATOMIC_REDUCE = 5  /* load + sum + extract + atomic add -> sile_hip_kernel_parallel_reduce */
+} sile_route_kind;
+
+typedef struct {
+  int32_t kind;              /* sile_route_kind */
+  int32_t reduce_op;         /* SILE_ROUTE_REDUCE_ROWS: sile_reduce_op */
+  int32_t buffer[3];         /* kernel-parameter index of each operand: inputs, then output */
+  int32_t shape_offset[3];   /* offset of each operand's dims in `shapes` */
+  int32_t rank[3];           /* rank of each operand (0: unused) */
+  int32_t num_buffers;       /* buffer parameters of the kernel */
+  int64_t num_shapes;        /* shape values the route was made with */
+  int64_t operand_shapes[6]; /* the operands' dims the route was made for */
+  int64_t num_threadgroups;  /* the grid the route was made for */
+  int64_t tile_m, tile_n, tile_k; /* BM, BN, BK (TILE in tile_n for the atomic reduce) */
+  int64_t rows, cols;        /* extents handed to the row kernels */
+  char reason[512];          /* SILE_ROUTE_NONE: why each detector declined */
+} sile_hip_route;
+
+/* Parses `tile_ir_text` and picks the kernel for a launch of num_threadgroups
+ * programs over buffers of the given shapes (every buffer parameter's dims,
+ * concatenated in parameter order, as for sile_kernel_<name>).  A pattern is
+ * routed only where the kernel writes exactly the tiles that the CPU
+ * backend's wrapper writes (crates/sile-backend/src/cpu/codegen.rs:409-555).
+ * Malformed text -> SILE_ERR_COMPILE; a kernel without a route is SILE_OK
+ * with kind SILE_ROUTE_NONE.  Needs no GPU. */
+int sile_hip_tile_ir_route(const char *tile_ir_text, const int64_t *shapes, int64_t num_shapes,
+                           int64_t num_threadgroups, sile_hip_route *out);
+/* Runs a route on device buffers (kernel parameter order) with the shapes and
+ * grid it was made for.  Synchronous, like the sile_kernel_<name> launches. */
+int sile_hip_tile_ir_launch(const sile_hip_route *route, void *const *buffers,
+                            int64_t num_buffers, const int64_t *shapes, int64_t num_shapes,
+                            int64_t num_threadgroups, sile_hip_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

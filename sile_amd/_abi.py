@@ -63,6 +63,38 @@ class DeviceProps(ctypes.Structure):
     ]
 
 
+ROUTE_NONE, ROUTE_MATMUL, ROUTE_SOFTMAX_ROWS, ROUTE_SOFTMAX_TILES, ROUTE_REDUCE_ROWS, \
+    ROUTE_ATOMIC_REDUCE = range(6)
+ROUTE_NAMES = {ROUTE_NONE: "none", ROUTE_MATMUL: "matmul", ROUTE_SOFTMAX_ROWS: "softmax_rows",
+               ROUTE_SOFTMAX_TILES: "softmax_tiles", ROUTE_REDUCE_ROWS: "reduce_rows",
+               ROUTE_ATOMIC_REDUCE: "atomic_reduce"}
+
+
+class Route(ctypes.Structure):
+    """sile_hip_route: the kernel the Tile IR router picked for one launch."""
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("reduce_op", ctypes.c_int32),
+        ("buffer", ctypes.c_int32 * 3),
+        ("shape_offset", ctypes.c_int32 * 3),
+        ("rank", ctypes.c_int32 * 3),
+        ("num_buffers", ctypes.c_int32),
+        ("num_shapes", ctypes.c_int64),
+        ("operand_shapes", ctypes.c_int64 * 6),
+        ("num_threadgroups", ctypes.c_int64),
+        ("tile_m", ctypes.c_int64),
+        ("tile_n", ctypes.c_int64),
+        ("tile_k", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("reason", ctypes.c_char * 512),
+    ]
+
+    @property
+    def name(self) -> str:
+        return ROUTE_NAMES.get(self.kind, f"kind{self.kind}")
+
+
 # name -> argtypes (every function returns int status unless listed in _RESTYPE)
 SIGNATURES = {
     "sile_hip_init": [_I32],
@@ -102,6 +134,8 @@ SIGNATURES = {
     "sile_hip_softmax_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _I64, _P],
     "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
     "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
+    "sile_hip_tile_ir_route": [ctypes.c_char_p, _P, _I64, _I64, ctypes.POINTER(Route)],
+    "sile_hip_tile_ir_launch": [ctypes.POINTER(Route), _P, _I64, _P, _I64, _I64, _P],
 }
 _RESTYPE = {"sile_hip_last_error": ctypes.c_char_p, "sile_hip_version": ctypes.c_char_p,
             "sile_hip_llir_free_code": None}
@@ -335,6 +369,24 @@ class LlirKernel:
         if self.module.value and _lib is not None:
             call("sile_hip_module_unload", self.module)
             self.module = _P()
+
+
+# ---------------------------------------------------------------------------
+# Tile IR pattern router
+# ---------------------------------------------------------------------------
+
+def tile_ir_route(text: str, shapes, num_threadgroups: int) -> Route:
+    """The kernel the router picks for `text` launched with `num_threadgroups`
+    programs over buffers of `shapes` (no GPU needed)."""
+    r = Route()
+    call("sile_hip_tile_ir_route", text.encode(), _i64_array(shapes), len(shapes),
+         num_threadgroups, ctypes.byref(r))
+    return r
+
+
+def tile_ir_launch(route: Route, bufs, shapes, num_threadgroups: int, stream=None) -> None:
+    call("sile_hip_tile_ir_launch", ctypes.byref(route), _ptr_array(bufs), len(bufs),
+         _i64_array(shapes), len(shapes), num_threadgroups, _sh(stream))
 
 
 # ---------------------------------------------------------------------------

@@ -28,7 +28,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 KERNELS = ["dsl", "softmax", "gemm", "attention", "flash_attn"]
-HOST_SOURCES = ["runtime.cpp", "ops.cpp", "llir.cpp"]
+HOST_SOURCES = ["runtime.cpp", "ops.cpp", "llir.cpp", "tile_ir.cpp"]
 
 # Device code: gfx950 only; packed-fp32 instructions disabled (the compiler
 # would otherwise form v_pk_{add,mul,fma}_f32 from scalar float code).

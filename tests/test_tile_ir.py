@@ -1,0 +1,205 @@
+"""The Tile IR pattern router on the CPU (no GPU needed): the printed Tile IR
+fixtures, which kernel each DSL kernel routes to for given shapes and grids,
+the detector's rejections (the conditions of the reference's
+CanonicalMatmulPlan::detect, canonical_matmul.rs:446-666) and parse errors."""
+import os
+
+import pytest
+
+from sile_amd import _abi as hip
+from tests import tile_ir_text as T
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "tile_ir")
+
+
+def _route(text, shapes, grid):
+    return hip.tile_ir_route(text, shapes, grid)
+
+
+def test_fixtures_match_the_derivation():
+    from tests.golden.make_tile_ir_fixtures import FIXTURES
+    for name, text in FIXTURES.items():
+        with open(os.path.join(GOLDEN, name)) as f:
+            assert f.read() == text, name
+
+
+def test_vec_add_text_has_what_the_reference_print_test_asserts():
+    # crates/sile/tests/tile_ir_print.rs:77-89 (lowering only) and :166-168 (after the passes)
+    printed = T.vec_add(4, passes=False)
+    for s in ["module {", "entry @vec_add(", 'kind = "launch.index", dim = 0', "load_ptr_tko",
+              "addf", "store_ptr_tko", ", [%5, %3] {shape = [1, 4], stride_dim = 0}", "return",
+              "tile<1x4xf32>", "tile<ptr<f32>>"]:
+        assert s in printed, s
+    for s in ['kind = "sile.program_id"', "sile.get_tile_block_id_dim", "dim = 1"]:
+        assert s not in printed, s
+    fused = T.vec_add(2)
+    assert "map addf(load_ptr_tko(" in fused
+    for s in ["= addf ", "= load_ptr_tko %0", "= load_ptr_tko %1"]:
+        assert s not in fused, s
+
+
+def test_matmul_routes_to_the_exact_tile_kernel():
+    r = _route(T.matmul(32, 32, 32), [512, 512, 512, 512, 512, 512], 256)
+    assert r.kind == hip.ROUTE_MATMUL
+    assert (r.tile_m, r.tile_n, r.tile_k) == (32, 32, 32)
+    assert list(r.buffer) == [0, 1, 2] and list(r.shape_offset) == [0, 2, 4]
+    r = _route(T.matmul(2, 2, 2), [4, 4, 4, 4, 4, 4], 4)
+    assert r.kind == hip.ROUTE_MATMUL and (r.tile_m, r.tile_n, r.tile_k) == (2, 2, 2)
+
+
+@pytest.mark.parametrize("passes", [True, False])
+def test_softmax_routes(passes):
+    # one column tile per row band -> the row softmax over run * BM rows
+    r = _route(T.softmax(2, 8, passes), [4, 8, 4, 8], 2)
+    assert r.kind == hip.ROUTE_SOFTMAX_ROWS and (r.rows, r.cols) == (4, 8)
+    # fewer programs than tiles: only their rows
+    r = _route(T.softmax(2, 8, passes), [4, 8, 4, 8], 1)
+    assert r.kind == hip.ROUTE_SOFTMAX_ROWS and (r.rows, r.cols) == (2, 8)
+    # y wider than the tile but less than two tiles: still one column tile
+    r = _route(T.softmax(2, 8, passes), [4, 12, 4, 12], 2)
+    assert r.kind == hip.ROUTE_SOFTMAX_ROWS and (r.rows, r.cols) == (4, 8)
+    # two column tiles per row band -> the tile kernel
+    r = _route(T.softmax(2, 4, passes), [4, 8, 4, 8], 4)
+    assert r.kind == hip.ROUTE_SOFTMAX_TILES and (r.tile_m, r.tile_n) == (2, 4)
+    # x narrower than a tile row: the tile kernel (which rejects the shapes)
+    r = _route(T.softmax(2, 8, passes), [4, 6, 4, 8], 2)
+    assert r.kind == hip.ROUTE_SOFTMAX_TILES
+
+
+def test_row_reduce_routes():
+    r = _route(T.row_reduce(4, 64, "sum"), [16, 64, 16, 1], 4)
+    assert r.kind == hip.ROUTE_REDUCE_ROWS and r.reduce_op == hip.REDUCE_SUM
+    assert (r.rows, r.cols) == (16, 64)
+    r = _route(T.row_reduce(4, 64, "max", out_rank=1), [16, 100, 16], 3)
+    assert r.kind == hip.ROUTE_REDUCE_ROWS and r.reduce_op == hip.REDUCE_MAX
+    assert (r.rows, r.cols) == (12, 64)
+    r = _route(T.row_reduce(1, 64), [16, 64, 16, 1], 16)
+    assert r.kind == hip.ROUTE_REDUCE_ROWS and (r.rows, r.cols) == (16, 64)
+    # more than one output column: every column tile re-reduces the same x columns
+    r = _route(T.row_reduce(4, 64), [16, 64, 16, 2], 8)
+    assert r.kind == hip.ROUTE_NONE and b"more than one column" in r.reason
+    # rank-1 output: 16 programs of 4 rows would write past y[16]
+    r = _route(T.row_reduce(4, 64, "max", out_rank=1), [64, 64, 16], 16)
+    assert r.kind == hip.ROUTE_NONE and b"past" in r.reason
+    # x narrower than the tile
+    r = _route(T.row_reduce(4, 64), [16, 32, 16, 1], 4)
+    assert r.kind == hip.ROUTE_NONE
+
+
+def test_parallel_reduce_routes():
+    r = _route(T.parallel_reduce(1000), [100000, 1], 100)
+    assert r.kind == hip.ROUTE_ATOMIC_REDUCE and r.tile_n == 1000
+
+
+@pytest.mark.parametrize("passes", [True, False])
+def test_vec_add_has_no_route(passes):
+    r = _route(T.vec_add(4, passes), [8, 8, 8], 2)
+    assert r.kind == hip.ROUTE_NONE
+    why = r.reason.decode()
+    for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:"):
+        assert d in why
+    assert list(r.buffer) == [-1, -1, -1]
+
+
+MATMUL_MUTATIONS = {
+    # each breaks one condition of CanonicalMatmulPlan::detect
+    "acc seed 1.0": ("%5 = constant <f32: 0.0>", "%5 = constant <f32: 1.0>"),
+    "k seed 1": ("%8 = constant <i64: 0>", "%8 = constant <i64: 1>"),
+    "step 2": ("%20 = constant <i64: 1>", "%20 = constant <i64: 2>"),
+    "bound k <= n": ('cmpi "lt"', 'cmpi "le"'),
+    "bound multiply": ("divi %10, %11", "muli %10, %11"),
+    "shape dim 0": ("sile.shape_dim %9 {dim = 1}", "sile.shape_dim %9 {dim = 0}"),
+    "bk differs from mma k": ("%11 = constant <i64: 32>", "%11 = constant <i64: 16>"),
+    "a loaded from b": ("%16 = load_ptr_tko %0,", "%16 = load_ptr_tko %1,"),
+    "b walked by n, k": ("load_ptr_tko %1, [%14, %4]", "load_ptr_tko %1, [%4, %14]"),
+    "store at swapped launch": ("store_ptr_tko %2, %22, [%3, %4]", "store_ptr_tko %2, %22, [%4, %3]"),
+    "store of the seed": ("store_ptr_tko %2, %22,", "store_ptr_tko %2, %5,"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MATMUL_MUTATIONS))
+def test_matmul_detector_rejections(name):
+    old, new = MATMUL_MUTATIONS[name]
+    text = T.matmul(32, 32, 32)
+    assert old in text
+    r = _route(text.replace(old, new), [64, 64, 64, 64, 64, 64], 4)
+    assert r.kind == hip.ROUTE_NONE, name
+    assert b"matmul:" in r.reason
+
+
+def test_matmul_launch_dims_must_be_row_0_col_1():
+    # both tiles from launch indices, but rows from dim 1: the detector of the
+    # reference fires; the exact-order kernel decodes (0, 1), so no route
+    text = T.matmul(32, 32, 32).replace('"__launch_idx0", kind = "launch.index", dim = 0',
+                                        '"__launch_idx0", kind = "launch.index", dim = 2')
+    r = _route(text, [64, 64, 64, 64, 64, 64], 4)
+    assert r.kind == hip.ROUTE_NONE and b"not (0, 1)" in r.reason
+
+
+def test_softmax_detector_rejections():
+    base = T.softmax(2, 8)
+    for old, new in [("exp(subf(", "negf(subf("),
+                     ('combiner = "max"', 'combiner = "sum"'),
+                     ("map divf(%9,", "map mulf(%9,"),
+                     ("store_ptr_tko %1, %13, [%3, %4]", "store_ptr_tko %1, %13, [%4, %3]")]:
+        assert old in base
+        r = _route(base.replace(old, new), [4, 8, 4, 8], 2)
+        assert r.kind == hip.ROUTE_NONE, old
+
+
+def test_buffer_order_follows_the_parameters():
+    # the same softmax with y declared first: operands map to buffer 1 (x) and 0 (y)
+    text = T.softmax(2, 8)
+    text = text.replace('%0 {sym_name = "x", rank = 2} : tile<ptr<f32>>,\n'
+                        '    %1 {sym_name = "y", rank = 2} : tile<ptr<f32>>,',
+                        '%1 {sym_name = "y", rank = 2} : tile<ptr<f32>>,\n'
+                        '    %0 {sym_name = "x", rank = 2} : tile<ptr<f32>>,')
+    r = _route(text, [6, 8, 4, 8], 2)  # y [6, 8], x [4, 8]
+    assert r.kind == hip.ROUTE_SOFTMAX_ROWS
+    assert list(r.buffer)[:2] == [1, 0] and list(r.shape_offset)[:2] == [2, 0]
+    assert (r.rows, r.cols) == (4, 8)
+    # three programs would read rows 4 and 5 of x [4, 8]: not the row kernel's domain
+    assert _route(text, [6, 8, 4, 8], 3).kind == hip.ROUTE_SOFTMAX_TILES
+
+
+@pytest.mark.parametrize("text,why", [
+    ("", "incomplete"),
+    ("module {\n  entry @k(\n  ) {\n    ^bb0:  // entry\n      %1 = frob %0 : none\n"
+     "      return\n  }\n}\n", "unknown op"),
+    ("module {\n  entry @k(\n  ) {\n    ^bb0:  // entry\n      cf.br ^bb7\n  }\n}\n",
+     "unknown block"),
+    ("module {\n  entry @k(\n  ) {\n    ^bb0:\n      return\n  }\n}\n", "no entry"),
+    ("module {\n  entry @k(\n  ) {\n    ^bb0:  // entry\n      %1 = constant <i64: 0> : tile<i64>\n"
+     "  }\n}\n", "terminator"),
+])
+def test_malformed_text_is_a_compile_error(text, why):
+    with pytest.raises(hip.SileError) as e:
+        _route(text, [], 1)
+    assert e.value.kind == "Compile"
+    assert why in str(e.value)
+
+
+def test_shape_count_must_match_the_buffers():
+    with pytest.raises(hip.SileError) as e:
+        _route(T.matmul(2, 2, 2), [4, 4, 4, 4, 4], 4)
+    assert e.value.kind == "Shape"
+    with pytest.raises(hip.SileError) as e:
+        _route(T.matmul(2, 2, 2), [4, 4, 4, -4, 4, 4], 4)
+    assert e.value.kind == "Shape"
+
+
+def test_launch_of_no_route_is_unsupported():
+    r = _route(T.vec_add(4), [8, 8, 8], 2)
+    with pytest.raises(hip.SileError) as e:
+        hip.tile_ir_launch(r, [0, 0, 0], [8, 8, 8], 2)
+    assert e.value.kind == "UnsupportedBackend"
+
+
+def test_launch_rejects_other_shapes_or_grid():
+    r = _route(T.softmax(2, 8), [4, 8, 4, 8], 2)
+    with pytest.raises(hip.SileError) as e:
+        hip.tile_ir_launch(r, [0, 0], [8, 8, 8, 8], 2)
+    assert e.value.kind == "Shape"
+    with pytest.raises(hip.SileError) as e:
+        hip.tile_ir_launch(r, [0, 0], [4, 8, 4, 8], 1)
+    assert e.value.kind == "Shape"

@@ -1,0 +1,188 @@
+"""Printed Tile IR of the DSL kernels on the hot path, as the reference's
+HIR -> Tile IR lowering and its default Tile IR passes produce it.
+
+The reference is Rust and cannot run here, so each text is derived by hand:
+the lowering (crates/sile-tile-ir/src/lower.rs) gives every emitted op and
+every parameter it creates (`__launch_idx<d>`, `__shape_<buf>`) the next value
+id in emission order; the passes are canonicalize_shape, canonicalize_tile_ops,
+pointwise_fusion, tile_expr_cse and dce
+(crates/sile-tile-ir/src/passes/mod.rs:31-42); the printer is
+crates/sile-tile-ir/src/print.rs:5-354.  The vec_add text carries every
+substring that crates/sile/tests/tile_ir_print.rs asserts, which pins the
+numbering procedure on the one kernel the reference prints in its tests.
+`passes=False` gives the text before the passes.
+
+The kernels (DSL source as in crates/sile/examples/*.rs):
+  matmul<BM,BN,BK>      crates/sile/examples/matmul.rs:3-19
+  softmax<BM,BN>        crates/sile/examples/softmax.rs:3-16
+  parallel_reduce<TILE> crates/sile/examples/parallel_reduce.rs:3-9
+  vec_add<TILE>         crates/sile/examples/vec_add.rs:3-14
+  row_reduce<BM,BN>     not in the reference: `let pid = tile::id().0;
+                        let t = x.load_tile([BM, BN], [pid, 0]);
+                        y.store(sile::reduce_{sum,max}(t, 1));` with y
+                        `[BM, 1]` (rank 2) or `[BM]` (rank 1)
+"""
+
+
+def _param_buf(v, name, rank):
+    return f'%{v} {{sym_name = "{name}", rank = {rank}}} : tile<ptr<f32>>'
+
+
+def _param_launch(v, dim):
+    return f'%{v} {{sym_name = "__launch_idx{dim}", kind = "launch.index", dim = {dim}}} : tile<i64>'
+
+
+def _param_shape(v, src, name, rank):
+    return (f'%{v} {{sym_name = "__shape_{name}", kind = "shape.desc", source = %{src}}} : '
+            f'shape_desc<{rank}>')
+
+
+def _tile(r, c):
+    return f"tile<{r}x{c}xf32>"
+
+
+def _module(name, params, blocks):
+    """blocks: [(header, [lines...])]; the first block is the entry."""
+    out = ["module {", f"  entry @{name}("]
+    for i, p in enumerate(params):
+        out.append(f"    {p}{',' if i + 1 < len(params) else ''}")
+    out.append("  ) {")
+    for i, (header, lines) in enumerate(blocks):
+        out.append(f"    {header}:{'  // entry' if i == 0 else ''}")
+        out.extend(f"      {ln}" for ln in lines)
+    out += ["  }", "}"]
+    return "\n".join(out) + "\n"
+
+
+def _fmt_float(x):
+    # print.rs:348-354: integral values print with one decimal
+    return f"{x:.1f}" if float(x).is_integer() else repr(float(x))
+
+
+def matmul(bm, bn, bk, splat=0.0):
+    """Canonical matmul: entry -> header(k, acc) -> body -> exit with one store."""
+    params = [_param_buf(0, "a", 2), _param_buf(1, "b", 2), _param_buf(2, "c", 2),
+              _param_launch(3, 0), _param_launch(4, 1),
+              _param_shape(9, 0, "a", 2), _param_shape(17, 1, "b", 2), _param_shape(23, 2, "c", 2)]
+    acc = _tile(bm, bn)
+    blocks = [
+        ("^bb0", [f"%5 = constant <f32: {_fmt_float(splat)}> : {acc}",
+                  "%8 = constant <i64: 0> : tile<i64>",
+                  "cf.br ^bb1(%8, %5)"]),
+        (f"^bb1(%6: tile<i64>, %7: {acc})",
+         ["%10 = sile.shape_dim %9 {dim = 1} : tile<i64>",
+          f"%11 = constant <i64: {bk}> : tile<i64>",
+          "%12 = divi %10, %11 : tile<i64>",
+          '%13 = cmpi "lt" %6, %12 : tile<i64>',
+          "cf.cond_br %13, ^bb2(%6, %7), ^bb3(%7)"]),
+        (f"^bb2(%14: tile<i64>, %15: {acc})",
+         [f"%16 = load_ptr_tko %0, [%3, %14] {{shape = [{bm}, {bk}], stride_dim = 1}} : "
+          f"{_tile(bm, bk)}",
+          f"%18 = load_ptr_tko %1, [%14, %4] {{shape = [{bk}, {bn}], stride_dim = 1}} : "
+          f"{_tile(bk, bn)}",
+          f"%19 = mmaf %16, %18, %15 {{m = {bm}, n = {bn}, k = {bk}}} : {acc}",
+          "%20 = constant <i64: 1> : tile<i64>",
+          "%21 = addi %14, %20 : tile<i64>",
+          "cf.br ^bb1(%21, %19)"]),
+        (f"^bb3(%22: {acc})",
+         [f"%24 = store_ptr_tko %2, %22, [%3, %4] {{shape = [{bm}, {bn}], stride_dim = 1}} : none",
+          "return"]),
+    ]
+    return _module("matmul", params, blocks)
+
+
+def softmax(bm, bn, passes=True):
+    params = [_param_buf(0, "x", 2), _param_buf(1, "y", 2), _param_shape(2, 0, "x", 2),
+              _param_launch(3, 0), _param_launch(4, 1), _param_shape(12, 1, "y", 2)]
+    t, col = _tile(bm, bn), _tile(bm, 1)
+    load = f"%5 = load_ptr_tko %0, [%3, %4] {{shape = [{bm}, {bn}], stride_dim = 1}} : {t}"
+    rmax = f'%6 = reduce %5 {{axis = 1, combiner = "max", input_shape = [{bm}, {bn}]}} : {col}'
+    rsum = f'%10 = reduce %9 {{axis = 1, combiner = "sum", input_shape = [{bm}, {bn}]}} : {col}'
+    store = f"%14 = store_ptr_tko %1, %13, [%3, %4] {{shape = [{bm}, {bn}], stride_dim = 1}} : none"
+    if passes:
+        lines = [load, rmax,
+                 f"%9 = map exp(subf(%5, broadcast(%6, src_shape=[{bm}, 1]))) "
+                 f"{{shape = [{bm}, {bn}]}} : {t}",
+                 rsum,
+                 f"%13 = map divf(%9, broadcast(%10, src_shape=[{bm}, 1])) "
+                 f"{{shape = [{bm}, {bn}]}} : {t}",
+                 store, "return"]
+    else:
+        lines = [load, rmax,
+                 f"%7 = broadcast %6 {{shape = [{bm}, {bn}]}} : {t}",
+                 f"%8 = subf %5, %7 : {t}",
+                 f"%9 = exp %8 : {t}",
+                 rsum,
+                 f"%11 = broadcast %10 {{shape = [{bm}, {bn}]}} : {t}",
+                 f"%13 = divf %9, %11 : {t}",
+                 store, "return"]
+    return _module("softmax", params, [("^bb0", lines)])
+
+
+def row_reduce(bm, bn, op="sum", out_rank=2):
+    """row_reduce<BM,BN> (see the module docstring); op 'sum' or 'max'."""
+    params = [_param_buf(0, "x", 2), _param_buf(1, "y", out_rank), _param_launch(2, 0),
+              _param_shape(3, 0, "x", 2), _param_shape(6, 1, "y", out_rank)]
+    lines = ["%4 = constant <i64: 0> : tile<i64>",
+             f"%5 = load_ptr_tko %0, [%2, %4] {{shape = [{bm}, {bn}], stride_dim = 1}} : "
+             f"{_tile(bm, bn)}",
+             f'%7 = reduce %5 {{axis = 1, combiner = "{op}", input_shape = [{bm}, {bn}]}} : '
+             f"{_tile(bm, 1)}"]
+    if out_rank == 2:
+        # the store's column is launch index 1 for a tile larger than 1x1
+        # (lower.rs:790-800), a constant 0 otherwise
+        if bm > 1:
+            params.append(_param_launch(8, 1))
+        else:
+            lines.append("%8 = constant <i64: 0> : tile<i64>")
+        lines.append(f"%9 = store_ptr_tko %1, %7, [%2, %8] {{shape = [{bm}, 1], stride_dim = 1}} "
+                     ": none")
+        if bm == 1:
+            # CSE folds the second constant 0 into %4
+            lines.pop(-2)
+            lines[-1] = lines[-1].replace("[%2, %8]", "[%2, %4]")
+    else:
+        lines.append(f"%9 = store_ptr_tko %1, %7, [%4, %2] {{shape = [{bm}, 1], stride_dim = 0}} "
+                     ": none")
+    lines.append("return")
+    return _module(f"row_{op}", params, [("^bb0", lines)])
+
+
+def parallel_reduce(tile):
+    params = [_param_buf(0, "a", 1), _param_buf(1, "out", 1), _param_launch(2, 0),
+              _param_shape(3, 0, "a", 1), _param_shape(7, 1, "out", 1)]
+    lines = ["%4 = constant <i64: 0> : tile<i64>",
+             f"%5 = load_ptr_tko %0, [%4, %2] {{shape = [1, {tile}], stride_dim = 0}} : "
+             f"{_tile(1, tile)}",
+             f'%6 = reduce %5 {{axis = 1, combiner = "sum", input_shape = [1, {tile}]}} : '
+             f"{_tile(1, 1)}",
+             "%10 = extract %6[%4, %4] : tile<f32>",
+             "%13 = sile.atomic_add %1, %10, [%4, %4] {stride_dim = 0} : none",
+             "return"]
+    return _module("parallel_reduce", params, [("^bb0", lines)])
+
+
+def vec_add(tile, passes=True):
+    params = [_param_buf(0, "a", 1), _param_buf(1, "b", 1), _param_buf(2, "c", 1),
+              _param_launch(3, 0), _param_shape(4, 0, "a", 1), _param_shape(7, 1, "b", 1),
+              _param_shape(10, 2, "c", 1)]
+    t = _tile(1, tile)
+    if passes:
+        lines = ["%5 = constant <i64: 0> : tile<i64>",
+                 f"%11 = map addf(load_ptr_tko(%0, [%5, %3], shape=[1, {tile}], stride_dim=0), "
+                 f"load_ptr_tko(%1, [%5, %3], shape=[1, {tile}], stride_dim=0)) "
+                 f"{{shape = [1, {tile}]}} : {t}",
+                 f"%13 = store_ptr_tko %2, %11, [%5, %3] {{shape = [1, {tile}], stride_dim = 0}} "
+                 ": none",
+                 "return"]
+    else:
+        lines = ["%5 = constant <i64: 0> : tile<i64>",
+                 f"%6 = load_ptr_tko %0, [%5, %3] {{shape = [1, {tile}], stride_dim = 0}} : {t}",
+                 "%8 = constant <i64: 0> : tile<i64>",
+                 f"%9 = load_ptr_tko %1, [%8, %3] {{shape = [1, {tile}], stride_dim = 0}} : {t}",
+                 f"%11 = addf %6, %9 : {t}",
+                 "%12 = constant <i64: 0> : tile<i64>",
+                 f"%13 = store_ptr_tko %2, %11, [%12, %3] {{shape = [1, {tile}], stride_dim = 0}} "
+                 ": none",
+                 "return"]
+    return _module("vec_add", params, [("^bb0", lines)])
