@@ -81,6 +81,7 @@ struct AttnArgs {
   float scale_log2;     // softmax scale * log2(e)
   int32_t causal;
   int32_t xcd_map;      // 1: head-per-XCD launch order (bh % 8 == 0)
+  int32_t pair;         // 1: causal query blocks in balanced pairs (v2 kernels)
 };
 
 template <bool kBF16, int kQT, int kNK>
@@ -385,309 +386,322 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
 
-  int bh, qb;
+  // Work unit u of a head: query block u, or with a.pair (causal) the pair of
+  // query blocks (q_blocks - 1 - u, u), whose key ranges add up to the same
+  // length for every u, so all workgroups carry equal work.  Causal blocks
+  // run largest first.
+  const int units = a.pair ? (a.q_blocks + 1) / 2 : a.q_blocks;
+  int bh, u;
   const int bid = blockIdx.x;
   if (a.xcd_map) {
     const int xcd = bid & 7, idx = bid >> 3;
-    bh = ((idx / a.q_blocks) << 3) + xcd;
-    qb = idx % a.q_blocks;
+    bh = ((idx / units) << 3) + xcd;
+    u = idx % units;
   } else {
     bh = bid % a.bh;
-    qb = bid / a.bh;
+    u = bid / a.bh;
   }
-  if (a.causal) qb = a.q_blocks - 1 - qb;
+  const int qb_first = a.causal ? a.q_blocks - 1 - u : u;
+  const int qb_second = a.pair ? u : qb_first;
   const int64_t S = a.seq;
   const int64_t head_off = (int64_t)bh * S * kD;
-  const int q0 = qb * kBQ;
-  const int wq0 = q0 + wave * kQT * 32;
 
-  // ---- Q^T fragments (B operand of S^T = K . Q^T) ----
-  u32x4 qf[kQT][8];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    const uint16_t* qrow = Q + head_off + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
-  }
+  for (int pass = 0; pass < (qb_second == qb_first ? 1 : 2); ++pass) {
+    const int qb = pass ? qb_second : qb_first;
+    // the previous block's last reads of both LDS stages are done before the
+    // prologue below refills them
+    if (pass) __syncthreads();
+    const int q0 = qb * kBQ;
+    const int wq0 = q0 + wave * kQT * 32;
 
-  // ---- LDS-DMA addressing: wave w's instruction i fills rows 4 (w + kW i) + (lane >> 4) ----
-  // (the swizzles depend on row & 15 and row & 3, the same for every i)
-  const int dma_row = 4 * wave + (lane >> 4), dma_pos = lane & 15;
-  const int k_voff = dma_row * kRowB + ((dma_pos ^ (dma_row & 15)) << 4);
-  const int v_voff = dma_row * kRowB + ((dma_pos ^ (4 * (dma_row & 3))) << 4);
-  const int kv_bytes = (int)(S * kRowB);
-  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(K + head_off), (short)0, kv_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(V + head_off), (short)0, kv_bytes, 0x00020000);
-  auto dma_k = [&](int blk, int stage) {
-    uint8_t* base = smem + stage * kStageB + wave * 1024;
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
-                                               k_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
-  };
-  auto dma_v = [&](int blk, int stage) {
-    uint8_t* base = smem + stage * kStageB + kTileB + wave * 1024;
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
-                                               v_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
-  };
-
-  // ---- fragment reads ----
-  // K fragment of S tile st, d-step kk: row 32 st + l32 (row & 15 == l32 & 15)
-  const int kf_off = l32 * kRowB;
-  const int kf_swz = l32 & 15;
-  auto k_frag = [&](const uint8_t* ks, int st, int kk) {
-    return *reinterpret_cast<const u32x4*>(ks + 32 * st * kRowB + (((2 * kk + g) ^ kf_swz) << 4));
-  };
-  auto s_block = [&](int stage, f32x16 (&sacc)[kQT][kST]) {
-    const uint8_t* ks = smem + stage * kStageB + kf_off;
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt)
-#pragma unroll
-      for (int st = 0; st < kST; ++st)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < kST; ++st)
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const u32x4 kf = k_frag(ks, st, kk);
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
-      }
-  };
-  // V^T fragment for d-tile dt, 16-key chunk cc: two transposing reads
-  const int tr_i = lane & 15, tr_s = (lane >> 4) & 1;
-  auto v_frag = [&](const uint8_t* vs, int dt, int cc) {
-    u32x4 out;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int key = 16 * cc + 8 * hh + 4 * g + (tr_i >> 2);
-      const int d = 32 * dt + 16 * tr_s + 4 * (tr_i & 3);
-      const int chunk = d >> 3;
-      const int off = key * kRowB + ((chunk ^ (4 * (key & 3))) << 4) + 8 * (tr_i & 1);
-      const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(vs + off));
-      const u32x2 w = __builtin_bit_cast(u32x2, v);
-      out[2 * hh] = w[0];
-      out[2 * hh + 1] = w[1];
-    }
-    return out;
-  };
-  auto pv_block = [&](int stage, const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oacc)[kQT][4]) {
-    const uint8_t* vs = smem + stage * kStageB + kTileB;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int cc = 0; cc < 2 * kST; ++cc) {
-        const u32x4 vf = v_frag(vs, dt, cc);
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oacc[qt][dt]);
-      }
-  };
-
-  // S_{j+1} over (S tile, d-step) and PV_{j-1} over (d-tile, key chunk), one
-  // step of each at a time: S step (st, kk) runs at step 8 st + kk, PV
-  // (dt, cc) at step dt + 4 cc
-  auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT][kST],
-                       const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oa)[kQT][4]) {
-    const uint8_t* ks = smem + kstage * kStageB + kf_off;
-    const uint8_t* vs = smem + vstage * kStageB + kTileB;
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt)
-#pragma unroll
-      for (int st = 0; st < kST; ++st)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
-#pragma unroll
-    for (int step = 0; step < 8 * kST; ++step) {
-      const int st = step >> 3, kk = step & 7;
-      const u32x4 kf = k_frag(ks, st, kk);
-      const int dt = step & 3, cc = step >> 2;
-      const u32x4 vf = v_frag(vs, dt, cc);
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
-    }
-  };
-
-  f32x16 oacc[kQT][4];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt)
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
-  float m_run[kQT], l_run[kQT], alpha[kQT];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    m_run[qt] = -__builtin_inff();
-    l_run[qt] = 0.0f;
-    alpha[qt] = 1.0f;
-  }
-  u32x4 pprev[kQT][2 * kST];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt)
-#pragma unroll
-    for (int cc = 0; cc < 2 * kST; ++cc) pprev[qt][cc] = u32x4{0u, 0u, 0u, 0u};
-
-  const int nb = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
-  const int last = nb - 1;
-  const float c = a.scale_log2;
-
-  // Stages: iteration j reads K_{j+1} and V_{j-1} (stage (j + 1) & 1) and loads
-  // K_{j+2} and V_j into stage j & 1, whose previous contents were read in
-  // iteration j - 1; the barrier closing iteration j waits for those loads.
-  // The key loop is unrolled by two so that stage indices and the roles of
-  // the two S and P register sets are compile-time constants (nb is even:
-  // S is a multiple of 256 and blocks hold at most 64 keys).
-  // Prologue: K_0, K_1 and a finite V tile in stage 1 for the empty PV_{-1}
-  // (its P is zero).
-  dma_k(0, 0);
-  dma_k(min(1, last), 1);
-  dma_v(0, 1);
-  __syncthreads();
-  f32x16 sa[kQT][kST], sb[kQT][kST];
-  u32x4 pb[kQT][2 * kST];
-  s_block(0, sa);
-  __syncthreads();
-
-  // One iteration: everything up to the optional O rescale is one basic block,
-  // so the scheduler interleaves the softmax VALU work of block j with the
-  // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
-  // code, needed only on the workgroup's diagonal.
-  auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT][kST],
-                       f32x16 (&snext)[kQT][kST], const u32x4 (&pprev)[kQT][2 * kST],
-                       u32x4 (&pnew)[kQT][2 * kST]) {
-    constexpr int kS = decltype(stage_c)::value;
-    constexpr bool kMasked = decltype(masked)::value;
-    dma_k(min(j + 2, last), kS);
-    dma_v(j, kS);
-    // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
-    // consecutive MFMAs never accumulate into the same registers
-    mma_block(kS ^ 1, kS ^ 1, snext, pprev, oacc);
-    // VALU: online softmax of S_j -> P_j
-    if constexpr (kMasked) {
-      const int kb = j * kNK;
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        const int q = wq0 + 32 * qt + l32 - kb - 4 * g;  // key offset limit for this lane
-#pragma unroll
-        for (int st = 0; st < kST; ++st)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            scur[qt][st][i] =
-                (32 * st + 8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][st][i];
-      }
-    }
-    bool grow_any = false;
-    float mx[kQT];
-#pragma unroll
+    // ---- Q^T fragments (B operand of S^T = K . Q^T) ----
+    u32x4 qf[kQT][8];
+  #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      float m = scur[qt][0][0];
-#pragma unroll
-      for (int st = 0; st < kST; ++st)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][st][i]);
-      mx[qt] = pair32_max(m);
-      grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
+      const uint16_t* qrow = Q + head_off + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
+  #pragma unroll
+      for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
     }
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-      const float m_new = grow_any ? __builtin_fmaxf(m_run[qt], mx[qt]) : m_run[qt];
-      alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
-      m_run[qt] = m_new;
-      const float mc = m_new * c;
-      float rs = l_run[qt] * alpha[qt];
-#pragma unroll
-      for (int st = 0; st < kST; ++st)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          u32x4 w;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const float p0 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj], c, -mc));
-            const float p1 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj + 1], c, -mc));
-            const uint32_t pk = pack2<kBF16>(p0, p1);
-            w[jj] = pk;
-            rs = pair_sum<kBF16>(pk, rs);
-          }
-          pnew[qt][2 * st + h] = w;
-        }
-      l_run[qt] = rs;
-    }
-    // keep the softmax in this region, beside the MFMAs (the compiler would
-    // otherwise sink it below the rescale branch)
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-#pragma unroll
-      for (int cc = 0; cc < 2 * kST; ++cc) asm volatile("" : "+v"(pnew[qt][cc]));
-      asm volatile("" : "+v"(l_run[qt]));
-    }
-    if constexpr (kSched > 0) {
-      // issue order: the DMA, the first fragments, then per MFMA step the
-      // fragments kSched steps ahead between the two MFMAs and a share of the
-      // softmax VALU after each
-      constexpr int kSteps = 8 * kST;
-      __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 2 * kDmaPerWave, 0);
-      __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3 * kSched, 0);
-#pragma unroll
-      for (int step = 0; step < kSteps; ++step) {
-        __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
-        if (step + kSched < kSteps) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3, 0);
-        __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
-      }
-    }
-    // lazy rescale of O (after PV_{j-1}, before PV_j); the empty asm keeps the
-    // compiler from turning the branch into an unconditional multiply
-    if (grow_any) {
-      asm volatile("");
-#pragma unroll
+
+    // ---- LDS-DMA addressing: wave w's instruction i fills rows 4 (w + kW i) + (lane >> 4) ----
+    // (the swizzles depend on row & 15 and row & 3, the same for every i)
+    const int dma_row = 4 * wave + (lane >> 4), dma_pos = lane & 15;
+    const int k_voff = dma_row * kRowB + ((dma_pos ^ (dma_row & 15)) << 4);
+    const int v_voff = dma_row * kRowB + ((dma_pos ^ (4 * (dma_row & 3))) << 4);
+    const int kv_bytes = (int)(S * kRowB);
+    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(K + head_off), (short)0, kv_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(V + head_off), (short)0, kv_bytes, 0x00020000);
+    auto dma_k = [&](int blk, int stage) {
+      uint8_t* base = smem + stage * kStageB + wave * 1024;
+  #pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
+                                                 k_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
+    };
+    auto dma_v = [&](int blk, int stage) {
+      uint8_t* base = smem + stage * kStageB + kTileB + wave * 1024;
+  #pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
+                                                 v_voff, (blk * kNK + 4 * kW * i) * kRowB, 0, 0);
+    };
+
+    // ---- fragment reads ----
+    // K fragment of S tile st, d-step kk: row 32 st + l32 (row & 15 == l32 & 15)
+    const int kf_off = l32 * kRowB;
+    const int kf_swz = l32 & 15;
+    auto k_frag = [&](const uint8_t* ks, int st, int kk) {
+      return *reinterpret_cast<const u32x4*>(ks + 32 * st * kRowB + (((2 * kk + g) ^ kf_swz) << 4));
+    };
+    auto s_block = [&](int stage, f32x16 (&sacc)[kQT][kST]) {
+      const uint8_t* ks = smem + stage * kStageB + kf_off;
+  #pragma unroll
       for (int qt = 0; qt < kQT; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha[qt];
-    }
-    __syncthreads();
-  };
-  // blocks left of the workgroup's diagonal need no mask
-  const int j_diag = a.causal ? q0 / kNK : nb;
-  using Z = std::integral_constant<int, 0>;
-  using One = std::integral_constant<int, 1>;
-  int j = 0;
-  for (; j < j_diag; j += 2) {
-    iteration(j, Z{}, std::false_type{}, sa, sb, pprev, pb);
-    iteration(j + 1, One{}, std::false_type{}, sb, sa, pb, pprev);
-  }
-  for (; j < nb; j += 2) {
-    iteration(j, Z{}, std::true_type{}, sa, sb, pprev, pb);
-    iteration(j + 1, One{}, std::true_type{}, sb, sa, pb, pprev);
-  }
-  // PV of the last block (nb is even: P_{nb-1} is in pprev, V_{nb-1} in stage 1)
-  pv_block(1, pprev, oacc);
-
-  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    const float l = pair32_sum(l_run[qt]);
-    const float inv = 1.0f / l;
-    const int q = wq0 + 32 * qt + l32;
-    uint16_t* orow = O + head_off + (int64_t)q * kD;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 32 * dt + 8 * r + 4 * g;
-        const f32x16& acc = oacc[qt][dt];
-        const u32x2 w = {pack2<kBF16>(acc[4 * r] * inv, acc[4 * r + 1] * inv),
-                         pack2<kBF16>(acc[4 * r + 2] * inv, acc[4 * r + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d) = w;
+  #pragma unroll
+        for (int st = 0; st < kST; ++st)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
+  #pragma unroll
+      for (int st = 0; st < kST; ++st)
+  #pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const u32x4 kf = k_frag(ks, st, kk);
+  #pragma unroll
+          for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
+        }
+    };
+    // V^T fragment for d-tile dt, 16-key chunk cc: two transposing reads
+    const int tr_i = lane & 15, tr_s = (lane >> 4) & 1;
+    auto v_frag = [&](const uint8_t* vs, int dt, int cc) {
+      u32x4 out;
+  #pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int key = 16 * cc + 8 * hh + 4 * g + (tr_i >> 2);
+        const int d = 32 * dt + 16 * tr_s + 4 * (tr_i & 3);
+        const int chunk = d >> 3;
+        const int off = key * kRowB + ((chunk ^ (4 * (key & 3))) << 4) + 8 * (tr_i & 1);
+        const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(vs + off));
+        const u32x2 w = __builtin_bit_cast(u32x2, v);
+        out[2 * hh] = w[0];
+        out[2 * hh + 1] = w[1];
       }
-  }
+      return out;
+    };
+    auto pv_block = [&](int stage, const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oacc)[kQT][4]) {
+      const uint8_t* vs = smem + stage * kStageB + kTileB;
+  #pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+  #pragma unroll
+        for (int cc = 0; cc < 2 * kST; ++cc) {
+          const u32x4 vf = v_frag(vs, dt, cc);
+  #pragma unroll
+          for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oacc[qt][dt]);
+        }
+    };
+
+    // S_{j+1} over (S tile, d-step) and PV_{j-1} over (d-tile, key chunk), one
+    // step of each at a time: S step (st, kk) runs at step 8 st + kk, PV
+    // (dt, cc) at step dt + 4 cc
+    auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT][kST],
+                         const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oa)[kQT][4]) {
+      const uint8_t* ks = smem + kstage * kStageB + kf_off;
+      const uint8_t* vs = smem + vstage * kStageB + kTileB;
+  #pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+        for (int st = 0; st < kST; ++st)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
+  #pragma unroll
+      for (int step = 0; step < 8 * kST; ++step) {
+        const int st = step >> 3, kk = step & 7;
+        const u32x4 kf = k_frag(ks, st, kk);
+        const int dt = step & 3, cc = step >> 2;
+        const u32x4 vf = v_frag(vs, dt, cc);
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
+      }
+    };
+
+    f32x16 oacc[kQT][4];
+  #pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
+    float m_run[kQT], l_run[kQT], alpha[kQT];
+  #pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      m_run[qt] = -__builtin_inff();
+      l_run[qt] = 0.0f;
+      alpha[qt] = 1.0f;
+    }
+    u32x4 pprev[kQT][2 * kST];
+  #pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+      for (int cc = 0; cc < 2 * kST; ++cc) pprev[qt][cc] = u32x4{0u, 0u, 0u, 0u};
+
+    const int nb = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
+    const int last = nb - 1;
+    const float c = a.scale_log2;
+
+    // Stages: iteration j reads K_{j+1} and V_{j-1} (stage (j + 1) & 1) and loads
+    // K_{j+2} and V_j into stage j & 1, whose previous contents were read in
+    // iteration j - 1; the barrier closing iteration j waits for those loads.
+    // The key loop is unrolled by two so that stage indices and the roles of
+    // the two S and P register sets are compile-time constants (nb is even:
+    // S is a multiple of 256 and blocks hold at most 64 keys).
+    // Prologue: K_0, K_1 and a finite V tile in stage 1 for the empty PV_{-1}
+    // (its P is zero).
+    dma_k(0, 0);
+    dma_k(min(1, last), 1);
+    dma_v(0, 1);
+    __syncthreads();
+    f32x16 sa[kQT][kST], sb[kQT][kST];
+    u32x4 pb[kQT][2 * kST];
+    s_block(0, sa);
+    __syncthreads();
+
+    // One iteration: everything up to the optional O rescale is one basic block,
+    // so the scheduler interleaves the softmax VALU work of block j with the
+    // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
+    // code, needed only on the workgroup's diagonal.
+    auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT][kST],
+                         f32x16 (&snext)[kQT][kST], const u32x4 (&pprev)[kQT][2 * kST],
+                         u32x4 (&pnew)[kQT][2 * kST]) {
+      constexpr int kS = decltype(stage_c)::value;
+      constexpr bool kMasked = decltype(masked)::value;
+      dma_k(min(j + 2, last), kS);
+      dma_v(j, kS);
+      // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
+      // consecutive MFMAs never accumulate into the same registers
+      mma_block(kS ^ 1, kS ^ 1, snext, pprev, oacc);
+      // VALU: online softmax of S_j -> P_j
+      if constexpr (kMasked) {
+        const int kb = j * kNK;
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          const int q = wq0 + 32 * qt + l32 - kb - 4 * g;  // key offset limit for this lane
+  #pragma unroll
+          for (int st = 0; st < kST; ++st)
+  #pragma unroll
+            for (int i = 0; i < 16; ++i)
+              scur[qt][st][i] =
+                  (32 * st + 8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][st][i];
+        }
+      }
+      bool grow_any = false;
+      float mx[kQT];
+  #pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        float m = scur[qt][0][0];
+  #pragma unroll
+        for (int st = 0; st < kST; ++st)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][st][i]);
+        mx[qt] = pair32_max(m);
+        grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
+      }
+  #pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        const float m_new = grow_any ? __builtin_fmaxf(m_run[qt], mx[qt]) : m_run[qt];
+        alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
+        m_run[qt] = m_new;
+        const float mc = m_new * c;
+        float rs = l_run[qt] * alpha[qt];
+  #pragma unroll
+        for (int st = 0; st < kST; ++st)
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            u32x4 w;
+  #pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              const float p0 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj], c, -mc));
+              const float p1 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj + 1], c, -mc));
+              const uint32_t pk = pack2<kBF16>(p0, p1);
+              w[jj] = pk;
+              rs = pair_sum<kBF16>(pk, rs);
+            }
+            pnew[qt][2 * st + h] = w;
+          }
+        l_run[qt] = rs;
+      }
+      // keep the softmax in this region, beside the MFMAs (the compiler would
+      // otherwise sink it below the rescale branch)
+  #pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+  #pragma unroll
+        for (int cc = 0; cc < 2 * kST; ++cc) asm volatile("" : "+v"(pnew[qt][cc]));
+        asm volatile("" : "+v"(l_run[qt]));
+      }
+      if constexpr (kSched > 0) {
+        // issue order: the DMA, the first fragments, then per MFMA step the
+        // fragments kSched steps ahead between the two MFMAs and a share of the
+        // softmax VALU after each
+        constexpr int kSteps = 8 * kST;
+        __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 2 * kDmaPerWave, 0);
+        __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3 * kSched, 0);
+  #pragma unroll
+        for (int step = 0; step < kSteps; ++step) {
+          __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
+          if (step + kSched < kSteps) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
+        }
+      }
+      // lazy rescale of O (after PV_{j-1}, before PV_j); the empty asm keeps the
+      // compiler from turning the branch into an unconditional multiply
+      if (grow_any) {
+        asm volatile("");
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+          for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha[qt];
+      }
+      __syncthreads();
+    };
+    // blocks left of the workgroup's diagonal need no mask
+    const int j_diag = a.causal ? q0 / kNK : nb;
+    using Z = std::integral_constant<int, 0>;
+    using One = std::integral_constant<int, 1>;
+    int j = 0;
+    for (; j < j_diag; j += 2) {
+      iteration(j, Z{}, std::false_type{}, sa, sb, pprev, pb);
+      iteration(j + 1, One{}, std::false_type{}, sb, sa, pb, pprev);
+    }
+    for (; j < nb; j += 2) {
+      iteration(j, Z{}, std::true_type{}, sa, sb, pprev, pb);
+      iteration(j + 1, One{}, std::true_type{}, sb, sa, pb, pprev);
+    }
+    // PV of the last block (nb is even: P_{nb-1} is in pprev, V_{nb-1} in stage 1)
+    pv_block(1, pprev, oacc);
+
+    // ---- epilogue: O[q][d] = O^T[d][q] / l ----
+  #pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      const float l = pair32_sum(l_run[qt]);
+      const float inv = 1.0f / l;
+      const int q = wq0 + 32 * qt + l32;
+      uint16_t* orow = O + head_off + (int64_t)q * kD;
+  #pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 32 * dt + 8 * r + 4 * g;
+          const f32x16& acc = oacc[qt][dt];
+          const u32x2 w = {pack2<kBF16>(acc[4 * r] * inv, acc[4 * r + 1] * inv),
+                           pack2<kBF16>(acc[4 * r + 2] * inv, acc[4 * r + 3] * inv)};
+          *reinterpret_cast<u32x2*>(orow + d) = w;
+        }
+    }
+  }  // pass
 }
 
 }  // namespace v2

@@ -363,14 +363,19 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     if (!pipelined && variant != "q1" && variant != "q2") variant = "v2w8";
     if (seq_len % 256 != 0 || (variant == "q2" && dtype != SILE_F16)) variant = "q1";
     const int64_t bq = variant == "q1" ? 128 : 256;
+    // causal pipelined kernels take query blocks in balanced pairs
+    // (SILE_HIP_FA_PAIR=0: one block per workgroup)
+    const char* pair_env = getenv("SILE_HIP_FA_PAIR");
+    const bool pair = causal && pipelined && !(pair_env && pair_env[0] == '0');
     struct {
       int64_t seq;
       int32_t bh, q_blocks;
       float scale_log2;
-      int32_t causal, xcd_map;
+      int32_t causal, xcd_map, pair;
     } fa{seq_len, (int32_t)bh, (int32_t)(seq_len / bq), scale * 1.4426950408889634f,
-         causal ? 1 : 0, (bh % 8 == 0) ? 1 : 0};
-    const int64_t blocks = bh * (seq_len / bq);
+         causal ? 1 : 0, (bh % 8 == 0) ? 1 : 0, pair ? 1 : 0};
+    const int64_t units = pair ? (seq_len / bq + 1) / 2 : seq_len / bq;
+    const int64_t blocks = bh * units;
     char name[64];
     if (variant == "v2" || variant == "v2w8" || variant == "v2k64")
       snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, variant.c_str());

@@ -33,7 +33,10 @@ def _run(hip, dt, b, h, s, d, qkv_bits, causal, scale):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 3, 384, 128), (1, 1, 256, 64)])
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 3, 384, 128), (1, 1, 256, 64),
+                                     # 3 query blocks of 256: causal pairs (2, 0) and (1)
+                                     # alone, without and with the head-per-XCD order
+                                     (1, 3, 768, 128), (2, 4, 768, 128)])
 def test_attention_small(hip, dt, causal, b, h, s, d):
     say(f"attention {dt} causal={causal} B={b} H={h} S={s} D={d}")
     scale = 1.0 / np.sqrt(d)
@@ -127,3 +130,19 @@ def test_flash_causal_row_independence(hip):
     second = _run(hip, "f16", b, h, s, d, bits, True, scale)
     assert np.array_equal(first[:, :, :p + 1], second[:, :, :p + 1])
     assert not np.array_equal(first[:, :, p + 1:], second[:, :, p + 1:])
+
+
+@pytest.mark.parametrize("variant", ["v2w8", "v2", "v2k64"])
+@pytest.mark.parametrize("b,h,s", [(2, 4, 768), (1, 3, 1024)])
+def test_flash_causal_pairs_bit_identical(hip, monkeypatch, variant, b, h, s):
+    """A workgroup that takes two query blocks in turn (balanced causal pairs)
+    computes each exactly as a workgroup of one block does."""
+    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
+    d = 128
+    say(f"flash {variant} causal pairs vs single blocks B={b} H={h} S={s}")
+    scale = 1.0 / np.sqrt(d)
+    bits = [x[0] for x in _inputs(b, h, s, d, "f16", seed=41)]
+    paired = _run(hip, "f16", b, h, s, d, bits, True, scale)
+    monkeypatch.setenv("SILE_HIP_FA_PAIR", "0")
+    single = _run(hip, "f16", b, h, s, d, bits, True, scale)
+    np.testing.assert_array_equal(paired, single)
