@@ -359,9 +359,12 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
     const char* env = getenv("SILE_HIP_FA_KERNEL");
     std::string variant = env ? env : "v2w8";
-    const bool pipelined = variant == "v2" || variant == "v2w8" || variant == "v2k64";
-    if (!pipelined && variant != "q1" && variant != "q2") variant = "v2w8";
+    auto is_pipelined = [](const std::string& v) {
+      return v == "v2" || v == "v2w8" || v == "v2k64";
+    };
+    if (!is_pipelined(variant) && variant != "q1" && variant != "q2") variant = "v2w8";
     if (seq_len % 256 != 0 || (variant == "q2" && dtype != SILE_F16)) variant = "q1";
+    const bool pipelined = is_pipelined(variant);
     const int64_t bq = variant == "q1" ? 128 : 256;
     // causal pipelined kernels take query blocks in balanced pairs
     // (SILE_HIP_FA_PAIR=0: one block per workgroup)
@@ -377,7 +380,7 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const int64_t units = pair ? (seq_len / bq + 1) / 2 : seq_len / bq;
     const int64_t blocks = bh * units;
     char name[64];
-    if (variant == "v2" || variant == "v2w8" || variant == "v2k64")
+    if (pipelined)
       snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, variant.c_str());
     else
       snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s_k64", dt, variant.c_str());

@@ -37,9 +37,14 @@ def fp8_quantise(x: np.ndarray):
 def assert_close(got, ref, atol, rtol, what=""):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
-    err = np.abs(got - ref)
-    bound = atol + rtol * np.abs(ref)
-    bad = err > bound
+    with np.errstate(invalid="ignore"):  # inf - inf: handled below
+        err = np.abs(got - ref)
+        bound = atol + rtol * np.abs(ref)
+    # NaN compares false: an element is good only if its error is provably within
+    # the bound of a finite reference, or it equals the reference (matching
+    # infinities, NaN for NaN)
+    good = ((err <= bound) & np.isfinite(ref)) | (got == ref) | (np.isnan(got) & np.isnan(ref))
+    bad = ~good
     if bad.any():
         idx = np.unravel_index(np.argmax(err - bound), err.shape)
         raise AssertionError(
