@@ -46,7 +46,9 @@ def assert_close(got, ref, atol, rtol, what=""):
     good = ((err <= bound) & np.isfinite(ref)) | (got == ref) | (np.isnan(got) & np.isnan(ref))
     bad = ~good
     if bad.any():
-        idx = np.unravel_index(np.argmax(err - bound), err.shape)
+        with np.errstate(invalid="ignore"):
+            excess = np.where(bad, np.nan_to_num(err - bound, nan=np.inf), -np.inf)
+        idx = np.unravel_index(np.argmax(excess), err.shape)
         raise AssertionError(
             f"{what}: {int(bad.sum())} of {bad.size} elements out of tolerance "
             f"(atol={atol}, rtol={rtol}); worst at {idx}: got {got[idx]!r}, ref {ref[idx]!r}")
