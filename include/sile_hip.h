@@ -214,8 +214,8 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *   f32  x f32  -> f32 : any shape/layout of B, A row-major; exact canonical order
  *                        (bit-identical to the CPU backend).
  *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
- *                        A row-major, B column-major, M and N multiples of 256,
- *                        K' a multiple of 32 (16-bit) or 64 (fp8), leading
+ *                        A row-major, B column-major, M >= 256, N >= 256 with N
+ *                        a multiple of 4, K' a multiple of 32 (16-bit) or 64 (fp8), leading
  *                        dimensions multiples of 16 bytes; MFMA path.
  * Anything else -> SILE_ERR_UNSUPPORTED_BACKEND or SILE_ERR_SHAPE. */
 int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,

@@ -40,6 +40,7 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;  // in elements
   int32_t tiles_m, tiles_n, k_steps;
   float alpha;
+  int32_t m, n;           // C extents (>= 256): the last tile row / column starts at m - 256 / n - 256
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -131,12 +132,17 @@ __device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
   const int in_group = lin - group * group_size;
   const int tile_m = first_m + in_group % rows_in_group;
   const int tile_n = in_group / rows_in_group;
+  // First row / column of the tile.  When M or N is not a multiple of 256 the
+  // last tile is moved back to end at M / N, so every load stays inside the
+  // operands; the rows or columns it shares with its neighbour are computed
+  // in the same order by both workgroups and written with the same values.
+  const int64_t row0 = min(tile_m * kBM, g.m - kBM), col0 = min(tile_n * kBN, g.n - kBN);
 
   const int a_rs = (int)(g.lda * kEB), b_rs = (int)(g.ldb * kEB);
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A + (int64_t)tile_m * kBM * a_rs), (short)0, kBM * a_rs, 0x00020000);
+      (void*)(A + row0 * a_rs), (short)0, kBM * a_rs, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(B + (int64_t)tile_n * kBN * b_rs), (short)0, kBN * b_rs, 0x00020000);
+      (void*)(B + col0 * b_rs), (short)0, kBN * b_rs, 0x00020000);
   // DMA: one instruction fills 1 KiB = 8 rows of 128 bytes; wave w's
   // instruction i (0..7) fills rows 8 (4 i + w) + (lane >> 3), position
   // lane & 7, whose chunk is (lane & 7) ^ ((row >> 1) & 7) with
@@ -286,8 +292,8 @@ __device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
   iteration(ks, ks & 1, std::true_type{});
 
   // ---- epilogue ----
-  const int64_t m_base = (int64_t)tile_m * kBM + wm * 128 + (lane & 31);
-  const int64_t n_base = (int64_t)tile_n * kBN + wn * 128 + 4 * (lane >> 5);
+  const int64_t m_base = row0 + wm * 128 + (lane & 31);
+  const int64_t n_base = col0 + wn * 128 + 4 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll

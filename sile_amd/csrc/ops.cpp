@@ -31,6 +31,7 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;
   int32_t tiles_m, tiles_n, k_steps;
   float alpha;
+  int32_t m, n;
 };
 
 const char* dtype_name(int t) {
@@ -228,18 +229,23 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   if (b_layout != SILE_COL_MAJOR)
     return fail(SILE_ERR_UNSUPPORTED_BACKEND, "%s GEMM needs B column-major (K contiguous)",
                 dtype_name(a_type));
-  if (m % 256 || n % 256 || kp % kstep || kp == 0)
+  // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
+  // K' a multiple of the half k-step
+  if (m < 256 || n < 256 || n % 4 || kp % kstep || kp == 0)
     return fail(SILE_ERR_SHAPE,
-                "%s GEMM needs M, N multiples of 256 and K' multiple of %lld (M=%lld N=%lld K'=%lld)",
+                "%s GEMM needs M >= 256, N >= 256 with N a multiple of 4, and K' a multiple of "
+                "%lld (M=%lld N=%lld K'=%lld)",
                 dtype_name(a_type), (long long)kstep, (long long)m, (long long)n, (long long)kp);
   const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
   if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
   if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
       !aligned16(c))
     return fail(SILE_ERR_SHAPE, "operands and leading dimensions must be 16-byte aligned");
-  if ((m / 256) * (n / 256) > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
-  GemmArgs g{lda, ldb, ldc, (int32_t)(m / 256), (int32_t)(n / 256), (int32_t)(kp / kstep),
-             scale_a * scale_b};
+  const int64_t tiles_m = (m + 255) / 256, tiles_n = (n + 255) / 256;
+  if (tiles_m * tiles_n > 0x7fffffffLL || m > 0x7fffffffLL || n > 0x7fffffffLL)
+    return fail(SILE_ERR_SHAPE, "GEMM too large");
+  GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)(kp / kstep),
+             scale_a * scale_b, (int32_t)m, (int32_t)n};
   void* params[] = {&a, &b, &c, &g};
   int rc = launch(Module::kGemm, name, dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), params,
                   s);

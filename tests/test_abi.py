@@ -60,8 +60,10 @@ NULL = None
 @pytest.mark.parametrize("args,code", [
     # unsupported dtype pair -> UnsupportedBackend
     ((_abi.F16, _abi.BF16, _abi.F32, 256, 256, 64), 2),
-    # MFMA path with non-multiple-of-256 M -> Shape
+    # MFMA path with M below one 256-row tile -> Shape
     ((_abi.BF16, _abi.BF16, _abi.BF16, 100, 256, 64), 5),
+    # MFMA path with N not a multiple of 4 -> Shape
+    ((_abi.BF16, _abi.BF16, _abi.BF16, 256, 258, 64), 5),
     # fp8 K' not a multiple of 64 -> Shape
     ((_abi.F8E4M3, _abi.F8E4M3, _abi.BF16, 256, 256, 96), 5),
 ])

@@ -181,6 +181,47 @@ def test_padded_leading_dimensions(hip, kind):
     assert (got[:, n:].view(np.uint32) == 0xFFFFFFFF).all()
 
 
+@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
+                                      ("fp8", "bf16")])
+@pytest.mark.parametrize("m,n,k", [(300, 260, 256), (257, 1028, 320), (768, 300, 448)])
+def test_ragged_m_n(hip, kind, out, m, n, k):
+    """M and N that are not multiples of the 256 x 256 tile: the last tile row /
+    column is computed from rows / columns M - 256 / N - 256 on.  Every
+    element is checked; C sits in a wider pitch whose columns past N must keep
+    their fill."""
+    if kind == "fp8" and k % 64:
+        pytest.skip("fp8 K' is a multiple of 64")
+    ldc = n + 12
+    say(f"gemm {kind} ragged {m}x{n}x{k} -> {out}")
+    a = rng(21).normal(size=(m, k)).astype(np.float32)
+    bt = rng(22).normal(size=(n, k)).astype(np.float32)
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(k)
+        bt /= np.sqrt(k)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    dc.fill_bytes(0xFF)
+    hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+             dc.ptr, ldc, sa, sb)
+    hip.synchronize()
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f, b_f)
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} ragged")
+    raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc))
+    assert (raw[:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
+
+
 def test_f32_gemm_exact(hip):
     say("gemm f32 exact 200x300x150 (both B layouts)")
     m, n, k = 200, 300, 150
