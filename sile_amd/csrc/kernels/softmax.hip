@@ -223,6 +223,71 @@ __device__ __forceinline__ void softmax_rows_packed_kernel(const void* x, void* 
                                   static_cast<uint16_t*>(y) + row * ldy, lane);
 }
 
+// ---- register-resident row softmax of any width up to kChunks * 64 * E ----
+// Chunks wholly inside the row are 128-bit accesses; the one chunk the row
+// ends in is read and written element by element; positions past the row are
+// -inf (exp 0) and never stored.
+template <int kIn, int kOut, int kChunks>
+__device__ __forceinline__ void softmax_row_masked(const typename Elem<kIn>::Storage* __restrict__ xr,
+                                                   typename Elem<kOut>::Storage* __restrict__ yr,
+                                                   int lane, int cols) {
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  float v[kChunks][kE];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int c0 = (j * 64 + lane) * kE;
+    if (c0 + kE <= cols) {
+      load_chunk<kIn, kE>(xr + c0, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        v[j][i] = c0 + i < cols ? Elem<kIn>::load1(xr + c0 + i) : -__builtin_inff();
+    }
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) m = fmax_ordered(m, v[j][i]);
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      v[j][i] = exp2_fast((v[j][i] - m) * kLog2e);  // -inf -> 0
+      s += v[j][i];
+    }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int c0 = (j * 64 + lane) * kE;
+#pragma unroll
+    for (int i = 0; i < kE; ++i) v[j][i] *= inv;
+    if (c0 + kE <= cols) {
+      store_chunk<kOut, kE>(yr + c0, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        if (c0 + i < cols) Elem<kOut>::store1(yr + c0 + i, v[j][i]);
+    }
+  }
+}
+
+template <int kIn, int kOut, int kChunks>
+__device__ __forceinline__ void softmax_rows_masked_kernel(const void* x, void* y, int64_t rows,
+                                                           int64_t cols, int64_t ldx,
+                                                           int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  softmax_row_masked<kIn, kOut, kChunks>(static_cast<const TI*>(x) + row * ldx,
+                                         static_cast<TO*>(y) + row * ldy, lane, (int)cols);
+}
+
 template <int kIn, int kOut, int kChunks>
 __device__ __forceinline__ void softmax_rows_regs_kernel(const void* x, void* y, int64_t rows,
                                                          int64_t ldx, int64_t ldy) {
@@ -279,6 +344,23 @@ SILE_SOFTMAX_WIDTHS(bf16_bf16, kBF16, kBF16)
 SILE_SOFTMAX_WIDTHS(f32_f32, kF32, kF32)
 SILE_SOFTMAX_REGS(sile_softmax_rows_f32_f32_c32, kF32, kF32, 32)
 SILE_SOFTMAX_WIDTHS(f16_f32, kF16, kF32)
+
+#define SILE_SOFTMAX_MASKED(NAME, IN, OUT, CH)                                                 \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows,   \
+                                                         int64_t cols, int64_t ldx, int64_t ldy) { \
+    softmax_rows_masked_kernel<IN, OUT, CH>(x, y, rows, cols, ldx, ldy);                         \
+  }
+#define SILE_SOFTMAX_MASKED_WIDTHS(TAG, IN, OUT)                  \
+  SILE_SOFTMAX_MASKED(sile_softmax_rows_##TAG##_m1, IN, OUT, 1)   \
+  SILE_SOFTMAX_MASKED(sile_softmax_rows_##TAG##_m2, IN, OUT, 2)   \
+  SILE_SOFTMAX_MASKED(sile_softmax_rows_##TAG##_m4, IN, OUT, 4)   \
+  SILE_SOFTMAX_MASKED(sile_softmax_rows_##TAG##_m8, IN, OUT, 8)   \
+  SILE_SOFTMAX_MASKED(sile_softmax_rows_##TAG##_m16, IN, OUT, 16)
+SILE_SOFTMAX_MASKED_WIDTHS(f16_f16, kF16, kF16)
+SILE_SOFTMAX_MASKED_WIDTHS(bf16_bf16, kBF16, kBF16)
+SILE_SOFTMAX_MASKED_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_MASKED(sile_softmax_rows_f32_f32_m32, kF32, kF32, 32)
+SILE_SOFTMAX_MASKED_WIDTHS(f16_f32, kF16, kF32)
 
 #define SILE_SOFTMAX_PACKED(NAME, T, CH)                                                     \
   extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows, \

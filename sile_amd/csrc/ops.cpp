@@ -293,9 +293,20 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
   const char* pk = getenv("SILE_HIP_SOFTMAX_PACKED");
   const bool packed = (chunks == 8 || chunks == 16) && !(pk && pk[0] == '0') &&
                       (!strcmp(tag, "f16_f16") || !strcmp(tag, "bf16_bf16"));
+  // other widths up to 8192 (16-bit) / 8192 (fp32): one pass with a masked
+  // last chunk, the smallest power-of-two chunk count that covers the row
+  int masked = 0;
+  if (!chunks && vec_ok) {
+    for (int c : {1, 2, 4, 8, 16, 32})
+      if (!masked && cols <= (int64_t)c * 64 * elems && (c < 32 || f32_rows)) masked = c;
+  }
   if (packed) {
     snprintf(name, sizeof name, "sile_softmax_rows_%s_p%d", tag, chunks);
     void* params[] = {&x, &y, &rows, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
+  } else if (masked) {
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_m%d", tag, masked);
+    void* params[] = {&x, &y, &rows, &cols, &ldx, &ldy};
     rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
   } else if (chunks) {
     snprintf(name, sizeof name, "sile_softmax_rows_%s_c%d", tag, chunks);

@@ -45,7 +45,7 @@ def test_softmax_f16_config2_full(hip):
     np.testing.assert_array_equal(got.argmax(axis=1), ref.argmax(axis=1))
 
 
-@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 100, 3000, 1])
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 100, 3000, 1, 257, 6100, 8000])
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32", "f16_f32"])
 def test_softmax_widths_and_types(hip, cols, dt):
     rows = 37
@@ -136,3 +136,33 @@ def test_softmax_many_ragged_rows(hip, dt, rows, cols):
     t = hip.F16 if dt == "f16" else hip.BF16
     got = _softmax_gpu(hip, xb, t, t, rows, cols)
     assert_close(got, cpuref.softmax_rows(xf), atol=1e-6, rtol=1e-2, what=f"softmax {dt}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+@pytest.mark.parametrize("cols", [1000, 5000])
+def test_softmax_masked_tail_padded(hip, dt, cols):
+    """Widths that end inside a lane's chunk (the one-pass kernel's masked last
+    chunk) in wider row pitches: the row is right and the pitch padding of y
+    keeps its fill."""
+    rows, ldx, ldy = 9, cols + 16, cols + 8
+    say(f"softmax {dt} {rows}x{cols} ldx={ldx} ldy={ldy}")
+    x = (rng(cols + 5).normal(size=(rows, ldx)) * 2.0).astype(np.float32)
+    if dt == "f16":
+        xb, xf = f16_round(x)
+        t, ob, fill = hip.F16, 2, np.uint16(0xABCD)
+    else:
+        xb = xf = x
+        t, ob, fill = hip.F32, 4, np.uint32(0xABCDEF01)
+    dx = hip.DeviceBuffer.from_array(xb)
+    dy = hip.DeviceBuffer(rows * ldy * ob)
+    dy.upload(np.full((rows, ldy), fill))
+    hip.softmax_rows(t, t, rows, cols, dx.ptr, ldx, dy.ptr, ldy)
+    hip.synchronize()
+    raw = dy.download(np.uint16 if ob == 2 else np.uint32, (rows, ldy))
+    got = raw.view(np.float16).astype(np.float32) if ob == 2 else raw.view(np.float32)
+    ref = cpuref.softmax_rows(np.ascontiguousarray(xf[:, :cols]))
+    if dt == "f16":
+        assert_close(got[:, :cols], ref, atol=1e-6, rtol=1e-2, what="masked tail")
+    else:
+        assert_close(got[:, :cols], ref, atol=1e-30, rtol=1e-4, what="masked tail")
+    assert (raw[:, cols:] == fill).all()
