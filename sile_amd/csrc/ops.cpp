@@ -241,6 +241,10 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
       !aligned16(c))
     return fail(SILE_ERR_SHAPE, "operands and leading dimensions must be 16-byte aligned");
+  // a 256-row panel of A or B is one buffer resource: 32-bit byte range
+  if (256 * std::max(lda, ldb) * (int64_t)eb > 0x7fffffffLL)
+    return fail(SILE_ERR_SHAPE, "leading dimension too large for a 256-row panel (%lld, %lld)",
+                (long long)lda, (long long)ldb);
   const int64_t tiles_m = (m + 255) / 256, tiles_n = (n + 255) / 256;
   if (tiles_m * tiles_n > 0x7fffffffLL || m > 0x7fffffffLL || n > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "GEMM too large");
@@ -365,6 +369,9 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   int64_t bh = batch * heads;
   if (bh > 0x7fffffffLL / std::max<int64_t>(seq_len, 1))
     return fail(SILE_ERR_SHAPE, "attention too large");
+  // one head's K or V is one buffer resource (32-bit byte range)
+  if (seq_len * head_dim * 2 > 0x7fffffffLL)
+    return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
   // MFMA flash kernels: head_dim 128, 16-byte aligned operands.
   //   v2w8 (default) / v2k64 / v2 (pipelined, 256-query blocks, 8 waves x 32

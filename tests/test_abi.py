@@ -115,3 +115,15 @@ def test_op_host_validation():
     assert _abi.status("sile_hip_flash_attn_fwd", _abi.F16, 1, 1, 128, 512, 16, 16, 16, 16,
                        1.0, 1, NULL) == 2
     assert _abi.status("sile_hip_launch_tiles", None, None, 0, None, 0, None, 1, NULL) == 3
+
+
+def test_32bit_buffer_range_guards():
+    # a 256-row panel of A past 2 GiB (lda = 5M bf16 elements)
+    lda = 5_000_000
+    rc = _abi.status("sile_hip_gemm", _abi.BF16, _abi.BF16, _abi.BF16, 256, 256, 64, 16, lda,
+                     _abi.ROW_MAJOR, 16, 64, _abi.COL_MAJOR, 16, 256, 1.0, 1.0, 0, NULL)
+    assert rc == 5 and "panel" in _abi.last_error()
+    # one head's K past 2 GiB (S = 2^23, D = 128)
+    rc = _abi.status("sile_hip_flash_attn_fwd", _abi.F16, 1, 1, 1 << 23, 128, 16, 16, 16, 16,
+                     1.0, 1, NULL)
+    assert rc == 5 and "sequence" in _abi.last_error()
