@@ -40,6 +40,9 @@ METRIC = ("bf16 GEMM & flash-attn fwd TFLOP/s (% MI355X MFMA peak), softmax GB/s
 # Published MI355X peaks (dense): bf16/fp16 MFMA 2.5 PFLOP/s, fp8 5.0 PFLOP/s, HBM3E 8 TB/s.
 PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0}
 PEAK_HBM_GBS = 8000.0
+# fp32 VALU lane rate (the published 157.3 TFLOP/s counts an FMA as 2 flops); an
+# exact-order GEMM issues one instruction per flop
+PEAK_VALU_F32_TOPS = 78.6
 SETTLE_S = 0.5  # untimed load before each workload's warmup (clock ramp-up)
 
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
@@ -292,6 +295,34 @@ def bench_tile_ir_softmax(name, steps, warmup):
     return res
 
 
+def bench_gemm_f32_exact(name, size, steps, warmup, stream):
+    """fp32 GEMM M=N=K=size in the reference's canonical per-cell order
+    (bit-identical to its CPU backend), A and B row-major U(-1,1) (seeds 1/2,
+    the recipe of BASELINE config 1).  Every flop is its own instruction (the
+    product and the sum are rounded separately), so the bound is the VALU's
+    lane rate: 256 CUs x 128 lanes x 2.4 GHz = 78.6 T instructions/s."""
+    n = size
+    a = np.random.default_rng(1).uniform(-1, 1, size=(n, n)).astype(np.float32)
+    b = np.random.default_rng(2).uniform(-1, 1, size=(n, n)).astype(np.float32)
+    da, db = hip.DeviceBuffer.from_array(a), hip.DeviceBuffer.from_array(b)
+    dc = hip.DeviceBuffer(n * n * 4)
+    del a, b
+
+    def launch(i):
+        hip.gemm(hip.F32, hip.F32, hip.F32, n, n, n, da.ptr, n, hip.ROW_MAJOR, db.ptr, n,
+                 hip.ROW_MAJOR, dc.ptr, n, 1.0, 1.0, 0, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    region = time_launches(launch, steps, warmup, stream)
+    flop = 2.0 * n ** 3
+    res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "valu", PEAK_VALU_F32_TOPS,
+                    None)
+    res["flop_per_launch"] = flop
+    for buf in (da, db, dc):
+        buf.close()
+    return res
+
+
 def bench_copy_calibration(name, steps, warmup):
     """A plain device-to-device copy of COPY_BYTES (the HIP runtime's blit
     kernel behind sile_hip_memcpy_dtod).  Run under rocprofv3 --pmc it gives
@@ -390,7 +421,8 @@ def traffic_from_pmc(root):
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
-EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192"]
+EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f32_exact_4096",
+         "gemm_f32_exact_512"]
 
 
 def main():
@@ -430,6 +462,9 @@ def main():
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
         elif name == "tile_ir_softmax_f32_8192":
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
+        elif name.startswith("gemm_f32_exact_"):
+            results[name] = bench_gemm_f32_exact(name, int(name.split("_")[-1]), args.steps,
+                                                 args.warmup, stream)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
             results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,

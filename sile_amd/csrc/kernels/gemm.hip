@@ -8,8 +8,8 @@
 // (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444) on the
 // matrix cores; k runs over K' = (K / bk) * bk as there, which the host
 // resolves before launch.  One body (gemm_k64_body) serves bf16, f16 and fp8
-// e4m3 operands; its design is described above it.  sile_gemm_f32_exact is the
-// fp32 path in the canonical order (bit-identical to the CPU backend).
+// e4m3 operands; its design is described above it.  sile_gemm_f32_exact_{nn,nt}_t{128,64,32}
+// are the fp32 path in the canonical order (bit-identical to the CPU backend).
 #include <type_traits>
 
 #include "common.h"
@@ -329,27 +329,145 @@ SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 // cell, s = s + a*b from 0.0f over k < kp with separate roundings (no FMA).
 // A row-major [M,K]; B either row-major [K,N] (b_col_major = 0, the reference
 // layout) or column-major (stored [N,K]).
-extern "C" __global__ __launch_bounds__(256) void sile_gemm_f32_exact(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int64_t M,
-    int64_t N, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc, int32_t b_col_major) {
+// fp32 GEMM in the canonical order, register-tiled.  Each output keeps the
+// reference's chain s = s + a[k] * b[k] from 0.0f in increasing k, the product
+// and the sum rounded separately (no contraction), so the result is the same
+// bit for bit as the CPU backend's.  The work is organised as T x T outputs
+// per workgroup of 256 threads (T = 128, 64 or 32: the largest that still gives
+// ~1024 workgroups), (T/16) x (T/16) independent chains per thread, operands staged in LDS
+// in 16-deep k-tiles (double-buffered), A and a column-major B transposed on
+// the way in so a thread reads its 8 rows / 8 columns of one k as two 16-byte
+// LDS reads.  Outside M, N and K' the staged values are zero: a padded term
+// adds +0.0f, which leaves every sum unchanged (a sum that starts at +0.0f
+// and adds products never becomes -0.0f).
+namespace f32t {
+constexpr int kK = 16, kPad = 4;
+}
+
+// kT x kT outputs per workgroup of 256 threads, kR x kR per thread (kR = kT / 16)
+template <bool kBCol, int kT>
+__device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
+                                                    const float* __restrict__ B,
+                                                    float* __restrict__ C, int64_t M, int64_t N,
+                                                    int64_t kp, int64_t lda, int64_t ldb,
+                                                    int64_t ldc) {
 #pragma clang fp contract(off)
-  const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x & 15);
-  const int64_t m = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
-  if (m >= M || n >= N) return;
-  const float* ap = A + m * lda;
-  float s = 0.0f;
-  if (b_col_major) {
-    const float* bp = B + n * ldb;
-    for (int64_t k = 0; k < kp; ++k) {
-      float p = ap[k] * bp[k];
-      s = s + p;
+  using namespace f32t;
+  constexpr int kR = kT / 16;           // outputs per thread and dimension
+  constexpr int kL = kT * kK / 256;     // staged elements per thread and operand
+  static_assert(kR == 2 || kR == 4 || kR == 8, "tile sizes 32, 64, 128");
+  __shared__ __attribute__((aligned(16))) float As[2][kK][kT + kPad];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kK][kT + kPad];
+  const int t = threadIdx.x;
+  const int tm = t >> 4, tn = t & 15;
+  const int64_t m0 = (int64_t)blockIdx.y * kT, n0 = (int64_t)blockIdx.x * kT;
+  // staging: A row m0 + la_r, k offsets la_k .. + kL; B likewise (column-major)
+  // or B row k0 + lb_r, columns n0 + lb_c .. + kL (row-major)
+  const int la_r = t / (kK / kL), la_k = (t % (kK / kL)) * kL;
+  const int lb_r = kBCol ? la_r : t / (kT / kL);
+  const int lb_c = kBCol ? la_k : (t % (kT / kL)) * kL;
+  float ra[kL], rb[kL];
+  auto gload = [&](int64_t k0) {
+    const int64_t am = m0 + la_r;
+#pragma unroll
+    for (int i = 0; i < kL; ++i) {
+      const int64_t k = k0 + la_k + i;
+      ra[i] = (am < M && k < kp) ? A[am * lda + k] : 0.0f;
     }
-  } else {
-    const float* bp = B + n;
-    for (int64_t k = 0; k < kp; ++k) {
-      float p = ap[k] * bp[k * ldb];
-      s = s + p;
+    if constexpr (kBCol) {
+      const int64_t bn = n0 + lb_r;
+#pragma unroll
+      for (int i = 0; i < kL; ++i) {
+        const int64_t k = k0 + lb_c + i;
+        rb[i] = (bn < N && k < kp) ? B[bn * ldb + k] : 0.0f;
+      }
+    } else {
+      const int64_t k = k0 + lb_r;
+#pragma unroll
+      for (int i = 0; i < kL; ++i) {
+        const int64_t bn = n0 + lb_c + i;
+        rb[i] = (bn < N && k < kp) ? B[k * ldb + bn] : 0.0f;
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kL; ++i) As[buf][la_k + i][la_r] = ra[i];
+    if constexpr (kBCol) {
+#pragma unroll
+      for (int i = 0; i < kL; ++i) Bs[buf][lb_c + i][lb_r] = rb[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kL; ++i) Bs[buf][lb_r][lb_c + i] = rb[i];
+    }
+  };
+  // kR consecutive floats of an LDS row
+  auto lread = [&](const float* p, float (&v)[kR]) {
+    if constexpr (kR == 2) {
+      const f32x2 x = *reinterpret_cast<const f32x2*>(p);
+      v[0] = x[0]; v[1] = x[1];
+    } else {
+#pragma unroll
+      for (int h = 0; h < kR / 4; ++h) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(p + 4 * h);
+        v[4 * h] = x[0]; v[4 * h + 1] = x[1]; v[4 * h + 2] = x[2]; v[4 * h + 3] = x[3];
+      }
+    }
+  };
+
+  float acc[kR][kR];
+#pragma unroll
+  for (int i = 0; i < kR; ++i)
+#pragma unroll
+    for (int j = 0; j < kR; ++j) acc[i][j] = 0.0f;
+
+  const int64_t ktiles = (kp + kK - 1) / kK;
+  if (ktiles > 0) {
+    gload(0);
+    sstore(0);
+  }
+  __syncthreads();
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int buf = (int)(kt & 1);
+    if (kt + 1 < ktiles) gload((kt + 1) * kK);
+#pragma unroll 2
+    for (int kk = 0; kk < kK; ++kk) {
+      float av[kR], bv[kR];
+      lread(&As[buf][kk][kR * tm], av);
+      lread(&Bs[buf][kk][kR * tn], bv);
+#pragma unroll
+      for (int i = 0; i < kR; ++i)
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+          const float p = av[i] * bv[j];
+          acc[i][j] = acc[i][j] + p;
+        }
+    }
+    if (kt + 1 < ktiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    const int64_t m = m0 + kR * tm + i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < kR; ++j) {
+      const int64_t n = n0 + kR * tn + j;
+      if (n < N) C[m * ldc + n] = acc[i][j];
     }
   }
-  C[m * ldc + n] = s;
 }
+
+#define SILE_GEMM_F32_TILED(NAME, BCOL, T)                                                     \
+  extern "C" __global__ __launch_bounds__(256, 2) void NAME(                                   \
+      const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,        \
+      int64_t M, int64_t N, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc) {             \
+    gemm_f32_tiled_body<BCOL, T>(A, B, C, M, N, kp, lda, ldb, ldc);                           \
+  }
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nn_t128, false, 128)
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nn_t64, false, 64)
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nn_t32, false, 32)
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nt_t128, true, 128)
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nt_t64, true, 64)
+SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nt_t32, true, 32)
+

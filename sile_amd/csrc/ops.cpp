@@ -17,6 +17,12 @@ using namespace sile_rt;
 
 namespace {
 
+// The exact-order fp32 GEMM: the largest tile (128, 64 or 32) that still gives
+// about 1024 workgroups (4 per CU), or 32.
+int launch_f32_exact(bool b_col_major, const void* a, const void* b, void* c, int64_t m,
+                     int64_t n, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc,
+                     hipStream_t s);
+
 // Kernel argument blocks; layouts match the structs in kernels/*.hip.
 struct MatmulTileArgs {
   int64_t lda, ldb, ldc, bm, bn, bk, tiles_n, total;
@@ -109,8 +115,16 @@ int sile_hip_kernel_matmul(void* const* buffers, int64_t num_threadgroups,
   const void* a = buffers[0];
   const void* b = buffers[1];
   void* c = buffers[2];
-  void* params[] = {&a, &b, &c, &t};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (run == t.total && (c0 / bm) * bm <= 65535LL * 32) {
+    // every tile runs: the tiles form the rectangle [0, M') x [0, N') of C,
+    // computed by the register-tiled kernel in the same per-cell order
+    rc = launch_f32_exact(false, a, b, c, (c0 / bm) * bm, t.tiles_n * bn, kp, a1, b1, c1, s);
+    if (rc != SILE_OK) return rc;
+    SILE_HIP_CHECK(hipStreamSynchronize(s));
+    return ok();
+  }
+  void* params[] = {&a, &b, &c, &t};
   rc = launch(Module::kDsl, "sile_dsl_matmul_f32", dim3((unsigned)run), dim3(256), params, s);
   if (rc != SILE_OK) return rc;
   SILE_HIP_CHECK(hipStreamSynchronize(s));
@@ -201,12 +215,8 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
     const bool bcol = b_layout == SILE_COL_MAJOR;
     if (lda < k || ldc < n || (bcol ? ldb < k : ldb < n))
       return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
-    int32_t bc = bcol ? 1 : 0;
-    void* params[] = {&a, &b, &c, &m, &n, (void*)&kp, &lda, &ldb, &ldc, &bc};
-    const int64_t gx = (n + 15) / 16, gy = (m + 15) / 16;
-    if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
-    int rc = launch(Module::kGemm, "sile_gemm_f32_exact", dim3((unsigned)gx, (unsigned)gy),
-                    dim3(256), params, s);
+    if (m > 65535LL * 32) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
+    int rc = launch_f32_exact(bcol, a, b, c, m, n, kp, lda, ldb, ldc, s);
     return rc == SILE_OK ? ok() : rc;
   }
 
@@ -424,3 +434,20 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
 }
 
 }  // extern "C"
+
+namespace {
+int launch_f32_exact(bool b_col_major, const void* a, const void* b, void* c, int64_t m,
+                     int64_t n, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc,
+                     hipStream_t s) {
+  int tile = 32;
+  for (int t : {128, 64})
+    if (tile == 32 && ((m + t - 1) / t) * ((n + t - 1) / t) >= 1024 && (m + t - 1) / t <= 65535)
+      tile = t;
+  const int64_t gx = (n + tile - 1) / tile, gy = (m + tile - 1) / tile;
+  if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
+  char name[64];
+  snprintf(name, sizeof name, "sile_gemm_f32_exact_%s_t%d", b_col_major ? "nt" : "nn", tile);
+  void* params[] = {(void*)&a, (void*)&b, &c, &m, &n, &kp, &lda, &ldb, &ldc};
+  return launch(Module::kGemm, name, dim3((unsigned)gx, (unsigned)gy), dim3(256), params, s);
+}
+}  // namespace

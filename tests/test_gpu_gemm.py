@@ -222,9 +222,13 @@ def test_ragged_m_n(hip, kind, out, m, n, k):
     assert (raw[:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
 
 
-def test_f32_gemm_exact(hip):
-    say("gemm f32 exact 200x300x150 (both B layouts)")
-    m, n, k = 200, 300, 150
+@pytest.mark.parametrize("m,n,k", [(200, 300, 150),      # 32-wide tiles, ragged edges
+                                   (2048, 2000, 40),      # 64-wide tiles, K' not a multiple of 16
+                                   (4096, 4096, 33)])     # 128-wide tiles
+def test_f32_gemm_exact(hip, m, n, k):
+    """The fp32 path keeps the canonical per-cell order whatever its tiling:
+    bit-identical to the oracle for both B layouts."""
+    say(f"gemm f32 exact {m}x{n}x{k} (both B layouts)")
     a = rng(1).uniform(-1, 1, size=(m, k)).astype(np.float32)
     b = rng(2).uniform(-1, 1, size=(k, n)).astype(np.float32)
     da, dbr = hip.DeviceBuffer.from_array(a), hip.DeviceBuffer.from_array(b)
