@@ -734,10 +734,6 @@ struct Emitter {
     } else if (in.op == "select") {
       o << "  " << r << " = (" << opnd(a[0]) << ") ? (" << opnd(a[1]) << ") : (" << opnd(a[2])
         << ");\n";
-    } else if (in.op == "call") {
-      o << "  " << (r.empty() ? "" : r + " = ") << in.sub << "(";
-      for (size_t k = 0; k < a.size(); ++k) o << (k ? ", " : "") << opnd(a[k]);
-      o << ");\n";
     } else if (in.op == "intr") {
       if (in.sub == "tid") o << "  " << r << " = 0;\n";
       else if (in.sub == "ctaid") o << "  " << r << " = sile_gid_" << in.dim << ";\n";
@@ -786,10 +782,6 @@ struct Emitter {
       o << "  } else {\n";
       jump(t.f, t.fargs);
       o << "  }\n";
-    } else if (t.kind == "switch") {
-      o << "  switch (" << opnd(t.cond) << ") {\n";
-      for (auto& c : t.cases) o << "    case " << c.first << "LL: goto L_" << ident(c.second) << ";\n";
-      o << "    default: goto L_" << ident(t.t) << ";\n  }\n";
     }
   }
 
@@ -924,6 +916,27 @@ struct Emitter {
   }
 };
 
+// The backends' shared contract (crates/sile-backend/src/verify.rs:21-43): no
+// switch terminators, no calls to tile helpers.  Like the Metal target
+// (crates/sile-backend/src/metal/codegen.rs), other calls are rejected too: the
+// generated HIP source defines no helpers to call.  Thread ids are allowed and
+// are 0, as in the C target (one program per thread).
+void verify(const Function& fn) {
+  for (const Block& b : fn.blocks) {
+    if (b.term.kind == "switch")
+      throw ParseError{"HIP backend emit does not support switch terminators (block `" +
+                       b.name + "`)"};
+    for (const Inst& in : b.insts) {
+      if (in.op != "call") continue;
+      if (starts_with(in.sub, "tile_"))
+        throw ParseError{"HIP backend emit does not allow tile helper calls in LLVM IR, got `" +
+                         in.sub + "` (block `" + b.name + "`)"};
+      throw ParseError{"HIP backend emit does not support LLVM IR call instructions, got `" +
+                       in.sub + "` (block `" + b.name + "`)"};
+    }
+  }
+}
+
 // parse + emit; returns a status and fills `src` / the last error
 int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::string& src,
            std::string& name) {
@@ -933,6 +946,7 @@ int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::
   try {
     Parser p;
     p.parse(std::string(text));
+    verify(p.fn);
     Emitter e{p.fn, p.types, {}};
     src = e.emit(plan_out, rows, cols);
     name = "sile_kernel_" + p.fn.name;

@@ -104,3 +104,37 @@ def test_tile_plan_must_name_a_shaped_parameter():
     with pytest.raises(hip.SileError) as e:
         hip.llir_to_hip(text("vec_add"), (2, 0, 4))
     assert e.value.kind == "Shape"
+
+
+def _fn(body, name="contract"):
+    return ("define void @" + name + "(ptr addrspace(4) %__sile_shapes) {\n"
+            "  ; sile.param %__sile_shapes [elem=i64]\n" + body + "}\n")
+
+
+def test_switch_terminator_is_rejected():
+    # crates/sile-backend/tests/compile.rs:23-57: every target rejects switch
+    src = _fn("entry:\n  switch i64 0, label %exit [1 , label %exit]\nexit:\n  ret void\n")
+    with pytest.raises(hip.SileError) as e:
+        hip.llir_to_hip(src)
+    assert e.value.kind == "Compile"
+    assert "does not support switch terminators" in str(e.value)
+
+
+def test_tile_helper_and_unknown_calls_are_rejected():
+    # crates/sile-backend/src/verify.rs:31-40 (tile helpers, every target) and
+    # crates/sile-backend/tests/compile.rs:81-103 (other calls, the Metal target;
+    # the generated HIP defines no helpers either)
+    for callee, why in [("tile_load", "does not allow tile helper calls"),
+                        ("unknown_helper", "does not support LLVM IR call instructions")]:
+        src = _fn(f"entry:\n  call void @{callee}()\n  ret void\n")
+        with pytest.raises(hip.SileError) as e:
+            hip.llir_to_hip(src)
+        assert e.value.kind == "Compile" and why in str(e.value), str(e.value)
+
+
+def test_thread_id_is_allowed_and_is_zero():
+    # crates/sile-backend/tests/compile.rs:105-131: the C target allows thread_id
+    # (one program per thread, so it is 0); so does the HIP target
+    src = _fn("entry:\n  %tid = call i32 @llvm.nvvm.tid.x()\n  ret void\n")
+    out = hip.llir_to_hip(src)
+    assert "v_tid = 0;" in out
