@@ -295,7 +295,7 @@ def bench_tile_ir_softmax(name, steps, warmup):
     return res
 
 
-def bench_gemm_f32_exact(name, size, steps, warmup, stream):
+def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic):
     """fp32 GEMM M=N=K=size in the reference's canonical per-cell order
     (bit-identical to its CPU backend), A and B row-major U(-1,1) (seeds 1/2,
     the recipe of BASELINE config 1).  Every flop is its own instruction (the
@@ -316,7 +316,7 @@ def bench_gemm_f32_exact(name, size, steps, warmup, stream):
     region = time_launches(launch, steps, warmup, stream)
     flop = 2.0 * n ** 3
     res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "valu", PEAK_VALU_F32_TOPS,
-                    None)
+                    traffic.get(name))
     res["flop_per_launch"] = flop
     for buf in (da, db, dc):
         buf.close()
@@ -384,7 +384,7 @@ def traffic_from_pmc(root):
     """Builds profiles/traffic.json from rocprofv3 --pmc runs of this script,
     one per workload and counter: ROOT/pmc_fetch_<name>/ (FETCH_SIZE) and
     ROOT/pmc_write_<name>/ (WRITE_SIZE), <name> being a workload of ALL or
-    copy_calibration.  The mean per-dispatch KiB of the workload's kernel is
+    EXTRA (those without both runs are left out).  The mean per-dispatch KiB of the workload's kernel is
     scaled by what the same counter reads for the copy calibration (COPY_BYTES
     each way): bytes = KiB * COPY_BYTES / copy_KiB."""
     import csv
@@ -409,7 +409,7 @@ def traffic_from_pmc(root):
     sf, sw = COPY_BYTES / (cf * 1024), COPY_BYTES / (cw * 1024)
     out = {"_scale": {"fetch": round(sf, 4), "write": round(sw, 4), "copy_bytes": COPY_BYTES,
                       "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1)}}
-    for name in ALL:
+    for name in ALL + EXTRA:
         def is_sile(k):
             return k.startswith("sile_")
         f = mean_kib(os.path.join(root, "pmc_fetch_" + name), "FETCH_SIZE", is_sile)
@@ -464,7 +464,7 @@ def main():
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
         elif name.startswith("gemm_f32_exact_"):
             results[name] = bench_gemm_f32_exact(name, int(name.split("_")[-1]), args.steps,
-                                                 args.warmup, stream)
+                                                 args.warmup, stream, traffic)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
             results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,
