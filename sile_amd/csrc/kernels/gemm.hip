@@ -7,8 +7,9 @@
 // This is the tile op `MmaF` of the canonical matmul
 // (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444) on the
 // matrix cores; k runs over K' = (K / bk) * bk as there, which the host
-// resolves before launch.  One body (gemm_k64_body) serves bf16, f16 and fp8
-// e4m3 operands; its design is described above it.  sile_gemm_f32_exact_{nn,nt}_t{128,64,32}
+// resolves before launch.  bf16 / f16 operands run on gemm_ring16_body
+// (16 x 16 MFMA blocks, a ring of 5 LDS tiles), fp8 e4m3 on gemm_k64_body
+// (32 x 32 blocks, 2 LDS stages); their designs are described above them.  sile_gemm_f32_exact_{nn,nt}_t{128,64,32}
 // are the fp32 path in the canonical order (bit-identical to the CPU backend).
 #include <type_traits>
 
@@ -66,30 +67,358 @@ SILE_DEV f32x16 mma32x32(const u32x4* a, const u32x4* b, f32x16 c) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16, f16 and fp8 e4m3 operands: 128-byte k-steps through 2 LDS stages.
+// Tile placement, shared by both bodies.
 //
-// 256 x 256 output tile per workgroup of 4 waves (2 x 2), 128 x 128 per wave
-// as 4 x 4 blocks of v_mfma_f32_32x32x16_{bf16,f16} or
-// v_mfma_f32_32x32x64_f8f6f4 (256 fp32 accumulators per lane).  The MFMA is
-// issued with the B fragment first, so accumulator register r of lane l is
-// C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of its block.
-//
+// 256 x 256 output tile per workgroup of 4 waves (2 x 2, 128 x 128 per wave).
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
 // instruction of a wave fills 1 KiB of LDS, lane l writing bytes
 // [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
-// at its LDS slot under the swizzle.  The buffer resources cover the tile's
-// 256-row A and B panels (loads past a panel return zero).  A k-step is 128
-// bytes of each row (64 16-bit or 128 fp8 elements), so one instruction
-// fetches 8 whole 128-byte lines.  Rows hold 8 chunks of 16 bytes; chunk c of
-// row r sits at c ^ ((r >> 1) & 7), conflict-free for the 32-row fragment
-// reads.  A stage (64 KiB) holds one k-step of A and B; there are 2.
+// at its LDS slot under the swizzle.  A k-step is 128 bytes of each row (64
+// 16-bit or 128 fp8 elements), so one instruction fetches 8 whole 128-byte
+// lines, and one operand of one k-step is a 32 KiB tile.  Rows hold 8 chunks
+// of 16 bytes; chunk c of row r sits at c ^ ((r >> 1) & 7), which puts the
+// fragment reads of 16 or 32 consecutive rows (one chunk each) on distinct
+// banks.  The buffer resources cover the tile's 256-row A and B panels (loads
+// past a panel return zero).
+// ---------------------------------------------------------------------------
+constexpr int kRowB = 128;            // bytes of a tile row per k-step
+constexpr int kTileB = 256 * kRowB;   // one operand of one k-step: 32 KiB
+
+struct TilePlan {
+  int64_t row0, col0;                 // first row / column of the tile in C
+  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+  int a_rs, b_rs;                     // bytes per row of A / B
+  int a_voff, b_voff;                 // this lane's byte offsets for the tile loads
+};
+
+template <int kEB>
+SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& g, int wave,
+                            int lane) {
+  TilePlan p;
+  // XCD-aware tile order: workgroups go round-robin to the 8 XCDs; each XCD
+  // gets a contiguous range of tiles, grouped 8 tile-rows at a time
+  const int num_tiles = g.tiles_m * g.tiles_n;
+  const int bid = blockIdx.x;
+  int lin = bid;
+  if ((num_tiles & 7) == 0) lin = (bid & 7) * (num_tiles >> 3) + (bid >> 3);
+  constexpr int kGroupM = 8;
+  const int group_size = kGroupM * g.tiles_n;
+  const int group = lin / group_size;
+  const int first_m = group * kGroupM;
+  const int rows_in_group = min(g.tiles_m - first_m, kGroupM);
+  const int in_group = lin - group * group_size;
+  const int tile_m = first_m + in_group % rows_in_group;
+  const int tile_n = in_group / rows_in_group;
+  // When M or N is not a multiple of 256 the last tile is moved back to end
+  // at M / N, so every load stays inside the operands; the rows or columns it
+  // shares with its neighbour are computed in the same order by both
+  // workgroups and written with the same values.
+  p.row0 = min(tile_m * kBM, g.m - kBM);
+  p.col0 = min(tile_n * kBN, g.n - kBN);
+  p.a_rs = (int)(g.lda * kEB);
+  p.b_rs = (int)(g.ldb * kEB);
+  p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs), (short)0,
+                                               kBM * p.a_rs, 0x00020000);
+  p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs), (short)0,
+                                               kBN * p.b_rs, 0x00020000);
+  // wave w's load instruction i (0..7) of an operand fills rows
+  // 8 (4 i + w) + (lane >> 3), position lane & 7, whose chunk is
+  // (lane & 7) ^ ((row >> 1) & 7) with (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3)
+  const int dma_row = 8 * wave + (lane >> 3);
+  const int dma_chunk = (lane & 7) ^ (((wave & 1) << 2) | ((lane >> 4) & 3));
+  p.a_voff = dma_row * p.a_rs + dma_chunk * 16;
+  p.b_voff = dma_row * p.b_rs + dma_chunk * 16;
+  return p;
+}
+
+// One 16 x 16 output block over 32 k with the accumulator pinned in AGPRs
+// ("+a"): for this shape the compiler's own allocation copies every
+// accumulator through VGPRs around each MFMA.  As the instruction is opaque
+// to the compiler, the caller pads before the accumulators are read.
+template <int kKind>
+SILE_DEV void mma16x16(const u32x4& a, const u32x4& b, f32x4& c) {
+  static_assert(kKind != kFP8, "fp8 uses the 32 x 32 blocks");
+  if constexpr (kKind == kBF16)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// 16-bit C through LDS: a wave's 128 x 128 results are put into LDS rows of
+// 256 + 16 bytes (the pad puts the rows that one put instruction of the
+// accumulator layouts writes on distinct banks), then written back so that
+// each store instruction covers whole 256-byte rows of C (16-byte stores, 4
+// rows per instruction; 8-byte stores, 2 rows, when C's rows are not 16-byte
+// aligned).  Writing straight from the accumulator layouts touches 16 or 32
+// rows per instruction with 8 bytes each and ran 5 % slower at 8192^3, with
+// twice C's size written to HBM.  fill(put) calls put(row, col, v) for 4
+// consecutive columns of the wave's tile; the wave's LDS region is its own.
+constexpr int kCRowB = 256 + 16;
+constexpr int kCStageB = 128 * kCRowB;   // one wave's staged C: 34 KiB
+
+template <int kOut, typename Fill>
+SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, uint8_t* cst,
+                                Fill fill) {
+  static_assert(kOut != kOutF32, "16-bit C");
+  fill([&](int row, int col, f32x4 v) {
+    const u32x2 w = kOut == kOutBF16 ? u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}
+                                     : u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(cst + row * kCRowB + col * 2) = w;
+  });
+  __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  const int lane = threadIdx.x & 63;
+  uint16_t* cbase = static_cast<uint16_t*>(C) + m0 * ldc + n0;
+  if ((ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(cbase) & 15) == 0) {
+    const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll 8
+    for (int t = 0; t < 32; ++t) {
+      const int row = 4 * t + lg;
+      *reinterpret_cast<u32x4*>(cbase + row * ldc + lr * 8) =
+          *reinterpret_cast<const u32x4*>(cst + row * kCRowB + lr * 16);
+    }
+  } else {
+    const int lr = lane & 31, lg = lane >> 5;
+#pragma unroll 8
+    for (int t = 0; t < 64; ++t) {
+      const int row = 2 * t + lg;
+      *reinterpret_cast<u32x2*>(cbase + row * ldc + lr * 4) =
+          *reinterpret_cast<const u32x2*>(cst + row * kCRowB + lr * 8);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 / f16 operands: v_mfma_f32_16x16x32 through a ring of 5 LDS tiles.
 //
-// A k-step is kSubs sub-steps of one MFMA depth (4 of 16 elements for 16-bit
-// operands, 2 of 64 for fp8) whose fragments (4 A + 4 B blocks per lane: row
-// l % 32 of a block, the kCh 16-byte chunks kCh (2 sub + l / 32) + h of the
-// row, kCh = 1 for 16-bit and 2 for fp8) alternate between register sets X
-// (even sub-steps) and Y (odd).  Iteration ks (stage ks & 1), after the
-// barrier that published k-step ks:
+// A wave's 128 x 128 is 8 x 8 blocks of v_mfma_f32_16x16x32_{bf16,f16} (256
+// fp32 accumulators per lane).  The MFMA is issued with the B fragment first,
+// so accumulator register r of lane l is C[m = l % 16][n = 4 (l / 16) + r] of
+// its block.  A k-step (64 elements) is two sub-steps of 32; a fragment is row
+// l % 16 of a 16-row block, chunk 4 sub + l / 16.  Sub-step 0's fragments go to
+// register set X, sub-step 1's to Y.
+//
+// LDS holds a ring of 5 operand tiles (160 KiB): k-step ks's A tile is chunk
+// 2 ks and its B tile chunk 2 ks + 1; chunk c sits in slot c % 5.  The barrier
+// that starts k-step ks frees the slots of k-step ks - 1, which receive B of
+// ks + 1 and A of ks + 2, so every tile load has one or two k-steps to land
+// and a wave's 16 load instructions of a k-step can be spread evenly over
+// it: one per 8 MFMAs (128 cycles).  (Two 64 KiB stages force the loads into
+// the first half of the k-step, where they fill the load queue and stall the
+// MFMAs issued behind them: 10-13 % slower at 4096^3 and 8192^3.)
+//
+// Iteration ks, after the barrier that published A and B of ks:
+//   phase 0, 4 groups:     MFMA Y(ks - 1) rows 4..7 | reads X(ks)
+//   sub-step 1, 8 groups:  MFMA X(ks) rows 0..7     | reads Y(ks)
+//   tail, 4 groups:        MFMA Y(ks) rows 0..3
+//   s_waitcnt (B of ks + 1 landed, A of ks + 2 may be in flight) + s_barrier
+// A group is the 8 MFMAs of one accumulator row with its fragment reads and
+// one tile load at fixed places (2 MFMA, read(s), 2 MFMA, read(s), 2 MFMA,
+// load, 2 MFMA), fenced so the compiler keeps that order; loads 0..7 of a
+// k-step are B of ks + 1, 8..15 A of ks + 2.  k_steps counts half k-steps
+// (32 elements): an odd count ends with a half k-step whose sub-step 1
+// multiplies zero fragments.
+// ---------------------------------------------------------------------------
+template <int kKind, int kOut>
+__device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
+                                                 const uint8_t* __restrict__ B,
+                                                 void* __restrict__ C, const GemmArgs& g,
+                                                 uint8_t* smem) {
+  static_assert(kKind != kFP8, "16-bit operands");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const TilePlan p = plan_tile<2>(A, B, g, wave, lane);
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // LDS-DMA bases in SGPRs
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  u32x4 xa[8], xb[8], ya[8], yb[8];
+  const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
+  const bool half_last = (g.k_steps & 1) != 0;
+  const int f_row = lane & 15, f_grp = lane >> 4;
+  const int f_swz = (f_row >> 1) & 7;         // block rows differ by multiples of 16
+  const int a_fb = (wm * 128 + f_row) * kRowB, b_fb = (wn * 128 + f_row) * kRowB;
+
+  // tile load instruction i (0..7) of operand B (or A) of k-step ks into slot
+  auto load = [&](bool is_b, int ks, int slot, int i) {
+    uint8_t* dst = smem + slot * kTileB + wave_s * 1024 + i * 4096;
+    if (is_b)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(p.b_rsrc, (lds_ptr_t)dst, 16, p.b_voff,
+                                               i * 32 * p.b_rs + ks * kRowB, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(p.a_rsrc, (lds_ptr_t)dst, 16, p.a_voff,
+                                               i * 32 * p.a_rs + ks * kRowB, 0, 0);
+  };
+  // fragment q of sub-step sub: the A block q (q < 8) or the B block q - 8
+  auto read = [&](int sa, int sb, int sub, int q, u32x4 (&fa)[8], u32x4 (&fb)[8]) {
+    const int off = ((4 * sub + f_grp) ^ f_swz) << 4;
+    if (q < 8)
+      fa[q] = *reinterpret_cast<const u32x4*>(smem + sa * kTileB + a_fb + q * 16 * kRowB + off);
+    else
+      fb[q - 8] =
+          *reinterpret_cast<const u32x4*>(smem + sb * kTileB + b_fb + (q - 8) * 16 * kRowB + off);
+  };
+  // MFMAs of accumulator row i, columns [j0, j1)
+  auto mma = [&](const u32x4 (&fa)[8], const u32x4 (&fb)[8], int i, int j0, int j1) {
+#pragma unroll
+    for (int j = j0; j < j1; ++j) mma16x16<kKind>(fb[i], fa[j], acc[i][j]);
+  };
+  auto mod5 = [](int x) { return x >= 5 ? x - 5 : x; };
+#define SILE_FENCE __builtin_amdgcn_sched_barrier(0)
+
+  // k-step ks with its A tile in slot c0 and B tile in slot c0 + 1 (mod 5);
+  // loads B of ks + 1 when kLoadB, A of ks + 2 when kLoadA
+  auto iteration = [&](int ks, int c0, auto load_b_c, auto load_a_c, auto final_c) {
+    constexpr bool kFinal = decltype(final_c)::value;
+    constexpr bool kLoadB = decltype(load_b_c)::value, kLoadA = decltype(load_a_c)::value;
+    const int sa = c0, sb = mod5(c0 + 1), lb = mod5(c0 + 3), la = mod5(c0 + 4);
+    int n = 0;   // tile loads issued so far in this k-step
+    auto load_next = [&]() {
+      if (n < 8) {
+        if constexpr (kLoadB) load(true, ks + 1, lb, n);
+      } else {
+        if constexpr (kLoadA) load(false, ks + 2, la, n - 8);
+      }
+      ++n;
+    };
+    // phase 0: MFMA Y(ks - 1) rows 4..7 | reads X(ks): 4 per group
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      SILE_FENCE; mma(ya, yb, 4 + r, 0, 2); SILE_FENCE;
+      read(sa, sb, 0, 4 * r, xa, xb);
+      read(sa, sb, 0, 4 * r + 1, xa, xb);
+      SILE_FENCE; mma(ya, yb, 4 + r, 2, 4); SILE_FENCE;
+      read(sa, sb, 0, 4 * r + 2, xa, xb);
+      read(sa, sb, 0, 4 * r + 3, xa, xb);
+      SILE_FENCE; mma(ya, yb, 4 + r, 4, 6); SILE_FENCE;
+      load_next();
+      SILE_FENCE; mma(ya, yb, 4 + r, 6, 8); SILE_FENCE;
+    }
+    // sub-step 1: MFMA X(ks) rows 0..7 | reads Y(ks): 2 per group (A blocks
+    // first: every MFMA of a row needs all of them)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      SILE_FENCE; mma(xa, xb, r, 0, 2); SILE_FENCE;
+      read(sa, sb, 1, 2 * r, ya, yb);
+      SILE_FENCE; mma(xa, xb, r, 2, 4); SILE_FENCE;
+      read(sa, sb, 1, 2 * r + 1, ya, yb);
+      if constexpr (kFinal) {
+        // a half final k-step: sub-step 1 multiplies zeros (the LDS bytes past
+        // the last 32 elements hold whatever followed them in memory)
+#pragma unroll
+        for (int q = 2 * r; q < 2 * r + 2; ++q) {
+          if (q < 8) ya[q] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[q];
+          else yb[q - 8] = half_last ? u32x4{0u, 0u, 0u, 0u} : yb[q - 8];
+        }
+      }
+      SILE_FENCE; mma(xa, xb, r, 4, 6); SILE_FENCE;
+      load_next();
+      SILE_FENCE; mma(xa, xb, r, 6, 8); SILE_FENCE;
+    }
+    if constexpr (kFinal) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) mma(ya, yb, r, 0, 8);
+      return;
+    }
+    // tail: MFMA Y(ks) rows 0..3
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      SILE_FENCE; mma(ya, yb, r, 0, 6); SILE_FENCE;
+      load_next();
+      SILE_FENCE; mma(ya, yb, r, 6, 8); SILE_FENCE;
+    }
+    // B of ks + 1 (and A of ks + 1, loaded a k-step earlier) landed: only the
+    // 8 loads of A of ks + 2 may still be in flight
+    if constexpr (kLoadA)
+      __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));
+    else
+      __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
+    __builtin_amdgcn_s_barrier();
+    SILE_FENCE;
+  };
+#undef SILE_FENCE
+
+  // prologue: A of 0 -> slot 0, B of 0 -> slot 1, A of 1 -> slot 2; Y(-1) is zero
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load(false, 0, 0, i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load(true, 0, 1, i);
+  if (last >= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load(false, 1, 2, i);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ya[i] = yb[i] = u32x4{0u, 0u, 0u, 0u};
+  if (last >= 1)
+    __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));   // A and B of 0 landed
+  else
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
+  __builtin_amdgcn_s_barrier();
+  int ks = 0, c0 = 0;
+  for (; ks + 2 <= last; ++ks) {
+    iteration(ks, c0, std::true_type{}, std::true_type{}, std::false_type{});
+    c0 = mod5(c0 + 2);
+  }
+  if (ks + 1 == last) {
+    iteration(ks, c0, std::true_type{}, std::false_type{}, std::false_type{});
+    c0 = mod5(c0 + 2);
+    ++ks;
+  }
+  iteration(ks, c0, std::false_type{}, std::false_type{}, std::true_type{});
+
+  // the last MFMAs' results are read below: wait states the compiler cannot
+  // insert for instructions it does not see (32 > what a 16x16x32 needs)
+  asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
+  // ---- epilogue: acc[i][j] register r = C[m = 16 j + l % 16][n = 16 i + 4 (l / 16) + r] ----
+  if constexpr (kOut != kOutF32) {
+    __syncthreads();   // every wave is done reading the ring
+    stage_and_store_c<kOut>(C, g.ldc, p.row0 + wm * 128, p.col0 + wn * 128,
+                            smem + wave * kCStageB, [&](auto put) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          f32x4 v = acc[i][j];
+          if (g.alpha != 1.0f) v *= g.alpha;
+          put(16 * j + (lane & 15), 16 * i + 4 * (lane >> 4), v);
+        }
+    });
+  } else {
+    const int64_t m_base = p.row0 + wm * 128 + (lane & 15);
+    const int64_t n_base = p.col0 + wn * 128 + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        f32x4 v = acc[i][j];
+        if (g.alpha != 1.0f) v *= g.alpha;
+        store_c4<kOut>(C, (m_base + 16 * j) * g.ldc + n_base + 16 * i, v);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp8 e4m3 operands: v_mfma_f32_32x32x64_f8f6f4 through 2 LDS stages.
+//
+// A wave's 128 x 128 is 4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (256 fp32
+// accumulators per lane; unscaled: zero scale operands select the plain
+// instruction).  The MFMA is issued with the B fragment first, so
+// accumulator register r of lane l is C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4]
+// of its block.  (The body is written for 16-bit operands too, on
+// v_mfma_f32_32x32x16_{bf16,f16}.)  A stage (64 KiB) holds one k-step of A
+// and B; there are 2.
+//
+// A k-step is kSubs sub-steps of one MFMA depth (2 of 64 for fp8, 4 of 16 for
+// 16-bit operands) whose fragments (4 A + 4 B blocks per lane: row l % 32 of
+// a block, the kCh 16-byte chunks kCh (2 sub + l / 32) + h of the row, kCh = 2
+// for fp8 and 1 for 16-bit) alternate between register sets X (even
+// sub-steps) and Y (odd).  Iteration ks (stage ks & 1), after the barrier that
+// published k-step ks:
 //   reads X(ks, 0) | tile loads of k-step ks + 1 into the other stage
 //     (spread over the first half) | MFMA of Y(ks - 1, last), second half
 //   MFMA X(0) | reads Y(1);  MFMA Y(1) | reads X(2);  ...
@@ -99,8 +428,6 @@ SILE_DEV f32x16 mma32x32(const u32x4* a, const u32x4* b, f32x16 c) {
 // count ends with a half k-step whose second half multiplies zero fragments.
 // ---------------------------------------------------------------------------
 namespace k64 {
-constexpr int kRowB = 128;                       // bytes of a tile row per k-step
-constexpr int kTileB = 256 * kRowB;              // 32 KiB per operand
 constexpr int kStageB = 2 * kTileB;              // A + B
 constexpr int kStages = 2;
 }  // namespace k64
@@ -118,38 +445,10 @@ __device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- XCD-aware tile order: workgroups go round-robin to the 8 XCDs; each
-  // XCD gets a contiguous range of tiles, grouped 8 tile-rows at a time ----
-  const int num_tiles = g.tiles_m * g.tiles_n;
-  const int bid = blockIdx.x;
-  int lin = bid;
-  if ((num_tiles & 7) == 0) lin = (bid & 7) * (num_tiles >> 3) + (bid >> 3);
-  constexpr int kGroupM = 8;
-  const int group_size = kGroupM * g.tiles_n;
-  const int group = lin / group_size;
-  const int first_m = group * kGroupM;
-  const int rows_in_group = min(g.tiles_m - first_m, kGroupM);
-  const int in_group = lin - group * group_size;
-  const int tile_m = first_m + in_group % rows_in_group;
-  const int tile_n = in_group / rows_in_group;
-  // First row / column of the tile.  When M or N is not a multiple of 256 the
-  // last tile is moved back to end at M / N, so every load stays inside the
-  // operands; the rows or columns it shares with its neighbour are computed
-  // in the same order by both workgroups and written with the same values.
-  const int64_t row0 = min(tile_m * kBM, g.m - kBM), col0 = min(tile_n * kBN, g.n - kBN);
-
-  const int a_rs = (int)(g.lda * kEB), b_rs = (int)(g.ldb * kEB);
-  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A + row0 * a_rs), (short)0, kBM * a_rs, 0x00020000);
-  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(B + col0 * b_rs), (short)0, kBN * b_rs, 0x00020000);
-  // DMA: one instruction fills 1 KiB = 8 rows of 128 bytes; wave w's
-  // instruction i (0..7) fills rows 8 (4 i + w) + (lane >> 3), position
-  // lane & 7, whose chunk is (lane & 7) ^ ((row >> 1) & 7) with
-  // (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3) for every i.
-  const int dma_row = 8 * wave + (lane >> 3);
-  const int dma_chunk = (lane & 7) ^ (((wave & 1) << 2) | ((lane >> 4) & 3));
-  const int a_voff = dma_row * a_rs + dma_chunk * 16, b_voff = dma_row * b_rs + dma_chunk * 16;
+  const TilePlan p = plan_tile<kEB>(A, B, g, wave, lane);
+  const __amdgpu_buffer_rsrc_t a_rsrc = p.a_rsrc, b_rsrc = p.b_rsrc;
+  const int a_rs = p.a_rs, b_rs = p.b_rs, a_voff = p.a_voff, b_voff = p.b_voff;
+  const int64_t row0 = p.row0, col0 = p.col0;
 
   const int fr_row = lane & 31, fr_g = lane >> 5;
   const int fr_swz = (fr_row >> 1) & 7;  // fragment rows differ by multiples of 32
@@ -291,37 +590,65 @@ __device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
   }
   iteration(ks, ks & 1, std::true_type{});
 
-  // ---- epilogue ----
-  const int64_t m_base = row0 + wm * 128 + (lane & 31);
-  const int64_t n_base = col0 + wn * 128 + 4 * (lane >> 5);
+  // ---- epilogue: acc[i][j] register 4 rg + e = C[m = 32 j + l % 32][n = 32 i + 8 rg + 4 (l / 32) + e] ----
+  if constexpr (kOut != kOutF32) {
+    __syncthreads();   // every wave is done reading the stages
+    stage_and_store_c<kOut>(C, g.ldc, row0 + wm * 128, col0 + wn * 128,
+                            smem + wave * kCStageB, [&](auto put) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        f32x4 v = {acc[i][j][4 * rg], acc[i][j][4 * rg + 1], acc[i][j][4 * rg + 2],
-                   acc[i][j][4 * rg + 3]};
-        if (g.alpha != 1.0f) v *= g.alpha;
-        store_c4<kOut>(C, (m_base + 32 * j) * g.ldc + n_base + 32 * i + 8 * rg, v);
-      }
+          for (int rg = 0; rg < 4; ++rg) {
+            f32x4 v = {acc[i][j][4 * rg], acc[i][j][4 * rg + 1], acc[i][j][4 * rg + 2],
+                       acc[i][j][4 * rg + 3]};
+            if (g.alpha != 1.0f) v *= g.alpha;
+            put(32 * j + (lane & 31), 32 * i + 8 * rg + 4 * (lane >> 5), v);
+          }
+    });
+  } else {
+    const int64_t m_base = row0 + wm * 128 + (lane & 31);
+    const int64_t n_base = col0 + wn * 128 + 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          f32x4 v = {acc[i][j][4 * rg], acc[i][j][4 * rg + 1], acc[i][j][4 * rg + 2],
+                     acc[i][j][4 * rg + 3]};
+          if (g.alpha != 1.0f) v *= g.alpha;
+          store_c4<kOut>(C, (m_base + 32 * j) * g.ldc + n_base + 32 * i + 8 * rg, v);
+        }
+  }
 }
 
 }  // namespace
 
+#define SILE_GEMM16_KERNEL(NAME, KIND, OUT)                                                   \
+  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
+                                                            void* C, GemmArgs g) {             \
+    static_assert(4 * kCStageB <= 5 * kTileB, "staged C fits the ring");                     \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[5 * kTileB];                       \
+    gemm_ring16_body<KIND, OUT>(static_cast<const uint8_t*>(A),                               \
+                                static_cast<const uint8_t*>(B), C, g, smem);                  \
+  }
 #define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                     \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
                                                             void* C, GemmArgs g) {             \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[k64::kStages * k64::kStageB];      \
+    constexpr int kLds = k64::kStages * k64::kStageB > 4 * kCStageB                           \
+                             ? k64::kStages * k64::kStageB : 4 * kCStageB;                    \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];                             \
     gemm_k64_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),   \
                              C, g, smem);                                                      \
   }
 
 // k_steps counts half k-steps: 32 elements (16-bit) or 64 (fp8)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
+SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
+SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
+SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 
