@@ -7,9 +7,9 @@
 // This is the tile op `MmaF` of the canonical matmul
 // (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444) on the
 // matrix cores; k runs over K' = (K / bk) * bk as there, which the host
-// resolves before launch.  bf16 / f16 operands run on gemm_ring16_body
-// (16 x 16 MFMA blocks, a ring of 5 LDS tiles), fp8 e4m3 on gemm_k64_body
-// (32 x 32 blocks, 2 LDS stages); their designs are described above them.  sile_gemm_f32_exact_{nn,nt}_t{128,64,32}
+// resolves before launch.  One body (gemm_ring_body) serves bf16, f16 (16 x 16
+// MFMA blocks) and fp8 e4m3 (32 x 32 blocks) operands through a ring of 5
+// LDS tiles; its design is described above it.  sile_gemm_f32_exact_{nn,nt}_t{128,64,32}
 // are the fp32 path in the canonical order (bit-identical to the CPU backend).
 #include <type_traits>
 
@@ -24,16 +24,18 @@ constexpr int kBM = 256, kBN = 256;
 enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
 enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
 
+// C is written once and not read back by the kernel: non-temporal stores
+// (streaming; 2-3 % faster for the staged 16-bit C than plain stores).
 template <int kOut>
 SILE_DEV void store_c4(void* C, int64_t idx, f32x4 v) {
   if constexpr (kOut == kOutF32) {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx) = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx));
   } else if constexpr (kOut == kOutBF16) {
-    u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx) = w;
+    const u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx));
   } else {
-    u32x2 w = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
-    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx) = w;
+    const u32x2 w = {pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx));
   }
 }
 
@@ -46,28 +48,19 @@ struct GemmArgs {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// One 32 x 32 output block: v_mfma_f32_32x32x16_{bf16,f16} on one 16-byte
-// chunk per lane, or v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3, zero scale
-// operands: the unscaled instruction) on two.
-template <int kKind>
-SILE_DEV f32x16 mma32x32(const u32x4* a, const u32x4* b, f32x16 c) {
-  if constexpr (kKind == kBF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
-                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
-  } else if constexpr (kKind == kF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
-                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
-  } else {
-    const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
-                      (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
-    const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
-                      (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
-  }
+// One 32 x 32 output block over 64 k of fp8 e4m3: v_mfma_f32_32x32x64_f8f6f4
+// on two 16-byte chunks per lane (e4m3 x e4m3, zero scale operands: the
+// unscaled instruction).
+SILE_DEV f32x16 mma32x32_fp8(const u32x4* a, const u32x4* b, f32x16 c) {
+  const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
+                    (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
+  const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                    (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
-// Tile placement, shared by both bodies.
+// Tile placement.
 //
 // 256 x 256 output tile per workgroup of 4 waves (2 x 2, 128 x 128 per wave).
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
@@ -174,73 +167,87 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 #pragma unroll 8
     for (int t = 0; t < 32; ++t) {
       const int row = 4 * t + lg;
-      *reinterpret_cast<u32x4*>(cbase + row * ldc + lr * 8) =
-          *reinterpret_cast<const u32x4*>(cst + row * kCRowB + lr * 16);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(cst + row * kCRowB + lr * 16),
+                                  reinterpret_cast<u32x4*>(cbase + row * ldc + lr * 8));
     }
   } else {
     const int lr = lane & 31, lg = lane >> 5;
 #pragma unroll 8
     for (int t = 0; t < 64; ++t) {
       const int row = 2 * t + lg;
-      *reinterpret_cast<u32x2*>(cbase + row * ldc + lr * 4) =
-          *reinterpret_cast<const u32x2*>(cst + row * kCRowB + lr * 8);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x2*>(cst + row * kCRowB + lr * 8),
+                                  reinterpret_cast<u32x2*>(cbase + row * ldc + lr * 4));
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// bf16 / f16 operands: v_mfma_f32_16x16x32 through a ring of 5 LDS tiles.
+// The GEMM body: a ring of 5 LDS tiles, tile loads spread over the k-step.
 //
-// A wave's 128 x 128 is 8 x 8 blocks of v_mfma_f32_16x16x32_{bf16,f16} (256
-// fp32 accumulators per lane).  The MFMA is issued with the B fragment first,
-// so accumulator register r of lane l is C[m = l % 16][n = 4 (l / 16) + r] of
-// its block.  A k-step (64 elements) is two sub-steps of 32; a fragment is row
-// l % 16 of a 16-row block, chunk 4 sub + l / 16.  Sub-step 0's fragments go to
-// register set X, sub-step 1's to Y.
+// A wave's 128 x 128 is kNB x kNB blocks of one MFMA (256 fp32 accumulators
+// per lane):
+//   bf16 / f16: 8 x 8 blocks of v_mfma_f32_16x16x32_{bf16,f16};
+//   fp8 e4m3:   4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (unscaled: zero
+//               scale operands select the plain instruction).
+// The MFMA is issued with the B fragment first, so accumulator register r of
+// lane l is C[m = l % 16][n = 4 (l / 16) + r] of a 16 x 16 block and
+// C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of a 32 x 32 block.  A
+// k-step (128 bytes of a row: 64 16-bit or 128 fp8 elements) is two
+// sub-steps of one MFMA depth; a fragment is row l % kBlk of a block, the kCh
+// 16-byte chunks 4 sub + kCh (l / kBlk) + h of the row (kCh = 1 for 16-bit,
+// 2 for fp8).  Sub-step 0's fragments go to register set X, sub-step 1's to Y.
 //
-// LDS holds a ring of 5 operand tiles (160 KiB): k-step ks's A tile is chunk
-// 2 ks and its B tile chunk 2 ks + 1; chunk c sits in slot c % 5.  The barrier
-// that starts k-step ks frees the slots of k-step ks - 1, which receive B of
+// LDS holds a ring of 5 tiles (160 KiB): k-step ks's A tile is chunk 2 ks and
+// its B tile chunk 2 ks + 1; chunk c sits in slot c % 5.  The barrier that
+// starts k-step ks frees the slots of k-step ks - 1, which receive B of
 // ks + 1 and A of ks + 2, so every tile load has one or two k-steps to land
-// and a wave's 16 load instructions of a k-step can be spread evenly over
-// it: one per 8 MFMAs (128 cycles).  (Two 64 KiB stages force the loads into
-// the first half of the k-step, where they fill the load queue and stall the
-// MFMAs issued behind them: 10-13 % slower at 4096^3 and 8192^3.)
+// and a wave's 16 load instructions of a k-step can be spread evenly over it
+// (one per 128 MFMA cycles).  (Two 64 KiB stages force the loads into the
+// first half of the k-step, where they fill the load queue and stall the
+// MFMAs issued behind them: 7-13 % slower.)
 //
 // Iteration ks, after the barrier that published A and B of ks:
-//   phase 0, 4 groups:     MFMA Y(ks - 1) rows 4..7 | reads X(ks)
-//   sub-step 1, 8 groups:  MFMA X(ks) rows 0..7     | reads Y(ks)
-//   tail, 4 groups:        MFMA Y(ks) rows 0..3
+//   phase 0, kNB/2 groups:   MFMA Y(ks - 1) rows kNB/2 .. kNB-1 | reads X(ks)
+//   sub-step 1, kNB groups:  MFMA X(ks) rows 0 .. kNB-1         | reads Y(ks)
+//   tail, kNB/2 groups:      MFMA Y(ks) rows 0 .. kNB/2-1
 //   s_waitcnt (B of ks + 1 landed, A of ks + 2 may be in flight) + s_barrier
-// A group is the 8 MFMAs of one accumulator row with its fragment reads and
-// one tile load at fixed places (2 MFMA, read(s), 2 MFMA, read(s), 2 MFMA,
-// load, 2 MFMA), fenced so the compiler keeps that order; loads 0..7 of a
-// k-step are B of ks + 1, 8..15 A of ks + 2.  k_steps counts half k-steps
-// (32 elements): an odd count ends with a half k-step whose sub-step 1
-// multiplies zero fragments.
+// A group is the kNB MFMAs of one accumulator row in quarters, with the
+// fragment reads and tile loads at fixed places (Q MFMA, reads, Q MFMA,
+// reads, Q MFMA, loads, Q MFMA), fenced so the compiler keeps that order;
+// loads 0..7 of a k-step are B of ks + 1, 8..15 A of ks + 2.  k_steps counts
+// half k-steps (64 bytes of a row): an odd count ends with a half k-step
+// whose sub-step 1 multiplies zero fragments.
 // ---------------------------------------------------------------------------
 template <int kKind, int kOut>
-__device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
-                                                 const uint8_t* __restrict__ B,
-                                                 void* __restrict__ C, const GemmArgs& g,
-                                                 uint8_t* smem) {
-  static_assert(kKind != kFP8, "16-bit operands");
+__device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
+                                               const uint8_t* __restrict__ B,
+                                               void* __restrict__ C, const GemmArgs& g,
+                                               uint8_t* smem) {
+  constexpr bool kIsFP8 = kKind == kFP8;
+  constexpr int kBlk = kIsFP8 ? 32 : 16;      // MFMA block edge
+  constexpr int kNB = 128 / kBlk;             // blocks per wave edge
+  constexpr int kCh = kIsFP8 ? 2 : 1;         // 16-byte chunks per lane per fragment
+  constexpr int kQ = kNB / 4;                 // MFMAs per quarter group
+  constexpr int kLoadsPerGroup = 16 / (2 * kNB);
+  using Acc = std::conditional_t<kIsFP8, f32x16, f32x4>;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const TilePlan p = plan_tile<2>(A, B, g, wave, lane);
+  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2>(A, B, g, wave, lane);
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // LDS-DMA bases in SGPRs
 
-  f32x4 acc[8][8];
+  Acc acc[kNB][kNB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kNB; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < kNB; ++j)
+#pragma unroll
+      for (int r = 0; r < (int)(sizeof(Acc) / 4); ++r) acc[i][j][r] = 0.0f;
 
-  u32x4 xa[8], xb[8], ya[8], yb[8];
+  u32x4 xa[kNB][kCh], xb[kNB][kCh], ya[kNB][kCh], yb[kNB][kCh];
   const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
   const bool half_last = (g.k_steps & 1) != 0;
-  const int f_row = lane & 15, f_grp = lane >> 4;
+  const int f_row = lane % kBlk, f_grp = lane / kBlk;
   const int f_swz = (f_row >> 1) & 7;         // block rows differ by multiples of 16
   const int a_fb = (wm * 128 + f_row) * kRowB, b_fb = (wn * 128 + f_row) * kRowB;
 
@@ -254,19 +261,30 @@ __device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
       __builtin_amdgcn_raw_ptr_buffer_load_lds(p.a_rsrc, (lds_ptr_t)dst, 16, p.a_voff,
                                                i * 32 * p.a_rs + ks * kRowB, 0, 0);
   };
-  // fragment q of sub-step sub: the A block q (q < 8) or the B block q - 8
-  auto read = [&](int sa, int sb, int sub, int q, u32x4 (&fa)[8], u32x4 (&fb)[8]) {
-    const int off = ((4 * sub + f_grp) ^ f_swz) << 4;
-    if (q < 8)
-      fa[q] = *reinterpret_cast<const u32x4*>(smem + sa * kTileB + a_fb + q * 16 * kRowB + off);
-    else
-      fb[q - 8] =
-          *reinterpret_cast<const u32x4*>(smem + sb * kTileB + b_fb + (q - 8) * 16 * kRowB + off);
+  // fragment q of sub-step sub: the A block q (q < kNB) or the B block q - kNB
+  auto read = [&](int sa, int sb, int sub, int q, u32x4 (&fa)[kNB][kCh],
+                  u32x4 (&fb)[kNB][kCh]) {
+#pragma unroll
+    for (int h = 0; h < kCh; ++h) {
+      const int off = ((4 * sub + kCh * f_grp + h) ^ f_swz) << 4;
+      if (q < kNB)
+        fa[q][h] = *reinterpret_cast<const u32x4*>(smem + sa * kTileB + a_fb +
+                                                   q * kBlk * kRowB + off);
+      else
+        fb[q - kNB][h] = *reinterpret_cast<const u32x4*>(smem + sb * kTileB + b_fb +
+                                                         (q - kNB) * kBlk * kRowB + off);
+    }
   };
   // MFMAs of accumulator row i, columns [j0, j1)
-  auto mma = [&](const u32x4 (&fa)[8], const u32x4 (&fb)[8], int i, int j0, int j1) {
+  auto mma = [&](const u32x4 (&fa)[kNB][kCh], const u32x4 (&fb)[kNB][kCh], int i, int j0,
+                 int j1) {
 #pragma unroll
-    for (int j = j0; j < j1; ++j) mma16x16<kKind>(fb[i], fa[j], acc[i][j]);
+    for (int j = j0; j < j1; ++j) {
+      if constexpr (kIsFP8)
+        acc[i][j] = mma32x32_fp8(fb[i], fa[j], acc[i][j]);
+      else
+        mma16x16<kKind>(fb[i][0], fa[j][0], acc[i][j]);
+    }
   };
   auto mod5 = [](int x) { return x >= 5 ? x - 5 : x; };
 #define SILE_FENCE __builtin_amdgcn_sched_barrier(0)
@@ -278,60 +296,58 @@ __device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
     constexpr bool kLoadB = decltype(load_b_c)::value, kLoadA = decltype(load_a_c)::value;
     const int sa = c0, sb = mod5(c0 + 1), lb = mod5(c0 + 3), la = mod5(c0 + 4);
     int n = 0;   // tile loads issued so far in this k-step
-    auto load_next = [&]() {
-      if (n < 8) {
-        if constexpr (kLoadB) load(true, ks + 1, lb, n);
-      } else {
-        if constexpr (kLoadA) load(false, ks + 2, la, n - 8);
-      }
-      ++n;
-    };
-    // phase 0: MFMA Y(ks - 1) rows 4..7 | reads X(ks): 4 per group
+    auto loads = [&]() {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      SILE_FENCE; mma(ya, yb, 4 + r, 0, 2); SILE_FENCE;
-      read(sa, sb, 0, 4 * r, xa, xb);
-      read(sa, sb, 0, 4 * r + 1, xa, xb);
-      SILE_FENCE; mma(ya, yb, 4 + r, 2, 4); SILE_FENCE;
-      read(sa, sb, 0, 4 * r + 2, xa, xb);
-      read(sa, sb, 0, 4 * r + 3, xa, xb);
-      SILE_FENCE; mma(ya, yb, 4 + r, 4, 6); SILE_FENCE;
-      load_next();
-      SILE_FENCE; mma(ya, yb, 4 + r, 6, 8); SILE_FENCE;
-    }
-    // sub-step 1: MFMA X(ks) rows 0..7 | reads Y(ks): 2 per group (A blocks
-    // first: every MFMA of a row needs all of them)
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      SILE_FENCE; mma(xa, xb, r, 0, 2); SILE_FENCE;
-      read(sa, sb, 1, 2 * r, ya, yb);
-      SILE_FENCE; mma(xa, xb, r, 2, 4); SILE_FENCE;
-      read(sa, sb, 1, 2 * r + 1, ya, yb);
-      if constexpr (kFinal) {
-        // a half final k-step: sub-step 1 multiplies zeros (the LDS bytes past
-        // the last 32 elements hold whatever followed them in memory)
-#pragma unroll
-        for (int q = 2 * r; q < 2 * r + 2; ++q) {
-          if (q < 8) ya[q] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[q];
-          else yb[q - 8] = half_last ? u32x4{0u, 0u, 0u, 0u} : yb[q - 8];
+      for (int t = 0; t < kLoadsPerGroup; ++t, ++n) {
+        if (n < 8) {
+          if constexpr (kLoadB) load(true, ks + 1, lb, n);
+        } else {
+          if constexpr (kLoadA) load(false, ks + 2, la, n - 8);
         }
       }
-      SILE_FENCE; mma(xa, xb, r, 4, 6); SILE_FENCE;
-      load_next();
-      SILE_FENCE; mma(xa, xb, r, 6, 8); SILE_FENCE;
+    };
+    // one group: row i of (fa, fb), reading fragments [q0, q0 + nq) of
+    // sub-step sub into (ra, rb) in two halves
+    auto group = [&](const u32x4 (&fa)[kNB][kCh], const u32x4 (&fb)[kNB][kCh], int i,
+                     int sub, int q0, int nq, u32x4 (&ra)[kNB][kCh], u32x4 (&rb)[kNB][kCh]) {
+      SILE_FENCE; mma(fa, fb, i, 0, kQ); SILE_FENCE;
+#pragma unroll
+      for (int q = q0; q < q0 + nq / 2; ++q) read(sa, sb, sub, q, ra, rb);
+      SILE_FENCE; mma(fa, fb, i, kQ, 2 * kQ); SILE_FENCE;
+#pragma unroll
+      for (int q = q0 + nq / 2; q < q0 + nq; ++q) read(sa, sb, sub, q, ra, rb);
+      SILE_FENCE; mma(fa, fb, i, 2 * kQ, 3 * kQ); SILE_FENCE;
+      loads();
+      SILE_FENCE; mma(fa, fb, i, 3 * kQ, kNB); SILE_FENCE;
+    };
+    // phase 0: MFMA Y(ks - 1) rows kNB/2 .. kNB-1 | reads X(ks), 4 fragments a group
+#pragma unroll
+    for (int r = 0; r < kNB / 2; ++r) group(ya, yb, kNB / 2 + r, 0, 4 * r, 4, xa, xb);
+    // sub-step 1: MFMA X(ks) | reads Y(ks), 2 fragments a group (A blocks
+    // first: every MFMA of a row needs all of them)
+#pragma unroll
+    for (int r = 0; r < kNB; ++r) {
+      group(xa, xb, r, 1, 2 * r, 2, ya, yb);
+      if constexpr (kFinal) {
+        // a half final k-step: sub-step 1 multiplies zeros (the LDS bytes past
+        // the last half k-step hold whatever followed it in memory)
+#pragma unroll
+        for (int q = 2 * r; q < 2 * r + 2; ++q)
+#pragma unroll
+          for (int h = 0; h < kCh; ++h) {
+            if (q < kNB) ya[q][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[q][h];
+            else yb[q - kNB][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : yb[q - kNB][h];
+          }
+      }
     }
     if constexpr (kFinal) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) mma(ya, yb, r, 0, 8);
+      for (int r = 0; r < kNB; ++r) mma(ya, yb, r, 0, kNB);
       return;
     }
-    // tail: MFMA Y(ks) rows 0..3
+    // tail: MFMA Y(ks) rows 0 .. kNB/2-1
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      SILE_FENCE; mma(ya, yb, r, 0, 6); SILE_FENCE;
-      load_next();
-      SILE_FENCE; mma(ya, yb, r, 6, 8); SILE_FENCE;
-    }
+    for (int r = 0; r < kNB / 2; ++r) group(ya, yb, r, 1, 0, 0, ya, yb);
     // B of ks + 1 (and A of ks + 1, loaded a k-step earlier) landed: only the
     // 8 loads of A of ks + 2 may still be in flight
     if constexpr (kLoadA)
@@ -353,7 +369,9 @@ __device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
     for (int i = 0; i < 8; ++i) load(false, 1, 2, i);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ya[i] = yb[i] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < kNB; ++i)
+#pragma unroll
+    for (int h = 0; h < kCh; ++h) ya[i][h] = yb[i][h] = u32x4{0u, 0u, 0u, 0u};
   if (last >= 1)
     __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));   // A and B of 0 landed
   else
@@ -371,284 +389,56 @@ __device__ __forceinline__ void gemm_ring16_body(const uint8_t* __restrict__ A,
   }
   iteration(ks, c0, std::false_type{}, std::false_type{}, std::true_type{});
 
-  // the last MFMAs' results are read below: wait states the compiler cannot
-  // insert for instructions it does not see (32 > what a 16x16x32 needs)
-  asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
-  // ---- epilogue: acc[i][j] register r = C[m = 16 j + l % 16][n = 16 i + 4 (l / 16) + r] ----
-  if constexpr (kOut != kOutF32) {
-    __syncthreads();   // every wave is done reading the ring
-    stage_and_store_c<kOut>(C, g.ldc, p.row0 + wm * 128, p.col0 + wn * 128,
-                            smem + wave * kCStageB, [&](auto put) {
+  // the 16 x 16 MFMAs are opaque to the compiler (inline assembly): pad the
+  // wait states before their results are read (32 > what a 16x16x32 needs)
+  if constexpr (!kIsFP8) asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
+  // ---- epilogue: calls f(row, col, v) for the 4 consecutive columns of each
+  // accumulator register group (row, col within the wave's 128 x 128) ----
+  auto each_c4 = [&](auto f) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kNB; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          f32x4 v = acc[i][j];
-          if (g.alpha != 1.0f) v *= g.alpha;
-          put(16 * j + (lane & 15), 16 * i + 4 * (lane >> 4), v);
-        }
-    });
-  } else {
-    const int64_t m_base = p.row0 + wm * 128 + (lane & 15);
-    const int64_t n_base = p.col0 + wn * 128 + 4 * (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        f32x4 v = acc[i][j];
-        if (g.alpha != 1.0f) v *= g.alpha;
-        store_c4<kOut>(C, (m_base + 16 * j) * g.ldc + n_base + 16 * i, v);
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// fp8 e4m3 operands: v_mfma_f32_32x32x64_f8f6f4 through 2 LDS stages.
-//
-// A wave's 128 x 128 is 4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (256 fp32
-// accumulators per lane; unscaled: zero scale operands select the plain
-// instruction).  The MFMA is issued with the B fragment first, so
-// accumulator register r of lane l is C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4]
-// of its block.  (The body is written for 16-bit operands too, on
-// v_mfma_f32_32x32x16_{bf16,f16}.)  A stage (64 KiB) holds one k-step of A
-// and B; there are 2.
-//
-// A k-step is kSubs sub-steps of one MFMA depth (2 of 64 for fp8, 4 of 16 for
-// 16-bit operands) whose fragments (4 A + 4 B blocks per lane: row l % 32 of
-// a block, the kCh 16-byte chunks kCh (2 sub + l / 32) + h of the row, kCh = 2
-// for fp8 and 1 for 16-bit) alternate between register sets X (even
-// sub-steps) and Y (odd).  Iteration ks (stage ks & 1), after the barrier that
-// published k-step ks:
-//   reads X(ks, 0) | tile loads of k-step ks + 1 into the other stage
-//     (spread over the first half) | MFMA of Y(ks - 1, last), second half
-//   MFMA X(0) | reads Y(1);  MFMA Y(1) | reads X(2);  ...
-//   MFMA Y(last), first half;  s_waitcnt (loads landed, reads done) + s_barrier
-// so the fragment reads after each barrier are covered by 8 MFMAs of the
-// previous k-step.  k_steps counts half k-steps (64 bytes of a row): an odd
-// count ends with a half k-step whose second half multiplies zero fragments.
-// ---------------------------------------------------------------------------
-namespace k64 {
-constexpr int kStageB = 2 * kTileB;              // A + B
-constexpr int kStages = 2;
-}  // namespace k64
-
-template <int kKind, int kOut>
-__device__ __forceinline__ void gemm_k64_body(const uint8_t* __restrict__ A,
-                                                const uint8_t* __restrict__ B,
-                                                void* __restrict__ C, const GemmArgs& g,
-                                                uint8_t* smem) {
-  using namespace k64;
-  constexpr int kEB = kKind == kFP8 ? 1 : 2;   // bytes per element
-  constexpr int kCh = kKind == kFP8 ? 2 : 1;   // 16-byte chunks per lane per MFMA
-  constexpr int kSubs = 4 / kCh;               // MFMA depths per 128-byte k-step
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const TilePlan p = plan_tile<kEB>(A, B, g, wave, lane);
-  const __amdgpu_buffer_rsrc_t a_rsrc = p.a_rsrc, b_rsrc = p.b_rsrc;
-  const int a_rs = p.a_rs, b_rs = p.b_rs, a_voff = p.a_voff, b_voff = p.b_voff;
-  const int64_t row0 = p.row0, col0 = p.col0;
-
-  const int fr_row = lane & 31, fr_g = lane >> 5;
-  const int fr_swz = (fr_row >> 1) & 7;  // fragment rows differ by multiples of 32
-  const int a_frag_base = (wm * 128 + fr_row) * kRowB;
-  const int b_frag_base = kTileB + (wn * 128 + fr_row) * kRowB;
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  u32x4 xa[4][kCh], xb[4][kCh], ya[4][kCh], yb[4][kCh];
-  const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
-  const bool half_last = (g.k_steps & 1) != 0;
-
-  // tile loads of k-step ks into stage: instructions [i0, i1) per operand
-  auto dload = [&](int ks, int stage, int i0, int i1) {
-    const int koff = ks * kRowB;
-    uint8_t* base = smem + stage * kStageB + wave * 1024;
-#pragma unroll
-    for (int i = i0; i < i1; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_ptr_t)(base + i * 4096), 16, a_voff,
-                                               i * 32 * a_rs + koff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_ptr_t)(base + kTileB + i * 4096),
-                                               16, b_voff, i * 32 * b_rs + koff, 0, 0);
-    }
-  };
-  auto fread = [&](int stage, int sub, u32x4 (&fa)[4][kCh], u32x4 (&fb)[4][kCh]) {
-    const uint8_t* sbase = smem + stage * kStageB;
-#pragma unroll
-    for (int h = 0; h < kCh; ++h) {
-      const int off = ((kCh * (2 * sub + fr_g) + h) ^ fr_swz) << 4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i][h] = *reinterpret_cast<const u32x4*>(sbase + a_frag_base + i * 32 * kRowB + off);
-        fb[i][h] = *reinterpret_cast<const u32x4*>(sbase + b_frag_base + i * 32 * kRowB + off);
-      }
-    }
-  };
-  // MFMAs of one sub-step on accumulator rows [i0, i1) (B-fragment index)
-  auto mma = [&](const u32x4 (&fa)[4][kCh], const u32x4 (&fb)[4][kCh], int i0, int i1) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mma32x32<kKind>(fb[i], fa[j], acc[i][j]);
-  };
-  // issue order of a phase of kM MFMAs with kD fragment reads and kV loads
-  auto order = [&](auto m_c, auto d_c, auto v_c) {
-    constexpr int kM = decltype(m_c)::value, kD = decltype(d_c)::value,
-                  kV = decltype(v_c)::value;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, kM / 8, 0);
-      if constexpr (kD > 0) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, kD / 4, 0);
-      __builtin_amdgcn_sched_group_barrier(sched::kMfma, kM / 8, 0);
-      if constexpr (kV > 0) __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, kV / 4, 0);
-    }
-  };
-  using I0 = std::integral_constant<int, 0>;
-  using I8 = std::integral_constant<int, 8>;
-  using I16 = std::integral_constant<int, 16>;
-  using IR = std::integral_constant<int, 8 * kCh>;  // fragment reads per sub-step
-
-  // One k-step in stage st (a compile-time constant in the main loop, a
-  // runtime value in the final k-step).  kFinal: no next k-step (no loads, no
-  // barrier; a half k-step when half_last).
-  auto iteration = [&](int ks, auto stage_c, auto final_c) {
-    constexpr bool kFinal = decltype(final_c)::value;
-    const int st = stage_c;
-    // X(ks, 0), loads of ks + 1 (first half), Y(ks - 1, last) second half
-    fread(st, 0, xa, xb);
-    if constexpr (!kFinal) dload(ks + 1, st ^ 1, 0, 4);
-    mma(ya, yb, 2, 4);
-    __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 8 * kCh, 0);
-    order(I8{}, I0{}, std::integral_constant<int, kFinal ? 0 : 8>{});
-    __builtin_amdgcn_sched_barrier(0);
-    // sub-steps 1 .. kSubs - 1: MFMA of sub - 1 | reads of sub (| the second
-    // half of the loads with sub 1).  A half final k-step multiplies zeros in
-    // its second half (the LDS bytes past the last half k-step hold whatever
-    // followed it in memory).
-#pragma unroll
-    for (int sub = 1; sub < kSubs; ++sub) {
-      auto& ra = (sub & 1) ? ya : xa;
-      auto& rb = (sub & 1) ? yb : xb;
-      const auto& pa = (sub & 1) ? xa : ya;
-      const auto& pb = (sub & 1) ? xb : yb;
-      if (sub == 1 && !kFinal) dload(ks + 1, st ^ 1, 4, 8);
-      fread(st, sub, ra, rb);
-      if (kFinal && sub >= kSubs / 2) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int h = 0; h < kCh; ++h) {
-            ra[i][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : ra[i][h];
-            rb[i][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : rb[i][h];
-          }
-      }
-      mma(pa, pb, 0, 4);
-      if (sub == 1 && !kFinal)
-        order(I16{}, IR{}, I8{});
-      else
-        order(I16{}, IR{}, I0{});
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (kFinal) {
-      mma(ya, yb, 0, 4);
-      return;
-    }
-    // MFMA Y(last), first half (kept above the wait); then every load of
-    // ks + 1 landed and every read done
-    mma(ya, yb, 0, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  // prologue: k-step 0 into stage 0; Y(-1, 3) is zero
-  dload(0, 0, 0, 8);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int h = 0; h < kCh; ++h) ya[i][h] = yb[i][h] = u32x4{0u, 0u, 0u, 0u};
-  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));  // own loads landed
-  __builtin_amdgcn_s_barrier();
-  int ks = 0;
-  for (; ks + 2 <= last; ks += 2) {
-    iteration(ks, S0{}, std::false_type{});
-    iteration(ks + 1, S1{}, std::false_type{});
-  }
-  if (ks < last) {
-    iteration(ks, S0{}, std::false_type{});
-    ++ks;
-  }
-  iteration(ks, ks & 1, std::true_type{});
-
-  // ---- epilogue: acc[i][j] register 4 rg + e = C[m = 32 j + l % 32][n = 32 i + 8 rg + 4 (l / 32) + e] ----
-  if constexpr (kOut != kOutF32) {
-    __syncthreads();   // every wave is done reading the stages
-    stage_and_store_c<kOut>(C, g.ldc, row0 + wm * 128, col0 + wn * 128,
-                            smem + wave * kCStageB, [&](auto put) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kNB; ++j) {
+        if constexpr (kIsFP8) {
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
             f32x4 v = {acc[i][j][4 * rg], acc[i][j][4 * rg + 1], acc[i][j][4 * rg + 2],
                        acc[i][j][4 * rg + 3]};
             if (g.alpha != 1.0f) v *= g.alpha;
-            put(32 * j + (lane & 31), 32 * i + 8 * rg + 4 * (lane >> 5), v);
+            f(32 * j + (lane & 31), 32 * i + 8 * rg + 4 * (lane >> 5), v);
           }
-    });
-  } else {
-    const int64_t m_base = row0 + wm * 128 + (lane & 31);
-    const int64_t n_base = col0 + wn * 128 + 4 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          f32x4 v = {acc[i][j][4 * rg], acc[i][j][4 * rg + 1], acc[i][j][4 * rg + 2],
-                     acc[i][j][4 * rg + 3]};
+        } else {
+          f32x4 v = acc[i][j];
           if (g.alpha != 1.0f) v *= g.alpha;
-          store_c4<kOut>(C, (m_base + 32 * j) * g.ldc + n_base + 32 * i + 8 * rg, v);
+          f(16 * j + (lane & 15), 16 * i + 4 * (lane >> 4), v);
         }
+      }
+  };
+  const int64_t m0 = p.row0 + wm * 128, n0 = p.col0 + wn * 128;
+  if constexpr (kOut != kOutF32) {
+    __syncthreads();   // every wave is done reading the ring
+    stage_and_store_c<kOut>(C, g.ldc, m0, n0, smem + wave * kCStageB, each_c4);
+  } else {
+    each_c4([&](int row, int col, f32x4 v) { store_c4<kOut>(C, (m0 + row) * g.ldc + n0 + col, v); });
   }
 }
 
 }  // namespace
 
-#define SILE_GEMM16_KERNEL(NAME, KIND, OUT)                                                   \
+#define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                     \
   extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
                                                             void* C, GemmArgs g) {             \
     static_assert(4 * kCStageB <= 5 * kTileB, "staged C fits the ring");                     \
     __shared__ __attribute__((aligned(1024))) uint8_t smem[5 * kTileB];                       \
-    gemm_ring16_body<KIND, OUT>(static_cast<const uint8_t*>(A),                               \
-                                static_cast<const uint8_t*>(B), C, g, smem);                  \
-  }
-#define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                     \
-  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
-                                                            void* C, GemmArgs g) {             \
-    constexpr int kLds = k64::kStages * k64::kStageB > 4 * kCStageB                           \
-                             ? k64::kStages * k64::kStageB : 4 * kCStageB;                    \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];                             \
-    gemm_k64_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),   \
-                             C, g, smem);                                                      \
+    gemm_ring_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),  \
+                              C, g, smem);                                                     \
   }
 
 // k_steps counts half k-steps: 32 elements (16-bit) or 64 (fp8)
-SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
-SILE_GEMM16_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
-SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
-SILE_GEMM16_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 
