@@ -188,7 +188,9 @@ def test_ragged_m_n(hip, kind, out, m, n, k):
     """M and N that are not multiples of the 256 x 256 tile: the last tile row /
     column is computed from rows / columns M - 256 / N - 256 on.  Every
     element is checked; C sits in a wider pitch whose columns past N must keep
-    their fill."""
+    their fill.  With N % 8 == 4 (all three N here) the last column tile's rows
+    start 8 bytes off a 16-byte boundary, so its 16-bit C is written back with
+    the 8-byte stores, the other tiles' with 16-byte stores."""
     if kind == "fp8" and k % 64:
         pytest.skip("fp8 K' is a multiple of 64")
     ldc = n + 12
@@ -262,3 +264,4 @@ def test_bf16_gemm_config3_sampled(hip, size):
     assert rows.sum() == 4 * 256
     assert_close(got[rows], ref[rows], atol=ATOL, rtol=RTOL, what="bf16 4096 sampled")
     assert np.isfinite(got).all()
+
