@@ -452,9 +452,11 @@ SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 // bit for bit as the CPU backend's.  The work is organised as T x T outputs
 // per workgroup of 256 threads (T = 128, 64 or 32: the largest that still gives
 // ~1024 workgroups), (T/16) x (T/16) independent chains per thread, operands staged in LDS
-// in 16-deep k-tiles (64 for T = 32; double-buffered), A and a column-major B transposed on
-// the way in so a thread reads its 8 rows / 8 columns of one k as two 16-byte
-// LDS reads.  Outside M, N and K' the staged values are zero: a padded term
+// in 16-deep k-tiles (64 for T = 32; double-buffered in LDS, with the global
+// loads issued two k-tiles ahead into two register sets, 16-byte loads where a
+// thread's run of a row is inside the operand), A and a column-major B
+// transposed on the way in so a thread reads its 8 rows / 8 columns of one k as
+// two 16-byte LDS reads.  Outside M, N and K' the staged values are zero: a padded term
 // adds +0.0f, which leaves every sum unchanged (a sum that starts at +0.0f
 // and adds products never becomes -0.0f).
 namespace f32t {
@@ -487,31 +489,58 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
   const int la_r = t / (kK / kL), la_k = (t % (kK / kL)) * kL;
   const int lb_r = kBCol ? la_r : t / (kT / kL);
   const int lb_c = kBCol ? la_k : (t % (kT / kL)) * kL;
-  float ra[kL], rb[kL];
-  auto gload = [&](int64_t k0) {
+  float ra_s[2][kL], rb_s[2][kL];
+  // whole rows of 16-byte vectors: A (and a column-major B) rows start 16-byte aligned
+  const bool vec_a = (lda & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 && kL % 4 == 0;
+  const bool vec_b = (ldb & 3) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0 && kL % 4 == 0;
+  auto gload = [&](int64_t k0, float (&ra)[kL], float (&rb)[kL]) {
     const int64_t am = m0 + la_r;
+    if (vec_a && am < M && k0 + la_k + kL <= kp) {
 #pragma unroll
-    for (int i = 0; i < kL; ++i) {
-      const int64_t k = k0 + la_k + i;
-      ra[i] = (am < M && k < kp) ? A[am * lda + k] : 0.0f;
+      for (int i = 0; i < kL; i += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(A + am * lda + k0 + la_k + i);
+        ra[i] = v[0]; ra[i + 1] = v[1]; ra[i + 2] = v[2]; ra[i + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kL; ++i) {
+        const int64_t k = k0 + la_k + i;
+        ra[i] = (am < M && k < kp) ? A[am * lda + k] : 0.0f;
+      }
     }
     if constexpr (kBCol) {
       const int64_t bn = n0 + lb_r;
+      if (vec_b && bn < N && k0 + lb_c + kL <= kp) {
 #pragma unroll
-      for (int i = 0; i < kL; ++i) {
-        const int64_t k = k0 + lb_c + i;
-        rb[i] = (bn < N && k < kp) ? B[bn * ldb + k] : 0.0f;
+        for (int i = 0; i < kL; i += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(B + bn * ldb + k0 + lb_c + i);
+          rb[i] = v[0]; rb[i + 1] = v[1]; rb[i + 2] = v[2]; rb[i + 3] = v[3];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) {
+          const int64_t k = k0 + lb_c + i;
+          rb[i] = (bn < N && k < kp) ? B[bn * ldb + k] : 0.0f;
+        }
       }
     } else {
       const int64_t k = k0 + lb_r;
+      if (vec_b && k < kp && n0 + lb_c + kL <= N) {
 #pragma unroll
-      for (int i = 0; i < kL; ++i) {
-        const int64_t bn = n0 + lb_c + i;
-        rb[i] = (bn < N && k < kp) ? B[k * ldb + bn] : 0.0f;
+        for (int i = 0; i < kL; i += 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(B + k * ldb + n0 + lb_c + i);
+          rb[i] = v[0]; rb[i + 1] = v[1]; rb[i + 2] = v[2]; rb[i + 3] = v[3];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) {
+          const int64_t bn = n0 + lb_c + i;
+          rb[i] = (bn < N && k < kp) ? B[k * ldb + bn] : 0.0f;
+        }
       }
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const float (&ra)[kL], const float (&rb)[kL]) {
 #pragma unroll
     for (int i = 0; i < kL; ++i) As[buf][la_k + i][la_r] = ra[i];
     if constexpr (kBCol) {
@@ -544,13 +573,18 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
 
   const int64_t ktiles = (kp + kK - 1) / kK;
   if (ktiles > 0) {
-    gload(0);
-    sstore(0);
+    gload(0, ra_s[0], rb_s[0]);
+    sstore(0, ra_s[0], rb_s[0]);
   }
+  if (ktiles > 1) gload(kK, ra_s[1], rb_s[1]);
   __syncthreads();
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int buf = (int)(kt & 1);
-    if (kt + 1 < ktiles) gload((kt + 1) * kK);
+  // k-tile kt is computed from LDS buffer kt & 1 while the global loads of
+  // k-tile kt + 2 are in flight into register set kt & 1; k-tile kt + 1 (in
+  // set (kt + 1) & 1 since the previous iteration) is stored after the compute
+  auto ktile = [&](int64_t kt, auto set_c) {
+    constexpr int kSet = decltype(set_c)::value;
+    const int buf = kSet;
+    if (kt + 2 < ktiles) gload((kt + 2) * kK, ra_s[kSet], rb_s[kSet]);
     // the 32-wide tile (one wave per SIMD, 4 chains a thread) waits on its
     // LDS reads unless they run several k ahead: unrolled 8 (512^3: 32 -> 21 us);
     // the larger tiles keep 2 (their chains hide the reads, and deeper unrolling
@@ -568,9 +602,15 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
           acc[i][j] = acc[i][j] + p;
         }
     }
-    if (kt + 1 < ktiles) sstore(buf ^ 1);
+    if (kt + 1 < ktiles) sstore(buf ^ 1, ra_s[kSet ^ 1], rb_s[kSet ^ 1]);
     __syncthreads();
+  };
+  int64_t kt = 0;
+  for (; kt + 2 <= ktiles; kt += 2) {
+    ktile(kt, std::integral_constant<int, 0>{});
+    ktile(kt + 1, std::integral_constant<int, 1>{});
   }
+  if (kt < ktiles) ktile(kt, std::integral_constant<int, 0>{});
 #pragma unroll
   for (int i = 0; i < kR; ++i) {
     const int64_t m = m0 + kR * tm + i;
