@@ -14,8 +14,10 @@ events recorded on the launch stream, bracketed by a device synchronisation on
 both sides, after an untimed clock-settle period and the W warmup steps.
 
 `cpu_baseline` times the CPU oracle (a restatement of sile's CPU backend loop
-nest, compiled like the reference's generated C) on a bounded sample of the
-same GEMM workload on this host's cores.
+nest, compiled like the reference's generated C) on the whole bf16 8192^3 GEMM
+on this host's cores; each component carries its own `cpu_baseline` on a
+bounded sample of its workload (whole softmax and 4096^3 GEMM, every 8th row
+tile of the fp8 GEMM, four whole heads of each attention workload).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
                        [--no-cpu-baseline]
@@ -135,7 +137,9 @@ def roofline_obj(bound, achieved, peak, unit, traffic):
 
 # ---------------------------------------------------------------- workloads
 
-def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
+def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0):
+    """cpu_tile_step > 0 also times the CPU oracle on every cpu_tile_step-th
+    256-row tile of C over the same (de)quantised inputs."""
     m = n = k = size
     log(f"[bench] {name}: generating inputs")
     if kind == "fp8":
@@ -155,6 +159,7 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
         sa = sb = 1.0
         t, c_t = hip.BF16, hip.BF16
     da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
+    host = (a_bits, b_bits) if cpu_tile_step else None
     del a_bits, b_bits
     dc = hip.DeviceBuffer(m * n * 2)
 
@@ -170,16 +175,38 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic):
     res["flop_per_launch"] = flop
     for buf in (da, db, dc):
         buf.close()
+    if host is not None:
+        from oracle import cpuref
+        if kind == "fp8":
+            a32, b32 = cpuref.e4m3_decode(host[0], sa), cpuref.e4m3_decode(host[1], sb)
+            what = "dequantised fp32 inputs q*s"
+        else:
+            a32, b32 = cpuref.f32_from_bf16(host[0]), cpuref.f32_from_bf16(host[1])
+            what = "up-cast fp32 inputs"
+        del host
+        c32 = np.zeros((m, n), np.float32)
+        rows = ((m // 256 + cpu_tile_step - 1) // cpu_tile_step) * 256
+        log(f"[bench] {name}: cpu oracle on {rows} of {m} rows")
+        res["cpu_baseline"] = cpu_timed(
+            lambda: cpuref.gemm_nt(a32, b32, bm=256, row_tile_step=cpu_tile_step, out=c32),
+            2.0 * rows * n * k, 1e12, "TFLOP/s",
+            (f"every {cpu_tile_step}th 256-row tile of C ({rows} of {m} rows, all columns, full K)"
+             if cpu_tile_step > 1 else "the whole GEMM")
+            + f" on {what}; canonical-matmul loop nest, gcc -O2 -fopenmp")
     return res
 
 
-def bench_attention(name, s, steps, warmup, stream, traffic):
+def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0):
+    """cpu_heads > 0 also times the CPU oracle on the first cpu_heads (b, h)
+    slices, every query row, causal."""
     b, h, d = 4, 32, 128
     log(f"[bench] {name}: generating inputs")
-    bufs = []
+    bufs, host = [], []
     for seed in (6, 7, 8):
         x = normal(seed, (b, h, s, d)).astype(np.float16)
         bufs.append(hip.DeviceBuffer.from_array(x.view(np.uint16)))
+        if cpu_heads:
+            host.append(x.reshape(b * h, s, d)[:cpu_heads].astype(np.float32))
         del x
     do = hip.DeviceBuffer(b * h * s * d * 2)
     scale = 1.0 / np.sqrt(d)
@@ -198,10 +225,24 @@ def bench_attention(name, s, steps, warmup, stream, traffic):
     res["flop_convention"] = "4*D*B*H*S*(S+1)/2 (causal pairs only)"
     for buf in bufs + [do]:
         buf.close()
+    if cpu_heads:
+        from oracle import cpuref
+        o32 = np.zeros((s, d), np.float32)
+
+        def run():
+            for i in range(cpu_heads):
+                cpuref.attention_fwd(host[0][i], host[1][i], host[2][i], scale, causal=True,
+                                     out=o32)
+
+        log(f"[bench] {name}: cpu oracle on {cpu_heads} of {b * h} heads")
+        res["cpu_baseline"] = cpu_timed(
+            run, flop * cpu_heads / (b * h), 1e12, "TFLOP/s",
+            f"{cpu_heads} of {b * h} (batch, head) slices, every query row, causal, on up-cast "
+            "fp32 Q/K/V; naive fp32 restatement (scores, max, expf, sum, P.V), gcc -O2 -fopenmp")
     return res
 
 
-def bench_softmax(name, steps, warmup, stream, traffic):
+def bench_softmax(name, steps, warmup, stream, traffic, cpu=False):
     rows = cols = 8192
     log(f"[bench] {name}: generating inputs")
     x = normal(3, (rows, cols), 2.0).astype(np.float16)
@@ -210,6 +251,7 @@ def bench_softmax(name, steps, warmup, stream, traffic):
     rotate = 4
     xs = [hip.DeviceBuffer.from_array(x.view(np.uint16)) for _ in range(rotate)]
     ys = [hip.DeviceBuffer(rows * cols * 2) for _ in range(rotate)]
+    x32 = x.astype(np.float32) if cpu else None
     del x
 
     def launch(i):
@@ -223,6 +265,14 @@ def bench_softmax(name, steps, warmup, stream, traffic):
     res["bytes_per_launch"] = nbytes
     for buf in xs + ys:
         buf.close()
+    if x32 is not None:
+        from oracle import cpuref
+        log(f"[bench] {name}: cpu oracle on the whole matrix")
+        res["cpu_baseline"] = cpu_timed(
+            lambda: cpuref.softmax_rows(x32), nbytes, 1e9, "GB/s",
+            "the whole [8192, 8192] softmax on up-cast fp32 input, rated by the fp16 "
+            "workload's algorithmic bytes (4 per element); sequential max / expf / sum / "
+            "divide per row, gcc -O2 -fopenmp")
     return res
 
 
@@ -295,7 +345,7 @@ def bench_tile_ir_softmax(name, steps, warmup):
     return res
 
 
-def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic):
+def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic, cpu=False):
     """fp32 GEMM M=N=K=size in the reference's canonical per-cell order
     (bit-identical to its CPU backend), A and B row-major U(-1,1) (seeds 1/2,
     the recipe of BASELINE config 1).  Every flop is its own instruction (the
@@ -306,6 +356,7 @@ def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic):
     b = np.random.default_rng(2).uniform(-1, 1, size=(n, n)).astype(np.float32)
     da, db = hip.DeviceBuffer.from_array(a), hip.DeviceBuffer.from_array(b)
     dc = hip.DeviceBuffer(n * n * 4)
+    host = (a, b) if cpu else None
     del a, b
 
     def launch(i):
@@ -320,6 +371,15 @@ def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic):
     res["flop_per_launch"] = flop
     for buf in (da, db, dc):
         buf.close()
+    if host is not None:
+        from oracle import cpuref
+        c32 = np.zeros((n, n), np.float32)
+        grid = (n // 32 * (n // 32), 1, 1)
+        log(f"[bench] {name}: cpu oracle, sile_kernel_matmul<32, 32, 32>")
+        res["cpu_baseline"] = cpu_timed(
+            lambda: cpuref.kernel_matmul(host[0], host[1], c32, grid, 32, 32, 32), flop, 1e12,
+            "TFLOP/s", f"the whole {n}^3 GEMM as sile_kernel_matmul with 32x32x32 tiles "
+            "(the reference's program loop and per-cell order), gcc -O2 -fopenmp")
     return res
 
 
@@ -346,6 +406,8 @@ def bench_copy_calibration(name, steps, warmup):
 
 
 COPY_BYTES = 512 << 20
+# (batch, head) slices of the attention workloads the CPU oracle runs in full
+CPU_ATTN_HEADS = 4
 
 
 def cpu_baseline(row_tile_step=1):
@@ -376,6 +438,26 @@ def cpu_baseline(row_tile_step=1):
                    " gcc -O2 -fopenmp"),
         "seconds": round(dt, 3),
     }
+
+
+def cpu_timed(run, work, unit_scale, unit, sample, min_s=1.0):
+    """Times `run()` (a CPU oracle call on this host's cores), repeated until
+    at least `min_s` seconds have passed; returns a cpu_baseline object whose
+    value is `work` (the algorithmic work of one run, in the GPU workload's
+    own unit) per second of one run."""
+    from oracle import cpuref
+
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            break
+    per = dt / reps
+    return {"value": round(work / per / unit_scale, 6), "unit": unit,
+            "cores": cpuref.num_threads(), "kind": "port",
+            "sample": f"{sample}; {reps} run(s), {per:.3f} s each", "seconds": round(dt, 3)}
 
 
 # ---------------------------------------------------------------- PMC traffic
@@ -454,6 +536,7 @@ def main():
     stream = hip.Stream()
     traffic = load_traffic()
     names = args.only or ALL
+    cpu = not args.no_cpu_baseline
     results = {}
     for name in names:
         if name == "copy_calibration":
@@ -463,27 +546,34 @@ def main():
         elif name == "tile_ir_softmax_f32_8192":
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
         elif name.startswith("gemm_f32_exact_"):
-            results[name] = bench_gemm_f32_exact(name, int(name.split("_")[-1]), args.steps,
-                                                 args.warmup, stream, traffic)
+            size = int(name.split("_")[-1])
+            results[name] = bench_gemm_f32_exact(name, size, args.steps, args.warmup, stream,
+                                                 traffic, cpu=cpu and size <= 1024)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
-            results[name] = bench_gemm(name, kind, int(name.split("_")[-1]), args.steps,
-                                       args.warmup, stream, traffic)
+            size = int(name.split("_")[-1])
+            # the bf16 8192^3 GEMM's CPU time is the headline cpu_baseline below
+            step = 0 if not cpu or name == "gemm_bf16_8192" else (8 if size >= 8192 else 1)
+            results[name] = bench_gemm(name, kind, size, args.steps, args.warmup, stream,
+                                       traffic, cpu_tile_step=step)
         elif name.startswith("flash_attn"):
             results[name] = bench_attention(name, int(name.split("_s")[-1]), args.steps,
-                                            args.warmup, stream, traffic)
+                                            args.warmup, stream, traffic,
+                                            cpu_heads=CPU_ATTN_HEADS if cpu else 0)
         else:
-            results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic)
+            results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic,
+                                          cpu=cpu)
         r = results[name]
         frac = r.get("roofline", {}).get("frac")
         log(f"[bench] {name}: {r['value']} {r['unit']} ({r['ms_per_step']} ms/step"
             + (f", {100 * frac:.1f}% of peak)" if frac is not None else ")"))
 
     head = results.get("gemm_bf16_8192") or next(iter(results.values()))
-    cpu = None
-    if not args.no_cpu_baseline and head["name"] == "gemm_bf16_8192":
-        cpu = cpu_baseline()
-        log(f"[bench] cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+    head_cpu = None
+    if cpu and head["name"] == "gemm_bf16_8192":
+        head_cpu = cpu_baseline()
+        head["cpu_baseline"] = head_cpu
+        log(f"[bench] cpu baseline: {head_cpu['value']} TFLOP/s on {head_cpu['cores']} threads")
     workloads = {
         "gemm_bf16_8192": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 acc, bf16 out",
     }
@@ -503,7 +593,7 @@ def main():
         "config": {"workload": workloads.get(head["name"], head["name"]),
                    "parallelism": "single GPU"},
         "roofline": head.get("roofline"),
-        "cpu_baseline": cpu,
+        "cpu_baseline": head_cpu,
         "components": results,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["compute_units"]},
     }

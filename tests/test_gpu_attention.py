@@ -146,3 +146,41 @@ def test_flash_causal_pairs_bit_identical(hip, monkeypatch, variant, b, h, s):
     monkeypatch.setenv("SILE_HIP_FA_PAIR", "0")
     single = _run(hip, "f16", b, h, s, d, bits, True, scale)
     np.testing.assert_array_equal(paired, single)
+
+
+@pytest.mark.parametrize("variant", ["v2w8", "v2", "v2k64", "q1"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("trend", ["rising", "falling", "large"])
+def test_flash_rescale_paths(hip, monkeypatch, variant, dt, causal, trend):
+    """Scores that move the running max across the sequence.  rising: key j
+    carries an offset growing with j, so later blocks exceed the running max
+    by far more than the lazy-rescale margin many times over (every rescale
+    and stale-block path of the kernels runs); falling: the first block holds
+    the maximum and later p underflow; large: scores of standard deviation
+    ~30, so many p of a block overflow the 16-bit type unless the block is
+    rescaled first."""
+    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
+    b, h, s, d = 1, 8, 512, 128
+    say(f"flash rescale {variant} {dt} causal={causal} {trend}")
+    r = rng(77)
+    q = r.normal(size=(b, h, s, d)).astype(np.float32)
+    k = r.normal(size=(b, h, s, d)).astype(np.float32)
+    v = r.normal(size=(b, h, s, d)).astype(np.float32)
+    if trend == "large":
+        q *= 5.0
+        k *= 5.0
+    else:
+        ramp = np.linspace(0.0, 1.0, s, dtype=np.float32)
+        if trend == "falling":
+            ramp = ramp[::-1].copy()
+        q += 1.0
+        k += 2.0 * ramp[None, None, :, None]
+    rnd = f16_round if dt == "f16" else bf16_round
+    qkv = [rnd(x) for x in (q, k, v)]
+    scale = 1.0 / np.sqrt(d)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
+    qf, kf, vf = (x[1] for x in qkv)
+    for hi in range(h):
+        ref = cpuref.attention_fwd(qf[0, hi], kf[0, hi], vf[0, hi], scale, causal=causal)
+        assert_close(got[0, hi], ref, atol=ATOL, rtol=RTOL, what=f"{trend} h{hi}")
