@@ -217,6 +217,9 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *                        A row-major, B column-major, M >= 256, N >= 256 with N
  *                        a multiple of 4, K' a multiple of 32 (16-bit) or 64 (fp8), leading
  *                        dimensions multiples of 16 bytes; MFMA path.
+ * M = 0 or N = 0: nothing is written.  K' = 0 (K below one bk): C = +0.0 for
+ * any M, N and supported types, as the canonical matmul's sums start at 0.0f
+ * and add no term (canonical_matmul.rs:58-73).
  * Anything else -> SILE_ERR_UNSUPPORTED_BACKEND or SILE_ERR_SHAPE. */
 int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
                   int64_t k, const void *a, int64_t lda, sile_layout a_layout, const void *b,

@@ -442,6 +442,16 @@ SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 
+// C = 0 for K' = 0 (K below one BK): the canonical matmul's sums start at
+// 0.0f and add no term (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:58-73,
+// k_limit = 0).  C is addressed in 16-bit words: n16 words per row, ldc16
+// words between rows (both exact for 16- and 32-bit C).
+extern "C" __global__ __launch_bounds__(256) void sile_gemm_zero_c(uint16_t* C, int64_t ldc16,
+                                                                   int64_t n16, int64_t m) {
+  for (int64_t r = blockIdx.x; r < m; r += gridDim.x)
+    for (int64_t c = threadIdx.x; c < n16; c += blockDim.x) C[r * ldc16 + c] = 0;
+}
+
 // fp32 GEMM on any shape in the canonical matmul's exact order: one thread per
 // cell, s = s + a*b from 0.0f over k < kp with separate roundings (no FMA).
 // A row-major [M,K]; B either row-major [K,N] (b_col_major = 0, the reference

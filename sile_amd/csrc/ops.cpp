@@ -239,9 +239,19 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   if (b_layout != SILE_COL_MAJOR)
     return fail(SILE_ERR_UNSUPPORTED_BACKEND, "%s GEMM needs B column-major (K contiguous)",
                 dtype_name(a_type));
+  if (kp == 0) {
+    // no k term: C = 0 (+0.0 in every output type), any M, N
+    const int64_t cb16 = (int64_t)dtype_bytes(c_type) / 2;
+    if (ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
+    int64_t ldc16 = ldc * cb16, n16 = n * cb16, rows = m;
+    void* zp[] = {&c, &ldc16, &n16, &rows};
+    int rc = launch(Module::kGemm, "sile_gemm_zero_c", dim3((unsigned)std::min<int64_t>(m, 4096)),
+                    dim3(256), zp, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
   // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
   // K' a multiple of the half k-step
-  if (m < 256 || n < 256 || n % 4 || kp % kstep || kp == 0)
+  if (m < 256 || n < 256 || n % 4 || kp % kstep)
     return fail(SILE_ERR_SHAPE,
                 "%s GEMM needs M >= 256, N >= 256 with N a multiple of 4, and K' a multiple of "
                 "%lld (M=%lld N=%lld K'=%lld)",
