@@ -44,6 +44,7 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n, k_steps;
   float alpha;
   int32_t m, n;           // C extents (>= 256): the last tile row / column starts at m - 256 / n - 256
+  int32_t k_rem;          // elements of the last half k-step inside K' (1 .. a half k-step)
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -218,6 +219,28 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 // half k-steps (64 bytes of a row): an odd count ends with a half k-step
 // whose sub-step 1 multiplies zero fragments.
 // ---------------------------------------------------------------------------
+// Keeps the elements e0 + j < k_rem of a 16-byte fragment chunk (8 16-bit or
+// 16 fp8 elements, element j at byte j * size) and zeroes the rest: the
+// last half k-step past K' holds whatever followed it in memory.
+template <bool kFp8>
+SILE_DEV u32x4 mask_k(u32x4 w, int e0, int k_rem) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t keep = 0;
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if (e0 + 4 * d + b < k_rem) keep |= 0xFFu << (8 * b);
+    } else {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        if (e0 + 2 * d + b < k_rem) keep |= 0xFFFFu << (16 * b);
+    }
+    w[d] &= keep;
+  }
+  return w;
+}
+
 template <int kKind, int kOut>
 __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
                                                const uint8_t* __restrict__ B,
@@ -323,6 +346,18 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
     // phase 0: MFMA Y(ks - 1) rows kNB/2 .. kNB-1 | reads X(ks), 4 fragments a group
 #pragma unroll
     for (int r = 0; r < kNB / 2; ++r) group(ya, yb, kNB / 2 + r, 0, 4 * r, 4, xa, xb);
+    if constexpr (kFinal) {
+      // K' ends inside X (the first half of the final k-step): mask it
+      if (half_last) {
+#pragma unroll
+        for (int q = 0; q < kNB; ++q)
+#pragma unroll
+          for (int h = 0; h < kCh; ++h) {
+            xa[q][h] = mask_k<kIsFP8>(xa[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), g.k_rem);
+            xb[q][h] = mask_k<kIsFP8>(xb[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), g.k_rem);
+          }
+      }
+    }
     // sub-step 1: MFMA X(ks) | reads Y(ks), 2 fragments a group (A blocks
     // first: every MFMA of a row needs all of them)
 #pragma unroll
@@ -330,13 +365,16 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
       group(xa, xb, r, 1, 2 * r, 2, ya, yb);
       if constexpr (kFinal) {
         // a half final k-step: sub-step 1 multiplies zeros (the LDS bytes past
-        // the last half k-step hold whatever followed it in memory)
+        // the last half k-step hold whatever followed it in memory); else
+        // K' ends inside Y: its elements past K' are zeroed
 #pragma unroll
         for (int q = 2 * r; q < 2 * r + 2; ++q)
 #pragma unroll
           for (int h = 0; h < kCh; ++h) {
-            if (q < kNB) ya[q][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : ya[q][h];
-            else yb[q - kNB][h] = half_last ? u32x4{0u, 0u, 0u, 0u} : yb[q - kNB][h];
+            const int e0 = (kCh * f_grp + h) * (kIsFP8 ? 16 : 8);
+            const int lim = half_last ? 0 : g.k_rem;
+            if (q < kNB) ya[q][h] = mask_k<kIsFP8>(ya[q][h], e0, lim);
+            else yb[q - kNB][h] = mask_k<kIsFP8>(yb[q - kNB][h], e0, lim);
           }
       }
     }

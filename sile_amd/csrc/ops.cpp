@@ -38,6 +38,7 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n, k_steps;
   float alpha;
   int32_t m, n;
+  int32_t k_rem;  // elements of the last half k-step inside K'
 };
 
 const char* dtype_name(int t) {
@@ -250,12 +251,11 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
     return rc == SILE_OK ? ok() : rc;
   }
   // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
-  // K' a multiple of the half k-step
-  if (m < 256 || n < 256 || n % 4 || kp % kstep)
+  // any K' (the kernel zeroes the elements of its last half k-step past K')
+  if (m < 256 || n < 256 || n % 4)
     return fail(SILE_ERR_SHAPE,
-                "%s GEMM needs M >= 256, N >= 256 with N a multiple of 4, and K' a multiple of "
-                "%lld (M=%lld N=%lld K'=%lld)",
-                dtype_name(a_type), (long long)kstep, (long long)m, (long long)n, (long long)kp);
+                "%s GEMM needs M >= 256, N >= 256 with N a multiple of 4 (M=%lld N=%lld)",
+                dtype_name(a_type), (long long)m, (long long)n);
   const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
   if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
   if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
@@ -268,8 +268,10 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   const int64_t tiles_m = (m + 255) / 256, tiles_n = (n + 255) / 256;
   if (tiles_m * tiles_n > 0x7fffffffLL || m > 0x7fffffffLL || n > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "GEMM too large");
-  GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)(kp / kstep),
-             scale_a * scale_b, (int32_t)m, (int32_t)n};
+  const int64_t half_steps = (kp + kstep - 1) / kstep;
+  if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
+  GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
+             scale_a * scale_b, (int32_t)m, (int32_t)n, (int32_t)(kp - (half_steps - 1) * kstep)};
   void* params[] = {&a, &b, &c, &g};
   int rc = launch(Module::kGemm, name, dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), params,
                   s);
