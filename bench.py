@@ -74,6 +74,40 @@ def normal(seed, shape, scale=1.0):
     return out
 
 
+def gemm_inputs(kind, size):
+    """Host operands of the GEMM configurations at M = N = K = size:
+    (a_bits [M, K], b_bits [N, K] (B column-major), scale_a, scale_b, a_type).
+    bf16: A, B ~ N(0, 1)/sqrt(K), seeds 4 / 5, rounded to bf16 (RNE).
+    fp8: A, B ~ N(0, 1), seeds 9 / 10, quantised per tensor to e4m3fn with
+    s = amax / 448, q = rne_sat(x / s)."""
+    m = n = k = size
+    if kind == "fp8":
+        # the oracle's encoder is the configuration's quantiser (input recipe,
+        # not timed work)
+        from oracle import cpuref
+        a = normal(9, (m, k))
+        b = normal(10, (n, k))
+        sa = float(np.float32(np.abs(a).max() / 448.0))
+        sb = float(np.float32(np.abs(b).max() / 448.0))
+        return cpuref.e4m3_encode(a, sa), cpuref.e4m3_encode(b, sb), sa, sb, hip.F8E4M3
+    a_bits = bf16_bits(normal(4, (m, k), 1 / np.sqrt(k)))
+    b_bits = bf16_bits(normal(5, (n, k), 1 / np.sqrt(k)))
+    return a_bits, b_bits, 1.0, 1.0, hip.BF16
+
+
+ATTN_SHAPE = (4, 32, 128)  # batch, heads, head_dim of the attention configuration
+
+
+def attention_inputs(s, b=ATTN_SHAPE[0], h=ATTN_SHAPE[1], d=ATTN_SHAPE[2]):
+    """Q, K, V [B, H, S, D] fp16 ~ N(0, 1), seeds 6 / 7 / 8."""
+    return [normal(seed, (b, h, s, d)).astype(np.float16) for seed in (6, 7, 8)]
+
+
+def softmax_input(rows=8192, cols=8192):
+    """x [rows, cols] fp16 ~ N(0, 4) (sigma 2), seed 3."""
+    return normal(3, (rows, cols), 2.0).astype(np.float16)
+
+
 # ---------------------------------------------------------------- timing
 
 def time_launches(launch, steps, warmup, stream, rotate=1):
@@ -142,22 +176,8 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0
     256-row tile of C over the same (de)quantised inputs."""
     m = n = k = size
     log(f"[bench] {name}: generating inputs")
-    if kind == "fp8":
-        # per-tensor e4m3fn quantisation of the seeded inputs (the input
-        # recipe of the fp8 configuration; not part of the timed work)
-        from oracle import cpuref
-        a = normal(9, (m, k))
-        b = normal(10, (n, k))
-        sa = float(np.float32(np.abs(a).max() / 448.0))
-        sb = float(np.float32(np.abs(b).max() / 448.0))
-        a_bits, b_bits = cpuref.e4m3_encode(a, sa), cpuref.e4m3_encode(b, sb)
-        del a, b
-        t, c_t = hip.F8E4M3, hip.BF16
-    else:
-        a_bits = bf16_bits(normal(4, (m, k), 1 / np.sqrt(k)))
-        b_bits = bf16_bits(normal(5, (n, k), 1 / np.sqrt(k)))
-        sa = sb = 1.0
-        t, c_t = hip.BF16, hip.BF16
+    a_bits, b_bits, sa, sb, t = gemm_inputs(kind, size)
+    c_t = hip.BF16
     da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
     host = (a_bits, b_bits) if cpu_tile_step else None
     del a_bits, b_bits
@@ -199,11 +219,10 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0
 def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0):
     """cpu_heads > 0 also times the CPU oracle on the first cpu_heads (b, h)
     slices, every query row, causal."""
-    b, h, d = 4, 32, 128
+    b, h, d = ATTN_SHAPE
     log(f"[bench] {name}: generating inputs")
     bufs, host = [], []
-    for seed in (6, 7, 8):
-        x = normal(seed, (b, h, s, d)).astype(np.float16)
+    for x in attention_inputs(s):
         bufs.append(hip.DeviceBuffer.from_array(x.view(np.uint16)))
         if cpu_heads:
             host.append(x.reshape(b * h, s, d)[:cpu_heads].astype(np.float32))
@@ -245,7 +264,7 @@ def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0):
 def bench_softmax(name, steps, warmup, stream, traffic, cpu=False):
     rows = cols = 8192
     log(f"[bench] {name}: generating inputs")
-    x = normal(3, (rows, cols), 2.0).astype(np.float16)
+    x = softmax_input(rows, cols)
     # 4 input/output pairs = 1 GiB, four times the 256 MiB Infinity Cache, so
     # every timed launch reads its input from HBM
     rotate = 4
@@ -276,15 +295,49 @@ def bench_softmax(name, steps, warmup, stream, traffic, cpu=False):
     return res
 
 
+# vec_add<TILE=4> (crates/sile/tests/backend_vec_add.rs:3-9) in the printed
+# LLIR form (crates/sile-llvm-ir/src/print.rs:6-57)
+LLIR_VEC_ADD4 = """\
+; vec_add<TILE=4> (crates/sile/examples/vec_add.rs:3-13) written by hand in the
+; printed LLIR form of crates/sile-llvm-ir/src/print.rs: c[4 pid + i] = a[..] + b[..]
+define void @vec_add(ptr addrspace(1) %a, ptr addrspace(1) %b, ptr addrspace(1) %c, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %a [rank=1, shape_offset=0, elem=f32]
+  ; sile.param %b [rank=1, shape_offset=1, elem=f32]
+  ; sile.param %c [rank=1, shape_offset=2, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %pid = call i32 @llvm.nvvm.ctaid.x()
+  %base = mul %pid, 4
+  br label %vec_add_header ; args(0)
+vec_add_header:
+  ; args(%i: i64)
+  %cond = icmp slt %i, 4
+  br i1 %cond, label %vec_add_body, label %vec_add_exit
+vec_add_body:
+  %idx = add %base, %i
+  %pa = getelementptr f32, ptr addrspace(1) %a, i64 %idx
+  %va = load f32, ptr addrspace(1) %pa
+  %pb = getelementptr f32, ptr addrspace(1) %b, i64 %idx
+  %vb = load f32, ptr addrspace(1) %pb
+  %sum = fadd %va, %vb
+  %pc = getelementptr f32, ptr addrspace(1) %c, i64 %idx
+  store f32 %sum, ptr addrspace(1) %pc
+  %next = add %i, 1
+  br label %vec_add_header ; args(%next)
+vec_add_exit:
+  ret void
+}
+"""
+
+
 def bench_llir_vec_add(name, steps, warmup):
-    """vec_add<TILE=4> generated from LLIR (tests/golden/llir/vec_add.llir) by
+    """vec_add<TILE=4> generated from LLIR (LLIR_VEC_ADD4) by
     sile_hip_llir_compile and run through sile_hip_launch_llir, which is
     synchronous like the reference's apply(): each step is one whole call
     (table upload, launch, wait).  c = a + b over 64M fp32 elements, 12 bytes
     of HBM traffic per element."""
     n = 64 << 20
-    with open(os.path.join(ROOT, "tests", "golden", "llir", "vec_add.llir")) as f:
-        kern = hip.LlirKernel(f.read(), (2, 1, 4))
+    kern = hip.LlirKernel(LLIR_VEC_ADD4, (2, 1, 4))
     a = hip.DeviceBuffer(n * 4)
     b = hip.DeviceBuffer(n * 4)
     c = hip.DeviceBuffer(n * 4)
@@ -306,16 +359,41 @@ def bench_llir_vec_add(name, steps, warmup):
     return res
 
 
+# softmax<BM=4, BN=8192> (crates/sile/examples/softmax.rs:3-16) in the
+# printed Tile IR form (crates/sile-tile-ir/src/print.rs:5-354) after the
+# default passes, the text a Rust HipBackend hands to sile_hip_tile_ir_route
+TILE_IR_SOFTMAX_4x8192 = """\
+module {
+  entry @softmax(
+    %0 {sym_name = "x", rank = 2} : tile<ptr<f32>>,
+    %1 {sym_name = "y", rank = 2} : tile<ptr<f32>>,
+    %2 {sym_name = "__shape_x", kind = "shape.desc", source = %0} : shape_desc<2>,
+    %3 {sym_name = "__launch_idx0", kind = "launch.index", dim = 0} : tile<i64>,
+    %4 {sym_name = "__launch_idx1", kind = "launch.index", dim = 1} : tile<i64>,
+    %12 {sym_name = "__shape_y", kind = "shape.desc", source = %1} : shape_desc<2>
+  ) {
+    ^bb0:  // entry
+      %5 = load_ptr_tko %0, [%3, %4] {shape = [4, 8192], stride_dim = 1} : tile<4x8192xf32>
+      %6 = reduce %5 {axis = 1, combiner = "max", input_shape = [4, 8192]} : tile<4x1xf32>
+      %9 = map exp(subf(%5, broadcast(%6, src_shape=[4, 1]))) {shape = [4, 8192]} : tile<4x8192xf32>
+      %10 = reduce %9 {axis = 1, combiner = "sum", input_shape = [4, 8192]} : tile<4x1xf32>
+      %13 = map divf(%9, broadcast(%10, src_shape=[4, 1])) {shape = [4, 8192]} : tile<4x8192xf32>
+      %14 = store_ptr_tko %1, %13, [%3, %4] {shape = [4, 8192], stride_dim = 1} : none
+      return
+  }
+}
+"""
+
+
 def bench_tile_ir_softmax(name, steps, warmup):
     """softmax<BM=4, BN=8192> over f32 [8192, 8192] given as printed Tile IR:
     routed once by sile_hip_tile_ir_route (to the row softmax kernel), then
     each step is one synchronous sile_hip_tile_ir_launch, like the reference's
     apply().  8 bytes of HBM traffic per element (read 4, write 4); two
     input/output pairs (1 GiB) rotate so every call reads from HBM."""
-    from tests import tile_ir_text
     rows = cols = 8192
     bm = 4
-    text = tile_ir_text.softmax(bm, cols)
+    text = TILE_IR_SOFTMAX_4x8192
     shapes, programs = [rows, cols, rows, cols], rows // bm
     route = hip.tile_ir_route(text, shapes, programs)
     if route.kind != hip.ROUTE_SOFTMAX_ROWS:

@@ -236,9 +236,24 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
 
 /* out[r] = max_c x[r][c] or sum_c x[r][c] in fp32 (ReduceMax/ReduceSum along
  * axis 1, crates/sile-tile-ir/src/passes/lowering/tile_compute/reduce.rs:10-112).
- * in: f32, f16, bf16.  `out` is fp32 [rows]. */
+ * in: f32, f16, bf16.  `out` is fp32 [rows].  The max equals the reference's
+ * fold; the sum is a wave tree, within fp32 rounding of the reference's
+ * order (sile_hip_reduce_rows_fused_sum keeps that order bit for bit). */
 int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, int64_t cols,
                          const void *x, int64_t ldx, float *out, sile_hip_stream stream);
+
+/* fp32 row sums in the order of the reference's fused load + reduce: the
+ * CPU backend's sum of a tile it reads straight from a buffer
+ * (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:31-177,
+ * 1142-1256), bit-identical to it.  4-element windows ((v0+v1)+v2)+v3 in
+ * order; for cols > 16 a step-4 loop from 0.0f while idx < cols, whose last
+ * window for cols % 4 != 0 reads the buffer's next elements past the row,
+ * then a scalar tail from 4*(cols/4).  x_len (>= (rows-1)*ldx + cols) is the
+ * number of elements of the buffer from x on; window elements past it are
+ * taken as 0.0f, where the reference reads past its buffer.  The router's
+ * row-sum route runs on this entry point. */
+int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                                   int64_t x_len, float *out, sile_hip_stream stream);
 
 /* Flash-attention forward, O = softmax(Q K^T * scale [+ causal mask]) V with
  * fp32 online-softmax state.  Q, K, V, O are [B, H, S, D] contiguous, f16 or

@@ -52,9 +52,9 @@ def lib() -> ctypes.CDLL:
         L.cpuref_kernel_matmul.argtypes = [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64]
         L.cpuref_kernel_softmax.argtypes = [_P, _I64, _I64, _P, _I64, _I64, _I64]
         L.cpuref_kernel_parallel_reduce.argtypes = [_P, _I64, _I64, _P, _I64, _I64]
-        L.cpuref_parallel_reduce_partials.argtypes = [_P, _P, _I64, _I64]
+        L.cpuref_parallel_reduce_partials.argtypes = [_P, _P, _I64, _I64, _I64]
         L.cpuref_gemm_nt.argtypes = [_P, _P, _P] + [_I64] * 9
-        L.cpuref_reduce_rows.argtypes = [ctypes.c_int, _P, _P, _I64, _I64, _I64]
+        L.cpuref_reduce_rows.argtypes = [ctypes.c_int, _P, _P, _I64, _I64, _I64, _I64]
         L.cpuref_softmax_rows.argtypes = [_P, _P, _I64, _I64, _I64, _I64]
         L.cpuref_attention_fwd.argtypes = [_P, _P, _P, _P, _I64, _I64, ctypes.c_float,
                                            ctypes.c_int, _I64, _I64]
@@ -119,9 +119,11 @@ def kernel_parallel_reduce(a, out, grid, tile):
 
 
 def parallel_reduce_partials(a, programs, tile):
+    """Each program's tile sum over the 1-D buffer a (programs * tile <= a.size)."""
     a = _f32(a)
+    assert a.ndim == 1 and programs * tile <= a.size
     out = np.zeros(programs, dtype=np.float32)
-    lib().cpuref_parallel_reduce_partials(_ptr(a), _ptr(out), programs, tile)
+    lib().cpuref_parallel_reduce_partials(_ptr(a), _ptr(out), programs, tile, a.size)
     return out
 
 
@@ -138,11 +140,17 @@ def gemm_nt(a, bt, bk=0, bm=1, row_tile_step=1, out=None):
 REDUCE_MAX, REDUCE_SUM, REDUCE_SUM_VEC4 = 0, 1, 2
 
 
-def reduce_rows(x, op):
+def reduce_rows(x, op, cols=None):
+    """Reduces the first `cols` columns (default: all) of every row of the
+    [rows, ldx] buffer x.  For REDUCE_SUM_VEC4 a window of the reference's
+    vec4 loop that runs past a row reads the buffer's next elements, and
+    0.0f past the end of x."""
     x = _f32(x)
-    rows, cols = x.shape
+    rows, ldx = x.shape
+    cols = ldx if cols is None else cols
+    assert 0 < cols <= ldx
     out = np.zeros(rows, dtype=np.float32)
-    lib().cpuref_reduce_rows(op, _ptr(x), _ptr(out), rows, cols, cols)
+    lib().cpuref_reduce_rows(op, _ptr(x), _ptr(out), rows, cols, ldx, x.size)
     return out
 
 

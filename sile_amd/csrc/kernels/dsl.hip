@@ -53,9 +53,11 @@ struct SoftmaxTileArgs {
 
 // Softmax DSL program (crates/sile/tests/backend_softmax.rs:3-15): for each of
 // the BM rows of the [BM, BN] tile at (gid0, gid1): m = row max, e = exp(x - m),
-// s = sum(e), y = e / s.  One wave per row; the max is order-independent, the
-// sum is a wave tree (the reference sums left to right; the results agree
-// within fp32 rounding of the sum, not bit for bit, and exp is the device's).
+// s = sum(e), y = e / s (IEEE division, as the reference's Div,
+// crates/sile-tile-ir/src/passes/lowering/tile_expr.rs:646-813).  One wave per
+// row; the max is order-independent, the sum is a wave tree (the reference
+// sums left to right; the results agree within fp32 rounding of the sum, not
+// bit for bit, and exp is the device's v_exp_f32, not the host's expf).
 extern "C" __global__ __launch_bounds__(256) void sile_dsl_softmax_f32(const float* __restrict__ x,
                                                                         float* __restrict__ y,
                                                                         SoftmaxTileArgs args) {
@@ -72,51 +74,65 @@ extern "C" __global__ __launch_bounds__(256) void sile_dsl_softmax_f32(const flo
     float s = 0.0f;
     for (int64_t c = lane; c < args.bn; c += 64) s += exp2_fast((xr[c] - m) * kLog2e);
     s = wave_sum(s);
-    const float inv = 1.0f / s;
-    for (int64_t c = lane; c < args.bn; c += 64) yr[c] = exp2_fast((xr[c] - m) * kLog2e) * inv;
+    for (int64_t c = lane; c < args.bn; c += 64) yr[c] = exp2_fast((xr[c] - m) * kLog2e) / s;
   }
 }
 
 struct ReduceTileArgs {
   int64_t tile;   // TILE const generic
   int64_t total;  // shape(a)[0] (wrapper fallback: no tile store to infer from)
+  int64_t len;    // elements of a
 };
 
 // parallel_reduce program (crates/sile/examples/parallel_reduce.rs:3-9): the
 // tile a[pid*TILE, pid*TILE+TILE) is summed in the fused load+reduce vec4
 // order (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:80-113,
-// 1182-1256): chunk sums ((v0+v1)+v2)+v3 added in chunk order to an
-// accumulator that starts at 0.0f (TILE > 16) or at chunk 0 (TILE <= 16), then
-// the scalar tail in order.  Lanes form the chunk sums in parallel; lane 0
-// folds them in order, so the per-program partial is bit-identical to the CPU
-// backend's.  Programs then add their partial to out[0] atomically; the order
-// across programs is unspecified there as here.
+// 1182-1256): window sums ((v0+v1)+v2)+v3 added in window order, then the
+// scalar tail from 4*(TILE/4) in order.
+//  * TILE <= 16: TILE/4 windows, the accumulator starts at window 0;
+//  * TILE > 16: the loop runs while idx < TILE (step 4,
+//    crates/sile-tile-ir/src/passes/lowering/core/emit/tile_loops/single_axis.rs:180-260)
+//    from 0.0f: ceil(TILE/4) windows, the last of which, for TILE % 4 != 0,
+//    reads the first elements of the next tile and is followed by the tail,
+//    which adds its in-tile elements again.  Window elements past the end of
+//    a (the last program) are taken as 0.0f; the reference reads past the
+//    buffer there.
+// Lanes form the window sums in parallel; lane 0 folds them in order, so the
+// per-program partial is bit-identical to the CPU backend's.  Programs then
+// add their partial to out[0] atomically; the order across programs is
+// unspecified there as here.
 extern "C" __global__ __launch_bounds__(64) void sile_dsl_parallel_reduce_f32(
     const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
     ReduceTileArgs args) {
 #pragma clang fp contract(off)
-  __shared__ float chunk_sums[64];
+  __shared__ float window_sums[64];
   const int64_t pid = blockIdx.x;
   if (pid >= args.total) return;
   const int lane = threadIdx.x;
   const float* t = a + pid * args.tile;
+  const int64_t avail = args.len - pid * args.tile;  // elements of a from t on
   const int64_t chunks = args.tile / 4;
+  const bool unrolled = args.tile <= 16;
+  const int64_t windows = unrolled ? chunks : (args.tile + 3) / 4;
   float acc = 0.0f;
   int64_t first = 0;
-  if (args.tile <= 16 && chunks > 0) {
+  if (unrolled && chunks > 0) {
     acc = ((t[0] + t[1]) + t[2]) + t[3];
     first = 1;
   }
-  for (int64_t base = first; base < chunks; base += 64) {
-    const int64_t ci = base + lane;
-    if (ci < chunks) {
-      const float* p = t + 4 * ci;
-      chunk_sums[lane] = ((p[0] + p[1]) + p[2]) + p[3];
+  for (int64_t base = first; base < windows; base += 64) {
+    const int64_t wi = base + lane;
+    if (wi < windows) {
+      const int64_t e = 4 * wi;
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = e + j < avail ? t[e + j] : 0.0f;
+      window_sums[lane] = ((v[0] + v[1]) + v[2]) + v[3];
     }
     __syncthreads();
     if (lane == 0) {
-      const int64_t n = (chunks - base) < 64 ? (chunks - base) : 64;
-      for (int64_t i = 0; i < n; ++i) acc = acc + chunk_sums[i];
+      const int64_t n = (windows - base) < 64 ? (windows - base) : 64;
+      for (int64_t i = 0; i < n; ++i) acc = acc + window_sums[i];
     }
     __syncthreads();
   }

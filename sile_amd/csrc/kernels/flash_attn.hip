@@ -712,15 +712,9 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::lds_bytes<NK>()];              \
     v2::attn_fwd_v2<BF, QT, W, NK, SCHED>(Q, K, V, O, a, smem);                               \
   }
-// 4 waves x 64 queries (one wave per SIMD) and 8 waves x 32 queries (two per
-// SIMD, the default) over 32-key blocks; 8 waves x 32 queries over 64-key
-// blocks with the issue order fixed
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2, false, 2, 4, 32, 0)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2, true, 2, 4, 32, 0)
+// 8 waves x 32 queries (two waves per SIMD) over 32-key blocks
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 0)
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32, 0)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2k64, false, 1, 8, 64, 1)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2k64, true, 1, 8, 64, 1)
 
 #define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \
@@ -730,5 +724,4 @@ SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2k64, true, 1, 8, 64, 1)
   }
 
 SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k64, false, 1, 64)
-SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q2_k64, false, 2, 64)
 SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k64, true, 1, 64)

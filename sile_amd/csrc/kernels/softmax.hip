@@ -117,6 +117,19 @@ SILE_DEV void store_chunk(typename Elem<kT>::Storage* p, const float* v) {
     Elem<kT>::store8(p, v);
 }
 
+// y = e / s.  fp32 outputs use IEEE division, as the reference's Div
+// (crates/sile-tile-ir/src/passes/lowering/tile_expr.rs:646-813); a 16-bit
+// output is rounded once more afterwards, so e * (1 / s), within an fp32 ulp
+// of e / s, stands in for it there.  exp is the device's v_exp_f32, not the
+// host libm expf of the reference (whose bits are not pinned by it).
+template <int kOut>
+SILE_DEV float normalise(float e, float s, float inv) {
+  if constexpr (kOut == kF32)
+    return e / s;
+  else
+    return e * inv;
+}
+
 // ---- register-resident row softmax: cols == kChunks * 64 * chunk_elems ----
 template <int kIn, int kOut, int kChunks>
 __device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Storage* __restrict__ xr,
@@ -145,7 +158,7 @@ __device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Stora
 #pragma unroll
   for (int j = 0; j < kChunks; ++j) {
 #pragma unroll
-    for (int i = 0; i < kE; ++i) v[j][i] *= inv;
+    for (int i = 0; i < kE; ++i) v[j][i] = normalise<kOut>(v[j][i], s, inv);
     store_chunk<kOut, kE>(yr + (j * 64 + lane) * kE, v[j]);
   }
 }
@@ -264,7 +277,7 @@ __device__ __forceinline__ void softmax_row_masked(const typename Elem<kIn>::Sto
   for (int j = 0; j < kChunks; ++j) {
     const int c0 = (j * 64 + lane) * kE;
 #pragma unroll
-    for (int i = 0; i < kE; ++i) v[j][i] *= inv;
+    for (int i = 0; i < kE; ++i) v[j][i] = normalise<kOut>(v[j][i], s, inv);
     if (c0 + kE <= cols) {
       store_chunk<kOut, kE>(yr + c0, v[j]);
     } else {
@@ -320,7 +333,8 @@ __device__ __forceinline__ void softmax_rows_generic_kernel(const void* x, void*
   s = wave_sum(s);
   const float inv = 1.0f / s;
   for (int64_t c = lane; c < cols; c += 64)
-    Elem<kOut>::store1(yr + c, exp2_fast((Elem<kIn>::load1(xr + c) - m) * kLog2e) * inv);
+    Elem<kOut>::store1(
+        yr + c, normalise<kOut>(exp2_fast((Elem<kIn>::load1(xr + c) - m) * kLog2e), s, inv));
 }
 
 #define SILE_SOFTMAX_REGS(NAME, IN, OUT, CH)                                                 \
@@ -416,4 +430,51 @@ extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_bf16(int op, 
                                                                         int64_t cols,
                                                                         int64_t ldx) {
   reduce_rows_kernel<kBF16>(op, vec, x, out, rows, cols, ldx);
+}
+
+// ---- fp32 row sums in the order of the reference's fused load + reduce ----
+// The CPU backend sums a row it loads straight from a buffer
+// (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:31-177)
+// in 4-element windows, each ((v0 + v1) + v2) + v3, added in window order:
+//  * cols <= 16: cols/4 windows, the accumulator starts at window 0 (:80-113);
+//  * cols > 16: a step-4 loop from 0.0f while idx < cols (:1182-1256,
+//    crates/sile-tile-ir/src/passes/lowering/core/emit/tile_loops/single_axis.rs:180-260),
+//    so for cols % 4 != 0 the last window reads the next elements of the
+//    buffer past the row;
+// then a scalar tail from 4*(cols/4), which re-adds the row's elements of a
+// partial last window.  cols < 4 is the plain fold from element 0.  Window
+// elements at or past x_len (the buffer's end) are taken as 0.0f.
+// Each row is one dependent chain, so one lane owns one row.
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32(
+    const float* __restrict__ x, float* __restrict__ out, int64_t rows, int64_t cols, int64_t ldx,
+    int64_t x_len) {
+#pragma clang fp contract(off)
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const float* xr = x + row * ldx;
+  const int64_t avail = x_len - row * ldx;
+  float acc;
+  if (cols < 4) {
+    acc = xr[0];
+    for (int64_t c = 1; c < cols; ++c) acc = acc + xr[c];
+  } else {
+    const int64_t chunks = cols / 4;
+    if (cols <= 16) {
+      acc = ((xr[0] + xr[1]) + xr[2]) + xr[3];
+      for (int64_t i = 1; i < chunks; ++i) {
+        const float* p = xr + 4 * i;
+        acc = acc + (((p[0] + p[1]) + p[2]) + p[3]);
+      }
+    } else {
+      acc = 0.0f;
+      for (int64_t idx = 0; idx < cols; idx += 4) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = idx + j < avail ? xr[idx + j] : 0.0f;
+        acc = acc + (((v[0] + v[1]) + v[2]) + v[3]);
+      }
+    }
+    for (int64_t c = chunks * 4; c < cols; ++c) acc = acc + xr[c];
+  }
+  out[row] = acc;
 }

@@ -31,7 +31,7 @@ struct SoftmaxTileArgs {
   int64_t ldx, ldy, bm, bn, tiles_n, total;
 };
 struct ReduceTileArgs {
-  int64_t tile, total;
+  int64_t tile, total, len;
 };
 struct GemmArgs {
   int64_t lda, ldb, ldc;
@@ -177,7 +177,7 @@ int sile_hip_kernel_parallel_reduce(void* const* buffers, int64_t num_threadgrou
   if (len < 0 || out_len < 1) return fail(SILE_ERR_SHAPE, "out must hold at least one element");
   // No tile store to infer a plan from: total = shape(first buffer)[0]
   // (crates/sile-backend/src/cpu/codegen.rs:479-503).
-  ReduceTileArgs t{tile, len};
+  ReduceTileArgs t{tile, len, len};
   int64_t run = 0;
   int rc = programs_to_run(num_threadgroups, threads_per_group, t.total, &run);
   if (rc != SILE_OK) return rc;
@@ -314,10 +314,8 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
   }
   char name[64];
   int rc;
-  // 16-bit rows of 4096 / 8192: the packed-row kernel (see softmax.hip) unless
-  // SILE_HIP_SOFTMAX_PACKED=0
-  const char* pk = getenv("SILE_HIP_SOFTMAX_PACKED");
-  const bool packed = (chunks == 8 || chunks == 16) && !(pk && pk[0] == '0') &&
+  // 16-bit rows of 4096 / 8192: the packed-row kernel (see softmax.hip)
+  const bool packed = (chunks == 8 || chunks == 16) &&
                       (!strcmp(tag, "f16_f16") || !strcmp(tag, "bf16_bf16"));
   // other widths up to 8192 (16-bit) / 8192 (fp32): one pass with a masked
   // last chunk, the smallest power-of-two chunk count that covers the row
@@ -373,6 +371,24 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
   return rc == SILE_OK ? ok() : rc;
 }
 
+int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float* x, int64_t ldx,
+                                   int64_t x_len, float* out, sile_hip_stream stream) {
+  if (rows < 0 || cols < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (rows == 0) return ok();
+  if (cols == 0) return fail(SILE_ERR_SHAPE, "reduce over an empty row");
+  if (!x || !out) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldx < cols) return fail(SILE_ERR_SHAPE, "leading dimension smaller than cols");
+  if (x_len < (rows - 1) * ldx + cols)
+    return fail(SILE_ERR_SHAPE, "x_len %lld does not cover %lld rows of %lld at pitch %lld",
+                (long long)x_len, (long long)rows, (long long)cols, (long long)ldx);
+  const int64_t blocks = (rows + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+  void* params[] = {(void*)&x, &out, &rows, &cols, &ldx, &x_len};
+  int rc = launch(Module::kSoftmax, "sile_reduce_rows_fused_sum_f32", dim3((unsigned)blocks),
+                  dim3(256), params, static_cast<hipStream_t>(stream));
+  return rc == SILE_OK ? ok() : rc;
+}
+
 // ---------------------------------------------------------------------------
 // Attention
 // ---------------------------------------------------------------------------
@@ -395,27 +411,16 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (seq_len * head_dim * 2 > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
-  // MFMA flash kernels: head_dim 128, 16-byte aligned operands.
-  //   v2w8 (default) / v2k64 / v2 (pipelined, 256-query blocks, 8 waves x 32
-  //   queries or 4 waves x 64 queries, 32- or 64-key blocks): S a multiple of 256;
-  //   q1 / q2 (128- / 256-query blocks): S a multiple of 128 / 256.
-  // SILE_HIP_FA_KERNEL=v2|v2w8|v2k64|q1|q2 overrides the choice (tuning, tests).
+  // MFMA flash kernels: head_dim 128, 16-byte aligned operands, chosen by shape:
+  //   S a multiple of 256: the pipelined kernel (8 waves x 32 queries, 32-key
+  //     blocks; causal query blocks taken in balanced pairs);
+  //   S a multiple of 128: the 128-query-block kernel.
   if (head_dim == 128 && seq_len % 128 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
       aligned16(o)) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const char* env = getenv("SILE_HIP_FA_KERNEL");
-    std::string variant = env ? env : "v2w8";
-    auto is_pipelined = [](const std::string& v) {
-      return v == "v2" || v == "v2w8" || v == "v2k64";
-    };
-    if (!is_pipelined(variant) && variant != "q1" && variant != "q2") variant = "v2w8";
-    if (seq_len % 256 != 0 || (variant == "q2" && dtype != SILE_F16)) variant = "q1";
-    const bool pipelined = is_pipelined(variant);
-    const int64_t bq = variant == "q1" ? 128 : 256;
-    // causal pipelined kernels take query blocks in balanced pairs
-    // (SILE_HIP_FA_PAIR=0: one block per workgroup)
-    const char* pair_env = getenv("SILE_HIP_FA_PAIR");
-    const bool pair = causal && pipelined && !(pair_env && pair_env[0] == '0');
+    const bool pipelined = seq_len % 256 == 0;
+    const int64_t bq = pipelined ? 256 : 128;
+    const bool pair = causal && pipelined;
     struct {
       int64_t seq;
       int32_t bh, q_blocks;
@@ -426,11 +431,8 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const int64_t units = pair ? (seq_len / bq + 1) / 2 : seq_len / bq;
     const int64_t blocks = bh * units;
     char name[64];
-    if (pipelined)
-      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, variant.c_str());
-    else
-      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s_k64", dt, variant.c_str());
-    const unsigned threads = (variant == "v2w8" || variant == "v2k64") ? 512 : 256;
+    snprintf(name, sizeof name, pipelined ? "sile_flash_attn_fwd_%s_v2w8" : "sile_flash_attn_fwd_%s_q1_k64", dt);
+    const unsigned threads = pipelined ? 512 : 256;
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(threads), params, s);
     return rc == SILE_OK ? ok() : rc;

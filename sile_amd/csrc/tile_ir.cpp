@@ -1223,9 +1223,16 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
                                  bufs[1], shp[3], stream);
       break;
     case SILE_ROUTE_REDUCE_ROWS:
-      rc = sile_hip_reduce_rows((sile_reduce_op)route->reduce_op, SILE_F32, route->rows,
-                                route->cols, bufs[0], shp[1], static_cast<float*>(bufs[1]),
-                                stream);
+      // a reduce of a load is the reference's fused load + reduce: the sum in
+      // its vec4 window order, which may read on into x past a row
+      if (route->reduce_op == SILE_REDUCE_SUM)
+        rc = sile_hip_reduce_rows_fused_sum(route->rows, route->cols,
+                                            static_cast<const float*>(bufs[0]), shp[1],
+                                            shp[0] * shp[1], static_cast<float*>(bufs[1]), stream);
+      else
+        rc = sile_hip_reduce_rows((sile_reduce_op)route->reduce_op, SILE_F32, route->rows,
+                                  route->cols, bufs[0], shp[1], static_cast<float*>(bufs[1]),
+                                  stream);
       break;
     default:
       return fail(SILE_ERR_SHAPE, "unknown route kind %d", route->kind);

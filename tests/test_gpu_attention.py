@@ -94,16 +94,20 @@ def test_attention_config4_full_shape_sampled(hip):
     assert np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("variant", ["v2", "v2w8", "v2k64", "q1", "q2"])
+# The MFMA kernel is chosen by shape: S a multiple of 256 runs the pipelined
+# kernel (causal query blocks in balanced pairs), other multiples of 128 the
+# 128-query-block kernel.
+KERNEL_S = {"pipelined": 512, "q128": 384}
+
+
+@pytest.mark.parametrize("kernel", ["pipelined", "q128"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_flash_variants_xcd_order(hip, monkeypatch, variant, dt, causal):
-    """Each MFMA flash kernel (pipelined v2 with 4 or 8 waves, q1 / q2)
-    on B*H = 8 heads (head-per-XCD launch order); every head and query is
-    compared with the fp32 oracle."""
-    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
-    b, h, s, d = 2, 4, 512, 128
-    say(f"flash {dt} {variant} causal={causal} B={b} H={h} S={s}")
+def test_flash_kernels_xcd_order(hip, kernel, dt, causal):
+    """Each MFMA flash kernel on B*H = 8 heads (head-per-XCD launch order);
+    every head and query is compared with the fp32 oracle."""
+    b, h, s, d = 2, 4, KERNEL_S[kernel], 128
+    say(f"flash {dt} {kernel} causal={causal} B={b} H={h} S={s}")
     scale = 1.0 / np.sqrt(d)
     qkv = _inputs(b, h, s, d, dt, seed=21)
     got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
@@ -132,27 +136,29 @@ def test_flash_causal_row_independence(hip):
     assert not np.array_equal(first[:, :, p + 1:], second[:, :, p + 1:])
 
 
-@pytest.mark.parametrize("variant", ["v2w8", "v2", "v2k64"])
-@pytest.mark.parametrize("b,h,s", [(2, 4, 768), (1, 3, 1024)])
-def test_flash_causal_pairs_bit_identical(hip, monkeypatch, variant, b, h, s):
-    """A workgroup that takes two query blocks in turn (balanced causal pairs)
-    computes each exactly as a workgroup of one block does."""
-    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
+@pytest.mark.parametrize("b,h", [(2, 4), (1, 3)])
+def test_flash_causal_pairs_bit_identical(hip, b, h):
+    """Causal rows depend only on the keys up to them, so the first 512
+    queries of S = 1024 (4 blocks of 256: pairs (3, 0), (2, 1)), S = 768
+    (pairs (2, 0), (1) alone) and S = 512 (pair (1, 0)) must be computed
+    bit for bit alike, whichever block a workgroup pairs them with."""
     d = 128
-    say(f"flash {variant} causal pairs vs single blocks B={b} H={h} S={s}")
+    say(f"flash causal pairs: S=1024 / 768 / 512 prefixes B={b} H={h}")
     scale = 1.0 / np.sqrt(d)
-    bits = [x[0] for x in _inputs(b, h, s, d, "f16", seed=41)]
-    paired = _run(hip, "f16", b, h, s, d, bits, True, scale)
-    monkeypatch.setenv("SILE_HIP_FA_PAIR", "0")
-    single = _run(hip, "f16", b, h, s, d, bits, True, scale)
-    np.testing.assert_array_equal(paired, single)
+    bits = [x[0] for x in _inputs(b, h, 1024, d, "f16", seed=41)]
+    outs = {}
+    for s in (1024, 768, 512):
+        outs[s] = _run(hip, "f16", b, h, s, d, [np.ascontiguousarray(x[:, :, :s]) for x in bits],
+                       True, scale)
+    np.testing.assert_array_equal(outs[1024][:, :, :768], outs[768])
+    np.testing.assert_array_equal(outs[1024][:, :, :512], outs[512])
 
 
-@pytest.mark.parametrize("variant", ["v2w8", "v2", "v2k64", "q1"])
+@pytest.mark.parametrize("kernel", ["pipelined", "q128"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("trend", ["rising", "falling", "large"])
-def test_flash_rescale_paths(hip, monkeypatch, variant, dt, causal, trend):
+def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     """Scores that move the running max across the sequence.  rising: key j
     carries an offset growing with j, so later blocks exceed the running max
     by far more than the lazy-rescale margin many times over (every rescale
@@ -160,9 +166,8 @@ def test_flash_rescale_paths(hip, monkeypatch, variant, dt, causal, trend):
     the maximum and later p underflow; large: scores of standard deviation
     ~30, so many p of a block overflow the 16-bit type unless the block is
     rescaled first."""
-    monkeypatch.setenv("SILE_HIP_FA_KERNEL", variant)
-    b, h, s, d = 1, 8, 512, 128
-    say(f"flash rescale {variant} {dt} causal={causal} {trend}")
+    b, h, s, d = 1, 8, KERNEL_S[kernel], 128
+    say(f"flash rescale {kernel} {dt} causal={causal} {trend}")
     r = rng(77)
     q = r.normal(size=(b, h, s, d)).astype(np.float32)
     k = r.normal(size=(b, h, s, d)).astype(np.float32)

@@ -127,11 +127,37 @@ def test_parallel_reduce_reference_fixtures(hip, fixtures, name):
     np.testing.assert_array_equal(parts, cpuref.parallel_reduce_partials(a, programs, fx["tile"]))
 
 
-@pytest.mark.parametrize("tile", [3, 12, 16, 1000, 1003])
-def test_parallel_reduce_partials_random(hip, tile):
-    say(f"dsl parallel_reduce random tile={tile}")
+@pytest.mark.parametrize("tile", [17, 18, 19, 20, 1003])
+def test_parallel_reduce_ones_closed_form(hip, tile):
+    """Ones: the reference's loop form reads ceil(TILE/4) windows (into the
+    next tile) and re-adds the TILE % 4 tail: TILE = 18 gives 16 + 4 + 2 = 22
+    per program; the last program's window runs past a (0.0f): 20."""
+    say(f"dsl parallel_reduce ones tile={tile}")
+    programs = 25
+    a = np.ones(programs * tile, np.float32)
+    da = hip.DeviceBuffer.from_array(a)
+    dout = hip.DeviceBuffer.from_array(np.zeros(1, np.float32))
+    dpart = hip.DeviceBuffer(programs * 4)
+    hip.kernel_parallel_reduce([da.ptr, dout.ptr], programs, [a.size, 1], tile, partials=dpart.ptr)
+    parts = dpart.download(np.float32, (programs,))
+    rem = tile % 4
+    interior = 4 * ((tile + 3) // 4) + rem if rem else tile
+    last = 4 * (tile // 4) + 2 * rem
+    np.testing.assert_array_equal(parts[:-1], interior)
+    assert parts[-1] == last
+    if tile == 18:
+        assert (interior, last) == (22, 20)
+    assert dout.download(np.float32, (1,))[0] == interior * (programs - 1) + last
+
+
+@pytest.mark.parametrize("tile,pad", [(3, 5), (12, 5), (16, 5), (1000, 5), (1003, 5), (1003, 0),
+                                      (17, 0), (17, 2)])
+def test_parallel_reduce_partials_random(hip, tile, pad):
+    """pad = elements of a past the last tile: the last program's final
+    window reads them (pad >= 4 - TILE % 4) or runs past a."""
+    say(f"dsl parallel_reduce random tile={tile} pad={pad}")
     programs = 37
-    a = rng(tile).normal(size=programs * tile + 5).astype(np.float32)
+    a = rng(tile).normal(size=programs * tile + pad).astype(np.float32)
     da = hip.DeviceBuffer.from_array(a)
     dout = hip.DeviceBuffer.from_array(np.zeros(1, np.float32))
     dpart = hip.DeviceBuffer(programs * 4)

@@ -2,10 +2,10 @@
 is routed (sile_hip_tile_ir_route) and launched (sile_hip_tile_ir_launch)
 through the C ABI, and compared with the reference's fixtures and the CPU
 oracle of the same kernel with the same grid.  Bars: matmul bit-exact (the
-exact-order tile kernel); max reductions bit-exact; softmax |g - r| <= 1e-6 +
-1e-5 |r| (device exp, tree sums; the reference test bounds row sums by 1e-4);
-sums within 1e-5 of the sum of |x| (tree order); the atomic sum of ones
-exact."""
+exact-order tile kernel); row max and row sum bit-exact (the sum in the fused
+load + reduce vec4 order); softmax |g - r| <= 1e-6 + 1e-5 |r| (device exp,
+tree sums; the reference test bounds row sums by 1e-4); the atomic sum of
+ones exact."""
 import json
 import os
 
@@ -105,8 +105,16 @@ def test_softmax_routes_match_the_oracle(hip, rows, cols, bm, bn, programs, kind
     (64, 1000, 4, 1000, 16, 2),
     (64, 1000, 4, 960, 9, 1),   # first 960 columns, 9 of 16 row bands
     (256, 8192, 1, 8192, 256, 2),
+    (40, 1003, 2, 1003, 20, 2),  # last window of each row reads the next row; the
+                                 # buffer's last row reads past x (0.0f)
+    (40, 1003, 2, 1001, 7, 1),   # windows read the row's own columns 1001..1003
+    (16, 18, 4, 17, 4, 2),       # 17 wide: one window of 1 + 3 elements past
+    (16, 12, 4, 7, 4, 2),        # unrolled form, 1 window and a tail of 3
+    (8, 3, 1, 3, 8, 2),          # below 4: the plain fold
 ])
 def test_row_reduce_matches_the_oracle(hip, op, rows, cols, bm, bn, programs, out_rank):
+    """The route is the reference's fused load + reduce: the max bit-exact,
+    the sum bit-exact in its vec4 window order (over-read included)."""
     say(f"tile ir row_{op} {rows}x{cols} BM={bm} BN={bn} programs={programs} rank={out_rank}")
     x = (rng(5).normal(size=(rows, cols)) * 3).astype(np.float32)
     yshape = (rows, 1) if out_rank == 2 else (rows,)
@@ -115,13 +123,22 @@ def test_row_reduce_matches_the_oracle(hip, op, rows, cols, bm, bn, programs, ou
                   hip.ROUTE_REDUCE_ROWS)
     got = got.reshape(rows)
     n = programs * bm
-    part = x[:n, :bn]
-    ref = cpuref.reduce_rows(part, cpuref.REDUCE_MAX if op == "max" else cpuref.REDUCE_SUM)
-    if op == "max":
-        np.testing.assert_array_equal(got[:n], ref)
-    else:
-        assert np.all(np.abs(got[:n] - ref) <= 1e-5 * np.abs(part).sum(axis=1))
+    ref = cpuref.reduce_rows(x, cpuref.REDUCE_MAX if op == "max" else cpuref.REDUCE_SUM_VEC4,
+                             cols=bn)
+    np.testing.assert_array_equal(got[:n], ref[:n])
     np.testing.assert_array_equal(got[n:], 11.0)
+
+
+def test_row_sum_route_ones_closed_form(hip):
+    """Rows of ones, 18 wide: every row but the buffer's last adds 16 + 4 + 2
+    = 22; the last row's window runs past x: 16 + 2 + 2 = 20."""
+    say("tile ir row_sum ones 18 wide")
+    rows, cols = 12, 18
+    x = np.ones((rows, cols), np.float32)
+    y0 = np.zeros((rows, 1), np.float32)
+    _, got = _run(hip, T.row_reduce(4, cols, "sum", 2), [x, y0], rows // 4, hip.ROUTE_REDUCE_ROWS)
+    np.testing.assert_array_equal(got[:-1, 0], 22.0)
+    assert got[-1, 0] == 20.0
 
 
 def test_parallel_reduce_reference_fixture(hip, fixtures):

@@ -132,28 +132,94 @@ def test_reduce_rows_max_and_sequential_sum():
     np.testing.assert_array_equal(cpuref.reduce_rows(x, cpuref.REDUCE_SUM), seq)
 
 
-def _vec4_fold(row, unrolled):
-    chunks = len(row) // 4
+def _ones_vec4_sum(extent, past_end):
+    """Closed form of the reference's fused vec4 sum over a row of ones
+    (fused_reduce.rs:1182-1256 with single_axis.rs:180-260): the loop form
+    (extent > 16) runs ceil(extent/4) windows of 4 and then re-adds the
+    extent % 4 elements of the partial last window in the scalar tail; a
+    window element past the buffer's end counts 0 (`past_end`), otherwise it
+    is the next element of the buffer (1 here).  The unrolled form (extent
+    <= 16) reads extent/4 windows and the tail once: exactly `extent`."""
+    if extent <= 16:
+        return float(extent)
+    rem = extent % 4
+    if rem == 0:
+        return float(extent)
+    windows = 4 * ((extent + 3) // 4) if not past_end else 4 * (extent // 4) + rem
+    return float(windows + rem)
+
+
+@pytest.mark.parametrize("tile", [4, 7, 16, 17, 18, 19, 20, 21, 1000, 1003])
+def test_parallel_reduce_vec4_ones_closed_form(tile):
+    """TILE = 18 over ones: every program but the last reads 2 elements of
+    the next tile in its last window and re-adds 2 in the tail: 16 + 4 + 2 =
+    22; the last program's window runs past the buffer (0.0f there): 16 + 2
+    + 2 = 20."""
+    programs = 9
+    a = np.ones(programs * tile, np.float32)
+    parts = cpuref.parallel_reduce_partials(a, programs, tile)
+    interior, last = _ones_vec4_sum(tile, False), _ones_vec4_sum(tile, True)
+    np.testing.assert_array_equal(parts[:-1], interior)
+    assert parts[-1] == last
+    if tile == 18:
+        assert (interior, last) == (22.0, 20.0)
+    out = np.zeros(1, np.float32)
+    cpuref.kernel_parallel_reduce(a, out, (programs, 1, 1), tile)
+    assert out[0] == interior * (programs - 1) + last
+
+
+@pytest.mark.parametrize("cols", [5, 17, 18, 19, 33])
+def test_reduce_rows_vec4_ones_closed_form(cols):
+    """Rows of a [rows, cols] buffer: the last window of a row reads the next
+    row's first elements; only the last row's reads past the buffer."""
+    x = np.ones((5, cols), np.float32)
+    got = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
+    np.testing.assert_array_equal(got[:-1], _ones_vec4_sum(cols, False))
+    assert got[-1] == _ones_vec4_sum(cols, True)
+    # inside a wider pitch the window reads the row's own padding (ones here)
+    xp = np.ones((3, cols + 8), np.float32)
+    np.testing.assert_array_equal(cpuref.reduce_rows(xp, cpuref.REDUCE_SUM_VEC4, cols=cols),
+                                  _ones_vec4_sum(cols, False))
+    xp[:, cols:] = 0.0
+    np.testing.assert_array_equal(cpuref.reduce_rows(xp, cpuref.REDUCE_SUM_VEC4, cols=cols),
+                                  _ones_vec4_sum(cols, True))
+
+
+def test_vec4_grouping_and_start_probes():
+    """Inputs whose result fixes the grouping, each chosen so a plausible
+    other order gives a different float:
+      [1, 1, 2^24, 0]           ((v0+v1)+v2)+v3 = 2^24+2; a pairwise tree 2^24
+      [2^24,0,0,0, 1,1,0,0]     chunk sums added: 2^24+2; an element-wise fold 2^24
+      16 x -0.0                 unrolled start at chunk 0: -0.0
+      20 x -0.0                 loop start at +0.0f: +0.0"""
     f = np.float32
-    acc = f(0.0)
-    start = 0
-    if unrolled:
-        acc = f(f(f(row[0] + row[1]) + row[2]) + row[3])
-        start = 1
-    for i in range(start, chunks):
-        v = row[4 * i:4 * i + 4]
-        acc = f(acc + f(f(f(v[0] + v[1]) + v[2]) + v[3]))
-    for j in range(chunks * 4, len(row)):
-        acc = f(acc + row[j])
-    return acc
+    big = f(2.0 ** 24)
+    x = np.array([[1, 1, big, 0]], np.float32)
+    assert cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)[0] == big + 2
+    x = np.array([[big, 0, 0, 0, 1, 1, 0, 0]], np.float32)
+    assert cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)[0] == big + 2
+    assert cpuref.reduce_rows(x, cpuref.REDUCE_SUM)[0] == big
+    z = cpuref.reduce_rows(np.full((1, 16), -0.0, np.float32), cpuref.REDUCE_SUM_VEC4)[0]
+    assert z == 0.0 and np.signbit(z)
+    z = cpuref.reduce_rows(np.full((1, 20), -0.0, np.float32), cpuref.REDUCE_SUM_VEC4)[0]
+    assert z == 0.0 and not np.signbit(z)
+    # loop form, 17 wide: the last window adds x[16] with 3 elements of the
+    # next row; the tail adds x[16] again
+    x = np.zeros((2, 17), np.float32)
+    x[0, 16] = 1.0
+    x[1, :3] = 100.0
+    assert cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)[0] == 302.0
 
 
 @pytest.mark.parametrize("cols", [4, 7, 16, 17, 1000, 1003])
-def test_reduce_rows_vec4_order(cols):
-    x = rng(cols).normal(size=(4, cols)).astype(np.float32) * np.float32(1e3)
-    got = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
-    ref = np.array([_vec4_fold(r, cols <= 16) for r in x], np.float32)
-    np.testing.assert_array_equal(got, ref)
+def test_reduce_rows_vec4_fp64_sanity(cols):
+    x = rng(cols).normal(size=(4, cols + 4)).astype(np.float32) * np.float32(1e3)
+    x[:, cols:] = 0.0  # the loop's over-read lands on zeros: the row sum itself
+    got = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4, cols=cols)
+    ref = x[:, :cols].astype(np.float64).sum(axis=1)
+    tail = (cols % 4) if cols > 16 else 0   # the re-added elements
+    ref += x[:, (cols // 4) * 4:cols].astype(np.float64).sum(axis=1) if tail else 0.0
+    assert_close(got, ref, atol=1e-2, rtol=1e-5, what="vec4 sum vs fp64")
 
 
 def test_vec4_order_is_observable():
@@ -179,13 +245,16 @@ def test_parallel_reduce_reference_fixtures(fixtures):
 
 
 def test_parallel_reduce_partials_order():
-    a = rng(13).normal(size=3000).astype(np.float32)
-    parts = cpuref.parallel_reduce_partials(a, 3, 1000)
-    ref = np.array([_vec4_fold(a[i * 1000:(i + 1) * 1000], False) for i in range(3)], np.float32)
-    np.testing.assert_array_equal(parts, ref)
-    small = cpuref.parallel_reduce_partials(a[:24], 2, 12)  # TILE <= 16: unrolled start
-    ref = np.array([_vec4_fold(a[i * 12:(i + 1) * 12], True) for i in range(2)], np.float32)
-    np.testing.assert_array_equal(small, ref)
+    """A program's tile of the rank-1 buffer is summed as a row of the same
+    buffer viewed [programs, TILE] (the windows read on into the next tile),
+    whose order the closed-form probes above pin; TILE < 4 is the plain
+    fold from element 0."""
+    a = rng(13).normal(size=3003).astype(np.float32)
+    for tile in (1000, 1001, 12):
+        progs = a.size // tile
+        parts = cpuref.parallel_reduce_partials(a[:progs * tile], progs, tile)
+        rows = cpuref.reduce_rows(a[:progs * tile].reshape(progs, tile), cpuref.REDUCE_SUM_VEC4)
+        np.testing.assert_array_equal(parts, rows)
     tiny = cpuref.parallel_reduce_partials(a[:6], 2, 3)  # TILE < 4: plain fold
     np.testing.assert_array_equal(tiny, np.add.accumulate(a[:6].reshape(2, 3), axis=1, dtype=np.float32)[:, -1])
 
