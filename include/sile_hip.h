@@ -133,6 +133,21 @@ int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t nu
                           const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],
                           uint32_t threads_per_program, sile_hip_stream stream);
 
+/* sile_hip_launch_tiles without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc).  Same
+ * arguments, semantics and synchronous return as sile_hip_launch_tiles, but
+ * the device copies of the buffer and shape tables go into a fixed 4 KiB
+ * array of the library (one per device, held until the process ends) rather
+ * than into a buffer allocated and freed per call: num_buffers + num_shapes
+ * may not exceed 512 (SILE_ERR_SHAPE beyond).  Calls on one device share
+ * that array, so calls that overlap on one device (from several threads or
+ * streams) race; each call writes the tables it needs before its launch. */
+int sile_hip_launch_tiles_noalloc(sile_hip_function fn, void *const *buffers,
+                                  int64_t num_buffers, const int64_t *shapes, int64_t num_shapes,
+                                  const uint32_t grid[3], uint32_t threads_per_program,
+                                  sile_hip_stream stream);
+
 /* ---- generic code generation for LLIR (sile_llvm_ir::Function) ----
  * `llir_text` is a function in the reference's printed LLIR form
  * (format_llvm_ir, crates/sile-llvm-ir/src/print.rs:6-57).  It is translated

@@ -121,6 +121,7 @@ SIGNATURES = {
     "sile_hip_module_unload": [_P],
     "sile_hip_module_get": [_P, ctypes.c_char_p, ctypes.POINTER(_P)],
     "sile_hip_launch_tiles": [_P, _P, _I64, _P, _I64, _P, ctypes.c_uint32, _P],
+    "sile_hip_launch_tiles_noalloc": [_P, _P, _I64, _P, _I64, _P, ctypes.c_uint32, _P],
     "sile_hip_llir_to_hip": [ctypes.c_char_p, _I64, _I64, _I64, _P, _SZ, ctypes.POINTER(_SZ)],
     "sile_hip_llir_compile": [ctypes.c_char_p, _I64, _I64, _I64, ctypes.POINTER(_P),
                               ctypes.POINTER(_SZ), _P, _SZ],

@@ -2,9 +2,11 @@
 
 1. Each kernels/<name>.hip is compiled for gfx950 into a raw ELF code object
    sile_amd/_build/<name>.hsaco (hipcc --genco --no-gpu-bundle-output).
-2. The host runtime (runtime.cpp, ops.cpp) is compiled with g++ against the
-   HIP runtime headers; runtime.cpp assembles the code objects into the
-   library image with .incbin.
+2. The host runtime (runtime.cpp, ops.cpp, llir.cpp, tile_ir.cpp) is
+   compiled with g++ against the HIP runtime headers; runtime.cpp assembles
+   the code objects into the library image with .incbin.  launch_noalloc.hip
+   (host code plus the device array its entry point uses) is compiled by
+   hipcc for the host and gfx950.
 3. The objects are linked into sile_amd/libsile_hip.so against libamdhip64.
 
 Run: python -m sile_amd.build
@@ -29,6 +31,7 @@ ARCH = "gfx950"
 
 KERNELS = ["dsl", "softmax", "gemm", "attention", "flash_attn"]
 HOST_SOURCES = ["runtime.cpp", "ops.cpp", "llir.cpp", "tile_ir.cpp"]
+HIP_HOST_SOURCES = ["launch_noalloc.hip"]
 
 # Device code: gfx950 only; packed-fp32 instructions disabled (the compiler
 # would otherwise form v_pk_{add,mul,fma}_f32 from scalar float code).
@@ -63,6 +66,16 @@ def build_host(src_name: str) -> str:
     return obj
 
 
+def build_hip_host(src_name: str) -> str:
+    """A host source with device data of its own: hipcc, host + gfx950."""
+    src = os.path.join(CSRC, src_name)
+    obj = os.path.join(BUILD, src_name + ".o")
+    _run([HIPCC, "-c", "-fPIC", "-O2", "-std=c++17", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-Wall", "-Wno-unused-command-line-argument", src, "-o", obj])
+    return obj
+
+
 def build(verbose: bool = True) -> str:
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
@@ -71,7 +84,7 @@ def build(verbose: bool = True) -> str:
         for path in ex.map(build_kernel, KERNELS):
             if verbose:
                 print("built", os.path.relpath(path, ROOT), flush=True)
-    objs = [build_host(s) for s in HOST_SOURCES]
+    objs = [build_host(s) for s in HOST_SOURCES] + [build_hip_host(s) for s in HIP_HOST_SOURCES]
     # Export the C ABI (sile_hip_*) and nothing else.
     vscript = os.path.join(BUILD, "exports.map")
     with open(vscript, "w") as f:

@@ -192,6 +192,10 @@ int sile_hip_init(int ordinal) {
   SILE_HIP_CHECK(hipSetDevice(ordinal));
   int rc = ensure_device();
   if (rc != SILE_OK) return rc;
+  // set-up of the no-allocation launch: this device's address of its tables
+  void* scratch = nullptr;
+  rc = noalloc_scratch(&scratch);
+  if (rc != SILE_OK) return rc;
   return ok();
 }
 

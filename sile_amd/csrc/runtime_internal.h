@@ -44,6 +44,9 @@ int get_function(Module m, const char* name, hipFunction_t* out);
 // Number of workgroups of `block_threads` threads of kernel `name` that fit on
 // the whole current device at once (CUs x resident workgroups per CU).
 int resident_blocks(Module m, const char* name, int block_threads, int64_t* out);
+// The current device's address of the no-allocation launch's table array
+// (launch_noalloc.hip); looked up once per device.
+int noalloc_scratch(void** out);
 // hipModuleLaunchKernel with kernelParams.
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds = 0);

@@ -115,6 +115,13 @@ def test_op_host_validation():
     assert _abi.status("sile_hip_flash_attn_fwd", _abi.F16, 1, 1, 128, 512, 16, 16, 16, 16,
                        1.0, 1, NULL) == 2
     assert _abi.status("sile_hip_launch_tiles", None, None, 0, None, 0, None, 1, NULL) == 3
+    # the no-allocation launch: no function, and tables past its 512 entries
+    assert _abi.status("sile_hip_launch_tiles_noalloc", None, None, 0, None, 0, None, 1,
+                       NULL) == 3
+    grid = (_abi.ctypes.c_uint32 * 3)(1, 1, 1)
+    rc = _abi.status("sile_hip_launch_tiles_noalloc", 16, _abi._ptr_array([16] * 3), 3,
+                     _abi._i64_array([4] * 510), 510, grid, 64, NULL)
+    assert rc == 5 and "exceed" in _abi.last_error()
 
 
 def test_32bit_buffer_range_guards():
