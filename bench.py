@@ -276,12 +276,26 @@ def bench_softmax(name, steps, warmup, stream, traffic, cpu=False):
     def launch(i):
         hip.softmax_rows(hip.F16, hip.F16, rows, cols, xs[i].ptr, cols, ys[i].ptr, cols, stream)
 
+    def copy(i):
+        hip.copy_rows(rows, cols * 2, xs[i].ptr, cols * 2, ys[i].ptr, cols * 2, stream)
+
     log(f"[bench] {name}: timing {steps} steps")
     region = time_launches(launch, steps, warmup, stream, rotate=rotate)
     nbytes = 4.0 * rows * cols  # read 2 B + write 2 B per element
     res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS,
                     traffic.get(name))
     res["bytes_per_launch"] = nbytes
+    # the ceiling of this traffic on this box: the same bytes copied by
+    # sile_hip_copy_rows (contiguous rows: sile_copy_flat_b128, the fastest
+    # copy shape measured on the device, 16-byte non-temporal accesses and no
+    # arithmetic) over the same rotating buffers
+    log(f"[bench] {name}: timing the copy ceiling ({steps} steps)")
+    copy_ms = time_launches(copy, steps, warmup, stream, rotate=rotate) / steps
+    ceiling = nbytes / (copy_ms * 1e-3) / 1e9
+    res["copy_ceiling"] = {"kernel": "sile_copy_flat_b128", "value": round(ceiling, 2),
+                           "unit": "GB/s", "ms_per_step": round(copy_ms, 4),
+                           "frac_of_peak": round(ceiling / PEAK_HBM_GBS, 4)}
+    res["frac_of_copy_ceiling"] = round(res["value"] / ceiling, 4)
     for buf in xs + ys:
         buf.close()
     if x32 is not None:

@@ -257,6 +257,15 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
 int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, int64_t cols,
                          const void *x, int64_t ldx, float *out, sile_hip_stream stream);
 
+/* y[r][0, row_bytes) = x[r][0, row_bytes) for r < rows, rows at byte pitches
+ * ldx_bytes / ldy_bytes: the HBM move of a tile store
+ * (crates/sile-tile-ir/src/passes/lowering/tile_memory.rs:114-162) with no
+ * arithmetic, in the row softmax's access pattern (one wave per row,
+ * non-temporal 16-byte accesses when rows and pitches are multiples of 16
+ * bytes); the read + write rate it reaches bounds the row softmax's. */
+int sile_hip_copy_rows(int64_t rows, int64_t row_bytes, const void *x, int64_t ldx_bytes,
+                       void *y, int64_t ldy_bytes, sile_hip_stream stream);
+
 /* fp32 row sums in the order of the reference's fused load + reduce: the
  * CPU backend's sum of a tile it reads straight from a buffer
  * (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:31-177,

@@ -135,6 +135,7 @@ SIGNATURES = {
     "sile_hip_softmax_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _I64, _P],
     "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
     "sile_hip_reduce_rows_fused_sum": [_I64, _I64, _P, _I64, _I64, _P, _P],
+    "sile_hip_copy_rows": [_I64, _I64, _P, _I64, _P, _I64, _P],
     "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
     "sile_hip_tile_ir_route": [ctypes.c_char_p, _P, _I64, _I64, ctypes.POINTER(Route)],
     "sile_hip_tile_ir_launch": [ctypes.POINTER(Route), _P, _I64, _P, _I64, _I64, _P],
@@ -411,6 +412,10 @@ def reduce_rows(op, in_type, rows, cols, x, ldx, out, stream=None):
 
 def reduce_rows_fused_sum(rows, cols, x, ldx, x_len, out, stream=None):
     call("sile_hip_reduce_rows_fused_sum", rows, cols, x, ldx, x_len, out, _sh(stream))
+
+
+def copy_rows(rows, row_bytes, x, ldx_bytes, y, ldy_bytes, stream=None):
+    call("sile_hip_copy_rows", rows, row_bytes, x, ldx_bytes, y, ldy_bytes, _sh(stream))
 
 
 def flash_attn_fwd(dtype, batch, heads, seq_len, head_dim, q, k, v, o, scale, causal=True,

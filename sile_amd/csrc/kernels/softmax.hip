@@ -6,16 +6,19 @@
 //   m = max_c x[c]; e[c] = exp(x[c] - m); s = sum_c e[c]; y[c] = e[c] / s
 // with fp32 max, exp and sum for every input type.
 //
-// Fast path: one wave per row with the whole row held in registers, so x is
-// read from HBM once and y written once (4 bytes per fp16 element in total).
-// The 128-bit loads and stores are non-temporal (streaming data, no reuse):
-// measured 5.4 TB/s on [8192, 8192] fp16, the rate of a plain device copy.
-// Each lane owns kChunks chunks of E consecutive elements (E = 8 for 16-bit
-// inputs, 4 for fp32, one 128-bit access); chunk j of lane l starts at column
-// (j * 64 + l) * E, so every load instruction of the wave reads one
-// contiguous KiB of the row.  The max and the sum are wave all-reductions over DPP row permutes
-// (common.h).  exp(x - m) is evaluated as 2^((x - m) * log2 e) on v_exp_f32.
-// Rows are assigned four per 256-thread workgroup.
+// Every kernel reads x from HBM once and writes y once (4 bytes per fp16
+// element in total), with non-temporal 128-bit loads and stores (streaming
+// data, no reuse).  A lane's chunk is E consecutive elements (E = 8 for
+// 16-bit inputs, 4 for fp32: one 128-bit access), and each load instruction
+// of a wave reads one contiguous KiB of the row.
+//  * rows of 256 / 512 / 1024 threads x 2 chunks (4096, 8192, 16384 16-bit
+//    or 2048, 4096, 8192 fp32 elements): one row per workgroup, the shape of
+//    the fastest copy measured on the device; the row max and sum are wave
+//    all-reductions plus one exchange of per-wave partials through LDS;
+//  * other widths: one wave per row with the row in registers (whole chunks,
+//    or a masked last chunk), or a three-pass kernel for rows past 8192.
+// Wave all-reductions use DPP row permutes (common.h); exp(x - m) is
+// 2^((x - m) * log2 e) on v_exp_f32.
 #include "common.h"
 
 using namespace sile;
@@ -163,79 +166,6 @@ __device__ __forceinline__ void softmax_row_regs(const typename Elem<kIn>::Stora
   }
 }
 
-// ---- 16-bit row softmax holding the row packed: cols == kChunks * 512 ----
-// The row stays in registers as raw 16-bit pairs (4 VGPRs per chunk instead of
-// 8), and exp(x - m) is evaluated twice (for the sum, then for the output),
-// so a wave needs about half the registers of softmax_row_regs and more waves
-// (more bytes of row in flight) fit on a SIMD.
-template <int kT>
-SILE_DEV void unpack8(const u32x4& w, float v[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t u = w[i];
-    if constexpr (kT == kF16) {
-      const f16x2 h = __builtin_bit_cast(f16x2, u);
-      v[2 * i] = (float)h[0];
-      v[2 * i + 1] = (float)h[1];
-    } else {
-      v[2 * i] = bits_f32(u << 16);
-      v[2 * i + 1] = bits_f32(u & 0xffff0000u);
-    }
-  }
-}
-
-template <int kT, int kChunks>
-__device__ __forceinline__ void softmax_row_packed(const uint16_t* __restrict__ xr,
-                                                   uint16_t* __restrict__ yr, int lane) {
-  u32x4 w[kChunks];
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j)
-    w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + (j * 64 + lane) * 8));
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j) {
-    float v[8];
-    unpack8<kT>(w[j], v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmax_ordered(m, v[i]);
-  }
-  m = wave_max(m);
-  // Opaque to the optimiser: without it the conversions of the first pass are
-  // kept alive for the later ones, which is the register cost this kernel avoids.
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j) asm volatile("" : "+v"(w[j]));
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j) {
-    float v[8];
-    unpack8<kT>(w[j], v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += exp2_fast((v[i] - m) * kLog2e);
-  }
-  s = wave_sum(s);
-  const float inv = 1.0f / s;
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j) asm volatile("" : "+v"(w[j]));
-#pragma unroll
-  for (int j = 0; j < kChunks; ++j) {
-    float v[8];
-    unpack8<kT>(w[j], v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = exp2_fast((v[i] - m) * kLog2e) * inv;
-    Elem<kT>::store8(yr + (j * 64 + lane) * 8, v);
-  }
-}
-
-template <int kT, int kChunks>
-__device__ __forceinline__ void softmax_rows_packed_kernel(const void* x, void* y, int64_t rows,
-                                                           int64_t ldx, int64_t ldy) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  softmax_row_packed<kT, kChunks>(static_cast<const uint16_t*>(x) + row * ldx,
-                                  static_cast<uint16_t*>(y) + row * ldy, lane);
-}
-
 // ---- register-resident row softmax of any width up to kChunks * 64 * E ----
 // Chunks wholly inside the row are 128-bit accesses; the one chunk the row
 // ends in is read and written element by element; positions past the row are
@@ -376,15 +306,79 @@ SILE_SOFTMAX_MASKED_WIDTHS(f32_f32, kF32, kF32)
 SILE_SOFTMAX_MASKED(sile_softmax_rows_f32_f32_m32, kF32, kF32, 32)
 SILE_SOFTMAX_MASKED_WIDTHS(f16_f32, kF16, kF32)
 
-#define SILE_SOFTMAX_PACKED(NAME, T, CH)                                                     \
-  extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows, \
-                                                         int64_t ldx, int64_t ldy) {         \
-    softmax_rows_packed_kernel<T, CH>(x, y, rows, ldx, ldy);                                 \
+
+// ---- one row per workgroup: cols == kThreads * kChunks * E ----
+// The copy shape that moves the most bytes on MI355X (two 16-byte chunks per
+// thread, 256-512 threads per 8-16 KiB) with the softmax's arithmetic in
+// between: chunk j of thread t at column (j * kThreads + t) * E, loaded
+// non-temporally, reduced to the row max and the row sum through a wave
+// all-reduction and one exchange of the per-wave partials in LDS each, then
+// exp, normalised and stored non-temporally.  The row is read once and
+// written once, as in the wave-per-row kernels, but each wave keeps only
+// kChunks chunks in flight and many more waves run.
+template <int kIn, int kOut, int kThreads, int kChunks>
+__device__ __forceinline__ void softmax_rows_block_kernel(const void* x, void* y, int64_t rows,
+                                                          int64_t ldx, int64_t ldy) {
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  constexpr int kWaves = kThreads / 64;
+  __shared__ float part[2][kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  TO* yr = static_cast<TO*>(y) + row * ldy;
+  float v[kChunks][kE];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) load_chunk<kIn, kE>(xr + (j * kThreads + t) * kE, v[j]);
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) m = fmax_ordered(m, v[j][i]);
+  m = wave_max(m);
+  if (lane == 0) part[0][wave] = m;
+  __syncthreads();
+  m = part[0][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmax_ordered(m, part[0][w]);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      v[j][i] = exp2_fast((v[j][i] - m) * kLog2e);
+      s += v[j][i];
+    }
+  s = wave_sum(s);
+  if (lane == 0) part[1][wave] = s;
+  __syncthreads();
+  s = part[1][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) s += part[1][w];
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+#pragma unroll
+    for (int i = 0; i < kE; ++i) v[j][i] = normalise<kOut>(v[j][i], s, inv);
+    store_chunk<kOut, kE>(yr + (j * kThreads + t) * kE, v[j]);
   }
-SILE_SOFTMAX_PACKED(sile_softmax_rows_f16_f16_p8, kF16, 8)
-SILE_SOFTMAX_PACKED(sile_softmax_rows_f16_f16_p16, kF16, 16)
-SILE_SOFTMAX_PACKED(sile_softmax_rows_bf16_bf16_p8, kBF16, 8)
-SILE_SOFTMAX_PACKED(sile_softmax_rows_bf16_bf16_p16, kBF16, 16)
+}
+
+#define SILE_SOFTMAX_BLOCK(NAME, IN, OUT, T)                                                 \
+  extern "C" __global__ __launch_bounds__(T) void NAME(const void* x, void* y, int64_t rows,   \
+                                                       int64_t ldx, int64_t ldy) {           \
+    softmax_rows_block_kernel<IN, OUT, T, 2>(x, y, rows, ldx, ldy);                          \
+  }
+#define SILE_SOFTMAX_BLOCK_WIDTHS(TAG, IN, OUT)                    \
+  SILE_SOFTMAX_BLOCK(sile_softmax_rows_##TAG##_b256, IN, OUT, 256) \
+  SILE_SOFTMAX_BLOCK(sile_softmax_rows_##TAG##_b512, IN, OUT, 512) \
+  SILE_SOFTMAX_BLOCK(sile_softmax_rows_##TAG##_b1024, IN, OUT, 1024)
+SILE_SOFTMAX_BLOCK_WIDTHS(f16_f16, kF16, kF16)
+SILE_SOFTMAX_BLOCK_WIDTHS(bf16_bf16, kBF16, kBF16)
+SILE_SOFTMAX_BLOCK_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_BLOCK_WIDTHS(f16_f32, kF16, kF32)
 
 // ---- row reduce (ReduceMax / ReduceSum along axis 1), fp32 result ----
 // op 0 = max (order-independent, so identical to the reference's fold),
@@ -477,4 +471,62 @@ extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32
     for (int64_t c = chunks * 4; c < cols; ++c) acc = acc + xr[c];
   }
   out[row] = acc;
+}
+
+// ---- 2-D copy: y[r][0, row_bytes) = x[r][0, row_bytes) ----
+// Workgroup (r, s) of the grid copies segment s of row r: kCopySegB bytes, two 16-byte
+// chunks per thread of 512 (chunk j of thread t at (j * 512 + t) * 16), both
+// loaded (non-temporal) before either is stored, so each load or store
+// instruction of a wave covers one contiguous KiB.  Of the copy shapes
+// measured on MI355X (chunks per thread 1-16, 128-1024 threads, one wave per
+// row, grid-stride; buffer loads / stores with every cache-policy
+// combination), this one moved the most bytes: 6.25-6.35 TB/s for 128 MiB
+// each way.  Rows and pitches are multiples of 16 bytes (checked by the host).
+constexpr int kCopyThreads = 512;
+constexpr int kCopySegB = kCopyThreads * 2 * 16;
+extern "C" __global__ __launch_bounds__(kCopyThreads) void sile_copy_rows_b128(
+    const uint8_t* __restrict__ x, uint8_t* __restrict__ y, int64_t rows, int64_t row_bytes,
+    int64_t ldx, int64_t ldy) {
+  const int64_t row = blockIdx.x, seg = blockIdx.y;
+  if (row >= rows) return;
+  const uint8_t* xr = x + row * ldx + seg * kCopySegB;
+  uint8_t* yr = y + row * ldy + seg * kCopySegB;
+  const int64_t n = (row_bytes - seg * kCopySegB) >> 4;  // chunks of this segment and beyond
+  const int t = threadIdx.x;
+  u32x4 w[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (j * kCopyThreads + t < n)
+      w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + (j * kCopyThreads + t) * 16));
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (j * kCopyThreads + t < n)
+      __builtin_nontemporal_store(w[j], reinterpret_cast<u32x4*>(yr + (j * kCopyThreads + t) * 16));
+}
+
+// Contiguous rows (pitch == row bytes): the matrix is one run of `chunks`
+// 16-byte chunks, workgroup b copying chunks [b * 1024, b * 1024 + 1024).
+extern "C" __global__ __launch_bounds__(kCopyThreads) void sile_copy_flat_b128(
+    const uint8_t* __restrict__ x, uint8_t* __restrict__ y, int64_t chunks) {
+  const int64_t c0 = (int64_t)blockIdx.x * (2 * kCopyThreads) + threadIdx.x;
+  u32x4 w[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (c0 + j * kCopyThreads < chunks)
+      w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x) + c0 + j * kCopyThreads);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (c0 + j * kCopyThreads < chunks)
+      __builtin_nontemporal_store(w[j], reinterpret_cast<u32x4*>(y) + c0 + j * kCopyThreads);
+}
+
+// Rows or pitches that are not multiples of 16 bytes: one byte per lane.
+extern "C" __global__ __launch_bounds__(256) void sile_copy_rows_b8(const uint8_t* x, uint8_t* y,
+                                                                   int64_t rows,
+                                                                   int64_t row_bytes, int64_t ldx,
+                                                                   int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  for (int64_t c = lane; c < row_bytes; c += 64) y[row * ldy + c] = x[row * ldx + c];
 }

@@ -314,9 +314,19 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
   }
   char name[64];
   int rc;
-  // 16-bit rows of 4096 / 8192: the packed-row kernel (see softmax.hip)
-  const bool packed = (chunks == 8 || chunks == 16) &&
-                      (!strcmp(tag, "f16_f16") || !strcmp(tag, "bf16_bf16"));
+  // rows of 256 / 512 / 1024 threads x 2 chunks: one row per workgroup
+  int block_threads = 0;
+  if (vec_ok) {
+    for (int t : {256, 512, 1024})
+      if (cols == (int64_t)t * 2 * elems) block_threads = t;
+  }
+  if (block_threads) {
+    if (rows > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_b%d", tag, block_threads);
+    void* params[] = {&x, &y, &rows, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)rows), dim3(block_threads), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
   // other widths up to 8192 (16-bit) / 8192 (fp32): one pass with a masked
   // last chunk, the smallest power-of-two chunk count that covers the row
   int masked = 0;
@@ -324,11 +334,7 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
     for (int c : {1, 2, 4, 8, 16, 32})
       if (!masked && cols <= (int64_t)c * 64 * elems && (c < 32 || f32_rows)) masked = c;
   }
-  if (packed) {
-    snprintf(name, sizeof name, "sile_softmax_rows_%s_p%d", tag, chunks);
-    void* params[] = {&x, &y, &rows, &ldx, &ldy};
-    rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
-  } else if (masked) {
+  if (masked) {
     snprintf(name, sizeof name, "sile_softmax_rows_%s_m%d", tag, masked);
     void* params[] = {&x, &y, &rows, &cols, &ldx, &ldy};
     rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
@@ -367,6 +373,37 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
   int vec = aligned16(x) && (ldx * (int64_t)dtype_bytes(in_type)) % 16 == 0 ? 1 : 0;
   void* params[] = {&iop, &vec, &x, &out, &rows, &cols, &ldx};
   int rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params,
+                  static_cast<hipStream_t>(stream));
+  return rc == SILE_OK ? ok() : rc;
+}
+
+int sile_hip_copy_rows(int64_t rows, int64_t row_bytes, const void* x, int64_t ldx_bytes,
+                       void* y, int64_t ldy_bytes, sile_hip_stream stream) {
+  if (rows < 0 || row_bytes < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (rows == 0 || row_bytes == 0) return ok();
+  if (!x || !y) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldx_bytes < row_bytes || ldy_bytes < row_bytes)
+    return fail(SILE_ERR_SHAPE, "pitch smaller than the row");
+  const bool vec = row_bytes % 16 == 0 && ldx_bytes % 16 == 0 && ldy_bytes % 16 == 0 &&
+                   aligned16(x) && aligned16(y);
+  if (vec && ldx_bytes == row_bytes && ldy_bytes == row_bytes) {
+    // contiguous rows: one flat run of 16-byte chunks, 16 KiB per workgroup
+    int64_t chunks = rows * (row_bytes / 16);
+    const int64_t groups = (chunks + 1023) / 1024;
+    if (groups > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "copy too large");
+    void* params[] = {(void*)&x, &y, &chunks};
+    int rc = launch(Module::kSoftmax, "sile_copy_flat_b128", dim3((unsigned)groups), dim3(512),
+                    params, static_cast<hipStream_t>(stream));
+    return rc == SILE_OK ? ok() : rc;
+  }
+  // 16-byte path: one workgroup of 512 threads per 16 KiB segment of a row
+  // (grid rows x segments); byte path: one wave per row
+  const int64_t segs = vec ? (row_bytes + 16383) / 16384 : 1;
+  const int64_t blocks = vec ? rows : (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL || segs > 65535) return fail(SILE_ERR_SHAPE, "too many rows");
+  void* params[] = {(void*)&x, &y, &rows, &row_bytes, &ldx_bytes, &ldy_bytes};
+  int rc = launch(Module::kSoftmax, vec ? "sile_copy_rows_b128" : "sile_copy_rows_b8",
+                  dim3((unsigned)blocks, (unsigned)segs), dim3(vec ? 512 : 256), params,
                   static_cast<hipStream_t>(stream));
   return rc == SILE_OK ? ok() : rc;
 }
