@@ -241,6 +241,20 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
                   int64_t ldb, sile_layout b_layout, void *c, int64_t ldc, float scale_a,
                   float scale_b, int64_t bk, sile_hip_stream stream);
 
+/* fp32 tile MMA with a seeded accumulator, in the reference's exact order:
+ * C[r][c] = the chain s = s + A[r][k] * B[k][c] over k < K' (K' = (K / bk) * bk,
+ * bk <= 0: K), the product and the sum rounded separately, starting from
+ * s = acc[r * ld_acc + c] (acc != NULL; acc may be C itself, for C += A.B) or
+ * from s = acc_value.  This is MmaF lowered with an accumulator that is a
+ * loaded tile or a constant splat (crates/sile-tile-ir/src/passes/lowering/tile_compute/mma.rs:25-260,
+ * 262-739, seeds at :213-229 and :483-558; plan crates/sile-tile-ir/src/passes/lowering/block.rs:294-377);
+ * acc_value = 0.0f with acc = NULL is the canonical matmul.  A row-major
+ * [M, K]; B row-major [K, N] or column-major.  Bit-identical to the CPU
+ * backend. */
+int sile_hip_mma_f32(int64_t m, int64_t n, int64_t k, const float *a, int64_t lda, const float *b,
+                     int64_t ldb, sile_layout b_layout, const float *acc, int64_t ld_acc,
+                     float acc_value, float *c, int64_t ldc, int64_t bk, sile_hip_stream stream);
+
 /* Row softmax of a [rows, cols] matrix: y = exp(x - max) / sum(exp(x - max))
  * per row with fp32 max/exp/sum (the softmax DSL kernel with BN = cols,
  * crates/sile/tests/backend_softmax.rs:3-15).  in/out dtypes: f16->f16,
@@ -300,7 +314,8 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
  * (sile_hip_llir_compile) only on SILE_ROUTE_NONE. */
 typedef enum {
   SILE_ROUTE_NONE = 0,          /* no hand-written kernel: use the LLIR code generation */
-  SILE_ROUTE_MATMUL = 1,        /* canonical matmul -> sile_hip_kernel_matmul (bit-identical) */
+  SILE_ROUTE_MATMUL = 1,        /* canonical matmul, or the tile MMA loop from a splat or a
+                                   loaded accumulator -> the matmul tile kernel (bit-identical) */
   SILE_ROUTE_SOFTMAX_ROWS = 2,  /* softmax chain, one tile per row band -> sile_hip_softmax_rows */
   SILE_ROUTE_SOFTMAX_TILES = 3, /* softmax chain, other tilings -> sile_hip_kernel_softmax */
   SILE_ROUTE_REDUCE_ROWS = 4,   /* load + reduce(axis 1) + store -> sile_hip_reduce_rows */
@@ -310,12 +325,15 @@ typedef enum {
 typedef struct {
   int32_t kind;              /* sile_route_kind */
   int32_t reduce_op;         /* SILE_ROUTE_REDUCE_ROWS: sile_reduce_op */
-  int32_t buffer[3];         /* kernel-parameter index of each operand: inputs, then output */
-  int32_t shape_offset[3];   /* offset of each operand's dims in `shapes` */
-  int32_t rank[3];           /* rank of each operand (0: unused) */
+  int32_t buffer[4];         /* kernel-parameter index of each operand: inputs, then output,
+                                then (matmul) the buffer the accumulator tile is loaded from */
+  int32_t shape_offset[4];   /* offset of each operand's dims in `shapes` */
+  int32_t rank[4];           /* rank of each operand (0: unused) */
   int32_t num_buffers;       /* buffer parameters of the kernel */
+  int32_t seed_from_tile;    /* SILE_ROUTE_MATMUL: 1 = accumulator loaded from operand 3 */
+  float seed_value;          /* SILE_ROUTE_MATMUL: the accumulator's splat value otherwise */
   int64_t num_shapes;        /* shape values the route was made with */
-  int64_t operand_shapes[6]; /* the operands' dims the route was made for */
+  int64_t operand_shapes[8]; /* the operands' dims the route was made for */
   int64_t num_threadgroups;  /* the grid the route was made for */
   int64_t tile_m, tile_n, tile_k; /* BM, BN, BK (TILE in tile_n for the atomic reduce) */
   int64_t rows, cols;        /* extents handed to the row kernels */

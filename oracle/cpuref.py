@@ -54,6 +54,8 @@ def lib() -> ctypes.CDLL:
         L.cpuref_kernel_parallel_reduce.argtypes = [_P, _I64, _I64, _P, _I64, _I64]
         L.cpuref_parallel_reduce_partials.argtypes = [_P, _P, _I64, _I64, _I64]
         L.cpuref_gemm_nt.argtypes = [_P, _P, _P] + [_I64] * 9
+        L.cpuref_mma_f32.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_int,
+                                     _I64, ctypes.c_float, _I64, _I64]
         L.cpuref_reduce_rows.argtypes = [ctypes.c_int, _P, _P, _I64, _I64, _I64, _I64]
         L.cpuref_softmax_rows.argtypes = [_P, _P, _I64, _I64, _I64, _I64]
         L.cpuref_attention_fwd.argtypes = [_P, _P, _P, _P, _I64, _I64, ctypes.c_float,
@@ -134,6 +136,23 @@ def gemm_nt(a, bt, bk=0, bm=1, row_tile_step=1, out=None):
     n = bt.shape[0]
     c = np.zeros((m, n), dtype=np.float32) if out is None else out
     lib().cpuref_gemm_nt(_ptr(a), _ptr(bt), _ptr(c), m, n, k, k, k, n, bk, bm, row_tile_step)
+    return c
+
+
+def mma_f32(a, b, acc=None, acc_value=0.0, bk=0, b_col_major=False, out=None):
+    """The seeded tile-MMA chain over a whole [M, N] result: C = fold from
+    acc (or the constant acc_value) through A[r][k] * B[k][c] in increasing k.
+    b is [K, N] row-major, or [N, K] when b_col_major."""
+    a, b = _f32(a), _f32(b)
+    m, k = a.shape
+    n = b.shape[0] if b_col_major else b.shape[1]
+    c = np.zeros((m, n), dtype=np.float32) if out is None else out
+    accp, ld_acc = None, 0
+    if acc is not None:
+        acc = _f32(acc)
+        accp, ld_acc = _ptr(acc), acc.shape[1]
+    lib().cpuref_mma_f32(_ptr(a), _ptr(b), accp, _ptr(c), m, n, k, k, b.shape[1], int(b_col_major),
+                         ld_acc, float(acc_value), c.shape[1], bk)
     return c
 
 

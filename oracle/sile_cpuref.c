@@ -21,10 +21,16 @@
  * literal fixtures in tests/golden/, closed forms and float64 brute force):
  *   cpuref_kernel_matmul          pinned (reference fixture + exact integer GEMMs + order check)
  *   cpuref_kernel_softmax         pinned (reference fixture row sums, closed forms, fp64)
- *   cpuref_kernel_parallel_reduce pinned (reference fixture, closed form n(n+1)/2, vec4 order check)
+ *   cpuref_kernel_parallel_reduce pinned (reference fixture, closed form n(n+1)/2; TILE = 18
+ *                                 ones give 22 per program, 20 for the last)
  *   cpuref_gemm_nt                pinned (equals cpuref_kernel_matmul on transposed B; fp64)
+ *   cpuref_mma_f32                pinned (seed 0 equals cpuref_kernel_matmul; exact integer
+ *                                 seeds + products; a 2^24 order probe that fails for a seed
+ *                                 added last; signed-zero seeds with K' = 0)
  *   cpuref_softmax_rows           pinned (same program body as cpuref_kernel_softmax)
- *   cpuref_reduce_rows            pinned (max exact vs numpy; sum order vs explicit fold)
+ *   cpuref_reduce_rows            pinned (max exact vs numpy; sequential sum vs a left fold;
+ *                                 the vec4 loop's windows, tail and over-read by closed forms
+ *                                 over ones and order probes)
  *   cpuref_attention_causal       pinned by closed forms and fp64 brute force only; the
  *                                 reference has no attention kernel (no mask/iota/transpose
  *                                 in its DSL), so there is no reference vector for it.
@@ -141,6 +147,38 @@ void cpuref_gemm_nt(const float *a, const float *bt, float *c, int64_t m, int64_
         s = s + p;
       }
       c[row * ldc + col] = s;
+    }
+  }
+}
+
+/* Tile MMA with a seeded accumulator (a2):
+ * crates/sile-tile-ir/src/passes/lowering/tile_compute/mma.rs.  Per k-step
+ * (one MmaF of a tile_k-deep slice) every cell runs sum = acc[r][c];
+ * sum = sum + (a[r][k] * b[k][c]) for k < tile_k; acc[r][c] = sum (the
+ * unfused form :25-260, init :213-229; the fused form :262-739 reads the same
+ * values straight from the buffers, :483-558 seeding the first k-step of a
+ * LoopCarriedSplat from its constant).  Over the k loop of a kernel the
+ * accumulator therefore carries one sequential chain per cell, from its seed
+ * (a loaded tile, or the splat value) through every product in increasing k,
+ * two roundings per step.  This function computes that chain over k < K'
+ * ((K / bk) * bk, bk <= 0: K) for a whole [M, N] result:
+ *   C[r][c] = fold(acc ? acc[r * ld_acc + c] : acc_value, A[r][k] * B[k][c])
+ * with B row-major [K, N] (b_col_major = 0, the reference's layout) or
+ * column-major (stored [N, K]).  acc may alias c. */
+void cpuref_mma_f32(const float *a, const float *b, const float *acc, float *c, int64_t m,
+                    int64_t n, int64_t k, int64_t lda, int64_t ldb, int b_col_major,
+                    int64_t ld_acc, float acc_value, int64_t ldc, int64_t bk) {
+  const int64_t kp = bk > 0 ? (k / bk) * bk : k;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < m; ++r) {
+    for (int64_t cc = 0; cc < n; ++cc) {
+      float s = acc ? acc[r * ld_acc + cc] : acc_value;
+      for (int64_t kk = 0; kk < kp; ++kk) {
+        const float bv = b_col_major ? b[cc * ldb + kk] : b[kk * ldb + cc];
+        float p = a[r * lda + kk] * bv;
+        s = s + p;
+      }
+      c[r * ldc + cc] = s;
     }
   }
 }

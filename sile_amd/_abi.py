@@ -75,12 +75,14 @@ class Route(ctypes.Structure):
     _fields_ = [
         ("kind", ctypes.c_int32),
         ("reduce_op", ctypes.c_int32),
-        ("buffer", ctypes.c_int32 * 3),
-        ("shape_offset", ctypes.c_int32 * 3),
-        ("rank", ctypes.c_int32 * 3),
+        ("buffer", ctypes.c_int32 * 4),
+        ("shape_offset", ctypes.c_int32 * 4),
+        ("rank", ctypes.c_int32 * 4),
         ("num_buffers", ctypes.c_int32),
+        ("seed_from_tile", ctypes.c_int32),
+        ("seed_value", ctypes.c_float),
         ("num_shapes", ctypes.c_int64),
-        ("operand_shapes", ctypes.c_int64 * 6),
+        ("operand_shapes", ctypes.c_int64 * 8),
         ("num_threadgroups", ctypes.c_int64),
         ("tile_m", ctypes.c_int64),
         ("tile_n", ctypes.c_int64),
@@ -132,6 +134,8 @@ SIGNATURES = {
     "sile_hip_kernel_parallel_reduce": [_P, _I64, _I64, _P, _I64, _I64, _P, _P],
     "sile_hip_gemm": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32, _P,
                       _I64, _F32, _F32, _I64, _P],
+    "sile_hip_mma_f32": [_I64, _I64, _I64, _P, _I64, _P, _I64, _I32, _P, _I64, _F32, _P, _I64, _I64,
+                         _P],
     "sile_hip_softmax_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _I64, _P],
     "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
     "sile_hip_reduce_rows_fused_sum": [_I64, _I64, _P, _I64, _I64, _P, _P],
@@ -400,6 +404,11 @@ def gemm(a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout, c,
          scale_a=1.0, scale_b=1.0, bk=0, stream=None):
     call("sile_hip_gemm", a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout,
          c, ldc, scale_a, scale_b, bk, _sh(stream))
+
+
+def mma_f32(m, n, k, a, lda, b, ldb, b_layout, acc, ld_acc, acc_value, c, ldc, bk=0, stream=None):
+    call("sile_hip_mma_f32", m, n, k, a, lda, b, ldb, b_layout, acc, ld_acc, acc_value, c, ldc, bk,
+         _sh(stream))
 
 
 def softmax_rows(in_type, out_type, rows, cols, x, ldx, y, ldy, stream=None):

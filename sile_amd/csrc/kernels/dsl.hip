@@ -13,16 +13,22 @@ struct MatmulTileArgs {
   int64_t bm, bn, bk;     // const generics of the DSL kernel
   int64_t tiles_n;        // shape(c)[1] / BN
   int64_t total;          // (shape(c)[0] / BM) * tiles_n
+  const float* seed;      // accumulator tile source (row stride ld_seed), or NULL
+  int64_t ld_seed;
+  float seed_value;       // the accumulator's splat value when seed is NULL
 };
 
-// Canonical matmul program (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444):
-// every cell sums a[.]*b[.] from 0.0f in increasing k with a separate rounding
-// for the product and for the add, over k < (lda / BK) * BK.  Threads own
+// Matmul program (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:24-444
+// and the tile MMA lowering, crates/sile-tile-ir/src/passes/lowering/tile_compute/mma.rs:25-739):
+// every cell sums a[.]*b[.] in increasing k with a separate rounding for the
+// product and for the add, over k < (lda / BK) * BK, starting from the
+// accumulator's seed: 0.0f for the canonical matmul, the splat value, or the
+// cell of a loaded accumulator tile (which may be c's own tile).  Threads own
 // cells; each cell keeps the reference's sequential order, so results are
 // bit-identical to the CPU backend's.
 extern "C" __global__ __launch_bounds__(256) void sile_dsl_matmul_f32(const float* __restrict__ a,
                                                                        const float* __restrict__ b,
-                                                                       float* __restrict__ c,
+                                                                       float* c,
                                                                        MatmulTileArgs args) {
 #pragma clang fp contract(off)
   const int64_t pid = blockIdx.x;
@@ -35,7 +41,8 @@ extern "C" __global__ __launch_bounds__(256) void sile_dsl_matmul_f32(const floa
     const int64_t r = cell / args.bn, cc = cell % args.bn;
     const float* ap = a + row0 * args.lda + r * args.lda;
     const float* bp = b + col0 + cc;
-    float s = 0.0f;
+    float s = args.seed ? args.seed[row0 * args.ld_seed + col0 + r * args.ld_seed + cc]
+                        : args.seed_value;
     for (int64_t k = 0; k < kp; ++k) {
       float p = ap[k] * bp[0];
       s = s + p;

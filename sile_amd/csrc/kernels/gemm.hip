@@ -504,9 +504,13 @@ extern "C" __global__ __launch_bounds__(256) void sile_gemm_zero_c(uint16_t* C, 
 // loads issued two k-tiles ahead into two register sets, 16-byte loads where a
 // thread's run of a row is inside the operand), A and a column-major B
 // transposed on the way in so a thread reads its 8 rows / 8 columns of one k as
-// two 16-byte LDS reads.  Outside M, N and K' the staged values are zero: a padded term
-// adds +0.0f, which leaves every sum unchanged (a sum that starts at +0.0f
-// and adds products never becomes -0.0f).
+// two 16-byte LDS reads.  Outside M, N and K' the staged A values are -0.0f and
+// the staged B values +0.0f, so a padded term adds -0.0f, which leaves every
+// sum unchanged (x + -0.0f == x for every x, +0.0f and -0.0f included).
+// The chain starts from its seed: S[m][n] when S is given (the reference's
+// tile MMA seeded from an accumulator tile, mma.rs:213-229; S may be C
+// itself), otherwise the constant `seed` (0.0f for the canonical matmul, the
+// splat value of a LoopCarriedSplat accumulator, mma.rs:483-558).
 namespace f32t {
 constexpr int kPad = 4;
 }
@@ -517,10 +521,10 @@ constexpr int kPad = 4;
 // 35 -> 32 us at 512^3, while 32-deep tiles made 64-wide ones slower)
 template <bool kBCol, int kT>
 __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
-                                                    const float* __restrict__ B,
-                                                    float* __restrict__ C, int64_t M, int64_t N,
-                                                    int64_t kp, int64_t lda, int64_t ldb,
-                                                    int64_t ldc) {
+                                                    const float* __restrict__ B, float* C,
+                                                    int64_t M, int64_t N, int64_t kp, int64_t lda,
+                                                    int64_t ldb, int64_t ldc, const float* S,
+                                                    int64_t lds, float seed) {
 #pragma clang fp contract(off)
   using namespace f32t;
   constexpr int kK = kT == 32 ? 64 : 16;  // k-tile depth
@@ -553,7 +557,7 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
 #pragma unroll
       for (int i = 0; i < kL; ++i) {
         const int64_t k = k0 + la_k + i;
-        ra[i] = (am < M && k < kp) ? A[am * lda + k] : 0.0f;
+        ra[i] = (am < M && k < kp) ? A[am * lda + k] : -0.0f;
       }
     }
     if constexpr (kBCol) {
@@ -617,7 +621,10 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
 #pragma unroll
   for (int i = 0; i < kR; ++i)
 #pragma unroll
-    for (int j = 0; j < kR; ++j) acc[i][j] = 0.0f;
+    for (int j = 0; j < kR; ++j) {
+      const int64_t m = m0 + kR * tm + i, n = n0 + kR * tn + j;
+      acc[i][j] = (S && m < M && n < N) ? S[m * lds + n] : seed;
+    }
 
   const int64_t ktiles = (kp + kK - 1) / kK;
   if (ktiles > 0) {
@@ -673,9 +680,10 @@ __device__ __forceinline__ void gemm_f32_tiled_body(const float* __restrict__ A,
 
 #define SILE_GEMM_F32_TILED(NAME, BCOL, T)                                                     \
   extern "C" __global__ __launch_bounds__(256, 2) void NAME(                                   \
-      const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,        \
-      int64_t M, int64_t N, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc) {             \
-    gemm_f32_tiled_body<BCOL, T>(A, B, C, M, N, kp, lda, ldb, ldc);                           \
+      const float* __restrict__ A, const float* __restrict__ B, float* C, int64_t M,          \
+      int64_t N, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc, const float* S,           \
+      int64_t lds, float seed) {                                                               \
+    gemm_f32_tiled_body<BCOL, T>(A, B, C, M, N, kp, lda, ldb, ldc, S, lds, seed);             \
   }
 SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nn_t128, false, 128)
 SILE_GEMM_F32_TILED(sile_gemm_f32_exact_nn_t64, false, 64)

@@ -21,11 +21,14 @@ namespace {
 // about 1024 workgroups (4 per CU), or 32.
 int launch_f32_exact(bool b_col_major, const void* a, const void* b, void* c, int64_t m,
                      int64_t n, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc,
-                     hipStream_t s);
+                     const float* seed, int64_t ld_seed, float seed_value, hipStream_t s);
 
 // Kernel argument blocks; layouts match the structs in kernels/*.hip.
 struct MatmulTileArgs {
   int64_t lda, ldb, ldc, bm, bn, bk, tiles_n, total;
+  const float* seed;
+  int64_t ld_seed;
+  float seed_value;
 };
 struct SoftmaxTileArgs {
   int64_t ldx, ldy, bm, bn, tiles_n, total;
@@ -91,12 +94,27 @@ int sile_hip_kernel_matmul(void* const* buffers, int64_t num_threadgroups,
   if (!buffers || !shapes || num_shapes != 6)
     return fail(SILE_ERR_SHAPE, "matmul expects 3 buffers and 6 shape values (got %lld)",
                 (long long)num_shapes);
+  return kernel_matmul_seeded(buffers, num_threadgroups, threads_per_group, shapes, bm, bn, bk,
+                              nullptr, nullptr, 0.0f, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace sile_rt {
+
+int kernel_matmul_seeded(void* const* buffers, int64_t num_threadgroups, int64_t threads_per_group,
+                         const int64_t* shapes, int64_t bm, int64_t bn, int64_t bk,
+                         const float* seed, const int64_t* seed_shape, float seed_value,
+                         hipStream_t s) {
+  if (!buffers || !shapes) return fail(SILE_ERR_SHAPE, "NULL buffers / shapes");
   if (bm <= 0 || bn <= 0 || bk <= 0) return fail(SILE_ERR_SHAPE, "BM, BN, BK must be positive");
   const int64_t a0 = shapes[0], a1 = shapes[1], b0 = shapes[2], b1 = shapes[3], c0 = shapes[4],
                 c1 = shapes[5];
   if (a0 < 0 || a1 < 0 || b0 < 0 || b1 < 0 || c0 < 0 || c1 < 0)
     return fail(SILE_ERR_SHAPE, "negative extent");
-  MatmulTileArgs t{a1, b1, c1, bm, bn, bk, c1 / bn, 0};
+  if (seed && (!seed_shape || seed_shape[0] < 0 || seed_shape[1] < 0))
+    return fail(SILE_ERR_SHAPE, "accumulator tile source without a valid shape");
+  MatmulTileArgs t{a1, b1, c1, bm, bn, bk, c1 / bn, 0, seed, seed ? seed_shape[1] : 0, seed_value};
   t.total = (c0 / bm) * t.tiles_n;
   int64_t run = 0;
   int rc = programs_to_run(num_threadgroups, threads_per_group, t.total, &run);
@@ -113,14 +131,18 @@ int sile_hip_kernel_matmul(void* const* buffers, int64_t num_threadgroups,
                 "%lld programs (BM=%lld BN=%lld BK=%lld)",
                 (long long)a0, (long long)a1, (long long)b0, (long long)b1, (long long)c0,
                 (long long)c1, (long long)run, (long long)bm, (long long)bn, (long long)bk);
+  if (seed && (seed_shape[0] < rows_needed || seed_shape[1] < cols_needed))
+    return fail(SILE_ERR_SHAPE,
+                "accumulator source [%lld,%lld] does not cover the tiles of %lld programs",
+                (long long)seed_shape[0], (long long)seed_shape[1], (long long)run);
   const void* a = buffers[0];
   const void* b = buffers[1];
   void* c = buffers[2];
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (run == t.total && (c0 / bm) * bm <= 65535LL * 32) {
     // every tile runs: the tiles form the rectangle [0, M') x [0, N') of C,
     // computed by the register-tiled kernel in the same per-cell order
-    rc = launch_f32_exact(false, a, b, c, (c0 / bm) * bm, t.tiles_n * bn, kp, a1, b1, c1, s);
+    rc = launch_f32_exact(false, a, b, c, (c0 / bm) * bm, t.tiles_n * bn, kp, a1, b1, c1, seed,
+                          t.ld_seed, seed_value, s);
     if (rc != SILE_OK) return rc;
     SILE_HIP_CHECK(hipStreamSynchronize(s));
     return ok();
@@ -131,6 +153,10 @@ int sile_hip_kernel_matmul(void* const* buffers, int64_t num_threadgroups,
   SILE_HIP_CHECK(hipStreamSynchronize(s));
   return ok();
 }
+
+}  // namespace sile_rt
+
+extern "C" {
 
 int sile_hip_kernel_softmax(void* const* buffers, int64_t num_threadgroups,
                             int64_t threads_per_group, const int64_t* shapes, int64_t num_shapes,
@@ -217,7 +243,7 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
     if (lda < k || ldc < n || (bcol ? ldb < k : ldb < n))
       return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
     if (m > 65535LL * 32) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
-    int rc = launch_f32_exact(bcol, a, b, c, m, n, kp, lda, ldb, ldc, s);
+    int rc = launch_f32_exact(bcol, a, b, c, m, n, kp, lda, ldb, ldc, nullptr, 0, 0.0f, s);
     return rc == SILE_OK ? ok() : rc;
   }
 
@@ -275,6 +301,25 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   void* params[] = {&a, &b, &c, &g};
   int rc = launch(Module::kGemm, name, dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), params,
                   s);
+  return rc == SILE_OK ? ok() : rc;
+}
+
+int sile_hip_mma_f32(int64_t m, int64_t n, int64_t k, const float* a, int64_t lda,
+                     const float* b, int64_t ldb, sile_layout b_layout, const float* acc,
+                     int64_t ld_acc, float acc_value, float* c, int64_t ldc, int64_t bk,
+                     sile_hip_stream stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (m == 0 || n == 0) return ok();
+  if (!a || !b || !c) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (b_layout != SILE_ROW_MAJOR && b_layout != SILE_COL_MAJOR)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "unknown layout of B");
+  const bool bcol = b_layout == SILE_COL_MAJOR;
+  const int64_t kp = bk > 0 ? (k / bk) * bk : k;
+  if (lda < k || ldc < n || (bcol ? ldb < k : ldb < n) || (acc && ld_acc < n))
+    return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
+  if (m > 65535LL * 32) return fail(SILE_ERR_SHAPE, "f32 MMA too large");
+  int rc = launch_f32_exact(bcol, a, b, c, m, n, kp, lda, ldb, ldc, acc, ld_acc, acc_value,
+                            static_cast<hipStream_t>(stream));
   return rc == SILE_OK ? ok() : rc;
 }
 
@@ -489,7 +534,7 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
 namespace {
 int launch_f32_exact(bool b_col_major, const void* a, const void* b, void* c, int64_t m,
                      int64_t n, int64_t kp, int64_t lda, int64_t ldb, int64_t ldc,
-                     hipStream_t s) {
+                     const float* seed, int64_t ld_seed, float seed_value, hipStream_t s) {
   int tile = 32;
   for (int t : {128, 64})
     if (tile == 32 && ((m + t - 1) / t) * ((n + t - 1) / t) >= 1024 && (m + t - 1) / t <= 65535)
@@ -498,7 +543,8 @@ int launch_f32_exact(bool b_col_major, const void* a, const void* b, void* c, in
   if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "f32 GEMM too large");
   char name[64];
   snprintf(name, sizeof name, "sile_gemm_f32_exact_%s_t%d", b_col_major ? "nt" : "nn", tile);
-  void* params[] = {(void*)&a, (void*)&b, &c, &m, &n, &kp, &lda, &ldb, &ldc};
+  void* params[] = {(void*)&a, (void*)&b, &c,    &m,      &n,        &kp,
+                    &lda,      &ldb,      &ldc,  &seed, &ld_seed, &seed_value};
   return launch(Module::kGemm, name, dim3((unsigned)gx, (unsigned)gy), dim3(256), params, s);
 }
 }  // namespace

@@ -47,6 +47,14 @@ int resident_blocks(Module m, const char* name, int block_threads, int64_t* out)
 // The current device's address of the no-allocation launch's table array
 // (launch_noalloc.hip); looked up once per device.
 int noalloc_scratch(void** out);
+// The matmul DSL kernel with the sile_kernel_<name> tile semantics
+// (buffers a, b, c; shapes of a, b, c: 6 values), each cell's chain seeded
+// from `seed` (an accumulator source of shape seed_shape[2], the same tile of
+// it as of c) or, when seed is NULL, from seed_value.  Synchronous.
+int kernel_matmul_seeded(void* const* buffers, int64_t num_threadgroups, int64_t threads_per_group,
+                         const int64_t* shapes, int64_t bm, int64_t bn, int64_t bk,
+                         const float* seed, const int64_t* seed_shape, float seed_value,
+                         hipStream_t s);
 // hipModuleLaunchKernel with kernelParams.
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds = 0);

@@ -782,10 +782,12 @@ struct Operand {
 struct Match {
   int kind = SILE_ROUTE_NONE;
   int reduce_op = 0;
-  Operand ops[3];  // inputs, then the output
+  Operand ops[4];  // inputs, then the output; a matmul's accumulator source fourth
   int nops = 0;
   int64_t tm = 0, tn = 0, tk = 0;
   bool out_rank1 = false;
+  bool seed_from_tile = false;  // matmul: accumulator loaded from ops[3]
+  double seed_value = 0.0;      // matmul: the accumulator's splat value otherwise
 };
 
 Operand operand_of(const Function& fn, uint32_t v) {
@@ -816,10 +818,24 @@ Match match_matmul(const Function& fn) {
   const Inst* acc_seed = find_inst(*entry, entry->term.targs[1]);
   if (!k_seed || k_seed->op != Op::ConstI64 || k_seed->ival != 0)
     no_route("loop counter does not start at constant 0");
-  if (!acc_seed || acc_seed->op != Op::Splat || acc_seed->fval != 0.0)
-    no_route("accumulator is not a splat of 0.0");
-  const int64_t tile_m = acc_seed->ty.rows, tile_n = acc_seed->ty.cols;
-  if (acc_seed->ty.k != Ty::Tile) no_route("accumulator is not a tile");
+  // the accumulator's seed: a splat (0.0 for the reference's canonical matmul,
+  // any value for the tile MMA lowering's LoopCarriedSplat,
+  // crates/sile-tile-ir/src/passes/lowering/block.rs:294-377) or a tile loaded
+  // before the loop (the MMA then starts every cell from it,
+  // crates/sile-tile-ir/src/passes/lowering/tile_compute/mma.rs:213-229)
+  int64_t tile_m = 0, tile_n = 0;
+  const Inst* acc_load = nullptr;
+  if (acc_seed && acc_seed->op == Op::Splat) {
+    if (acc_seed->ty.k != Ty::Tile) no_route("accumulator is not a tile");
+    tile_m = acc_seed->ty.rows;
+    tile_n = acc_seed->ty.cols;
+  } else if (acc_seed && acc_seed->op == Op::LoadTko && acc_seed->stride == 1) {
+    acc_load = acc_seed;
+    tile_m = acc_seed->rows;
+    tile_n = acc_seed->cols;
+  } else {
+    no_route("accumulator is neither a splat nor a rank-2 tile load");
+  }
 
   const Block* header = fn.block(entry->term.t);
   if (header->params.size() != 2) no_route("loop header does not carry (k, acc)");
@@ -832,13 +848,20 @@ Match match_matmul(const Function& fn) {
   const Inst* cmp = find_inst(*header, ht.cond);
   if (!cmp || cmp->op != Op::ICmp || cmp->sub != "lt" || cmp->uses[0] != loop_k)
     no_route("loop condition is not k < bound");
-  const Inst* ktiles = find_inst(*header, cmp->uses[1]);
+  // the bound shape(a)[1] / BK, computed in the loop header (the reference's
+  // canonical form) or once before the loop (`let k_tiles = a.shape()[1] / BK`,
+  // crates/sile/examples/mlp.rs:6-23)
+  auto def = [&](uint32_t v) {
+    const Inst* i = find_inst(*header, v);
+    return i ? i : find_inst(*entry, v);
+  };
+  const Inst* ktiles = def(cmp->uses[1]);
   if (!ktiles || ktiles->op != Op::IBin || ktiles->sub != "divi")
     no_route("loop bound is not a division");
-  const Inst* tile_k_inst = find_inst(*header, ktiles->uses[1]);
+  const Inst* tile_k_inst = def(ktiles->uses[1]);
   if (!tile_k_inst || tile_k_inst->op != Op::ConstI64) no_route("loop bound divisor is not constant");
   const int64_t tile_k = tile_k_inst->ival;
-  const Inst* sdim = find_inst(*header, ktiles->uses[0]);
+  const Inst* sdim = def(ktiles->uses[0]);
   if (!sdim || sdim->op != Op::ShapeDim || sdim->ival != 1)
     no_route("loop bound is not shape(a)[1] / BK");
   const Param* sdesc = fn.param(sdim->uses[0]);
@@ -892,13 +915,23 @@ Match match_matmul(const Function& fn) {
              std::to_string(launch_dim(fn, row_launch)) + ", " +
              std::to_string(launch_dim(fn, col_launch)) + "), not (0, 1)");
 
+  if (acc_load && (acc_load->uses[1] != row_launch || acc_load->uses[2] != col_launch))
+    no_route("accumulator tile is not loaded at the program's tile");
+
   Match m;
   m.kind = SILE_ROUTE_MATMUL;
   m.ops[0] = operand_of(fn, a_buf);
   m.ops[1] = operand_of(fn, lb->uses[0]);
   m.ops[2] = operand_of(fn, st.uses[0]);
   m.nops = 3;
-  for (int i = 0; i < 3; ++i)
+  if (acc_load) {
+    m.ops[3] = operand_of(fn, acc_load->uses[0]);
+    m.nops = 4;
+    m.seed_from_tile = true;
+  } else {
+    m.seed_value = acc_seed->fval;
+  }
+  for (int i = 0; i < m.nops; ++i)
     if (m.ops[i].rank != 2) no_route("matmul operand is not rank 2");
   m.tm = tile_m;
   m.tn = tile_n;
@@ -1072,7 +1105,9 @@ void set_reason(sile_hip_route* r, const std::string& s) {
 void plan(const Match& m, const int64_t* shapes, int64_t programs, sile_hip_route* r) {
   r->kind = m.kind;
   r->reduce_op = m.reduce_op;
-  for (int i = 0; i < 3; ++i) {
+  r->seed_from_tile = m.seed_from_tile ? 1 : 0;
+  r->seed_value = (float)m.seed_value;
+  for (int i = 0; i < 4; ++i) {
     r->buffer[i] = i < m.nops ? m.ops[i].index : -1;
     r->shape_offset[i] = i < m.nops ? m.ops[i].shape_offset : -1;
     r->rank[i] = i < m.nops ? m.ops[i].rank : 0;
@@ -1160,7 +1195,7 @@ int sile_hip_tile_ir_route(const char* tile_ir_text, const int64_t* shapes, int6
     const Match m = detect(fn, reasons);
     if (m.kind == SILE_ROUTE_NONE) {
       out->kind = SILE_ROUTE_NONE;
-      for (int i = 0; i < 3; ++i) out->buffer[i] = out->shape_offset[i] = -1;
+      for (int i = 0; i < 4; ++i) out->buffer[i] = out->shape_offset[i] = -1;
       set_reason(out, reasons);
       return ok();
     }
@@ -1187,9 +1222,9 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
                 "%d / %lld", (long long)num_buffers, (long long)num_shapes, route->num_buffers,
                 (long long)route->num_shapes);
   if (!buffers || (num_shapes > 0 && !shapes)) return fail(SILE_ERR_SHAPE, "NULL buffers / shapes");
-  const int nops = route->kind == SILE_ROUTE_MATMUL ? 3 : 2;
-  void* bufs[3] = {nullptr, nullptr, nullptr};
-  int64_t shp[6] = {0, 0, 0, 0, 0, 0};
+  const int nops = route->kind == SILE_ROUTE_MATMUL ? (route->seed_from_tile ? 4 : 3) : 2;
+  void* bufs[4] = {nullptr, nullptr, nullptr, nullptr};
+  int64_t shp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int64_t nshp = 0;
   for (int i = 0; i < nops; ++i) {
     const int b = route->buffer[i], off = route->shape_offset[i], rk = route->rank[i];
@@ -1209,8 +1244,11 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
   int rc = SILE_OK;
   switch (route->kind) {
     case SILE_ROUTE_MATMUL:
-      return sile_hip_kernel_matmul(bufs, num_threadgroups, 1, shp, 6, route->tile_m,
-                                    route->tile_n, route->tile_k, stream);
+      // the canonical matmul, or the tile MMA from a splat or a loaded accumulator
+      return sile_rt::kernel_matmul_seeded(bufs, num_threadgroups, 1, shp, route->tile_m, route->tile_n,
+                                  route->tile_k,
+                                  route->seed_from_tile ? static_cast<const float*>(bufs[3]) : nullptr,
+                                  route->seed_from_tile ? shp + 6 : nullptr, route->seed_value, s);
     case SILE_ROUTE_SOFTMAX_TILES:
       return sile_hip_kernel_softmax(bufs, num_threadgroups, 1, shp, 4, route->tile_m,
                                      route->tile_n, stream);

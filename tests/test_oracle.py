@@ -409,3 +409,49 @@ def test_bf16_rne():
     np.testing.assert_array_equal(got[finite], want[finite].astype(np.uint16))
     assert got[-1] == 0x7F80 and got[-2] == 0x8000
     assert got[-4] == 0x3F80 and got[-3] == 0x3F82  # ties to even
+
+
+# ---------------------------------------------------------------- seeded tile MMA (a2)
+
+def test_mma_seed_zero_is_the_canonical_matmul():
+    a = rng(21).uniform(-1, 1, size=(64, 96)).astype(np.float32)
+    b = rng(22).uniform(-1, 1, size=(96, 48)).astype(np.float32)
+    c = np.zeros((64, 48), np.float32)
+    cpuref.kernel_matmul(a, b, c, (1000, 1, 1), 16, 16, 32)
+    np.testing.assert_array_equal(cpuref.mma_f32(a, b, acc_value=0.0, bk=32), c)
+    np.testing.assert_array_equal(cpuref.mma_f32(a, np.ascontiguousarray(b.T), b_col_major=True,
+                                                 bk=32), c)
+
+
+def test_mma_integer_seeds_are_exact():
+    r = rng(23)
+    a = r.integers(-8, 9, size=(40, 30)).astype(np.float32)
+    b = r.integers(-8, 9, size=(30, 20)).astype(np.float32)
+    d = r.integers(-1000, 1000, size=(40, 20)).astype(np.float32)
+    want = d.astype(np.int64) + a.astype(np.int64) @ b.astype(np.int64)
+    np.testing.assert_array_equal(cpuref.mma_f32(a, b, acc=d), want.astype(np.float32))
+    want = 7 + a.astype(np.int64) @ b.astype(np.int64)
+    np.testing.assert_array_equal(cpuref.mma_f32(a, b, acc_value=7.0), want.astype(np.float32))
+    # K truncation: only k < (30 // 8) * 8 = 24 contributes
+    want = d.astype(np.int64) + a[:, :24].astype(np.int64) @ b[:24].astype(np.int64)
+    np.testing.assert_array_equal(cpuref.mma_f32(a, b, acc=d, bk=8), want.astype(np.float32))
+
+
+def test_mma_seed_starts_the_chain():
+    """Seed 2^24 then two products of 1: the chain from the seed gives
+    (2^24 + 1) + 1 = 2^24 (each add rounds to even); adding the seed after the
+    products would give 2^24 + 2."""
+    a = np.ones((1, 2), np.float32)
+    b = np.ones((2, 1), np.float32)
+    big = np.float32(2.0 ** 24)
+    assert cpuref.mma_f32(a, b, acc_value=big)[0, 0] == big
+    assert cpuref.mma_f32(a, b, acc=np.full((1, 1), big, np.float32))[0, 0] == big
+
+
+def test_mma_signed_zero_seeds():
+    a = np.zeros((2, 3), np.float32)
+    b = np.zeros((3, 2), np.float32)
+    z = cpuref.mma_f32(a, b, acc_value=-0.0, bk=4)   # K' = 0: the seed itself
+    assert (z == 0).all() and np.signbit(z).all()
+    z = cpuref.mma_f32(a, b, acc_value=-0.0)         # -0.0 + (+0.0) = +0.0
+    assert (z == 0).all() and not np.signbit(z).any()

@@ -4,6 +4,7 @@ the detector's rejections (the conditions of the reference's
 CanonicalMatmulPlan::detect, canonical_matmul.rs:446-666) and parse errors."""
 import os
 
+import numpy as np
 import pytest
 
 from sile_amd import _abi as hip
@@ -42,7 +43,8 @@ def test_matmul_routes_to_the_exact_tile_kernel():
     r = _route(T.matmul(32, 32, 32), [512, 512, 512, 512, 512, 512], 256)
     assert r.kind == hip.ROUTE_MATMUL
     assert (r.tile_m, r.tile_n, r.tile_k) == (32, 32, 32)
-    assert list(r.buffer) == [0, 1, 2] and list(r.shape_offset) == [0, 2, 4]
+    assert list(r.buffer) == [0, 1, 2, -1] and list(r.shape_offset) == [0, 2, 4, -1]
+    assert r.seed_from_tile == 0 and r.seed_value == 0.0
     r = _route(T.matmul(2, 2, 2), [4, 4, 4, 4, 4, 4], 4)
     assert r.kind == hip.ROUTE_MATMUL and (r.tile_m, r.tile_n, r.tile_k) == (2, 2, 2)
 
@@ -98,12 +100,11 @@ def test_vec_add_has_no_route(passes):
     why = r.reason.decode()
     for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:"):
         assert d in why
-    assert list(r.buffer) == [-1, -1, -1]
+    assert list(r.buffer) == [-1, -1, -1, -1]
 
 
 MATMUL_MUTATIONS = {
     # each breaks one condition of CanonicalMatmulPlan::detect
-    "acc seed 1.0": ("%5 = constant <f32: 0.0>", "%5 = constant <f32: 1.0>"),
     "k seed 1": ("%8 = constant <i64: 0>", "%8 = constant <i64: 1>"),
     "step 2": ("%20 = constant <i64: 1>", "%20 = constant <i64: 2>"),
     "bound k <= n": ('cmpi "lt"', 'cmpi "le"'),
@@ -203,3 +204,43 @@ def test_launch_rejects_other_shapes_or_grid():
     with pytest.raises(hip.SileError) as e:
         hip.tile_ir_launch(r, [0, 0], [4, 8, 4, 8], 1)
     assert e.value.kind == "Shape"
+
+
+# ---------------------------------------------------------------- seeded tile MMA forms
+
+@pytest.mark.parametrize("splat", [1.5, -0.0, 3.0])
+def test_matmul_with_a_splat_seed_routes(splat):
+    """A splat other than 0.0 fails the reference's canonical detector but is
+    the same MMA loop with a LoopCarriedSplat seed: routed with its value."""
+    r = _route(T.matmul(32, 32, 32, splat=splat), [512, 512, 512, 512, 512, 512], 256)
+    assert r.kind == hip.ROUTE_MATMUL, r.reason
+    assert r.seed_from_tile == 0 and r.seed_value == splat
+    assert np.signbit(np.float32(r.seed_value)) == np.signbit(np.float32(splat))
+
+
+@pytest.mark.parametrize("src", ["d", "c"])
+def test_matmul_with_a_loaded_accumulator_routes(src):
+    if src == "d":
+        shapes = [64, 96, 96, 48, 64, 48, 64, 48]   # a, b, d, c
+        want_buf, want_off = [0, 1, 3, 2], [0, 2, 6, 4]
+    else:
+        shapes = [64, 96, 96, 48, 64, 48]           # a, b, c (the seed is c itself)
+        want_buf, want_off = [0, 1, 2, 2], [0, 2, 4, 4]
+    r = _route(T.matmul_acc(16, 16, 32, src=src), shapes, 12)
+    assert r.kind == hip.ROUTE_MATMUL, r.reason
+    assert r.seed_from_tile == 1
+    assert list(r.buffer) == want_buf and list(r.shape_offset) == want_off
+
+
+def test_mlp_gemm_routes():
+    """crates/sile/examples/mlp.rs:6-23 hoists the k-tile count out of the loop."""
+    r = _route(T.mlp_gemm(32, 32, 8), [64, 64, 64, 64, 64, 64], 4)
+    assert r.kind == hip.ROUTE_MATMUL, r.reason
+    assert (r.tile_m, r.tile_n, r.tile_k) == (32, 32, 8) and r.seed_value == 0.0
+
+
+def test_loaded_accumulator_must_be_the_programs_tile():
+    text = T.matmul_acc(16, 16, 32, src="d").replace(
+        "%7 = load_ptr_tko %2, [%4, %5]", "%7 = load_ptr_tko %2, [%5, %4]")
+    r = _route(text, [64, 96, 96, 48, 64, 48, 64, 48], 12)
+    assert r.kind == hip.ROUTE_NONE and b"accumulator tile" in r.reason

@@ -13,7 +13,11 @@ numbering procedure on the one kernel the reference prints in its tests.
 `passes=False` gives the text before the passes.
 
 The kernels (DSL source as in crates/sile/examples/*.rs):
-  matmul<BM,BN,BK>      crates/sile/examples/matmul.rs:3-19
+  matmul<BM,BN,BK>      crates/sile/examples/matmul.rs:3-19 (splat seeds other
+                        than 0.0: `sile::constant(v, [BM, BN])`)
+  matmul_acc<BM,BN,BK>  not in the reference: the matmul with its accumulator
+                        loaded from a tile (`d.load_tile` or `c.load_tile`)
+  gemm<BM,BN,BK>        crates/sile/examples/mlp.rs:6-23
   softmax<BM,BN>        crates/sile/examples/softmax.rs:3-16
   parallel_reduce<TILE> crates/sile/examples/parallel_reduce.rs:3-9
   vec_add<TILE>         crates/sile/examples/vec_add.rs:3-14
@@ -89,6 +93,92 @@ def matmul(bm, bn, bk, splat=0.0):
           "return"]),
     ]
     return _module("matmul", params, blocks)
+
+
+def matmul_acc(bm, bn, bk, src="d"):
+    """C = D + A.B as a tile MMA whose accumulator starts from a loaded tile:
+    `let mut acc = d.load_tile([BM, BN], [m, n]); for k in 0..a.shape()[1] / BK
+    { acc = sile::mma(a.load_tile(..), b.load_tile(..), acc) } c.store(acc)`,
+    with d a fourth parameter (src="d") or c itself (src="c", C += A.B in
+    place).  The accumulator seed is a tile, so the reference lowers the mma
+    through its general tile-MMA path (mma.rs:25-739, init :213-229)."""
+    acc = _tile(bm, bn)
+    if src == "c":
+        params = [_param_buf(0, "a", 2), _param_buf(1, "b", 2), _param_buf(2, "c", 2),
+                  _param_launch(3, 0), _param_launch(4, 1), _param_shape(5, 2, "c", 2),
+                  _param_shape(10, 0, "a", 2), _param_shape(18, 1, "b", 2)]
+        seed_buf = "%2"
+    else:
+        params = [_param_buf(0, "a", 2), _param_buf(1, "b", 2), _param_buf(2, "d", 2),
+                  _param_buf(3, "c", 2), _param_launch(4, 0), _param_launch(5, 1),
+                  _param_shape(6, 2, "d", 2), _param_shape(10, 0, "a", 2),
+                  _param_shape(18, 1, "b", 2), _param_shape(24, 3, "c", 2)]
+        seed_buf = "%2"
+    m_idx, n_idx = ("%3", "%4") if src == "c" else ("%4", "%5")
+    out = "%2" if src == "c" else "%3"
+    blocks = [
+        ("^bb0", [f"%7 = load_ptr_tko {seed_buf}, [{m_idx}, {n_idx}] {{shape = [{bm}, {bn}], "
+                  f"stride_dim = 1}} : {acc}",
+                  "%9 = constant <i64: 0> : tile<i64>",
+                  "cf.br ^bb1(%9, %7)"]),
+        (f"^bb1(%11: tile<i64>, %12: {acc})",
+         ["%13 = sile.shape_dim %10 {dim = 1} : tile<i64>",
+          f"%14 = constant <i64: {bk}> : tile<i64>",
+          "%15 = divi %13, %14 : tile<i64>",
+          '%16 = cmpi "lt" %11, %15 : tile<i64>',
+          "cf.cond_br %16, ^bb2(%11, %12), ^bb3(%12)"]),
+        (f"^bb2(%19: tile<i64>, %20: {acc})",
+         [f"%17 = load_ptr_tko %0, [{m_idx}, %19] {{shape = [{bm}, {bk}], stride_dim = 1}} : "
+          f"{_tile(bm, bk)}",
+          f"%21 = load_ptr_tko %1, [%19, {n_idx}] {{shape = [{bk}, {bn}], stride_dim = 1}} : "
+          f"{_tile(bk, bn)}",
+          f"%22 = mmaf %17, %21, %20 {{m = {bm}, n = {bn}, k = {bk}}} : {acc}",
+          "%23 = constant <i64: 1> : tile<i64>",
+          "%25 = addi %19, %23 : tile<i64>",
+          "cf.br ^bb1(%25, %22)"]),
+        (f"^bb3(%26: {acc})",
+         [f"%27 = store_ptr_tko {out}, %26, [{m_idx}, {n_idx}] {{shape = [{bm}, {bn}], "
+          f"stride_dim = 1}} : none",
+          "return"]),
+    ]
+    return _module("matmul_acc", params, blocks)
+
+
+def mlp_gemm(bm, bn, bk):
+    """The gemm kernel of crates/sile/examples/mlp.rs:6-23: the canonical
+    matmul except that `let k_tiles = x.shape()[1] / BK;` is computed once
+    before the loop, so the bound's division sits in the entry block and the
+    reference's CanonicalMatmulPlan::detect (canonical_matmul.rs:511-534,
+    which looks for it in the loop header) declines it; the general tile-MMA
+    lowering (LoopCarriedSplat seed 0.0) gives the same per-cell chain."""
+    acc = _tile(bm, bn)
+    params = [_param_buf(0, "x", 2), _param_buf(1, "y", 2), _param_buf(2, "z", 2),
+              _param_launch(3, 0), _param_launch(4, 1), _param_shape(6, 0, "x", 2),
+              _param_shape(17, 1, "y", 2), _param_shape(23, 2, "z", 2)]
+    blocks = [
+        ("^bb0", [f"%5 = constant <f32: 0.0> : {acc}",
+                  "%7 = sile.shape_dim %6 {dim = 1} : tile<i64>",
+                  f"%8 = constant <i64: {bk}> : tile<i64>",
+                  "%9 = divi %7, %8 : tile<i64>",
+                  "%10 = constant <i64: 0> : tile<i64>",
+                  "cf.br ^bb1(%10, %5)"]),
+        (f"^bb1(%11: tile<i64>, %12: {acc})",
+         ['%13 = cmpi "lt" %11, %9 : tile<i64>',
+          "cf.cond_br %13, ^bb2(%11, %12), ^bb3(%12)"]),
+        (f"^bb2(%14: tile<i64>, %15: {acc})",
+         [f"%16 = load_ptr_tko %0, [%3, %14] {{shape = [{bm}, {bk}], stride_dim = 1}} : "
+          f"{_tile(bm, bk)}",
+          f"%18 = load_ptr_tko %1, [%14, %4] {{shape = [{bk}, {bn}], stride_dim = 1}} : "
+          f"{_tile(bk, bn)}",
+          f"%19 = mmaf %16, %18, %15 {{m = {bm}, n = {bn}, k = {bk}}} : {acc}",
+          "%20 = constant <i64: 1> : tile<i64>",
+          "%21 = addi %14, %20 : tile<i64>",
+          "cf.br ^bb1(%21, %19)"]),
+        (f"^bb3(%22: {acc})",
+         [f"%24 = store_ptr_tko %2, %22, [%3, %4] {{shape = [{bm}, {bn}], stride_dim = 1}} : none",
+          "return"]),
+    ]
+    return _module("gemm", params, blocks)
 
 
 def softmax(bm, bn, passes=True):
