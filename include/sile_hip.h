@@ -229,9 +229,11 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *   f32  x f32  -> f32 : any shape/layout of B, A row-major; exact canonical order
  *                        (bit-identical to the CPU backend).
  *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
- *                        A row-major, B column-major, M >= 256, N >= 256 with N
- *                        a multiple of 4, any K', leading dimensions multiples
- *                        of 16 bytes; MFMA path.
+ *                        A row-major, B column-major, any M, N, K', A and B
+ *                        (and their leading dimensions) 16-byte aligned; MFMA
+ *                        path (M, N >= 256 with N a multiple of 4 and C's rows
+ *                        16-byte aligned: 256 x 256 tiles through LDS; other
+ *                        shapes: 64 x 64 tiles).
  * M = 0 or N = 0: nothing is written.  K' = 0 (K below one bk): C = +0.0 for
  * any M, N and supported types, as the canonical matmul's sums start at 0.0f
  * and add no term (canonical_matmul.rs:58-73).

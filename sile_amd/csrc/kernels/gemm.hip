@@ -480,6 +480,118 @@ SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
 
+// ---------------------------------------------------------------------------
+// Any shape: M or N below one 256 x 256 tile, or N not a multiple of 4.
+//
+// 64 x 64 output tile per workgroup of 4 waves (2 x 2), a 32 x 32 block per
+// wave on v_mfma_f32_32x32x16_{bf16,f16} (16 k per MFMA) or
+// v_mfma_f32_32x32x64_f8f6f4 (64 k).  The operands are small, so each lane
+// loads its fragments straight from global memory (L2): lane l supplies row
+// (A) or column (B, stored [N, K]) l % 32 and the 8 (16-bit) or 32 (fp8)
+// consecutive k of k-group l / 32, one or two 16-byte loads.  Rows past M,
+// columns past N and k past K' are zero in both operands (the last k-step
+// element by element), so NaN or Inf past K' never reaches a product.  The
+// accumulator register i of lane l is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]
+// of the block; stores skip C outside [M, N].
+// ---------------------------------------------------------------------------
+struct SmallArgs {
+  int64_t lda, ldb, ldc;  // in elements
+  int64_t m, n, kp;
+  float alpha;
+};
+
+template <int kKind, int kOut>
+__device__ __forceinline__ void gemm_small_body(const uint8_t* __restrict__ A,
+                                                const uint8_t* __restrict__ B, void* __restrict__ C,
+                                                const SmallArgs& g) {
+  constexpr bool kIsFP8 = kKind == kFP8;
+  constexpr int kEB = kIsFP8 ? 1 : 2;        // bytes per element
+  constexpr int kKStep = kIsFP8 ? 64 : 16;   // k per MFMA
+  constexpr int kGrpK = kKStep / 2;          // k per lane group (16 or 32 bytes)
+  constexpr int kCh = kGrpK * kEB / 16;      // 16-byte chunks per fragment
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, grp = lane >> 5;
+  const int64_t row0 = (int64_t)blockIdx.y * 64 + (wave >> 1) * 32;
+  const int64_t col0 = (int64_t)blockIdx.x * 64 + (wave & 1) * 32;
+  const int64_t arow = row0 + r, bcol = col0 + r;
+  const bool a_ok = arow < g.m, b_ok = bcol < g.n;
+  const uint8_t* ap = A + (a_ok ? arow : 0) * g.lda * kEB;
+  const uint8_t* bp = B + (b_ok ? bcol : 0) * g.ldb * kEB;
+  // one operand fragment at k = kg: whole 16-byte chunks inside K', else
+  // element by element with zeros past K' (and everywhere for a row past M /
+  // a column past N)
+  auto frag = [&](const uint8_t* base, bool ok, int64_t kg, u32x4 (&f)[kCh]) {
+    if (ok && kg + kGrpK <= g.kp) {
+#pragma unroll
+      for (int h = 0; h < kCh; ++h) f[h] = *reinterpret_cast<const u32x4*>(base + kg * kEB + 16 * h);
+    } else {
+#pragma unroll
+      for (int h = 0; h < kCh; ++h) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t v = 0;
+#pragma unroll
+          for (int e = 0; e < 4 / kEB; ++e) {
+            const int64_t k = kg + (16 * h + 4 * q) / kEB + e;
+            uint32_t x = 0;
+            if (ok && k < g.kp)
+              x = kEB == 1 ? base[k] : *reinterpret_cast<const uint16_t*>(base + 2 * k);
+            v |= x << (8 * kEB * e);
+          }
+          w[q] = v;
+        }
+        f[h] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  for (int64_t k0 = 0; k0 < g.kp; k0 += kKStep) {
+    const int64_t kg = k0 + grp * kGrpK;
+    u32x4 fa[kCh], fb[kCh];
+    frag(ap, a_ok, kg, fa);
+    frag(bp, b_ok, kg, fb);
+    if constexpr (kIsFP8) {
+      acc = mma32x32_fp8(fa, fb, acc);
+    } else if constexpr (kKind == kBF16) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[0]),
+                                                     __builtin_bit_cast(bf16x8, fb[0]), acc, 0, 0, 0);
+    } else {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[0]),
+                                                    __builtin_bit_cast(f16x8, fb[0]), acc, 0, 0, 0);
+    }
+  }
+  const int64_t col = col0 + r;
+  if (col >= g.n) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = row0 + 8 * (i / 4) + 4 * grp + (i % 4);
+    if (row >= g.m) continue;
+    const float v = g.alpha != 1.0f ? acc[i] * g.alpha : acc[i];
+    if constexpr (kOut == kOutF32)
+      static_cast<float*>(C)[row * g.ldc + col] = v;
+    else if constexpr (kOut == kOutBF16)
+      static_cast<uint16_t*>(C)[row * g.ldc + col] = bf16_rne(v);
+    else
+      static_cast<uint16_t*>(C)[row * g.ldc + col] = f16_rne(v);
+  }
+}
+
+#define SILE_GEMM_SMALL_KERNEL(NAME, KIND, OUT)                                                \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const void* A, const void* B, void* C, \
+                                                         SmallArgs g) {                        \
+    gemm_small_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B), \
+                               C, g);                                                          \
+  }
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_bf16_bf16, kBF16, kOutBF16)
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_bf16_f32, kBF16, kOutF32)
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_f16_f16, kF16, kOutF16)
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_f16_f32, kF16, kOutF32)
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_fp8_bf16, kFP8, kOutBF16)
+SILE_GEMM_SMALL_KERNEL(sile_gemm_small_fp8_f32, kFP8, kOutF32)
+
 // C = 0 for K' = 0 (K below one BK): the canonical matmul's sums start at
 // 0.0f and add no term (crates/sile-tile-ir/src/passes/lowering/canonical_matmul.rs:58-73,
 // k_limit = 0).  C is addressed in 16-bit words: n16 words per row, ldc16

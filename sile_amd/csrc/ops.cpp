@@ -276,14 +276,27 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
                     dim3(256), zp, s);
     return rc == SILE_OK ? ok() : rc;
   }
-  // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
-  // any K' (the kernel zeroes the elements of its last half k-step past K')
-  if (m < 256 || n < 256 || n % 4)
-    return fail(SILE_ERR_SHAPE,
-                "%s GEMM needs M >= 256, N >= 256 with N a multiple of 4 (M=%lld N=%lld)",
-                dtype_name(a_type), (long long)m, (long long)n);
   const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
   if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
+  if (m < 256 || n < 256 || n % 4) {
+    // below one 256 x 256 tile (or N not a multiple of 4): the any-shape
+    // kernel, 64 x 64 tiles with fragments loaded straight from the operands
+    if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
+      return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
+    const int64_t gx = (n + 63) / 64, gy = (m + 63) / 64;
+    if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "GEMM too large");
+    char sname[64];
+    snprintf(sname, sizeof sname, "sile_gemm_small_%s", name + strlen("sile_gemm_nt_"));
+    struct {
+      int64_t lda, ldb, ldc, m, n, kp;
+      float alpha;
+    } sg{lda, ldb, ldc, m, n, kp, scale_a * scale_b};
+    void* sp[] = {&a, &b, &c, &sg};
+    int rc = launch(Module::kGemm, sname, dim3((unsigned)gx, (unsigned)gy), dim3(256), sp, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+  // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
+  // any K' (the kernel zeroes the elements of its last half k-step past K')
   if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
       !aligned16(c))
     return fail(SILE_ERR_SHAPE, "operands and leading dimensions must be 16-byte aligned");

@@ -267,3 +267,141 @@ def test_bf16_gemm_config3_sampled(hip, size):
     assert_close(got[rows], ref[rows], atol=ATOL, rtol=RTOL, what="bf16 4096 sampled")
     assert np.isfinite(got).all()
 
+
+
+@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
+                                      ("f16", "f32"), ("fp8", "bf16"), ("fp8", "f32")])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (100, 256, 64), (16, 300, 130), (255, 255, 255),
+                                   (300, 100, 64), (2, 1000, 37), (257, 258, 96), (64, 64, 64)])
+def test_small_shapes_mfma(hip, kind, out, m, n, k):
+    """Shapes below one 256 x 256 tile, or N not a multiple of 4, run the
+    any-shape MFMA kernel: every element against the oracle, C in a wider
+    pitch whose columns past N keep their fill."""
+    ldc = n + 3
+    say(f"gemm small {kind} {m}x{n}x{k} -> {out}")
+    a = rng(41).normal(size=(m, k)).astype(np.float32)
+    bt = rng(42).normal(size=(n, k)).astype(np.float32)
+    # leading dimensions: 16-byte multiples of the element size
+    ea = 1 if kind == "fp8" else 2
+    lda = ldb = -(-k * ea // 16) * 16 // ea
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(k)
+        bt /= np.sqrt(k)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
+    pad = 0x7F if kind == "fp8" else 0x7FC0 if kind == "bf16" else 0x7E00   # NaN
+    ap = np.full((m, lda), pad, qa.dtype)
+    ap[:, :k] = qa
+    bp = np.full((n, ldb), pad, qb.dtype)
+    bp[:, :k] = qb
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    da, db = hip.DeviceBuffer.from_array(ap), hip.DeviceBuffer.from_array(bp)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    dc.fill_bytes(0xFF)
+    hip.gemm(t, t, c_t, m, n, k, da.ptr, lda, hip.ROW_MAJOR, db.ptr, ldb, hip.COL_MAJOR,
+             dc.ptr, ldc, sa, sb)
+    hip.synchronize()
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f, b_f)
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} small {m}x{n}x{k}")
+    raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc))
+    assert (raw[:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("k,bk", [(192, 50), (192, 7), (48, 33), (130, 64)])
+def test_small_shapes_truncated_k(hip, kind, k, bk):
+    """K' = (K / bk) * bk inside a k-step of the any-shape kernel, with NaN /
+    Inf past K' in the operands: masked out."""
+    m, n = 100, 72
+    kp = (k // bk) * bk
+    say(f"gemm small {kind} {m}x{n} K={k} bk={bk}")
+    a = rng(43).normal(size=(m, k)).astype(np.float32)
+    bt = rng(44).normal(size=(n, k)).astype(np.float32)
+    if kind == "bf16":
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        qa, a_f = bf16_round(a)
+        qb, b_f = bf16_round(bt)
+        qa[:, kp:] = 0x7FC0
+        qb[:, kp:] = 0x7F80
+        t, sa, sb = hip.BF16, 1.0, 1.0
+    else:
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        qa[:, kp:] = 0x7F
+        qb[:, kp:] = 0xFF
+        t = hip.F8E4M3
+    ea = 1 if kind == "fp8" else 2
+    ld = -(-k * ea // 16) * 16 // ea
+    ap = np.zeros((m, ld), qa.dtype)
+    ap[:, :k] = qa
+    bp = np.zeros((n, ld), qb.dtype)
+    bp[:, :k] = qb
+    da, db = hip.DeviceBuffer.from_array(ap), hip.DeviceBuffer.from_array(bp)
+    dc = hip.DeviceBuffer(m * n * 4)
+    hip.gemm(t, t, hip.F32, m, n, k, da.ptr, ld, hip.ROW_MAJOR, db.ptr, ld, hip.COL_MAJOR,
+             dc.ptr, n, sa, sb, bk)
+    hip.synchronize()
+    got = dc.download(np.float32, (m, n))
+    ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+    tol = (1e-4, 1e-4) if kind == "bf16" else (ATOL, RTOL)
+    assert_close(got, ref, atol=tol[0], rtol=tol[1], what=f"{kind} small truncated K")
+    assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("f16", "f16"), ("fp8", "bf16"),
+                                      ("bf16", "f32")])
+@pytest.mark.parametrize("k,bk", [(192, 50), (192, 100), (320, 70)])
+def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, k, bk):
+    """The any-K' masking of the 256 x 256 kernel on a ragged shape (300 x 260:
+    the last tile row and column moved back) with lda = ldb = K + 64: the
+    elements past K' inside each row (up to K, then the row padding) are
+    NaN / Inf and must be masked, for 16-bit and fp8 -> bf16 outputs too."""
+    m, n = 300, 260
+    kp = (k // bk) * bk
+    ea = 1 if kind == "fp8" else 2
+    ld = k + 64
+    say(f"gemm {kind} {m}x{n} K={k} bk={bk} (K'={kp}) lda=ldb={ld} -> {out}")
+    a = rng(45).normal(size=(m, k)).astype(np.float32)
+    bt = rng(46).normal(size=(n, k)).astype(np.float32)
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        nan_a, inf_b = 0x7F, 0xFF
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        nan_a = 0x7FC0 if kind == "bf16" else 0x7E00
+        inf_b = 0x7F80 if kind == "bf16" else 0x7C00
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
+    ap = np.full((m, ld), nan_a, qa.dtype)
+    ap[:, :kp] = qa[:, :kp]
+    bp = np.full((n, ld), inf_b, qb.dtype)
+    bp[:, :kp] = qb[:, :kp]
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    ldc = n + 4
+    da, db = hip.DeviceBuffer.from_array(ap), hip.DeviceBuffer.from_array(bp)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    dc.fill_bytes(0xFF)
+    hip.gemm(t, t, c_t, m, n, k, da.ptr, ld, hip.ROW_MAJOR, db.ptr, ld, hip.COL_MAJOR, dc.ptr,
+             ldc, sa, sb, bk)
+    hip.synchronize()
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} truncated ragged")
+    assert np.isfinite(got[:, :n]).all()
