@@ -84,7 +84,12 @@ struct AttnArgs {
   int32_t pair;         // 1: causal query blocks in balanced pairs (v2 kernels)
 };
 
-template <bool kBF16, int kQT, int kNK>
+// Block kernel for any S (and head_dim 64 or 128): 4 waves x kQT * 32 queries,
+// kNK-key blocks staged through LDS by plain loads (double-buffered through
+// registers).  Keys and queries past S are zero in the staged operands, keys
+// past S are masked to -inf, and queries past S are not stored, so S need
+// not be a multiple of any block.
+template <bool kBF16, int kQT, int kNK, int kDh>
 __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
                                               const uint16_t* __restrict__ K,
                                               const uint16_t* __restrict__ V,
@@ -92,11 +97,16 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
                                               uint8_t* smem) {
   constexpr int kBQ = kWaves * kQT * 32;
   constexpr int kKT = kNK / 32;                     // 32-key tiles per block
-  constexpr int kKBytes = kNK * kRowB;              // K stage bytes
+  constexpr int kRB = kDh * 2;                      // bytes of one K / V row
+  constexpr int kRC = kDh / 8;                      // 16-byte chunks per row
+  constexpr int kKBytes = kNK * kRB;                // K stage bytes
   constexpr int kVRowB = kNK * 2;                   // V^T row bytes
   constexpr int kStageB = 2 * kKBytes;              // K + V^T (same size)
-  constexpr int kKLoads = kNK * 16 / kThreads;      // 16-byte K chunks per thread
-  constexpr int kVItems = kNK * 4 / kThreads;       // (4 keys x 8 d) items per thread
+  constexpr int kRowsPerPass = kThreads / kRC;      // K rows one pass of the workgroup loads
+  constexpr int kKLoads = kNK / kRowsPerPass;       // 16-byte K chunks per thread
+  constexpr int kVItems = kNK * kRC / 4 / kThreads; // (4 keys x 8 d) items per thread
+  constexpr int kDT = kDh / 32;                     // 32-row tiles of O^T
+  constexpr int kDK = kDh / 16;                     // MFMA k-steps over d
   static_assert(kKLoads >= 1 && kVItems >= 1, "block too small for the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -115,7 +125,8 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
   }
   if (a.causal) qb = a.q_blocks - 1 - qb;  // largest causal blocks first
   const int64_t S = a.seq;
-  const int64_t head_off = (int64_t)bh * S * kD;
+  const int S32 = (int)S;
+  const int64_t head_off = (int64_t)bh * S * kDh;
   const uint16_t* Qh = Q + head_off;
   const uint8_t* Kh = reinterpret_cast<const uint8_t*>(K + head_off);
   const uint8_t* Vh = reinterpret_cast<const uint8_t*>(V + head_off);
@@ -123,32 +134,40 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
   const int wq0 = q0 + wave * kQT * 32;  // first query of this wave
 
   // ---- Q^T fragments: lane holds query wq0 + 32 qt + l32, d = 16 kk + 8 g + [0, 8) ----
-  u32x4 qf[kQT][8];
+  u32x4 qf[kQT][kDK];
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    const uint16_t* qrow = Qh + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
+    const int q = wq0 + qt * 32 + l32;
+    const uint16_t* qrow = Qh + (int64_t)(q < S32 ? q : 0) * kDh + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
+    for (int kk = 0; kk < kDK; ++kk)
+      qf[qt][kk] = q < S32 ? *reinterpret_cast<const u32x4*>(qrow + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  // ---- K / V global -> register staging ----
-  // K: thread moves chunk (tid & 15) of rows (tid >> 4) + 16 i.
-  // V: item (key group kg = 4 keys, d chunk dc = 8 d): dc = tid & 15, kg = (tid >> 4) + 16 i.
-  const int k_chunk = tid & 15, k_row = tid >> 4;
+  // ---- K / V global -> register staging (rows past S: zero) ----
+  // K: thread moves chunk (tid % kRC) of rows tid / kRC + kRowsPerPass i.
+  // V: item (key group kg = 4 keys, d chunk dc = 8 d): dc = tid % kRC,
+  //    kg = tid / kRC + kRowsPerPass i.
+  const int k_chunk = tid % kRC, k_row = tid / kRC;
   u32x4 kreg[kKLoads];
   u32x4 vreg[kVItems][4];
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
   auto global_load = [&](int kb) {
-    const uint8_t* kp = Kh + (int64_t)kb * kRowB;
-    const uint8_t* vp = Vh + (int64_t)kb * kRowB;
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i)
-      kreg[i] = *reinterpret_cast<const u32x4*>(kp + (k_row + 16 * i) * kRowB + k_chunk * 16);
+    for (int i = 0; i < kKLoads; ++i) {
+      const int key = kb + k_row + kRowsPerPass * i;
+      kreg[i] = key < S32 ? *reinterpret_cast<const u32x4*>(Kh + (int64_t)key * kRB + k_chunk * 16)
+                          : zero4;
+    }
 #pragma unroll
     for (int i = 0; i < kVItems; ++i) {
-      const int kg = k_row + 16 * i;
+      const int kg = k_row + kRowsPerPass * i;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vreg[i][r] = *reinterpret_cast<const u32x4*>(vp + (4 * kg + r) * kRowB + k_chunk * 16);
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 4 * kg + r;
+        vreg[i][r] = key < S32 ? *reinterpret_cast<const u32x4*>(Vh + (int64_t)key * kRB + k_chunk * 16)
+                               : zero4;
+      }
     }
   };
   auto lds_store = [&](int stage) {
@@ -156,12 +175,12 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
     uint8_t* vs = ks + kKBytes;
 #pragma unroll
     for (int i = 0; i < kKLoads; ++i) {
-      const int row = k_row + 16 * i;
-      *reinterpret_cast<u32x4*>(ks + row * kRowB + ((k_chunk ^ (row & 15)) << 4)) = kreg[i];
+      const int row = k_row + kRowsPerPass * i;
+      *reinterpret_cast<u32x4*>(ks + row * kRB + ((k_chunk ^ (row & (kRC - 1))) << 4)) = kreg[i];
     }
 #pragma unroll
     for (int i = 0; i < kVItems; ++i) {
-      const int kg = k_row + 16 * i;
+      const int kg = k_row + kRowsPerPass * i;
       const int kp = kperm(4 * kg);          // 4 keys stay contiguous
       const int chunk = kp >> 3, half = (kp >> 2) & 1;
 #pragma unroll
@@ -176,11 +195,11 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
     }
   };
 
-  f32x16 oacc[kQT][4];
+  f32x16 oacc[kQT][kDT];
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt)
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
   float m_run[kQT], l_run[kQT];
@@ -190,7 +209,8 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
     l_run[qt] = 0.0f;
   }
 
-  const int nblocks = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
+  const int key_end = a.causal ? min(q0 + kBQ, S32) : S32;  // keys any query here sees
+  const int nblocks = (key_end + kNK - 1) / kNK;
   const float c = a.scale_log2;
 
   global_load(0);
@@ -201,7 +221,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
     const int stage = jb & 1;
     const int kb = jb * kNK;
     if (jb + 1 < nblocks) global_load(kb + kNK);
-    const bool active = !a.causal || kb <= wq0 + kQT * 32 - 1;
+    const bool active = (!a.causal || kb <= wq0 + kQT * 32 - 1) && wq0 < S32;
     if (active) {
       const uint8_t* ks = smem + stage * kStageB;
       const uint8_t* vs = ks + kKBytes;
@@ -216,25 +236,27 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 #pragma unroll
       for (int t = 0; t < kKT; ++t) {
         const int row = 32 * t + l32;
-        const uint8_t* krow = ks + row * kRowB;
+        const uint8_t* krow = ks + row * kRB;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(krow + (((2 * kk + g) ^ (row & 15)) << 4));
+        for (int kk = 0; kk < kDK; ++kk) {
+          const u32x4 kf =
+              *reinterpret_cast<const u32x4*>(krow + (((2 * kk + g) ^ (row & (kRC - 1))) << 4));
 #pragma unroll
           for (int qt = 0; qt < kQT; ++qt) sacc[t][qt] = mma32<kBF16>(kf, qf[qt][kk], sacc[t][qt]);
         }
       }
-      // ---- causal mask on the diagonal blocks ----
-      if (a.causal && kb + kNK - 1 > wq0) {
+      // ---- causal mask on the diagonal blocks, keys past S ----
+      if ((a.causal && kb + kNK - 1 > wq0) || kb + kNK > S32) {
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
           const int q = wq0 + 32 * qt + l32;
+          const int lim = a.causal ? min(q, S32 - 1) : S32 - 1;  // last visible key
 #pragma unroll
           for (int t = 0; t < kKT; ++t)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int key = kb + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
-              if (key > q) sacc[t][qt][i] = -__builtin_inff();
+              if (key > lim) sacc[t][qt][i] = -__builtin_inff();
             }
         }
       }
@@ -259,7 +281,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
           m_run[qt] = m_new;
           l_run[qt] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha;
+          for (int dt = 0; dt < kDT; ++dt) oacc[qt][dt] *= alpha;
         }
         const float mc = m_run[qt] * c;
         float rs = 0.0f;
@@ -285,7 +307,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
       }
       // ---- O^T += V^T . P^T ----
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < kDT; ++dt) {
         const int d = 32 * dt + l32;
         const uint8_t* vrow = vs + d * kVRowB;
 #pragma unroll
@@ -301,15 +323,16 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
     __syncthreads();
   }
 
-  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
+  // ---- epilogue: O[q][d] = O^T[d][q] / l (queries past S not stored) ----
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
     const float l = pair32_sum(l_run[qt]);
     const float inv = 1.0f / l;
     const int q = wq0 + 32 * qt + l32;
-    uint16_t* orow = O + head_off + (int64_t)q * kD;
+    if (q >= S32) continue;
+    uint16_t* orow = O + head_off + (int64_t)q * kDh;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = 32 * dt + 8 * r + 4 * g;
@@ -716,12 +739,16 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 0)
 SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32, 0)
 
-#define SILE_FA_KERNEL(NAME, BF, QT, NK)                                                      \
+#define SILE_FA_KERNEL(NAME, BF, QT, NK, DH)                                                  \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \
       const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * NK * kRowB];                 \
-    attn_fwd_body<BF, QT, NK>(Q, K, V, O, a, smem);                                           \
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * NK * DH * 2];                \
+    attn_fwd_body<BF, QT, NK, DH>(Q, K, V, O, a, smem);                                       \
   }
 
-SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k64, false, 1, 64)
-SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k64, true, 1, 64)
+// 128 queries per workgroup, any S: head_dim 128 over 64-key blocks, head_dim
+// 64 over 128-key blocks (the same LDS bytes per stage)
+SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k64, false, 1, 64, 128)
+SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k64, true, 1, 64, 128)
+SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k128_d64, false, 1, 128, 64)
+SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k128_d64, true, 1, 128, 64)

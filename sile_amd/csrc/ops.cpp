@@ -506,27 +506,37 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (seq_len * head_dim * 2 > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
-  // MFMA flash kernels: head_dim 128, 16-byte aligned operands, chosen by shape:
-  //   S a multiple of 256: the pipelined kernel (8 waves x 32 queries, 32-key
-  //     blocks; causal query blocks taken in balanced pairs);
-  //   S a multiple of 128: the 128-query-block kernel.
-  if (head_dim == 128 && seq_len % 128 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
-      aligned16(o)) {
+  // MFMA flash kernels, 16-byte aligned operands, chosen by shape:
+  //   head_dim 128, S a multiple of 256: the pipelined kernel (8 waves x 32
+  //     queries, 32-key blocks through LDS-DMA; causal query blocks taken in
+  //     balanced pairs);
+  //   head_dim 128 or 64, any other S: the block kernel (128 queries per
+  //     workgroup, keys and queries past S masked).
+  const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  if ((head_dim == 128 || head_dim == 64) && aligned) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const bool pipelined = seq_len % 256 == 0;
+    const bool pipelined = head_dim == 128 && seq_len % 256 == 0;
     const int64_t bq = pipelined ? 256 : 128;
     const bool pair = causal && pipelined;
+    const int64_t q_blocks = (seq_len + bq - 1) / bq;
+    if (q_blocks > 0x7fffffffLL / std::max<int64_t>(bh, 1))
+      return fail(SILE_ERR_SHAPE, "attention too large");
     struct {
       int64_t seq;
       int32_t bh, q_blocks;
       float scale_log2;
       int32_t causal, xcd_map, pair;
-    } fa{seq_len, (int32_t)bh, (int32_t)(seq_len / bq), scale * 1.4426950408889634f,
+    } fa{seq_len, (int32_t)bh, (int32_t)q_blocks, scale * 1.4426950408889634f,
          causal ? 1 : 0, (bh % 8 == 0) ? 1 : 0, pair ? 1 : 0};
-    const int64_t units = pair ? (seq_len / bq + 1) / 2 : seq_len / bq;
+    const int64_t units = pair ? (q_blocks + 1) / 2 : q_blocks;
     const int64_t blocks = bh * units;
     char name[64];
-    snprintf(name, sizeof name, pipelined ? "sile_flash_attn_fwd_%s_v2w8" : "sile_flash_attn_fwd_%s_q1_k64", dt);
+    if (pipelined)
+      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2w8", dt);
+    else if (head_dim == 128)
+      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q1_k64", dt);
+    else
+      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q1_k128_d64", dt);
     const unsigned threads = pipelined ? 512 : 256;
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(threads), params, s);

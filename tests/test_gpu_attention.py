@@ -189,3 +189,41 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     for hi in range(h):
         ref = cpuref.attention_fwd(qf[0, hi], kf[0, hi], vf[0, hi], scale, causal=causal)
         assert_close(got[0, hi], ref, atol=ATOL, rtol=RTOL, what=f"{trend} h{hi}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 100, 128), (2, 3, 333, 128), (1, 8, 1000, 128),
+                                     (1, 2, 64, 64), (2, 3, 200, 64), (1, 8, 1024, 64),
+                                     (1, 1, 1, 128), (1, 1, 31, 64), (1, 4, 2049, 64)])
+def test_flash_any_seq_len_and_head_dim_64(hip, dt, causal, b, h, s, d):
+    """The block MFMA kernel for sequence lengths that are not multiples of
+    a block (keys and queries past S masked) and for head_dim 64; every head
+    and query against the fp32 oracle, and O past the last query untouched."""
+    say(f"flash any-S {dt} causal={causal} B={b} H={h} S={s} D={d}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, dt, seed=51)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
+    assert np.isfinite(got).all()
+    qf, kf, vf = (x[1] for x in qkv)
+    for bi in range(b):
+        for hi in range(h):
+            ref = cpuref.attention_fwd(qf[bi, hi], kf[bi, hi], vf[bi, hi], scale, causal=causal)
+            assert_close(got[bi, hi], ref, atol=ATOL, rtol=RTOL, what=f"attn b{bi} h{hi}")
+
+
+def test_flash_any_seq_len_writes_nothing_past_o(hip):
+    """O sits inside a larger buffer: nothing past its B*H*S*D elements is written."""
+    b, h, s, d = 1, 3, 333, 64
+    say(f"flash any-S bounds B={b} H={h} S={s} D={d}")
+    qkv = _inputs(b, h, s, d, "f16", seed=52)
+    bufs = [hip.DeviceBuffer.from_array(x[0]) for x in qkv]
+    n = b * h * s * d
+    do = hip.DeviceBuffer((n + 4096) * 2)
+    do.fill_bytes(0xFF)
+    hip.flash_attn_fwd(hip.F16, b, h, s, d, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, do.ptr,
+                       1.0 / np.sqrt(d), True)
+    hip.synchronize()
+    raw = do.download(np.uint16, (n + 4096,))
+    assert (raw[n:] == 0xFFFF).all()
+    assert np.isfinite(raw[:n].view(np.float16)).all()
