@@ -45,6 +45,7 @@ PEAK_HBM_GBS = 8000.0
 # fp32 VALU lane rate (the published 157.3 TFLOP/s counts an FMA as 2 flops); an
 # exact-order GEMM issues one instruction per flop
 PEAK_VALU_F32_TOPS = 78.6
+PEAK_F32_PUBLISHED_TFLOPS = 157.3
 SETTLE_S = 0.5  # untimed load before each workload's warmup (clock ramp-up)
 
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
@@ -460,6 +461,9 @@ def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic, cpu=False):
     flop = 2.0 * n ** 3
     res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "valu", PEAK_VALU_F32_TOPS,
                     traffic.get(name))
+    # the same rate against the published fp32 peak (which counts an FMA as 2
+    # flops; the reference's order forbids FMA, so 0.5 is this path's ceiling)
+    res["frac_of_published_fp32_peak"] = round(res["value"] / PEAK_F32_PUBLISHED_TFLOPS, 4)
     res["flop_per_launch"] = flop
     for buf in (da, db, dc):
         buf.close()
@@ -584,14 +588,24 @@ def traffic_from_pmc(root):
     out = {"_scale": {"fetch": round(sf, 4), "write": round(sw, 4), "copy_bytes": COPY_BYTES,
                       "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1)}}
     for name in ALL + EXTRA:
+        prefix = WORKLOAD_KERNEL.get(name, "sile_")
+
         def is_sile(k):
-            return k.startswith("sile_")
+            return k.startswith(prefix)
         f = mean_kib(os.path.join(root, "pmc_fetch_" + name), "FETCH_SIZE", is_sile)
         w = mean_kib(os.path.join(root, "pmc_write_" + name), "WRITE_SIZE", is_sile)
         if f is not None and w is not None:
             out[name] = round(f * 1024 * sf + w * 1024 * sw)
     return out
 
+
+# the kernel a workload's line is about (the softmax workload also runs the copy
+# that measures its ceiling)
+WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "sile_gemm_nt",
+                   "gemm_bf16_4096": "sile_gemm_nt", "gemm_fp8_8192": "sile_gemm_nt",
+                   "flash_attn_fwd_f16_s8192": "sile_flash_attn", "flash_attn_fwd_f16_s4096":
+                   "sile_flash_attn", "gemm_f32_exact_4096": "sile_gemm_f32_exact",
+                   "gemm_f32_exact_512": "sile_gemm_f32_exact"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
