@@ -54,6 +54,9 @@ constexpr int kRowB = kD * 2;  // bytes of one K row
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
+// fast-path limit on one lane's block sum of p (pipelined kernel): below it
+// every p of the block is <= 2^kRescaleLog2
+constexpr float kBlockSumLimit = 256.0f;
 
 template <bool kBF16>
 SILE_DEV f32x16 mma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -347,13 +350,16 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 }  // namespace
 
 // ===========================================================================
-// Pipelined kernel (S a multiple of 256): 64 queries per wave, 32-key blocks.
+// Pipelined kernel (S a multiple of 256): 8 waves x 32 queries, 32-key blocks.
 //
 // Iteration j of the key loop issues, as one scheduling region,
 //   * on the matrix cores: S_{j+1} = K_{j+1} . Q^T  and  O^T += V_{j-1}^T . P_{j-1}
-//   * on the VALU: the online softmax of S_j (mask, max, exp, row sum) -> P_j
+//   * on the VALU: the online softmax of S_j (mask, exp against the running
+//     max, row sum) -> P_j
 // so the softmax of one block runs while the matrix cores work on its
-// neighbours; the lazy O rescale (rare) follows the MFMAs.  K and V tiles go
+// neighbours.  The block max is taken only when a lane's block sum of p
+// exceeds 2^8 (a row's first block, or a max that has moved): that rare path
+// recomputes P_j against the new max and rescales O lazily.  K and V tiles go
 // from HBM straight into LDS (buffer_load_dwordx4 ... lds), double-buffered:
 // iteration j loads K_{j+2} and V_j.
 //
@@ -393,7 +399,7 @@ constexpr int lds_bytes() { return 2 * 2 * kNK * kRowB; }
 // kQT 32-query tiles per wave, kW waves per workgroup: kW * kQT * 32 queries
 // per workgroup (256 for every instantiation); kNK keys per block (32 or 64),
 // i.e. kST = kNK / 32 S tiles of 32 keys x 32 queries per query tile.
-template <bool kBF16, int kQT, int kW, int kNK, int kSched>
+template <bool kBF16, int kQT, int kW, int kNK>
 __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
@@ -557,12 +563,11 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       for (int dt = 0; dt < 4; ++dt)
   #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.0f;
-    float m_run[kQT], l_run[kQT], alpha[kQT];
+    float m_run[kQT], l_run[kQT];
   #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
       m_run[qt] = -__builtin_inff();
       l_run[qt] = 0.0f;
-      alpha[qt] = 1.0f;
     }
     u32x4 pprev[kQT][2 * kST];
   #pragma unroll
@@ -619,25 +624,17 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                   (32 * st + 8 * (i >> 2) + (i & 3) > q) ? -__builtin_inff() : scur[qt][st][i];
         }
       }
-      bool grow_any = false;
-      float mx[kQT];
+      // Fast path: P_j against the running max, with no block max.  Every p
+      // of a lane stays <= 2^kRescaleLog2 as long as the lane's block sum of p
+      // does.  A lane whose block sum is larger, or NaN (a row's first block,
+      // where the running max is -inf), sends the wave to the block-max update
+      // below, which recomputes P_j exactly as a max-first softmax would.
+      bool slow = false;
+      float rs_blk[kQT];
   #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
-        float m = scur[qt][0][0];
-  #pragma unroll
-        for (int st = 0; st < kST; ++st)
-  #pragma unroll
-          for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][st][i]);
-        mx[qt] = pair32_max(m);
-        grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
-      }
-  #pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        const float m_new = grow_any ? __builtin_fmaxf(m_run[qt], mx[qt]) : m_run[qt];
-        alpha[qt] = exp2_fast((m_run[qt] - m_new) * c);
-        m_run[qt] = m_new;
-        const float mc = m_new * c;
-        float rs = l_run[qt] * alpha[qt];
+        const float mc = m_run[qt] * c;
+        float rs = 0.0f;
   #pragma unroll
         for (int st = 0; st < kST; ++st)
   #pragma unroll
@@ -653,40 +650,69 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
             }
             pnew[qt][2 * st + h] = w;
           }
-        l_run[qt] = rs;
+        slow |= __builtin_amdgcn_ballot_w64(!(rs <= kBlockSumLimit)) != 0;
+        rs_blk[qt] = rs;
       }
-      // keep the softmax in this region, beside the MFMAs (the compiler would
-      // otherwise sink it below the rescale branch)
+      if (slow) {
+        // Rare: the running max moves only when a block max exceeds it by more
+        // than kRescaleLog2 for some lane of the wave (lazy rescale of O).  The
+        // scores pass through an empty asm so that the block max is not
+        // computed ahead of the branch.
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+          for (int st = 0; st < kST; ++st) asm volatile("" : "+v"(scur[qt][st]));
+        bool grow_any = false;
+        float mx[kQT];
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          float m = scur[qt][0][0];
+  #pragma unroll
+          for (int st = 0; st < kST; ++st)
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, scur[qt][st][i]);
+          mx[qt] = pair32_max(m);
+          grow_any |= __builtin_amdgcn_ballot_w64((mx[qt] - m_run[qt]) * c > kRescaleLog2) != 0;
+        }
+  #pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          const float m_new = grow_any ? __builtin_fmaxf(m_run[qt], mx[qt]) : m_run[qt];
+          const float alpha = exp2_fast((m_run[qt] - m_new) * c);
+          m_run[qt] = m_new;
+          const float mc = m_new * c;
+          float rs = 0.0f;
+  #pragma unroll
+          for (int st = 0; st < kST; ++st)
+  #pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              u32x4 w;
+  #pragma unroll
+              for (int jj = 0; jj < 4; ++jj) {
+                const float p0 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj], c, -mc));
+                const float p1 = exp2_fast(__builtin_fmaf(scur[qt][st][8 * h + 2 * jj + 1], c, -mc));
+                const uint32_t pk = pack2<kBF16>(p0, p1);
+                w[jj] = pk;
+                rs = pair_sum<kBF16>(pk, rs);
+              }
+              pnew[qt][2 * st + h] = w;
+            }
+          rs_blk[qt] = rs;
+          l_run[qt] *= alpha;
+          // O rescale after PV_{j-1} (issued above), before PV_j
+          if (grow_any) {
+  #pragma unroll
+            for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha;
+          }
+        }
+      }
+  #pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) l_run[qt] += rs_blk[qt];
+      // keep P_j and l in this region, beside the MFMAs
   #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
   #pragma unroll
         for (int cc = 0; cc < 2 * kST; ++cc) asm volatile("" : "+v"(pnew[qt][cc]));
         asm volatile("" : "+v"(l_run[qt]));
-      }
-      if constexpr (kSched > 0) {
-        // issue order: the DMA, the first fragments, then per MFMA step the
-        // fragments kSched steps ahead between the two MFMAs and a share of the
-        // softmax VALU after each
-        constexpr int kSteps = 8 * kST;
-        __builtin_amdgcn_sched_group_barrier(sched::kVmemRead, 2 * kDmaPerWave, 0);
-        __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3 * kSched, 0);
-  #pragma unroll
-        for (int step = 0; step < kSteps; ++step) {
-          __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
-          if (step + kSched < kSteps) __builtin_amdgcn_sched_group_barrier(sched::kDsRead, 3, 0);
-          __builtin_amdgcn_sched_group_barrier(sched::kMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(sched::kValu, 3, 0);
-        }
-      }
-      // lazy rescale of O (after PV_{j-1}, before PV_j); the empty asm keeps the
-      // compiler from turning the branch into an unconditional multiply
-      if (grow_any) {
-        asm volatile("");
-  #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
-  #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= alpha[qt];
       }
       __syncthreads();
     };
@@ -729,15 +755,15 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 
 }  // namespace v2
 
-#define SILE_FA_V2_KERNEL(NAME, BF, QT, W, NK, SCHED)                                         \
+#define SILE_FA_V2_KERNEL(NAME, BF, QT, W, NK)                                                \
   extern "C" __global__ __launch_bounds__(W * 64, 1) void NAME(                               \
       const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
     __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::lds_bytes<NK>()];              \
-    v2::attn_fwd_v2<BF, QT, W, NK, SCHED>(Q, K, V, O, a, smem);                               \
+    v2::attn_fwd_v2<BF, QT, W, NK>(Q, K, V, O, a, smem);                                      \
   }
 // 8 waves x 32 queries (two waves per SIMD) over 32-key blocks
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 0)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32, 0)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32)
+SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32)
 
 #define SILE_FA_KERNEL(NAME, BF, QT, NK, DH)                                                  \
   extern "C" __global__ __launch_bounds__(kThreads, 1) void NAME(                             \

@@ -157,7 +157,7 @@ def test_flash_causal_pairs_bit_identical(hip, b, h):
 @pytest.mark.parametrize("kernel", ["pipelined", "q128"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("trend", ["rising", "falling", "large"])
+@pytest.mark.parametrize("trend", ["rising", "falling", "large", "plateau"])
 def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     """Scores that move the running max across the sequence.  rising: key j
     carries an offset growing with j, so later blocks exceed the running max
@@ -165,7 +165,11 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     and stale-block path of the kernels runs); falling: the first block holds
     the maximum and later p underflow; large: scores of standard deviation
     ~30, so many p of a block overflow the 16-bit type unless the block is
-    rescaled first."""
+    rescaled first; plateau: the first 32 keys score 0 and every later key
+    ~39.19 (5 log2 units after the softmax scale, inside the lazy margin), so
+    every later block's p are 2^5 = 32 against the stale max: each lane's
+    block sum (512) takes the pipelined kernel's block-max path, which finds
+    no growth and keeps the max."""
     b, h, s, d = 1, 8, KERNEL_S[kernel], 128
     say(f"flash rescale {kernel} {dt} causal={causal} {trend}")
     r = rng(77)
@@ -175,6 +179,11 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     if trend == "large":
         q *= 5.0
         k *= 5.0
+    elif trend == "plateau":
+        q[:] = 0.0
+        q[..., 0] = 4.0
+        k[..., 0] = 0.0
+        k[:, :, 32:, 0] = 9.8
     else:
         ramp = np.linspace(0.0, 1.0, s, dtype=np.float32)
         if trend == "falling":
