@@ -19,6 +19,13 @@ on this host's cores; each component carries its own `cpu_baseline` on a
 bounded sample of its workload (whole softmax and 4096^3 GEMM, every 8th row
 tile of the fp8 GEMM, four whole heads of each attention workload).
 
+Each MFMA workload also carries `same_kernel_on_zero_inputs`: the same launch
+timed again after its inputs are zero-filled.  The chip is power-limited under
+random data (its engine clock falls from 2.4 GHz to ~1.8 GHz), and all-zero
+operands do not toggle the matrix-core datapath, so the ratio of that rate to
+`value` is the clock the workload loses to the power limit.  It never replaces
+`value`.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
                        [--no-cpu-baseline]
 """
@@ -165,6 +172,26 @@ def load_traffic():
     return {}
 
 
+ZERO_STEPS = 10  # launches timed again on all-zero inputs (MFMA workloads)
+
+
+def zero_input_rate(launch, inputs, work, peak, steps, stream):
+    """The same launch, timed again after its input buffers are filled with
+    zeros: with nothing toggling the matrix-core datapath the power-managed
+    engine clock stays near its 2.4 GHz peak, so this rate over `value` is
+    the clock the chip gives up under the random-data workload.  Reported
+    beside `value`, never in its place."""
+    for buf in inputs:
+        buf.fill_bytes(0)
+    n = min(steps, ZERO_STEPS)
+    region = time_launches(launch, n, 2, stream)
+    v = work / (region / n * 1e-3) / 1e12
+    return {"value": round(v, 2), "unit": "TFLOP/s", "frac_of_peak": round(v / peak, 4),
+            "ms_per_step": round(region / n, 4),
+            "note": "same kernel and launch on all-zero inputs (output not checked); "
+                    "the ratio to value is the engine-clock loss under random data"}
+
+
 def roofline_obj(bound, achieved, peak, unit, traffic):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -194,6 +221,8 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0
     res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "mfma", PEAK_TFLOPS[kind],
                     traffic.get(name))
     res["flop_per_launch"] = flop
+    res["same_kernel_on_zero_inputs"] = zero_input_rate(launch, (da, db), flop, PEAK_TFLOPS[kind],
+                                                        steps, stream)
     for buf in (da, db, dc):
         buf.close()
     if host is not None:
@@ -243,6 +272,8 @@ def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0):
                     traffic.get(name))
     res["flop_per_launch"] = flop
     res["flop_convention"] = "4*D*B*H*S*(S+1)/2 (causal pairs only)"
+    res["same_kernel_on_zero_inputs"] = zero_input_rate(launch, bufs, flop, PEAK_TFLOPS["f16"],
+                                                        steps, stream)
     for buf in bufs + [do]:
         buf.close()
     if cpu_heads:
@@ -673,6 +704,10 @@ def main():
         frac = r.get("roofline", {}).get("frac")
         log(f"[bench] {name}: {r['value']} {r['unit']} ({r['ms_per_step']} ms/step"
             + (f", {100 * frac:.1f}% of peak)" if frac is not None else ")"))
+        z = r.get("same_kernel_on_zero_inputs")
+        if z:
+            log(f"[bench] {name}: same kernel on all-zero inputs {z['value']} {z['unit']} "
+                f"({100 * z['frac_of_peak']:.1f}% of peak; the rest is the power-managed clock)")
 
     head = results.get("gemm_bf16_8192") or next(iter(results.values()))
     head_cpu = None
