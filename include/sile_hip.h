@@ -161,7 +161,10 @@ int sile_hip_launch_tiles_noalloc(sile_hip_function fn, void *const *buffers,
  * the result of crates/sile-backend/src/emit.rs:241-296 infer_tile_plan;
  * plan_output_param < 0 selects the CPU wrapper's fallbacks.  This is the
  * codegen half of CodegenTarget / BackendArtifact
- * (crates/sile-backend/src/lib.rs:11-26) for a HIP target. */
+ * (crates/sile-backend/src/lib.rs:11-26) for a HIP target.  The buffer
+ * parameters are emitted restrict-qualified: as for the DSL's tensors (`&T`
+ * inputs, `&mut T` outputs, crates/sile-core/src/kernel.rs:8-14), a buffer a
+ * kernel writes must not overlap any other buffer argument of the launch. */
 
 /* Writes the generated HIP source (NUL-terminated) into out[out_capacity];
  * *out_len receives its length.  Parse errors -> SILE_ERR_COMPILE.  Needs no

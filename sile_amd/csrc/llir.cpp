@@ -665,6 +665,23 @@ std::string c_decl(const Type& t, const std::string& name) {
   return c_scalar(t) + " " + name;
 }
 
+// declaration of a kernel buffer parameter: restrict-qualified.  A DSL
+// kernel's tensors are Rust references (`&T` inputs, `&mut T` outputs,
+// crates/sile-core/src/kernel.rs:8-14), so no output aliases another
+// parameter; the qualifier lets the compiler overlap the loads of one
+// element with the stores of another.
+std::string c_decl_buffer(const Type& t, const std::string& name) {
+  if (t.k != TK::Ptr) return c_decl(t, name);
+  if (!t.elem) return "float* __restrict__ " + name;
+  Type base;
+  std::vector<int64_t> dims;
+  array_shape(*t.elem, base, dims);
+  if (dims.empty()) return c_scalar(base) + "* __restrict__ " + name;
+  std::string d;
+  for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
+  return c_scalar(base) + " (* __restrict__ " + name + ")" + d;
+}
+
 std::string ident(const std::string& name) {
   std::string out = "v_";
   for (char c : name) out += (isalnum((unsigned char)c) || c == '_') ? c : '_';
@@ -791,7 +808,7 @@ struct Emitter {
     o << "__device__ static void sile_llvm_ir_" << fn.name << "(";
     for (size_t k = 0; k < fn.params.size(); ++k) {
       const Param& p = fn.params[k];
-      o << (k ? ", " : "") << (is_shapes(p) ? "long long* " + ident(p.name) : c_decl(p.ty, ident(p.name)));
+      o << (k ? ", " : "") << (is_shapes(p) ? "long long* " + ident(p.name) : c_decl_buffer(p.ty, ident(p.name)));
     }
     o << ", long long sile_gid_0, long long sile_gid_1, long long sile_gid_2) {\n";
     o << "  (void)sile_gid_0; (void)sile_gid_1; (void)sile_gid_2;\n";
