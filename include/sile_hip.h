@@ -128,7 +128,9 @@ int sile_hip_module_get(sile_hip_module module, const char *name, sile_hip_funct
  * const int64_t *shapes, int64_t num_shapes) where `buffers` and `shapes` are
  * device copies of the host arrays given here (buffers in kernel-param order,
  * shapes = every arg's dims concatenated).  The kernel applies the
- * `pid < total_tiles` guard itself.  Synchronous, like apply(). */
+ * `pid < total_tiles` guard itself.  Synchronous, like apply().  The device
+ * copies of the tables go into buffers of a per-device pool that the library
+ * allocates on demand and reuses (never freed before the process ends). */
 int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t num_buffers,
                           const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],
                           uint32_t threads_per_program, sile_hip_stream stream);
@@ -139,7 +141,8 @@ int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t nu
  * arguments, semantics and synchronous return as sile_hip_launch_tiles, but
  * the device copies of the buffer and shape tables go into a fixed 4 KiB
  * array of the library (one per device, held until the process ends) rather
- * than into a buffer allocated and freed per call: num_buffers + num_shapes
+ * than into a pooled buffer that sile_hip_launch_tiles allocates when its
+ * per-device pool has none free: num_buffers + num_shapes
  * may not exceed 512 (SILE_ERR_SHAPE beyond).  Calls on one device share
  * that array, so calls that overlap on one device (from several threads or
  * streams) race; each call writes the tables it needs before its launch. */

@@ -1,7 +1,8 @@
 // sile_hip_launch_tiles_noalloc: the generic tile launch for callers that
 // cannot allocate device memory (code under HIP graph capture, serving loops
 // that forbid allocation).  sile_hip_launch_tiles copies the buffer-pointer
-// and shape tables into a device buffer it allocates and frees on every call;
+// and shape tables into a device buffer from a per-device pool, which it
+// allocates (hipMalloc) whenever no pooled buffer is free or large enough;
 // this variant copies them into `scratch`, a fixed device array of this
 // library that lives until the process ends, and calls no allocating routine.
 //

@@ -338,6 +338,46 @@ int sile_hip_module_get(sile_hip_module module, const char* name, sile_hip_funct
 
 namespace {
 
+// Device buffers for the launch tables, kept per device and reused: a launch
+// takes one, and returns it once the kernel has finished, so the synchronous
+// launches neither allocate nor free device memory after the first calls
+// (hipFree would also wait for the whole device, other streams included).
+constexpr int kTablePoolDevices = 64;
+struct TablePool {
+  std::mutex mu;
+  std::vector<std::pair<void*, size_t>> free_list;
+};
+TablePool g_table_pools[kTablePoolDevices];
+
+int table_acquire(size_t bytes, int* dev_out, void** out, size_t* cap_out) {
+  int dev = 0;
+  SILE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kTablePoolDevices)
+    return fail(SILE_ERR_INVALID_DEVICE, "device %d beyond the %d the table pool covers", dev,
+                kTablePoolDevices);
+  *dev_out = dev;
+  {
+    std::lock_guard<std::mutex> lk(g_table_pools[dev].mu);
+    auto& fl = g_table_pools[dev].free_list;
+    for (size_t i = 0; i < fl.size(); ++i)
+      if (fl[i].second >= bytes) {
+        *out = fl[i].first;
+        *cap_out = fl[i].second;
+        fl.erase(fl.begin() + (long)i);
+        return ok();
+      }
+  }
+  const size_t cap = bytes < 4096 ? 4096 : bytes;
+  SILE_HIP_CHECK(hipMalloc(out, cap));
+  *cap_out = cap;
+  return ok();
+}
+
+void table_release(int dev, void* p, size_t cap) {
+  std::lock_guard<std::mutex> lk(g_table_pools[dev].mu);
+  g_table_pools[dev].free_list.push_back({p, cap});
+}
+
 // Uploads the buffer-pointer and shape tables, launches `fn` over `workgroups`
 // workgroups of `threads` threads with (buffers, programs, shapes, num_shapes)
 // and waits for it.
@@ -349,7 +389,10 @@ int launch_with_tables(hipFunction_t fn, void* const* buffers, int64_t num_buffe
   const size_t buf_bytes = (size_t)num_buffers * sizeof(void*);
   const size_t shp_bytes = (size_t)num_shapes * sizeof(int64_t);
   void* table = nullptr;
-  SILE_HIP_CHECK(hipMalloc(&table, buf_bytes + shp_bytes + 16));
+  size_t table_cap = 0;
+  int dev = 0;
+  int rc = table_acquire(buf_bytes + shp_bytes + 16, &dev, &table, &table_cap);
+  if (rc != SILE_OK) return rc;
   std::vector<unsigned char> host(buf_bytes + shp_bytes + 16);
   if (buf_bytes) memcpy(host.data(), buffers, buf_bytes);
   if (shp_bytes) memcpy(host.data() + buf_bytes, shapes, shp_bytes);
@@ -362,9 +405,11 @@ int launch_with_tables(hipFunction_t fn, void* const* buffers, int64_t num_buffe
     e = hipModuleLaunchKernel(fn, (unsigned)workgroups, 1, 1, threads, 1, 1, 0, s, params, nullptr);
   }
   if (e == hipSuccess) e = hipStreamSynchronize(s);
-  hipError_t e2 = hipFree(table);
-  if (e != hipSuccess) return hip_fail(e, "kernel launch");
-  if (e2 != hipSuccess) return hip_fail(e2, "hipFree");
+  if (e != hipSuccess) {
+    // the table may still be in use by a failed or unfinished launch: not reused
+    return hip_fail(e, "kernel launch");
+  }
+  table_release(dev, table, table_cap);
   return ok();
 }
 
