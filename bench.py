@@ -469,6 +469,71 @@ def bench_tile_ir_softmax(name, steps, warmup):
     return res
 
 
+def bench_reduce_rows(name, steps, warmup, stream):
+    """Row max and row sum over fp32 [8192, 8192] (the reference's reduce and
+    its fused load + vec4 sum, bit-identical): sile_hip_reduce_rows (max) and
+    sile_hip_reduce_rows_fused_sum, each launch reading 256 MiB from HBM (two
+    inputs rotate, 512 MiB, past the 256 MiB Infinity Cache).  `value` is the
+    row sum's rate; the max is listed beside it."""
+    rows = cols = 8192
+    log(f"[bench] {name}: generating inputs")
+    x = normal(3, (rows, cols), 2.0)
+    rotate = 2
+    xs = [hip.DeviceBuffer.from_array(x) for _ in range(rotate)]
+    del x
+    out = hip.DeviceBuffer(rows * 4)
+    nbytes = 4.0 * rows * cols + 4.0 * rows
+
+    def row_sum(i):
+        hip.reduce_rows_fused_sum(rows, cols, xs[i].ptr, cols, rows * cols, out.ptr, stream)
+
+    def row_max(i):
+        hip.reduce_rows(hip.REDUCE_MAX, hip.F32, rows, cols, xs[i].ptr, cols, out.ptr, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    region = time_launches(row_sum, steps, warmup, stream, rotate=rotate)
+    res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    mx = time_launches(row_max, steps, warmup, stream, rotate=rotate) / steps
+    res["row_max"] = {"value": round(nbytes / (mx * 1e-3) / 1e9, 2), "unit": "GB/s",
+                      "ms_per_step": round(mx, 4),
+                      "frac_of_peak": round(nbytes / (mx * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    for buf in xs + [out]:
+        buf.close()
+    return res
+
+
+def bench_parallel_reduce(name, steps, warmup):
+    """The reference's parallel_reduce (crates/sile/examples/parallel_reduce.rs: one atomic add of
+    each program's fused vec4 tile sum into out[0]) over 64M fp32 elements,
+    TILE = 4096 (16384 programs), through the synchronous DSL entry point
+    sile_hip_kernel_parallel_reduce, like apply(); 256 MiB read per call."""
+    n, tile = 1 << 26, 4096
+    programs = n // tile
+    log(f"[bench] {name}: generating inputs")
+    a = normal(1, (n,), 1.0)
+    da = hip.DeviceBuffer.from_array(a)
+    del a
+    dout = hip.DeviceBuffer.from_array(np.zeros(1, np.float32))
+
+    def call():
+        hip.kernel_parallel_reduce([da.ptr, dout.ptr], programs, [n, 1], tile)
+
+    for _ in range(warmup):
+        call()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    dt = (time.perf_counter() - t0) / steps
+    nbytes = 4.0 * n
+    res = summarise(name, nbytes, 1e9, "GB/s", dt * 1e3 * steps, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    res["note"] = "synchronous calls timed on the host clock (launch and wait per call)"
+    for buf in (da, dout):
+        buf.close()
+    return res
+
+
 def bench_gemm_f32_exact(name, size, steps, warmup, stream, traffic, cpu=False):
     """fp32 GEMM M=N=K=size in the reference's canonical per-cell order
     (bit-identical to its CPU backend), A and B row-major U(-1,1) (seeds 1/2,
@@ -641,7 +706,7 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
 EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f32_exact_4096",
-         "gemm_f32_exact_512"]
+         "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32"]
 
 
 def main():
@@ -682,6 +747,10 @@ def main():
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
         elif name == "tile_ir_softmax_f32_8192":
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
+        elif name == "reduce_rows_f32_8192":
+            results[name] = bench_reduce_rows(name, args.steps, args.warmup, stream)
+        elif name == "parallel_reduce_f32":
+            results[name] = bench_parallel_reduce(name, args.steps, args.warmup)
         elif name.startswith("gemm_f32_exact_"):
             size = int(name.split("_")[-1])
             results[name] = bench_gemm_f32_exact(name, size, args.steps, args.warmup, stream,

@@ -126,6 +126,53 @@ namespace sched {
 constexpr int kValu = 0x002, kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 }
 
+// Fused load + vec4 sums of rows whose width is a multiple of 4 past 16
+// (the reference's loop form: windows ((v0 + v1) + v2) + v3 added in window
+// order from 0.0f, crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:1182-1256),
+// at HBM rate.  The window sums are independent; only their accumulation is
+// one chain per row.  A workgroup of 256 threads owns kFsRows rows (16-byte
+// aligned) and walks them in chunks of kFsChunk columns: all threads load the
+// chunk with 16-byte loads and write its window sums to LDS `w`
+// (kFsRows * kFsPitch floats), then lane r of wave 0 adds row r's window sums
+// to its running sum in window order, reading them four at a time (row pitch
+// kFsWin + 4 floats: 16-byte aligned, rows 4 banks apart).  Several
+// workgroups per CU overlap one's chains with another's loads.  Returns the
+// sum of row row0 + tid for tid < nrows (0.0f elsewhere).
+constexpr int kFsRows = 4;
+constexpr int kFsChunk = 1024;                  // columns per chunk
+constexpr int kFsWin = kFsChunk / 4;            // windows per row and chunk
+constexpr int kFsPitch = kFsWin + 4;            // LDS floats per row
+SILE_DEV float fused_sum_rows_tiled(const float* __restrict__ x, int64_t cols, int64_t ldx,
+                                    int64_t row0, int nrows, float* w) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  float acc = 0.0f;
+  for (int64_t c0 = 0; c0 < cols; c0 += kFsChunk) {
+    const int win = (int)((cols - c0) / 4 < kFsWin ? (cols - c0) / 4 : kFsWin);
+    for (int e = tid; e < nrows * win; e += 256) {
+      const int r = e / win, i = e - r * win;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(x + (row0 + r) * ldx + c0 + 4 * i);
+      w[r * kFsPitch + i] = ((v[0] + v[1]) + v[2]) + v[3];
+    }
+    __syncthreads();
+    if (tid < nrows) {
+      const float* wr = w + tid * kFsPitch;
+      const int win4 = win & ~3;
+#pragma unroll 4
+      for (int i = 0; i < win4; i += 4) {
+        const f32x4 q = *reinterpret_cast<const f32x4*>(wr + i);
+        acc = acc + q[0];
+        acc = acc + q[1];
+        acc = acc + q[2];
+        acc = acc + q[3];
+      }
+      for (int i = win4; i < win; ++i) acc = acc + wr[i];
+    }
+    __syncthreads();
+  }
+  return acc;
+}
+
 // 2^x on the transcendental unit (v_exp_f32).
 SILE_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -108,6 +108,23 @@ struct ReduceTileArgs {
 // per-program partial is bit-identical to the CPU backend's.  Programs then
 // add their partial to out[0] atomically; the order across programs is
 // unspecified there as here.
+// TILE > 16 with TILE % 4 == 0 and a 16-byte aligned: no window runs past a
+// tile and there is no tail, so kFsRows programs share a workgroup and their
+// tile sums come from fused_sum_rows_tiled (the same windows, added in the
+// same order: bit-identical partials), then go to out[0] atomically.
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_parallel_reduce_f32_tiled(
+    const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
+    int64_t programs, int64_t tile) {
+  __shared__ __attribute__((aligned(16))) float w[kFsRows * kFsPitch];
+  const int64_t pid0 = (int64_t)blockIdx.x * kFsRows;
+  const int nprog = (int)min((int64_t)kFsRows, programs - pid0);
+  const float acc = fused_sum_rows_tiled(a, tile, tile, pid0, nprog, w);
+  if ((int)threadIdx.x < nprog) {
+    if (partials) partials[pid0 + threadIdx.x] = acc;
+    atomicAdd(out, acc);
+  }
+}
+
 extern "C" __global__ __launch_bounds__(64) void sile_dsl_parallel_reduce_f32(
     const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
     ReduceTileArgs args) {

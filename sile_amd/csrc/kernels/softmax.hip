@@ -473,6 +473,19 @@ extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32
   out[row] = acc;
 }
 
+// The same sums for cols > 16 with cols % 4 == 0 and 16-byte aligned rows
+// (no window runs past a row, no tail), at HBM rate (fused_sum_rows_tiled):
+// same arithmetic, same order as sile_reduce_rows_fused_sum_f32, so
+// bit-identical to it.
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32_tiled(
+    const float* __restrict__ x, float* __restrict__ out, int64_t rows, int64_t cols, int64_t ldx) {
+  __shared__ __attribute__((aligned(16))) float w[kFsRows * kFsPitch];
+  const int64_t row0 = (int64_t)blockIdx.x * kFsRows;
+  const int nrows = (int)min((int64_t)kFsRows, rows - row0);
+  const float acc = fused_sum_rows_tiled(x, cols, ldx, row0, nrows, w);
+  if ((int)threadIdx.x < nrows) out[row0 + threadIdx.x] = acc;
+}
+
 // ---- 2-D copy: y[r][0, row_bytes) = x[r][0, row_bytes) ----
 // Workgroup (r, s) of the grid copies segment s of row r: kCopySegB bytes, two 16-byte
 // chunks per thread of 512 (chunk j of thread t at (j * 512 + t) * 16), both

@@ -213,10 +213,17 @@ int sile_hip_kernel_parallel_reduce(void* const* buffers, int64_t num_threadgrou
                 (long long)tile, (long long)len);
   const void* a = buffers[0];
   void* out = buffers[1];
-  void* params[] = {&a, &out, &partials, &t};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32", dim3((unsigned)run), dim3(64), params,
-              s);
+  if (tile > 16 && tile % 4 == 0 && aligned16(a)) {
+    // whole windows only: 4 programs per workgroup, window sums in parallel
+    void* params[] = {&a, &out, &partials, &run, &tile};
+    rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32_tiled", dim3((unsigned)((run + 3) / 4)),
+                dim3(256), params, s);
+  } else {
+    void* params[] = {&a, &out, &partials, &t};
+    rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32", dim3((unsigned)run), dim3(64),
+                params, s);
+  }
   if (rc != SILE_OK) return rc;
   SILE_HIP_CHECK(hipStreamSynchronize(s));
   return ok();
@@ -476,6 +483,15 @@ int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float* x, i
   if (x_len < (rows - 1) * ldx + cols)
     return fail(SILE_ERR_SHAPE, "x_len %lld does not cover %lld rows of %lld at pitch %lld",
                 (long long)x_len, (long long)rows, (long long)cols, (long long)ldx);
+  if (cols > 16 && cols % 4 == 0 && ldx % 4 == 0 && aligned16(x)) {
+    // no window past a row: window sums in parallel, one chain per row (4 rows per workgroup)
+    const int64_t blocks = (rows + 3) / 4;
+    if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+    void* params[] = {(void*)&x, &out, &rows, &cols, &ldx};
+    int rc = launch(Module::kSoftmax, "sile_reduce_rows_fused_sum_f32_tiled",
+                    dim3((unsigned)blocks), dim3(256), params, static_cast<hipStream_t>(stream));
+    return rc == SILE_OK ? ok() : rc;
+  }
   const int64_t blocks = (rows + 255) / 256;
   if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
   void* params[] = {(void*)&x, &out, &rows, &cols, &ldx, &x_len};

@@ -166,3 +166,46 @@ def test_softmax_masked_tail_padded(hip, dt, cols):
     else:
         assert_close(got[:, :cols], ref, atol=1e-30, rtol=1e-4, what="masked tail")
     assert (raw[:, cols:] == fill).all()
+
+
+@pytest.mark.parametrize("rows,cols,ldx", [(33, 20, 20), (100, 1000, 1000), (64, 1024, 1028),
+                                           (31, 4100, 4100), (70, 8192, 8192), (5, 12288, 12300),
+                                           (40, 18, 18), (9, 1003, 1003), (7, 16, 16), (3, 3, 3)])
+def test_reduce_rows_fused_sum_bit_exact(hip, rows, cols, ldx):
+    """sile_hip_reduce_rows_fused_sum against the oracle's fused vec4 order,
+    bit for bit: aligned rows of a multiple of 4 past 16 columns run the
+    chunked kernel (window sums in parallel, one chain per row; chunks of
+    1024 columns, ragged last chunk, row pitch past cols, rows not a multiple
+    of 32), the others the one-lane-per-row kernel."""
+    say(f"fused row sum {rows}x{cols} ldx={ldx}")
+    x = rng(rows * cols).normal(size=(rows, ldx)).astype(np.float32) * np.float32(3.0)
+    x[:, :cols:7] = -0.0
+    want = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4, cols=cols)
+    dx = hip.DeviceBuffer.from_array(x)
+    dout = hip.DeviceBuffer(rows * 4)
+    dout.fill_bytes(0xFF)
+    hip.reduce_rows_fused_sum(rows, cols, dx.ptr, ldx, x.size, dout.ptr)
+    hip.synchronize()
+    got = dout.download(np.float32, (rows,))
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_reduce_rows_fused_sum_order_probes(hip):
+    """Closed forms the chunked kernel must keep: [1, 1, 2^24, 0] windows give
+    2^24 + 2 per window order (a pairwise tree gives 2^24), rows of -0.0 past
+    16 columns sum to +0.0 (the loop starts from 0.0f), and a row of ones of
+    width 4 k sums to 4 k."""
+    big = np.float32(2.0 ** 24)
+    rows, cols = 3, 2048
+    x = np.zeros((rows, cols), np.float32)
+    x[0, 0:4] = [1.0, 1.0, big, 0.0]
+    x[1, :] = -0.0
+    x[2, :] = 1.0
+    dx = hip.DeviceBuffer.from_array(x)
+    dout = hip.DeviceBuffer(rows * 4)
+    hip.reduce_rows_fused_sum(rows, cols, dx.ptr, cols, x.size, dout.ptr)
+    hip.synchronize()
+    got = dout.download(np.float32, (rows,))
+    want = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert got[0] == big + 2 and not np.signbit(got[1]) and got[1] == 0.0 and got[2] == cols
