@@ -548,11 +548,7 @@ __device__ __forceinline__ void gemm_small_body(const uint8_t* __restrict__ A,
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  for (int64_t k0 = 0; k0 < g.kp; k0 += kKStep) {
-    const int64_t kg = k0 + grp * kGrpK;
-    u32x4 fa[kCh], fb[kCh];
-    frag(ap, a_ok, kg, fa);
-    frag(bp, b_ok, kg, fb);
+  auto mma = [&](const u32x4 (&fa)[kCh], const u32x4 (&fb)[kCh]) {
     if constexpr (kIsFP8) {
       acc = mma32x32_fp8(fa, fb, acc);
     } else if constexpr (kKind == kBF16) {
@@ -562,6 +558,48 @@ __device__ __forceinline__ void gemm_small_body(const uint8_t* __restrict__ A,
       acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[0]),
                                                     __builtin_bit_cast(f16x8, fb[0]), acc, 0, 0, 0);
     }
+  };
+  // Whole k-steps in blocks of kU, the loads of the next block in flight
+  // while the current block's MFMAs run (two register sets), so the chain is
+  // not held up by the global-load latency of each step; then the remaining
+  // steps one at a time (the last may be partial).  The k order is the same.
+  constexpr int kU = kIsFP8 ? 4 : 8;
+  constexpr int64_t kBlk = (int64_t)kU * kKStep;
+  const int64_t kfull = (g.kp / kBlk) * kBlk;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  auto load_blk = [&](int64_t k0, u32x4 (&fa)[kU][kCh], u32x4 (&fb)[kU][kCh]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t kg = k0 + u * kKStep + grp * kGrpK;
+#pragma unroll
+      for (int h = 0; h < kCh; ++h) {
+        fa[u][h] = a_ok ? *reinterpret_cast<const u32x4*>(ap + kg * kEB + 16 * h) : zero4;
+        fb[u][h] = b_ok ? *reinterpret_cast<const u32x4*>(bp + kg * kEB + 16 * h) : zero4;
+      }
+    }
+  };
+  auto mma_blk = [&](const u32x4 (&fa)[kU][kCh], const u32x4 (&fb)[kU][kCh]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) mma(fa[u], fb[u]);
+  };
+  if (kfull > 0) {
+    u32x4 fa0[kU][kCh], fb0[kU][kCh], fa1[kU][kCh], fb1[kU][kCh];
+    load_blk(0, fa0, fb0);
+    for (int64_t k0 = 0; k0 < kfull; k0 += 2 * kBlk) {
+      const bool more = k0 + kBlk < kfull;
+      if (more) load_blk(k0 + kBlk, fa1, fb1);
+      mma_blk(fa0, fb0);
+      if (!more) break;
+      if (k0 + 2 * kBlk < kfull) load_blk(k0 + 2 * kBlk, fa0, fb0);
+      mma_blk(fa1, fb1);
+    }
+  }
+  for (int64_t k0 = kfull; k0 < g.kp; k0 += kKStep) {
+    const int64_t kg = k0 + grp * kGrpK;
+    u32x4 fa[kCh], fb[kCh];
+    frag(ap, a_ok, kg, fa);
+    frag(bp, b_ok, kg, fb);
+    mma(fa, fb);
   }
   const int64_t col = col0 + r;
   if (col >= g.n) return;
