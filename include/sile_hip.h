@@ -240,6 +240,13 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *                        path (M, N >= 256 with N a multiple of 4 and C's rows
  *                        16-byte aligned: 256 x 256 tiles through LDS; other
  *                        shapes: 64 x 64 tiles).
+ * When the 256 x 256 tiles are fewer than the device's CUs and K' is long, K'
+ * is split into ranges computed side by side: their fp32 partial C planes go
+ * to a device scratch buffer shared by all calls on the device (allocated on
+ * the first such call, grown when a call needs more, at most
+ * 4 * (CUs * 65536) bytes; calls on different streams are ordered on the GPU
+ * by an event) and a second kernel adds them in range order.  The result
+ * does not depend on the stream or on earlier calls.
  * M = 0 or N = 0: nothing is written.  K' = 0 (K below one bk): C = +0.0 for
  * any M, N and supported types, as the canonical matmul's sums start at 0.0f
  * and add no term (canonical_matmul.rs:58-73).

@@ -45,7 +45,27 @@ struct GemmArgs {
   float alpha;
   int32_t m, n;           // C extents (>= 256): the last tile row / column starts at m - 256 / n - 256
   int32_t k_rem;          // elements of the last half k-step inside K' (1 .. a half k-step)
+  int32_t split_steps;    // half k-steps per k-range (even, or k_steps when K is not split)
+  int64_t c_split;        // elements between the C planes of consecutive k-ranges
 };
+
+// The k-range of a workgroup: blockIdx.y selects half k-steps
+// [y * split_steps, min((y + 1) * split_steps, k_steps)); only the range that
+// ends at K' has a partial last half k-step.
+struct KRange {
+  int64_t byte0;          // first byte of the range in a row of A / B
+  int32_t k_steps, k_rem;
+};
+template <int kEB>
+SILE_DEV KRange k_range(const GemmArgs& g) {
+  const int y = blockIdx.y;
+  const int h0 = y * g.split_steps;
+  KRange r;
+  r.byte0 = (int64_t)h0 * 64;
+  r.k_steps = min(g.split_steps, g.k_steps - h0);
+  r.k_rem = h0 + r.k_steps == g.k_steps ? g.k_rem : 64 / kEB;
+  return r;
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -86,8 +106,8 @@ struct TilePlan {
 };
 
 template <int kEB>
-SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& g, int wave,
-                            int lane) {
+SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& g, int64_t byte0,
+                            int wave, int lane) {
   TilePlan p;
   // XCD-aware tile order: workgroups go round-robin to the 8 XCDs; each XCD
   // gets a contiguous range of tiles, grouped 8 tile-rows at a time
@@ -111,10 +131,11 @@ SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& 
   p.col0 = min(tile_n * kBN, g.n - kBN);
   p.a_rs = (int)(g.lda * kEB);
   p.b_rs = (int)(g.ldb * kEB);
-  p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs), (short)0,
-                                               kBM * p.a_rs, 0x00020000);
-  p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs), (short)0,
-                                               kBN * p.b_rs, 0x00020000);
+  // (a k-range that starts byte0 bytes into the rows moves the base, not the end)
+  p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs + byte0), (short)0,
+                                               (int)(kBM * p.a_rs - byte0), 0x00020000);
+  p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs + byte0), (short)0,
+                                               (int)(kBN * p.b_rs - byte0), 0x00020000);
   // wave w's load instruction i (0..7) of an operand fills rows
   // 8 (4 i + w) + (lane >> 3), position lane & 7, whose chunk is
   // (lane & 7) ^ ((row >> 1) & 7) with (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3)
@@ -256,7 +277,8 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2>(A, B, g, wave, lane);
+  const KRange kr = k_range<kIsFP8 ? 1 : 2>(g);
+  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2>(A, B, g, kr.byte0, wave, lane);
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // LDS-DMA bases in SGPRs
 
   Acc acc[kNB][kNB];
@@ -268,8 +290,8 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
       for (int r = 0; r < (int)(sizeof(Acc) / 4); ++r) acc[i][j][r] = 0.0f;
 
   u32x4 xa[kNB][kCh], xb[kNB][kCh], ya[kNB][kCh], yb[kNB][kCh];
-  const int last = (g.k_steps - 1) >> 1;      // index of the last (possibly half) k-step
-  const bool half_last = (g.k_steps & 1) != 0;
+  const int last = (kr.k_steps - 1) >> 1;     // index of the last (possibly half) k-step
+  const bool half_last = (kr.k_steps & 1) != 0;
   const int f_row = lane % kBlk, f_grp = lane / kBlk;
   const int f_swz = (f_row >> 1) & 7;         // block rows differ by multiples of 16
   const int a_fb = (wm * 128 + f_row) * kRowB, b_fb = (wn * 128 + f_row) * kRowB;
@@ -353,8 +375,8 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
         for (int q = 0; q < kNB; ++q)
 #pragma unroll
           for (int h = 0; h < kCh; ++h) {
-            xa[q][h] = mask_k<kIsFP8>(xa[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), g.k_rem);
-            xb[q][h] = mask_k<kIsFP8>(xb[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), g.k_rem);
+            xa[q][h] = mask_k<kIsFP8>(xa[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), kr.k_rem);
+            xb[q][h] = mask_k<kIsFP8>(xb[q][h], (kCh * f_grp + h) * (kIsFP8 ? 16 : 8), kr.k_rem);
           }
       }
     }
@@ -372,7 +394,7 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 #pragma unroll
           for (int h = 0; h < kCh; ++h) {
             const int e0 = (kCh * f_grp + h) * (kIsFP8 ? 16 : 8);
-            const int lim = half_last ? 0 : g.k_rem;
+            const int lim = half_last ? 0 : kr.k_rem;
             if (q < kNB) ya[q][h] = mask_k<kIsFP8>(ya[q][h], e0, lim);
             else yb[q - kNB][h] = mask_k<kIsFP8>(yb[q - kNB][h], e0, lim);
           }
@@ -457,7 +479,9 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
     __syncthreads();   // every wave is done reading the ring
     stage_and_store_c<kOut>(C, g.ldc, m0, n0, smem + wave * kCStageB, each_c4);
   } else {
-    each_c4([&](int row, int col, f32x4 v) { store_c4<kOut>(C, (m0 + row) * g.ldc + n0 + col, v); });
+    // fp32 C: the plane of this workgroup's k-range (plane 0 when K is not split)
+    float* cz = static_cast<float*>(C) + (int64_t)blockIdx.y * g.c_split;
+    each_c4([&](int row, int col, f32x4 v) { store_c4<kOut>(cz, (m0 + row) * g.ldc + n0 + col, v); });
   }
 }
 
@@ -479,6 +503,38 @@ SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
+
+// Split K: the ring kernel above writes one fp32 plane of C per k-range
+// (planes `plane` elements apart, rows n elements long); this kernel adds the
+// planes in k-range order, scales by alpha and writes C in its type.  N is a
+// multiple of 4; workgroup (x, y) takes 4-element groups 256 x + t of rows
+// y, y + gridDim.y, ...
+template <int kOut>
+__device__ __forceinline__ void splitk_reduce_body(const float* __restrict__ ws,
+                                                   void* __restrict__ C, int64_t ldc, int64_t m,
+                                                   int64_t n, int64_t plane, int splits,
+                                                   float alpha) {
+  const int64_t c4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (c4 >= n) return;
+  for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
+    const float* src = ws + row * n + c4;
+    f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src));
+    for (int z = 1; z < splits; ++z)
+      v += __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + z * plane));
+    if (alpha != 1.0f) v *= alpha;
+    store_c4<kOut>(C, row * ldc + c4, v);
+  }
+}
+
+#define SILE_GEMM_SPLITK_REDUCE(NAME, OUT)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const float* ws, void* C, int64_t ldc, \
+                                                         int64_t m, int64_t n, int64_t plane,   \
+                                                         int splits, float alpha) {             \
+    splitk_reduce_body<OUT>(ws, C, ldc, m, n, plane, splits, alpha);                          \
+  }
+SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_bf16, kOutBF16)
+SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_f16, kOutF16)
+SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_f32, kOutF32)
 
 // ---------------------------------------------------------------------------
 // Any shape: M or N below one 256 x 256 tile, or N not a multiple of 4.

@@ -42,7 +42,47 @@ struct GemmArgs {
   float alpha;
   int32_t m, n;
   int32_t k_rem;  // elements of the last half k-step inside K'
+  int32_t split_steps;  // half k-steps per k-range (even, or k_steps unsplit)
+  int64_t c_split;      // elements between the fp32 C planes of the k-ranges
 };
+
+// K split for the 256 x 256-tile GEMM when its tiles leave CUs idle: the
+// number of k-ranges that minimises a time model fitted to measurements on
+// MI355X (bf16, 14 shapes from 1024^3 to 256 x 8192 x 8192, most within 10 %):
+//   a tile over k elements of K' takes k * t(w) + 6 us, t(w) = 16 ns per
+//   element while w <= 128 workgroups run, rising linearly to 21.8 ns at
+//   256 (the clock drops as more CUs draw power); half that for fp8;
+//   a split adds the burst of fp32 planes the workgroups write as they all
+//   finish, the second launch reading them and writing C (both at 5.2 TB/s),
+//   and 4 us of launch and ordering.
+// Every range keeps at least 8 whole k-steps.
+int64_t gemm_splits(int64_t tiles, int64_t half_steps, int64_t kp, int64_t m, int64_t n,
+                    int64_t cb, bool fp8) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 1;
+  if (tiles >= cus) return 1;
+  auto per_k = [&](int64_t w) {
+    const double t = w <= 128 ? 16e-9 : 16e-9 + 5.8e-9 * (double)(w - 128) / 128.0;
+    return fp8 ? t / 2 : t;
+  };
+  const int64_t max_splits = std::min<int64_t>(cus / tiles, half_steps / 16);
+  const double t1 = per_k(tiles) * (double)kp + 6e-6;
+  int64_t best = 1;
+  double best_t = t1;
+  for (int64_t sp = 2; sp <= max_splits; ++sp) {
+    const double planes = 4.0 * (double)sp * (double)m * (double)n;
+    const double t = per_k(tiles * sp) * (double)((kp + sp - 1) / sp) + 6e-6 +
+                     (2 * planes + (double)(cb * m * n)) / 5.2e12 + 4e-6;
+    if (t < best_t) {
+      best_t = t;
+      best = sp;
+    }
+  }
+  // a split only when the model expects it to save more than 5 %
+  return best_t < 0.95 * t1 ? best : 1;
+}
 
 const char* dtype_name(int t) {
   switch (t) {
@@ -317,10 +357,49 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   const int64_t half_steps = (kp + kstep - 1) / kstep;
   if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
   GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
-             scale_a * scale_b, (int32_t)m, (int32_t)n, (int32_t)(kp - (half_steps - 1) * kstep)};
-  void* params[] = {&a, &b, &c, &g};
-  int rc = launch(Module::kGemm, name, dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), params,
-                  s);
+             scale_a * scale_b, (int32_t)m, (int32_t)n, (int32_t)(kp - (half_steps - 1) * kstep),
+             (int32_t)half_steps, 0};
+  const unsigned tiles = (unsigned)(g.tiles_m * g.tiles_n);
+  int64_t splits = gemm_splits(tiles, half_steps, kp, m, n, (int64_t)cb, kstep == 64);
+  void* ws = nullptr;
+  if (splits >= 2) {
+    // whole k-steps per range; the last range takes what is left of K'
+    int64_t per = (half_steps + splits - 1) / splits;
+    per += per & 1;
+    splits = (half_steps + per - 1) / per;
+    g.split_steps = (int32_t)per;
+  }
+  if (splits < 2) {
+    void* params[] = {&a, &b, &c, &g};
+    int rc = launch(Module::kGemm, name, dim3(tiles), dim3(256), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+  // k-ranges side by side: fp32 planes of C in the device scratch, then their
+  // sum in k-range order, scaled and converted
+  int rc = scratch_acquire((size_t)(splits * m * n) * sizeof(float), s, &ws);
+  if (rc != SILE_OK) return rc;
+  char pname[64];
+  snprintf(pname, sizeof pname, "sile_gemm_nt_%s_f32",
+           a_type == SILE_BF16 ? "bf16" : a_type == SILE_F16 ? "f16" : "fp8");
+  const float alpha = g.alpha;
+  g.alpha = 1.0f;
+  g.ldc = n;
+  g.c_split = m * n;
+  void* params[] = {&a, &b, &ws, &g};
+  rc = launch(Module::kGemm, pname, dim3(tiles, (unsigned)splits), dim3(256), params, s);
+  if (rc == SILE_OK) {
+    const char* rname = c_type == SILE_BF16  ? "sile_gemm_splitk_reduce_bf16"
+                        : c_type == SILE_F16 ? "sile_gemm_splitk_reduce_f16"
+                                             : "sile_gemm_splitk_reduce_f32";
+    int64_t plane = m * n, ldc_ = ldc, m_ = m, n_ = n;
+    int sp = (int)splits;
+    float al = alpha;
+    void* rp[] = {&ws, &c, &ldc_, &m_, &n_, &plane, &sp, &al};
+    rc = launch(Module::kGemm, rname,
+                dim3((unsigned)((n / 4 + 255) / 256), (unsigned)std::min<int64_t>(m, 65535)),
+                dim3(256), rp, s);
+  }
+  scratch_release(s);
   return rc == SILE_OK ? ok() : rc;
 }
 

@@ -154,6 +154,68 @@ int resident_blocks(Module m, const char* name, int block_threads, int64_t* out)
   return SILE_OK;
 }
 
+namespace {
+constexpr int kScratchDevices = 64;
+struct DeviceScratch {
+  std::mutex mu;
+  void* p = nullptr;
+  size_t cap = 0;
+  hipEvent_t last = nullptr;   // recorded after the last user's kernels
+  bool used = false;
+};
+DeviceScratch g_scratch[kScratchDevices];
+thread_local int t_scratch_dev = -1;   // the device whose lock this thread holds
+}  // namespace
+
+int scratch_acquire(size_t bytes, hipStream_t s, void** out) {
+  int dev = 0;
+  SILE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(SILE_ERR_INVALID_DEVICE, "device %d beyond the %d the scratch covers", dev,
+                kScratchDevices);
+  DeviceScratch& d = g_scratch[dev];
+  d.mu.lock();
+  auto bail = [&](hipError_t e, const char* what) {
+    d.mu.unlock();
+    return hip_fail(e, what);
+  };
+  hipError_t e = hipSuccess;
+  if (!d.last && (e = hipEventCreateWithFlags(&d.last, hipEventDisableTiming)) != hipSuccess)
+    return bail(e, "hipEventCreateWithFlags");
+  if (d.cap < bytes) {
+    if (d.p) {
+      // the previous buffer may still be in use on another stream
+      if (d.used && (e = hipEventSynchronize(d.last)) != hipSuccess)
+        return bail(e, "hipEventSynchronize");
+      (void)hipFree(d.p);
+      d.p = nullptr;
+      d.cap = 0;
+    }
+    if ((e = hipMalloc(&d.p, bytes)) != hipSuccess) {
+      d.p = nullptr;
+      return bail(e, "hipMalloc(scratch)");
+    }
+    d.cap = bytes;
+  }
+  if (d.used && (e = hipStreamWaitEvent(s, d.last, 0)) != hipSuccess)
+    return bail(e, "hipStreamWaitEvent");
+  t_scratch_dev = dev;
+  *out = d.p;
+  return SILE_OK;
+}
+
+void scratch_release(hipStream_t s) {
+  const int dev = t_scratch_dev;
+  if (dev < 0) return;
+  DeviceScratch& d = g_scratch[dev];
+  if (hipEventRecord(d.last, s) == hipSuccess)
+    d.used = true;
+  else
+    (void)hipStreamSynchronize(s);   // this call's kernels (and those s waited for) are done
+  t_scratch_dev = -1;
+  d.mu.unlock();
+}
+
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds) {
   hipFunction_t f = nullptr;

@@ -405,3 +405,51 @@ def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, k, bk):
     tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
     assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} truncated ragged")
     assert np.isfinite(got[:, :n]).all()
+
+
+@pytest.mark.parametrize("kind,out,m,n,k,bk", [
+    ("bf16", "bf16", 256, 256, 8192, 0),    # 1 tile: 16 k-ranges of 512
+    ("bf16", "f32", 300, 260, 5000, 0),     # 4 tiles, ragged; the last range ends in a half k-step
+    ("f16", "f16", 512, 512, 6000, 70),     # K' = 5950 ends 30 elements into a half k-step
+    ("fp8", "bf16", 512, 256, 4096, 0),     # scales applied once, after the ranges are summed
+    ("fp8", "f32", 256, 300, 3072, 0),
+])
+def test_split_k(hip, kind, out, m, n, k, bk):
+    """Few 256 x 256 tiles and a long K': the GEMM splits K' into ranges that
+    run side by side (fp32 planes of C in stream-ordered scratch) and sums
+    them in range order; on a 256-CU device every case here splits.  Every
+    element is checked, C sits in a wider pitch whose columns past N keep
+    their fill, and a second call gives the same bits."""
+    kp = (k // bk) * bk if bk else k
+    ldc = n + 8
+    say(f"gemm split-K {kind} {m}x{n}x{k} bk={bk} -> {out}")
+    a = rng(31).normal(size=(m, k)).astype(np.float32)
+    bt = rng(32).normal(size=(n, k)).astype(np.float32)
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    raws = []
+    for _ in range(2):
+        dc.fill_bytes(0xFF)
+        hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+                 dc.ptr, ldc, sa, sb, bk)
+        hip.synchronize()
+        raws.append(dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc)))
+    assert (raws[0] == raws[1]).all(), "split-K result differs between two calls"
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} split-K")
+    assert (raws[0][:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
