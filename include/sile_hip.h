@@ -237,11 +237,12 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
  *                        A row-major, B column-major, any M, N, K', A and B
  *                        (and their leading dimensions) 16-byte aligned; MFMA
- *                        path (M, N >= 256 with N a multiple of 4 and C's rows
- *                        16-byte aligned: 256 x 256 tiles through LDS; other
- *                        shapes: 64 x 64 tiles).
- * When the 256 x 256 tiles are fewer than the device's CUs and K' is long, K'
- * is split into ranges computed side by side: their fp32 partial C planes go
+ *                        path (M, N >= 256, or >= 128 with 16-bit operands,
+ *                        N a multiple of 4 and C's rows 16-byte aligned:
+ *                        256 x 256 or 128 x 128 tiles through LDS, the size
+ *                        chosen by shape; other shapes: 64 x 64 tiles).
+ * When the tiles are fewer than the device's CUs and K' is long, K' may be
+ * split into ranges computed side by side: their fp32 partial C planes go
  * to a device scratch buffer shared by all calls on the device (allocated on
  * the first such call, grown when a call needs more, at most
  * 4 * (CUs * 65536) bytes; calls on different streams are ordered on the GPU
@@ -255,6 +256,19 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
                   int64_t k, const void *a, int64_t lda, sile_layout a_layout, const void *b,
                   int64_t ldb, sile_layout b_layout, void *c, int64_t ldc, float scale_a,
                   float scale_b, int64_t bk, sile_hip_stream stream);
+
+/* sile_hip_gemm with the tile size and the K split chosen by the caller
+ * instead of by shape.  No counterpart in the reference; for tests that must
+ * reach each kernel and for tuning.  tile: 0 (by shape), 256, or 128 (16-bit
+ * operands only); a forced size the shape cannot take (M or N below it, N not
+ * a multiple of 4, C's rows not 16-byte aligned) -> SILE_ERR_SHAPE.  splits:
+ * 0 (by shape) or 1 .. 64 ranges of K' (fewer when K' has fewer whole
+ * k-steps); a split needs splits * M * N * 4 bytes of the device scratch. */
+int sile_hip_gemm_tiled(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m,
+                        int64_t n, int64_t k, const void *a, int64_t lda, sile_layout a_layout,
+                        const void *b, int64_t ldb, sile_layout b_layout, void *c, int64_t ldc,
+                        float scale_a, float scale_b, int64_t bk, int32_t tile, int32_t splits,
+                        sile_hip_stream stream);
 
 /* fp32 tile MMA with a seeded accumulator, in the reference's exact order:
  * C[r][c] = the chain s = s + A[r][k] * B[k][c] over k < K' (K' = (K / bk) * bk,

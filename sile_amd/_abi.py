@@ -134,6 +134,8 @@ SIGNATURES = {
     "sile_hip_kernel_parallel_reduce": [_P, _I64, _I64, _P, _I64, _I64, _P, _P],
     "sile_hip_gemm": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32, _P,
                       _I64, _F32, _F32, _I64, _P],
+    "sile_hip_gemm_tiled": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32,
+                            _P, _I64, _F32, _F32, _I64, _I32, _I32, _P],
     "sile_hip_mma_f32": [_I64, _I64, _I64, _P, _I64, _P, _I64, _I32, _P, _I64, _F32, _P, _I64, _I64,
                          _P],
     "sile_hip_softmax_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _I64, _P],
@@ -401,9 +403,15 @@ def tile_ir_launch(route: Route, bufs, shapes, num_threadgroups: int, stream=Non
 # ---------------------------------------------------------------------------
 
 def gemm(a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout, c, ldc,
-         scale_a=1.0, scale_b=1.0, bk=0, stream=None):
-    call("sile_hip_gemm", a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout,
-         c, ldc, scale_a, scale_b, bk, _sh(stream))
+         scale_a=1.0, scale_b=1.0, bk=0, stream=None, tile=0, splits=0):
+    """sile_hip_gemm; tile / splits other than 0 force the tile size and the
+    K split (sile_hip_gemm_tiled)."""
+    if tile or splits:
+        call("sile_hip_gemm_tiled", a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb,
+             b_layout, c, ldc, scale_a, scale_b, bk, tile, splits, _sh(stream))
+    else:
+        call("sile_hip_gemm", a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb,
+             b_layout, c, ldc, scale_a, scale_b, bk, _sh(stream))
 
 
 def mma_f32(m, n, k, a, lda, b, ldb, b_layout, acc, ld_acc, acc_value, c, ldc, bk=0, stream=None):

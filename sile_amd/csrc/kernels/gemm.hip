@@ -19,8 +19,6 @@ using namespace sile;
 
 namespace {
 
-constexpr int kBM = 256, kBN = 256;
-
 enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
 enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
 
@@ -83,20 +81,20 @@ SILE_DEV f32x16 mma32x32_fp8(const u32x4* a, const u32x4* b, f32x16 c) {
 // ---------------------------------------------------------------------------
 // Tile placement.
 //
-// 256 x 256 output tile per workgroup of 4 waves (2 x 2, 128 x 128 per wave).
+// kT x kT output tile per workgroup of 4 waves (2 x 2, kT/2 x kT/2 per wave),
+// kT = 256 (one workgroup per CU) or 128 (16-bit operands, two per CU).
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
 // instruction of a wave fills 1 KiB of LDS, lane l writing bytes
 // [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
 // at its LDS slot under the swizzle.  A k-step is 128 bytes of each row (64
 // 16-bit or 128 fp8 elements), so one instruction fetches 8 whole 128-byte
-// lines, and one operand of one k-step is a 32 KiB tile.  Rows hold 8 chunks
+// lines, and one operand of one k-step is a kT x 128-byte tile (32 or 16 KiB).  Rows hold 8 chunks
 // of 16 bytes; chunk c of row r sits at c ^ ((r >> 1) & 7), which puts the
 // fragment reads of 16 or 32 consecutive rows (one chunk each) on distinct
-// banks.  The buffer resources cover the tile's 256-row A and B panels (loads
+// banks.  The buffer resources cover the tile's kT-row A and B panels (loads
 // past a panel return zero).
 // ---------------------------------------------------------------------------
 constexpr int kRowB = 128;            // bytes of a tile row per k-step
-constexpr int kTileB = 256 * kRowB;   // one operand of one k-step: 32 KiB
 
 struct TilePlan {
   int64_t row0, col0;                 // first row / column of the tile in C
@@ -105,7 +103,7 @@ struct TilePlan {
   int a_voff, b_voff;                 // this lane's byte offsets for the tile loads
 };
 
-template <int kEB>
+template <int kEB, int kT>
 SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& g, int64_t byte0,
                             int wave, int lane) {
   TilePlan p;
@@ -123,19 +121,19 @@ SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& 
   const int in_group = lin - group * group_size;
   const int tile_m = first_m + in_group % rows_in_group;
   const int tile_n = in_group / rows_in_group;
-  // When M or N is not a multiple of 256 the last tile is moved back to end
+  // When M or N is not a multiple of kT the last tile is moved back to end
   // at M / N, so every load stays inside the operands; the rows or columns it
   // shares with its neighbour are computed in the same order by both
   // workgroups and written with the same values.
-  p.row0 = min(tile_m * kBM, g.m - kBM);
-  p.col0 = min(tile_n * kBN, g.n - kBN);
+  p.row0 = min(tile_m * kT, g.m - kT);
+  p.col0 = min(tile_n * kT, g.n - kT);
   p.a_rs = (int)(g.lda * kEB);
   p.b_rs = (int)(g.ldb * kEB);
   // (a k-range that starts byte0 bytes into the rows moves the base, not the end)
   p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs + byte0), (short)0,
-                                               (int)(kBM * p.a_rs - byte0), 0x00020000);
+                                               (int)(kT * p.a_rs - byte0), 0x00020000);
   p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs + byte0), (short)0,
-                                               (int)(kBN * p.b_rs - byte0), 0x00020000);
+                                               (int)(kT * p.b_rs - byte0), 0x00020000);
   // wave w's load instruction i (0..7) of an operand fills rows
   // 8 (4 i + w) + (lane >> 3), position lane & 7, whose chunk is
   // (lane & 7) ^ ((row >> 1) & 7) with (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3)
@@ -159,45 +157,48 @@ SILE_DEV void mma16x16(const u32x4& a, const u32x4& b, f32x4& c) {
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 
-// 16-bit C through LDS: a wave's 128 x 128 results are put into LDS rows of
-// 256 + 16 bytes (the pad puts the rows that one put instruction of the
-// accumulator layouts writes on distinct banks), then written back so that
-// each store instruction covers whole 256-byte rows of C (16-byte stores, 4
-// rows per instruction; 8-byte stores, 2 rows, when C's rows are not 16-byte
-// aligned).  Writing straight from the accumulator layouts touches 16 or 32
+// 16-bit C through LDS: a wave's kW x kW results (kW = 128 or 64) are put
+// into LDS rows of 2 kW + 16 bytes (the pad puts the rows that one put
+// instruction of the accumulator layouts writes on distinct banks), then
+// written back so that each store instruction covers whole 2 kW-byte rows of
+// C (16-byte stores, 512 / kW rows per instruction; 8-byte stores, half as
+// many, when C's rows are not 16-byte aligned).  Writing straight from the accumulator layouts touches 16 or 32
 // rows per instruction with 8 bytes each and ran 5 % slower at 8192^3, with
 // twice C's size written to HBM.  fill(put) calls put(row, col, v) for 4
 // consecutive columns of the wave's tile; the wave's LDS region is its own.
-constexpr int kCRowB = 256 + 16;
-constexpr int kCStageB = 128 * kCRowB;   // one wave's staged C: 34 KiB
+template <int kW> constexpr int kCRowB = 2 * kW + 16;
+template <int kW> constexpr int kCStageB = kW * kCRowB<kW>;   // one wave's staged C (34 KiB at kW = 128)
 
-template <int kOut, typename Fill>
+template <int kOut, int kW, typename Fill>
 SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, uint8_t* cst,
                                 Fill fill) {
   static_assert(kOut != kOutF32, "16-bit C");
+  constexpr int kRowBytes = kCRowB<kW>;
   fill([&](int row, int col, f32x4 v) {
     const u32x2 w = kOut == kOutBF16 ? u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}
                                      : u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
-    *reinterpret_cast<u32x2*>(cst + row * kCRowB + col * 2) = w;
+    *reinterpret_cast<u32x2*>(cst + row * kRowBytes + col * 2) = w;
   });
   __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));  // lgkmcnt(0)
   __builtin_amdgcn_wave_barrier();
   const int lane = threadIdx.x & 63;
   uint16_t* cbase = static_cast<uint16_t*>(C) + m0 * ldc + n0;
   if ((ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(cbase) & 15) == 0) {
-    const int lr = lane & 15, lg = lane >> 4;
+    constexpr int kLanesPerRow = kW / 8, kRowsPerStore = 64 / kLanesPerRow;
+    const int lr = lane % kLanesPerRow, lg = lane / kLanesPerRow;
 #pragma unroll 8
-    for (int t = 0; t < 32; ++t) {
-      const int row = 4 * t + lg;
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(cst + row * kCRowB + lr * 16),
+    for (int t = 0; t < kW / kRowsPerStore; ++t) {
+      const int row = kRowsPerStore * t + lg;
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(cst + row * kRowBytes + lr * 16),
                                   reinterpret_cast<u32x4*>(cbase + row * ldc + lr * 8));
     }
   } else {
-    const int lr = lane & 31, lg = lane >> 5;
+    constexpr int kLanesPerRow = kW / 4, kRowsPerStore = 64 / kLanesPerRow;
+    const int lr = lane % kLanesPerRow, lg = lane / kLanesPerRow;
 #pragma unroll 8
-    for (int t = 0; t < 64; ++t) {
-      const int row = 2 * t + lg;
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x2*>(cst + row * kCRowB + lr * 8),
+    for (int t = 0; t < kW / kRowsPerStore; ++t) {
+      const int row = kRowsPerStore * t + lg;
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x2*>(cst + row * kRowBytes + lr * 8),
                                   reinterpret_cast<u32x2*>(cbase + row * ldc + lr * 4));
     }
   }
@@ -206,11 +207,11 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 // ---------------------------------------------------------------------------
 // The GEMM body: a ring of 5 LDS tiles, tile loads spread over the k-step.
 //
-// A wave's 128 x 128 is kNB x kNB blocks of one MFMA (256 fp32 accumulators
-// per lane):
-//   bf16 / f16: 8 x 8 blocks of v_mfma_f32_16x16x32_{bf16,f16};
-//   fp8 e4m3:   4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (unscaled: zero
-//               scale operands select the plain instruction).
+// A wave's kW x kW (kW = kT / 2) is kNB x kNB blocks of one MFMA (256 fp32
+// accumulators per lane at kW = 128, 64 at kW = 64):
+//   bf16 / f16: kW / 16 square blocks of v_mfma_f32_16x16x32_{bf16,f16};
+//   fp8 e4m3:   4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (kT = 256 only;
+//               unscaled: zero scale operands select the plain instruction).
 // The MFMA is issued with the B fragment first, so accumulator register r of
 // lane l is C[m = l % 16][n = 4 (l / 16) + r] of a 16 x 16 block and
 // C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of a 32 x 32 block.  A
@@ -219,12 +220,12 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 // 16-byte chunks 4 sub + kCh (l / kBlk) + h of the row (kCh = 1 for 16-bit,
 // 2 for fp8).  Sub-step 0's fragments go to register set X, sub-step 1's to Y.
 //
-// LDS holds a ring of 5 tiles (160 KiB): k-step ks's A tile is chunk 2 ks and
+// LDS holds a ring of 5 tiles (160 KiB; 80 at kT = 128): k-step ks's A tile is chunk 2 ks and
 // its B tile chunk 2 ks + 1; chunk c sits in slot c % 5.  The barrier that
 // starts k-step ks frees the slots of k-step ks - 1, which receive B of
 // ks + 1 and A of ks + 2, so every tile load has one or two k-steps to land
-// and a wave's 16 load instructions of a k-step can be spread evenly over it
-// (one per 128 MFMA cycles).  (Two 64 KiB stages force the loads into the
+// and a wave's kT / 16 load instructions of a k-step can be spread evenly
+// over it (one per group of MFMAs).  (Two 64 KiB stages force the loads into the
 // first half of the k-step, where they fill the load queue and stall the
 // MFMAs issued behind them: 7-13 % slower.)
 //
@@ -236,7 +237,7 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 // A group is the kNB MFMAs of one accumulator row in quarters, with the
 // fragment reads and tile loads at fixed places (Q MFMA, reads, Q MFMA,
 // reads, Q MFMA, loads, Q MFMA), fenced so the compiler keeps that order;
-// loads 0..7 of a k-step are B of ks + 1, 8..15 A of ks + 2.  k_steps counts
+// the first kT / 32 loads of a k-step are B of ks + 1, the rest A of ks + 2.  k_steps counts
 // half k-steps (64 bytes of a row): an odd count ends with a half k-step
 // whose sub-step 1 multiplies zero fragments.
 // ---------------------------------------------------------------------------
@@ -262,23 +263,27 @@ SILE_DEV u32x4 mask_k(u32x4 w, int e0, int k_rem) {
   return w;
 }
 
-template <int kKind, int kOut>
+template <int kKind, int kOut, int kT>
 __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
                                                const uint8_t* __restrict__ B,
                                                void* __restrict__ C, const GemmArgs& g,
                                                uint8_t* smem) {
   constexpr bool kIsFP8 = kKind == kFP8;
   constexpr int kBlk = kIsFP8 ? 32 : 16;      // MFMA block edge
-  constexpr int kNB = 128 / kBlk;             // blocks per wave edge
+  constexpr int kW = kT / 2;                  // wave tile edge
+  constexpr int kNB = kW / kBlk;              // blocks per wave edge
+  constexpr int kTB = kT * kRowB;             // one operand tile of one k-step in LDS
+  constexpr int kOpLoads = kT / 32;           // load instructions per operand, k-step and wave
+  static_assert(kNB % 4 == 0, "groups are issued in quarters");
   constexpr int kCh = kIsFP8 ? 2 : 1;         // 16-byte chunks per lane per fragment
   constexpr int kQ = kNB / 4;                 // MFMAs per quarter group
-  constexpr int kLoadsPerGroup = 16 / (2 * kNB);
+  constexpr int kLoadsPerGroup = 2 * kOpLoads / (2 * kNB);
   using Acc = std::conditional_t<kIsFP8, f32x16, f32x4>;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const KRange kr = k_range<kIsFP8 ? 1 : 2>(g);
-  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2>(A, B, g, kr.byte0, wave, lane);
+  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2, kT>(A, B, g, kr.byte0, wave, lane);
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // LDS-DMA bases in SGPRs
 
   Acc acc[kNB][kNB];
@@ -294,11 +299,11 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   const bool half_last = (kr.k_steps & 1) != 0;
   const int f_row = lane % kBlk, f_grp = lane / kBlk;
   const int f_swz = (f_row >> 1) & 7;         // block rows differ by multiples of 16
-  const int a_fb = (wm * 128 + f_row) * kRowB, b_fb = (wn * 128 + f_row) * kRowB;
+  const int a_fb = (wm * kW + f_row) * kRowB, b_fb = (wn * kW + f_row) * kRowB;
 
   // tile load instruction i (0..7) of operand B (or A) of k-step ks into slot
   auto load = [&](bool is_b, int ks, int slot, int i) {
-    uint8_t* dst = smem + slot * kTileB + wave_s * 1024 + i * 4096;
+    uint8_t* dst = smem + slot * kTB + wave_s * 1024 + i * 4096;
     if (is_b)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(p.b_rsrc, (lds_ptr_t)dst, 16, p.b_voff,
                                                i * 32 * p.b_rs + ks * kRowB, 0, 0);
@@ -313,10 +318,10 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
     for (int h = 0; h < kCh; ++h) {
       const int off = ((4 * sub + kCh * f_grp + h) ^ f_swz) << 4;
       if (q < kNB)
-        fa[q][h] = *reinterpret_cast<const u32x4*>(smem + sa * kTileB + a_fb +
+        fa[q][h] = *reinterpret_cast<const u32x4*>(smem + sa * kTB + a_fb +
                                                    q * kBlk * kRowB + off);
       else
-        fb[q - kNB][h] = *reinterpret_cast<const u32x4*>(smem + sb * kTileB + b_fb +
+        fb[q - kNB][h] = *reinterpret_cast<const u32x4*>(smem + sb * kTB + b_fb +
                                                          (q - kNB) * kBlk * kRowB + off);
     }
   };
@@ -344,10 +349,10 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
     auto loads = [&]() {
 #pragma unroll
       for (int t = 0; t < kLoadsPerGroup; ++t, ++n) {
-        if (n < 8) {
+        if (n < kOpLoads) {
           if constexpr (kLoadB) load(true, ks + 1, lb, n);
         } else {
-          if constexpr (kLoadA) load(false, ks + 2, la, n - 8);
+          if constexpr (kLoadA) load(false, ks + 2, la, n - kOpLoads);
         }
       }
     };
@@ -409,9 +414,9 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 #pragma unroll
     for (int r = 0; r < kNB / 2; ++r) group(ya, yb, r, 1, 0, 0, ya, yb);
     // B of ks + 1 (and A of ks + 1, loaded a k-step earlier) landed: only the
-    // 8 loads of A of ks + 2 may still be in flight
+    // kOpLoads loads of A of ks + 2 may still be in flight
     if constexpr (kLoadA)
-      __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));
+      __builtin_amdgcn_s_waitcnt(kOpLoads | (0x7 << 4) | (0x0 << 8));
     else
       __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
     __builtin_amdgcn_s_barrier();
@@ -421,19 +426,19 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 
   // prologue: A of 0 -> slot 0, B of 0 -> slot 1, A of 1 -> slot 2; Y(-1) is zero
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load(false, 0, 0, i);
+  for (int i = 0; i < kOpLoads; ++i) load(false, 0, 0, i);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load(true, 0, 1, i);
+  for (int i = 0; i < kOpLoads; ++i) load(true, 0, 1, i);
   if (last >= 1) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load(false, 1, 2, i);
+    for (int i = 0; i < kOpLoads; ++i) load(false, 1, 2, i);
   }
 #pragma unroll
   for (int i = 0; i < kNB; ++i)
 #pragma unroll
     for (int h = 0; h < kCh; ++h) ya[i][h] = yb[i][h] = u32x4{0u, 0u, 0u, 0u};
   if (last >= 1)
-    __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0x0 << 8));   // A and B of 0 landed
+    __builtin_amdgcn_s_waitcnt(kOpLoads | (0x7 << 4) | (0x0 << 8));   // A and B of 0 landed
   else
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0x0 << 8));
   __builtin_amdgcn_s_barrier();
@@ -453,7 +458,7 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   // wait states before their results are read (32 > what a 16x16x32 needs)
   if constexpr (!kIsFP8) asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
   // ---- epilogue: calls f(row, col, v) for the 4 consecutive columns of each
-  // accumulator register group (row, col within the wave's 128 x 128) ----
+  // accumulator register group (row, col within the wave's kW x kW) ----
   auto each_c4 = [&](auto f) {
 #pragma unroll
     for (int i = 0; i < kNB; ++i)
@@ -474,10 +479,10 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
         }
       }
   };
-  const int64_t m0 = p.row0 + wm * 128, n0 = p.col0 + wn * 128;
+  const int64_t m0 = p.row0 + wm * kW, n0 = p.col0 + wn * kW;
   if constexpr (kOut != kOutF32) {
     __syncthreads();   // every wave is done reading the ring
-    stage_and_store_c<kOut>(C, g.ldc, m0, n0, smem + wave * kCStageB, each_c4);
+    stage_and_store_c<kOut, kW>(C, g.ldc, m0, n0, smem + wave * kCStageB<kW>, each_c4);
   } else {
     // fp32 C: the plane of this workgroup's k-range (plane 0 when K is not split)
     float* cz = static_cast<float*>(C) + (int64_t)blockIdx.y * g.c_split;
@@ -487,22 +492,29 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 
 }  // namespace
 
-#define SILE_GEMM_KERNEL(NAME, KIND, OUT)                                                     \
-  extern "C" __global__ __launch_bounds__(256, 1) void NAME(const void* A, const void* B,      \
-                                                            void* C, GemmArgs g) {             \
-    static_assert(4 * kCStageB <= 5 * kTileB, "staged C fits the ring");                     \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[5 * kTileB];                       \
-    gemm_ring_body<KIND, OUT>(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),  \
-                              C, g, smem);                                                     \
+#define SILE_GEMM_KERNEL(NAME, KIND, OUT, KT)                                                 \
+  extern "C" __global__ __launch_bounds__(256, 256 / KT) void NAME(const void* A,              \
+                                                                   const void* B, void* C,      \
+                                                                   GemmArgs g) {               \
+    static_assert(4 * kCStageB<KT / 2> <= 5 * KT * kRowB, "staged C fits the ring");           \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[5 * KT * kRowB];                   \
+    gemm_ring_body<KIND, OUT, KT>(static_cast<const uint8_t*>(A),                             \
+                                  static_cast<const uint8_t*>(B), C, g, smem);                \
   }
 
 // k_steps counts half k-steps: 32 elements (16-bit) or 64 (fp8)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16)
-SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt_bf16_f32, kBF16, kOutF32, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32, 256)
+// 128 x 128 tiles (16-bit operands): shapes whose 256 x 256 tiles would leave
+// CUs idle, and M or N in [128, 256)
+SILE_GEMM_KERNEL(sile_gemm_nt128_bf16_bf16, kBF16, kOutBF16, 128)
+SILE_GEMM_KERNEL(sile_gemm_nt128_bf16_f32, kBF16, kOutF32, 128)
+SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f16, kF16, kOutF16, 128)
+SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f32, kF16, kOutF32, 128)
 
 // Split K: the ring kernel above writes one fp32 plane of C per k-range
 // (planes `plane` elements apart, rows n elements long); this kernel adds the

@@ -46,42 +46,74 @@ struct GemmArgs {
   int64_t c_split;      // elements between the fp32 C planes of the k-ranges
 };
 
-// K split for the 256 x 256-tile GEMM when its tiles leave CUs idle: the
-// number of k-ranges that minimises a time model fitted to measurements on
-// MI355X (bf16, 14 shapes from 1024^3 to 256 x 8192 x 8192, most within 10 %):
-//   a tile over k elements of K' takes k * t(w) + 6 us, t(w) = 16 ns per
-//   element while w <= 128 workgroups run, rising linearly to 21.8 ns at
-//   256 (the clock drops as more CUs draw power); half that for fp8;
-//   a split adds the burst of fp32 planes the workgroups write as they all
-//   finish, the second launch reading them and writing C (both at 5.2 TB/s),
-//   and 4 us of launch and ordering.
-// Every range keeps at least 8 whole k-steps.
-int64_t gemm_splits(int64_t tiles, int64_t half_steps, int64_t kp, int64_t m, int64_t n,
-                    int64_t cb, bool fp8) {
+// Tile size and K split of the LDS GEMM kernels: the pair that minimises a
+// time model fitted to measurements on MI355X (forced tile sizes and split
+// counts over bf16 shapes from 1024^3 to 256 x 8192 x 8192):
+//   a tile over k elements of K' takes k * t(w) + 6 us (4.7 us for 128 x
+//   128), where t depends on the tile size and on how many workgroups w run
+//   at once (the clock drops as more CUs draw power; two 128 x 128
+//   workgroups share a CU); half that for fp8 (256 x 256 only); workgroups
+//   beyond what the device holds at once run in further rounds;
+//   a split of K' into S ranges (at least 8 whole k-steps each, all ranges
+//   resident at once) adds the burst of fp32 planes the workgroups write as
+//   they finish, the second launch reading them and writing C (both at
+//   5.2 TB/s), and 4 us of launch and ordering; it is taken only for a
+//   modelled gain above 5 %.
+struct GemmPlan {
+  int tile;        // 256 or 128
+  int64_t splits;  // k-ranges (1: K' not split)
+};
+
+// seconds per element of K' for one tile, with w workgroups of that size
+// running at once on `cus` CUs (fitted: 256 x 256 16 ns up to cus / 2
+// workgroups, 21.8 ns at cus; 128 x 128 7.2 ns up to cus / 2, 7.8 ns at cus,
+// 13.3 ns at 2 cus, two sharing each CU)
+double tile_time_per_k(int tile, int64_t w, int cus) {
+  const double half = cus / 2.0;
+  const double f = std::min(1.0, std::max(0.0, ((double)w - half) / half));
+  if (tile == 256) return 16e-9 + 5.8e-9 * f;
+  if (w <= cus) return 7.2e-9 + 0.6e-9 * f;
+  return 7.8e-9 + 5.5e-9 * std::min(1.0, (double)(w - cus) / cus);
+}
+
+GemmPlan gemm_plan(int64_t m, int64_t n, int64_t kp, int64_t half_steps, int64_t cb, bool fp8,
+                   int only_tile) {
+  GemmPlan best{only_tile ? only_tile : m >= 256 && n >= 256 ? 256 : 128, 1};
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 1;
-  if (tiles >= cus) return 1;
-  auto per_k = [&](int64_t w) {
-    const double t = w <= 128 ? 16e-9 : 16e-9 + 5.8e-9 * (double)(w - 128) / 128.0;
-    return fp8 ? t / 2 : t;
-  };
-  const int64_t max_splits = std::min<int64_t>(cus / tiles, half_steps / 16);
-  const double t1 = per_k(tiles) * (double)kp + 6e-6;
-  int64_t best = 1;
-  double best_t = t1;
-  for (int64_t sp = 2; sp <= max_splits; ++sp) {
-    const double planes = 4.0 * (double)sp * (double)m * (double)n;
-    const double t = per_k(tiles * sp) * (double)((kp + sp - 1) / sp) + 6e-6 +
-                     (2 * planes + (double)(cb * m * n)) / 5.2e12 + 4e-6;
-    if (t < best_t) {
-      best_t = t;
-      best = sp;
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return best;
+  double best_t = 1e30, best_unsplit_t = 1e30;
+  GemmPlan best_unsplit = best;
+  for (int tile : {256, 128}) {
+    if (tile == 128 && fp8) continue;
+    if (m < tile || n < tile || (only_tile && tile != only_tile)) continue;
+    const int64_t tiles = ((m + tile - 1) / tile) * ((n + tile - 1) / tile);
+    const int64_t slots = (int64_t)cus * (tile == 256 ? 1 : 2);
+    const int64_t max_splits = std::min<int64_t>(slots / tiles, half_steps / 16);
+    for (int64_t sp = 1; sp == 1 || sp <= max_splits; ++sp) {
+      // full rounds of `slots` workgroups, then the rest
+      const int64_t w = tiles * sp, full = w / slots, rest = w % slots;
+      const double per_k = (double)full * tile_time_per_k(tile, slots, cus) +
+                           (rest ? tile_time_per_k(tile, rest, cus) : 0.0);
+      double t = per_k * (double)((kp + sp - 1) / sp) * (fp8 ? 0.5 : 1.0) +
+                 (tile == 256 ? 6e-6 : 4.7e-6);
+      if (sp > 1) {
+        const double planes = 4.0 * (double)sp * (double)m * (double)n;
+        t += (2 * planes + (double)(cb * m * n)) / 5.2e12 + 4e-6;
+      }
+      if (sp == 1 && t < best_unsplit_t) {
+        best_unsplit_t = t;
+        best_unsplit = {tile, 1};
+      }
+      if (t < best_t) {
+        best_t = t;
+        best = {tile, sp};
+      }
     }
   }
-  // a split only when the model expects it to save more than 5 %
-  return best_t < 0.95 * t1 ? best : 1;
+  return best.splits > 1 && !(best_t < 0.95 * best_unsplit_t) ? best_unsplit : best;
 }
 
 const char* dtype_name(int t) {
@@ -273,10 +305,16 @@ int sile_hip_kernel_parallel_reduce(void* const* buffers, int64_t num_threadgrou
 // GEMM
 // ---------------------------------------------------------------------------
 
-int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
-                  int64_t k, const void* a, int64_t lda, sile_layout a_layout, const void* b,
-                  int64_t ldb, sile_layout b_layout, void* c, int64_t ldc, float scale_a,
-                  float scale_b, int64_t bk, sile_hip_stream stream) {
+}  // extern "C"
+
+namespace {
+
+// sile_hip_gemm with an optional forced tile size (0: by shape) and K split
+// (0: by shape)
+int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
+              int64_t k, const void* a, int64_t lda, sile_layout a_layout, const void* b,
+              int64_t ldb, sile_layout b_layout, void* c, int64_t ldc, float scale_a,
+              float scale_b, int64_t bk, int tile_req, int splits_req, sile_hip_stream stream) {
   if (m < 0 || n < 0 || k < 0) return fail(SILE_ERR_SHAPE, "negative GEMM extent");
   const int64_t kp = bk > 0 ? (k / bk) * bk : k;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -325,11 +363,20 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   }
   const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
   if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
-  if (m < 256 || n < 256 || n % 4) {
-    // below one 256 x 256 tile (or N not a multiple of 4): the any-shape
-    // kernel, 64 x 64 tiles with fragments loaded straight from the operands
-    if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
-      return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
+  const bool fp8 = kstep == 64;
+  if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
+    return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
+  const int64_t min_tile = tile_req ? tile_req : fp8 ? 256 : 128;
+  const bool lds_ok = m >= min_tile && n >= min_tile && n % 4 == 0 && (ldc * cb) % 16 == 0 &&
+                      aligned16(c) && !(fp8 && min_tile == 128);
+  if (tile_req && !lds_ok)
+    return fail(SILE_ERR_SHAPE,
+                "%d x %d tiles need M, N >= %d, N a multiple of 4, C's rows 16-byte aligned%s",
+                tile_req, tile_req, tile_req, tile_req == 128 ? " and 16-bit operands" : "");
+  if (!lds_ok) {
+    // below one tile of the LDS kernels, N not a multiple of 4 or C's rows
+    // not 16-byte aligned: the any-shape kernel, 64 x 64 tiles with fragments
+    // loaded straight from the operands
     const int64_t gx = (n + 63) / 64, gy = (m + 63) / 64;
     if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "GEMM too large");
     char sname[64];
@@ -342,26 +389,28 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
     int rc = launch(Module::kGemm, sname, dim3((unsigned)gx, (unsigned)gy), dim3(256), sp, s);
     return rc == SILE_OK ? ok() : rc;
   }
-  // any M, N of at least one 256 x 256 tile (N a multiple of 4: 4-element stores);
-  // any K' (the kernel zeroes the elements of its last half k-step past K')
-  if ((lda * eb) % 16 || (ldb * eb) % 16 || (ldc * cb) % 16 || !aligned16(a) || !aligned16(b) ||
-      !aligned16(c))
-    return fail(SILE_ERR_SHAPE, "operands and leading dimensions must be 16-byte aligned");
-  // a 256-row panel of A or B is one buffer resource: 32-bit byte range
+  // the LDS kernels: 256 x 256 or (16-bit operands) 128 x 128 tiles, any
+  // M, N of at least one tile (N a multiple of 4: 4-element stores); any K'
+  // (the kernel zeroes the elements of its last half k-step past K')
+  // a tile's panel of A or B is one buffer resource: 32-bit byte range
   if (256 * std::max(lda, ldb) * (int64_t)eb > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "leading dimension too large for a 256-row panel (%lld, %lld)",
                 (long long)lda, (long long)ldb);
-  const int64_t tiles_m = (m + 255) / 256, tiles_n = (n + 255) / 256;
-  if (tiles_m * tiles_n > 0x7fffffffLL || m > 0x7fffffffLL || n > 0x7fffffffLL)
-    return fail(SILE_ERR_SHAPE, "GEMM too large");
+  if (m > 0x7fffffffLL || n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
   const int64_t half_steps = (kp + kstep - 1) / kstep;
   if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
+  GemmPlan plan = gemm_plan(m, n, kp, half_steps, (int64_t)cb, fp8, tile_req);
+  if (splits_req) plan.splits = splits_req;
+  const int64_t tiles_m = (m + plan.tile - 1) / plan.tile, tiles_n = (n + plan.tile - 1) / plan.tile;
+  if (tiles_m * tiles_n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
   GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
              scale_a * scale_b, (int32_t)m, (int32_t)n, (int32_t)(kp - (half_steps - 1) * kstep),
              (int32_t)half_steps, 0};
-  const unsigned tiles = (unsigned)(g.tiles_m * g.tiles_n);
-  int64_t splits = gemm_splits(tiles, half_steps, kp, m, n, (int64_t)cb, kstep == 64);
-  void* ws = nullptr;
+  const unsigned tiles = (unsigned)(tiles_m * tiles_n);
+  const char* tname = plan.tile == 256 ? "sile_gemm_nt_" : "sile_gemm_nt128_";
+  const char* ab = a_type == SILE_BF16 ? "bf16" : a_type == SILE_F16 ? "f16" : "fp8";
+  char kname[64];
+  int64_t splits = plan.splits;
   if (splits >= 2) {
     // whole k-steps per range; the last range takes what is left of K'
     int64_t per = (half_steps + splits - 1) / splits;
@@ -370,23 +419,23 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
     g.split_steps = (int32_t)per;
   }
   if (splits < 2) {
+    snprintf(kname, sizeof kname, "%s%s", tname, name + strlen("sile_gemm_nt_"));
     void* params[] = {&a, &b, &c, &g};
-    int rc = launch(Module::kGemm, name, dim3(tiles), dim3(256), params, s);
+    int rc = launch(Module::kGemm, kname, dim3(tiles), dim3(256), params, s);
     return rc == SILE_OK ? ok() : rc;
   }
   // k-ranges side by side: fp32 planes of C in the device scratch, then their
   // sum in k-range order, scaled and converted
+  void* ws = nullptr;
   int rc = scratch_acquire((size_t)(splits * m * n) * sizeof(float), s, &ws);
   if (rc != SILE_OK) return rc;
-  char pname[64];
-  snprintf(pname, sizeof pname, "sile_gemm_nt_%s_f32",
-           a_type == SILE_BF16 ? "bf16" : a_type == SILE_F16 ? "f16" : "fp8");
+  snprintf(kname, sizeof kname, "%s%s_f32", tname, ab);
   const float alpha = g.alpha;
   g.alpha = 1.0f;
   g.ldc = n;
   g.c_split = m * n;
   void* params[] = {&a, &b, &ws, &g};
-  rc = launch(Module::kGemm, pname, dim3(tiles, (unsigned)splits), dim3(256), params, s);
+  rc = launch(Module::kGemm, kname, dim3(tiles, (unsigned)splits), dim3(256), params, s);
   if (rc == SILE_OK) {
     const char* rname = c_type == SILE_BF16  ? "sile_gemm_splitk_reduce_bf16"
                         : c_type == SILE_F16 ? "sile_gemm_splitk_reduce_f16"
@@ -401,6 +450,31 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
   }
   scratch_release(s);
   return rc == SILE_OK ? ok() : rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m, int64_t n,
+                  int64_t k, const void* a, int64_t lda, sile_layout a_layout, const void* b,
+                  int64_t ldb, sile_layout b_layout, void* c, int64_t ldc, float scale_a,
+                  float scale_b, int64_t bk, sile_hip_stream stream) {
+  return gemm_impl(a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout, c, ldc,
+                   scale_a, scale_b, bk, 0, 0, stream);
+}
+
+int sile_hip_gemm_tiled(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m,
+                        int64_t n, int64_t k, const void* a, int64_t lda, sile_layout a_layout,
+                        const void* b, int64_t ldb, sile_layout b_layout, void* c, int64_t ldc,
+                        float scale_a, float scale_b, int64_t bk, int32_t tile, int32_t splits,
+                        sile_hip_stream stream) {
+  if (tile != 0 && tile != 128 && tile != 256)
+    return fail(SILE_ERR_SHAPE, "tile must be 0 (by shape), 128 or 256 (got %d)", tile);
+  if (splits < 0 || splits > 64)
+    return fail(SILE_ERR_SHAPE, "splits must be 0 (by shape) or 1 .. 64 (got %d)", splits);
+  return gemm_impl(a_type, b_type, c_type, m, n, k, a, lda, a_layout, b, ldb, b_layout, c, ldc,
+                   scale_a, scale_b, bk, tile, splits, stream);
 }
 
 int sile_hip_mma_f32(int64_t m, int64_t n, int64_t k, const float* a, int64_t lda,

@@ -88,6 +88,23 @@ def test_gemm_rejects_unaligned_and_row_major_b():
     assert rc == 5 and "aligned" in _abi.last_error()
 
 
+@pytest.mark.parametrize("a_t,m,n,tile,splits,needle", [
+    (_abi.BF16, 256, 256, 64, 0, "tile must be"),        # not a tile size
+    (_abi.BF16, 256, 256, 256, 65, "splits must be"),    # too many ranges
+    (_abi.BF16, 256, 256, 0, -1, "splits must be"),
+    (_abi.BF16, 200, 512, 256, 0, "256 x 256 tiles need"),   # M below the forced tile
+    (_abi.F8E4M3, 512, 512, 128, 0, "16-bit operands"),      # no 128 x 128 fp8 kernel
+    (_abi.BF16, 512, 258, 128, 0, "128 x 128 tiles need"),   # N not a multiple of 4
+])
+def test_gemm_tiled_host_validation(a_t, m, n, tile, splits, needle):
+    """A forced tile size or split the shape cannot take is a Shape error,
+    raised before any device work."""
+    c_t = _abi.BF16
+    rc = _abi.status("sile_hip_gemm_tiled", a_t, a_t, c_t, m, n, 64, 16, 64, _abi.ROW_MAJOR,
+                     16, 64, _abi.COL_MAJOR, 16, n, 1.0, 1.0, 0, tile, splits, NULL)
+    assert rc == 5 and needle in _abi.last_error(), _abi.last_error()
+
+
 def test_dsl_kernel_host_validation():
     bufs = (_abi.ctypes.c_void_p * 3)(16, 16, 16)
     # wrong shape count

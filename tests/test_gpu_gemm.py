@@ -25,16 +25,22 @@ def _to_f32(hip, buf, c_type, m, n):
     return bits.view(np.float16).astype(np.float32)
 
 
-def _run(hip, a_t, c_t, a_bits, b_bits, m, n, k, scale_a=1.0, scale_b=1.0, bk=0):
+def _run(hip, a_t, c_t, a_bits, b_bits, m, n, k, scale_a=1.0, scale_b=1.0, bk=0, tile=0,
+         splits=0):
     da = hip.DeviceBuffer.from_array(a_bits)
     db = hip.DeviceBuffer.from_array(b_bits)
     cbytes = 4 if c_t == hip.F32 else 2
     dc = hip.DeviceBuffer(m * n * cbytes)
     dc.fill_bytes(0xFF)  # NaN pattern: any cell the kernel skips is caught
     hip.gemm(a_t, a_t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-             dc.ptr, n, scale_a, scale_b, bk)
+             dc.ptr, n, scale_a, scale_b, bk, tile=tile, splits=splits)
     hip.synchronize()
     return _to_f32(hip, dc, c_t, m, n)
+
+
+# tile sizes of the LDS kernels: 0 lets the shape choose, 256 / 128 force one
+# (sile_hip_gemm_tiled), so every case reaches both kernels
+TILES = [0, 256, 128]
 
 
 SHAPES = [(256, 256, 64), (512, 256, 128), (768, 1024, 320), (2048, 2048, 1024), (256, 512, 32),
@@ -43,14 +49,15 @@ SHAPES = [(256, 256, 64), (512, 256, 128), (768, 1024, 320), (2048, 2048, 1024),
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
 @pytest.mark.parametrize("out", ["bf16", "f32"])
-def test_bf16_gemm(hip, m, n, k, out):
-    say(f"gemm bf16 {m}x{n}x{k} -> {out}")
+@pytest.mark.parametrize("tile", TILES)
+def test_bf16_gemm(hip, m, n, k, out, tile):
+    say(f"gemm bf16 {m}x{n}x{k} -> {out} tile={tile}")
     a = (rng(4).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
     bt = (rng(5).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
     a_bits, a_f = bf16_round(a)
     b_bits, b_f = bf16_round(bt)
     c_t = hip.BF16 if out == "bf16" else hip.F32
-    got = _run(hip, hip.BF16, c_t, a_bits, b_bits, m, n, k)
+    got = _run(hip, hip.BF16, c_t, a_bits, b_bits, m, n, k, tile=tile)
     ref = cpuref.gemm_nt(a_f, b_f)
     if out == "f32":
         assert_close(got, ref, atol=1e-4, rtol=1e-4, what="bf16 gemm f32 out")
@@ -61,13 +68,14 @@ def test_bf16_gemm(hip, m, n, k, out):
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES[:3])
-def test_f16_gemm(hip, m, n, k):
-    say(f"gemm f16 {m}x{n}x{k}")
+@pytest.mark.parametrize("tile", TILES)
+def test_f16_gemm(hip, m, n, k, tile):
+    say(f"gemm f16 {m}x{n}x{k} tile={tile}")
     a = (rng(14).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
     bt = (rng(15).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
     a_bits, a_f = f16_round(a)
     b_bits, b_f = f16_round(bt)
-    got = _run(hip, hip.F16, hip.F16, a_bits, b_bits, m, n, k)
+    got = _run(hip, hip.F16, hip.F16, a_bits, b_bits, m, n, k, tile=tile)
     assert_close(got, cpuref.gemm_nt(a_f, b_f), atol=ATOL, rtol=RTOL, what="f16 gemm")
 
 
@@ -111,17 +119,17 @@ def test_fp8_gemm(hip, m, n, k, out):
     assert_close(got, ref, atol=ATOL, rtol=RTOL, what=f"fp8 gemm {out} out")
 
 
-@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("kind,tile", [("bf16", 256), ("bf16", 128), ("fp8", 0)])
 @pytest.mark.parametrize("k,bk", [(192, 96), (192, 64), (192, 50), (192, 7), (192, 100),
                                   (192, 190), (48, 33), (48, 9)])
-def test_truncated_k_ignores_nonfinite_tail(hip, kind, k, bk):
+def test_truncated_k_ignores_nonfinite_tail(hip, kind, tile, k, bk):
     """K' = (K / bk) * bk stops anywhere inside a k-step (K' = 192, 150, 189,
     100, 190, 33, 45: inside the first or the second half k-step, or at its
     end): the columns past K' (here NaN and Inf) reach LDS with the last
     k-step and must be masked out of the result."""
     m, n = 256, 512
     kp = (k // bk) * bk
-    say(f"gemm {kind} K={k} bk={bk} (K'={kp}) with a non-finite tail")
+    say(f"gemm {kind} K={k} bk={bk} (K'={kp}) with a non-finite tail, tile={tile}")
     a = rng(11).normal(size=(m, k)).astype(np.float32)
     bt = rng(12).normal(size=(n, k)).astype(np.float32)
     if kind == "bf16":
@@ -131,7 +139,7 @@ def test_truncated_k_ignores_nonfinite_tail(hip, kind, k, bk):
         b_bits, b_f = bf16_round(bt)
         a_bits[:, kp:] = 0x7FC0          # NaN
         b_bits[:, kp:] = 0x7F80          # +Inf
-        got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=bk)
+        got = _run(hip, hip.BF16, hip.F32, a_bits, b_bits, m, n, k, bk=bk, tile=tile)
         ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
         assert_close(got, ref, atol=1e-4, rtol=1e-4, what="bf16 truncated K")
     else:
@@ -183,12 +191,15 @@ def test_padded_leading_dimensions(hip, kind):
     assert (got[:, n:].view(np.uint32) == 0xFFFFFFFF).all()
 
 
-@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
-                                      ("fp8", "bf16")])
+@pytest.mark.parametrize("kind,out,tile", [("bf16", "bf16", 256), ("bf16", "bf16", 128),
+                                           ("bf16", "f32", 256), ("bf16", "f32", 128),
+                                           ("f16", "f16", 256), ("f16", "f16", 128),
+                                           ("fp8", "bf16", 256)])
 @pytest.mark.parametrize("m,n,k", [(300, 260, 256), (257, 1028, 320), (768, 300, 448)])
-def test_ragged_m_n(hip, kind, out, m, n, k):
-    """M and N that are not multiples of the 256 x 256 tile: the last tile row /
-    column is computed from rows / columns M - 256 / N - 256 on.  Every
+def test_ragged_m_n(hip, kind, out, tile, m, n, k):
+    """M and N that are not multiples of the tile (256 or 128, forced): the
+    last tile row / column is computed from rows / columns M - tile / N - tile
+    on.  Every
     element is checked; C sits in a wider pitch whose columns past N must keep
     their fill.  With N % 8 == 4 (all three N here) the last column tile's rows
     start 8 bytes off a 16-byte boundary, so its 16-bit C is written back with
@@ -196,7 +207,7 @@ def test_ragged_m_n(hip, kind, out, m, n, k):
     if kind == "fp8" and k % 64:
         pytest.skip("fp8 K' is a multiple of 64")
     ldc = n + 12
-    say(f"gemm {kind} ragged {m}x{n}x{k} -> {out}")
+    say(f"gemm {kind} ragged {m}x{n}x{k} -> {out} tile={tile}")
     a = rng(21).normal(size=(m, k)).astype(np.float32)
     bt = rng(22).normal(size=(n, k)).astype(np.float32)
     if kind == "fp8":
@@ -216,7 +227,7 @@ def test_ragged_m_n(hip, kind, out, m, n, k):
     dc = hip.DeviceBuffer(m * ldc * cb)
     dc.fill_bytes(0xFF)
     hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-             dc.ptr, ldc, sa, sb)
+             dc.ptr, ldc, sa, sb, tile=tile)
     hip.synchronize()
     got = _to_f32(hip, dc, c_t, m, ldc)
     ref = cpuref.gemm_nt(a_f, b_f)
@@ -274,9 +285,10 @@ def test_bf16_gemm_config3_sampled(hip, size):
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (100, 256, 64), (16, 300, 130), (255, 255, 255),
                                    (300, 100, 64), (2, 1000, 37), (257, 258, 96), (64, 64, 64)])
 def test_small_shapes_mfma(hip, kind, out, m, n, k):
-    """Shapes below one 256 x 256 tile, or N not a multiple of 4, run the
-    any-shape MFMA kernel: every element against the oracle, C in a wider
-    pitch whose columns past N keep their fill."""
+    """Shapes below one LDS tile, N not a multiple of 4, or (here, always)
+    C's rows not 16-byte aligned run the any-shape MFMA kernel: every element
+    against the oracle, C in a wider pitch whose columns past N keep their
+    fill."""
     ldc = n + 3
     say(f"gemm small {kind} {m}x{n}x{k} -> {out}")
     a = rng(41).normal(size=(m, k)).astype(np.float32)
@@ -358,19 +370,22 @@ def test_small_shapes_truncated_k(hip, kind, k, bk):
     assert np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("f16", "f16"), ("fp8", "bf16"),
-                                      ("bf16", "f32")])
+@pytest.mark.parametrize("kind,out,tile", [("bf16", "bf16", 256), ("bf16", "bf16", 128),
+                                           ("f16", "f16", 256), ("f16", "f16", 128),
+                                           ("fp8", "bf16", 256), ("bf16", "f32", 256),
+                                           ("bf16", "f32", 128)])
 @pytest.mark.parametrize("k,bk", [(192, 50), (192, 100), (320, 70)])
-def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, k, bk):
-    """The any-K' masking of the 256 x 256 kernel on a ragged shape (300 x 260:
-    the last tile row and column moved back) with lda = ldb = K + 64: the
+def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, tile, k, bk):
+    """The any-K' masking of the LDS kernels (256 and 128 tiles, forced) on a
+    ragged shape (300 x 260: the last tile row and column moved back) with
+    lda = ldb = K + 64: the
     elements past K' inside each row (up to K, then the row padding) are
     NaN / Inf and must be masked, for 16-bit and fp8 -> bf16 outputs too."""
     m, n = 300, 260
     kp = (k // bk) * bk
     ea = 1 if kind == "fp8" else 2
     ld = k + 64
-    say(f"gemm {kind} {m}x{n} K={k} bk={bk} (K'={kp}) lda=ldb={ld} -> {out}")
+    say(f"gemm {kind} {m}x{n} K={k} bk={bk} (K'={kp}) lda=ldb={ld} -> {out} tile={tile}")
     a = rng(45).normal(size=(m, k)).astype(np.float32)
     bt = rng(46).normal(size=(n, k)).astype(np.float32)
     if kind == "fp8":
@@ -398,7 +413,7 @@ def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, k, bk):
     dc = hip.DeviceBuffer(m * ldc * cb)
     dc.fill_bytes(0xFF)
     hip.gemm(t, t, c_t, m, n, k, da.ptr, ld, hip.ROW_MAJOR, db.ptr, ld, hip.COL_MAJOR, dc.ptr,
-             ldc, sa, sb, bk)
+             ldc, sa, sb, bk, tile=tile)
     hip.synchronize()
     got = _to_f32(hip, dc, c_t, m, ldc)
     ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
@@ -407,22 +422,27 @@ def test_truncated_k_ragged_tiles_padded_rows(hip, kind, out, k, bk):
     assert np.isfinite(got[:, :n]).all()
 
 
-@pytest.mark.parametrize("kind,out,m,n,k,bk", [
-    ("bf16", "bf16", 256, 256, 8192, 0),    # 1 tile: 16 k-ranges of 512
-    ("bf16", "f32", 300, 260, 5000, 0),     # 4 tiles, ragged; the last range ends in a half k-step
-    ("f16", "f16", 512, 512, 6000, 70),     # K' = 5950 ends 30 elements into a half k-step
-    ("fp8", "bf16", 512, 256, 4096, 0),     # scales applied once, after the ranges are summed
-    ("fp8", "f32", 256, 300, 3072, 0),
+@pytest.mark.parametrize("kind,out,m,n,k,bk,tile,splits", [
+    ("bf16", "bf16", 256, 256, 8192, 0, 256, 16),   # 1 tile: 16 k-ranges of 512
+    ("bf16", "f32", 300, 260, 5000, 0, 256, 9),     # the last range ends in a half k-step
+    ("bf16", "bf16", 300, 260, 5000, 0, 128, 5),
+    ("f16", "f16", 512, 512, 6000, 70, 128, 3),     # K' = 5950 ends 30 elements into a half k-step
+    ("bf16", "bf16", 256, 256, 8192, 0, 0, 0),      # chosen by shape
+    ("bf16", "f32", 300, 260, 5000, 0, 0, 0),
+    ("f16", "f16", 512, 512, 6000, 70, 0, 0),
+    ("fp8", "bf16", 512, 256, 4096, 0, 0, 0),       # scales applied once, after the ranges are summed
+    ("fp8", "f32", 256, 300, 3072, 0, 256, 3),
 ])
-def test_split_k(hip, kind, out, m, n, k, bk):
-    """Few 256 x 256 tiles and a long K': the GEMM splits K' into ranges that
-    run side by side (fp32 planes of C in stream-ordered scratch) and sums
-    them in range order; on a 256-CU device every case here splits.  Every
-    element is checked, C sits in a wider pitch whose columns past N keep
-    their fill, and a second call gives the same bits."""
+def test_split_k(hip, kind, out, m, n, k, bk, tile, splits):
+    """Few tiles and a long K': K' split into ranges that run side by side
+    (fp32 planes of C in the device scratch), summed in range order; the
+    split forced on either tile size, or chosen by shape (on a 256-CU device
+    every such case here splits).  Every element is checked, C sits in a
+    wider pitch whose columns past N keep their fill, and a second call gives
+    the same bits."""
     kp = (k // bk) * bk if bk else k
-    ldc = n + 8
-    say(f"gemm split-K {kind} {m}x{n}x{k} bk={bk} -> {out}")
+    ldc = -(-(n + 8) // 8) * 8   # 16-byte rows for every C type
+    say(f"gemm split-K {kind} {m}x{n}x{k} bk={bk} -> {out} tile={tile} splits={splits}")
     a = rng(31).normal(size=(m, k)).astype(np.float32)
     bt = rng(32).normal(size=(n, k)).astype(np.float32)
     if kind == "fp8":
@@ -444,7 +464,7 @@ def test_split_k(hip, kind, out, m, n, k, bk):
     for _ in range(2):
         dc.fill_bytes(0xFF)
         hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-                 dc.ptr, ldc, sa, sb, bk)
+                 dc.ptr, ldc, sa, sb, bk, tile=tile, splits=splits)
         hip.synchronize()
         raws.append(dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc)))
     assert (raws[0] == raws[1]).all(), "split-K result differs between two calls"
@@ -453,3 +473,38 @@ def test_split_k(hip, kind, out, m, n, k, bk):
     tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
     assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} split-K")
     assert (raws[0][:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
+
+
+@pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
+                                      ("f16", "f32")])
+@pytest.mark.parametrize("m,n,k,bk", [(128, 128, 64, 0), (200, 300, 320, 0), (130, 1028, 448, 0),
+                                      (255, 260, 192, 50), (128, 256, 8192, 0),
+                                      (192, 1024, 2048, 0)])
+def test_tile128(hip, kind, out, m, n, k, bk):
+    """M or N in [128, 256) with 16-bit operands: 128 x 128 tiles through LDS
+    (the last tile row / column moved back to end at M / N, C in a wider
+    pitch; N % 8 == 4 puts the last column tile's rows 8 bytes off a 16-byte
+    boundary), K' truncated inside a half k-step (255 x 260 x 192, bk = 50),
+    and K' long enough to be split (128 x 256 x 8192)."""
+    kp = (k // bk) * bk if bk else k
+    ldc = n + 8
+    say(f"gemm tile128 {kind} {m}x{n}x{k} bk={bk} -> {out}")
+    a = (rng(41).normal(size=(m, k)) / np.sqrt(kp)).astype(np.float32)
+    bt = (rng(42).normal(size=(n, k)) / np.sqrt(kp)).astype(np.float32)
+    rnd = bf16_round if kind == "bf16" else f16_round
+    (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+    t = hip.BF16 if kind == "bf16" else hip.F16
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    dc.fill_bytes(0xFF)
+    hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+             dc.ptr, ldc, 1.0, 1.0, bk)
+    hip.synchronize()
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+    tol = (1e-4, 1e-4) if out == "f32" else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} tile128")
+    raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc))
+    assert (raw[:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
