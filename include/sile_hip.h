@@ -237,10 +237,11 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
  *                        A row-major, B column-major, any M, N, K', A and B
  *                        (and their leading dimensions) 16-byte aligned; MFMA
- *                        path (M, N >= 256, or >= 128 with 16-bit operands,
- *                        N a multiple of 4 and C's rows 16-byte aligned:
- *                        256 x 256 or 128 x 128 tiles through LDS, the size
- *                        chosen by shape; other shapes: 64 x 64 tiles).
+ *                        path (N a multiple of 4, C's rows 16-byte aligned
+ *                        and M, N >= 256, or, with 16-bit operands, N >= 128
+ *                        and any M: 256 x 256 or 128 x 128 tiles through LDS,
+ *                        the size chosen by shape; other shapes: 64 x 64
+ *                        tiles).
  * When the tiles are fewer than the device's CUs and K' is long, K' may be
  * split into ranges computed side by side: their fp32 partial C planes go
  * to a device scratch buffer shared by all calls on the device (allocated on
@@ -260,8 +261,9 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
 /* sile_hip_gemm with the tile size and the K split chosen by the caller
  * instead of by shape.  No counterpart in the reference; for tests that must
  * reach each kernel and for tuning.  tile: 0 (by shape), 256, or 128 (16-bit
- * operands only); a forced size the shape cannot take (M or N below it, N not
- * a multiple of 4, C's rows not 16-byte aligned) -> SILE_ERR_SHAPE.  splits:
+ * operands only); a forced size the shape cannot take (N below it, M below
+ * 256 for 256, N not a multiple of 4, C's rows not 16-byte aligned) ->
+ * SILE_ERR_SHAPE.  splits:
  * 0 (by shape) or 1 .. 64 ranges of K' (fewer when K' has fewer whole
  * k-steps); a split needs splits * M * N * 4 bytes of the device scratch. */
 int sile_hip_gemm_tiled(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m,

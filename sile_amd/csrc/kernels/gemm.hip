@@ -41,7 +41,8 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;  // in elements
   int32_t tiles_m, tiles_n, k_steps;
   float alpha;
-  int32_t m, n;           // C extents (>= 256): the last tile row / column starts at m - 256 / n - 256
+  int32_t m, n;           // C extents (>= the tile edge kT, except m for kT = 128): the last tile
+                          // row / column starts at m - kT / n - kT
   int32_t k_rem;          // elements of the last half k-step inside K' (1 .. a half k-step)
   int32_t split_steps;    // half k-steps per k-range (even, or k_steps when K is not split)
   int64_t c_split;        // elements between the C planes of consecutive k-ranges
@@ -125,13 +126,16 @@ SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& 
   // at M / N, so every load stays inside the operands; the rows or columns it
   // shares with its neighbour are computed in the same order by both
   // workgroups and written with the same values.
-  p.row0 = min(tile_m * kT, g.m - kT);
+  // 128 x 128 tiles also take M below one tile: the tile starts at row 0 and
+  // the rows past M load as zeros (outside A's buffer resource)
+  p.row0 = kT == 256 || g.m >= kT ? min(tile_m * kT, g.m - kT) : 0;
+  const int a_rows = kT == 256 ? kT : min(kT, g.m);
   p.col0 = min(tile_n * kT, g.n - kT);
   p.a_rs = (int)(g.lda * kEB);
   p.b_rs = (int)(g.ldb * kEB);
   // (a k-range that starts byte0 bytes into the rows moves the base, not the end)
   p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs + byte0), (short)0,
-                                               (int)(kT * p.a_rs - byte0), 0x00020000);
+                                               (int)(a_rows * p.a_rs - byte0), 0x00020000);
   p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs + byte0), (short)0,
                                                (int)(kT * p.b_rs - byte0), 0x00020000);
   // wave w's load instruction i (0..7) of an operand fills rows
@@ -169,9 +173,11 @@ SILE_DEV void mma16x16(const u32x4& a, const u32x4& b, f32x4& c) {
 template <int kW> constexpr int kCRowB = 2 * kW + 16;
 template <int kW> constexpr int kCStageB = kW * kCRowB<kW>;   // one wave's staged C (34 KiB at kW = 128)
 
-template <int kOut, int kW, typename Fill>
+// kGuardRows: only the first `rows` rows of the wave's tile are stored (C
+// ends inside the tile).
+template <int kOut, int kW, bool kGuardRows, typename Fill>
 SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, uint8_t* cst,
-                                Fill fill) {
+                                int rows, Fill fill) {
   static_assert(kOut != kOutF32, "16-bit C");
   constexpr int kRowBytes = kCRowB<kW>;
   fill([&](int row, int col, f32x4 v) {
@@ -189,6 +195,7 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 #pragma unroll 8
     for (int t = 0; t < kW / kRowsPerStore; ++t) {
       const int row = kRowsPerStore * t + lg;
+      if (kGuardRows && row >= rows) continue;
       __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(cst + row * kRowBytes + lr * 16),
                                   reinterpret_cast<u32x4*>(cbase + row * ldc + lr * 8));
     }
@@ -198,6 +205,7 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 #pragma unroll 8
     for (int t = 0; t < kW / kRowsPerStore; ++t) {
       const int row = kRowsPerStore * t + lg;
+      if (kGuardRows && row >= rows) continue;
       __builtin_nontemporal_store(*reinterpret_cast<const u32x2*>(cst + row * kRowBytes + lr * 8),
                                   reinterpret_cast<u32x2*>(cbase + row * ldc + lr * 4));
     }
@@ -480,13 +488,18 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
       }
   };
   const int64_t m0 = p.row0 + wm * kW, n0 = p.col0 + wn * kW;
+  constexpr bool kGuardRows = kT == 128;   // M may end inside the tile
+  const int rows = kGuardRows ? (int)min<int64_t>(kW, (int64_t)g.m - m0) : kW;
   if constexpr (kOut != kOutF32) {
     __syncthreads();   // every wave is done reading the ring
-    stage_and_store_c<kOut, kW>(C, g.ldc, m0, n0, smem + wave * kCStageB<kW>, each_c4);
+    stage_and_store_c<kOut, kW, kGuardRows>(C, g.ldc, m0, n0, smem + wave * kCStageB<kW>, rows,
+                                            each_c4);
   } else {
     // fp32 C: the plane of this workgroup's k-range (plane 0 when K is not split)
     float* cz = static_cast<float*>(C) + (int64_t)blockIdx.y * g.c_split;
-    each_c4([&](int row, int col, f32x4 v) { store_c4<kOut>(cz, (m0 + row) * g.ldc + n0 + col, v); });
+    each_c4([&](int row, int col, f32x4 v) {
+      if (!kGuardRows || row < rows) store_c4<kOut>(cz, (m0 + row) * g.ldc + n0 + col, v);
+    });
   }
 }
 

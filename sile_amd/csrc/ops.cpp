@@ -88,7 +88,7 @@ GemmPlan gemm_plan(int64_t m, int64_t n, int64_t kp, int64_t half_steps, int64_t
   GemmPlan best_unsplit = best;
   for (int tile : {256, 128}) {
     if (tile == 128 && fp8) continue;
-    if (m < tile || n < tile || (only_tile && tile != only_tile)) continue;
+    if ((tile == 256 && m < tile) || n < tile || (only_tile && tile != only_tile)) continue;
     const int64_t tiles = ((m + tile - 1) / tile) * ((n + tile - 1) / tile);
     const int64_t slots = (int64_t)cus * (tile == 256 ? 1 : 2);
     const int64_t max_splits = std::min<int64_t>(slots / tiles, half_steps / 16);
@@ -366,17 +366,20 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   const bool fp8 = kstep == 64;
   if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
     return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
+  // the LDS kernels need N >= the tile edge (256, or 128 with 16-bit
+  // operands) and M >= 256 for 256 x 256 tiles (128 x 128 tiles take any M)
   const int64_t min_tile = tile_req ? tile_req : fp8 ? 256 : 128;
-  const bool lds_ok = m >= min_tile && n >= min_tile && n % 4 == 0 && (ldc * cb) % 16 == 0 &&
-                      aligned16(c) && !(fp8 && min_tile == 128);
+  const bool lds_ok = (min_tile == 128 || m >= min_tile) && n >= min_tile && n % 4 == 0 &&
+                      (ldc * cb) % 16 == 0 && aligned16(c) && !(fp8 && min_tile == 128);
   if (tile_req && !lds_ok)
     return fail(SILE_ERR_SHAPE,
-                "%d x %d tiles need M, N >= %d, N a multiple of 4, C's rows 16-byte aligned%s",
-                tile_req, tile_req, tile_req, tile_req == 128 ? " and 16-bit operands" : "");
+                "%d x %d tiles need %sN >= %d, N a multiple of 4, C's rows 16-byte aligned%s",
+                tile_req, tile_req, tile_req == 256 ? "M, " : "", tile_req,
+                tile_req == 128 ? " and 16-bit operands" : "");
   if (!lds_ok) {
-    // below one tile of the LDS kernels, N not a multiple of 4 or C's rows
-    // not 16-byte aligned: the any-shape kernel, 64 x 64 tiles with fragments
-    // loaded straight from the operands
+    // N below one tile of the LDS kernels (M too for fp8), N not a multiple
+    // of 4 or C's rows not 16-byte aligned: the any-shape kernel, 64 x 64
+    // tiles with fragments loaded straight from the operands
     const int64_t gx = (n + 63) / 64, gy = (m + 63) / 64;
     if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "GEMM too large");
     char sname[64];

@@ -477,18 +477,23 @@ def test_split_k(hip, kind, out, m, n, k, bk, tile, splits):
 
 @pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
                                       ("f16", "f32")])
-@pytest.mark.parametrize("m,n,k,bk", [(128, 128, 64, 0), (200, 300, 320, 0), (130, 1028, 448, 0),
-                                      (255, 260, 192, 50), (128, 256, 8192, 0),
-                                      (192, 1024, 2048, 0)])
-def test_tile128(hip, kind, out, m, n, k, bk):
+@pytest.mark.parametrize("m,n,k,bk,tile", [(128, 128, 64, 0, 0), (200, 300, 320, 0, 0),
+                                           (130, 1028, 448, 0, 0), (255, 260, 192, 50, 0),
+                                           (128, 256, 8192, 0, 0), (192, 1024, 2048, 0, 0),
+                                           (1, 128, 64, 0, 128), (64, 512, 256, 0, 128),
+                                           (100, 300, 320, 0, 128), (16, 1024, 4096, 0, 128),
+                                           (127, 260, 192, 50, 128)])
+def test_tile128(hip, kind, out, m, n, k, bk, tile):
     """M or N in [128, 256) with 16-bit operands: 128 x 128 tiles through LDS
     (the last tile row / column moved back to end at M / N, C in a wider
     pitch; N % 8 == 4 puts the last column tile's rows 8 bytes off a 16-byte
     boundary), K' truncated inside a half k-step (255 x 260 x 192, bk = 50),
-    and K' long enough to be split (128 x 256 x 8192)."""
+    and K' long enough to be split (128 x 256 x 8192).  M below one tile:
+    the rows past M load as zeros and are not stored (a row of C past M keeps
+    its fill)."""
     kp = (k // bk) * bk if bk else k
-    ldc = n + 8
-    say(f"gemm tile128 {kind} {m}x{n}x{k} bk={bk} -> {out}")
+    ldc = -(-(n + 8) // 8) * 8   # 16-byte rows for every C type
+    say(f"gemm tile128 {kind} {m}x{n}x{k} bk={bk} -> {out} tile={tile}")
     a = (rng(41).normal(size=(m, k)) / np.sqrt(kp)).astype(np.float32)
     bt = (rng(42).normal(size=(n, k)) / np.sqrt(kp)).astype(np.float32)
     rnd = bf16_round if kind == "bf16" else f16_round
@@ -497,14 +502,16 @@ def test_tile128(hip, kind, out, m, n, k, bk):
     c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
     cb = 4 if out == "f32" else 2
     da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
-    dc = hip.DeviceBuffer(m * ldc * cb)
+    # one spare row past M: the forced 128 x 128 tile must not write it
+    dc = hip.DeviceBuffer((m + 1) * ldc * cb)
     dc.fill_bytes(0xFF)
     hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-             dc.ptr, ldc, 1.0, 1.0, bk)
+             dc.ptr, ldc, 1.0, 1.0, bk, tile=tile)
     hip.synchronize()
     got = _to_f32(hip, dc, c_t, m, ldc)
     ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
     tol = (1e-4, 1e-4) if out == "f32" else (ATOL, RTOL)
     assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} tile128")
-    raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc))
-    assert (raw[:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
+    raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m + 1, ldc))
+    fill = 0xFFFFFFFF if cb == 4 else 0xFFFF
+    assert (raw[:m, n:] == fill).all() and (raw[m] == fill).all()
