@@ -240,15 +240,19 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *                        path (N a multiple of 4, C's rows 16-byte aligned
  *                        and M, N >= 256, or, with 16-bit operands, N >= 128
  *                        and any M: 256 x 256 or 128 x 128 tiles through LDS,
- *                        the size chosen by shape; other shapes: 64 x 64
- *                        tiles).
+ *                        the size chosen by shape; when C cannot take the
+ *                        tiles' stores but M is a multiple of 4 and at least
+ *                        one tile, the same kernels compute C^T into fp32
+ *                        scratch and a second kernel writes C; other shapes:
+ *                        64 x 64 tiles).
  * When the tiles are fewer than the device's CUs and K' is long, K' may be
  * split into ranges computed side by side: their fp32 partial C planes go
  * to a device scratch buffer shared by all calls on the device (allocated on
  * the first such call, grown when a call needs more, at most
  * 4 * (CUs * 65536) bytes; calls on different streams are ordered on the GPU
  * by an event) and a second kernel adds them in range order.  The result
- * does not depend on the stream or on earlier calls.
+ * does not depend on the stream or on earlier calls.  The transposed form
+ * (above) keeps all of C^T there, up to 256 MiB (larger: 64 x 64 tiles).
  * M = 0 or N = 0: nothing is written.  K' = 0 (K below one bk): C = +0.0 for
  * any M, N and supported types, as the canonical matmul's sums start at 0.0f
  * and add no term (canonical_matmul.rs:58-73).

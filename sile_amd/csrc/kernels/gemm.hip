@@ -561,6 +561,60 @@ SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_bf16, kOutBF16)
 SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_f16, kOutF16)
 SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_f32, kOutF32)
 
+// The same sum for the transposed form: the ring kernel ran C^T = B . A^T
+// (A and B swapped), so plane z holds C^T as n rows of `pitch` fp32 (pitch a
+// multiple of 4, at least m).  C[i][j] = alpha * sum_z plane_z[j][i], in plane
+// order.  A workgroup moves one 64 x 64 block through LDS: 16-byte reads
+// along i, element stores along j (C may have any pitch and alignment).
+template <int kOut>
+__device__ __forceinline__ void splitk_reduce_t_body(const float* __restrict__ ws,
+                                                     void* __restrict__ C, int64_t ldc, int64_t m,
+                                                     int64_t n, int64_t plane, int64_t pitch,
+                                                     int splits, float alpha) {
+  __shared__ float blk[64][65];
+  const int tid = threadIdx.x;
+  const int64_t i0 = (int64_t)blockIdx.x * 64, j0 = (int64_t)blockIdx.y * 64;
+  const int iq = 4 * (tid & 15);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int jj = (tid >> 4) + 16 * p;
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (j0 + jj < n && i0 + iq < m) {
+      const float* src = ws + (j0 + jj) * pitch + i0 + iq;
+      v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src));
+      for (int z = 1; z < splits; ++z)
+        v += __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + z * plane));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) blk[jj][iq + e] = v[e];
+  }
+  __syncthreads();
+  const int jj = tid & 63;
+#pragma unroll 4
+  for (int q = 0; q < 16; ++q) {
+    const int ii = (tid >> 6) + 4 * q;
+    const int64_t i = i0 + ii, j = j0 + jj;
+    if (i >= m || j >= n) continue;
+    const float x = alpha != 1.0f ? blk[jj][ii] * alpha : blk[jj][ii];
+    if constexpr (kOut == kOutF32)
+      static_cast<float*>(C)[i * ldc + j] = x;
+    else if constexpr (kOut == kOutBF16)
+      static_cast<uint16_t*>(C)[i * ldc + j] = bf16_rne(x);
+    else
+      static_cast<uint16_t*>(C)[i * ldc + j] = f16_rne(x);
+  }
+}
+
+#define SILE_GEMM_SPLITK_REDUCE_T(NAME, OUT)                                                  \
+  extern "C" __global__ __launch_bounds__(256) void NAME(                                     \
+      const float* ws, void* C, int64_t ldc, int64_t m, int64_t n, int64_t plane,             \
+      int64_t pitch, int splits, float alpha) {                                               \
+    splitk_reduce_t_body<OUT>(ws, C, ldc, m, n, plane, pitch, splits, alpha);                 \
+  }
+SILE_GEMM_SPLITK_REDUCE_T(sile_gemm_splitk_reduce_t_bf16, kOutBF16)
+SILE_GEMM_SPLITK_REDUCE_T(sile_gemm_splitk_reduce_t_f16, kOutF16)
+SILE_GEMM_SPLITK_REDUCE_T(sile_gemm_splitk_reduce_t_f32, kOutF32)
+
 // ---------------------------------------------------------------------------
 // Any shape: M or N below one 256 x 256 tile, or N not a multiple of 4.
 //

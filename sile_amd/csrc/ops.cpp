@@ -59,6 +59,10 @@ struct GemmArgs {
 //   they finish, the second launch reading them and writing C (both at
 //   5.2 TB/s), and 4 us of launch and ordering; it is taken only for a
 //   modelled gain above 5 %.
+// Largest fp32 planes the transposed GEMM form keeps in the device scratch
+// (the split form stays below 4 * CUs * 65536 bytes by construction).
+constexpr int64_t kScratchPlanesMax = 256ll << 20;
+
 struct GemmPlan {
   int tile;        // 256 or 128
   int64_t splits;  // k-ranges (1: K' not split)
@@ -376,10 +380,18 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
                 "%d x %d tiles need %sN >= %d, N a multiple of 4, C's rows 16-byte aligned%s",
                 tile_req, tile_req, tile_req == 256 ? "M, " : "", tile_req,
                 tile_req == 128 ? " and 16-bit operands" : "");
-  if (!lds_ok) {
-    // N below one tile of the LDS kernels (M too for fp8), N not a multiple
-    // of 4 or C's rows not 16-byte aligned: the any-shape kernel, 64 x 64
-    // tiles with fragments loaded straight from the operands
+  // The transposed form runs C^T = B . A^T (A and B swapped) into fp32
+  // planes of C^T and writes them back transposed, for the shapes the direct
+  // form cannot take (N below one tile, N not a multiple of 4, C's rows not
+  // 16-byte aligned) whose M can be the column extent: a multiple of 4 and
+  // at least one tile.
+  // Its fp32 planes (all of C^T) are kept to kScratchPlanesMax bytes.
+  const bool transposed = !lds_ok && m % 4 == 0 &&
+                          (fp8 ? (m >= 256 && n >= 256) : m >= 128) &&
+                          m * n * 4 <= kScratchPlanesMax;
+  if (!lds_ok && !transposed) {
+    // the any-shape kernel, 64 x 64 tiles with fragments loaded straight
+    // from the operands
     const int64_t gx = (n + 63) / 64, gy = (m + 63) / 64;
     if (gx > 0x7fffffffLL || gy > 65535) return fail(SILE_ERR_SHAPE, "GEMM too large");
     char sname[64];
@@ -392,9 +404,13 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
     int rc = launch(Module::kGemm, sname, dim3((unsigned)gx, (unsigned)gy), dim3(256), sp, s);
     return rc == SILE_OK ? ok() : rc;
   }
-  // the LDS kernels: 256 x 256 or (16-bit operands) 128 x 128 tiles, any
-  // M, N of at least one tile (N a multiple of 4: 4-element stores); any K'
-  // (the kernel zeroes the elements of its last half k-step past K')
+  // the LDS kernels: 256 x 256 or (16-bit operands) 128 x 128 tiles over the
+  // form that runs, (ra: [rm, K], rb: [rn, K]) -> [rm, rn]; any K' (the kernel
+  // zeroes the elements of its last half k-step past K')
+  const void* ra = transposed ? b : a;
+  const void* rb = transposed ? a : b;
+  const int64_t rlda = transposed ? ldb : lda, rldb = transposed ? lda : ldb;
+  const int64_t rm = transposed ? n : m, rn = transposed ? m : n;
   // a tile's panel of A or B is one buffer resource: 32-bit byte range
   if (256 * std::max(lda, ldb) * (int64_t)eb > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "leading dimension too large for a 256-row panel (%lld, %lld)",
@@ -402,13 +418,15 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (m > 0x7fffffffLL || n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
   const int64_t half_steps = (kp + kstep - 1) / kstep;
   if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
-  GemmPlan plan = gemm_plan(m, n, kp, half_steps, (int64_t)cb, fp8, tile_req);
+  GemmPlan plan = gemm_plan(rm, rn, kp, half_steps, (int64_t)cb, fp8, tile_req);
   if (splits_req) plan.splits = splits_req;
-  const int64_t tiles_m = (m + plan.tile - 1) / plan.tile, tiles_n = (n + plan.tile - 1) / plan.tile;
+  if (transposed) plan.splits = std::max<int64_t>(1, std::min(plan.splits, kScratchPlanesMax / (rm * rn * 4)));
+  const int64_t tiles_m = (rm + plan.tile - 1) / plan.tile;
+  const int64_t tiles_n = (rn + plan.tile - 1) / plan.tile;
   if (tiles_m * tiles_n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
-  GemmArgs g{lda, ldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
-             scale_a * scale_b, (int32_t)m, (int32_t)n, (int32_t)(kp - (half_steps - 1) * kstep),
-             (int32_t)half_steps, 0};
+  GemmArgs g{rlda, rldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
+             scale_a * scale_b, (int32_t)rm, (int32_t)rn,
+             (int32_t)(kp - (half_steps - 1) * kstep), (int32_t)half_steps, 0};
   const unsigned tiles = (unsigned)(tiles_m * tiles_n);
   const char* tname = plan.tile == 256 ? "sile_gemm_nt_" : "sile_gemm_nt128_";
   const char* ab = a_type == SILE_BF16 ? "bf16" : a_type == SILE_F16 ? "f16" : "fp8";
@@ -421,35 +439,43 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
     splits = (half_steps + per - 1) / per;
     g.split_steps = (int32_t)per;
   }
-  if (splits < 2) {
+  if (splits < 2 && !transposed) {
     snprintf(kname, sizeof kname, "%s%s", tname, name + strlen("sile_gemm_nt_"));
-    void* params[] = {&a, &b, &c, &g};
+    void* params[] = {&ra, &rb, &c, &g};
     int rc = launch(Module::kGemm, kname, dim3(tiles), dim3(256), params, s);
     return rc == SILE_OK ? ok() : rc;
   }
-  // k-ranges side by side: fp32 planes of C in the device scratch, then their
-  // sum in k-range order, scaled and converted
+  // fp32 planes in the device scratch (one per k-range; rows of rn, a
+  // multiple of 4), then their sum in k-range order, scaled, converted and,
+  // for the transposed form, transposed
   void* ws = nullptr;
-  int rc = scratch_acquire((size_t)(splits * m * n) * sizeof(float), s, &ws);
+  int rc = scratch_acquire((size_t)(splits * rm * rn) * sizeof(float), s, &ws);
   if (rc != SILE_OK) return rc;
   snprintf(kname, sizeof kname, "%s%s_f32", tname, ab);
   const float alpha = g.alpha;
   g.alpha = 1.0f;
-  g.ldc = n;
-  g.c_split = m * n;
-  void* params[] = {&a, &b, &ws, &g};
+  g.ldc = rn;
+  g.c_split = rm * rn;
+  void* params[] = {&ra, &rb, &ws, &g};
   rc = launch(Module::kGemm, kname, dim3(tiles, (unsigned)splits), dim3(256), params, s);
   if (rc == SILE_OK) {
-    const char* rname = c_type == SILE_BF16  ? "sile_gemm_splitk_reduce_bf16"
-                        : c_type == SILE_F16 ? "sile_gemm_splitk_reduce_f16"
-                                             : "sile_gemm_splitk_reduce_f32";
-    int64_t plane = m * n, ldc_ = ldc, m_ = m, n_ = n;
+    const char* out = c_type == SILE_BF16 ? "bf16" : c_type == SILE_F16 ? "f16" : "f32";
+    char rname[64];
+    int64_t plane = rm * rn, ldc_ = ldc, m_ = m, n_ = n, pitch = rn;
     int sp = (int)splits;
     float al = alpha;
-    void* rp[] = {&ws, &c, &ldc_, &m_, &n_, &plane, &sp, &al};
-    rc = launch(Module::kGemm, rname,
-                dim3((unsigned)((n / 4 + 255) / 256), (unsigned)std::min<int64_t>(m, 65535)),
-                dim3(256), rp, s);
+    if (transposed) {
+      snprintf(rname, sizeof rname, "sile_gemm_splitk_reduce_t_%s", out);
+      void* rp[] = {&ws, &c, &ldc_, &m_, &n_, &plane, &pitch, &sp, &al};
+      rc = launch(Module::kGemm, rname, dim3((unsigned)((m + 63) / 64), (unsigned)((n + 63) / 64)),
+                  dim3(256), rp, s);
+    } else {
+      snprintf(rname, sizeof rname, "sile_gemm_splitk_reduce_%s", out);
+      void* rp[] = {&ws, &c, &ldc_, &m_, &n_, &plane, &sp, &al};
+      rc = launch(Module::kGemm, rname,
+                  dim3((unsigned)((n / 4 + 255) / 256), (unsigned)std::min<int64_t>(m, 65535)),
+                  dim3(256), rp, s);
+    }
   }
   scratch_release(s);
   return rc == SILE_OK ? ok() : rc;

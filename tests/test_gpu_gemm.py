@@ -286,9 +286,9 @@ def test_bf16_gemm_config3_sampled(hip, size):
                                    (300, 100, 64), (2, 1000, 37), (257, 258, 96), (64, 64, 64)])
 def test_small_shapes_mfma(hip, kind, out, m, n, k):
     """Shapes below one LDS tile, N not a multiple of 4, or (here, always)
-    C's rows not 16-byte aligned run the any-shape MFMA kernel: every element
-    against the oracle, C in a wider pitch whose columns past N keep their
-    fill."""
+    C's rows not 16-byte aligned run the any-shape MFMA kernel (300 x 100,
+    16-bit: the transposed LDS form): every element against the oracle, C in
+    a wider pitch whose columns past N keep their fill."""
     ldc = n + 3
     say(f"gemm small {kind} {m}x{n}x{k} -> {out}")
     a = rng(41).normal(size=(m, k)).astype(np.float32)
@@ -515,3 +515,55 @@ def test_tile128(hip, kind, out, m, n, k, bk, tile):
     raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m + 1, ldc))
     fill = 0xFFFFFFFF if cb == 4 else 0xFFFF
     assert (raw[:m, n:] == fill).all() and (raw[m] == fill).all()
+
+
+@pytest.mark.parametrize("kind,out,m,n,k,ldc_pad,bk", [
+    ("bf16", "bf16", 512, 64, 256, 8, 0),      # N below one tile
+    ("f16", "f16", 1024, 100, 320, 0, 0),
+    ("bf16", "f32", 256, 1, 64, 3, 0),
+    ("bf16", "bf16", 512, 1023, 128, 0, 0),    # N not a multiple of 4
+    ("f16", "f32", 300, 258, 200, 1, 50),      # K' = 200 from bk = 50
+    ("bf16", "bf16", 256, 256, 64, 3, 0),      # C's rows not 16-byte aligned
+    ("bf16", "bf16", 512, 64, 8192, 0, 0),     # and K' split
+    ("fp8", "bf16", 512, 258, 256, 0, 0),      # fp8 needs M, N >= 256
+    ("fp8", "f32", 256, 300, 320, 5, 0),
+])
+def test_transposed_form(hip, kind, out, m, n, k, ldc_pad, bk):
+    """Shapes the direct LDS form cannot take (N below one tile, N not a
+    multiple of 4, C's rows not 16-byte aligned) with M a multiple of 4 and at
+    least one tile run C^T = B . A^T on the LDS kernels into fp32 planes,
+    written back transposed with element stores.  Every element is checked,
+    the pitch past N keeps its fill, and a second call gives the same bits."""
+    kp = (k // bk) * bk if bk else k
+    ldc = n + ldc_pad
+    say(f"gemm transposed {kind} {m}x{n}x{k} ldc={ldc} bk={bk} -> {out}")
+    a = rng(51).normal(size=(m, k)).astype(np.float32)
+    bt = rng(52).normal(size=(n, k)).astype(np.float32)
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
+    c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
+    cb = 4 if out == "f32" else 2
+    da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
+    dc = hip.DeviceBuffer(m * ldc * cb)
+    raws = []
+    for _ in range(2):
+        dc.fill_bytes(0xFF)
+        hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
+                 dc.ptr, ldc, sa, sb, bk)
+        hip.synchronize()
+        raws.append(dc.download(np.uint32 if cb == 4 else np.uint16, (m, ldc)))
+    assert (raws[0] == raws[1]).all(), "transposed form differs between two calls"
+    got = _to_f32(hip, dc, c_t, m, ldc)
+    ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
+    assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} transposed")
+    assert (raws[0][:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
