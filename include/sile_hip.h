@@ -238,8 +238,8 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *                        A row-major, B column-major, any M, N, K', A and B
  *                        (and their leading dimensions) 16-byte aligned; MFMA
  *                        path (N a multiple of 4, C's rows 16-byte aligned
- *                        and M, N >= 256, or, with 16-bit operands, N >= 128
- *                        and any M: 256 x 256 or 128 x 128 tiles through LDS,
+ *                        and N >= 128, any M: 256 x 256 or 128 x 128 tiles
+ *                        through LDS,
  *                        the size chosen by shape; when C cannot take the
  *                        tiles' stores but M is a multiple of 4 and at least
  *                        one tile, the same kernels compute C^T into fp32
@@ -264,10 +264,9 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
 
 /* sile_hip_gemm with the tile size and the K split chosen by the caller
  * instead of by shape.  No counterpart in the reference; for tests that must
- * reach each kernel and for tuning.  tile: 0 (by shape), 256, or 128 (16-bit
- * operands only); a forced size the shape cannot take (N below it, M below
- * 256 for 256, N not a multiple of 4, C's rows not 16-byte aligned) ->
- * SILE_ERR_SHAPE.  splits:
+ * reach each kernel and for tuning.  tile: 0 (by shape), 256 or 128; a
+ * forced size the shape cannot take (N below it, M below 256 for 256, N not
+ * a multiple of 4, C's rows not 16-byte aligned) -> SILE_ERR_SHAPE.  splits:
  * 0 (by shape) or 1 .. 64 ranges of K' (fewer when K' has fewer whole
  * k-steps); a split needs splits * M * N * 4 bytes of the device scratch. */
 int sile_hip_gemm_tiled(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m,

@@ -22,12 +22,16 @@ namespace {
 enum Kind : int { kBF16 = 0, kF16 = 1, kFP8 = 2 };
 enum Out : int { kOutBF16 = 0, kOutF16 = 1, kOutF32 = 2 };
 
-// C is written once and not read back by the kernel: non-temporal stores
-// (streaming; 2-3 % faster for the staged 16-bit C than plain stores).
+// 16-bit C is written once and not read back by the kernel: non-temporal
+// stores (streaming; 2-3 % faster for the staged 16-bit C than plain stores).
+// fp32 C goes straight from the accumulators, 32 or 64 bytes of a row per
+// instruction: plain stores, so that L2 merges a row's pieces into whole
+// lines (non-temporal ones made the fp8 kernel's fp32 C 1.3x and its split-K
+// planes up to 2.7x slower).
 template <int kOut>
 SILE_DEV void store_c4(void* C, int64_t idx, f32x4 v) {
   if constexpr (kOut == kOutF32) {
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx));
+    *reinterpret_cast<f32x4*>(static_cast<float*>(C) + idx) = v;
   } else if constexpr (kOut == kOutBF16) {
     const u32x2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(C) + idx));
@@ -83,7 +87,7 @@ SILE_DEV f32x16 mma32x32_fp8(const u32x4* a, const u32x4* b, f32x16 c) {
 // Tile placement.
 //
 // kT x kT output tile per workgroup of 4 waves (2 x 2, kT/2 x kT/2 per wave),
-// kT = 256 (one workgroup per CU) or 128 (16-bit operands, two per CU).
+// kT = 256 (one workgroup per CU) or 128 (two per CU).
 // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds): one
 // instruction of a wave fills 1 KiB of LDS, lane l writing bytes
 // [16 l, 16 l + 16) of it, so each lane fetches the global chunk that belongs
@@ -218,8 +222,8 @@ SILE_DEV void stage_and_store_c(void* C, int64_t ldc, int64_t m0, int64_t n0, ui
 // A wave's kW x kW (kW = kT / 2) is kNB x kNB blocks of one MFMA (256 fp32
 // accumulators per lane at kW = 128, 64 at kW = 64):
 //   bf16 / f16: kW / 16 square blocks of v_mfma_f32_16x16x32_{bf16,f16};
-//   fp8 e4m3:   4 x 4 blocks of v_mfma_f32_32x32x64_f8f6f4 (kT = 256 only;
-//               unscaled: zero scale operands select the plain instruction).
+//   fp8 e4m3:   kW / 32 square blocks of v_mfma_f32_32x32x64_f8f6f4
+//               (unscaled: zero scale operands select the plain instruction).
 // The MFMA is issued with the B fragment first, so accumulator register r of
 // lane l is C[m = l % 16][n = 4 (l / 16) + r] of a 16 x 16 block and
 // C[m = l % 32][n = 8 (r / 4) + 4 (l / 32) + r % 4] of a 32 x 32 block.  A
@@ -282,9 +286,10 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   constexpr int kNB = kW / kBlk;              // blocks per wave edge
   constexpr int kTB = kT * kRowB;             // one operand tile of one k-step in LDS
   constexpr int kOpLoads = kT / 32;           // load instructions per operand, k-step and wave
-  static_assert(kNB % 4 == 0, "groups are issued in quarters");
+  static_assert(kNB % 2 == 0, "two sub-step halves of fragments per row");
   constexpr int kCh = kIsFP8 ? 2 : 1;         // 16-byte chunks per lane per fragment
-  constexpr int kQ = kNB / 4;                 // MFMAs per quarter group
+  // a group's MFMAs in quarters [kQ_s, kQ_{s+1}) (kNB = 2: quarters of 0 and 1)
+  constexpr int kQ1 = kNB / 4, kQ2 = kNB / 2, kQ3 = 3 * kNB / 4;
   constexpr int kLoadsPerGroup = 2 * kOpLoads / (2 * kNB);
   using Acc = std::conditional_t<kIsFP8, f32x16, f32x4>;
   const int tid = threadIdx.x;
@@ -368,15 +373,15 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
     // sub-step sub into (ra, rb) in two halves
     auto group = [&](const u32x4 (&fa)[kNB][kCh], const u32x4 (&fb)[kNB][kCh], int i,
                      int sub, int q0, int nq, u32x4 (&ra)[kNB][kCh], u32x4 (&rb)[kNB][kCh]) {
-      SILE_FENCE; mma(fa, fb, i, 0, kQ); SILE_FENCE;
+      SILE_FENCE; mma(fa, fb, i, 0, kQ1); SILE_FENCE;
 #pragma unroll
       for (int q = q0; q < q0 + nq / 2; ++q) read(sa, sb, sub, q, ra, rb);
-      SILE_FENCE; mma(fa, fb, i, kQ, 2 * kQ); SILE_FENCE;
+      SILE_FENCE; mma(fa, fb, i, kQ1, kQ2); SILE_FENCE;
 #pragma unroll
       for (int q = q0 + nq / 2; q < q0 + nq; ++q) read(sa, sb, sub, q, ra, rb);
-      SILE_FENCE; mma(fa, fb, i, 2 * kQ, 3 * kQ); SILE_FENCE;
+      SILE_FENCE; mma(fa, fb, i, kQ2, kQ3); SILE_FENCE;
       loads();
-      SILE_FENCE; mma(fa, fb, i, 3 * kQ, kNB); SILE_FENCE;
+      SILE_FENCE; mma(fa, fb, i, kQ3, kNB); SILE_FENCE;
     };
     // phase 0: MFMA Y(ks - 1) rows kNB/2 .. kNB-1 | reads X(ks), 4 fragments a group
 #pragma unroll
@@ -522,12 +527,14 @@ SILE_GEMM_KERNEL(sile_gemm_nt_f16_f16, kF16, kOutF16, 256)
 SILE_GEMM_KERNEL(sile_gemm_nt_f16_f32, kF16, kOutF32, 256)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_bf16, kFP8, kOutBF16, 256)
 SILE_GEMM_KERNEL(sile_gemm_nt_fp8_f32, kFP8, kOutF32, 256)
-// 128 x 128 tiles (16-bit operands): shapes whose 256 x 256 tiles would leave
-// CUs idle, and M or N in [128, 256)
+// 128 x 128 tiles: shapes whose 256 x 256 tiles would leave CUs idle, and M
+// or N below 256
 SILE_GEMM_KERNEL(sile_gemm_nt128_bf16_bf16, kBF16, kOutBF16, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_bf16_f32, kBF16, kOutF32, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f16, kF16, kOutF16, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f32, kF16, kOutF32, 128)
+SILE_GEMM_KERNEL(sile_gemm_nt128_fp8_bf16, kFP8, kOutBF16, 128)
+SILE_GEMM_KERNEL(sile_gemm_nt128_fp8_f32, kFP8, kOutF32, 128)
 
 // Split K: the ring kernel above writes one fp32 plane of C per k-range
 // (planes `plane` elements apart, rows n elements long); this kernel adds the

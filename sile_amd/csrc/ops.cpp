@@ -52,7 +52,7 @@ struct GemmArgs {
 //   a tile over k elements of K' takes k * t(w) + 6 us (4.7 us for 128 x
 //   128), where t depends on the tile size and on how many workgroups w run
 //   at once (the clock drops as more CUs draw power; two 128 x 128
-//   workgroups share a CU); half that for fp8 (256 x 256 only); workgroups
+//   workgroups share a CU); half that for fp8; workgroups
 //   beyond what the device holds at once run in further rounds;
 //   a split of K' into S ranges (at least 8 whole k-steps each, all ranges
 //   resident at once) adds the burst of fp32 planes the workgroups write as
@@ -91,7 +91,6 @@ GemmPlan gemm_plan(int64_t m, int64_t n, int64_t kp, int64_t half_steps, int64_t
   double best_t = 1e30, best_unsplit_t = 1e30;
   GemmPlan best_unsplit = best;
   for (int tile : {256, 128}) {
-    if (tile == 128 && fp8) continue;
     if ((tile == 256 && m < tile) || n < tile || (only_tile && tile != only_tile)) continue;
     const int64_t tiles = ((m + tile - 1) / tile) * ((n + tile - 1) / tile);
     const int64_t slots = (int64_t)cus * (tile == 256 ? 1 : 2);
@@ -370,25 +369,22 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   const bool fp8 = kstep == 64;
   if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
     return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
-  // the LDS kernels need N >= the tile edge (256, or 128 with 16-bit
-  // operands) and M >= 256 for 256 x 256 tiles (128 x 128 tiles take any M)
-  const int64_t min_tile = tile_req ? tile_req : fp8 ? 256 : 128;
+  // the LDS kernels need N >= the tile edge (128 x 128 tiles take any M,
+  // 256 x 256 tiles M >= 256)
+  const int64_t min_tile = tile_req ? tile_req : 128;
   const bool lds_ok = (min_tile == 128 || m >= min_tile) && n >= min_tile && n % 4 == 0 &&
-                      (ldc * cb) % 16 == 0 && aligned16(c) && !(fp8 && min_tile == 128);
+                      (ldc * cb) % 16 == 0 && aligned16(c);
   if (tile_req && !lds_ok)
     return fail(SILE_ERR_SHAPE,
-                "%d x %d tiles need %sN >= %d, N a multiple of 4, C's rows 16-byte aligned%s",
-                tile_req, tile_req, tile_req == 256 ? "M, " : "", tile_req,
-                tile_req == 128 ? " and 16-bit operands" : "");
+                "%d x %d tiles need %sN >= %d, N a multiple of 4 and C's rows 16-byte aligned",
+                tile_req, tile_req, tile_req == 256 ? "M, " : "", tile_req);
   // The transposed form runs C^T = B . A^T (A and B swapped) into fp32
   // planes of C^T and writes them back transposed, for the shapes the direct
   // form cannot take (N below one tile, N not a multiple of 4, C's rows not
   // 16-byte aligned) whose M can be the column extent: a multiple of 4 and
   // at least one tile.
   // Its fp32 planes (all of C^T) are kept to kScratchPlanesMax bytes.
-  const bool transposed = !lds_ok && m % 4 == 0 &&
-                          (fp8 ? (m >= 256 && n >= 256) : m >= 128) &&
-                          m * n * 4 <= kScratchPlanesMax;
+  const bool transposed = !lds_ok && m % 4 == 0 && m >= 128 && m * n * 4 <= kScratchPlanesMax;
   if (!lds_ok && !transposed) {
     // the any-shape kernel, 64 x 64 tiles with fragments loaded straight
     // from the operands
@@ -404,7 +400,7 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
     int rc = launch(Module::kGemm, sname, dim3((unsigned)gx, (unsigned)gy), dim3(256), sp, s);
     return rc == SILE_OK ? ok() : rc;
   }
-  // the LDS kernels: 256 x 256 or (16-bit operands) 128 x 128 tiles over the
+  // the LDS kernels: 256 x 256 or 128 x 128 tiles over the
   // form that runs, (ra: [rm, K], rb: [rn, K]) -> [rm, rn]; any K' (the kernel
   // zeroes the elements of its last half k-step past K')
   const void* ra = transposed ? b : a;

@@ -93,7 +93,7 @@ def test_gemm_rejects_unaligned_and_row_major_b():
     (_abi.BF16, 256, 256, 256, 65, "splits must be"),    # too many ranges
     (_abi.BF16, 256, 256, 0, -1, "splits must be"),
     (_abi.BF16, 200, 512, 256, 0, "256 x 256 tiles need"),   # M below the forced tile
-    (_abi.F8E4M3, 512, 512, 128, 0, "16-bit operands"),      # no 128 x 128 fp8 kernel
+    (_abi.F8E4M3, 200, 512, 256, 0, "256 x 256 tiles need"),
     (_abi.BF16, 512, 258, 128, 0, "128 x 128 tiles need"),   # N not a multiple of 4
 ])
 def test_gemm_tiled_host_validation(a_t, m, n, tile, splits, needle):

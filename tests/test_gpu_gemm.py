@@ -476,7 +476,7 @@ def test_split_k(hip, kind, out, m, n, k, bk, tile, splits):
 
 
 @pytest.mark.parametrize("kind,out", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"),
-                                      ("f16", "f32")])
+                                      ("f16", "f32"), ("fp8", "bf16"), ("fp8", "f32")])
 @pytest.mark.parametrize("m,n,k,bk,tile", [(128, 128, 64, 0, 0), (200, 300, 320, 0, 0),
                                            (130, 1028, 448, 0, 0), (255, 260, 192, 50, 0),
                                            (128, 256, 8192, 0, 0), (192, 1024, 2048, 0, 0),
@@ -484,7 +484,7 @@ def test_split_k(hip, kind, out, m, n, k, bk, tile, splits):
                                            (100, 300, 320, 0, 128), (16, 1024, 4096, 0, 128),
                                            (127, 260, 192, 50, 128)])
 def test_tile128(hip, kind, out, m, n, k, bk, tile):
-    """M or N in [128, 256) with 16-bit operands: 128 x 128 tiles through LDS
+    """M or N in [128, 256): 128 x 128 tiles through LDS
     (the last tile row / column moved back to end at M / N, C in a wider
     pitch; N % 8 == 4 puts the last column tile's rows 8 bytes off a 16-byte
     boundary), K' truncated inside a half k-step (255 x 260 x 192, bk = 50),
@@ -494,11 +494,19 @@ def test_tile128(hip, kind, out, m, n, k, bk, tile):
     kp = (k // bk) * bk if bk else k
     ldc = -(-(n + 8) // 8) * 8   # 16-byte rows for every C type
     say(f"gemm tile128 {kind} {m}x{n}x{k} bk={bk} -> {out} tile={tile}")
-    a = (rng(41).normal(size=(m, k)) / np.sqrt(kp)).astype(np.float32)
-    bt = (rng(42).normal(size=(n, k)) / np.sqrt(kp)).astype(np.float32)
-    rnd = bf16_round if kind == "bf16" else f16_round
-    (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
-    t = hip.BF16 if kind == "bf16" else hip.F16
+    a = rng(41).normal(size=(m, k)).astype(np.float32)
+    bt = rng(42).normal(size=(n, k)).astype(np.float32)
+    if kind == "fp8":
+        qa, sa, a_f = fp8_quantise(a)
+        qb, sb, b_f = fp8_quantise(bt)
+        t = hip.F8E4M3
+    else:
+        a /= np.sqrt(kp)
+        bt /= np.sqrt(kp)
+        rnd = bf16_round if kind == "bf16" else f16_round
+        (qa, a_f), (qb, b_f) = rnd(a), rnd(bt)
+        sa = sb = 1.0
+        t = hip.BF16 if kind == "bf16" else hip.F16
     c_t = {"bf16": hip.BF16, "f16": hip.F16, "f32": hip.F32}[out]
     cb = 4 if out == "f32" else 2
     da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
@@ -506,11 +514,11 @@ def test_tile128(hip, kind, out, m, n, k, bk, tile):
     dc = hip.DeviceBuffer((m + 1) * ldc * cb)
     dc.fill_bytes(0xFF)
     hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-             dc.ptr, ldc, 1.0, 1.0, bk, tile=tile)
+             dc.ptr, ldc, sa, sb, bk, tile=tile)
     hip.synchronize()
     got = _to_f32(hip, dc, c_t, m, ldc)
     ref = cpuref.gemm_nt(a_f[:, :kp], b_f[:, :kp])
-    tol = (1e-4, 1e-4) if out == "f32" else (ATOL, RTOL)
+    tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
     assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} tile128")
     raw = dc.download(np.uint32 if cb == 4 else np.uint16, (m + 1, ldc))
     fill = 0xFFFFFFFF if cb == 4 else 0xFFFF
@@ -525,7 +533,8 @@ def test_tile128(hip, kind, out, m, n, k, bk, tile):
     ("f16", "f32", 300, 258, 200, 1, 50),      # K' = 200 from bk = 50
     ("bf16", "bf16", 256, 256, 64, 3, 0),      # C's rows not 16-byte aligned
     ("bf16", "bf16", 512, 64, 8192, 0, 0),     # and K' split
-    ("fp8", "bf16", 512, 258, 256, 0, 0),      # fp8 needs M, N >= 256
+    ("fp8", "bf16", 512, 258, 256, 0, 0),
+    ("fp8", "bf16", 512, 64, 320, 0, 0),
     ("fp8", "f32", 256, 300, 320, 5, 0),
 ])
 def test_transposed_form(hip, kind, out, m, n, k, ldc_pad, bk):
