@@ -82,13 +82,15 @@ def normal(seed, shape, scale=1.0):
     return out
 
 
-def gemm_inputs(kind, size):
-    """Host operands of the GEMM configurations at M = N = K = size:
-    (a_bits [M, K], b_bits [N, K] (B column-major), scale_a, scale_b, a_type).
+def gemm_inputs(kind, m, n=None, k=None):
+    """Host operands of the GEMM configurations at M x N x K (M = N = K = m
+    when n and k are not given): (a_bits [M, K], b_bits [N, K] (B
+    column-major), scale_a, scale_b, a_type).
     bf16: A, B ~ N(0, 1)/sqrt(K), seeds 4 / 5, rounded to bf16 (RNE).
     fp8: A, B ~ N(0, 1), seeds 9 / 10, quantised per tensor to e4m3fn with
     s = amax / 448, q = rne_sat(x / s)."""
-    m = n = k = size
+    n = m if n is None else n
+    k = m if k is None else k
     if kind == "fp8":
         # the oracle's encoder is the configuration's quantiser (input recipe,
         # not timed work)
@@ -199,12 +201,14 @@ def roofline_obj(bound, achieved, peak, unit, traffic):
 
 # ---------------------------------------------------------------- workloads
 
-def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0):
+def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_step=0):
     """cpu_tile_step > 0 also times the CPU oracle on every cpu_tile_step-th
-    256-row tile of C over the same (de)quantised inputs."""
-    m = n = k = size
+    256-row tile of C over the same (de)quantised inputs (the whole GEMM when
+    M is below one tile).  The roofline is the matrix cores' unless streaming
+    A, B and C once at the HBM peak takes longer (skinny shapes): then it is
+    the algorithmic bytes over the step time, in GB/s."""
     log(f"[bench] {name}: generating inputs")
-    a_bits, b_bits, sa, sb, t = gemm_inputs(kind, size)
+    a_bits, b_bits, sa, sb, t = gemm_inputs(kind, m, n, k)
     c_t = hip.BF16
     da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
     host = (a_bits, b_bits) if cpu_tile_step else None
@@ -218,11 +222,18 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0
     log(f"[bench] {name}: timing {steps} steps")
     region = time_launches(launch, steps, warmup, stream)
     flop = 2.0 * m * n * k
+    eb = 1 if kind == "fp8" else 2
+    nbytes = float(eb * (m * k + n * k) + 2 * m * n)
     res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "mfma", PEAK_TFLOPS[kind],
                     traffic.get(name))
     res["flop_per_launch"] = flop
-    res["same_kernel_on_zero_inputs"] = zero_input_rate(launch, (da, db), flop, PEAK_TFLOPS[kind],
-                                                        steps, stream)
+    if nbytes / (PEAK_HBM_GBS * 1e9) > flop / (PEAK_TFLOPS[kind] * 1e12):
+        gbs = nbytes / (res["ms_per_step"] * 1e-3) / 1e9
+        res["roofline"] = roofline_obj("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic.get(name))
+        res["bytes_per_launch"] = nbytes
+    else:
+        res["same_kernel_on_zero_inputs"] = zero_input_rate(launch, (da, db), flop,
+                                                            PEAK_TFLOPS[kind], steps, stream)
     for buf in (da, db, dc):
         buf.close()
     if host is not None:
@@ -235,10 +246,12 @@ def bench_gemm(name, kind, size, steps, warmup, stream, traffic, cpu_tile_step=0
             what = "up-cast fp32 inputs"
         del host
         c32 = np.zeros((m, n), np.float32)
-        rows = ((m // 256 + cpu_tile_step - 1) // cpu_tile_step) * 256
+        if m < 256:
+            cpu_tile_step = 1
+        rows = m if m < 256 else ((m // 256 + cpu_tile_step - 1) // cpu_tile_step) * 256
         log(f"[bench] {name}: cpu oracle on {rows} of {m} rows")
         res["cpu_baseline"] = cpu_timed(
-            lambda: cpuref.gemm_nt(a32, b32, bm=256, row_tile_step=cpu_tile_step, out=c32),
+            lambda: cpuref.gemm_nt(a32, b32, bm=min(256, m), row_tile_step=cpu_tile_step, out=c32),
             2.0 * rows * n * k, 1e12, "TFLOP/s",
             (f"every {cpu_tile_step}th 256-row tile of C ({rows} of {m} rows, all columns, full K)"
              if cpu_tile_step > 1 else "the whole GEMM")
@@ -706,7 +719,11 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
 EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f32_exact_4096",
-         "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32"]
+         "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
+         # shapes off the headline configurations: 128 x 128 tiles, split K', the
+         # transposed form (M x N x K)
+         "gemm_bf16_2048x2048x2048", "gemm_bf16_128x8192x8192", "gemm_bf16_8192x64x8192",
+         "gemm_fp8_256x8192x8192"]
 
 
 def main():
@@ -757,10 +774,12 @@ def main():
                                                  traffic, cpu=cpu and size <= 1024)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
-            size = int(name.split("_")[-1])
+            dims = name.split("_")[-1]
+            m, n, k = map(int, dims.split("x")) if "x" in dims else (int(dims),) * 3
             # the bf16 8192^3 GEMM's CPU time is the headline cpu_baseline below
-            step = 0 if not cpu or name == "gemm_bf16_8192" else (8 if size >= 8192 else 1)
-            results[name] = bench_gemm(name, kind, size, args.steps, args.warmup, stream,
+            step = (0 if not cpu or name == "gemm_bf16_8192"
+                    else 8 if 2.0 * m * n * k > 2e11 else 1)
+            results[name] = bench_gemm(name, kind, m, n, k, args.steps, args.warmup, stream,
                                        traffic, cpu_tile_step=step)
         elif name.startswith("flash_attn"):
             results[name] = bench_attention(name, int(name.split("_s")[-1]), args.steps,

@@ -571,20 +571,20 @@ SILE_GEMM_SPLITK_REDUCE(sile_gemm_splitk_reduce_f32, kOutF32)
 // The same sum for the transposed form: the ring kernel ran C^T = B . A^T
 // (A and B swapped), so plane z holds C^T as n rows of `pitch` fp32 (pitch a
 // multiple of 4, at least m).  C[i][j] = alpha * sum_z plane_z[j][i], in plane
-// order.  A workgroup moves one 64 x 64 block through LDS: 16-byte reads
-// along i, element stores along j (C may have any pitch and alignment).
+// order.  A workgroup moves one 32 (i) x 64 (j) block through LDS: 16-byte
+// reads along i, element stores along j (C may have any pitch and alignment).
 template <int kOut>
 __device__ __forceinline__ void splitk_reduce_t_body(const float* __restrict__ ws,
                                                      void* __restrict__ C, int64_t ldc, int64_t m,
                                                      int64_t n, int64_t plane, int64_t pitch,
                                                      int splits, float alpha) {
-  __shared__ float blk[64][65];
+  __shared__ float blk[64][33];
   const int tid = threadIdx.x;
-  const int64_t i0 = (int64_t)blockIdx.x * 64, j0 = (int64_t)blockIdx.y * 64;
-  const int iq = 4 * (tid & 15);
+  const int64_t i0 = (int64_t)blockIdx.x * 32, j0 = (int64_t)blockIdx.y * 64;
+  const int iq = 4 * (tid & 7);
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int jj = (tid >> 4) + 16 * p;
+  for (int p = 0; p < 2; ++p) {
+    const int jj = (tid >> 3) + 32 * p;
     f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
     if (j0 + jj < n && i0 + iq < m) {
       const float* src = ws + (j0 + jj) * pitch + i0 + iq;
@@ -597,8 +597,8 @@ __device__ __forceinline__ void splitk_reduce_t_body(const float* __restrict__ w
   }
   __syncthreads();
   const int jj = tid & 63;
-#pragma unroll 4
-  for (int q = 0; q < 16; ++q) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
     const int ii = (tid >> 6) + 4 * q;
     const int64_t i = i0 + ii, j = j0 + jj;
     if (i >= m || j >= n) continue;

@@ -463,7 +463,7 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
     if (transposed) {
       snprintf(rname, sizeof rname, "sile_gemm_splitk_reduce_t_%s", out);
       void* rp[] = {&ws, &c, &ldc_, &m_, &n_, &plane, &pitch, &sp, &al};
-      rc = launch(Module::kGemm, rname, dim3((unsigned)((m + 63) / 64), (unsigned)((n + 63) / 64)),
+      rc = launch(Module::kGemm, rname, dim3((unsigned)((m + 31) / 32), (unsigned)((n + 63) / 64)),
                   dim3(256), rp, s);
     } else {
       snprintf(rname, sizeof rname, "sile_gemm_splitk_reduce_%s", out);
