@@ -576,3 +576,40 @@ def test_transposed_form(hip, kind, out, m, n, k, ldc_pad, bk):
     tol = (1e-4, 1e-4) if (out == "f32" and kind != "fp8") else (ATOL, RTOL)
     assert_close(got[:, :n], ref, atol=tol[0], rtol=tol[1], what=f"{kind} transposed")
     assert (raws[0][:, n:] == (0xFFFFFFFF if cb == 4 else 0xFFFF)).all()
+
+
+def test_split_k_scratch_across_streams_and_growth(hip):
+    """The split and transposed forms share one scratch buffer per device.
+    Calls queued on two streams without waiting in between must not see each
+    other's planes (the library orders them with an event), and a call that
+    needs more scratch than an earlier one grows it while the earlier work
+    may still be running.  Sequence: small split on stream 1, large split on
+    stream 2 (grows the scratch), transposed form on stream 1, small split on
+    stream 2, each with its own inputs; every result against the oracle."""
+    say("gemm scratch: two streams, growth")
+    cases = [(256, 256, 4096, 1), (512, 512, 8192, 2), (512, 64, 2048, 1), (256, 256, 2048, 2)]
+    s1, s2 = hip.Stream(), hip.Stream()
+    streams = {1: s1, 2: s2}
+    runs = []
+    for idx, (m, n, k, sid) in enumerate(cases):
+        a = (rng(60 + 2 * idx).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+        bt = (rng(61 + 2 * idx).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+        (qa, a_f), (qb, b_f) = bf16_round(a), bf16_round(bt)
+        da, db = hip.DeviceBuffer.from_array(qa), hip.DeviceBuffer.from_array(qb)
+        dc = hip.DeviceBuffer(m * n * 4)
+        dc.fill_bytes(0xFF)
+        runs.append((m, n, a_f, b_f, da, db, dc))
+    hip.synchronize()
+    for (m, n, k, sid), (_, _, _, _, da, db, dc) in zip(cases, runs):
+        hip.gemm(hip.BF16, hip.BF16, hip.F32, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k,
+                 hip.COL_MAJOR, dc.ptr, n, 1.0, 1.0, 0, streams[sid])
+    s1.synchronize()
+    s2.synchronize()
+    for idx, (m, n, a_f, b_f, da, db, dc) in enumerate(runs):
+        got = dc.download(np.float32, (m, n))
+        assert_close(got, cpuref.gemm_nt(a_f, b_f), atol=1e-4, rtol=1e-4,
+                     what=f"scratch case {idx}")
+        for x in (da, db, dc):
+            x.close()
+    s1.close()
+    s2.close()
