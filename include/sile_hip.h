@@ -61,6 +61,7 @@ typedef void *sile_hip_stream;   /* hipStream_t */
 typedef void *sile_hip_event;    /* hipEvent_t */
 typedef void *sile_hip_module;   /* hipModule_t */
 typedef void *sile_hip_function; /* hipFunction_t */
+typedef void *sile_hip_graph;    /* hipGraphExec_t */
 
 typedef struct {
   char name[256];
@@ -108,6 +109,20 @@ int sile_hip_event_destroy(sile_hip_event event);
 int sile_hip_event_record(sile_hip_event event, sile_hip_stream stream);
 int sile_hip_event_synchronize(sile_hip_event event);
 int sile_hip_event_elapsed_ms(float *ms, sile_hip_event start, sile_hip_event stop);
+
+/* ---- graphs (no counterpart in the reference, whose launches are host
+ *      calls; for callers that replay a fixed sequence of op calls) ---------
+ * sile_hip_graph_begin starts capturing `stream` (not the null stream;
+ * thread-local mode); op calls on it are then recorded, not run.
+ * sile_hip_graph_end stops the capture and instantiates what was recorded.
+ * The op entry points record plain kernel launches (sile_hip_gemm leaves out
+ * its scratch-using forms under capture); the synchronous calls
+ * (sile_hip_launch_tiles and the sile_hip_kernel_* DSL kernels) cannot be
+ * captured and fail on a capturing stream. */
+int sile_hip_graph_begin(sile_hip_stream stream);
+int sile_hip_graph_end(sile_hip_stream stream, sile_hip_graph *out);
+int sile_hip_graph_launch(sile_hip_graph graph, sile_hip_stream stream);
+int sile_hip_graph_destroy(sile_hip_graph graph);
 
 /* ---- code objects and the generic tile launch --------------------------- */
 
@@ -251,8 +266,12 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  * the first such call, grown when a call needs more, at most
  * 4 * (CUs * 65536) bytes; calls on different streams are ordered on the GPU
  * by an event) and a second kernel adds them in range order.  The result
- * does not depend on the stream or on earlier calls.  The transposed form
+ * does not depend on the stream or on earlier calls (outside graph capture,
+ * below).  The transposed form
  * (above) keeps all of C^T there, up to 256 MiB (larger: 64 x 64 tiles).
+ * On a stream that is being captured into a graph neither form is used (no
+ * split; the 64 x 64 kernel instead of the transposed form), so a captured
+ * call is plain kernel launches.
  * M = 0 or N = 0: nothing is written.  K' = 0 (K below one bk): C = +0.0 for
  * any M, N and supported types, as the canonical matmul's sums start at 0.0f
  * and add no term (canonical_matmul.rs:58-73).

@@ -134,6 +134,10 @@ SIGNATURES = {
     "sile_hip_kernel_parallel_reduce": [_P, _I64, _I64, _P, _I64, _I64, _P, _P],
     "sile_hip_gemm": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32, _P,
                       _I64, _F32, _F32, _I64, _P],
+    "sile_hip_graph_begin": [_P],
+    "sile_hip_graph_end": [_P, ctypes.POINTER(_P)],
+    "sile_hip_graph_launch": [_P, _P],
+    "sile_hip_graph_destroy": [_P],
     "sile_hip_gemm_tiled": [_I32, _I32, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _I64, _I32,
                             _P, _I64, _F32, _F32, _I64, _I32, _I32, _P],
     "sile_hip_mma_f32": [_I64, _I64, _I64, _P, _I64, _P, _I64, _I32, _P, _I64, _F32, _P, _I64, _I64,
@@ -269,6 +273,36 @@ class Stream:
     def close(self) -> None:
         if self.handle:
             call("sile_hip_stream_destroy", self.handle)
+            self.handle = None
+
+
+class Graph:
+    """A captured sequence of op calls on `stream` (sile_hip_graph_begin /
+    end), replayed by launch()."""
+
+    def __init__(self, stream: "Stream"):
+        self.stream = stream
+        self.handle = None
+
+    def __enter__(self):
+        call("sile_hip_graph_begin", self.stream.handle)
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        p = _P()
+        rc = lib().sile_hip_graph_end(self.stream.handle, ctypes.byref(p))
+        if exc_type is None:
+            if rc != SILE_OK:
+                raise SileError(rc, last_error(), "sile_hip_graph_end")
+            self.handle = p.value
+        return False
+
+    def launch(self, stream: "Stream | None" = None) -> None:
+        call("sile_hip_graph_launch", self.handle, (stream or self.stream).handle)
+
+    def close(self) -> None:
+        if self.handle:
+            call("sile_hip_graph_destroy", self.handle)
             self.handle = None
 
 

@@ -383,8 +383,19 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   // form cannot take (N below one tile, N not a multiple of 4, C's rows not
   // 16-byte aligned) whose M can be the column extent: a multiple of 4 and
   // at least one tile.
-  // Its fp32 planes (all of C^T) are kept to kScratchPlanesMax bytes.
-  const bool transposed = !lds_ok && m % 4 == 0 && m >= 128 && m * n * 4 <= kScratchPlanesMax;
+  // Its fp32 planes (all of C^T) are kept to kScratchPlanesMax bytes.  The
+  // forms that use the device scratch (this one and the K split) are left
+  // out while the stream is being captured into a graph: the scratch is
+  // ordered by events recorded at call time, which a graph's replays would
+  // not follow.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+  if (capturing && splits_req > 1)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "a K split needs the device scratch, which stream "
+                                              "capture cannot order");
+  const bool transposed = !lds_ok && !capturing && m % 4 == 0 && m >= 128 &&
+                          m * n * 4 <= kScratchPlanesMax;
   if (!lds_ok && !transposed) {
     // the any-shape kernel, 64 x 64 tiles with fragments loaded straight
     // from the operands
@@ -416,6 +427,7 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
   GemmPlan plan = gemm_plan(rm, rn, kp, half_steps, (int64_t)cb, fp8, tile_req);
   if (splits_req) plan.splits = splits_req;
+  if (capturing) plan.splits = 1;
   if (transposed) plan.splits = std::max<int64_t>(1, std::min(plan.splits, kScratchPlanesMax / (rm * rn * 4)));
   const int64_t tiles_m = (rm + plan.tile - 1) / plan.tile;
   const int64_t tiles_n = (rn + plan.tile - 1) / plan.tile;

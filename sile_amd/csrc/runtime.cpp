@@ -339,6 +339,37 @@ int sile_hip_stream_synchronize(sile_hip_stream stream) {
   return ok();
 }
 
+int sile_hip_graph_begin(sile_hip_stream stream) {
+  if (!stream) return fail(SILE_ERR_SHAPE, "the null stream cannot be captured");
+  SILE_HIP_CHECK(hipStreamBeginCapture(static_cast<hipStream_t>(stream),
+                                       hipStreamCaptureModeThreadLocal));
+  return ok();
+}
+
+int sile_hip_graph_end(sile_hip_stream stream, sile_hip_graph* out) {
+  if (!stream || !out) return fail(SILE_ERR_SHAPE, "NULL stream or out");
+  hipGraph_t g = nullptr;
+  SILE_HIP_CHECK(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *out = exec;
+  return ok();
+}
+
+int sile_hip_graph_launch(sile_hip_graph graph, sile_hip_stream stream) {
+  if (!graph) return fail(SILE_ERR_SHAPE, "graph is NULL");
+  SILE_HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(graph),
+                                static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int sile_hip_graph_destroy(sile_hip_graph graph) {
+  if (graph) SILE_HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
+  return ok();
+}
+
 int sile_hip_event_create(sile_hip_event* out) {
   if (!out) return fail(SILE_ERR_SHAPE, "out is NULL");
   hipEvent_t e = nullptr;

@@ -156,3 +156,11 @@ def test_32bit_buffer_range_guards():
     rc = _abi.status("sile_hip_flash_attn_fwd", _abi.F16, 1, 1, 1 << 23, 128, 16, 16, 16, 16,
                      1.0, 1, NULL)
     assert rc == 5 and "sequence" in _abi.last_error()
+
+
+def test_graph_capture_rejects_the_null_stream():
+    """Capture needs a stream of its own (checked before any HIP call)."""
+    rc = _abi.status("sile_hip_graph_begin", NULL)
+    assert rc == 5 and "null stream" in _abi.last_error()
+    rc = _abi.status("sile_hip_graph_launch", NULL, NULL)
+    assert rc == 5 and "graph is NULL" in _abi.last_error()
