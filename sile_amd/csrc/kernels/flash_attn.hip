@@ -350,7 +350,7 @@ __device__ __forceinline__ void attn_fwd_body(const uint16_t* __restrict__ Q,
 }  // namespace
 
 // ===========================================================================
-// Pipelined kernel (S a multiple of 256): 8 waves x 32 queries, 32-key blocks.
+// Pipelined kernel (any S): 8 waves x 32 queries, 32-key blocks.
 //
 // Iteration j of the key loop issues, as one scheduling region,
 //   * on the matrix cores: S_{j+1} = K_{j+1} . Q^T  and  O^T += V_{j-1}^T . P_{j-1}
@@ -447,7 +447,10 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     u32x4 qf[kQT][8];
   #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      const uint16_t* qrow = Q + head_off + (int64_t)(wq0 + qt * 32 + l32) * kD + 8 * g;
+      // queries past S (the last block of an S that is not a multiple of
+      // 256) read row S - 1 and are not stored
+      const int64_t qr = min((int64_t)(wq0 + qt * 32 + l32), S - 1);
+      const uint16_t* qrow = Q + head_off + qr * kD + 8 * g;
   #pragma unroll
       for (int kk = 0; kk < 8; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
     }
@@ -575,7 +578,12 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   #pragma unroll
       for (int cc = 0; cc < 2 * kST; ++cc) pprev[qt][cc] = u32x4{0u, 0u, 0u, 0u};
 
-    const int nb = a.causal ? (q0 + kBQ) / kNK : (int)(S / kNK);
+    // key blocks: through the block's last query (causal) or S, rounded up
+    // to even (the loop runs in pairs); keys past S load as zeros (outside
+    // the K / V buffer resources) and are masked
+    const int64_t kend = a.causal ? min((int64_t)(q0 + kBQ), S) : S;
+    int nb = (int)((kend + kNK - 1) / kNK);
+    nb += nb & 1;
     const int last = nb - 1;
     const float c = a.scale_log2;
 
@@ -583,8 +591,8 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     // K_{j+2} and V_j into stage j & 1, whose previous contents were read in
     // iteration j - 1; the barrier closing iteration j waits for those loads.
     // The key loop is unrolled by two so that stage indices and the roles of
-    // the two S and P register sets are compile-time constants (nb is even:
-    // S is a multiple of 256 and blocks hold at most 64 keys).
+    // the two S and P register sets are compile-time constants (nb is even,
+    // rounded up above).
     // Prologue: K_0, K_1 and a finite V tile in stage 1 for the empty PV_{-1}
     // (its P is zero).
     dma_k(0, 0);
@@ -615,7 +623,9 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
         const int kb = j * kNK;
   #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
-          const int q = wq0 + 32 * qt + l32 - kb - 4 * g;  // key offset limit for this lane
+          // last key this lane's query sees: the query itself (causal) or S - 1
+          const int lim = a.causal ? min(wq0 + 32 * qt + l32, (int)S - 1) : (int)S - 1;
+          const int q = lim - kb - 4 * g;  // key offset limit for this lane
   #pragma unroll
           for (int st = 0; st < kST; ++st)
   #pragma unroll
@@ -716,8 +726,9 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       }
       __syncthreads();
     };
-    // blocks left of the workgroup's diagonal need no mask
-    const int j_diag = a.causal ? q0 / kNK : nb;
+    // blocks left of the workgroup's diagonal (causal) or of the block that
+    // holds key S (S not a multiple of the block) need no mask
+    const int j_diag = a.causal ? q0 / kNK : (int)(S / kNK) & ~1;
     using Z = std::integral_constant<int, 0>;
     using One = std::integral_constant<int, 1>;
     int j = 0;
@@ -738,6 +749,7 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       const float l = pair32_sum(l_run[qt]);
       const float inv = 1.0f / l;
       const int q = wq0 + 32 * qt + l32;
+      if (q >= S) continue;
       uint16_t* orow = O + head_off + (int64_t)q * kD;
   #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
@@ -772,9 +784,6 @@ SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32)
     attn_fwd_body<BF, QT, NK, DH>(Q, K, V, O, a, smem);                                       \
   }
 
-// 128 queries per workgroup, any S: head_dim 128 over 64-key blocks, head_dim
-// 64 over 128-key blocks (the same LDS bytes per stage)
-SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k64, false, 1, 64, 128)
-SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k64, true, 1, 64, 128)
+// 128 queries per workgroup, any S, head_dim 64 over 128-key blocks
 SILE_FA_KERNEL(sile_flash_attn_fwd_f16_q1_k128_d64, false, 1, 128, 64)
 SILE_FA_KERNEL(sile_flash_attn_fwd_bf16_q1_k128_d64, true, 1, 128, 64)

@@ -713,15 +713,15 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
   // MFMA flash kernels, 16-byte aligned operands, chosen by shape:
-  //   head_dim 128, S a multiple of 256: the pipelined kernel (8 waves x 32
-  //     queries, 32-key blocks through LDS-DMA; causal query blocks taken in
-  //     balanced pairs);
-  //   head_dim 128 or 64, any other S: the block kernel (128 queries per
-  //     workgroup, keys and queries past S masked).
+  //   head_dim 128, any S: the pipelined kernel (8 waves x 32 queries, 32-key
+  //     blocks through LDS-DMA; causal query blocks taken in balanced pairs;
+  //     keys and queries past S masked);
+  //   head_dim 64: the block kernel (128 queries per workgroup, keys and
+  //     queries past S masked).
   const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   if ((head_dim == 128 || head_dim == 64) && aligned) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const bool pipelined = head_dim == 128 && seq_len % 256 == 0;
+    const bool pipelined = head_dim == 128;
     const int64_t bq = pipelined ? 256 : 128;
     const bool pair = causal && pipelined;
     const int64_t q_blocks = (seq_len + bq - 1) / bq;
@@ -739,8 +739,6 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     char name[64];
     if (pipelined)
       snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2w8", dt);
-    else if (head_dim == 128)
-      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q1_k64", dt);
     else
       snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q1_k128_d64", dt);
     const unsigned threads = pipelined ? 512 : 256;

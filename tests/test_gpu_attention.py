@@ -94,19 +94,20 @@ def test_attention_config4_full_shape_sampled(hip):
     assert np.isfinite(got).all()
 
 
-# The MFMA kernel is chosen by shape: S a multiple of 256 runs the pipelined
-# kernel (causal query blocks in balanced pairs), other multiples of 128 the
-# 128-query-block kernel.
-KERNEL_S = {"pipelined": 512, "q128": 384}
+# The MFMA kernel is chosen by head_dim: 128 runs the pipelined kernel
+# (256-query blocks, causal ones in balanced pairs; S = 384 leaves the last
+# block half empty), 64 the 128-query-block kernel.
+KERNEL_CASE = {"pipelined": (512, 128), "partial": (384, 128), "d64": (384, 64)}
 
 
-@pytest.mark.parametrize("kernel", ["pipelined", "q128"])
+@pytest.mark.parametrize("kernel", ["pipelined", "partial", "d64"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_kernels_xcd_order(hip, kernel, dt, causal):
     """Each MFMA flash kernel on B*H = 8 heads (head-per-XCD launch order);
     every head and query is compared with the fp32 oracle."""
-    b, h, s, d = 2, 4, KERNEL_S[kernel], 128
+    b, h = 2, 4
+    s, d = KERNEL_CASE[kernel]
     say(f"flash {dt} {kernel} causal={causal} B={b} H={h} S={s}")
     scale = 1.0 / np.sqrt(d)
     qkv = _inputs(b, h, s, d, dt, seed=21)
@@ -140,21 +141,24 @@ def test_flash_causal_row_independence(hip):
 def test_flash_causal_pairs_bit_identical(hip, b, h):
     """Causal rows depend only on the keys up to them, so the first 512
     queries of S = 1024 (4 blocks of 256: pairs (3, 0), (2, 1)), S = 768
-    (pairs (2, 0), (1) alone) and S = 512 (pair (1, 0)) must be computed
-    bit for bit alike, whichever block a workgroup pairs them with."""
+    (pairs (2, 0), (1) alone), S = 640 (the same pairs, the last block with
+    128 queries and 20 key blocks) and S = 512 (pair (1, 0)) must be
+    computed bit for bit alike, whichever block a workgroup pairs them with
+    and however many masked key blocks follow."""
     d = 128
-    say(f"flash causal pairs: S=1024 / 768 / 512 prefixes B={b} H={h}")
+    say(f"flash causal pairs: S=1024 / 768 / 640 / 512 prefixes B={b} H={h}")
     scale = 1.0 / np.sqrt(d)
     bits = [x[0] for x in _inputs(b, h, 1024, d, "f16", seed=41)]
     outs = {}
-    for s in (1024, 768, 512):
+    for s in (1024, 768, 640, 512):
         outs[s] = _run(hip, "f16", b, h, s, d, [np.ascontiguousarray(x[:, :, :s]) for x in bits],
                        True, scale)
     np.testing.assert_array_equal(outs[1024][:, :, :768], outs[768])
+    np.testing.assert_array_equal(outs[1024][:, :, :640], outs[640])
     np.testing.assert_array_equal(outs[1024][:, :, :512], outs[512])
 
 
-@pytest.mark.parametrize("kernel", ["pipelined", "q128"])
+@pytest.mark.parametrize("kernel", ["pipelined", "partial", "d64"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("trend", ["rising", "falling", "large", "plateau"])
@@ -170,7 +174,8 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
     every later block's p are 2^5 = 32 against the stale max: each lane's
     block sum (512) takes the pipelined kernel's block-max path, which finds
     no growth and keeps the max."""
-    b, h, s, d = 1, 8, KERNEL_S[kernel], 128
+    b, h = 1, 8
+    s, d = KERNEL_CASE[kernel]
     say(f"flash rescale {kernel} {dt} causal={causal} {trend}")
     r = rng(77)
     q = r.normal(size=(b, h, s, d)).astype(np.float32)
@@ -204,11 +209,13 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("b,h,s,d", [(1, 2, 100, 128), (2, 3, 333, 128), (1, 8, 1000, 128),
                                      (1, 2, 64, 64), (2, 3, 200, 64), (1, 8, 1024, 64),
-                                     (1, 1, 1, 128), (1, 1, 31, 64), (1, 4, 2049, 64)])
+                                     (1, 1, 1, 128), (1, 1, 31, 64), (1, 4, 2049, 64),
+                                     (1, 2, 31, 128), (1, 8, 1535, 128), (2, 4, 2049, 128)])
 def test_flash_any_seq_len_and_head_dim_64(hip, dt, causal, b, h, s, d):
-    """The block MFMA kernel for sequence lengths that are not multiples of
-    a block (keys and queries past S masked) and for head_dim 64; every head
-    and query against the fp32 oracle, and O past the last query untouched."""
+    """Sequence lengths that are not multiples of a query or key block (keys
+    and queries past S masked; the pipelined kernel for head_dim 128 with a
+    partial last query block and padded key blocks, the block kernel for
+    head_dim 64); every head and query against the fp32 oracle."""
     say(f"flash any-S {dt} causal={causal} B={b} H={h} S={s} D={d}")
     scale = 1.0 / np.sqrt(d)
     qkv = _inputs(b, h, s, d, dt, seed=51)
