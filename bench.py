@@ -259,13 +259,13 @@ def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_ste
     return res
 
 
-def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0):
+def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0, d=ATTN_SHAPE[2]):
     """cpu_heads > 0 also times the CPU oracle on the first cpu_heads (b, h)
     slices, every query row, causal."""
-    b, h, d = ATTN_SHAPE
+    b, h = ATTN_SHAPE[:2]
     log(f"[bench] {name}: generating inputs")
     bufs, host = [], []
-    for x in attention_inputs(s):
+    for x in attention_inputs(s, d=d):
         bufs.append(hip.DeviceBuffer.from_array(x.view(np.uint16)))
         if cpu_heads:
             host.append(x.reshape(b * h, s, d)[:cpu_heads].astype(np.float32))
@@ -724,8 +724,9 @@ EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f
          # transposed form (M x N x K)
          "gemm_bf16_2048x2048x2048", "gemm_bf16_128x8192x8192", "gemm_bf16_8192x64x8192",
          "gemm_fp8_256x8192x8192",
-         # causal attention at an S that is not a multiple of the query block
-         "flash_attn_fwd_f16_s8000"]
+         # causal attention at an S that is not a multiple of the query block,
+         # and at head_dim 64
+         "flash_attn_fwd_f16_s8000", "flash_attn_fwd_f16_s8192_d64"]
 
 
 def main():
@@ -784,9 +785,11 @@ def main():
             results[name] = bench_gemm(name, kind, m, n, k, args.steps, args.warmup, stream,
                                        traffic, cpu_tile_step=step)
         elif name.startswith("flash_attn"):
-            results[name] = bench_attention(name, int(name.split("_s")[-1]), args.steps,
-                                            args.warmup, stream, traffic,
-                                            cpu_heads=CPU_ATTN_HEADS if cpu else 0)
+            # flash_attn_fwd_f16_s<S>[_d<D>]
+            tail = name.split("_s")[-1]
+            s_len, d = (map(int, tail.split("_d")) if "_d" in tail else (int(tail), ATTN_SHAPE[2]))
+            results[name] = bench_attention(name, s_len, args.steps, args.warmup, stream, traffic,
+                                            cpu_heads=CPU_ATTN_HEADS if cpu else 0, d=d)
         else:
             results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic,
                                           cpu=cpu)

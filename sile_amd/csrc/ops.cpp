@@ -712,18 +712,15 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (seq_len * head_dim * 2 > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
-  // MFMA flash kernels, 16-byte aligned operands, chosen by shape:
-  //   head_dim 128, any S: the pipelined kernel (8 waves x 32 queries, 32-key
-  //     blocks through LDS-DMA; causal query blocks taken in balanced pairs;
-  //     keys and queries past S masked);
-  //   head_dim 64: the block kernel (128 queries per workgroup, keys and
-  //     queries past S masked).
+  // MFMA flash kernel, 16-byte aligned operands, head_dim 128 or 64, any S:
+  //   the pipelined kernel (8 waves x 32 queries, 32-key (head_dim 128) or
+  //   64-key (head_dim 64) blocks through LDS-DMA; causal query blocks taken
+  //   in balanced pairs; keys and queries past S masked).
   const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   if ((head_dim == 128 || head_dim == 64) && aligned) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const bool pipelined = head_dim == 128;
-    const int64_t bq = pipelined ? 256 : 128;
-    const bool pair = causal && pipelined;
+    const int64_t bq = 256;
+    const bool pair = causal;
     const int64_t q_blocks = (seq_len + bq - 1) / bq;
     if (q_blocks > 0x7fffffffLL / std::max<int64_t>(bh, 1))
       return fail(SILE_ERR_SHAPE, "attention too large");
@@ -737,11 +734,9 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const int64_t units = pair ? (q_blocks + 1) / 2 : q_blocks;
     const int64_t blocks = bh * units;
     char name[64];
-    if (pipelined)
-      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2w8", dt);
-    else
-      snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_q1_k128_d64", dt);
-    const unsigned threads = pipelined ? 512 : 256;
+    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2w8%s", dt,
+             head_dim == 64 ? "_d64" : "");
+    const unsigned threads = 512;
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(threads), params, s);
     return rc == SILE_OK ? ok() : rc;

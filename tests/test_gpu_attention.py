@@ -94,9 +94,9 @@ def test_attention_config4_full_shape_sampled(hip):
     assert np.isfinite(got).all()
 
 
-# The MFMA kernel is chosen by head_dim: 128 runs the pipelined kernel
-# (256-query blocks, causal ones in balanced pairs; S = 384 leaves the last
-# block half empty), 64 the 128-query-block kernel.
+# One MFMA kernel, 256-query blocks (causal ones in balanced pairs): head_dim
+# 128 over 32-key blocks, head_dim 64 over 64-key blocks; S = 384 leaves the
+# last query block half empty.
 KERNEL_CASE = {"pipelined": (512, 128), "partial": (384, 128), "d64": (384, 64)}
 
 
@@ -213,9 +213,9 @@ def test_flash_rescale_paths(hip, kernel, dt, causal, trend):
                                      (1, 2, 31, 128), (1, 8, 1535, 128), (2, 4, 2049, 128)])
 def test_flash_any_seq_len_and_head_dim_64(hip, dt, causal, b, h, s, d):
     """Sequence lengths that are not multiples of a query or key block (keys
-    and queries past S masked; the pipelined kernel for head_dim 128 with a
-    partial last query block and padded key blocks, the block kernel for
-    head_dim 64); every head and query against the fp32 oracle."""
+    and queries past S masked: a partial last query block, key blocks padded
+    to an even count), head_dim 128 and 64; every head and query against the
+    fp32 oracle."""
     say(f"flash any-S {dt} causal={causal} B={b} H={h} S={s} D={d}")
     scale = 1.0 / np.sqrt(d)
     qkv = _inputs(b, h, s, d, dt, seed=51)
