@@ -15,8 +15,12 @@
 //    or 2048, 4096, 8192 fp32 elements): one row per workgroup, the shape of
 //    the fastest copy measured on the device; the row max and sum are wave
 //    all-reductions plus one exchange of per-wave partials through LDS;
-//  * other widths: one wave per row with the row in registers (whole chunks,
-//    or a masked last chunk), or a three-pass kernel for rows past 8192.
+//  * other widths: kL lanes per row for rows of up to 32 chunks (4..32 rows
+//    per wave), one wave per row with the row in registers (whole chunks, or
+//    a masked last chunk) up to 8192, one row per 1024-thread workgroup with
+//    a masked last chunk up to 1024 * 8 chunks, two passes over the row by
+//    one workgroup beyond that; a three-pass element-wise kernel when the
+//    rows are not 16-byte aligned.
 // Wave all-reductions use DPP row permutes (common.h); exp(x - m) is
 // 2^((x - m) * log2 e) on v_exp_f32.
 #include "common.h"
@@ -379,6 +383,255 @@ SILE_SOFTMAX_BLOCK_WIDTHS(f16_f16, kF16, kF16)
 SILE_SOFTMAX_BLOCK_WIDTHS(bf16_bf16, kBF16, kBF16)
 SILE_SOFTMAX_BLOCK_WIDTHS(f32_f32, kF32, kF32)
 SILE_SOFTMAX_BLOCK_WIDTHS(f16_f32, kF16, kF32)
+
+// ---- narrow rows: kL lanes per row, one chunk per lane ----
+// cols <= kL * E; a wave holds 64 / kL rows and a workgroup of 4 waves
+// 256 / kL, so short rows still fill whole load instructions.  The row max
+// and sum are reductions inside kL-lane groups (DPP quad / half-row / row
+// permutes, a 16-lane swizzle for 32); every lane takes part in them, rows
+// past the last only neither load nor store.
+template <int kL>
+SILE_DEV float group_max(float v) {
+  v = fmax_ordered(v, dpp<kDppXor1>(v));
+  v = fmax_ordered(v, dpp<kDppXor2>(v));
+  if constexpr (kL >= 8) v = fmax_ordered(v, dpp<kDppHalfMirror>(v));
+  if constexpr (kL >= 16) v = fmax_ordered(v, dpp<kDppMirror>(v));
+  if constexpr (kL >= 32) v = fmax_ordered(v, swizzle_xor16(v));
+  return v;
+}
+template <int kL>
+SILE_DEV float group_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  if constexpr (kL >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (kL >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (kL >= 32) v += swizzle_xor16(v);
+  return v;
+}
+
+template <int kIn, int kOut, int kL>
+__device__ __forceinline__ void softmax_rows_narrow_kernel(const void* x, void* y, int64_t rows,
+                                                           int64_t cols, int64_t ldx,
+                                                           int64_t ldy) {
+  static_assert(kL == 4 || kL == 8 || kL == 16 || kL == 32, "lanes per row");
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  const int lane = threadIdx.x & 63, li = lane % kL;
+  const int64_t row = (int64_t)blockIdx.x * (256 / kL) + (threadIdx.x >> 6) * (64 / kL) + lane / kL;
+  const bool live = row < rows;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  const int c0 = li * kE;
+  float v[kE];
+  if (live && c0 + kE <= cols) {
+    load_chunk<kIn, kE>(static_cast<const TI*>(x) + row * ldx + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kE; ++i)
+      v[i] = live && c0 + i < cols ? Elem<kIn>::load1(static_cast<const TI*>(x) + row * ldx + c0 + i)
+                                   : -__builtin_inff();
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kE; ++i) m = fmax_ordered(m, v[i]);
+  m = group_max<kL>(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kE; ++i) {
+    v[i] = exp2_fast((v[i] - m) * kLog2e);   // -inf -> 0
+    s += v[i];
+  }
+  s = group_sum<kL>(s);
+  if (!live) return;
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < kE; ++i) v[i] = normalise<kOut>(v[i], s, inv);
+  TO* yr = static_cast<TO*>(y) + row * ldy;
+  if (c0 + kE <= cols) {
+    store_chunk<kOut, kE>(yr + c0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kE; ++i)
+      if (c0 + i < cols) Elem<kOut>::store1(yr + c0 + i, v[i]);
+  }
+}
+
+#define SILE_SOFTMAX_NARROW(NAME, IN, OUT, L)                                                    \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const void* x, void* y, int64_t rows,   \
+                                                         int64_t cols, int64_t ldx, int64_t ldy) { \
+    softmax_rows_narrow_kernel<IN, OUT, L>(x, y, rows, cols, ldx, ldy);                          \
+  }
+#define SILE_SOFTMAX_NARROW_WIDTHS(TAG, IN, OUT)                 \
+  SILE_SOFTMAX_NARROW(sile_softmax_rows_##TAG##_n4, IN, OUT, 4)   \
+  SILE_SOFTMAX_NARROW(sile_softmax_rows_##TAG##_n8, IN, OUT, 8)   \
+  SILE_SOFTMAX_NARROW(sile_softmax_rows_##TAG##_n16, IN, OUT, 16) \
+  SILE_SOFTMAX_NARROW(sile_softmax_rows_##TAG##_n32, IN, OUT, 32)
+SILE_SOFTMAX_NARROW_WIDTHS(f16_f16, kF16, kF16)
+SILE_SOFTMAX_NARROW_WIDTHS(bf16_bf16, kBF16, kBF16)
+SILE_SOFTMAX_NARROW_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_NARROW_WIDTHS(f16_f32, kF16, kF32)
+
+// ---- wide rows: one row per workgroup of 1024 threads ----
+// Masked form of the row-per-workgroup kernel for any width up to
+// 1024 * kChunks * E: chunk j of thread t at column (j * 1024 + t) * E, whole
+// chunks as 16-byte accesses, the chunk the row ends in element by element,
+// positions past the row -inf (exp 0) and never stored.
+template <int kIn, int kOut, int kChunks>
+__device__ __forceinline__ void softmax_rows_wide_regs_kernel(const void* x, void* y,
+                                                              int64_t rows, int64_t cols,
+                                                              int64_t ldx, int64_t ldy) {
+  constexpr int kT = 1024;
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  constexpr int kWaves = kT / 64;
+  __shared__ float part[2][kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  TO* yr = static_cast<TO*>(y) + row * ldy;
+  float v[kChunks][kE];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int64_t c0 = ((int64_t)j * kT + t) * kE;
+    if (c0 + kE <= cols) {
+      load_chunk<kIn, kE>(xr + c0, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        v[j][i] = c0 + i < cols ? Elem<kIn>::load1(xr + c0 + i) : -__builtin_inff();
+    }
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) m = fmax_ordered(m, v[j][i]);
+  m = wave_max(m);
+  if (lane == 0) part[0][wave] = m;
+  __syncthreads();
+  m = part[0][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmax_ordered(m, part[0][w]);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      v[j][i] = exp2_fast((v[j][i] - m) * kLog2e);
+      s += v[j][i];
+    }
+  s = wave_sum(s);
+  if (lane == 0) part[1][wave] = s;
+  __syncthreads();
+  s = part[1][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) s += part[1][w];
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int64_t c0 = ((int64_t)j * kT + t) * kE;
+#pragma unroll
+    for (int i = 0; i < kE; ++i) v[j][i] = normalise<kOut>(v[j][i], s, inv);
+    if (c0 + kE <= cols) {
+      store_chunk<kOut, kE>(yr + c0, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        if (c0 + i < cols) Elem<kOut>::store1(yr + c0 + i, v[j][i]);
+    }
+  }
+}
+
+// Rows past 1024 * 8 * E: two passes over the row by one workgroup of 1024
+// threads, 16-byte accesses.  Pass 1 keeps a running (max, sum) per thread
+// (the sum rescaled when the max grows), then the workgroup combines them:
+// M = max of the maxima, S = sum of sum_t * exp(m_t - M).  Pass 2 reads the
+// row again (mostly from L2 / MALL) and writes exp(x - M) / S.  3 row
+// accesses per element instead of 2.
+template <int kIn, int kOut>
+__device__ __forceinline__ void softmax_rows_wide_kernel(const void* x, void* y, int64_t rows,
+                                                         int64_t cols, int64_t ldx,
+                                                         int64_t ldy) {
+  constexpr int kT = 1024;
+  constexpr int kE = chunk_elems<kIn, kOut>();
+  constexpr int kWaves = kT / 64;
+  __shared__ float part[2][kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  using TO = typename Elem<kOut>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  TO* yr = static_cast<TO*>(y) + row * ldy;
+  auto load = [&](int64_t c0, float (&v)[kE]) {
+    if (c0 + kE <= cols) {
+      load_chunk<kIn, kE>(xr + c0, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        v[i] = c0 + i < cols ? Elem<kIn>::load1(xr + c0 + i) : -__builtin_inff();
+    }
+  };
+  float m = -__builtin_inff(), s = 0.0f;
+  for (int64_t c0 = (int64_t)t * kE; c0 < cols; c0 += (int64_t)kT * kE) {
+    float v[kE];
+    load(c0, v);
+    float cm = v[0];
+#pragma unroll
+    for (int i = 1; i < kE; ++i) cm = fmax_ordered(cm, v[i]);
+    const float mn = fmax_ordered(m, cm);
+    if (mn == -__builtin_inff()) continue;   // nothing but -inf so far: s stays 0
+    s = (m == mn ? s : s * exp2_fast((m - mn) * kLog2e));   // m = -inf: s is 0
+#pragma unroll
+    for (int i = 0; i < kE; ++i) s += exp2_fast((v[i] - mn) * kLog2e);
+    m = mn;
+  }
+  float M = wave_max(m);
+  if (lane == 0) part[0][wave] = M;
+  __syncthreads();
+  M = part[0][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmax_ordered(M, part[0][w]);
+  float S = wave_sum(m == -__builtin_inff() ? 0.0f : s * exp2_fast((m - M) * kLog2e));
+  if (lane == 0) part[1][wave] = S;
+  __syncthreads();
+  S = part[1][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) S += part[1][w];
+  const float inv = 1.0f / S;
+  for (int64_t c0 = (int64_t)t * kE; c0 < cols; c0 += (int64_t)kT * kE) {
+    float v[kE];
+    load(c0, v);
+#pragma unroll
+    for (int i = 0; i < kE; ++i) v[i] = normalise<kOut>(exp2_fast((v[i] - M) * kLog2e), S, inv);
+    if (c0 + kE <= cols) {
+      store_chunk<kOut, kE>(yr + c0, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kE; ++i)
+        if (c0 + i < cols) Elem<kOut>::store1(yr + c0 + i, v[i]);
+    }
+  }
+}
+
+#define SILE_SOFTMAX_WIDE_REGS(NAME, IN, OUT, CH)                                              \
+  extern "C" __global__ __launch_bounds__(1024) void NAME(const void* x, void* y, int64_t rows,  \
+                                                          int64_t cols, int64_t ldx, int64_t ldy) { \
+    softmax_rows_wide_regs_kernel<IN, OUT, CH>(x, y, rows, cols, ldx, ldy);                      \
+  }
+#define SILE_SOFTMAX_WIDE_WIDTHS(TAG, IN, OUT)                      \
+  SILE_SOFTMAX_WIDE_REGS(sile_softmax_rows_##TAG##_w2, IN, OUT, 2)   \
+  SILE_SOFTMAX_WIDE_REGS(sile_softmax_rows_##TAG##_w4, IN, OUT, 4)   \
+  SILE_SOFTMAX_WIDE_REGS(sile_softmax_rows_##TAG##_w8, IN, OUT, 8)   \
+  extern "C" __global__ __launch_bounds__(1024) void sile_softmax_rows_##TAG##_wide(          \
+      const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy) {        \
+    softmax_rows_wide_kernel<IN, OUT>(x, y, rows, cols, ldx, ldy);                           \
+  }
+SILE_SOFTMAX_WIDE_WIDTHS(f16_f16, kF16, kF16)
+SILE_SOFTMAX_WIDE_WIDTHS(bf16_bf16, kBF16, kBF16)
+SILE_SOFTMAX_WIDE_WIDTHS(f32_f32, kF32, kF32)
+SILE_SOFTMAX_WIDE_WIDTHS(f16_f32, kF16, kF32)
 
 // ---- row reduce (ReduceMax / ReduceSum along axis 1), fp32 result ----
 // op 0 = max (order-independent, so identical to the reference's fold),

@@ -582,12 +582,41 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
     rc = launch(Module::kSoftmax, name, dim3((unsigned)rows), dim3(block_threads), params, s);
     return rc == SILE_OK ? ok() : rc;
   }
+  // rows of up to 32 chunks: kL lanes per row (the smallest of 4, 8, 16, 32
+  // that covers it), several rows per wave
+  if (vec_ok && cols <= 32 * elems) {
+    int lanes = 4;
+    while ((int64_t)lanes * elems < cols) lanes *= 2;
+    const int64_t per_block = 256 / lanes;
+    if ((rows + per_block - 1) / per_block > 0x7fffffffLL)
+      return fail(SILE_ERR_SHAPE, "too many rows");
+    snprintf(name, sizeof name, "sile_softmax_rows_%s_n%d", tag, lanes);
+    void* params[] = {&x, &y, &rows, &cols, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)((rows + per_block - 1) / per_block)),
+                dim3(256), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
   // other widths up to 8192 (16-bit) / 8192 (fp32): one pass with a masked
   // last chunk, the smallest power-of-two chunk count that covers the row
   int masked = 0;
   if (!chunks && vec_ok) {
     for (int c : {1, 2, 4, 8, 16, 32})
       if (!masked && cols <= (int64_t)c * 64 * elems && (c < 32 || f32_rows)) masked = c;
+  }
+  // wider rows: one row per 1024-thread workgroup, in registers up to
+  // 1024 * 8 chunks, in two passes beyond
+  if (!chunks && !masked && vec_ok) {
+    if (rows > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+    int wide = 0;
+    for (int c : {2, 4, 8})
+      if (!wide && cols <= (int64_t)c * 1024 * elems) wide = c;
+    if (wide)
+      snprintf(name, sizeof name, "sile_softmax_rows_%s_w%d", tag, wide);
+    else
+      snprintf(name, sizeof name, "sile_softmax_rows_%s_wide", tag);
+    void* params[] = {&x, &y, &rows, &cols, &ldx, &ldy};
+    rc = launch(Module::kSoftmax, name, dim3((unsigned)rows), dim3(1024), params, s);
+    return rc == SILE_OK ? ok() : rc;
   }
   if (masked) {
     snprintf(name, sizeof name, "sile_softmax_rows_%s_m%d", tag, masked);

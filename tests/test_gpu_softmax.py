@@ -45,9 +45,14 @@ def test_softmax_f16_config2_full(hip):
     np.testing.assert_array_equal(got.argmax(axis=1), ref.argmax(axis=1))
 
 
-@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 100, 3000, 1, 257, 6100, 8000])
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 100, 3000, 1, 257, 6100, 8000,
+                                  13, 32, 128, 200, 256, 9000, 16384, 20000, 32768, 50000,
+                                  70000])
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32", "f16_f32"])
 def test_softmax_widths_and_types(hip, cols, dt):
+    """Every kernel of the row softmax: kL lanes per row (up to 32 chunks),
+    a wave per row (whole or masked last chunk), a workgroup per row (exact
+    widths, masked up to 1024 x 8 chunks), and two passes beyond."""
     rows = 37
     say(f"softmax {dt} {rows}x{cols}")
     x = (rng(cols).normal(size=(rows, cols)) * 2.0).astype(np.float32)
@@ -70,6 +75,50 @@ def test_softmax_widths_and_types(hip, cols, dt):
     else:
         rtol = 1e-2
         assert_close(got, ref, atol=1e-6, rtol=rtol, what=f"softmax {dt}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+@pytest.mark.parametrize("rows,cols", [(1001, 128), (77, 33), (5, 4), (300, 250)])
+def test_softmax_narrow_rows_many(hip, dt, rows, cols):
+    """Rows of up to 32 chunks share waves (256 / kL rows per workgroup): row
+    counts that leave the last workgroup and wave partly empty, padded
+    leading dimensions, every element against the oracle."""
+    say(f"softmax narrow {dt} {rows}x{cols}")
+    ld = cols + (8 if dt == "f16" else 4) - cols % (8 if dt == "f16" else 4)
+    x = (rng(rows + cols).normal(size=(rows, ld)) * 2.0).astype(np.float32)
+    if dt == "f16":
+        xb, xf = f16_round(x)
+        t = hip.F16
+    else:
+        xb = xf = x
+        t = hip.F32
+    got = _softmax_gpu(hip, xb, t, t, rows, cols, ldx=ld, ldy=ld)
+    ref = cpuref.softmax_rows(np.ascontiguousarray(xf[:, :cols]))
+    if dt == "f32":
+        assert_close(got, ref, atol=1e-30, rtol=1e-4, what="narrow f32")
+    else:
+        assert_close(got, ref, atol=1e-6, rtol=1e-2, what="narrow f16")
+
+
+@pytest.mark.parametrize("cols", [20000, 70000])
+def test_softmax_wide_rows_with_minus_inf(hip, cols):
+    """Wide rows with -inf runs (masked scores): a row whose first 60 % is
+    -inf, a row with one finite entry at its end, a row of -inf save one
+    entry in the middle; the workgroup-per-row kernels (in registers, and
+    the two-pass one with its running max starting at -inf) give exp 0 there
+    and the oracle's values elsewhere."""
+    say(f"softmax f32 wide rows with -inf, cols={cols}")
+    rows = 4
+    x = (rng(cols).normal(size=(rows, cols)) * 2.0).astype(np.float32)
+    x[0, : int(0.6 * cols)] = -np.inf
+    x[1, :-1] = -np.inf
+    x[2, :] = -np.inf
+    x[2, cols // 2] = 3.0
+    got = _softmax_gpu(hip, x, hip.F32, hip.F32, rows, cols)
+    ref = cpuref.softmax_rows(x)
+    assert np.isfinite(got).all()
+    assert got[1, -1] == 1.0 and got[2, cols // 2] == 1.0
+    assert_close(got, ref, atol=1e-30, rtol=1e-4, what="wide -inf")
 
 
 def test_softmax_padded_rows(hip):
