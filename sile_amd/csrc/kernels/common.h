@@ -126,37 +126,59 @@ namespace sched {
 constexpr int kValu = 0x002, kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 }
 
-// Fused load + vec4 sums of rows whose width is a multiple of 4 past 16
-// (the reference's loop form: windows ((v0 + v1) + v2) + v3 added in window
-// order from 0.0f, crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:1182-1256),
-// at HBM rate.  The window sums are independent; only their accumulation is
-// one chain per row.  A workgroup of 256 threads owns kFsRows rows (16-byte
-// aligned) and walks them in chunks of kFsChunk columns: all threads load the
-// chunk with 16-byte loads and write its window sums to LDS `w`
-// (kFsRows * kFsPitch floats), then lane r of wave 0 adds row r's window sums
-// to its running sum in window order, reading them four at a time (row pitch
-// kFsWin + 4 floats: 16-byte aligned, rows 4 banks apart).  Several
-// workgroups per CU overlap one's chains with another's loads.  Returns the
-// sum of row row0 + tid for tid < nrows (0.0f elsewhere).
+// Fused load + vec4 sums of rows wider than 16 in the reference's loop form
+// (windows ((v0 + v1) + v2) + v3 from 0.0f while idx < cols, added in window
+// order, crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:1182-1256;
+// then, for cols % 4 != 0, a scalar tail from 4 * (cols / 4) that re-adds
+// the row's elements of the last window), at HBM rate.  The window sums are
+// independent; only their accumulation is one chain per row.  A workgroup
+// of 256 threads owns kFsRows rows and walks them kFsWin windows at a time:
+// all threads form the next block's window sums into one half of LDS `w`
+// (2 * kFsRows * kFsPitch floats) while lane r of wave 0 adds row r's window
+// sums of the current block, from the other half, to its running sum in
+// window order, four per LDS read (row pitch kFsWin + 4 floats: 16-byte
+// aligned, rows 4 banks apart).  kAny = false: cols % 4 == 0 and 16-byte
+// aligned rows, 16-byte loads; kAny = true: any cols, ldx and alignment,
+// element loads, window elements at or past x_len (the buffer's end) taken
+// as 0.0f, where the reference reads past its buffer (a last window past the
+// row reads the next elements of the buffer, as the reference's does).
+// Returns the sum of row row0 + tid for tid < nrows (0.0f elsewhere).
 constexpr int kFsRows = 4;
-constexpr int kFsChunk = 1024;                  // columns per chunk
-constexpr int kFsWin = kFsChunk / 4;            // windows per row and chunk
+constexpr int kFsWin = 256;                     // windows per row and block
 constexpr int kFsPitch = kFsWin + 4;            // LDS floats per row
+constexpr int kFsLds = 2 * kFsRows * kFsPitch;  // floats of `w`
+template <bool kAny>
 SILE_DEV float fused_sum_rows_tiled(const float* __restrict__ x, int64_t cols, int64_t ldx,
-                                    int64_t row0, int nrows, float* w) {
+                                    int64_t x_len, int64_t row0, int nrows, float* w) {
 #pragma clang fp contract(off)
   const int tid = threadIdx.x;
-  float acc = 0.0f;
-  for (int64_t c0 = 0; c0 < cols; c0 += kFsChunk) {
-    const int win = (int)((cols - c0) / 4 < kFsWin ? (cols - c0) / 4 : kFsWin);
+  const int64_t nwin = kAny ? (cols + 3) / 4 : cols / 4;
+  // window sums of windows [wb, wb + kFsWin) of each row into buf
+  auto fill = [&](int64_t wb, float* buf) {
+    const int win = (int)(nwin - wb < kFsWin ? nwin - wb : kFsWin);
     for (int e = tid; e < nrows * win; e += 256) {
       const int r = e / win, i = e - r * win;
-      const f32x4 v = *reinterpret_cast<const f32x4*>(x + (row0 + r) * ldx + c0 + 4 * i);
-      w[r * kFsPitch + i] = ((v[0] + v[1]) + v[2]) + v[3];
+      const int64_t base = (row0 + r) * ldx + 4 * (wb + i);
+      float v[4];
+      if constexpr (kAny) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = base + j < x_len ? x[base + j] : 0.0f;
+      } else {
+        const f32x4 q = *reinterpret_cast<const f32x4*>(x + base);
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+      }
+      buf[r * kFsPitch + i] = ((v[0] + v[1]) + v[2]) + v[3];
     }
-    __syncthreads();
+  };
+  float acc = 0.0f;
+  fill(0, w);
+  __syncthreads();
+  int k = 0;
+  for (int64_t wb = 0; wb < nwin; wb += kFsWin, ++k) {
+    if (wb + kFsWin < nwin) fill(wb + kFsWin, w + ((k + 1) & 1) * kFsRows * kFsPitch);
     if (tid < nrows) {
-      const float* wr = w + tid * kFsPitch;
+      const float* wr = w + (k & 1) * kFsRows * kFsPitch + tid * kFsPitch;
+      const int win = (int)(nwin - wb < kFsWin ? nwin - wb : kFsWin);
       const int win4 = win & ~3;
 #pragma unroll 4
       for (int i = 0; i < win4; i += 4) {
@@ -169,6 +191,10 @@ SILE_DEV float fused_sum_rows_tiled(const float* __restrict__ x, int64_t cols, i
       for (int i = win4; i < win; ++i) acc = acc + wr[i];
     }
     __syncthreads();
+  }
+  if constexpr (kAny) {
+    if (tid < nrows)
+      for (int64_t c = (cols / 4) * 4; c < cols; ++c) acc = acc + x[(row0 + tid) * ldx + c];
   }
   return acc;
 }

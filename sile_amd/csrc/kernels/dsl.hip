@@ -115,10 +115,26 @@ struct ReduceTileArgs {
 extern "C" __global__ __launch_bounds__(256) void sile_dsl_parallel_reduce_f32_tiled(
     const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
     int64_t programs, int64_t tile) {
-  __shared__ __attribute__((aligned(16))) float w[kFsRows * kFsPitch];
+  __shared__ __attribute__((aligned(16))) float w[kFsLds];
   const int64_t pid0 = (int64_t)blockIdx.x * kFsRows;
   const int nprog = (int)min((int64_t)kFsRows, programs - pid0);
-  const float acc = fused_sum_rows_tiled(a, tile, tile, pid0, nprog, w);
+  const float acc = fused_sum_rows_tiled<false>(a, tile, tile, 0, pid0, nprog, w);
+  if ((int)threadIdx.x < nprog) {
+    if (partials) partials[pid0 + threadIdx.x] = acc;
+    atomicAdd(out, acc);
+  }
+}
+
+// TILE > 16 otherwise (a ragged last window, read past the tile as the
+// reference does, then the scalar tail; elements past len taken as 0.0f):
+// the same windows and order through fused_sum_rows_tiled<true>.
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_parallel_reduce_f32_tiled_any(
+    const float* __restrict__ a, float* __restrict__ out, float* __restrict__ partials,
+    int64_t programs, int64_t tile, int64_t len) {
+  __shared__ __attribute__((aligned(16))) float w[kFsLds];
+  const int64_t pid0 = (int64_t)blockIdx.x * kFsRows;
+  const int nprog = (int)min((int64_t)kFsRows, programs - pid0);
+  const float acc = fused_sum_rows_tiled<true>(a, tile, tile, len, pid0, nprog, w);
   if ((int)threadIdx.x < nprog) {
     if (partials) partials[pid0 + threadIdx.x] = acc;
     atomicAdd(out, acc);

@@ -662,6 +662,97 @@ __device__ __forceinline__ void reduce_rows_kernel(int op, int vec, const void* 
   if (lane == 0) out[row] = acc;
 }
 
+// Narrow rows (up to 32 chunks): kL lanes per row, one chunk per lane, 64 /
+// kL rows per wave; rows of 16-byte aligned chunks only.
+template <int kIn, int kL>
+__device__ __forceinline__ void reduce_rows_narrow_kernel(int op, const void* x, float* out,
+                                                          int64_t rows, int64_t cols,
+                                                          int64_t ldx) {
+  constexpr int kE = chunk_elems<kIn, kF32>();
+  const int lane = threadIdx.x & 63, li = lane % kL;
+  const int64_t row = (int64_t)blockIdx.x * (256 / kL) + (threadIdx.x >> 6) * (64 / kL) + lane / kL;
+  const bool live = row < rows;
+  using TI = typename Elem<kIn>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + (live ? row : 0) * ldx;
+  const int c0 = li * kE;
+  float acc = op == 0 ? -__builtin_inff() : 0.0f;
+  if (live && c0 + kE <= cols) {
+    float v[kE];
+    load_chunk<kIn, kE>(xr + c0, v);
+#pragma unroll
+    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+  } else if (live) {
+    for (int i = 0; c0 + i < cols && i < kE; ++i) {
+      const float v = Elem<kIn>::load1(xr + c0 + i);
+      acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
+    }
+  }
+  acc = op == 0 ? group_max<kL>(acc) : group_sum<kL>(acc);
+  if (live && li == 0) out[row] = acc;
+}
+
+// Wide rows, few of them: one row per workgroup of 1024 threads, 16-byte
+// chunks strided by the workgroup, wave all-reductions plus one exchange of
+// the per-wave partials through LDS.
+template <int kIn>
+__device__ __forceinline__ void reduce_rows_block_kernel(int op, const void* x, float* out,
+                                                         int64_t rows, int64_t cols,
+                                                         int64_t ldx) {
+  constexpr int kT = 1024;
+  constexpr int kE = chunk_elems<kIn, kF32>();
+  __shared__ float part[kT / 64];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  float acc = op == 0 ? -__builtin_inff() : 0.0f;
+  const int64_t vec_cols = cols & ~(int64_t)(kE - 1);
+  for (int64_t c = (int64_t)t * kE; c < vec_cols; c += (int64_t)kT * kE) {
+    float v[kE];
+    load_chunk<kIn, kE>(xr + c, v);
+#pragma unroll
+    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+  }
+  for (int64_t c = vec_cols + t; c < cols; c += kT) {
+    const float v = Elem<kIn>::load1(xr + c);
+    acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
+  }
+  acc = op == 0 ? wave_max(acc) : wave_sum(acc);
+  if (lane == 0) part[wave] = acc;
+  __syncthreads();
+  if (t == 0) {
+    float r = part[0];
+    for (int w = 1; w < kT / 64; ++w) r = op == 0 ? fmax_ordered(r, part[w]) : r + part[w];
+    out[row] = r;
+  }
+}
+
+#define SILE_REDUCE_SHAPES(TAG, IN)                                                           \
+  extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_n4(              \
+      int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
+    reduce_rows_narrow_kernel<IN, 4>(op, x, out, rows, cols, ldx);                          \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_n8(              \
+      int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
+    reduce_rows_narrow_kernel<IN, 8>(op, x, out, rows, cols, ldx);                          \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_n16(             \
+      int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
+    reduce_rows_narrow_kernel<IN, 16>(op, x, out, rows, cols, ldx);                         \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_n32(             \
+      int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
+    reduce_rows_narrow_kernel<IN, 32>(op, x, out, rows, cols, ldx);                         \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(1024) void sile_reduce_rows_##TAG##_block(          \
+      int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
+    reduce_rows_block_kernel<IN>(op, x, out, rows, cols, ldx);                              \
+  }
+SILE_REDUCE_SHAPES(f32, kF32)
+SILE_REDUCE_SHAPES(f16, kF16)
+SILE_REDUCE_SHAPES(bf16, kBF16)
+
 extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_f32(int op, int vec, const void* x,
                                                                        float* out, int64_t rows,
                                                                        int64_t cols, int64_t ldx) {
@@ -726,16 +817,25 @@ extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32
   out[row] = acc;
 }
 
-// The same sums for cols > 16 with cols % 4 == 0 and 16-byte aligned rows
-// (no window runs past a row, no tail), at HBM rate (fused_sum_rows_tiled):
-// same arithmetic, same order as sile_reduce_rows_fused_sum_f32, so
-// bit-identical to it.
+// The same sums for cols > 16 at HBM rate (fused_sum_rows_tiled): the same
+// arithmetic in the same order as sile_reduce_rows_fused_sum_f32, so
+// bit-identical to it; _tiled for cols % 4 == 0 and 16-byte aligned rows
+// (16-byte loads), _tiled_any for any cols, pitch and alignment.
 extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32_tiled(
     const float* __restrict__ x, float* __restrict__ out, int64_t rows, int64_t cols, int64_t ldx) {
-  __shared__ __attribute__((aligned(16))) float w[kFsRows * kFsPitch];
+  __shared__ __attribute__((aligned(16))) float w[kFsLds];
   const int64_t row0 = (int64_t)blockIdx.x * kFsRows;
   const int nrows = (int)min((int64_t)kFsRows, rows - row0);
-  const float acc = fused_sum_rows_tiled(x, cols, ldx, row0, nrows, w);
+  const float acc = fused_sum_rows_tiled<false>(x, cols, ldx, 0, row0, nrows, w);
+  if ((int)threadIdx.x < nrows) out[row0 + threadIdx.x] = acc;
+}
+extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_fused_sum_f32_tiled_any(
+    const float* __restrict__ x, float* __restrict__ out, int64_t rows, int64_t cols, int64_t ldx,
+    int64_t x_len) {
+  __shared__ __attribute__((aligned(16))) float w[kFsLds];
+  const int64_t row0 = (int64_t)blockIdx.x * kFsRows;
+  const int nrows = (int)min((int64_t)kFsRows, rows - row0);
+  const float acc = fused_sum_rows_tiled<true>(x, cols, ldx, x_len, row0, nrows, w);
   if ((int)threadIdx.x < nrows) out[row0 + threadIdx.x] = acc;
 }
 

@@ -294,6 +294,12 @@ int sile_hip_kernel_parallel_reduce(void* const* buffers, int64_t num_threadgrou
     void* params[] = {&a, &out, &partials, &run, &tile};
     rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32_tiled", dim3((unsigned)((run + 3) / 4)),
                 dim3(256), params, s);
+  } else if (tile > 16) {
+    // any other TILE past 16: the same windows with element loads
+    int64_t len_ = len;
+    void* params[] = {&a, &out, &partials, &run, &tile, &len_};
+    rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32_tiled_any",
+                dim3((unsigned)((run + 3) / 4)), dim3(256), params, s);
   } else {
     void* params[] = {&a, &out, &partials, &t};
     rc = launch(Module::kDsl, "sile_dsl_parallel_reduce_f32", dim3((unsigned)run), dim3(64),
@@ -652,12 +658,32 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
   int iop = (int)op;
-  // The 128-bit path needs every row start 16-byte aligned; otherwise the
-  // kernel runs its scalar loop only.
+  // The 128-bit paths need every row start 16-byte aligned; otherwise the
+  // wave-per-row kernel runs its scalar loop only.
   int vec = aligned16(x) && (ldx * (int64_t)dtype_bytes(in_type)) % 16 == 0 ? 1 : 0;
+  const int64_t elems = in_type == SILE_F32 ? 4 : 8;   // per 16-byte chunk
+  char kname[64];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vec && cols <= 32 * elems) {
+    // up to 32 chunks: kL lanes per row, several rows per wave
+    int lanes = 4;
+    while ((int64_t)lanes * elems < cols) lanes *= 2;
+    const int64_t per_block = 256 / lanes;
+    snprintf(kname, sizeof kname, "%s_n%d", name, lanes);
+    void* params[] = {&iop, &x, &out, &rows, &cols, &ldx};
+    int rc = launch(Module::kSoftmax, kname, dim3((unsigned)((rows + per_block - 1) / per_block)),
+                    dim3(256), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+  if (vec && cols >= 16384 && rows <= 4096) {
+    // few wide rows: a 1024-thread workgroup per row
+    snprintf(kname, sizeof kname, "%s_block", name);
+    void* params[] = {&iop, &x, &out, &rows, &cols, &ldx};
+    int rc = launch(Module::kSoftmax, kname, dim3((unsigned)rows), dim3(1024), params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
   void* params[] = {&iop, &vec, &x, &out, &rows, &cols, &ldx};
-  int rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params,
-                  static_cast<hipStream_t>(stream));
+  int rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
   return rc == SILE_OK ? ok() : rc;
 }
 
@@ -708,6 +734,16 @@ int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float* x, i
     if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
     void* params[] = {(void*)&x, &out, &rows, &cols, &ldx};
     int rc = launch(Module::kSoftmax, "sile_reduce_rows_fused_sum_f32_tiled",
+                    dim3((unsigned)blocks), dim3(256), params, static_cast<hipStream_t>(stream));
+    return rc == SILE_OK ? ok() : rc;
+  }
+  if (cols > 16) {
+    // any pitch / alignment / width: element loads, windows past a row read
+    // the buffer's next elements (zero past x_len), then the scalar tail
+    const int64_t blocks = (rows + 3) / 4;
+    if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+    void* params[] = {(void*)&x, &out, &rows, &cols, &ldx, &x_len};
+    int rc = launch(Module::kSoftmax, "sile_reduce_rows_fused_sum_f32_tiled_any",
                     dim3((unsigned)blocks), dim3(256), params, static_cast<hipStream_t>(stream));
     return rc == SILE_OK ? ok() : rc;
   }

@@ -151,7 +151,8 @@ def test_parallel_reduce_ones_closed_form(hip, tile):
 
 
 @pytest.mark.parametrize("tile,pad", [(3, 5), (12, 5), (16, 5), (1000, 5), (1003, 5), (1003, 0),
-                                      (17, 0), (17, 2), (20, 0), (2052, 3), (4096, 0)])
+                                      (17, 0), (17, 2), (20, 0), (2052, 3), (4096, 0), (5003, 1),
+                                      (5003, 0)])
 def test_parallel_reduce_partials_random(hip, tile, pad):
     """pad = elements of a past the last tile: the last program's final
     window reads them (pad >= 4 - TILE % 4) or runs past a."""

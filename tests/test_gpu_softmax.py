@@ -145,8 +145,12 @@ def test_softmax_extremes(hip):
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
-@pytest.mark.parametrize("cols", [8192, 1000, 13])
+@pytest.mark.parametrize("cols", [8192, 1000, 13, 4, 100, 256, 16384, 65537])
 def test_reduce_rows(hip, dt, cols):
+    """Row max (bit-identical: order-independent) and row sum (within
+    1e-5 of the row's absolute sum) for every kernel: kL lanes per row up to
+    32 chunks, a wave per row, a 1024-thread workgroup per row for few wide
+    rows (16384, and 65537 with a ragged end)."""
     rows = 41
     say(f"reduce_rows {dt} {rows}x{cols}")
     x = rng(cols + 1).normal(size=(rows, cols)).astype(np.float32) * 3
@@ -219,13 +223,17 @@ def test_softmax_masked_tail_padded(hip, dt, cols):
 
 @pytest.mark.parametrize("rows,cols,ldx", [(33, 20, 20), (100, 1000, 1000), (64, 1024, 1028),
                                            (31, 4100, 4100), (70, 8192, 8192), (5, 12288, 12300),
-                                           (40, 18, 18), (9, 1003, 1003), (7, 16, 16), (3, 3, 3)])
+                                           (40, 18, 18), (9, 1003, 1003), (7, 16, 16), (3, 3, 3),
+                                           (8, 8190, 8190), (4, 65537, 65537), (3, 600, 603),
+                                           (1, 17, 17), (6, 2049, 2051)])
 def test_reduce_rows_fused_sum_bit_exact(hip, rows, cols, ldx):
     """sile_hip_reduce_rows_fused_sum against the oracle's fused vec4 order,
-    bit for bit: aligned rows of a multiple of 4 past 16 columns run the
-    chunked kernel (window sums in parallel, one chain per row; chunks of
-    1024 columns, ragged last chunk, row pitch past cols, rows not a multiple
-    of 32), the others the one-lane-per-row kernel."""
+    bit for bit: rows past 16 columns run the chunked kernel (window sums in
+    parallel, one chain per row; blocks of 256 windows double-buffered,
+    ragged last block, row pitch past cols, rows not a multiple of 4; with
+    16-byte loads for aligned multiples of 4, element loads otherwise, the
+    last window reading the next row's first elements and the last row's
+    running past the buffer), rows of up to 16 the one-lane-per-row kernel."""
     say(f"fused row sum {rows}x{cols} ldx={ldx}")
     x = rng(rows * cols).normal(size=(rows, ldx)).astype(np.float32) * np.float32(3.0)
     x[:, :cols:7] = -0.0
