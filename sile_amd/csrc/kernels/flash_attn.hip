@@ -112,14 +112,19 @@ SILE_DEV float pair_sum(uint32_t pk, float acc) {
                                   false);
 }
 
-// LDS bytes of the two stages (K and V tiles of kNK keys of head_dim kDh each)
-template <int kNK, int kDh>
-constexpr int lds_bytes() { return 2 * 2 * kNK * 2 * kDh; }
+// LDS bytes of the two stages (K and V tiles of kNK keys, rows of kDp
+// 16-bit elements each)
+template <int kNK, int kDp>
+constexpr int lds_bytes() { return 2 * 2 * kNK * 2 * kDp; }
 
 // kQT 32-query tiles per wave, kW waves per workgroup: kW * kQT * 32 queries
 // per workgroup (256 for every instantiation); kNK keys per block (32 or 64),
 // i.e. kST = kNK / 32 S tiles of 32 keys x 32 queries per query tile.
-template <bool kBF16, int kQT, int kW, int kNK, int kDh>
+// kDh: the head dimension (a multiple of 16); kDp: the LDS row length (64,
+// 128 or 256 elements, at least kDh): the chunks of a row past kDh are
+// loaded as zeros (outside the buffer resources), so the products over them
+// add nothing and the O^T rows past kDh are zero and not stored.
+template <bool kBF16, int kQT, int kW, int kNK, int kDh, int kDp>
 __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
@@ -127,12 +132,15 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
                                             uint8_t* smem) {
   constexpr int kBQ = kW * kQT * 32;
   constexpr int kST = kNK / 32;
-  constexpr int kRow = 2 * kDh;          // bytes of a K or V row
-  constexpr int kChunks = kRow / 16;     // 16-byte chunks per row
+  constexpr int kRow = 2 * kDp;          // bytes of a K or V row in LDS
+  constexpr int kRowG = 2 * kDh;         // bytes of a K or V row in HBM
+  constexpr int kChunks = kRow / 16;     // 16-byte chunks per LDS row
+  constexpr int kChunksG = kRowG / 16;   // of them holding data
   constexpr int kKK = kDh / 16;          // d-steps of S^T = K . Q^T
-  constexpr int kDT = kDh / 32;          // 32-d tiles of O^T
+  constexpr int kDT = (kDh + 31) / 32;   // 32-d tiles of O^T
   constexpr int kDmaRows = 1024 / kRow;  // rows one 1 KiB DMA instruction fills
-  static_assert(kDh == 64 || kDh == 128, "head_dim 64 or 128");
+  static_assert(kDh % 16 == 0 && kDh <= kDp && (kDp == 64 || kDp == 128 || kDp == 256),
+                "head_dim a multiple of 16 up to the LDS row");
   constexpr int kTileB = kNK * kRow;     // one K or V tile
   constexpr int kStageB = 2 * kTileB;    // K + V
   constexpr int kDmaPerWave = kTileB / 1024 / kW;  // 1 KiB DMA instructions per wave per tile
@@ -160,13 +168,13 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   const int qb_second = a.pair ? u : qb_first;
   const int64_t S = a.seq;
   const int64_t head_off = (int64_t)bh * S * kDh;
-  // K: chunk c of row r at c ^ kswz(r); V: at c ^ vswz(r).  With 256-byte
-  // rows (kDh = 128) a row spans every bank and r & 15 separates 16 rows;
+  // K: chunk c of row r at c ^ kswz(r); V: at c ^ vswz(r).  With rows of
+  // 256 bytes or more a row spans every bank and r & 15 separates 16 rows;
   // with 128-byte rows two rows share the banks, so (r >> 1) & 7 separates
   // the 8 pairs.  V's swizzle puts the four keys of a transposing read on
   // distinct banks.
-  auto kswz = [](int r) { return kChunks == 16 ? (r & 15) : ((r >> 1) & 7); };
-  auto vswz = [](int r) { return (kChunks / 4) * (r & 3); };
+  auto kswz = [](int r) { return kChunks == 8 ? ((r >> 1) & 7) : (r & 15); };
+  auto vswz = [](int r) { return (kChunks == 8 ? 2 : 4) * (r & 3); };
 
   for (int pass = 0; pass < (qb_second == qb_first ? 1 : 2); ++pass) {
     const int qb = pass ? qb_second : qb_first;
@@ -188,12 +196,20 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       for (int kk = 0; kk < kKK; ++kk) qf[qt][kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk);
     }
 
-    // ---- LDS-DMA addressing: wave w's instruction i fills rows
-    // kDmaRows (w + kW i) + lane / kChunks (the swizzles are the same for every i) ----
-    const int dma_row = kDmaRows * wave + lane / kChunks, dma_pos = lane % kChunks;
-    const int k_voff = dma_row * kRow + ((dma_pos ^ kswz(dma_row)) << 4);
-    const int v_voff = dma_row * kRow + ((dma_pos ^ vswz(dma_row)) << 4);
-    const int kv_bytes = (int)(S * kRow);
+    // ---- LDS-DMA addressing: wave w's instruction i fills LDS rows
+    // kDmaRows (w + kW i) + lane / kChunks; lane l writes slot l % kChunks of
+    // its row, so it fetches the HBM chunk that belongs there under the
+    // swizzle, or, for a chunk past the row's data, an offset past the
+    // buffer (zeros) ----
+    const int kv_bytes = (int)(S * kRowG);
+    int k_voff[kDmaPerWave], v_voff[kDmaPerWave];
+  #pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const int row = kDmaRows * (wave + kW * i) + lane / kChunks, pos = lane % kChunks;
+      const int kc = pos ^ kswz(row), vc = pos ^ vswz(row);
+      k_voff[i] = kc < kChunksG ? row * kRowG + kc * 16 : kv_bytes;
+      v_voff[i] = vc < kChunksG ? row * kRowG + vc * 16 : kv_bytes;
+    }
     const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(K + head_off), (short)0, kv_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -203,14 +219,14 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
-                                                 k_voff, (blk * kNK + kDmaRows * kW * i) * kRow, 0, 0);
+                                                 k_voff[i], blk * kNK * kRowG, 0, 0);
     };
     auto dma_v = [&](int blk, int stage) {
       uint8_t* base = smem + stage * kStageB + kTileB + wave * 1024;
   #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rsrc, (lds_ptr_t)(base + i * kW * 1024), 16,
-                                                 v_voff, (blk * kNK + kDmaRows * kW * i) * kRow, 0, 0);
+                                                 v_voff[i], blk * kNK * kRowG, 0, 0);
     };
 
     // ---- fragment reads ----
@@ -268,7 +284,8 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 
     // S_{j+1} over (S tile, d-step) and PV_{j-1} over (d-tile, key chunk), one
     // step of each at a time: S step (st, kk) runs at step kKK st + kk, PV
-    // (dt, cc) at step dt + kDT cc (kST kKK = 2 kST kDT steps of each)
+    // (dt, cc) at step dt + kDT cc (kST kKK and 2 kST kDT steps: equal
+    // unless kDh % 32 == 16)
     auto mma_block = [&](int kstage, int vstage, f32x16 (&sacc)[kQT][kST],
                          const u32x4 (&pf)[kQT][2 * kST], f32x16 (&oa)[kQT][kDT]) {
       const uint8_t* ks = smem + kstage * kStageB + kf_off;
@@ -279,16 +296,21 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
         for (int st = 0; st < kST; ++st)
   #pragma unroll
           for (int i = 0; i < 16; ++i) sacc[qt][st][i] = 0.0f;
+      constexpr int kSSteps = kKK * kST, kPSteps = 2 * kDT * kST;
   #pragma unroll
-      for (int step = 0; step < kKK * kST; ++step) {
-        const int st = step / kKK, kk = step % kKK;
-        const u32x4 kf = k_frag(ks, st, kk);
-        const int dt = step % kDT, cc = step / kDT;
-        const u32x4 vf = v_frag(vs, dt, cc);
+      for (int step = 0; step < (kSSteps > kPSteps ? kSSteps : kPSteps); ++step) {
+        if (step < kSSteps) {
+          const int st = step / kKK, kk = step % kKK;
+          const u32x4 kf = k_frag(ks, st, kk);
   #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
+          for (int qt = 0; qt < kQT; ++qt) sacc[qt][st] = mma32<kBF16>(kf, qf[qt][kk], sacc[qt][st]);
+        }
+        if (step < kPSteps) {
+          const int dt = step % kDT, cc = step / kDT;
+          const u32x4 vf = v_frag(vs, dt, cc);
   #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
+          for (int qt = 0; qt < kQT; ++qt) oa[qt][dt] = mma32<kBF16>(vf, pf[qt][cc], oa[qt][dt]);
+        }
       }
     };
 
@@ -489,6 +511,7 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
   #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int d = 32 * dt + 8 * r + 4 * g;
+          if (d >= kDh) continue;   // O^T rows past the head dimension (zero)
           const f32x16& acc = oacc[qt][dt];
           const u32x2 w = {pack2<kBF16>(acc[4 * r] * inv, acc[4 * r + 1] * inv),
                            pack2<kBF16>(acc[4 * r + 2] * inv, acc[4 * r + 3] * inv)};
@@ -500,15 +523,24 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 
 }  // namespace v2
 
-#define SILE_FA_V2_KERNEL(NAME, BF, QT, W, NK, DH)                                            \
+#define SILE_FA_V2_KERNEL(NAME, BF, QT, W, NK, DH, DP)                                        \
   extern "C" __global__ __launch_bounds__(W * 64, 1) void NAME(                               \
       const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O, AttnArgs a) {     \
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::lds_bytes<NK, DH>()];          \
-    v2::attn_fwd_v2<BF, QT, W, NK, DH>(Q, K, V, O, a, smem);                                  \
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[v2::lds_bytes<NK, DP>()];          \
+    v2::attn_fwd_v2<BF, QT, W, NK, DH, DP>(Q, K, V, O, a, smem);                              \
   }
-// 8 waves x 32 queries (two waves per SIMD): head_dim 128 over 32-key blocks,
-// head_dim 64 over 64-key blocks (the same LDS bytes and MFMAs per block)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8, false, 1, 8, 32, 128)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8, true, 1, 8, 32, 128)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_v2w8_d64, false, 1, 8, 64, 64)
-SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_v2w8_d64, true, 1, 8, 64, 64)
+// 8 waves x 32 queries (two waves per SIMD) for head_dim up to 128: 32-key
+// blocks over 256-byte LDS rows, 64-key blocks over 128-byte rows (the same
+// LDS bytes and MFMAs per block); 4 waves (one per SIMD, room for the O
+// accumulators) over 512-byte rows for head_dim up to 256.
+#define SILE_FA_V2_DTYPES(SUFFIX, W, NK, DH, DP)                                              \
+  SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_##SUFFIX, false, 1, W, NK, DH, DP)                  \
+  SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_##SUFFIX, true, 1, W, NK, DH, DP)
+SILE_FA_V2_DTYPES(v2w8, 8, 32, 128, 128)
+SILE_FA_V2_DTYPES(v2w8_d64, 8, 64, 64, 64)
+SILE_FA_V2_DTYPES(v2w8_d32, 8, 64, 32, 64)
+SILE_FA_V2_DTYPES(v2w8_d80, 8, 32, 80, 128)
+SILE_FA_V2_DTYPES(v2w8_d96, 8, 32, 96, 128)
+SILE_FA_V2_DTYPES(v2w4_d160, 4, 32, 160, 256)
+SILE_FA_V2_DTYPES(v2w4_d192, 4, 32, 192, 256)
+SILE_FA_V2_DTYPES(v2w4_d256, 4, 32, 256, 256)

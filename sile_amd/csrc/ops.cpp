@@ -777,14 +777,27 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   if (seq_len * head_dim * 2 > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "sequence too long for one head (S=%lld)", (long long)seq_len);
 
-  // MFMA flash kernel, 16-byte aligned operands, head_dim 128 or 64, any S:
-  //   the pipelined kernel (8 waves x 32 queries, 32-key (head_dim 128) or
-  //   64-key (head_dim 64) blocks through LDS-DMA; causal query blocks taken
-  //   in balanced pairs; keys and queries past S masked).
+  // MFMA flash kernel, 16-byte aligned operands, any S: the pipelined kernel
+  // (32-query waves, key blocks through LDS-DMA; causal query blocks taken
+  // in balanced pairs; keys and queries past S masked), one instantiation
+  // per head dimension: 8 waves for head_dim up to 128 (32-key blocks, or
+  // 64-key blocks over 128-byte rows for 32 and 64), 4 waves for 160 to 256.
+  struct FaShape {
+    int64_t d;
+    const char* suffix;
+    int waves;
+  };
+  static const FaShape kFaShapes[] = {{32, "v2w8_d32", 8},   {64, "v2w8_d64", 8},
+                                      {80, "v2w8_d80", 8},   {96, "v2w8_d96", 8},
+                                      {128, "v2w8", 8},      {160, "v2w4_d160", 4},
+                                      {192, "v2w4_d192", 4}, {256, "v2w4_d256", 4}};
+  const FaShape* fs = nullptr;
+  for (const FaShape& f : kFaShapes)
+    if (f.d == head_dim) fs = &f;
   const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  if ((head_dim == 128 || head_dim == 64) && aligned) {
+  if (fs && aligned) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const int64_t bq = 256;
+    const int64_t bq = 32 * fs->waves;
     const bool pair = causal;
     const int64_t q_blocks = (seq_len + bq - 1) / bq;
     if (q_blocks > 0x7fffffffLL / std::max<int64_t>(bh, 1))
@@ -799,9 +812,8 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const int64_t units = pair ? (q_blocks + 1) / 2 : q_blocks;
     const int64_t blocks = bh * units;
     char name[64];
-    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_v2w8%s", dt,
-             head_dim == 64 ? "_d64" : "");
-    const unsigned threads = 512;
+    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, fs->suffix);
+    const unsigned threads = 64 * fs->waves;
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(threads), params, s);
     return rc == SILE_OK ? ok() : rc;

@@ -243,3 +243,25 @@ def test_flash_any_seq_len_writes_nothing_past_o(hip):
     raw = do.download(np.uint16, (n + 4096,))
     assert (raw[n:] == 0xFFFF).all()
     assert np.isfinite(raw[:n].view(np.float16)).all()
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d", [32, 80, 96, 160, 192, 256])
+@pytest.mark.parametrize("s", [100, 384, 1000])
+def test_flash_other_head_dims(hip, dt, causal, d, s):
+    """Head dimensions past the benchmarked 128 and 64 on the same pipelined
+    kernel: 32 (128-byte LDS rows, half of each row zero), 80 and 96 (256-byte
+    rows, 80 with an O^T tile half past the head dimension), 160, 192 and 256
+    (512-byte rows, 4 waves); B = 1, H = 8 (head-per-XCD order), every head
+    and query against the fp32 oracle."""
+    b, h = 1, 8
+    say(f"flash D={d} {dt} causal={causal} S={s}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, dt, seed=61 + d)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
+    assert np.isfinite(got).all()
+    qf, kf, vf = (x[1] for x in qkv)
+    for hi in range(h):
+        ref = cpuref.attention_fwd(qf[0, hi], kf[0, hi], vf[0, hi], scale, causal=causal)
+        assert_close(got[0, hi], ref, atol=ATOL, rtol=RTOL, what=f"D={d} h{hi}")
