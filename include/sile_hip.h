@@ -348,9 +348,9 @@ int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float *x, i
 
 /* Flash-attention forward, O = softmax(Q K^T * scale [+ causal mask]) V with
  * fp32 online-softmax state.  Q, K, V, O are [B, H, S, D] contiguous, f16 or
- * bf16, any S.  D = 32, 64, 80, 96, 128, 160, 192 or 256 with 16-byte
- * aligned operands run on the matrix cores; other D up to 256 (or unaligned
- * operands) on a VALU kernel of one wave per query row.  No reference counterpart: sile's DSL
+ * bf16, any S.  D a multiple of 16 up to 256 with 16-byte aligned operands
+ * runs on the matrix cores; other D up to 256 (or unaligned operands) on a
+ * VALU kernel of one wave per query row.  No reference counterpart: sile's DSL
  * cannot express attention (no mask/iota/transpose); built from the Tile IR
  * ops MmaF, ReduceMax, Exp, ReduceSum (crates/sile-tile-ir/src/ir.rs:128-262). */
 int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int64_t seq_len,

@@ -536,11 +536,20 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
 #define SILE_FA_V2_DTYPES(SUFFIX, W, NK, DH, DP)                                              \
   SILE_FA_V2_KERNEL(sile_flash_attn_fwd_f16_##SUFFIX, false, 1, W, NK, DH, DP)                  \
   SILE_FA_V2_KERNEL(sile_flash_attn_fwd_bf16_##SUFFIX, true, 1, W, NK, DH, DP)
-SILE_FA_V2_DTYPES(v2w8, 8, 32, 128, 128)
-SILE_FA_V2_DTYPES(v2w8_d64, 8, 64, 64, 64)
+// every head dimension that is a multiple of 16 from 16 to 256
+SILE_FA_V2_DTYPES(v2w8_d16, 8, 64, 16, 64)
 SILE_FA_V2_DTYPES(v2w8_d32, 8, 64, 32, 64)
+SILE_FA_V2_DTYPES(v2w8_d48, 8, 64, 48, 64)
+SILE_FA_V2_DTYPES(v2w8_d64, 8, 64, 64, 64)
 SILE_FA_V2_DTYPES(v2w8_d80, 8, 32, 80, 128)
 SILE_FA_V2_DTYPES(v2w8_d96, 8, 32, 96, 128)
+SILE_FA_V2_DTYPES(v2w8_d112, 8, 32, 112, 128)
+SILE_FA_V2_DTYPES(v2w8, 8, 32, 128, 128)
+SILE_FA_V2_DTYPES(v2w4_d144, 4, 32, 144, 256)
 SILE_FA_V2_DTYPES(v2w4_d160, 4, 32, 160, 256)
+SILE_FA_V2_DTYPES(v2w4_d176, 4, 32, 176, 256)
 SILE_FA_V2_DTYPES(v2w4_d192, 4, 32, 192, 256)
+SILE_FA_V2_DTYPES(v2w4_d208, 4, 32, 208, 256)
+SILE_FA_V2_DTYPES(v2w4_d224, 4, 32, 224, 256)
+SILE_FA_V2_DTYPES(v2w4_d240, 4, 32, 240, 256)
 SILE_FA_V2_DTYPES(v2w4_d256, 4, 32, 256, 256)

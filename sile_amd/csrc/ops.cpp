@@ -780,24 +780,19 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
   // MFMA flash kernel, 16-byte aligned operands, any S: the pipelined kernel
   // (32-query waves, key blocks through LDS-DMA; causal query blocks taken
   // in balanced pairs; keys and queries past S masked), one instantiation
-  // per head dimension: 8 waves for head_dim up to 128 (32-key blocks, or
-  // 64-key blocks over 128-byte rows for 32 and 64), 4 waves for 160 to 256.
-  struct FaShape {
-    int64_t d;
-    const char* suffix;
-    int waves;
-  };
-  static const FaShape kFaShapes[] = {{32, "v2w8_d32", 8},   {64, "v2w8_d64", 8},
-                                      {80, "v2w8_d80", 8},   {96, "v2w8_d96", 8},
-                                      {128, "v2w8", 8},      {160, "v2w4_d160", 4},
-                                      {192, "v2w4_d192", 4}, {256, "v2w4_d256", 4}};
-  const FaShape* fs = nullptr;
-  for (const FaShape& f : kFaShapes)
-    if (f.d == head_dim) fs = &f;
+  // per head dimension (a multiple of 16 up to 256): 8 waves up to 128
+  // (32-key blocks, or 64-key blocks over 128-byte rows up to 64), 4 waves
+  // past 128.
   const bool aligned = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  if (fs && aligned) {
+  if (head_dim % 16 == 0 && head_dim >= 16 && head_dim <= 256 && aligned) {
     const char* dt = dtype == SILE_F16 ? "f16" : "bf16";
-    const int64_t bq = 32 * fs->waves;
+    const int waves = head_dim <= 128 ? 8 : 4;
+    char suffix[32];
+    if (head_dim == 128)
+      snprintf(suffix, sizeof suffix, "v2w8");
+    else
+      snprintf(suffix, sizeof suffix, "v2w%d_d%d", waves, (int)head_dim);
+    const int64_t bq = 32 * waves;
     const bool pair = causal;
     const int64_t q_blocks = (seq_len + bq - 1) / bq;
     if (q_blocks > 0x7fffffffLL / std::max<int64_t>(bh, 1))
@@ -812,8 +807,8 @@ int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int6
     const int64_t units = pair ? (q_blocks + 1) / 2 : q_blocks;
     const int64_t blocks = bh * units;
     char name[64];
-    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, fs->suffix);
-    const unsigned threads = 64 * fs->waves;
+    snprintf(name, sizeof name, "sile_flash_attn_fwd_%s_%s", dt, suffix);
+    const unsigned threads = 64 * waves;
     void* params[] = {(void*)&q, (void*)&k, (void*)&v, &o, &fa};
     int rc = launch(Module::kFlashAttn, name, dim3((unsigned)blocks), dim3(threads), params, s);
     return rc == SILE_OK ? ok() : rc;

@@ -247,14 +247,14 @@ def test_flash_any_seq_len_writes_nothing_past_o(hip):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("d", [32, 80, 96, 160, 192, 256])
+@pytest.mark.parametrize("d", [16, 32, 48, 80, 96, 112, 144, 160, 176, 192, 208, 224, 240, 256])
 @pytest.mark.parametrize("s", [100, 384, 1000])
 def test_flash_other_head_dims(hip, dt, causal, d, s):
     """Head dimensions past the benchmarked 128 and 64 on the same pipelined
-    kernel: 32 (128-byte LDS rows, half of each row zero), 80 and 96 (256-byte
-    rows, 80 with an O^T tile half past the head dimension), 160, 192 and 256
-    (512-byte rows, 4 waves); B = 1, H = 8 (head-per-XCD order), every head
-    and query against the fp32 oracle."""
+    kernel: 16 to 48 (128-byte LDS rows, the rest of each row zero), 80 to
+    112 (256-byte rows; 80 and 112 with an O^T tile half past the head
+    dimension), 144 to 256 (512-byte rows, 4 waves); B = 1, H = 8
+    (head-per-XCD order), every head and query against the fp32 oracle."""
     b, h = 1, 8
     say(f"flash D={d} {dt} causal={causal} S={s}")
     scale = 1.0 / np.sqrt(d)
