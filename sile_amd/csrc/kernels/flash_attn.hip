@@ -1,4 +1,5 @@
-// Flash-attention forward on the gfx950 matrix cores, head_dim 128 or 64.
+// Flash-attention forward on the gfx950 matrix cores, any sequence length,
+// head_dim a multiple of 16 up to 256.
 //
 //   O = softmax(Q K^T * scale [+ causal mask]) V     Q, K, V, O: [B*H, S, D] 16-bit
 //
@@ -68,8 +69,9 @@ struct AttnArgs {
 
 // ===========================================================================
 // Pipelined kernel (any S): 8 waves x 32 queries = 256 queries per
-// workgroup, two waves per SIMD; 32-key blocks for head_dim 128, 64-key
-// blocks for head_dim 64 (the same LDS bytes and MFMAs per block).
+// workgroup, two waves per SIMD, for head_dim up to 128 (32-key blocks over
+// 256-byte LDS rows, 64-key blocks over 128-byte rows: the same LDS bytes and
+// MFMAs per block); 4 waves x 32 queries over 512-byte rows up to 256.
 //
 // Iteration j of the key loop issues, as one scheduling region,
 //   * on the matrix cores: S_{j+1} = K_{j+1} . Q^T  and  O^T += V_{j-1}^T . P_{j-1}
@@ -359,21 +361,11 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
     s_block(0, sa);
     __syncthreads();
 
-    // One iteration: everything up to the optional O rescale is one basic block,
-    // so the scheduler interleaves the softmax VALU work of block j with the
-    // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
-    // code, needed only on the workgroup's diagonal.
-    auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT][kST],
-                         f32x16 (&snext)[kQT][kST], const u32x4 (&pprev)[kQT][2 * kST],
-                         u32x4 (&pnew)[kQT][2 * kST]) {
-      constexpr int kS = decltype(stage_c)::value;
+    // The online softmax of S_j -> P_j on the VALU (causal / past-S mask
+    // first when kMasked).
+    auto softmax_block = [&](int j, auto masked, f32x16 (&scur)[kQT][kST],
+                             u32x4 (&pnew)[kQT][2 * kST]) {
       constexpr bool kMasked = decltype(masked)::value;
-      dma_k(min(j + 2, last), kS);
-      dma_v(j, kS);
-      // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
-      // consecutive MFMAs never accumulate into the same registers
-      mma_block(kS ^ 1, kS ^ 1, snext, pprev, oacc);
-      // VALU: online softmax of S_j -> P_j
       if constexpr (kMasked) {
         const int kb = j * kNK;
   #pragma unroll
@@ -472,6 +464,33 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       }
   #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) l_run[qt] += rs_blk[qt];
+    };
+    // Last key block this wave needs: the one holding its last query (causal)
+    // or key S - 1.  On the diagonal the wave skips iteration j once block
+    // j - 1 is past it: S_{j+1}, P_j and PV_{j-1} are then all of masked keys
+    // (their P is zero), and the block's DMA and barrier stay.  (Skipping the
+    // unneeded half of iterations jw and jw + 1 as well keeps registers of the
+    // skipped branches live and spills.)
+    const int jw = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal ? min((int64_t)(wq0 + 32 * kQT - 1), S - 1) : S - 1) / kNK));
+
+    // One iteration: everything up to the optional O rescale is one basic block,
+    // so the scheduler interleaves the softmax VALU work of block j with the
+    // MFMAs of blocks j + 1 (S) and j - 1 (PV).  kMasked selects the causal-mask
+    // code, needed only on the workgroup's diagonal.
+    auto iteration = [&](int j, auto stage_c, auto masked, f32x16 (&scur)[kQT][kST],
+                         f32x16 (&snext)[kQT][kST], const u32x4 (&pprev)[kQT][2 * kST],
+                         u32x4 (&pnew)[kQT][2 * kST]) {
+      constexpr int kS = decltype(stage_c)::value;
+      constexpr bool kMasked = decltype(masked)::value;
+      dma_k(min(j + 2, last), kS);
+      dma_v(j, kS);
+      if (!kMasked || j - 1 <= jw) {
+        // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
+        // consecutive MFMAs never accumulate into the same registers
+        mma_block(kS ^ 1, kS ^ 1, snext, pprev, oacc);
+        softmax_block(j, masked, scur, pnew);
+      }
       // keep P_j and l in this region, beside the MFMAs
   #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
@@ -496,7 +515,7 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       iteration(j + 1, One{}, std::true_type{}, sb, sa, pb, pprev);
     }
     // PV of the last block (nb is even: P_{nb-1} is in pprev, V_{nb-1} in stage 1)
-    pv_block(1, pprev, oacc);
+    if (last <= jw) pv_block(1, pprev, oacc);
 
     // ---- epilogue: O[q][d] = O^T[d][q] / l ----
   #pragma unroll
