@@ -673,7 +673,10 @@ def traffic_from_pmc(root):
     ROOT/pmc_write_<name>/ (WRITE_SIZE), <name> being a workload of ALL or
     EXTRA (those without both runs are left out).  The mean per-dispatch KiB of the workload's kernel is
     scaled by what the same counter reads for the copy calibration (COPY_BYTES
-    each way): bytes = KiB * COPY_BYTES / copy_KiB."""
+    each way): bytes = KiB * COPY_BYTES / copy_KiB.  Only the dispatches of
+    the random-data run count: those after the inputs are zero-filled for
+    `same_kernel_on_zero_inputs` (a runtime fill dispatch after the workload's
+    first) run at another clock and fetch differently through the L2."""
     import csv
     import glob
 
@@ -681,9 +684,13 @@ def traffic_from_pmc(root):
         vals = []
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             with open(path) as f:
-                for row in csv.DictReader(f):
-                    if row.get("Counter_Name") == counter and want(row["Kernel_Name"]):
-                        vals.append(float(row["Counter_Value"]))
+                rows = [r for r in csv.DictReader(f) if r.get("Counter_Name") == counter]
+            first = min((int(r["Dispatch_Id"]) for r in rows if want(r["Kernel_Name"])), default=0)
+            cut = min((int(r["Dispatch_Id"]) for r in rows
+                       if "fillBuffer" in r["Kernel_Name"] and int(r["Dispatch_Id"]) > first),
+                      default=None)
+            vals += [float(r["Counter_Value"]) for r in rows
+                     if want(r["Kernel_Name"]) and (cut is None or int(r["Dispatch_Id"]) < cut)]
         return sum(vals) / len(vals) if vals else None
 
     def is_copy(k):
