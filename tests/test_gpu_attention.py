@@ -265,3 +265,28 @@ def test_flash_other_head_dims(hip, dt, causal, d, s):
     for hi in range(h):
         ref = cpuref.attention_fwd(qf[0, hi], kf[0, hi], vf[0, hi], scale, causal=causal)
         assert_close(got[0, hi], ref, atol=ATOL, rtol=RTOL, what=f"D={d} h{hi}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("causal,b,h,s,d", [
+    (True, 2, 64, 1280, 128),   # 384 items (pairs and a middle block alone), head-per-XCD order
+    (True, 1, 100, 1280, 128),  # 300 items, plain order (B*H not a multiple of 8)
+    (False, 1, 72, 1100, 128),  # 360 one-block items, the last block partial
+    (True, 2, 64, 1000, 64),    # 64-key blocks
+    (True, 1, 96, 700, 256)])   # 4 waves
+def test_flash_many_work_items(hip, dt, causal, b, h, s, d):
+    """More work items (query blocks or causal pairs of them) than CUs, in
+    both launch orders, with partial last blocks and the 4-wave kernel.
+    Every output is written and finite; every 9th head and the last one
+    against the fp32 oracle."""
+    say(f"flash many items {dt} causal={causal} B={b} H={h} S={s} D={d}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, dt, seed=71)
+    got = _run(hip, dt, b, h, s, d, [x[0] for x in qkv], causal, scale)
+    assert np.isfinite(got).all()
+    qf, kf, vf = (x[1] for x in qkv)
+    heads = sorted(set(range(0, b * h, 9)) | {b * h - 1})
+    for n in heads:
+        bi, hi = divmod(n, h)
+        ref = cpuref.attention_fwd(qf[bi, hi], kf[bi, hi], vf[bi, hi], scale, causal=causal)
+        assert_close(got[bi, hi], ref, atol=ATOL, rtol=RTOL, what=f"attn b{bi} h{hi}")
