@@ -290,3 +290,27 @@ def test_flash_many_work_items(hip, dt, causal, b, h, s, d):
         bi, hi = divmod(n, h)
         ref = cpuref.attention_fwd(qf[bi, hi], kf[bi, hi], vf[bi, hi], scale, causal=causal)
         assert_close(got[bi, hi], ref, atol=ATOL, rtol=RTOL, what=f"attn b{bi} h{hi}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_long_sequence(hip, causal):
+    """S = 65536 (B = 1, H = 8, D = 128, f16): block, key and byte offsets at
+    64 times the benchmarked length.  Every output is finite; 24 query rows of
+    two heads (the first and last rows of query blocks, the last row, and
+    seeded ones) against a float64 softmax over the same 16-bit inputs."""
+    b, h, s, d = 1, 8, 65536, 128
+    say(f"flash long S={s} causal={causal}")
+    scale = 1.0 / np.sqrt(d)
+    qkv = _inputs(b, h, s, d, "f16", seed=81)
+    got = _run(hip, "f16", b, h, s, d, [x[0] for x in qkv], causal, scale)
+    assert np.isfinite(got).all()
+    qf, kf, vf = (x[1].astype(np.float64) for x in qkv)
+    rows = sorted({0, 1, 255, 256, 4095, 32767, 32768, s - 257, s - 256, s - 1} |
+                  set(rng(82).integers(0, s, size=14).tolist()))
+    for hi in (0, h - 1):
+        for i in rows:
+            n = i + 1 if causal else s
+            sc = kf[0, hi, :n] @ qf[0, hi, i] * scale
+            p = np.exp(sc - sc.max())
+            ref = (p @ vf[0, hi, :n]) / p.sum()
+            assert_close(got[0, hi, i], ref, atol=ATOL, rtol=RTOL, what=f"h{hi} row {i}")

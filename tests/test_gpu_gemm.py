@@ -613,3 +613,24 @@ def test_split_k_scratch_across_streams_and_growth(hip):
             x.close()
     s1.close()
     s2.close()
+
+
+@pytest.mark.parametrize("m,n,k,out", [(256, 256, 1 << 20, "f32"), (256, 256, 1 << 20, "bf16"),
+                                       (200, 512, 1 << 19, "f32")])
+def test_gemm_long_k(hip, m, n, k, out):
+    """K' of 2^19 and 2^20 bf16 elements (1-2 MiB rows, 512 MiB operands):
+    half-k-step counts, k-range offsets and the split sums far past the sizes
+    benchmarked.  Every element is written and finite; 16 seeded rows (with
+    the first and last) against a float64 product of the same bf16 inputs."""
+    say(f"gemm long K {m}x{n}x{k} -> {out}")
+    a = (rng(91).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(92).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    (qa, a_f), (qb, b_f) = bf16_round(a), bf16_round(bt)
+    del a, bt
+    c_t = hip.F32 if out == "f32" else hip.BF16
+    got = _run(hip, hip.BF16, c_t, qa, qb, m, n, k)
+    assert np.isfinite(got).all()
+    rows = sorted({0, m - 1} | set(rng(93).integers(0, m, size=14).tolist()))
+    ref = a_f[rows].astype(np.float64) @ b_f.astype(np.float64).T
+    tol = (1e-4, 1e-4) if out == "f32" else (ATOL, RTOL)
+    assert_close(got[rows], ref, atol=tol[0], rtol=tol[1], what=f"long K rows {rows[:3]}...")
