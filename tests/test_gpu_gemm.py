@@ -634,3 +634,24 @@ def test_gemm_long_k(hip, m, n, k, out):
     ref = a_f[rows].astype(np.float64) @ b_f.astype(np.float64).T
     tol = (1e-4, 1e-4) if out == "f32" else (ATOL, RTOL)
     assert_close(got[rows], ref, atol=tol[0], rtol=tol[1], what=f"long K rows {rows[:3]}...")
+
+
+@pytest.mark.parametrize("m,n,k", [(1 << 20, 256, 128), (1 << 20, 200, 64), (1 << 20, 100, 64),
+                                   ((1 << 20) + 3, 130, 96)])
+def test_gemm_tall(hip, m, n, k):
+    """M of 2^20 rows (and 2^20 + 3): the LDS kernels' tile grid and row
+    offsets, and the any-shape kernel (N = 100 and M not a multiple of 4,
+    whose C^T planes would pass the transposed form's scratch limit) with
+    its 64-row tiles in grid y.  bf16 in and out; every element written and
+    finite; 64 seeded rows (with the first and last) against a float64
+    product of the same bf16 inputs."""
+    say(f"gemm tall {m}x{n}x{k}")
+    a = (rng(95).normal(size=(m, k)) / np.sqrt(k)).astype(np.float32)
+    bt = (rng(96).normal(size=(n, k)) / np.sqrt(k)).astype(np.float32)
+    (qa, a_f), (qb, b_f) = bf16_round(a), bf16_round(bt)
+    del a, bt
+    got = _run(hip, hip.BF16, hip.BF16, qa, qb, m, n, k)
+    assert np.isfinite(got).all()
+    rows = sorted({0, m - 1} | set(rng(97).integers(0, m, size=62).tolist()))
+    ref = a_f[rows].astype(np.float64) @ b_f.astype(np.float64).T
+    assert_close(got[rows], ref, atol=ATOL, rtol=RTOL, what="tall GEMM rows")
