@@ -255,7 +255,8 @@ def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_ste
             2.0 * rows * n * k, 1e12, "TFLOP/s",
             (f"every {cpu_tile_step}th 256-row tile of C ({rows} of {m} rows, all columns, full K)"
              if cpu_tile_step > 1 else "the whole GEMM")
-            + f" on {what}; canonical-matmul loop nest, gcc -O2 -fopenmp")
+            + f" on {what}; canonical-matmul loop nest, gcc -O2 -fopenmp",
+            full_work=2.0 * m * n * k)
     return res
 
 
@@ -302,7 +303,8 @@ def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0, d=ATTN
         res["cpu_baseline"] = cpu_timed(
             run, flop * cpu_heads / (b * h), 1e12, "TFLOP/s",
             f"{cpu_heads} of {b * h} (batch, head) slices, every query row, causal, on up-cast "
-            "fp32 Q/K/V; naive fp32 restatement (scores, max, expf, sum, P.V), gcc -O2 -fopenmp")
+            "fp32 Q/K/V; naive fp32 restatement (scores, max, expf, sum, P.V), gcc -O2 -fopenmp",
+            full_work=flop)
     return res
 
 
@@ -642,14 +644,20 @@ def cpu_baseline(row_tile_step=1):
                    " oracle = canonical-matmul loop nest (sequential fp32 mul-then-add per cell),"
                    " gcc -O2 -fopenmp"),
         "seconds": round(dt, 3),
+        **({"extrapolated_full_seconds": round(dt * m / rows, 3),
+            "extrapolated_note": "extrapolated, not measured: the sample's time scaled by "
+                                 "the whole GEMM's rows over the sample's"}
+           if rows < m else {}),
     }
 
 
-def cpu_timed(run, work, unit_scale, unit, sample, min_s=1.0):
+def cpu_timed(run, work, unit_scale, unit, sample, min_s=1.0, full_work=None):
     """Times `run()` (a CPU oracle call on this host's cores), repeated until
     at least `min_s` seconds have passed; returns a cpu_baseline object whose
     value is `work` (the algorithmic work of one run, in the GPU workload's
-    own unit) per second of one run."""
+    own unit) per second of one run.  For a sample of the workload,
+    `full_work` (the whole workload's work) adds the time the whole workload
+    would take at the sample's rate, labelled as extrapolated."""
     from oracle import cpuref
 
     reps, t0 = 0, time.perf_counter()
@@ -660,9 +668,14 @@ def cpu_timed(run, work, unit_scale, unit, sample, min_s=1.0):
         if dt >= min_s:
             break
     per = dt / reps
-    return {"value": round(work / per / unit_scale, 6), "unit": unit,
-            "cores": cpuref.num_threads(), "kind": "port",
-            "sample": f"{sample}; {reps} run(s), {per:.3f} s each", "seconds": round(dt, 3)}
+    out = {"value": round(work / per / unit_scale, 6), "unit": unit,
+           "cores": cpuref.num_threads(), "kind": "port",
+           "sample": f"{sample}; {reps} run(s), {per:.3f} s each", "seconds": round(dt, 3)}
+    if full_work is not None and full_work > work:
+        out["extrapolated_full_seconds"] = round(per * full_work / work, 3)
+        out["extrapolated_note"] = ("extrapolated, not measured: one run's time scaled by the "
+                                    "whole workload's work over the sample's")
+    return out
 
 
 # ---------------------------------------------------------------- PMC traffic
