@@ -485,6 +485,17 @@ __device__ __forceinline__ void attn_fwd_v2(const uint16_t* __restrict__ Q,
       constexpr bool kMasked = decltype(masked)::value;
       dma_k(min(j + 2, last), kS);
       dma_v(j, kS);
+      if constexpr (kMasked) {
+        // From S_{jw+1} on this wave's scores are all masked: its Q^T
+        // operand is zeroed, so the S products it still issues run on zeros
+        // (the matrix cores draw far less power on zero data).
+        if (j == jw) {
+  #pragma unroll
+          for (int qt = 0; qt < kQT; ++qt)
+  #pragma unroll
+            for (int kk = 0; kk < kKK; ++kk) qf[qt][kk] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
       if (!kMasked || j - 1 <= jw) {
         // matrix cores: S_{j+1} and PV_{j-1}, interleaved step by step so that
         // consecutive MFMAs never accumulate into the same registers
