@@ -39,6 +39,15 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_abi.SIGNATURES), sorted(declared ^ set(_abi.SIGNATURES))
 
 
+def test_integration_binding_declares_every_function():
+    """The Rust FFI block of the integration guide names exactly the functions
+    the header declares, so a maintainer copying it binds the whole ABI."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text[text.index("## 3. FFI declarations"):text.index("## 4.")]
+    bound = set(re.findall(r"pub fn (sile_hip_\w+)\s*\(", block))
+    assert bound == set(declared_functions()), sorted(bound ^ set(declared_functions()))
+
+
 def test_library_loads_and_reports_version():
     lib = _abi.lib()
     assert b"gfx950" in lib.sile_hip_version()
