@@ -734,7 +734,9 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
                    "gemm_bf16_4096": "sile_gemm_nt", "gemm_fp8_8192": "sile_gemm_nt",
                    "flash_attn_fwd_f16_s8192": "sile_flash_attn", "flash_attn_fwd_f16_s4096":
                    "sile_flash_attn", "gemm_f32_exact_4096": "sile_gemm_f32_exact",
-                   "gemm_f32_exact_512": "sile_gemm_f32_exact"}
+                   "gemm_f32_exact_512": "sile_gemm_f32_exact",
+                   "flash_attn_fwd_f16_s8000": "sile_flash_attn",
+                   "flash_attn_fwd_f16_s8192_d64": "sile_flash_attn"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
