@@ -1,7 +1,7 @@
 """ctypes binding of libsile_hip.so (the C ABI declared in include/sile_hip.h).
 
 This is the Python caller of the drop-in boundary: tests, bench.py and the
-Python mirror of sile's launch API (sile_amd.api) go through it.  There is no
+host mirror of sile's backend plugin (sile_amd.backend) go through it.  There is no
 fallback: if the library is missing, loading raises immediately.
 """
 from __future__ import annotations
