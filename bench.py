@@ -260,32 +260,45 @@ def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_ste
     return res
 
 
-def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0, d=ATTN_SHAPE[2]):
+def bench_attention(name, s, steps, warmup, stream, traffic, cpu_heads=0, d=ATTN_SHAPE[2],
+                    dt="f16", causal=True):
     """cpu_heads > 0 also times the CPU oracle on the first cpu_heads (b, h)
-    slices, every query row, causal."""
+    slices, every query row, causal (fp16 causal lines only).  dt "bf16"
+    rounds the same N(0, 1) inputs to bf16; causal False attends to every
+    key."""
     b, h = ATTN_SHAPE[:2]
+    if dt != "f16" or not causal:
+        cpu_heads = 0
     log(f"[bench] {name}: generating inputs")
     bufs, host = [], []
-    for x in attention_inputs(s, d=d):
+    if dt == "bf16":
+        xs = [bf16_bits(normal(seed, (b, h, s, d))) for seed in (6, 7, 8)]
+    else:
+        xs = attention_inputs(s, d=d)
+    for x in xs:
         bufs.append(hip.DeviceBuffer.from_array(x.view(np.uint16)))
         if cpu_heads:
             host.append(x.reshape(b * h, s, d)[:cpu_heads].astype(np.float32))
         del x
+    del xs
     do = hip.DeviceBuffer(b * h * s * d * 2)
     scale = 1.0 / np.sqrt(d)
 
+    t = hip.BF16 if dt == "bf16" else hip.F16
+
     def launch(_):
-        hip.flash_attn_fwd(hip.F16, b, h, s, d, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, do.ptr,
-                           scale, True, stream)
+        hip.flash_attn_fwd(t, b, h, s, d, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, do.ptr,
+                           scale, causal, stream)
 
     log(f"[bench] {name}: timing {steps} steps")
     region = time_launches(launch, steps, warmup, stream)
     # unmasked (query, key) pairs only: 2 products x 2 flop x D per pair
-    flop = 4.0 * d * b * h * s * (s + 1) / 2
+    flop = 4.0 * d * b * h * (s * (s + 1) / 2 if causal else s * s)
     res = summarise(name, flop, 1e12, "TFLOP/s", region, steps, "mfma", PEAK_TFLOPS["f16"],
                     traffic.get(name))
     res["flop_per_launch"] = flop
-    res["flop_convention"] = "4*D*B*H*S*(S+1)/2 (causal pairs only)"
+    res["flop_convention"] = ("4*D*B*H*S*(S+1)/2 (causal pairs only)" if causal
+                              else "4*D*B*H*S*S (every pair)")
     res["same_kernel_on_zero_inputs"] = zero_input_rate(launch, bufs, flop, PEAK_TFLOPS["f16"],
                                                         steps, stream)
     for buf in bufs + [do]:
@@ -748,7 +761,9 @@ EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f
          "gemm_fp8_256x8192x8192",
          # causal attention at an S that is not a multiple of the query block,
          # and at head_dim 64
-         "flash_attn_fwd_f16_s8000", "flash_attn_fwd_f16_s8192_d64"]
+         "flash_attn_fwd_f16_s8000", "flash_attn_fwd_f16_s8192_d64",
+         # bf16 inputs, and every (query, key) pair (not causal)
+         "flash_attn_fwd_bf16_s8192", "flash_attn_fwd_f16_s8192_nc"]
 
 
 def main():
@@ -807,11 +822,14 @@ def main():
             results[name] = bench_gemm(name, kind, m, n, k, args.steps, args.warmup, stream,
                                        traffic, cpu_tile_step=step)
         elif name.startswith("flash_attn"):
-            # flash_attn_fwd_f16_s<S>[_d<D>]
-            tail = name.split("_s")[-1]
+            # flash_attn_fwd_<f16|bf16>_s<S>[_d<D>][_nc] (_nc: not causal)
+            causal = not name.endswith("_nc")
+            tail = name.removesuffix("_nc").split("_s")[-1]
             s_len, d = (map(int, tail.split("_d")) if "_d" in tail else (int(tail), ATTN_SHAPE[2]))
             results[name] = bench_attention(name, s_len, args.steps, args.warmup, stream, traffic,
-                                            cpu_heads=CPU_ATTN_HEADS if cpu else 0, d=d)
+                                            cpu_heads=CPU_ATTN_HEADS if cpu else 0, d=d,
+                                            dt="bf16" if "_bf16_" in name else "f16",
+                                            causal=causal)
         else:
             results[name] = bench_softmax(name, args.steps, args.warmup, stream, traffic,
                                           cpu=cpu)
