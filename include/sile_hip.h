@@ -151,16 +151,18 @@ int sile_hip_launch_tiles(sile_hip_function fn, void *const *buffers, int64_t nu
                           uint32_t threads_per_program, sile_hip_stream stream);
 
 /* sile_hip_launch_tiles without any allocation.  No counterpart in the
- * reference: for callers that cannot allocate device memory (code under HIP
- * graph capture, serving loops or harnesses that forbid hipMalloc).  Same
+ * reference: for callers that cannot allocate device memory (serving loops
+ * or harnesses that forbid hipMalloc).  Same
  * arguments, semantics and synchronous return as sile_hip_launch_tiles, but
  * the device copies of the buffer and shape tables go into a fixed 4 KiB
  * array of the library (one per device, held until the process ends) rather
  * than into a pooled buffer that sile_hip_launch_tiles allocates when its
  * per-device pool has none free: num_buffers + num_shapes
  * may not exceed 512 (SILE_ERR_SHAPE beyond).  Calls on one device share
- * that array, so calls that overlap on one device (from several threads or
- * streams) race; each call writes the tables it needs before its launch. */
+ * that array: a call holds it (a per-device lock) from its table copy until
+ * its launch has completed, so calls from several host threads run one
+ * after another.  The call waits for its launch, so a stream being captured
+ * into a graph is refused (SILE_ERR_UNSUPPORTED_BACKEND). */
 int sile_hip_launch_tiles_noalloc(sile_hip_function fn, void *const *buffers,
                                   int64_t num_buffers, const int64_t *shapes, int64_t num_shapes,
                                   const uint32_t grid[3], uint32_t threads_per_program,
@@ -264,8 +266,9 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  * split into ranges computed side by side: their fp32 partial C planes go
  * to a device scratch buffer shared by all calls on the device (allocated on
  * the first such call, grown when a call needs more, at most
- * 4 * (CUs * 65536) bytes; calls on different streams are ordered on the GPU
- * by an event) and a second kernel adds them in range order.  The result
+ * 4 * (CUs * 65536) bytes for the split chosen by shape and 256 MiB for
+ * any form; calls on different streams are ordered on the GPU by an event)
+ * and a second kernel adds them in range order.  The result
  * does not depend on the stream or on earlier calls (outside graph capture,
  * below).  The transposed form
  * (above) keeps all of C^T there, up to 256 MiB (larger: 64 x 64 tiles).
@@ -287,7 +290,8 @@ int sile_hip_gemm(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64
  * forced size the shape cannot take (N below it, M below 256 for 256, N not
  * a multiple of 4, C's rows not 16-byte aligned) -> SILE_ERR_SHAPE.  splits:
  * 0 (by shape) or 1 .. 64 ranges of K' (fewer when K' has fewer whole
- * k-steps); a split needs splits * M * N * 4 bytes of the device scratch. */
+ * k-steps); a split needs splits * M * N * 4 bytes of the device scratch,
+ * and a forced split beyond 256 MiB of it -> SILE_ERR_SHAPE. */
 int sile_hip_gemm_tiled(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m,
                         int64_t n, int64_t k, const void *a, int64_t lda, sile_layout a_layout,
                         const void *b, int64_t ldb, sile_layout b_layout, void *c, int64_t ldc,
@@ -318,9 +322,12 @@ int sile_hip_softmax_rows(sile_dtype in_type, sile_dtype out_type, int64_t rows,
 
 /* out[r] = max_c x[r][c] or sum_c x[r][c] in fp32 (ReduceMax/ReduceSum along
  * axis 1, crates/sile-tile-ir/src/passes/lowering/tile_compute/reduce.rs:10-112).
- * in: f32, f16, bf16.  `out` is fp32 [rows].  The max equals the reference's
- * fold; the sum is a wave tree, within fp32 rounding of the reference's
- * order (sile_hip_reduce_rows_fused_sum keeps that order bit for bit). */
+ * in: f32, f16, bf16.  `out` is fp32 [rows].  The max is the reference's
+ * fold acc = x0; acc = x > acc ? x : acc bit for bit: a NaN in column 0
+ * gives NaN, NaNs elsewhere never enter, and of a +0 / -0 tie the first in
+ * row order is kept (cols < 2^31).  The sum is a tree, within fp32 rounding
+ * of the reference's order (sile_hip_reduce_rows_fused_sum keeps that order
+ * bit for bit). */
 int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, int64_t cols,
                          const void *x, int64_t ldx, float *out, sile_hip_stream stream);
 

@@ -295,6 +295,9 @@ class Graph:
             if rc != SILE_OK:
                 raise SileError(rc, last_error(), "sile_hip_graph_end")
             self.handle = p.value
+        elif rc == SILE_OK and p.value:
+            # the body raised: capture ended cleanly, but the graph is not kept
+            lib().sile_hip_graph_destroy(p)
         return False
 
     def launch(self, stream: "Stream | None" = None) -> None:

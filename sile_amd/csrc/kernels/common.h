@@ -121,6 +121,61 @@ SILE_DEV float wave_sum(float v) {
   return pair32_sum(v);
 }
 
+// ---- the reference's row max, computed in parallel ----
+// ReduceMax folds from the row's first element, acc = x0; acc = x > acc ? x : acc
+// (crates/sile-tile-ir/src/passes/lowering/tile_compute/reduce.rs:10-30), so
+//  * x0 NaN gives NaN (no x compares greater than NaN);
+//  * otherwise NaN elements never enter, and of the elements equal to the max
+//    the first one in row order is kept (only +0 / -0 ties differ in bits).
+// A lane folds its elements in increasing index order into (v, i), the value
+// and column of its first maximum (start: -inf at column kNoCol); partials
+// merge by the larger value, then the smaller column, an associative and
+// commutative rule, so any reduction tree gives the fold's bits.  The caller
+// returns x0 instead when x0 is NaN.
+constexpr int kNoCol = 0x7fffffff;
+SILE_DEV void first_max_fold(float& v, int& i, float x, int xi) {
+  const bool gt = x > v;
+  v = gt ? x : v;
+  i = gt ? xi : i;
+}
+SILE_DEV void first_max_merge(float& v, int& i, float ov, int oi) {
+  const bool take = ov > v || (ov == v && oi < i);
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+template <int kCtrl>
+SILE_DEV int dpp_int(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xf, 0xf, false);
+}
+template <int kCtrl>
+SILE_DEV void first_max_dpp(float& v, int& i) {
+  first_max_merge(v, i, dpp<kCtrl>(v), dpp_int<kCtrl>(i));
+}
+SILE_DEV void first_max_swizzle16(float& v, int& i) {
+  first_max_merge(v, i, swizzle_xor16(v), __builtin_amdgcn_ds_swizzle(i, 0x401F));
+}
+// (v, i) merged over groups of kL lanes (kL = 4 .. 32), all lanes of a group
+// holding the result.
+template <int kL>
+SILE_DEV void group_first_max(float& v, int& i) {
+  first_max_dpp<kDppXor1>(v, i);
+  first_max_dpp<kDppXor2>(v, i);
+  if constexpr (kL >= 8) first_max_dpp<kDppHalfMirror>(v, i);
+  if constexpr (kL >= 16) first_max_dpp<kDppMirror>(v, i);
+  if constexpr (kL >= 32) first_max_swizzle16(v, i);
+}
+SILE_DEV void wave_first_max(float& v, int& i) {
+  group_first_max<32>(v, i);
+  float lo, hi;
+  half_swap(v, lo, hi);
+  const unsigned iu = (unsigned)i;
+  const auto r = __builtin_amdgcn_permlane32_swap(iu, iu, false, false);
+  const unsigned ilo = r[0], ihi = r[1];
+  v = lo;
+  i = (int)ilo;
+  first_max_merge(v, i, hi, (int)ihi);
+}
+
 // Instruction classes of __builtin_amdgcn_sched_group_barrier masks.
 namespace sched {
 constexpr int kValu = 0x002, kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;

@@ -634,8 +634,16 @@ SILE_SOFTMAX_WIDE_WIDTHS(f32_f32, kF32, kF32)
 SILE_SOFTMAX_WIDE_WIDTHS(f16_f32, kF16, kF32)
 
 // ---- row reduce (ReduceMax / ReduceSum along axis 1), fp32 result ----
-// op 0 = max (order-independent, so identical to the reference's fold),
-// op 1 = sum (wave tree; the reference folds left to right).
+// op 0 = max, the reference's fold from x0 bit for bit (first_max_* in
+// common.h: NaN at column 0 gives NaN, other NaNs never enter, a +0 / -0 tie
+// keeps the first in row order); op 1 = sum (a tree; the reference folds left
+// to right).  The lane that stores a row's result always owns its column 0.
+template <int kIn>
+SILE_DEV float max_result(float v, const typename Elem<kIn>::Storage* xr) {
+  const float x0 = Elem<kIn>::load1(xr);
+  return x0 != x0 ? x0 : v;
+}
+
 template <int kIn>
 __device__ __forceinline__ void reduce_rows_kernel(int op, int vec, const void* x, float* out,
                                                    int64_t rows, int64_t cols, int64_t ldx) {
@@ -646,19 +654,32 @@ __device__ __forceinline__ void reduce_rows_kernel(int op, int vec, const void* 
   const TI* xr = static_cast<const TI*>(x) + row * ldx;
   constexpr int kE = chunk_elems<kIn, kF32>();  // one 16-byte load per lane
   const int64_t vec_cols = vec ? (cols & ~(int64_t)(kE - 1)) : 0;
-  float acc = op == 0 ? -__builtin_inff() : 0.0f;
+  if (op == 0) {
+    float m = -__builtin_inff();
+    int mi = kNoCol;
+    int64_t c = (int64_t)lane * kE;
+    for (; c + kE <= vec_cols; c += 64 * kE) {
+      float v[kE];
+      load_chunk<kIn, kE>(xr + c, v);
+#pragma unroll
+      for (int i = 0; i < kE; ++i) first_max_fold(m, mi, v[i], (int)c + i);
+    }
+    for (int64_t cc = vec_cols + lane; cc < cols; cc += 64)
+      first_max_fold(m, mi, Elem<kIn>::load1(xr + cc), (int)cc);
+    wave_first_max(m, mi);
+    if (lane == 0) out[row] = max_result<kIn>(m, xr);
+    return;
+  }
+  float acc = 0.0f;
   int64_t c = (int64_t)lane * kE;
   for (; c + kE <= vec_cols; c += 64 * kE) {
     float v[kE];
     load_chunk<kIn, kE>(xr + c, v);
 #pragma unroll
-    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+    for (int i = 0; i < kE; ++i) acc = acc + v[i];
   }
-  for (int64_t cc = vec_cols + lane; cc < cols; cc += 64) {
-    const float v = Elem<kIn>::load1(xr + cc);
-    acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
-  }
-  acc = op == 0 ? wave_max(acc) : wave_sum(acc);
+  for (int64_t cc = vec_cols + lane; cc < cols; cc += 64) acc = acc + Elem<kIn>::load1(xr + cc);
+  acc = wave_sum(acc);
   if (lane == 0) out[row] = acc;
 }
 
@@ -675,19 +696,32 @@ __device__ __forceinline__ void reduce_rows_narrow_kernel(int op, const void* x,
   using TI = typename Elem<kIn>::Storage;
   const TI* xr = static_cast<const TI*>(x) + (live ? row : 0) * ldx;
   const int c0 = li * kE;
-  float acc = op == 0 ? -__builtin_inff() : 0.0f;
+  if (op == 0) {
+    float m = -__builtin_inff();
+    int mi = kNoCol;
+    if (live && c0 + kE <= cols) {
+      float v[kE];
+      load_chunk<kIn, kE>(xr + c0, v);
+#pragma unroll
+      for (int i = 0; i < kE; ++i) first_max_fold(m, mi, v[i], c0 + i);
+    } else if (live) {
+      for (int i = 0; c0 + i < cols && i < kE; ++i)
+        first_max_fold(m, mi, Elem<kIn>::load1(xr + c0 + i), c0 + i);
+    }
+    group_first_max<kL>(m, mi);
+    if (live && li == 0) out[row] = max_result<kIn>(m, xr);
+    return;
+  }
+  float acc = 0.0f;
   if (live && c0 + kE <= cols) {
     float v[kE];
     load_chunk<kIn, kE>(xr + c0, v);
 #pragma unroll
-    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+    for (int i = 0; i < kE; ++i) acc = acc + v[i];
   } else if (live) {
-    for (int i = 0; c0 + i < cols && i < kE; ++i) {
-      const float v = Elem<kIn>::load1(xr + c0 + i);
-      acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
-    }
+    for (int i = 0; c0 + i < cols && i < kE; ++i) acc = acc + Elem<kIn>::load1(xr + c0 + i);
   }
-  acc = op == 0 ? group_max<kL>(acc) : group_sum<kL>(acc);
+  acc = group_sum<kL>(acc);
   if (live && li == 0) out[row] = acc;
 }
 
@@ -701,29 +735,50 @@ __device__ __forceinline__ void reduce_rows_block_kernel(int op, const void* x, 
   constexpr int kT = 1024;
   constexpr int kE = chunk_elems<kIn, kF32>();
   __shared__ float part[kT / 64];
+  __shared__ int part_col[kT / 64];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t row = blockIdx.x;
   if (row >= rows) return;
   using TI = typename Elem<kIn>::Storage;
   const TI* xr = static_cast<const TI*>(x) + row * ldx;
-  float acc = op == 0 ? -__builtin_inff() : 0.0f;
   const int64_t vec_cols = cols & ~(int64_t)(kE - 1);
+  if (op == 0) {
+    float m = -__builtin_inff();
+    int mi = kNoCol;
+    for (int64_t c = (int64_t)t * kE; c < vec_cols; c += (int64_t)kT * kE) {
+      float v[kE];
+      load_chunk<kIn, kE>(xr + c, v);
+#pragma unroll
+      for (int i = 0; i < kE; ++i) first_max_fold(m, mi, v[i], (int)c + i);
+    }
+    for (int64_t c = vec_cols + t; c < cols; c += kT)
+      first_max_fold(m, mi, Elem<kIn>::load1(xr + c), (int)c);
+    wave_first_max(m, mi);
+    if (lane == 0) {
+      part[wave] = m;
+      part_col[wave] = mi;
+    }
+    __syncthreads();
+    if (t == 0) {
+      for (int w = 1; w < kT / 64; ++w) first_max_merge(m, mi, part[w], part_col[w]);
+      out[row] = max_result<kIn>(m, xr);
+    }
+    return;
+  }
+  float acc = 0.0f;
   for (int64_t c = (int64_t)t * kE; c < vec_cols; c += (int64_t)kT * kE) {
     float v[kE];
     load_chunk<kIn, kE>(xr + c, v);
 #pragma unroll
-    for (int i = 0; i < kE; ++i) acc = op == 0 ? fmax_ordered(acc, v[i]) : acc + v[i];
+    for (int i = 0; i < kE; ++i) acc = acc + v[i];
   }
-  for (int64_t c = vec_cols + t; c < cols; c += kT) {
-    const float v = Elem<kIn>::load1(xr + c);
-    acc = op == 0 ? fmax_ordered(acc, v) : acc + v;
-  }
-  acc = op == 0 ? wave_max(acc) : wave_sum(acc);
+  for (int64_t c = vec_cols + t; c < cols; c += kT) acc = acc + Elem<kIn>::load1(xr + c);
+  acc = wave_sum(acc);
   if (lane == 0) part[wave] = acc;
   __syncthreads();
   if (t == 0) {
     float r = part[0];
-    for (int w = 1; w < kT / 64; ++w) r = op == 0 ? fmax_ordered(r, part[w]) : r + part[w];
+    for (int w = 1; w < kT / 64; ++w) r = r + part[w];
     out[row] = r;
   }
 }

@@ -1,6 +1,6 @@
 // sile_hip_launch_tiles_noalloc: the generic tile launch for callers that
-// cannot allocate device memory (code under HIP graph capture, serving loops
-// that forbid allocation).  sile_hip_launch_tiles copies the buffer-pointer
+// cannot allocate device memory (serving loops or harnesses that forbid
+// hipMalloc).  sile_hip_launch_tiles copies the buffer-pointer
 // and shape tables into a device buffer from a per-device pool, which it
 // allocates (hipMalloc) whenever no pooled buffer is free or large enough;
 // this variant copies them into `scratch`, a fixed device array of this
@@ -30,15 +30,20 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+// Held by a call from the table copy until its launch has completed, so calls
+// from several host threads on one device take the shared array in turn.
+std::mutex g_call_mu[kMaxDevices];
 
 }  // namespace
 
 namespace sile_rt {
 
-// The current device's address of `scratch`, looked up once per device.
-int noalloc_scratch(void** out) {
+// The current device's address of `scratch`, looked up once per device;
+// *dev_out is the current device.
+int noalloc_scratch(void** out, int* dev_out) {
   int dev = 0;
   SILE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev_out) *dev_out = dev;
   if (dev < 0 || dev >= kMaxDevices)
     return fail(SILE_ERR_INVALID_DEVICE, "device %d beyond the %d the scratch table covers", dev,
                 kMaxDevices);
@@ -78,16 +83,26 @@ extern "C" int sile_hip_launch_tiles_noalloc(sile_hip_function fn, void* const* 
   if (programs > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "too many programs (%lld)", (long long)programs);
   if (programs == 0) return ok();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The call waits for its launch (a capturing stream cannot be waited on) and
+  // copies its tables from the stack (a captured copy would read them again
+  // after the call returned): both rule out graph capture.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  SILE_HIP_CHECK(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND,
+                "the no-allocation launch is synchronous and cannot run on a capturing stream");
   void* table = nullptr;
-  int rc = noalloc_scratch(&table);
+  int dev = 0;
+  int rc = noalloc_scratch(&table, &dev);
   if (rc != SILE_OK) return rc;
+  std::lock_guard<std::mutex> lk(g_call_mu[dev]);
   // host image of the tables on the stack (no heap allocation either)
   unsigned char host[kNoallocScratchBytes];
   const size_t buf_bytes = (size_t)num_buffers * sizeof(void*);
   const size_t shp_bytes = (size_t)num_shapes * sizeof(int64_t);
   if (buf_bytes) memcpy(host, buffers, buf_bytes);
   if (shp_bytes) memcpy(host + buf_bytes, shapes, shp_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (buf_bytes + shp_bytes)
     SILE_HIP_CHECK(hipMemcpyAsync(table, host, buf_bytes + shp_bytes, hipMemcpyHostToDevice, s));
   void* dev_buffers = table;

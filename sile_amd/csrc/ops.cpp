@@ -59,8 +59,9 @@ struct GemmArgs {
 //   they finish, the second launch reading them and writing C (both at
 //   5.2 TB/s), and 4 us of launch and ordering; it is taken only for a
 //   modelled gain above 5 %.
-// Largest fp32 planes the transposed GEMM form keeps in the device scratch
-// (the split form stays below 4 * CUs * 65536 bytes by construction).
+// Largest fp32 planes a GEMM keeps in the device scratch: the transposed
+// form's and a forced split's are checked against it; the split the planner
+// chooses stays below 4 * CUs * 65536 bytes (64 MiB) by construction.
 constexpr int64_t kScratchPlanesMax = 256ll << 20;
 
 struct GemmPlan {
@@ -433,6 +434,11 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (half_steps > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM K too large");
   GemmPlan plan = gemm_plan(rm, rn, kp, half_steps, (int64_t)cb, fp8, tile_req);
   if (splits_req) plan.splits = splits_req;
+  if (splits_req > 1 && (double)splits_req * (double)rm * (double)rn * 4.0 > (double)kScratchPlanesMax)
+    return fail(SILE_ERR_SHAPE,
+                "%d k-ranges of %lld x %lld fp32 planes exceed the %lld MiB of device scratch a "
+                "GEMM may use", splits_req, (long long)rm, (long long)rn,
+                (long long)(kScratchPlanesMax >> 20));
   if (capturing) plan.splits = 1;
   if (transposed) plan.splits = std::max<int64_t>(1, std::min(plan.splits, kScratchPlanesMax / (rm * rn * 4)));
   const int64_t tiles_m = (rm + plan.tile - 1) / plan.tile;
@@ -655,6 +661,9 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
   if (cols == 0) return fail(SILE_ERR_SHAPE, "reduce over an empty row");
   if (!x || !out) return fail(SILE_ERR_SHAPE, "NULL operand");
   if (ldx < cols) return fail(SILE_ERR_SHAPE, "leading dimension smaller than cols");
+  // the max kernels carry the column of each partial maximum in 32 bits
+  if (op == SILE_REDUCE_MAX && cols > 0x7fffffffLL)
+    return fail(SILE_ERR_SHAPE, "row max over more than 2^31 - 1 columns");
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
   int iop = (int)op;

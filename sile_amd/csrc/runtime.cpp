@@ -256,7 +256,7 @@ int sile_hip_init(int ordinal) {
   if (rc != SILE_OK) return rc;
   // set-up of the no-allocation launch: this device's address of its tables
   void* scratch = nullptr;
-  rc = noalloc_scratch(&scratch);
+  rc = noalloc_scratch(&scratch, nullptr);
   if (rc != SILE_OK) return rc;
   return ok();
 }

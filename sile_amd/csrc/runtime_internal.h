@@ -46,7 +46,7 @@ int get_function(Module m, const char* name, hipFunction_t* out);
 int resident_blocks(Module m, const char* name, int block_threads, int64_t* out);
 // The current device's address of the no-allocation launch's table array
 // (launch_noalloc.hip); looked up once per device.
-int noalloc_scratch(void** out);
+int noalloc_scratch(void** out, int* dev_out);
 // The matmul DSL kernel with the sile_kernel_<name> tile semantics
 // (buffers a, b, c; shapes of a, b, c: 6 values), each cell's chain seeded
 // from `seed` (an accumulator source of shape seed_shape[2], the same tile of
@@ -56,7 +56,7 @@ int kernel_matmul_seeded(void* const* buffers, int64_t num_threadgroups, int64_t
                          const float* seed, const int64_t* seed_shape, float seed_value,
                          hipStream_t s);
 // Device scratch shared by the calls on one device (the split-K GEMM's fp32
-// partials, at most 64 MiB): scratch_acquire makes stream s wait for the
+// partials and the transposed form's planes, at most 256 MiB): scratch_acquire makes stream s wait for the
 // kernels of the previous user (an event, so calls on different streams are
 // ordered on the GPU, not on the host), and returns at least `bytes` of it;
 // the caller launches its kernels on s and then calls scratch_release, which

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 from oracle import cpuref
-from tests.helpers import assert_close, bf16_round, f16_round, rng, say
+from tests.helpers import (assert_close, assert_same_bits, bf16_round, f16_round,
+                           max_fold_probe_rows, rng, say)
 
 pytestmark = pytest.mark.gpu
 
@@ -156,7 +157,7 @@ def test_softmax_extremes(hip):
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("cols", [8192, 1000, 13, 4, 100, 256, 16384, 65537, (1 << 20) + 5])
 def test_reduce_rows(hip, dt, cols):
-    """Row max (bit-identical: order-independent) and row sum (within
+    """Row max (bit-identical to the reference's fold) and row sum (within
     1e-5 of the row's absolute sum) for every kernel: kL lanes per row up to
     32 chunks, a wave per row, a 1024-thread workgroup per row for few wide
     rows (16384, and 65537 with a ragged end)."""
@@ -176,7 +177,7 @@ def test_reduce_rows(hip, dt, cols):
     dout = hip.DeviceBuffer(rows * 4)
     hip.reduce_rows(hip.REDUCE_MAX, t, rows, cols, dx.ptr, cols, dout.ptr)
     hip.synchronize()
-    # max is order-independent: bit-identical to the reference's fold
+    # the max is the reference's fold from x0, bit for bit
     np.testing.assert_array_equal(dout.download(np.float32, (rows,)),
                                   cpuref.reduce_rows(xf, cpuref.REDUCE_MAX))
     hip.reduce_rows(hip.REDUCE_SUM, t, rows, cols, dx.ptr, cols, dout.ptr)
@@ -275,3 +276,38 @@ def test_reduce_rows_fused_sum_order_probes(hip):
     want = cpuref.reduce_rows(x, cpuref.REDUCE_SUM_VEC4)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     assert got[0] == big + 2 and not np.signbit(got[1]) and got[1] == 0.0 and got[2] == cols
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("cols,pitch_pad", [
+    (13, 0), (100, 0), (256, 0),   # kL lanes per row (f32 up to 128, 16-bit up to 256)
+    (1000, 0), (8192, 0),          # a wave per row, 16-byte chunks
+    (1000, 1), (37, 1),            # a wave per row, element loads (pitch not 16-byte aligned)
+    (16384, 0), (65537, 0),        # a 1024-thread workgroup per row
+])
+def test_reduce_rows_max_follows_the_fold(hip, dt, cols, pitch_pad):
+    """Row max with NaN, -inf and +0 / -0 ties, bit-exact against the oracle's
+    fold (reduce.rs:10-30) through every max kernel; NaN matches NaN."""
+    x = max_fold_probe_rows(cols, cols + pitch_pad)
+    rows = x.shape[0]
+    ldx = cols + pitch_pad
+    say(f"reduce_rows max special values {dt} {rows}x{cols} ldx={ldx}")
+    xp = np.full((rows, ldx), 7.0, np.float32)
+    xp[:, :cols] = x
+    if dt == "f16":
+        xb, xf = f16_round(xp)
+        t = hip.F16
+    elif dt == "bf16":
+        xb, xf = bf16_round(xp)
+        t = hip.BF16
+    else:
+        xb = xf = xp
+        t = hip.F32
+    dx = hip.DeviceBuffer.from_array(xb)
+    dout = hip.DeviceBuffer(rows * 4)
+    hip.reduce_rows(hip.REDUCE_MAX, t, rows, cols, dx.ptr, ldx, dout.ptr)
+    hip.synchronize()
+    got = dout.download(np.float32, (rows,))
+    ref = cpuref.reduce_rows(np.ascontiguousarray(xf), cpuref.REDUCE_MAX, cols=cols)
+    assert np.isnan(ref[0]) and not np.isnan(ref[1])
+    assert_same_bits(got, ref, what=f"row max {dt} {cols}")

@@ -14,7 +14,7 @@ import pytest
 
 from oracle import cpuref
 from tests import tile_ir_text as T
-from tests.helpers import assert_close, rng, say
+from tests.helpers import assert_close, assert_same_bits, max_fold_probe_rows, rng, say
 
 pytestmark = pytest.mark.gpu
 
@@ -150,3 +150,18 @@ def test_parallel_reduce_reference_fixture(hip, fixtures):
     _, got = _run(hip, _golden_text("parallel_reduce_1000.tir"), [a, out], programs,
                   hip.ROUTE_ATOMIC_REDUCE)
     assert got[0] == fx["expected"]
+
+
+@pytest.mark.parametrize("cols,bm", [(1000, 4), (8192, 1), (100, 2)])
+def test_row_max_route_follows_the_fold(hip, cols, bm):
+    """The routed row max on rows with NaN, -inf and +0 / -0 ties is the
+    reference's fold from x0 bit for bit (NaN matches NaN)."""
+    x = max_fold_probe_rows(cols, 3 * cols)
+    rows = x.shape[0] - x.shape[0] % bm
+    x = np.ascontiguousarray(x[:rows])
+    say(f"tile ir row_max special values {rows}x{cols} BM={bm}")
+    y0 = np.full((rows, 1), 11.0, np.float32)
+    _, got = _run(hip, T.row_reduce(bm, cols, "max", 2), [x, y0], rows // bm,
+                  hip.ROUTE_REDUCE_ROWS)
+    assert_same_bits(got.reshape(rows), cpuref.reduce_rows(x, cpuref.REDUCE_MAX),
+                     what="routed row max")

@@ -132,6 +132,35 @@ def test_reduce_rows_max_and_sequential_sum():
     np.testing.assert_array_equal(cpuref.reduce_rows(x, cpuref.REDUCE_SUM), seq)
 
 
+def test_reduce_rows_max_special_values():
+    """The reference's ReduceMax folds acc = x0; acc = (x > acc) ? x : acc
+    (reduce.rs:10-30), which fixes these cases: NaN at column 0 gives NaN, a
+    NaN later never replaces acc, an all -inf row gives -inf, and of a +0 / -0
+    tie the first in row order is kept.  numpy's max (NaN-propagating, tie
+    sign unspecified) differs on them, so each case is a closed form."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rows = [
+        ([nan, 1, 2, 3], nan),
+        ([1, nan, 3, 2], 3.0),
+        ([nan] * 4, nan),
+        ([-inf] * 4, -inf),
+        ([-inf, nan, nan, nan], -inf),
+        ([-1, -0.0, 0.0, -2], -0.0),
+        ([-1, 0.0, -0.0, -2], 0.0),
+        ([-0.0, -5, 0.0, 0.0], -0.0),
+        ([nan, inf, 0.0, -inf], nan),
+        ([5, inf, nan, inf], inf),
+    ]
+    x = np.array([r for r, _ in rows], np.float32)
+    got = cpuref.reduce_rows(x, cpuref.REDUCE_MAX)
+    for (_, want), g in zip(rows, got):
+        want = np.float32(want)
+        if np.isnan(want):
+            assert np.isnan(g)
+        else:
+            assert g.view(np.uint32) == want.view(np.uint32), (g, want)
+
+
 def _ones_vec4_sum(extent, past_end):
     """Closed form of the reference's fused vec4 sum over a row of ones
     (fused_reduce.rs:1182-1256 with single_axis.rs:180-260): the loop form
