@@ -356,7 +356,31 @@ def bench_softmax(name, steps, warmup, stream, traffic, cpu=False):
                            "unit": "GB/s", "ms_per_step": round(copy_ms, 4),
                            "frac_of_peak": round(ceiling / PEAK_HBM_GBS, 4)}
     res["frac_of_copy_ceiling"] = round(res["value"] / ceiling, 4)
-    for buf in xs + ys:
+    # each direction of that traffic alone, at the same bytes per launch
+    # (256 MiB, over four rotating buffers of their own): the write-only
+    # stream (a splat stored to [2 rows, cols] f16, sile_hip_fill_rows) and
+    # the read-only stream (the row max of what it wrote, sile_hip_reduce_rows,
+    # on the softmax's row shape: one 8192-element row per 512-thread
+    # workgroup)
+    zs = [hip.DeviceBuffer(int(nbytes)) for _ in range(rotate)]
+    outs = [hip.DeviceBuffer(2 * rows * 4) for _ in range(rotate)]
+    streams = {}
+    for kind, fn, kernel in (
+            ("write_stream", lambda i: hip.fill_rows(hip.F16, 2 * rows, cols, 0.5, zs[i].ptr,
+                                                     cols, stream),
+             "sile_fill_flat_b128"),
+            ("read_stream", lambda i: hip.reduce_rows(hip.REDUCE_MAX, hip.F16, 2 * rows, cols,
+                                                      zs[i].ptr, cols, outs[i].ptr, stream),
+             "sile_reduce_rows_f16_b512")):
+        log(f"[bench] {name}: timing the {kind.replace('_', ' ')} ({steps} steps)")
+        ms = time_launches(fn, steps, warmup, stream, rotate=rotate) / steps
+        rate = nbytes / (ms * 1e-3) / 1e9
+        streams[kind] = rate
+        res[kind] = {"kernel": kernel, "value": round(rate, 2), "unit": "GB/s",
+                     "bytes_per_launch": nbytes, "ms_per_step": round(ms, 4),
+                     "frac_of_peak": round(rate / PEAK_HBM_GBS, 4)}
+    res["frac_of_best_stream"] = round(res["value"] / max(ceiling, *streams.values()), 4)
+    for buf in xs + ys + zs + outs:
         buf.close()
     if x32 is not None:
         from oracle import cpuref

@@ -340,6 +340,17 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
 int sile_hip_copy_rows(int64_t rows, int64_t row_bytes, const void *x, int64_t ldx_bytes,
                        void *y, int64_t ldy_bytes, sile_hip_stream stream);
 
+/* y[r][c] = value (rounded to nearest even for f16 / bf16) for r < rows,
+ * c < cols, rows at pitch ldy elements: the store of a splat tile, DSL
+ * `y.store(sile::constant(value, [BM, BN]))` (Splat,
+ * crates/sile-tile-ir/src/lower.rs:509-524, stored by
+ * crates/sile-tile-ir/src/passes/lowering/tile_memory.rs:114-162).  type:
+ * f32, f16, bf16.  Write-only: contiguous 16-byte aligned rows are written in
+ * the copy's shape (non-temporal 16-byte stores), the rate that bounds the
+ * write half of the row softmax. */
+int sile_hip_fill_rows(sile_dtype type, int64_t rows, int64_t cols, float value, void *y,
+                       int64_t ldy, sile_hip_stream stream);
+
 /* fp32 row sums in the order of the reference's fused load + reduce: the
  * CPU backend's sum of a tile it reads straight from a buffer
  * (crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:31-177,
@@ -352,6 +363,23 @@ int sile_hip_copy_rows(int64_t rows, int64_t row_bytes, const void *x, int64_t l
  * row-sum route runs on this entry point. */
 int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float *x, int64_t ldx,
                                    int64_t x_len, float *out, sile_hip_stream stream);
+
+/* fp32 attention with K given transposed, the attention program of sile's
+ * DSL: per query row, over keys 0 .. n_k - 1 in order, s = (q . kt[:, j]) *
+ * scale, an online softmax whose running max starts at m0 and is updated as
+ * m_new = m >= rowmax ? m : rowmax, o = (sum_j p_j v[j]) / l.  No single
+ * counterpart in the reference: it composes the ops the DSL program uses
+ * (mma, tile_compute/mma.rs:25-739; max_tile, crates/sile-tile-ir/src/lower.rs:619-641;
+ * reduce_max / reduce_sum, tile_compute/reduce.rs:10-112; exp, broadcast and
+ * the pointwise maps, tile_expr.rs:646-813) and is the kernel the Tile IR
+ * router sends that program to.  q [n_q, ldq], kt [head_dim, ldkt] (key j,
+ * dim t at kt[t * ldkt + j]), v [n_k, ldv], o [n_q, ldo]; head_dim <= 128;
+ * results within fp32 rounding of the program (sums in another order; exp
+ * is the device's). */
+int sile_hip_attention_f32_kt(int64_t n_q, int64_t n_k, int64_t head_dim, const float *q,
+                              int64_t ldq, const float *kt, int64_t ldkt, const float *v,
+                              int64_t ldv, float *o, int64_t ldo, float scale, float m0,
+                              sile_hip_stream stream);
 
 /* Flash-attention forward, O = softmax(Q K^T * scale [+ causal mask]) V with
  * fp32 online-softmax state.  Q, K, V, O are [B, H, S, D] contiguous, f16 or
@@ -381,7 +409,9 @@ typedef enum {
   SILE_ROUTE_SOFTMAX_ROWS = 2,  /* softmax chain, one tile per row band -> sile_hip_softmax_rows */
   SILE_ROUTE_SOFTMAX_TILES = 3, /* softmax chain, other tilings -> sile_hip_kernel_softmax */
   SILE_ROUTE_REDUCE_ROWS = 4,   /* load + reduce(axis 1) + store -> sile_hip_reduce_rows */
-  SILE_ROUTE_ATOMIC_REDUCE = 5  /* load + sum + extract + atomic add -> sile_hip_kernel_parallel_reduce */
+  SILE_ROUTE_ATOMIC_REDUCE = 5, /* load + sum + extract + atomic add -> sile_hip_kernel_parallel_reduce */
+  SILE_ROUTE_ATTENTION = 6      /* the DSL's online-softmax attention loop (K transposed)
+                                   -> sile_hip_attention_f32_kt */
 } sile_route_kind;
 
 typedef struct {
@@ -394,11 +424,14 @@ typedef struct {
   int32_t num_buffers;       /* buffer parameters of the kernel */
   int32_t seed_from_tile;    /* SILE_ROUTE_MATMUL: 1 = accumulator loaded from operand 3 */
   float seed_value;          /* SILE_ROUTE_MATMUL: the accumulator's splat value otherwise */
+  float attn_scale;          /* SILE_ROUTE_ATTENTION: the score scale (1 without one) */
+  float attn_m0;             /* SILE_ROUTE_ATTENTION: the running max's initial value */
   int64_t num_shapes;        /* shape values the route was made with */
   int64_t operand_shapes[8]; /* the operands' dims the route was made for */
   int64_t num_threadgroups;  /* the grid the route was made for */
-  int64_t tile_m, tile_n, tile_k; /* BM, BN, BK (TILE in tile_n for the atomic reduce) */
-  int64_t rows, cols;        /* extents handed to the row kernels */
+  int64_t tile_m, tile_n, tile_k; /* BM, BN, BK (TILE in tile_n for the atomic reduce;
+                                      BM, BN, D for attention) */
+  int64_t rows, cols;        /* extents handed to the row kernels; attention: queries, keys */
   char reason[512];          /* SILE_ROUTE_NONE: why each detector declined */
 } sile_hip_route;
 

@@ -60,6 +60,9 @@ def lib() -> ctypes.CDLL:
         L.cpuref_softmax_rows.argtypes = [_P, _P, _I64, _I64, _I64, _I64]
         L.cpuref_attention_fwd.argtypes = [_P, _P, _P, _P, _I64, _I64, ctypes.c_float,
                                            ctypes.c_int, _I64, _I64]
+        L.cpuref_dsl_attention_f32.argtypes = [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64,
+                                               _I64, _I64, ctypes.c_float, ctypes.c_float,
+                                               _I64, _I64]
         L.cpuref_bf16_from_f32.argtypes = [_P, _P, _I64]
         L.cpuref_f32_from_bf16.argtypes = [_P, _P, _I64]
         L.cpuref_e4m3_encode.argtypes = [_P, _P, _I64, ctypes.c_float]
@@ -190,6 +193,21 @@ def attention_fwd(q, k, v, scale, causal=True, q_begin=0, q_end=None, out=None):
     o = np.zeros((s, d), dtype=np.float32) if out is None else out
     lib().cpuref_attention_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s, d, float(scale),
                                1 if causal else 0, q_begin, q_end)
+    return o
+
+
+def dsl_attention_f32(q, kt, v, bn, scale, m0, d=None, n_q=None, s_k=None):
+    """The DSL attention program (K transposed, no mask) over rows 0..n_q of
+    q [*, ldq], kt [D, ldkt], v [*, ldv]; keys 0 .. (s_k / bn) * bn, where s_k
+    defaults to kt's column count.  Returns o [n_q, d]."""
+    q, kt, v = _f32(q), _f32(kt), _f32(v)
+    d = kt.shape[0] if d is None else d
+    n_q = q.shape[0] if n_q is None else n_q
+    s_k = kt.shape[1] if s_k is None else s_k
+    o = np.zeros((n_q, d), dtype=np.float32)
+    lib().cpuref_dsl_attention_f32(_ptr(q), q.shape[1], _ptr(kt), kt.shape[1], _ptr(v),
+                                   v.shape[1], _ptr(o), d, d, s_k, bn, float(scale), float(m0),
+                                   0, n_q)
     return o
 
 

@@ -34,6 +34,10 @@
  *   cpuref_attention_causal       pinned by closed forms and fp64 brute force only; the
  *                                 reference has no attention kernel (no mask/iota/transpose
  *                                 in its DSL), so there is no reference vector for it.
+ *   cpuref_dsl_attention_f32      pinned by fp64 brute force (any initial max below the
+ *                                 scores), key truncation to whole BN blocks, the initial
+ *                                 max's underflow closed form (m0 above every score: 0 / 0),
+ *                                 and agreement with cpuref_attention_fwd (non-causal)
  *   cpuref_e4m3_encode/decode     pinned (OCP e4m3fn table: 448 max, 2^-9 min subnormal,
  *                                 exhaustive decode/encode round trip of all 254 finite codes)
  *   cpuref_bf16_from_f32          pinned (RNE vs exhaustive cases and numpy bit tricks)
@@ -388,6 +392,79 @@ void cpuref_parallel_reduce_partials(const float *a, float *partials, int64_t pr
 /* ------------------------------------------------------------------------ */
 /* a9: causal attention forward (new; no reference kernel).                  */
 /* ------------------------------------------------------------------------ */
+
+/* The attention program written in sile's DSL (no causal mask: the DSL has
+ * no iota or select on indices), K given transposed as kt [D, S_k]:
+ *
+ *   let pid = tile::id().0;
+ *   let qt = q.load_tile([BM, D], [pid, 0]);
+ *   let mut m = <m0 splat [BM, 1]>; let mut l = constant(0.0, [BM, 1]);
+ *   let mut acc = constant(0.0, [BM, D]);
+ *   for j in 0..kt.shape()[1] / BN {
+ *       let s = mma(qt, kt.load_tile([D, BN], [0, j]), constant(0.0, [BM, BN]))
+ *               * constant(scale, [BM, BN]);
+ *       let m_new = max_tile(m, reduce_max(s, 1));
+ *       let p = exp(s - m_new.broadcast([BM, BN]));
+ *       let alpha = exp(m - m_new);
+ *       l = l * alpha + reduce_sum(p, 1);
+ *       acc = mma(p, v.load_tile([BN, D], [j, 0]), acc * alpha.broadcast([BM, D]));
+ *       m = m_new;
+ *   }
+ *   o.store(acc / l.broadcast([BM, D]));
+ *
+ * with the reference's op semantics: mma = a per-cell chain from its seed,
+ * s = s + a*b in increasing k with two roundings (tile_compute/mma.rs:25-739);
+ * max_tile(a, b) = a >= b ? a : b (crates/sile-tile-ir/src/lower.rs:619-641);
+ * the row max and row sum are the folds from element 0 (reduce.rs:10-112);
+ * exp = expf; the maps round each operation.  Rows q_begin..q_end of
+ * q [*, ldq], kt [D, ldkt], v [*, ldv], o [*, ldo]; keys
+ * 0 .. (s_k / bn) * bn (the loop bound truncates). */
+void cpuref_dsl_attention_f32(const float *q, int64_t ldq, const float *kt, int64_t ldkt,
+                              const float *v, int64_t ldv, float *o, int64_t ldo, int64_t d,
+                              int64_t s_k, int64_t bn, float scale, float m0, int64_t q_begin,
+                              int64_t q_end) {
+  const int64_t blocks = s_k / bn;
+#pragma omp parallel
+  {
+    float *sc = (float *)__builtin_malloc((size_t)bn * sizeof(float));
+    float *acc = (float *)__builtin_malloc((size_t)d * sizeof(float));
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t i = q_begin; i < q_end; ++i) {
+      const float *qi = q + i * ldq;
+      float m = m0, l = 0.0f;
+      for (int64_t t = 0; t < d; ++t) acc[t] = 0.0f;
+      for (int64_t j = 0; j < blocks; ++j) {
+        for (int64_t c = 0; c < bn; ++c) {
+          float sum = 0.0f;
+          for (int64_t t = 0; t < d; ++t) {
+            float prod = qi[t] * kt[t * ldkt + j * bn + c];
+            sum = sum + prod;
+          }
+          sc[c] = sum * scale;
+        }
+        const float rmax = reduce_row_seq(sc, bn, 1);
+        const float m_new = m >= rmax ? m : rmax;
+        for (int64_t c = 0; c < bn; ++c) sc[c] = expf(sc[c] - m_new);
+        const float alpha = expf(m - m_new);
+        const float rsum = reduce_row_seq(sc, bn, 0);
+        const float la = l * alpha;
+        l = la + rsum;
+        for (int64_t t = 0; t < d; ++t) {
+          float a = acc[t] * alpha;
+          for (int64_t c = 0; c < bn; ++c) {
+            float prod = sc[c] * v[(j * bn + c) * ldv + t];
+            a = a + prod;
+          }
+          acc[t] = a;
+        }
+        m = m_new;
+      }
+      for (int64_t t = 0; t < d; ++t) o[i * ldo + t] = acc[t] / l;
+    }
+    __builtin_free(acc);
+    __builtin_free(sc);
+  }
+}
 
 /* Naive fp32 causal attention for one (batch, head) slice, queries
  * [q_begin, q_end).  Q, K, V, O are [S, D] row-major.  For query i:

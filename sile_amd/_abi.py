@@ -64,10 +64,10 @@ class DeviceProps(ctypes.Structure):
 
 
 ROUTE_NONE, ROUTE_MATMUL, ROUTE_SOFTMAX_ROWS, ROUTE_SOFTMAX_TILES, ROUTE_REDUCE_ROWS, \
-    ROUTE_ATOMIC_REDUCE = range(6)
+    ROUTE_ATOMIC_REDUCE, ROUTE_ATTENTION = range(7)
 ROUTE_NAMES = {ROUTE_NONE: "none", ROUTE_MATMUL: "matmul", ROUTE_SOFTMAX_ROWS: "softmax_rows",
                ROUTE_SOFTMAX_TILES: "softmax_tiles", ROUTE_REDUCE_ROWS: "reduce_rows",
-               ROUTE_ATOMIC_REDUCE: "atomic_reduce"}
+               ROUTE_ATOMIC_REDUCE: "atomic_reduce", ROUTE_ATTENTION: "attention"}
 
 
 class Route(ctypes.Structure):
@@ -81,6 +81,8 @@ class Route(ctypes.Structure):
         ("num_buffers", ctypes.c_int32),
         ("seed_from_tile", ctypes.c_int32),
         ("seed_value", ctypes.c_float),
+        ("attn_scale", ctypes.c_float),
+        ("attn_m0", ctypes.c_float),
         ("num_shapes", ctypes.c_int64),
         ("operand_shapes", ctypes.c_int64 * 8),
         ("num_threadgroups", ctypes.c_int64),
@@ -146,7 +148,10 @@ SIGNATURES = {
     "sile_hip_reduce_rows": [_I32, _I32, _I64, _I64, _P, _I64, _P, _P],
     "sile_hip_reduce_rows_fused_sum": [_I64, _I64, _P, _I64, _I64, _P, _P],
     "sile_hip_copy_rows": [_I64, _I64, _P, _I64, _P, _I64, _P],
+    "sile_hip_fill_rows": [_I32, _I64, _I64, _F32, _P, _I64, _P],
     "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
+    "sile_hip_attention_f32_kt": [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _F32,
+                                  _F32, _P],
     "sile_hip_tile_ir_route": [ctypes.c_char_p, _P, _I64, _I64, ctypes.POINTER(Route)],
     "sile_hip_tile_ir_launch": [ctypes.POINTER(Route), _P, _I64, _P, _I64, _I64, _P],
 }
@@ -468,6 +473,10 @@ def reduce_rows_fused_sum(rows, cols, x, ldx, x_len, out, stream=None):
     call("sile_hip_reduce_rows_fused_sum", rows, cols, x, ldx, x_len, out, _sh(stream))
 
 
+def fill_rows(dtype, rows, cols, value, y, ldy, stream=None):
+    call("sile_hip_fill_rows", dtype, rows, cols, value, y, ldy, _sh(stream))
+
+
 def copy_rows(rows, row_bytes, x, ldx_bytes, y, ldy_bytes, stream=None):
     call("sile_hip_copy_rows", rows, row_bytes, x, ldx_bytes, y, ldy_bytes, _sh(stream))
 
@@ -476,6 +485,12 @@ def flash_attn_fwd(dtype, batch, heads, seq_len, head_dim, q, k, v, o, scale, ca
                    stream=None):
     call("sile_hip_flash_attn_fwd", dtype, batch, heads, seq_len, head_dim, q, k, v, o, scale,
          1 if causal else 0, _sh(stream))
+
+
+def attention_f32_kt(n_q, n_k, head_dim, q, ldq, kt, ldkt, v, ldv, o, ldo, scale, m0,
+                     stream=None):
+    call("sile_hip_attention_f32_kt", n_q, n_k, head_dim, q, ldq, kt, ldkt, v, ldv, o, ldo, scale,
+         m0, _sh(stream))
 
 
 def dtype_bytes(t: int) -> int:

@@ -121,6 +121,20 @@ SILE_DEV float wave_sum(float v) {
   return pair32_sum(v);
 }
 
+// max and sum over each 16-lane row of the wave (all 16 lanes hold the result)
+SILE_DEV float group_max16(float v) {
+  v = fmax_ordered(v, dpp<kDppXor1>(v));
+  v = fmax_ordered(v, dpp<kDppXor2>(v));
+  v = fmax_ordered(v, dpp<kDppHalfMirror>(v));
+  return fmax_ordered(v, dpp<kDppMirror>(v));
+}
+SILE_DEV float group_sum16(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v + dpp<kDppMirror>(v);
+}
+
 // ---- the reference's row max, computed in parallel ----
 // ReduceMax folds from the row's first element, acc = x0; acc = x > acc ? x : acc
 // (crates/sile-tile-ir/src/passes/lowering/tile_compute/reduce.rs:10-30), so

@@ -783,6 +783,60 @@ __device__ __forceinline__ void reduce_rows_block_kernel(int op, const void* x, 
   }
 }
 
+// Rows of exactly 2 * kT chunks (the softmax's row-block widths): one row per
+// workgroup of kT threads, both chunks of a thread loaded before either is
+// folded (chunk j of thread t at column (j * kT + t) * E, folded in column
+// order), wave all-reductions and one exchange of the per-wave partials.
+template <int kIn, int kT>
+__device__ __forceinline__ void reduce_rows_rowblock_kernel(int op, const void* x, float* out,
+                                                            int64_t rows, int64_t ldx) {
+  constexpr int kE = chunk_elems<kIn, kF32>();
+  constexpr int kWaves = kT / 64;
+  __shared__ float part[kWaves];
+  __shared__ int part_col[kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  using TI = typename Elem<kIn>::Storage;
+  const TI* xr = static_cast<const TI*>(x) + row * ldx;
+  float v[2][kE];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) load_chunk<kIn, kE>(xr + (j * kT + t) * kE, v[j]);
+  if (op == 0) {
+    float m = -__builtin_inff();
+    int mi = kNoCol;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < kE; ++i) first_max_fold(m, mi, v[j][i], (j * kT + t) * kE + i);
+    wave_first_max(m, mi);
+    if (lane == 0) {
+      part[wave] = m;
+      part_col[wave] = mi;
+    }
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) first_max_merge(m, mi, part[w], part_col[w]);
+      out[row] = max_result<kIn>(m, xr);
+    }
+    return;
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) acc = acc + v[j][i];
+  acc = wave_sum(acc);
+  if (lane == 0) part[wave] = acc;
+  __syncthreads();
+  if (t == 0) {
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) acc = acc + part[w];
+    out[row] = acc;
+  }
+}
+
 #define SILE_REDUCE_SHAPES(TAG, IN)                                                           \
   extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_n4(              \
       int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
@@ -803,6 +857,18 @@ __device__ __forceinline__ void reduce_rows_block_kernel(int op, const void* x, 
   extern "C" __global__ __launch_bounds__(1024) void sile_reduce_rows_##TAG##_block(          \
       int op, const void* x, float* out, int64_t rows, int64_t cols, int64_t ldx) {          \
     reduce_rows_block_kernel<IN>(op, x, out, rows, cols, ldx);                              \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(256) void sile_reduce_rows_##TAG##_b256(            \
+      int op, const void* x, float* out, int64_t rows, int64_t ldx) {                       \
+    reduce_rows_rowblock_kernel<IN, 256>(op, x, out, rows, ldx);                            \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(512) void sile_reduce_rows_##TAG##_b512(            \
+      int op, const void* x, float* out, int64_t rows, int64_t ldx) {                       \
+    reduce_rows_rowblock_kernel<IN, 512>(op, x, out, rows, ldx);                            \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(1024) void sile_reduce_rows_##TAG##_b1024(          \
+      int op, const void* x, float* out, int64_t rows, int64_t ldx) {                       \
+    reduce_rows_rowblock_kernel<IN, 1024>(op, x, out, rows, ldx);                           \
   }
 SILE_REDUCE_SHAPES(f32, kF32)
 SILE_REDUCE_SHAPES(f16, kF16)
@@ -939,6 +1005,37 @@ extern "C" __global__ __launch_bounds__(kCopyThreads) void sile_copy_flat_b128(
   for (int j = 0; j < 2; ++j)
     if (c0 + j * kCopyThreads < chunks)
       __builtin_nontemporal_store(w[j], reinterpret_cast<u32x4*>(y) + c0 + j * kCopyThreads);
+}
+
+// ---- tile store of a splat (Splat + StorePtrTko): y[r][c] = v ----
+// The write-only counterpart of the copy: contiguous 16-byte aligned rows are
+// one run of `chunks` 16-byte chunks, each holding the element's bits
+// repeated (`word`: one fp32, or two 16-bit elements), stored non-temporally
+// in the copy's shape (512 threads x 2 chunks per workgroup).
+extern "C" __global__ __launch_bounds__(kCopyThreads) void sile_fill_flat_b128(
+    uint8_t* __restrict__ y, int64_t chunks, uint32_t word) {
+  const int64_t c0 = (int64_t)blockIdx.x * (2 * kCopyThreads) + threadIdx.x;
+  const u32x4 w = {word, word, word, word};
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (c0 + j * kCopyThreads < chunks)
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(y) + c0 + j * kCopyThreads);
+}
+// Any rows, pitch and alignment: one wave per row, one element per lane;
+// `bits` is the element (2 or 4 bytes wide, `eb`).
+extern "C" __global__ __launch_bounds__(256) void sile_fill_rows_elem(uint8_t* y, int64_t rows,
+                                                                     int64_t cols, int64_t ldy,
+                                                                     uint32_t bits, int eb) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  if (eb == 4) {
+    float* yr = reinterpret_cast<float*>(y) + row * ldy;
+    for (int64_t c = lane; c < cols; c += 64) yr[c] = bits_f32(bits);
+  } else {
+    uint16_t* yr = reinterpret_cast<uint16_t*>(y) + row * ldy;
+    for (int64_t c = lane; c < cols; c += 64) yr[c] = (uint16_t)bits;
+  }
 }
 
 // Rows or pitches that are not multiples of 16 bytes: one byte per lane.

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -118,6 +119,31 @@ GemmPlan gemm_plan(int64_t m, int64_t n, int64_t kp, int64_t half_steps, int64_t
     }
   }
   return best.splits > 1 && !(best_t < 0.95 * best_unsplit_t) ? best_unsplit : best;
+}
+
+// fp32 -> 16-bit element bits, round to nearest even (NaN stays a quiet NaN),
+// for fill values converted on the host.
+uint32_t bf16_bits_rne(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (x >> 16) | 0x40u;
+  return (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+}
+uint32_t f16_bits_rne(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return sign | 0x7e00u;
+  if (ax >= 0x477ff000u) return sign | 0x7c00u;  // |f| >= 65520 rounds to inf
+  if (ax < 0x38800000u) {                        // below 2^-14: subnormal (exact scaling)
+    float v;
+    memcpy(&v, &ax, 4);
+    return sign | (uint32_t)nearbyintf(v * 16777216.0f);
+  }
+  uint32_t h = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return sign | h;
 }
 
 const char* dtype_name(int t) {
@@ -684,6 +710,16 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
                     dim3(256), params, s);
     return rc == SILE_OK ? ok() : rc;
   }
+  for (int t : {256, 512, 1024}) {
+    if (vec && cols == (int64_t)t * 2 * elems) {
+      // rows of 2 chunks per thread of a 256 / 512 / 1024-thread workgroup
+      if (rows > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+      snprintf(kname, sizeof kname, "%s_b%d", name, t);
+      void* params[] = {&iop, &x, &out, &rows, &ldx};
+      int rc = launch(Module::kSoftmax, kname, dim3((unsigned)rows), dim3(t), params, s);
+      return rc == SILE_OK ? ok() : rc;
+    }
+  }
   if (vec && cols >= 16384 && rows <= 4096) {
     // few wide rows: a 1024-thread workgroup per row
     snprintf(kname, sizeof kname, "%s_block", name);
@@ -693,6 +729,40 @@ int sile_hip_reduce_rows(sile_reduce_op op, sile_dtype in_type, int64_t rows, in
   }
   void* params[] = {&iop, &vec, &x, &out, &rows, &cols, &ldx};
   int rc = launch(Module::kSoftmax, name, dim3((unsigned)blocks), dim3(256), params, s);
+  return rc == SILE_OK ? ok() : rc;
+}
+
+int sile_hip_fill_rows(sile_dtype type, int64_t rows, int64_t cols, float value, void* y,
+                       int64_t ldy, sile_hip_stream stream) {
+  if (type != SILE_F32 && type != SILE_F16 && type != SILE_BF16)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "fill of %s not supported", dtype_name(type));
+  if (rows < 0 || cols < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (rows == 0 || cols == 0) return ok();
+  if (!y) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldy < cols) return fail(SILE_ERR_SHAPE, "leading dimension smaller than cols");
+  const int eb = (int)dtype_bytes(type);
+  uint32_t bits = 0;
+  if (type == SILE_F32) {
+    memcpy(&bits, &value, 4);
+  } else {
+    bits = type == SILE_BF16 ? bf16_bits_rne(value) : f16_bits_rne(value);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ldy == cols && (cols * eb) % 16 == 0 && aligned16(y)) {
+    int64_t chunks = rows * cols * eb / 16;
+    const int64_t groups = (chunks + 1023) / 1024;
+    if (groups > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "fill too large");
+    uint32_t word = eb == 4 ? bits : bits | (bits << 16);
+    void* params[] = {&y, &chunks, &word};
+    int rc = launch(Module::kSoftmax, "sile_fill_flat_b128", dim3((unsigned)groups), dim3(512),
+                    params, s);
+    return rc == SILE_OK ? ok() : rc;
+  }
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+  void* params[] = {&y, &rows, &cols, &ldy, &bits, (void*)&eb};
+  int rc = launch(Module::kSoftmax, "sile_fill_rows_elem", dim3((unsigned)blocks), dim3(256),
+                  params, s);
   return rc == SILE_OK ? ok() : rc;
 }
 
@@ -767,6 +837,30 @@ int sile_hip_reduce_rows_fused_sum(int64_t rows, int64_t cols, const float* x, i
 // ---------------------------------------------------------------------------
 // Attention
 // ---------------------------------------------------------------------------
+
+int sile_hip_attention_f32_kt(int64_t n_q, int64_t n_k, int64_t head_dim, const float* q,
+                              int64_t ldq, const float* kt, int64_t ldkt, const float* v,
+                              int64_t ldv, float* o, int64_t ldo, float scale, float m0,
+                              sile_hip_stream stream) {
+  if (n_q < 0 || n_k < 0 || head_dim <= 0) return fail(SILE_ERR_SHAPE, "invalid attention shape");
+  if (head_dim > 128)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "fp32 attention: head_dim > 128 not supported");
+  if (n_q == 0) return ok();
+  if (!q || !kt || !v || !o) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldq < head_dim || ldkt < n_k || ldv < head_dim || ldo < head_dim)
+    return fail(SILE_ERR_SHAPE, "leading dimension smaller than the matrix extent");
+  const int64_t blocks = (n_q + 63) / 64;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "attention too large");
+  const int dp = (int)((head_dim + 15) / 16 * 16);
+  char name[64];
+  snprintf(name, sizeof name, "sile_attn_f32_kt_d%d", dp);
+  int d = (int)head_dim;
+  void* params[] = {(void*)&q, &ldq, (void*)&kt, &ldkt, (void*)&v, &ldv, &o, &ldo,
+                    &n_q, &n_k, &d, &scale, &m0};
+  int rc = launch(Module::kAttention, name, dim3((unsigned)blocks), dim3(256), params,
+                  static_cast<hipStream_t>(stream));
+  return rc == SILE_OK ? ok() : rc;
+}
 
 int sile_hip_flash_attn_fwd(sile_dtype dtype, int64_t batch, int64_t heads, int64_t seq_len,
                             int64_t head_dim, const void* q, const void* k, const void* v,

@@ -15,7 +15,9 @@
 //     (crates/sile/examples/softmax.rs:3-16)      whole row, else the tile kernel;
 //   * load + row reduce + store -> the row reduce kernel;
 //   * load + reduce + extract + atomic add -> the parallel-reduce kernel
-//     (crates/sile/examples/parallel_reduce.rs:3-9).
+//     (crates/sile/examples/parallel_reduce.rs:3-9);
+//   * the online-softmax attention loop the DSL can write (K given
+//     transposed, no mask) -> the fp32 attention kernel.
 // A route is taken only where the routed kernel writes exactly the elements,
 // in exactly the tile decomposition, that the CPU backend's launch wrapper
 // writes for the same shapes and grid (crates/sile-backend/src/cpu/codegen.rs:409-555).
@@ -23,6 +25,7 @@
 // the kernel to LLIR and uses the generic code generation.
 #include <algorithm>
 #include <cctype>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -710,10 +713,15 @@ int buffer_index(const Function& fn, uint32_t v) {
 
 // Expands value `v` of block `b` into a map expression, following the
 // pointwise ops the fusion pass folds into maps
-// (crates/sile-tile-ir/src/passes/pointwise_fusion.rs:47-58) and maps
+// (crates/sile-tile-ir/src/passes/pointwise_fusion.rs:47-58), splats, and maps
 // themselves; any other value stays a leaf.  Fused and unfused forms of the
 // same computation give the same tree.
 ExprP expand(const Block& b, uint32_t v, int depth = 0);
+
+// Types of every value of the function being matched (block parameters
+// included), for the source shape of a broadcast of a block parameter; set by
+// detect() for the duration of one detection on this thread.
+thread_local const std::map<uint32_t, Ty>* t_types = nullptr;
 
 ExprP expand_expr(const Block& b, const ExprP& e, int depth) {
   if (depth > 64) no_route("pointwise chain too deep");
@@ -749,13 +757,28 @@ ExprP expand(const Block& b, uint32_t v, int depth) {
     case Op::DivF: return node(Expr::Div, {i->uses[0], i->uses[1]});
     case Op::NegF: return node(Expr::Neg, {i->uses[0]});
     case Op::Exp: return node(Expr::Exp, {i->uses[0]});
+    case Op::Splat: {
+      // a splat reads as its constant, whether the fusion folded it into the
+      // map (single use) or left it standing (several uses)
+      auto e = std::make_shared<Expr>();
+      e->k = Expr::Splat;
+      e->f = i->fval;
+      return e;
+    }
     case Op::Broadcast: {
       auto e = node(Expr::Bcast, {i->uses[0]});
       // the source shape is the source value's tile type (pointwise_fusion.rs:150-163)
       const Inst* src = find_inst(b, i->uses[0]);
-      if (!src || src->ty.k != Ty::Tile) no_route("broadcast of a value without a tile shape");
-      e->rows = src->ty.rows;
-      e->cols = src->ty.cols;
+      Ty st;
+      if (src) {
+        st = src->ty;
+      } else if (t_types) {
+        auto it = t_types->find(i->uses[0]);
+        if (it != t_types->end()) st = it->second;
+      }
+      if (st.k != Ty::Tile) no_route("broadcast of a value without a tile shape");
+      e->rows = st.rows;
+      e->cols = st.cols;
       return e;
     }
     default:
@@ -788,6 +811,7 @@ struct Match {
   bool out_rank1 = false;
   bool seed_from_tile = false;  // matmul: accumulator loaded from ops[3]
   double seed_value = 0.0;      // matmul: the accumulator's splat value otherwise
+  float scale = 1.0f, m0 = 0.0f;  // attention: score scale, initial running max
 };
 
 Operand operand_of(const Function& fn, uint32_t v) {
@@ -1072,14 +1096,270 @@ Match match_atomic_reduce(const Function& fn) {
   return m;
 }
 
+// Structural equality of two expanded map expressions.
+bool same(const ExprP& x, const ExprP& y) {
+  if (x->k != y->k || x->a.size() != y->a.size()) return false;
+  switch (x->k) {
+    case Expr::Value: return x->v == y->v;
+    case Expr::Load:
+      return x->buf == y->buf && x->row == y->row && x->col == y->col && x->rows == y->rows &&
+             x->cols == y->cols && x->stride == y->stride;
+    case Expr::Splat: return x->f == y->f;
+    case Expr::Cmp: if (x->cmp != y->cmp) return false; break;
+    case Expr::Bcast: if (x->rows != y->rows || x->cols != y->cols) return false; break;
+    default: break;
+  }
+  for (size_t i = 0; i < x->a.size(); ++i)
+    if (!same(x->a[i], y->a[i])) return false;
+  return true;
+}
+
+bool is_val(const ExprP& e, uint32_t v) { return e->k == Expr::Value && e->v == v; }
+
+// e = op(l, r) with l and r matching the two predicates in either order
+// (Add and Mul commute).
+template <class L, class R>
+bool commuted(const ExprP& e, Expr::K op, L lhs, R rhs) {
+  if (e->k != op || e->a.size() != 2) return false;
+  return (lhs(e->a[0]) && rhs(e->a[1])) || (lhs(e->a[1]) && rhs(e->a[0]));
+}
+
+// Value of an expression of splats and pointwise ops only, in fp32 with each
+// operation rounded, as the CPU backend evaluates a map
+// (crates/sile-tile-ir/src/passes/lowering/tile_expr.rs:646-813); false if it
+// reads anything else.
+bool const_eval(const ExprP& e, float& out) {
+  float a = 0.0f, b = 0.0f;
+  switch (e->k) {
+    case Expr::Splat: out = (float)e->f; return true;
+    case Expr::Neg:
+      if (!const_eval(e->a[0], a)) return false;
+      out = 0.0f - a;
+      return true;
+    case Expr::Exp:
+      if (!const_eval(e->a[0], a)) return false;
+      out = expf(a);
+      return true;
+    case Expr::Bcast: return const_eval(e->a[0], out);
+    case Expr::Add: case Expr::Sub: case Expr::Mul: case Expr::Div:
+      if (!const_eval(e->a[0], a) || !const_eval(e->a[1], b)) return false;
+      out = e->k == Expr::Add ? a + b : e->k == Expr::Sub ? a - b : e->k == Expr::Mul ? a * b : a / b;
+      return true;
+    default: return false;
+  }
+}
+
+// The value an entry-block loop argument starts from, when it is a constant
+// tile of the given shape (a splat, or a map of splats).
+bool const_tile(const Block& entry, uint32_t v, int64_t rows, int64_t cols, float& out) {
+  const Inst* i = find_inst(entry, v);
+  if (!i || i->ty.k != Ty::Tile || i->ty.rows != rows || i->ty.cols != cols) return false;
+  return const_eval(expand(entry, v), out);
+}
+
+// The attention program of the DSL (online softmax, K given transposed as
+// kt [D, S]; the DSL has no mask, so it is not causal):
+//   qt = load Q[pid0, 0] [BM, D]; m, l, acc = m0, 0, 0 tiles;
+//   for j in 0 .. shape(kt)[1] / BN {
+//     s = mma(qt, load KT[0, j] [D, BN], splat 0) (* splat scale);
+//     m_new = max_tile(m, reduce_max(s, 1));     (select(m >= r, m, r))
+//     p = exp(s - broadcast(m_new)); alpha = exp(m - m_new);
+//     l = l * alpha + reduce_sum(p, 1);
+//     acc = mma(p, load V[j, 0] [BN, D], acc * broadcast(alpha)); m = m_new }
+//   store O[pid0, pid1] <- acc / broadcast(l)
+// with its loop-carried values in any order
+// (find_loop_carried_vars, crates/sile-tile-ir/src/lower.rs:446-465).
+Match match_attention(const Function& fn) {
+  if (fn.blocks.size() != 4) no_route("not an entry / loop header / body / exit function");
+  const Block* entry = fn.block(fn.entry);
+  if (entry->term.k != Term::Br || entry->term.targs.size() != 4)
+    no_route("entry block does not jump into a loop carrying three tiles");
+  if (!is_const(*entry, entry->term.targs[0], 0)) no_route("loop counter does not start at 0");
+  const Block* header = fn.block(entry->term.t);
+  if (!header || header->params.size() != 4) no_route("loop header does not carry (j, three tiles)");
+  const Term& ht = header->term;
+  const std::vector<uint32_t> carried(header->params.begin() + 1, header->params.end());
+  if (ht.k != Term::CondBr || ht.targs != header->params || ht.fargs != carried)
+    no_route("loop header branch arguments are not (j, tiles) / (tiles)");
+  const Block* body = fn.block(ht.t);
+  const Block* exit = fn.block(ht.f);
+  if (!body || !exit || body->params.size() != 4 || exit->params.size() != 3)
+    no_route("loop body / exit do not take the carried tiles");
+  if (body->term.k != Term::Br || body->term.t != header->id || body->term.targs.size() != 4)
+    no_route("loop body does not jump back with (j', tiles')");
+  const uint32_t bj = body->params[0];
+  const Inst* next = find_inst(*body, body->term.targs[0]);
+  if (!next || next->op != Op::IBin || next->sub != "addi" ||
+      !((next->uses[0] == bj && is_const(*body, next->uses[1], 1)) ||
+        (next->uses[1] == bj && is_const(*body, next->uses[0], 1))))
+    no_route("loop step is not j + 1");
+
+  // exit: store O[pid0, pid1] <- acc / broadcast(l)
+  const Inst* st = nullptr;
+  for (const Inst& i : exit->insts) {
+    if (i.op == Op::StoreTko || i.op == Op::AtomicAdd) {
+      if (st) no_route("loop exit holds more than one store");
+      st = &i;
+    }
+  }
+  if (!st || st->op != Op::StoreTko || st->stride != 1 || exit->term.k != Term::Ret)
+    no_route("loop exit does not store a rank-2 tile");
+  const int64_t bm = st->rows, d = st->cols;
+  const ExprP out = expand(*exit, st->uses[1]);
+  uint32_t e_l = 0;
+  if (out->k != Expr::Div || out->a[0]->k != Expr::Value || !bcast_col_of(out->a[1], bm, e_l))
+    no_route("stored value is not acc / broadcast(l)");
+  const uint32_t e_acc = out->a[0]->v;
+  int pa = -1, pl = -1;
+  for (int i = 0; i < 3; ++i) {
+    if (exit->params[i] == e_acc) pa = i;
+    if (exit->params[i] == e_l) pl = i;
+  }
+  if (pa < 0 || pl < 0 || pa == pl) no_route("stored acc / l are not the loop's carried tiles");
+  const int pm = 3 - pa - pl;
+  const uint32_t b_acc = body->params[1 + pa], b_l = body->params[1 + pl],
+                 b_m = body->params[1 + pm];
+  const uint32_t n_acc = body->term.targs[1 + pa], n_l = body->term.targs[1 + pl],
+                 n_m = body->term.targs[1 + pm];
+
+  // m_new = select(m >= rowmax(s), m, rowmax(s))
+  const ExprP mnew = expand(*body, n_m);
+  if (mnew->k != Expr::Select || mnew->a[0]->k != Expr::Cmp || mnew->a[0]->cmp != "ge" ||
+      !is_val(mnew->a[0]->a[0], b_m) || mnew->a[0]->a[1]->k != Expr::Value ||
+      !is_val(mnew->a[1], b_m) || !same(mnew->a[2], mnew->a[0]->a[1]))
+    no_route("carried max is not max_tile(m, reduce_max(s, 1))");
+  const Inst* rmax = find_inst(*body, mnew->a[2]->v);
+  if (!rmax || rmax->op != Op::Reduce || !rmax->is_max || rmax->axis != 1 || rmax->rows != bm)
+    no_route("max_tile's second operand is not a row max");
+  const int64_t bn = rmax->cols;
+  // s = mma(qt, kt tile, 0) [* scale]
+  const ExprP s_tree = expand(*body, rmax->uses[0]);
+  ExprP mma_leaf = s_tree;
+  float scale = 1.0f;
+  if (s_tree->k == Expr::Mul) {
+    const int si = s_tree->a[0]->k == Expr::Splat ? 0 : s_tree->a[1]->k == Expr::Splat ? 1 : -1;
+    if (si < 0) no_route("scores are scaled by something other than a constant");
+    scale = (float)s_tree->a[si]->f;
+    mma_leaf = s_tree->a[1 - si];
+  }
+  if (mma_leaf->k != Expr::Value) no_route("scores are not an mma result");
+  const Inst* smma = find_inst(*body, mma_leaf->v);
+  if (!smma || smma->op != Op::Mma || smma->m != bm || smma->n != bn || smma->k != d)
+    no_route("scores are not mma(Q tile, K^T tile) of [BM, D] x [D, BN]");
+  const Inst* zero = find_inst(*body, smma->uses[2]);
+  if (!zero) zero = find_inst(*entry, smma->uses[2]);
+  if (!zero || zero->op != Op::Splat || zero->fval != 0.0)
+    no_route("score mma does not start from a zero tile");
+  const Inst* lq = find_inst(*entry, smma->uses[0]);
+  if (!lq || lq->op != Op::LoadTko || lq->stride != 1 || lq->rows != bm || lq->cols != d ||
+      launch_dim(fn, lq->uses[1]) != 0 || !is_const(*entry, lq->uses[2], 0))
+    no_route("Q tile is not loaded at (launch 0, 0) before the loop");
+  const Inst* lk = find_inst(*body, smma->uses[1]);
+  if (!lk || lk->op != Op::LoadTko || lk->stride != 1 || lk->rows != d || lk->cols != bn ||
+      !is_const(*body, lk->uses[1], 0) || lk->uses[2] != bj)
+    no_route("K^T tile is not loaded at (0, j)");
+  // loop bound: shape(kt)[1] / BN
+  const Inst* cmp = find_inst(*header, ht.cond);
+  if (!cmp || cmp->op != Op::ICmp || cmp->sub != "lt" || cmp->uses[0] != header->params[0])
+    no_route("loop condition is not j < bound");
+  auto def = [&](uint32_t v) {
+    const Inst* i = find_inst(*header, v);
+    return i ? i : find_inst(*entry, v);
+  };
+  const Inst* div = def(cmp->uses[1]);
+  const Inst* sdim = div && div->op == Op::IBin && div->sub == "divi" ? def(div->uses[0]) : nullptr;
+  const Inst* bnc = div && div->op == Op::IBin && div->sub == "divi" ? def(div->uses[1]) : nullptr;
+  const Param* sdesc = sdim && sdim->op == Op::ShapeDim ? fn.param(sdim->uses[0]) : nullptr;
+  if (!sdim || sdim->ival != 1 || !bnc || bnc->op != Op::ConstI64 || bnc->ival != bn || !sdesc ||
+      sdesc->kind != Param::Shape || sdesc->source != lk->uses[0])
+    no_route("loop bound is not shape(kt)[1] / BN");
+
+  // p = exp(s - broadcast(m_new)); alpha = exp(m - m_new)
+  auto bcast_of = [&](const ExprP& e, const ExprP& src) {
+    return e->k == Expr::Bcast && e->rows == bm && e->cols == 1 && same(e->a[0], src);
+  };
+  auto is_p = [&](const ExprP& e) {
+    return e->k == Expr::Exp && e->a[0]->k == Expr::Sub && same(e->a[0]->a[0], s_tree) &&
+           bcast_of(e->a[0]->a[1], mnew);
+  };
+  auto is_alpha = [&](const ExprP& e) {
+    return e->k == Expr::Exp && e->a[0]->k == Expr::Sub && is_val(e->a[0]->a[0], b_m) &&
+           same(e->a[0]->a[1], mnew);
+  };
+  // acc' = mma(p, V tile, acc * broadcast(alpha))
+  const Inst* pv = find_inst(*body, n_acc);
+  if (!pv || pv->op != Op::Mma || pv->m != bm || pv->n != d || pv->k != bn)
+    no_route("carried acc is not an mma of [BM, BN] x [BN, D]");
+  if (!is_p(expand(*body, pv->uses[0]))) no_route("P is not exp(s - broadcast(m_new))");
+  const Inst* lv = find_inst(*body, pv->uses[1]);
+  if (!lv || lv->op != Op::LoadTko || lv->stride != 1 || lv->rows != bn || lv->cols != d ||
+      lv->uses[1] != bj || !is_const(*body, lv->uses[2], 0))
+    no_route("V tile is not loaded at (j, 0)");
+  if (!commuted(expand(*body, pv->uses[2]), Expr::Mul,
+                [&](const ExprP& e) { return is_val(e, b_acc); },
+                [&](const ExprP& e) { return e->k == Expr::Bcast && e->rows == bm && e->cols == 1 &&
+                                             is_alpha(e->a[0]); }))
+    no_route("PV accumulator is not acc * broadcast(exp(m - m_new))");
+  // l' = l * alpha + reduce_sum(p, 1)
+  const ExprP lnew = expand(*body, n_l);
+  uint32_t rsum_v = 0;
+  const bool l_ok = commuted(
+      lnew, Expr::Add,
+      [&](const ExprP& e) {
+        return commuted(e, Expr::Mul, [&](const ExprP& x) { return is_val(x, b_l); }, is_alpha);
+      },
+      [&](const ExprP& e) {
+        if (e->k != Expr::Value) return false;
+        rsum_v = e->v;
+        return true;
+      });
+  const Inst* rsum = l_ok ? find_inst(*body, rsum_v) : nullptr;
+  if (!rsum || rsum->op != Op::Reduce || rsum->is_max || rsum->axis != 1 || rsum->rows != bm ||
+      rsum->cols != bn || !is_p(expand(*body, rsum->uses[0])))
+    no_route("carried l is not l * alpha + reduce_sum(p, 1)");
+
+  // initial tiles: m = m0 (any constant), l = 0, acc = 0
+  float m0 = 0.0f, l0 = 1.0f, acc0 = 1.0f;
+  if (!const_tile(*entry, entry->term.targs[1 + pm], bm, 1, m0))
+    no_route("running max does not start from a constant tile");
+  if (!const_tile(*entry, entry->term.targs[1 + pl], bm, 1, l0) || l0 != 0.0f ||
+      !const_tile(*entry, entry->term.targs[1 + pa], bm, d, acc0) || acc0 != 0.0f)
+    no_route("l and acc do not start from zero tiles");
+  // the store at the program's tile
+  if (st->uses[2] != lq->uses[1] || launch_dim(fn, st->uses[3]) != 1)
+    no_route("output tile is not stored at (launch 0, launch 1)");
+  if (d > 128) no_route("head dim above 128");
+
+  Match m;
+  m.kind = SILE_ROUTE_ATTENTION;
+  m.ops[0] = operand_of(fn, lq->uses[0]);
+  m.ops[1] = operand_of(fn, lk->uses[0]);
+  m.ops[2] = operand_of(fn, lv->uses[0]);
+  m.ops[3] = operand_of(fn, st->uses[0]);
+  m.nops = 4;
+  for (int i = 0; i < 4; ++i)
+    if (m.ops[i].rank != 2) no_route("attention operand is not rank 2");
+  m.tm = bm;
+  m.tn = bn;
+  m.tk = d;
+  m.scale = scale;
+  m.m0 = m0;
+  return m;
+}
+
 // Tries each detector; collects the reasons of the ones that did not fire.
 Match detect(const Function& fn, std::string& reasons) {
+  struct TypesScope {
+    explicit TypesScope(const std::map<uint32_t, Ty>* t) { t_types = t; }
+    ~TypesScope() { t_types = nullptr; }
+  } scope(&fn.types);
   using Fn = Match (*)(const Function&);
   const std::pair<const char*, Fn> detectors[] = {
       {"matmul", match_matmul},
       {"softmax", match_softmax},
       {"row reduce", match_row_reduce},
       {"atomic reduce", match_atomic_reduce},
+      {"attention", match_attention},
   };
   for (const auto& d : detectors) {
     try {
@@ -1120,7 +1400,25 @@ void plan(const Match& m, const int64_t* shapes, int64_t programs, sile_hip_rout
   r->tile_n = m.tn;
   r->tile_k = m.tk;
   r->rows = r->cols = 0;
-  if (m.kind == SILE_ROUTE_SOFTMAX_TILES) {
+  r->attn_scale = m.scale;
+  r->attn_m0 = m.m0;
+  if (m.kind == SILE_ROUTE_ATTENTION) {
+    // o [n, d'] in tiles of [BM, D]: one column tile, programs take row bands
+    const Operand &q = m.ops[0], &kt = m.ops[1], &v = m.ops[2], &o = m.ops[3];
+    auto decline = [&](const char* why) {
+      r->kind = SILE_ROUTE_NONE;
+      set_reason(r, std::string("attention: ") + why);
+    };
+    if (dim(shapes, o, 1) / m.tk != 1) return decline("output has more than one column tile");
+    const int64_t run = std::max<int64_t>(0, std::min(programs, dim(shapes, o, 0) / m.tm));
+    const int64_t n_keys = (dim(shapes, kt, 1) / m.tn) * m.tn;
+    if (dim(shapes, q, 0) < run * m.tm || dim(shapes, q, 1) < m.tk)
+      return decline("Q does not cover the query tiles");
+    if (dim(shapes, kt, 0) < m.tk || dim(shapes, v, 0) < n_keys || dim(shapes, v, 1) < m.tk)
+      return decline("K^T / V do not cover the key tiles");
+    r->rows = run * m.tm;
+    r->cols = n_keys;
+  } else if (m.kind == SILE_ROUTE_SOFTMAX_TILES) {
     const Operand &x = m.ops[0], &y = m.ops[1];
     const int64_t tiles_n = m.tn > 0 ? dim(shapes, y, 1) / m.tn : 0;
     const int64_t total = m.tm > 0 ? (dim(shapes, y, 0) / m.tm) * tiles_n : 0;
@@ -1222,7 +1520,8 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
                 "%d / %lld", (long long)num_buffers, (long long)num_shapes, route->num_buffers,
                 (long long)route->num_shapes);
   if (!buffers || (num_shapes > 0 && !shapes)) return fail(SILE_ERR_SHAPE, "NULL buffers / shapes");
-  const int nops = route->kind == SILE_ROUTE_MATMUL ? (route->seed_from_tile ? 4 : 3) : 2;
+  const int nops = route->kind == SILE_ROUTE_MATMUL ? (route->seed_from_tile ? 4 : 3)
+                   : route->kind == SILE_ROUTE_ATTENTION ? 4 : 2;
   void* bufs[4] = {nullptr, nullptr, nullptr, nullptr};
   int64_t shp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int64_t nshp = 0;
@@ -1255,6 +1554,15 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
     case SILE_ROUTE_ATOMIC_REDUCE:
       return sile_hip_kernel_parallel_reduce(bufs, num_threadgroups, 1, shp, 2, route->tile_n,
                                              nullptr, stream);
+    case SILE_ROUTE_ATTENTION:
+      // q [q0, q1], kt [k0, k1], v [v0, v1], o [o0, o1]: leading dimensions q1, k1, v1, o1
+      rc = sile_hip_attention_f32_kt(route->rows, route->cols, route->tile_k,
+                                     static_cast<const float*>(bufs[0]), shp[1],
+                                     static_cast<const float*>(bufs[1]), shp[3],
+                                     static_cast<const float*>(bufs[2]), shp[5],
+                                     static_cast<float*>(bufs[3]), shp[7], route->attn_scale,
+                                     route->attn_m0, stream);
+      break;
     case SILE_ROUTE_SOFTMAX_ROWS:
       // x [x0, x1], y [y0, y1]: rows of BN elements at leading dimensions x1 / y1
       rc = sile_hip_softmax_rows(SILE_F32, SILE_F32, route->rows, route->cols, bufs[0], shp[1],

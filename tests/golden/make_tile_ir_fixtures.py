@@ -20,6 +20,9 @@ FIXTURES = {
     "vec_add_4_unfused.tir": T.vec_add(4, passes=False),
     "row_sum_4x64.tir": T.row_reduce(4, 64, "sum"),
     "row_max_4x64_rank1.tir": T.row_reduce(4, 64, "max", out_rank=1),
+    "attention_32x64x128.tir": T.attention(32, 64, 128, 0.08838834764831845),
+    "attention_32x64x128_unfused.tir": T.attention(32, 64, 128, 0.08838834764831845,
+                                                   passes=False),
 }
 
 

@@ -314,3 +314,57 @@ def test_flash_long_sequence(hip, causal):
             p = np.exp(sc - sc.max())
             ref = (p @ vf[0, hi, :n]) / p.sum()
             assert_close(got[0, hi, i], ref, atol=ATOL, rtol=RTOL, what=f"h{hi} row {i}")
+
+
+# ---- fp32 attention with K transposed (the DSL attention program) ----
+
+def _dsl_attn_inputs(n_q, s_k, d, seed, ldq=None, ldkt=None, ldv=None):
+    r = rng(seed)
+    q = np.zeros((n_q, ldq or d), np.float32)
+    kt = np.zeros((d, ldkt or s_k), np.float32)
+    v = np.zeros((s_k, ldv or d), np.float32)
+    q[:, :d] = r.normal(size=(n_q, d))
+    kt[:, :s_k] = r.normal(size=(d, s_k))
+    v[:, :d] = r.normal(size=(s_k, d))
+    return q, kt, v
+
+
+@pytest.mark.parametrize("n_q,n_k,d,pad,m0", [
+    (256, 512, 128, 0, -1e30),
+    (100, 333, 64, 0, -1e30),     # partial query and key blocks
+    (64, 64, 16, 3, 0.0),         # pitched rows; an initial max inside the score range
+    (77, 130, 100, 5, -2.0),      # head dim padded to 112
+    (1, 1, 8, 0, -1e30),
+    (130, 4096, 128, 0, -1e30),
+])
+def test_attention_f32_kt_matches_the_program(hip, n_q, n_k, d, pad, m0):
+    """sile_hip_attention_f32_kt against the oracle of the DSL program (one
+    BN = n_k block: the online softmax is exact in any blocking) within fp32
+    tolerance |g - r| <= 1e-5 + 1e-4 |r|; nothing past each output row's d
+    columns is written."""
+    say(f"attention_f32_kt n_q={n_q} n_k={n_k} d={d} pad={pad} m0={m0}")
+    ldq, ldkt, ldv, ldo = d + pad, n_k + pad, d + pad, d + pad
+    q, kt, v = _dsl_attn_inputs(n_q, n_k, d, n_q + n_k + d, ldq, ldkt, ldv)
+    scale = 1 / np.sqrt(d)
+    o0 = np.full((n_q, ldo), 7.0, np.float32)
+    bufs = [hip.DeviceBuffer.from_array(t) for t in (q, kt, v, o0)]
+    hip.attention_f32_kt(n_q, n_k, d, bufs[0].ptr, ldq, bufs[1].ptr, ldkt, bufs[2].ptr, ldv,
+                         bufs[3].ptr, ldo, scale, m0)
+    hip.synchronize()
+    got = bufs[3].download(np.float32, (n_q, ldo))
+    ref = cpuref.dsl_attention_f32(q, kt, v, n_k, scale, m0, d=d, n_q=n_q, s_k=n_k)
+    assert_close(got[:, :d], ref, atol=1e-5, rtol=1e-4, what="attention f32 kt")
+    assert (got[:, d:] == 7.0).all()
+
+
+def test_attention_f32_kt_closed_forms(hip):
+    """An initial max above every score gives 0 / 0 everywhere, as the
+    program does; no keys gives 0 / 0 too."""
+    say("attention_f32_kt closed forms")
+    q, kt, v = _dsl_attn_inputs(64, 128, 32, 5)
+    bufs = [hip.DeviceBuffer.from_array(t) for t in (q, kt, v, np.zeros((64, 32), np.float32))]
+    for n_k, m0 in ((128, 1e30), (0, -1e30)):
+        hip.attention_f32_kt(64, n_k, 32, bufs[0].ptr, 32, bufs[1].ptr, 128, bufs[2].ptr, 32,
+                             bufs[3].ptr, 32, 0.5, m0)
+        hip.synchronize()
+        assert np.isnan(bufs[3].download(np.float32, (64, 32))).all(), (n_k, m0)

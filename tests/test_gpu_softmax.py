@@ -155,7 +155,8 @@ def test_softmax_extremes(hip):
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
-@pytest.mark.parametrize("cols", [8192, 1000, 13, 4, 100, 256, 16384, 65537, (1 << 20) + 5])
+@pytest.mark.parametrize("cols", [8192, 1000, 13, 4, 100, 256, 2048, 4096, 16384, 65537,
+                                  (1 << 20) + 5])
 def test_reduce_rows(hip, dt, cols):
     """Row max (bit-identical to the reference's fold) and row sum (within
     1e-5 of the row's absolute sum) for every kernel: kL lanes per row up to
@@ -281,7 +282,8 @@ def test_reduce_rows_fused_sum_order_probes(hip):
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("cols,pitch_pad", [
     (13, 0), (100, 0), (256, 0),   # kL lanes per row (f32 up to 128, 16-bit up to 256)
-    (1000, 0), (8192, 0),          # a wave per row, 16-byte chunks
+    (1000, 0), (6000, 0),          # a wave per row, 16-byte chunks
+    (2048, 0), (4096, 0), (8192, 0),  # a row per 256 / 512 / 1024-thread workgroup
     (1000, 1), (37, 1),            # a wave per row, element loads (pitch not 16-byte aligned)
     (16384, 0), (65537, 0),        # a 1024-thread workgroup per row
 ])

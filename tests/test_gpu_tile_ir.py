@@ -165,3 +165,27 @@ def test_row_max_route_follows_the_fold(hip, cols, bm):
                   hip.ROUTE_REDUCE_ROWS)
     assert_same_bits(got.reshape(rows), cpuref.reduce_rows(x, cpuref.REDUCE_MAX),
                      what="routed row max")
+
+
+@pytest.mark.parametrize("bm,bn,d,n_q,s_k,programs,passes", [
+    (32, 64, 128, 256, 512, 8, True),
+    (16, 32, 64, 96, 200, 5, False),   # keys truncated to 192; 5 of 6 query tiles
+    (64, 16, 48, 64, 64, 1, True),
+])
+def test_attention_route_matches_the_oracle(hip, bm, bn, d, n_q, s_k, programs, passes):
+    """The DSL attention loop (K transposed, no mask), routed and launched:
+    within fp32 tolerance (|g - r| <= 1e-5 + 1e-4 |r|) of the oracle's
+    statement of the same program; rows no program owns stay untouched."""
+    say(f"tile ir attention BM={bm} BN={bn} D={d} n_q={n_q} S={s_k} programs={programs}")
+    scale = 1 / np.sqrt(d)
+    r = rng(bm + bn + d)
+    q = r.normal(size=(n_q, d)).astype(np.float32)
+    kt = r.normal(size=(d, s_k)).astype(np.float32)
+    v = r.normal(size=(s_k, d)).astype(np.float32)
+    o0 = np.full((n_q, d), 11.0, np.float32)
+    *_, got = _run(hip, T.attention(bm, bn, d, scale, passes=passes), [q, kt, v, o0], programs,
+                   hip.ROUTE_ATTENTION)
+    rows = programs * bm
+    ref = cpuref.dsl_attention_f32(q, kt, v, bn, np.float32(scale), np.float32(-1e30), n_q=rows)
+    assert_close(got[:rows], ref, atol=1e-5, rtol=1e-4, what="routed attention")
+    np.testing.assert_array_equal(got[rows:], 11.0)

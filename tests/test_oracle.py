@@ -375,6 +375,61 @@ def test_attention_closed_forms():
     assert np.all(part[:10] == 0) and np.all(part[20:] == 0)
 
 
+def _dsl_attn_fp64(q, kt, v, scale, n_keys):
+    s = (q.astype(np.float64) @ kt[:, :n_keys].astype(np.float64)) * scale
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    return (p @ v[:n_keys].astype(np.float64)) / p.sum(axis=1, keepdims=True)
+
+
+@pytest.mark.parametrize("n_q,d,s_k,bn,m0", [
+    (48, 32, 256, 32, -1.0e30),
+    (17, 64, 200, 64, -1.0e30),   # keys truncated to 192 = 3 whole blocks
+    (8, 16, 96, 16, 0.0),         # an initial max inside the score range
+    (5, 128, 64, 64, -3.0),
+])
+def test_dsl_attention_fp64(n_q, d, s_k, bn, m0):
+    """The DSL program's online softmax equals softmax(Q K^T scale) V over the
+    first (s_k / bn) * bn keys for any initial max the scores do not
+    underflow against."""
+    r = rng(n_q + d + s_k)
+    q = r.normal(size=(n_q, d)).astype(np.float32)
+    kt = r.normal(size=(d, s_k)).astype(np.float32)
+    v = r.normal(size=(s_k, d)).astype(np.float32)
+    scale = 1 / np.sqrt(d)
+    o = cpuref.dsl_attention_f32(q, kt, v, bn, scale, m0)
+    assert_close(o, _dsl_attn_fp64(q, kt, v, scale, (s_k // bn) * bn), atol=1e-5, rtol=1e-4,
+                 what="dsl attention")
+
+
+def test_dsl_attention_closed_forms():
+    r = rng(40)
+    n_q, d, s_k, bn = 16, 32, 100, 32
+    q = r.normal(size=(n_q, d)).astype(np.float32)
+    kt = r.normal(size=(d, s_k)).astype(np.float32)
+    v = r.normal(size=(s_k, d)).astype(np.float32)
+    # keys past the last whole block never enter, however large their scores
+    kt2, v2 = kt.copy(), v.copy()
+    kt2[:, 96:] = 50.0
+    v2[96:] = 1e6
+    np.testing.assert_array_equal(cpuref.dsl_attention_f32(q, kt2, v2, bn, 0.2, -1e30),
+                                  cpuref.dsl_attention_f32(q, kt, v, bn, 0.2, -1e30))
+    # an initial max above every score: every p and alpha-weighted sum is 0,
+    # so each output is 0 / 0
+    assert np.isnan(cpuref.dsl_attention_f32(q, kt, v, bn, 0.2, 1e30)).all()
+    # one block, constant V rows: every output row is that row
+    vc = np.tile(v[:1], (s_k, 1))
+    assert_close(cpuref.dsl_attention_f32(q, kt, vc, bn, 0.2, -1e30), vc[:n_q], atol=1e-6,
+                 rtol=1e-6, what="const V")
+    # the non-causal attention oracle on the same keys (K = kt^T), 3 blocks
+    k96 = np.ascontiguousarray(kt[:, :96].T)
+    qq = np.zeros((96, d), np.float32)
+    qq[:n_q] = q
+    o_ref = cpuref.attention_fwd(qq, k96, v[:96], 0.2, causal=False, q_end=n_q)[:n_q]
+    assert_close(cpuref.dsl_attention_f32(q, kt, v, bn, 0.2, -1e30), o_ref, atol=1e-6,
+                 rtol=1e-5, what="vs attention_fwd")
+
+
 # ---------------------------------------------------------------- number formats
 
 def _e4m3_table():

@@ -98,7 +98,7 @@ def test_vec_add_has_no_route(passes):
     r = _route(T.vec_add(4, passes), [8, 8, 8], 2)
     assert r.kind == hip.ROUTE_NONE
     why = r.reason.decode()
-    for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:"):
+    for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:", "attention:"):
         assert d in why
     assert list(r.buffer) == [-1, -1, -1, -1]
 
@@ -244,3 +244,75 @@ def test_loaded_accumulator_must_be_the_programs_tile():
         "%7 = load_ptr_tko %2, [%4, %5]", "%7 = load_ptr_tko %2, [%5, %4]")
     r = _route(text, [64, 96, 96, 48, 64, 48, 64, 48], 12)
     assert r.kind == hip.ROUTE_NONE and b"accumulator tile" in r.reason
+
+
+ATTN = dict(bm=32, bn=64, d=128, scale=0.08838834764831845)
+
+
+def _attn_shapes(n_q=256, s_k=512, d=128, ldq=None, ldv=None):
+    return [n_q, ldq or d, d, s_k, s_k, ldv or d, n_q, d]
+
+
+@pytest.mark.parametrize("passes", [True, False])
+def test_attention_routes(passes):
+    """The DSL's attention loop routes to the fp32 attention kernel with the
+    scale and initial max read from the text; programs * BM queries and
+    (S / BN) * BN keys."""
+    text = T.attention(**ATTN, passes=passes)
+    r = _route(text, _attn_shapes(), 8)
+    assert r.kind == hip.ROUTE_ATTENTION, r.reason
+    assert (r.tile_m, r.tile_n, r.tile_k) == (32, 64, 128)
+    assert list(r.buffer) == [0, 1, 2, 3] and list(r.shape_offset) == [0, 2, 4, 6]
+    assert r.attn_scale == np.float32(ATTN["scale"]) and r.attn_m0 == np.float32(-1e30)
+    assert (r.rows, r.cols) == (256, 512)
+    # fewer programs than query tiles; keys truncated to whole BN blocks
+    r = _route(text, _attn_shapes(s_k=500), 3)
+    assert r.kind == hip.ROUTE_ATTENTION and (r.rows, r.cols) == (96, 448)
+    # another initial max and no scale multiply
+    t2 = T.attention(16, 32, 64, 1.0, m0=5.0, passes=passes)
+    r = _route(t2.replace("mulf(%30, constant(1.0))", "mulf(constant(1.0), %30)"),
+               _attn_shapes(n_q=64, s_k=96, d=64), 4)
+    assert r.kind == hip.ROUTE_ATTENTION and r.attn_m0 == -5.0 and r.attn_scale == 1.0
+
+
+def test_attention_route_declines_uncovered_shapes():
+    text = T.attention(**ATTN)
+    for shapes, why in [([256, 128, 128, 512, 512, 128, 256, 256], b"column tile"),
+                        ([100, 128, 128, 512, 512, 128, 256, 128], b"query tiles"),
+                        ([256, 128, 128, 512, 400, 128, 256, 128], b"key tiles"),
+                        ([256, 128, 64, 512, 512, 128, 256, 128], b"key tiles")]:
+        r = _route(text, shapes, 8)
+        assert r.kind == hip.ROUTE_NONE and why in r.reason, (shapes, r.reason)
+
+
+ATTN_MUTATIONS = {
+    # each breaks one condition of the attention program
+    "max not ge": ('cmpf("ge", %26, %33)', 'cmpf("gt", %26, %33)'),
+    "max keeps the row max": ("select(cmpf(\"ge\", %26, %33), %26, %33)",
+                              "select(cmpf(\"ge\", %26, %33), %33, %26)"),
+    "reduce sum as max": ('combiner = "max", input_shape = [32, 64]} : tile<32x1xf32>\n      %34',
+                          'combiner = "sum", input_shape = [32, 64]} : tile<32x1xf32>\n      %34'),
+    "p without the shift": ("map exp(subf(%32, broadcast(%34, src_shape=[32, 1])))",
+                            "map exp(subf(%32, broadcast(%26, src_shape=[32, 1])))"),
+    "alpha reversed": ("map exp(subf(%26, %34))", "map exp(subf(%34, %26))"),
+    "l not rescaled": ("map addf(mulf(%24, %39), %41)", "map addf(mulf(%24, %24), %41)"),
+    "acc not rescaled": ("map mulf(%25, broadcast(%39,", "map mulf(%25, broadcast(%34,"),
+    "v walked by (0, j)": ("load_ptr_tko %2, [%23, %27]", "load_ptr_tko %2, [%27, %23]"),
+    "kt walked by (j, 0)": ("load_ptr_tko %1, [%27, %23]", "load_ptr_tko %1, [%23, %27]"),
+    "score seed 1": ("%29 = constant <f32: 0.0>", "%29 = constant <f32: 1.0>"),
+    "l starts at 1": ("cf.br ^bb1(%6, %8, %12, %10)", "cf.br ^bb1(%6, %10, %12, %8)"),
+    "output not divided": ("map divf(%52, broadcast(%51,", "map mulf(%52, broadcast(%51,"),
+    "bound from q": ("%19 = sile.shape_dim %18 {dim = 1}", "%19 = sile.shape_dim %5 {dim = 1}"),
+    "bound BN differs": ("%20 = constant <i64: 64>", "%20 = constant <i64: 32>"),
+    "store at swapped launch": ("[%4, %57] {shape = [32, 128]", "[%57, %4] {shape = [32, 128]"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ATTN_MUTATIONS))
+def test_attention_detector_rejections(name):
+    old, new = ATTN_MUTATIONS[name]
+    text = T.attention(**ATTN)
+    assert old in text, name
+    r = _route(text.replace(old, new), _attn_shapes(), 8)
+    assert r.kind == hip.ROUTE_NONE, name
+    assert b"attention:" in r.reason

@@ -21,11 +21,15 @@ The kernels (DSL source as in crates/sile/examples/*.rs):
   softmax<BM,BN>        crates/sile/examples/softmax.rs:3-16
   parallel_reduce<TILE> crates/sile/examples/parallel_reduce.rs:3-9
   vec_add<TILE>         crates/sile/examples/vec_add.rs:3-14
+  attention<BM,BN,D>    not in the reference (it has no attention kernel): the
+                        DSL program below, non-causal (the DSL has no iota or
+                        select on indices), K given transposed as kt [D, S]
   row_reduce<BM,BN>     not in the reference: `let pid = tile::id().0;
                         let t = x.load_tile([BM, BN], [pid, 0]);
                         y.store(sile::reduce_{sum,max}(t, 1));` with y
                         `[BM, 1]` (rank 2) or `[BM]` (rank 1)
 """
+import numpy as np
 
 
 def _param_buf(v, name, rank):
@@ -276,3 +280,123 @@ def vec_add(tile, passes=True):
                  ": none",
                  "return"]
     return _module("vec_add", params, [("^bb0", lines)])
+
+
+def attention(bm, bn, d, scale, m0=1.0e30, passes=True):
+    """attention<BM, BN, D> in the DSL (a negative literal does not parse in
+    the DSL, crates/sile-macros/src/frontend/parse.rs:407-470, so the initial
+    max is the tile difference constant(0.0) - constant(m0)):
+
+        let pid = tile::id().0;
+        let qt = q.load_tile([BM, D], [pid, 0]);
+        let mut m = sile::constant(0.0, [BM, 1]) - sile::constant(M0, [BM, 1]);
+        let mut l = sile::constant(0.0, [BM, 1]);
+        let mut acc = sile::constant(0.0, [BM, D]);
+        for j in 0..kt.shape()[1] / BN {
+            let s = sile::mma(qt, kt.load_tile([D, BN], [0, j]), sile::constant(0.0, [BM, BN]))
+                * sile::constant(SCALE, [BM, BN]);
+            let m_new = sile::max_tile(m, sile::reduce_max(s, 1));
+            let p = sile::exp(s - m_new.broadcast([BM, BN]));
+            let alpha = sile::exp(m - m_new);
+            l = l * alpha + sile::reduce_sum(p, 1);
+            acc = sile::mma(p, v.load_tile([BN, D], [j, 0]), acc * alpha.broadcast([BM, D]));
+            m = m_new;
+        }
+        o.store(acc / l.broadcast([BM, D]));
+
+    The loop carries l, acc, m in the order the body first assigns them
+    (find_loop_carried_vars, crates/sile-tile-ir/src/lower.rs:446-465);
+    max_tile is a select map at lowering (lower.rs:619-641).  After the
+    passes: single-use splats and pointwise chains fold into maps (the scale
+    into s's map, both constants into m's initial map), CSE merges the second
+    i64 0 of each block and the entry's second [BM, 1] zero splat into the
+    first, DCE drops the folded values."""
+    f32 = np.float32
+    m0s, sc = _fmt_float(float(f32(m0))), _fmt_float(float(f32(scale)))
+    col, acc_t, s_t = _tile(bm, 1), _tile(bm, d), _tile(bm, bn)
+    params = [_param_buf(0, "q", 2), _param_buf(1, "kt", 2), _param_buf(2, "v", 2),
+              _param_buf(3, "o", 2), _param_launch(4, 0), _param_shape(5, 0, "q", 2),
+              _param_shape(18, 1, "kt", 2), _param_shape(43, 2, "v", 2),
+              _param_shape(54, 3, "o", 2), _param_launch(57, 1)]
+    load_q = (f"%7 = load_ptr_tko %0, [%4, %6] {{shape = [{bm}, {d}], stride_dim = 1}} : "
+              f"{acc_t}")
+    header = (f"^bb1(%13: tile<i64>, %14: {col}, %15: {acc_t}, %16: {col})",
+              ["%19 = sile.shape_dim %18 {dim = 1} : tile<i64>",
+               f"%20 = constant <i64: {bn}> : tile<i64>",
+               "%21 = divi %19, %20 : tile<i64>",
+               '%22 = cmpi "lt" %13, %21 : tile<i64>',
+               "cf.cond_br %22, ^bb2(%13, %14, %15, %16), ^bb3(%14, %15, %16)"])
+    body_hdr = f"^bb2(%23: tile<i64>, %24: {col}, %25: {acc_t}, %26: {col})"
+    exit_hdr = f"^bb3(%51: {col}, %52: {acc_t}, %53: {col})"
+    load_kt = (f"%28 = load_ptr_tko %1, [%27, %23] {{shape = [{d}, {bn}], stride_dim = 1}} : "
+               f"{_tile(d, bn)}")
+    mma_s = f"%30 = mmaf %7, %28, %29 {{m = {bm}, n = {bn}, k = {d}}} : {s_t}"
+    rmax = (f'%33 = reduce %32 {{axis = 1, combiner = "max", input_shape = [{bm}, {bn}]}} : '
+            f"{col}")
+    m_new = (f'%34 = map select(cmpf("ge", %26, %33), %26, %33) {{shape = [{bm}, 1]}} : '
+             f"{col}")
+    rsum = (f'%41 = reduce %37 {{axis = 1, combiner = "sum", input_shape = [{bm}, {bn}]}} : '
+            f"{col}")
+    mma_pv = f"%48 = mmaf %37, %45, %47 {{m = {bm}, n = {d}, k = {bn}}} : {acc_t}"
+    store = (f"%58 = store_ptr_tko %3, %56, [%4, %57] {{shape = [{bm}, {d}], stride_dim = 1}} "
+             ": none")
+    if passes:
+        entry = ["%6 = constant <i64: 0> : tile<i64>", load_q,
+                 f"%8 = constant <f32: 0.0> : {col}",
+                 f"%10 = map subf(constant(0.0), constant({m0s})) {{shape = [{bm}, 1]}} : {col}",
+                 f"%12 = constant <f32: 0.0> : {acc_t}",
+                 "cf.br ^bb1(%6, %8, %12, %10)"]
+        body = ["%27 = constant <i64: 0> : tile<i64>", load_kt,
+                f"%29 = constant <f32: 0.0> : {s_t}", mma_s,
+                f"%32 = map mulf(%30, constant({sc})) {{shape = [{bm}, {bn}]}} : {s_t}",
+                rmax, m_new,
+                f"%37 = map exp(subf(%32, broadcast(%34, src_shape=[{bm}, 1]))) "
+                f"{{shape = [{bm}, {bn}]}} : {s_t}",
+                f"%39 = map exp(subf(%26, %34)) {{shape = [{bm}, 1]}} : {col}",
+                rsum,
+                f"%42 = map addf(mulf(%24, %39), %41) {{shape = [{bm}, 1]}} : {col}",
+                f"%45 = load_ptr_tko %2, [%23, %27] {{shape = [{bn}, {d}], stride_dim = 1}} : "
+                f"{_tile(bn, d)}",
+                f"%47 = map mulf(%25, broadcast(%39, src_shape=[{bm}, 1])) "
+                f"{{shape = [{bm}, {d}]}} : {acc_t}",
+                mma_pv,
+                "%49 = constant <i64: 1> : tile<i64>",
+                "%50 = addi %23, %49 : tile<i64>",
+                "cf.br ^bb1(%50, %42, %48, %34)"]
+        exit_ = [f"%56 = map divf(%52, broadcast(%51, src_shape=[{bm}, 1])) "
+                 f"{{shape = [{bm}, {d}]}} : {acc_t}", store, "return"]
+    else:
+        entry = ["%6 = constant <i64: 0> : tile<i64>", load_q,
+                 f"%8 = constant <f32: 0.0> : {col}",
+                 f"%9 = constant <f32: {m0s}> : {col}",
+                 f"%10 = subf %8, %9 : {col}",
+                 f"%11 = constant <f32: 0.0> : {col}",
+                 f"%12 = constant <f32: 0.0> : {acc_t}",
+                 "%17 = constant <i64: 0> : tile<i64>",
+                 "cf.br ^bb1(%17, %11, %12, %10)"]
+        body = ["%27 = constant <i64: 0> : tile<i64>", load_kt,
+                f"%29 = constant <f32: 0.0> : {s_t}", mma_s,
+                f"%31 = constant <f32: {sc}> : {s_t}",
+                f"%32 = mulf %30, %31 : {s_t}",
+                rmax, m_new,
+                f"%35 = broadcast %34 {{shape = [{bm}, {bn}]}} : {s_t}",
+                f"%36 = subf %32, %35 : {s_t}",
+                f"%37 = exp %36 : {s_t}",
+                f"%38 = subf %26, %34 : {col}",
+                f"%39 = exp %38 : {col}",
+                f"%40 = mulf %24, %39 : {col}",
+                rsum,
+                f"%42 = addf %40, %41 : {col}",
+                "%44 = constant <i64: 0> : tile<i64>",
+                f"%45 = load_ptr_tko %2, [%23, %44] {{shape = [{bn}, {d}], stride_dim = 1}} : "
+                f"{_tile(bn, d)}",
+                f"%46 = broadcast %39 {{shape = [{bm}, {d}]}} : {acc_t}",
+                f"%47 = mulf %25, %46 : {acc_t}",
+                mma_pv,
+                "%49 = constant <i64: 1> : tile<i64>",
+                "%50 = addi %23, %49 : tile<i64>",
+                "cf.br ^bb1(%50, %42, %48, %34)"]
+        exit_ = [f"%55 = broadcast %51 {{shape = [{bm}, {d}]}} : {acc_t}",
+                 f"%56 = divf %52, %55 : {acc_t}", store, "return"]
+    return _module("attention", params, [("^bb0", entry), header, (body_hdr, body),
+                                         (exit_hdr, exit_)])
