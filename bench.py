@@ -201,14 +201,18 @@ def roofline_obj(bound, achieved, peak, unit, traffic):
 
 # ---------------------------------------------------------------- workloads
 
-def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_step=0):
+def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_step=0,
+               b_row=False):
     """cpu_tile_step > 0 also times the CPU oracle on every cpu_tile_step-th
     256-row tile of C over the same (de)quantised inputs (the whole GEMM when
     M is below one tile).  The roofline is the matrix cores' unless streaming
     A, B and C once at the HBM peak takes longer (skinny shapes): then it is
-    the algorithmic bytes over the step time, in GB/s."""
+    the algorithmic bytes over the step time, in GB/s.  b_row: the same B
+    given row-major [K, N] (the canonical matmul's own layout)."""
     log(f"[bench] {name}: generating inputs")
     a_bits, b_bits, sa, sb, t = gemm_inputs(kind, m, n, k)
+    if b_row:
+        b_bits = np.ascontiguousarray(b_bits.T)
     c_t = hip.BF16
     da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
     host = (a_bits, b_bits) if cpu_tile_step else None
@@ -216,8 +220,8 @@ def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_ste
     dc = hip.DeviceBuffer(m * n * 2)
 
     def launch(_):
-        hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-                 dc.ptr, n, sa, sb, 0, stream)
+        hip.gemm(t, t, c_t, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, n if b_row else k,
+                 hip.ROW_MAJOR if b_row else hip.COL_MAJOR, dc.ptr, n, sa, sb, 0, stream)
 
     log(f"[bench] {name}: timing {steps} steps")
     region = time_launches(launch, steps, warmup, stream)
@@ -238,6 +242,8 @@ def bench_gemm(name, kind, m, n, k, steps, warmup, stream, traffic, cpu_tile_ste
         buf.close()
     if host is not None:
         from oracle import cpuref
+        if b_row:
+            host = (host[0], np.ascontiguousarray(host[1].T))
         if kind == "fp8":
             a32, b32 = cpuref.e4m3_decode(host[0], sa), cpuref.e4m3_decode(host[1], sb)
             what = "dequantised fp32 inputs q*s"
@@ -768,6 +774,7 @@ def traffic_from_pmc(root):
 # the kernel a workload's line is about (the softmax workload also runs the copy
 # that measures its ceiling)
 WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "sile_gemm_nt",
+                   "gemm_bf16_8192_brow": "sile_gemm_nn", "gemm_fp8_8192_brow": "sile_gemm_nt",
                    "gemm_bf16_4096": "sile_gemm_nt", "gemm_fp8_8192": "sile_gemm_nt",
                    "flash_attn_fwd_f16_s8192": "sile_flash_attn", "flash_attn_fwd_f16_s4096":
                    "sile_flash_attn", "gemm_f32_exact_4096": "sile_gemm_f32_exact",
@@ -787,7 +794,9 @@ EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f
          # and at head_dim 64
          "flash_attn_fwd_f16_s8000", "flash_attn_fwd_f16_s8192_d64",
          # bf16 inputs, and every (query, key) pair (not causal)
-         "flash_attn_fwd_bf16_s8192", "flash_attn_fwd_f16_s8192_nc"]
+         "flash_attn_fwd_bf16_s8192", "flash_attn_fwd_f16_s8192_nc",
+         # B row-major [K, N], the canonical matmul's own layout
+         "gemm_bf16_8192_brow", "gemm_fp8_8192_brow"]
 
 
 def main():
@@ -838,13 +847,14 @@ def main():
                                                  traffic, cpu=cpu and size <= 1024)
         elif name.startswith("gemm_"):
             kind = "fp8" if "fp8" in name else "bf16"
-            dims = name.split("_")[-1]
+            b_row = name.endswith("_brow")
+            dims = name.removesuffix("_brow").split("_")[-1]
             m, n, k = map(int, dims.split("x")) if "x" in dims else (int(dims),) * 3
             # the bf16 8192^3 GEMM's CPU time is the headline cpu_baseline below
             step = (0 if not cpu or name == "gemm_bf16_8192"
                     else 8 if 2.0 * m * n * k > 2e11 else 1)
             results[name] = bench_gemm(name, kind, m, n, k, args.steps, args.warmup, stream,
-                                       traffic, cpu_tile_step=step)
+                                       traffic, cpu_tile_step=step, b_row=b_row)
         elif name.startswith("flash_attn"):
             # flash_attn_fwd_<f16|bf16>_s<S>[_d<D>][_nc] (_nc: not causal)
             causal = not name.endswith("_nc")

@@ -252,8 +252,17 @@ int sile_hip_kernel_parallel_reduce(void *const *buffers, int64_t num_threadgrou
  *   f32  x f32  -> f32 : any shape/layout of B, A row-major; exact canonical order
  *                        (bit-identical to the CPU backend).
  *   bf16 x bf16 -> bf16|f32, f16 x f16 -> f16|f32, f8e4m3 x f8e4m3 -> bf16|f32:
- *                        A row-major, B column-major, any M, N, K', A and B
- *                        (and their leading dimensions) 16-byte aligned; MFMA
+ *                        A row-major, B column-major ([N, K]) or row-major
+ *                        ([K, N], the canonical matmul's own layout,
+ *                        canonical_matmul.rs:55-57), any M, N, K', A and a
+ *                        column-major B (and their leading dimensions)
+ *                        16-byte aligned.  A row-major 16-bit B runs the LDS
+ *                        kernels with transposed fragment reads when N is a
+ *                        multiple of 8, B's rows are 16-byte aligned and the
+ *                        shape takes the direct form below; any other
+ *                        row-major B (and every fp8 one) is first written
+ *                        column-major into a second device scratch buffer
+ *                        (at most 256 MiB; not under graph capture).  MFMA
  *                        path (N a multiple of 4, C's rows 16-byte aligned
  *                        and N >= 128, any M: 256 x 256 or 128 x 128 tiles
  *                        through LDS,

@@ -50,6 +50,7 @@ struct GemmArgs {
   int32_t k_rem;          // elements of the last half k-step inside K' (1 .. a half k-step)
   int32_t split_steps;    // half k-steps per k-range (even, or k_steps when K is not split)
   int64_t c_split;        // elements between the C planes of consecutive k-ranges
+  int64_t b_rows;         // B row-major [K, N]: rows of B's buffer (loads stay below them)
 };
 
 // The k-range of a workgroup: blockIdx.y selects half k-steps
@@ -106,9 +107,27 @@ struct TilePlan {
   __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
   int a_rs, b_rs;                     // bytes per row of A / B
   int a_voff, b_voff;                 // this lane's byte offsets for the tile loads
+  int b_voff1;                        // B row-major: the offset for odd load instructions
 };
 
-template <int kEB, int kT>
+// ---------------------------------------------------------------------------
+// B row-major ([K, N], N contiguous; the canonical matmul's own layout,
+// canonical_matmul.rs:55-57).  A k-step's B tile is kept as it lies in
+// memory, 64 rows of k by kT columns of n (kT * 2 bytes a row), and the MFMA
+// fragments, which hold 8 consecutive k of one n, are read transposed with
+// ds_read_b64_tr_b16: in each 16-lane group, result slot j of lane i is
+// element (i & 3) of the 8 bytes addressed by lane 4 j + (i >> 2), so lane i
+// addressing B[k0 + (i >> 2)][n0 + 4 (i & 3) .. + 4] receives
+// B[k0 .. k0 + 3][n0 + i]; two such reads (k0 and k0 + 4) give a fragment.
+// 16-byte chunk c of tile row k sits at c ^ swz_b(k), swz_b(k) =
+// 2 ((k & 3) | ((k >> 1) & 4)): one transposing read touches 16 rows
+// (k & 3 over the lane's quarter, k >> 3 over the 16-lane groups) with 32
+// contiguous bytes each, and the swizzle puts those 16 pairs of chunks on
+// each bank twice, the minimum for 512 bytes.
+// ---------------------------------------------------------------------------
+SILE_DEV int swz_b(int k) { return 2 * ((k & 3) | ((k >> 1) & 4)); }
+
+template <int kEB, int kT, bool kBRow>
 SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& g, int64_t byte0,
                             int wave, int lane) {
   TilePlan p;
@@ -140,15 +159,33 @@ SILE_DEV TilePlan plan_tile(const uint8_t* A, const uint8_t* B, const GemmArgs& 
   // (a k-range that starts byte0 bytes into the rows moves the base, not the end)
   p.a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(A + p.row0 * p.a_rs + byte0), (short)0,
                                                (int)(a_rows * p.a_rs - byte0), 0x00020000);
-  p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs + byte0), (short)0,
-                                               (int)(kT * p.b_rs - byte0), 0x00020000);
+  if constexpr (kBRow) {
+    // the tile's columns of B from the k-range's first row to B's last row
+    const int64_t base = byte0 / kEB * p.b_rs + p.col0 * kEB;
+    p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + base), (short)0,
+                                                 (int)(g.b_rows * p.b_rs - base), 0x00020000);
+  } else {
+    p.b_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(B + p.col0 * p.b_rs + byte0), (short)0,
+                                                 (int)(kT * p.b_rs - byte0), 0x00020000);
+  }
   // wave w's load instruction i (0..7) of an operand fills rows
   // 8 (4 i + w) + (lane >> 3), position lane & 7, whose chunk is
   // (lane & 7) ^ ((row >> 1) & 7) with (row >> 1) & 7 = ((w & 1) << 2) | ((lane >> 4) & 3)
   const int dma_row = 8 * wave + (lane >> 3);
   const int dma_chunk = (lane & 7) ^ (((wave & 1) << 2) | ((lane >> 4) & 3));
   p.a_voff = dma_row * p.a_rs + dma_chunk * 16;
-  p.b_voff = dma_row * p.b_rs + dma_chunk * 16;
+  p.b_voff = p.b_voff1 = dma_row * p.b_rs + dma_chunk * 16;
+  if constexpr (kBRow) {
+    // instruction i of wave w fills LDS KiB 4 i + w: rows kRI (4 i + w) ..,
+    // kSlots chunks a row; lane l takes row kRI w + l / kSlots (plus 4 kRI i,
+    // in the scalar offset) and slot l % kSlots, i.e. global chunk
+    // slot ^ swz_b(row); swz_b of the row depends on i only through its
+    // parity (bit 3 of the row, for 2 rows an instruction)
+    constexpr int kSlots = kT * kEB / 16, kRI = 64 / kSlots;
+    const int r0 = kRI * wave + lane / kSlots, slot = lane % kSlots;
+    p.b_voff = r0 * p.b_rs + ((slot ^ swz_b(r0)) << 4);
+    p.b_voff1 = r0 * p.b_rs + ((slot ^ swz_b(r0 + 4 * kRI)) << 4);
+  }
   return p;
 }
 
@@ -275,11 +312,15 @@ SILE_DEV u32x4 mask_k(u32x4 w, int e0, int k_rem) {
   return w;
 }
 
-template <int kKind, int kOut, int kT>
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
+
+template <int kKind, int kOut, int kT, bool kBRow>
 __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
                                                const uint8_t* __restrict__ B,
                                                void* __restrict__ C, const GemmArgs& g,
                                                uint8_t* smem) {
+  static_assert(!kBRow || kKind != kFP8, "row-major B: 16-bit operands");
   constexpr bool kIsFP8 = kKind == kFP8;
   constexpr int kBlk = kIsFP8 ? 32 : 16;      // MFMA block edge
   constexpr int kW = kT / 2;                  // wave tile edge
@@ -296,7 +337,7 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const KRange kr = k_range<kIsFP8 ? 1 : 2>(g);
-  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2, kT>(A, B, g, kr.byte0, wave, lane);
+  const TilePlan p = plan_tile<kIsFP8 ? 1 : 2, kT, kBRow>(A, B, g, kr.byte0, wave, lane);
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // LDS-DMA bases in SGPRs
 
   Acc acc[kNB][kNB];
@@ -313,11 +354,23 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
   const int f_row = lane % kBlk, f_grp = lane / kBlk;
   const int f_swz = (f_row >> 1) & 7;         // block rows differ by multiples of 16
   const int a_fb = (wm * kW + f_row) * kRowB, b_fb = (wn * kW + f_row) * kRowB;
+  // row-major B: a transposing read of lane l covers tile row
+  // 32 sub + 8 (l >> 4) + 4 h + ((l >> 2) & 3) and chunk (n0 / 8 + ((l & 3) >> 1))
+  // ^ swz_b(row), half l & 1, for the block at column n0 (swz_b(row) is fixed
+  // per lane: row & 3 = (l >> 2) & 3, bit 3 of row = (l >> 4) & 1)
+  constexpr int kBRowBytes = kT * 2;
+  const int tr_row = 8 * (lane >> 4) + ((lane >> 2) & 3);
+  const int tr_swz = swz_b(tr_row), tr_hi = (lane & 3) >> 1, tr_half = (lane & 1) << 3;
 
   // tile load instruction i (0..7) of operand B (or A) of k-step ks into slot
   auto load = [&](bool is_b, int ks, int slot, int i) {
     uint8_t* dst = smem + slot * kTB + wave_s * 1024 + i * 4096;
-    if (is_b)
+    if (is_b && kBRow)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(p.b_rsrc, (lds_ptr_t)dst, 16,
+                                               (i & 1) ? p.b_voff1 : p.b_voff,
+                                               (i * 4 * (1024 / kBRowBytes) + ks * 64) * p.b_rs,
+                                               0, 0);
+    else if (is_b)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(p.b_rsrc, (lds_ptr_t)dst, 16, p.b_voff,
                                                i * 32 * p.b_rs + ks * kRowB, 0, 0);
     else
@@ -330,12 +383,28 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 #pragma unroll
     for (int h = 0; h < kCh; ++h) {
       const int off = ((4 * sub + kCh * f_grp + h) ^ f_swz) << 4;
-      if (q < kNB)
+      if (q < kNB) {
         fa[q][h] = *reinterpret_cast<const u32x4*>(smem + sa * kTB + a_fb +
                                                    q * kBlk * kRowB + off);
-      else
+      } else if constexpr (kBRow) {
+        // 8 consecutive k of column n0 + (l & 15): two transposing reads
+        const int n0 = wn * kW + (q - kNB) * kBlk;
+        const int col = ((((n0 >> 3) | tr_hi) ^ tr_swz) << 4) | tr_half;
+        uint32_t w[4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int row = 32 * sub + 4 * t + tr_row;
+          const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_ptr)(smem + sb * kTB + row * kBRowBytes + col));
+          const short v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+          w[2 * t] = (uint16_t)v0 | ((uint32_t)(uint16_t)v1 << 16);
+          w[2 * t + 1] = (uint16_t)v2 | ((uint32_t)(uint16_t)v3 << 16);
+        }
+        fb[q - kNB][h] = u32x4{w[0], w[1], w[2], w[3]};
+      } else {
         fb[q - kNB][h] = *reinterpret_cast<const u32x4*>(smem + sb * kTB + b_fb +
                                                          (q - kNB) * kBlk * kRowB + off);
+      }
     }
   };
   // MFMAs of accumulator row i, columns [j0, j1)
@@ -510,15 +579,16 @@ __device__ __forceinline__ void gemm_ring_body(const uint8_t* __restrict__ A,
 
 }  // namespace
 
-#define SILE_GEMM_KERNEL(NAME, KIND, OUT, KT)                                                 \
+#define SILE_GEMM_KERNEL_B(NAME, KIND, OUT, KT, BROW)                                         \
   extern "C" __global__ __launch_bounds__(256, 256 / KT) void NAME(const void* A,              \
                                                                    const void* B, void* C,      \
                                                                    GemmArgs g) {               \
     static_assert(4 * kCStageB<KT / 2> <= 5 * KT * kRowB, "staged C fits the ring");           \
     __shared__ __attribute__((aligned(1024))) uint8_t smem[5 * KT * kRowB];                   \
-    gemm_ring_body<KIND, OUT, KT>(static_cast<const uint8_t*>(A),                             \
-                                  static_cast<const uint8_t*>(B), C, g, smem);                \
+    gemm_ring_body<KIND, OUT, KT, BROW>(static_cast<const uint8_t*>(A),                       \
+                                        static_cast<const uint8_t*>(B), C, g, smem);          \
   }
+#define SILE_GEMM_KERNEL(NAME, KIND, OUT, KT) SILE_GEMM_KERNEL_B(NAME, KIND, OUT, KT, false)
 
 // k_steps counts half k-steps: 32 elements (16-bit) or 64 (fp8)
 SILE_GEMM_KERNEL(sile_gemm_nt_bf16_bf16, kBF16, kOutBF16, 256)
@@ -535,6 +605,88 @@ SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f16, kF16, kOutF16, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_f16_f32, kF16, kOutF32, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_fp8_bf16, kFP8, kOutBF16, 128)
 SILE_GEMM_KERNEL(sile_gemm_nt128_fp8_f32, kFP8, kOutF32, 128)
+// B row-major [K, N] (16-bit operands), the same two tile sizes
+SILE_GEMM_KERNEL_B(sile_gemm_nn_bf16_bf16, kBF16, kOutBF16, 256, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn_bf16_f32, kBF16, kOutF32, 256, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn_f16_f16, kF16, kOutF16, 256, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn_f16_f32, kF16, kOutF32, 256, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn128_bf16_bf16, kBF16, kOutBF16, 128, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn128_bf16_f32, kBF16, kOutF32, 128, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn128_f16_f16, kF16, kOutF16, 128, true)
+SILE_GEMM_KERNEL_B(sile_gemm_nn128_f16_f32, kF16, kOutF32, 128, true)
+
+// out[c][r] = in[r][c] for r < rows, c < cols (elements of 1 or 2 bytes):
+// a row-major B [K, N] written column-major ([N, K], K contiguous) for the
+// GEMM shapes whose row-major kernels cannot take it.  A workgroup moves a
+// tile of 128 x 128 bytes (128 rows of 128 or 64 elements) through LDS:
+// 16-byte loads along the input rows, 16-byte stores along the output rows
+// (each gathered from 16 / sizeof(T) input rows in LDS), when the tile lies
+// inside both matrices and `vec` says rows start on 16-byte boundaries;
+// element by element otherwise.  LDS rows are padded by 4 bytes, so the
+// gathers of one column touch distinct banks.
+template <typename T>
+__device__ __forceinline__ void transpose_body(const T* __restrict__ in, int64_t ldi,
+                                               T* __restrict__ out, int64_t ldo, int64_t rows,
+                                               int64_t cols, int vec) {
+  constexpr int kR = 128, kC = 128 / sizeof(T), kE = 16 / sizeof(T);  // tile rows, cols
+  constexpr int kPitch = 128 + 4;                                       // LDS row bytes
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kR * kPitch];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * kR, c0 = (int64_t)blockIdx.x * kC;
+  auto at = [&](int r, int c) -> T& { return *reinterpret_cast<T*>(tile + r * kPitch + c * sizeof(T)); };
+  if (vec && r0 + kR <= rows && c0 + kC <= cols) {
+    // 128 rows x 8 chunks in, 4 a thread
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = j * 256 + t, r = e >> 3, ch = e & 7;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(in + (r0 + r) * ldi + c0 + ch * kE);
+      uint32_t* d = reinterpret_cast<uint32_t*>(tile + r * kPitch + ch * 16);
+      d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+    }
+    __syncthreads();
+    // kC output rows of kR elements, kCh chunks of kE each: 4 chunks a thread
+    constexpr int kCh = kR / kE;
+#pragma unroll
+    for (int j = 0; j < kC * kCh / 256; ++j) {
+      const int e = j * 256 + t, c = e / kCh, ch = e % kCh;
+      T g[kE];
+#pragma unroll
+      for (int i = 0; i < kE; ++i) g[i] = at(ch * kE + i, c);
+      u32x4 w;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int b = 0; b < 4 / (int)sizeof(T); ++b)
+          x |= (uint32_t)g[q * (4 / sizeof(T)) + b] << (8 * sizeof(T) * b);
+        w[q] = x;
+      }
+      *reinterpret_cast<u32x4*>(out + (c0 + c) * ldo + r0 + ch * kE) = w;
+    }
+    return;
+  }
+  for (int e = t; e < kR * kC; e += 256) {
+    const int r = e / kC, c = e % kC;
+    if (r0 + r < rows && c0 + c < cols) at(r, c) = in[(r0 + r) * ldi + c0 + c];
+  }
+  __syncthreads();
+  for (int e = t; e < kR * kC; e += 256) {
+    const int c = e / kR, r = e % kR;
+    if (c0 + c < cols && r0 + r < rows) out[(c0 + c) * ldo + r0 + r] = at(r, c);
+  }
+}
+extern "C" __global__ __launch_bounds__(256) void sile_transpose_e1(const uint8_t* in, int64_t ldi,
+                                                                    uint8_t* out, int64_t ldo,
+                                                                    int64_t rows, int64_t cols,
+                                                                    int vec) {
+  transpose_body<uint8_t>(in, ldi, out, ldo, rows, cols, vec);
+}
+extern "C" __global__ __launch_bounds__(256) void sile_transpose_e2(const uint16_t* in,
+                                                                    int64_t ldi, uint16_t* out,
+                                                                    int64_t ldo, int64_t rows,
+                                                                    int64_t cols, int vec) {
+  transpose_body<uint16_t>(in, ldi, out, ldo, rows, cols, vec);
+}
 
 // Split K: the ring kernel above writes one fp32 plane of C per k-range
 // (planes `plane` elements apart, rows n elements long); this kernel adds the

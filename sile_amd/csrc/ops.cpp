@@ -45,6 +45,7 @@ struct GemmArgs {
   int32_t k_rem;  // elements of the last half k-step inside K'
   int32_t split_steps;  // half k-steps per k-range (even, or k_steps unsplit)
   int64_t c_split;      // elements between the fp32 C planes of the k-ranges
+  int64_t b_rows;       // B row-major: rows of B's buffer
 };
 
 // Tile size and K split of the LDS GEMM kernels: the pair that minimises a
@@ -384,9 +385,9 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (!name)
     return fail(SILE_ERR_UNSUPPORTED_BACKEND, "GEMM %s x %s -> %s not supported",
                 dtype_name(a_type), dtype_name(b_type), dtype_name(c_type));
-  if (b_layout != SILE_COL_MAJOR)
-    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "%s GEMM needs B column-major (K contiguous)",
-                dtype_name(a_type));
+  if (b_layout != SILE_COL_MAJOR && b_layout != SILE_ROW_MAJOR)
+    return fail(SILE_ERR_UNSUPPORTED_BACKEND, "unknown B layout %d", (int)b_layout);
+  const bool b_row = b_layout == SILE_ROW_MAJOR;
   if (kp == 0) {
     // no k term: C = 0 (+0.0 in every output type), any M, N
     const int64_t cb16 = (int64_t)dtype_bytes(c_type) / 2;
@@ -398,9 +399,10 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
     return rc == SILE_OK ? ok() : rc;
   }
   const size_t eb = dtype_bytes(a_type), cb = dtype_bytes(c_type);
-  if (lda < k || ldb < k || ldc < n) return fail(SILE_ERR_SHAPE, "leading dimension too small");
+  if (lda < k || (b_row ? ldb < n : ldb < k) || ldc < n)
+    return fail(SILE_ERR_SHAPE, "leading dimension too small");
   const bool fp8 = kstep == 64;
-  if ((lda * eb) % 16 || (ldb * eb) % 16 || !aligned16(a) || !aligned16(b))
+  if ((lda * eb) % 16 || !aligned16(a) || (!b_row && ((ldb * eb) % 16 || !aligned16(b))))
     return fail(SILE_ERR_SHAPE, "A, B and their leading dimensions must be 16-byte aligned");
   // the LDS kernels need N >= the tile edge (128 x 128 tiles take any M,
   // 256 x 256 tiles M >= 256)
@@ -427,7 +429,42 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (capturing && splits_req > 1)
     return fail(SILE_ERR_UNSUPPORTED_BACKEND, "a K split needs the device scratch, which stream "
                                               "capture cannot order");
-  const bool transposed = !lds_ok && !capturing && m % 4 == 0 && m >= 128 &&
+  // Row-major B ([K, N], N contiguous): the LDS kernels read its tiles
+  // transposed (16-bit operands; N a multiple of 8, so every tile's columns
+  // start on a 16-byte boundary; B's rows 0 .. K as one buffer resource).
+  // Other row-major shapes and fp8 write B column-major into the device
+  // scratch first (slot 1) and take the column-major path below.
+  if (b_row && !(eb == 2 && lds_ok && n % 8 == 0 && (ldb * eb) % 16 == 0 && aligned16(b) &&
+                 (double)k * (double)ldb * (double)eb <= 2147483647.0)) {
+    if (capturing)
+      return fail(SILE_ERR_UNSUPPORTED_BACKEND, "row-major B of this shape needs the device "
+                                                "scratch, which stream capture cannot order");
+    const int64_t per16 = 16 / (int64_t)eb;
+    const int64_t ldt = (kp + per16 - 1) / per16 * per16;   // 16-byte aligned rows of B^T
+    if ((double)n * (double)ldt * (double)eb > (double)kScratchPlanesMax)
+      return fail(SILE_ERR_SHAPE, "row-major B of %lld x %lld exceeds the %lld MiB of scratch a "
+                  "GEMM may use", (long long)kp, (long long)n, (long long)(kScratchPlanesMax >> 20));
+    void* bt = nullptr;
+    int rc = scratch_acquire((size_t)(n * ldt) * eb, s, &bt, 1);
+    if (rc != SILE_OK) return rc;
+    int64_t rows = kp, cols = n, ldi = ldb, ldo = ldt;
+    int vec = (ldb * (int64_t)eb) % 16 == 0 && aligned16(b) ? 1 : 0;   // B^T rows are aligned
+    void* tp[] = {(void*)&b, &ldi, &bt, &ldo, &rows, &cols, &vec};
+    const int64_t tcols = 128 / (int64_t)eb;   // a tile: 128 rows of 128 bytes
+    if ((kp + 127) / 128 > 65535) {
+      rc = fail(SILE_ERR_SHAPE, "K too large for the transpose");
+    } else {
+      rc = launch(Module::kGemm, eb == 1 ? "sile_transpose_e1" : "sile_transpose_e2",
+                  dim3((unsigned)((n + tcols - 1) / tcols), (unsigned)((kp + 127) / 128)),
+                  dim3(256), tp, s);
+    }
+    if (rc == SILE_OK)
+      rc = gemm_impl(a_type, b_type, c_type, m, n, kp, a, lda, a_layout, bt, ldt, SILE_COL_MAJOR,
+                     c, ldc, scale_a, scale_b, 0, tile_req, splits_req, stream);
+    scratch_release(s, 1);
+    return rc;
+  }
+  const bool transposed = !b_row && !lds_ok && !capturing && m % 4 == 0 && m >= 128 &&
                           m * n * 4 <= kScratchPlanesMax;
   if (!lds_ok && !transposed) {
     // the any-shape kernel, 64 x 64 tiles with fragments loaded straight
@@ -452,7 +489,7 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   const int64_t rlda = transposed ? ldb : lda, rldb = transposed ? lda : ldb;
   const int64_t rm = transposed ? n : m, rn = transposed ? m : n;
   // a tile's panel of A or B is one buffer resource: 32-bit byte range
-  if (256 * std::max(lda, ldb) * (int64_t)eb > 0x7fffffffLL)
+  if (256 * std::max(lda, b_row ? 0 : ldb) * (int64_t)eb > 0x7fffffffLL)
     return fail(SILE_ERR_SHAPE, "leading dimension too large for a 256-row panel (%lld, %lld)",
                 (long long)lda, (long long)ldb);
   if (m > 0x7fffffffLL || n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
@@ -472,9 +509,10 @@ int gemm_impl(sile_dtype a_type, sile_dtype b_type, sile_dtype c_type, int64_t m
   if (tiles_m * tiles_n > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "GEMM too large");
   GemmArgs g{rlda, rldb, ldc, (int32_t)tiles_m, (int32_t)tiles_n, (int32_t)half_steps,
              scale_a * scale_b, (int32_t)rm, (int32_t)rn,
-             (int32_t)(kp - (half_steps - 1) * kstep), (int32_t)half_steps, 0};
+             (int32_t)(kp - (half_steps - 1) * kstep), (int32_t)half_steps, 0, k};
   const unsigned tiles = (unsigned)(tiles_m * tiles_n);
-  const char* tname = plan.tile == 256 ? "sile_gemm_nt_" : "sile_gemm_nt128_";
+  const char* tname = b_row ? (plan.tile == 256 ? "sile_gemm_nn_" : "sile_gemm_nn128_")
+                            : (plan.tile == 256 ? "sile_gemm_nt_" : "sile_gemm_nt128_");
   const char* ab = a_type == SILE_BF16 ? "bf16" : a_type == SILE_F16 ? "f16" : "fp8";
   char kname[64];
   int64_t splits = plan.splits;

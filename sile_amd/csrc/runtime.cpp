@@ -163,17 +163,18 @@ struct DeviceScratch {
   hipEvent_t last = nullptr;   // recorded after the last user's kernels
   bool used = false;
 };
-DeviceScratch g_scratch[kScratchDevices];
-thread_local int t_scratch_dev = -1;   // the device whose lock this thread holds
+DeviceScratch g_scratch[kScratchDevices][kScratchSlots];
+thread_local int t_scratch_dev[kScratchSlots] = {-1, -1};  // device whose slot lock this thread holds
 }  // namespace
 
-int scratch_acquire(size_t bytes, hipStream_t s, void** out) {
+int scratch_acquire(size_t bytes, hipStream_t s, void** out, int slot) {
   int dev = 0;
   SILE_HIP_CHECK(hipGetDevice(&dev));
   if (dev < 0 || dev >= kScratchDevices)
     return fail(SILE_ERR_INVALID_DEVICE, "device %d beyond the %d the scratch covers", dev,
                 kScratchDevices);
-  DeviceScratch& d = g_scratch[dev];
+  if (slot < 0 || slot >= kScratchSlots) return fail(SILE_ERR_SHAPE, "scratch slot %d", slot);
+  DeviceScratch& d = g_scratch[dev][slot];
   d.mu.lock();
   auto bail = [&](hipError_t e, const char* what) {
     d.mu.unlock();
@@ -199,20 +200,21 @@ int scratch_acquire(size_t bytes, hipStream_t s, void** out) {
   }
   if (d.used && (e = hipStreamWaitEvent(s, d.last, 0)) != hipSuccess)
     return bail(e, "hipStreamWaitEvent");
-  t_scratch_dev = dev;
+  t_scratch_dev[slot] = dev;
   *out = d.p;
   return SILE_OK;
 }
 
-void scratch_release(hipStream_t s) {
-  const int dev = t_scratch_dev;
+void scratch_release(hipStream_t s, int slot) {
+  if (slot < 0 || slot >= kScratchSlots) return;
+  const int dev = t_scratch_dev[slot];
   if (dev < 0) return;
-  DeviceScratch& d = g_scratch[dev];
+  DeviceScratch& d = g_scratch[dev][slot];
   if (hipEventRecord(d.last, s) == hipSuccess)
     d.used = true;
   else
     (void)hipStreamSynchronize(s);   // this call's kernels (and those s waited for) are done
-  t_scratch_dev = -1;
+  t_scratch_dev[slot] = -1;
   d.mu.unlock();
 }
 

@@ -55,15 +55,19 @@ int kernel_matmul_seeded(void* const* buffers, int64_t num_threadgroups, int64_t
                          const int64_t* shapes, int64_t bm, int64_t bn, int64_t bk,
                          const float* seed, const int64_t* seed_shape, float seed_value,
                          hipStream_t s);
-// Device scratch shared by the calls on one device (the split-K GEMM's fp32
-// partials and the transposed form's planes, at most 256 MiB): scratch_acquire makes stream s wait for the
-// kernels of the previous user (an event, so calls on different streams are
-// ordered on the GPU, not on the host), and returns at least `bytes` of it;
-// the caller launches its kernels on s and then calls scratch_release, which
-// records the event on s.  The device's lock is held in between.  The memory
-// is allocated on first use and grows when a call needs more.
-int scratch_acquire(size_t bytes, hipStream_t s, void** out);
-void scratch_release(hipStream_t s);
+// Device scratch shared by the calls on one device, in two slots: slot 0 the
+// split-K GEMM's fp32 partials and the transposed form's planes, slot 1 a
+// row-major B transposed for the column-major kernels (each at most
+// 256 MiB).  scratch_acquire makes stream s wait for the kernels of the
+// slot's previous user (an event, so calls on different streams are ordered
+// on the GPU, not on the host), and returns at least `bytes` of it; the
+// caller launches its kernels on s and then calls scratch_release, which
+// records the event on s.  The slot's lock is held in between; a caller
+// holding both takes slot 1 first.  The memory is allocated on first use and
+// grows when a call needs more.
+constexpr int kScratchSlots = 2;
+int scratch_acquire(size_t bytes, hipStream_t s, void** out, int slot = 0);
+void scratch_release(hipStream_t s, int slot = 0);
 // hipModuleLaunchKernel with kernelParams.
 int launch(Module m, const char* name, dim3 grid, dim3 block, void** params, hipStream_t stream,
            size_t dynamic_lds = 0);

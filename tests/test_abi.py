@@ -88,10 +88,18 @@ def test_small_gemm_shapes_need_aligned_operands(m, n):
     assert rc == 5 and "aligned" in _abi.last_error()
 
 
-def test_gemm_rejects_unaligned_and_row_major_b():
+def test_gemm_rejects_unaligned_a_and_unknown_b_layout():
     rc = _abi.status("sile_hip_gemm", _abi.BF16, _abi.BF16, _abi.BF16, 256, 256, 64, 16, 64,
+                     _abi.ROW_MAJOR, 16, 256, 7, 16, 256, 1.0, 1.0, 0, NULL)
+    assert rc == 2 and "layout" in _abi.last_error()
+    # row-major B: A's rows must still be 16-byte aligned (checked before device work)
+    rc = _abi.status("sile_hip_gemm", _abi.BF16, _abi.BF16, _abi.BF16, 256, 256, 64, 16, 66,
                      _abi.ROW_MAJOR, 16, 256, _abi.ROW_MAJOR, 16, 256, 1.0, 1.0, 0, NULL)
-    assert rc == 2 and "column-major" in _abi.last_error()
+    assert rc == 5 and "aligned" in _abi.last_error()
+    # row-major B narrower than N
+    rc = _abi.status("sile_hip_gemm", _abi.BF16, _abi.BF16, _abi.BF16, 256, 256, 64, 16, 64,
+                     _abi.ROW_MAJOR, 16, 200, _abi.ROW_MAJOR, 16, 256, 1.0, 1.0, 0, NULL)
+    assert rc == 5 and "leading dimension" in _abi.last_error()
     rc = _abi.status("sile_hip_gemm", _abi.BF16, _abi.BF16, _abi.BF16, 256, 256, 64, 18, 64,
                      _abi.ROW_MAJOR, 16, 64, _abi.COL_MAJOR, 16, 256, 1.0, 1.0, 0, NULL)
     assert rc == 5 and "aligned" in _abi.last_error()

@@ -4,9 +4,10 @@ Every workload bench.py times is run here once with the inputs bench.py
 generates (its gemm_inputs / attention_inputs / softmax_input recipes, the
 seeded configurations), and a deterministic sample of the output is compared
 with the CPU oracle:
-  * GEMM M = N = K = 8192 (bf16 and fp8) and 4096 (bf16): every 16th (8192)
-    or 4th (4096) 256-row tile of C, all columns, full K, against the
-    canonical matmul on the (de)quantised fp32 inputs;
+  * GEMM M = N = K = 8192 (bf16 and fp8, B column-major and row-major) and
+    4096 (bf16): every 16th (8192) or 4th (4096) 256-row tile of C, all
+    columns, full K, against the canonical matmul on the (de)quantised fp32
+    inputs;
   * causal flash attention B=4 H=32 D=128 at S = 4096 and 8192: three
     (batch, head) pairs, the first, the last and every 16th 128-query block;
   * row softmax [8192, 8192] fp16: every 64th row.
@@ -25,17 +26,23 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-2, 1e-2
 
 
-@pytest.mark.parametrize("kind,size,step", [("bf16", 8192, 16), ("fp8", 8192, 16),
-                                            ("bf16", 4096, 4)])
-def test_gemm_at_bench_shape(hip, kind, size, step):
+@pytest.mark.parametrize("kind,size,step,b_row", [("bf16", 8192, 16, False),
+                                                  ("fp8", 8192, 16, False),
+                                                  ("bf16", 4096, 4, False),
+                                                  ("bf16", 8192, 16, True),
+                                                  ("fp8", 8192, 16, True)])
+def test_gemm_at_bench_shape(hip, kind, size, step, b_row):
+    """b_row: the same B given row-major [K, N] (bench.py's *_brow lines)."""
     m = n = k = size
-    say(f"bench-shape gemm {kind} {size}^3 (every {step}th 256-row tile checked)")
+    say(f"bench-shape gemm {kind} {size}^3 B {'row' if b_row else 'column'}-major "
+        f"(every {step}th 256-row tile checked)")
     a_bits, b_bits, sa, sb, t = bench.gemm_inputs(kind, size)
-    da, db = hip.DeviceBuffer.from_array(a_bits), hip.DeviceBuffer.from_array(b_bits)
+    da = hip.DeviceBuffer.from_array(a_bits)
+    db = hip.DeviceBuffer.from_array(np.ascontiguousarray(b_bits.T) if b_row else b_bits)
     dc = hip.DeviceBuffer(m * n * 2)
     dc.fill_bytes(0xFF)  # NaN: a cell the kernel skips is caught
-    hip.gemm(t, t, hip.BF16, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, k, hip.COL_MAJOR,
-             dc.ptr, n, sa, sb)
+    hip.gemm(t, t, hip.BF16, m, n, k, da.ptr, k, hip.ROW_MAJOR, db.ptr, n if b_row else k,
+             hip.ROW_MAJOR if b_row else hip.COL_MAJOR, dc.ptr, n, sa, sb)
     hip.synchronize()
     got = cpuref.f32_from_bf16(dc.download(np.uint16, (m, n)))
     for buf in (da, db, dc):
