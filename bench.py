@@ -463,6 +463,111 @@ def bench_llir_vec_add(name, steps, warmup):
     return res
 
 
+# softmax<BM=4, BN=8192> (crates/sile/examples/softmax.rs:3-16) in the printed
+# LLIR form (crates/sile-llvm-ir/src/print.rs:6-57), as the generic code
+# generation gets it when the pattern router is not used: its three column
+# loops (8192 iterations) are spread over a 1024-lane workgroup per program
+LLIR_SOFTMAX_4x8192 = """\
+define void @softmax(ptr addrspace(1) %x, ptr addrspace(1) %y, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %x [rank=2, shape_offset=0, elem=f32]
+  ; sile.param %y [rank=2, shape_offset=2, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %__shape_x = getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0
+  %ldx_p = getelementptr i64, ptr addrspace(4) %__shape_x, i64 1
+  %ldx = load i64, ptr addrspace(4) %ldx_p
+  %__shape_y = getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2
+  %ldy_p = getelementptr i64, ptr addrspace(4) %__shape_y, i64 1
+  %ldy = load i64, ptr addrspace(4) %ldy_p
+  %m = call i32 @llvm.nvvm.ctaid.x()
+  %row0 = mul %m, 4
+  %tile = alloca [4 x [8192 x f32]], addrspace(5)
+  br label %sm_row_header ; args(0)
+sm_row_header:
+  ; args(%r: i64)
+  %rc = icmp slt %r, 4
+  br i1 %rc, label %sm_row_body, label %sm_exit
+sm_row_body:
+  %row = add %row0, %r
+  %xrow = mul %row, %ldx
+  %x0p = getelementptr f32, ptr addrspace(1) %x, i64 %xrow
+  %x0 = load f32, ptr addrspace(1) %x0p
+  br label %sm_max_header ; args(1, %x0)
+sm_max_header:
+  ; args(%c: i64, %mx: f32)
+  %mc = icmp slt %c, 8192
+  br i1 %mc, label %sm_max_body, label %sm_exp_header ; false_args(0, 0.0)
+sm_max_body:
+  %xi = add %xrow, %c
+  %xp = getelementptr f32, ptr addrspace(1) %x, i64 %xi
+  %xv = load f32, ptr addrspace(1) %xp
+  %gt = fcmp ogt %xv, %mx
+  %mx_next = select i1 %gt, f32 %xv, f32 %mx
+  %c_next = add %c, 1
+  br label %sm_max_header ; args(%c_next, %mx_next)
+sm_exp_header:
+  ; args(%e: i64, %sum: f32)
+  %ec = icmp slt %e, 8192
+  br i1 %ec, label %sm_exp_body, label %sm_div_header ; false_args(0)
+sm_exp_body:
+  %xe = add %xrow, %e
+  %xep = getelementptr f32, ptr addrspace(1) %x, i64 %xe
+  %xev = load f32, ptr addrspace(1) %xep
+  %d = fsub %xev, %mx
+  %ex = call f32 @llvm.exp.f32(f32 %d)
+  %tp = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 0, i64 %r, i64 %e
+  store f32 %ex, ptr addrspace(5) %tp
+  %sum_next = fadd %sum, %ex
+  %e_next = add %e, 1
+  br label %sm_exp_header ; args(%e_next, %sum_next)
+sm_div_header:
+  ; args(%q: i64)
+  %qc = icmp slt %q, 8192
+  br i1 %qc, label %sm_div_body, label %sm_row_latch
+sm_div_body:
+  %tq = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 0, i64 %r, i64 %q
+  %tv = load f32, ptr addrspace(5) %tq
+  %yv = fdiv %tv, %sum
+  %yrow = mul %row, %ldy
+  %yi = add %yrow, %q
+  %yp = getelementptr f32, ptr addrspace(1) %y, i64 %yi
+  store f32 %yv, ptr addrspace(1) %yp [writeonly]
+  %q_next = add %q, 1
+  br label %sm_div_header ; args(%q_next)
+sm_row_latch:
+  %r_next = add %r, 1
+  br label %sm_row_header ; args(%r_next)
+sm_exit:
+  ret void
+}
+"""
+
+
+def bench_llir_softmax(name, steps, warmup):
+    """softmax<BM=4, BN=8192> over f32 [8192, 8192] generated from LLIR
+    (LLIR_SOFTMAX_4x8192), one workgroup per program, through the synchronous
+    sile_hip_launch_llir (table upload, launch, wait per call), rated by the
+    routed softmax's algorithmic bytes (8 per element: read x, write y)."""
+    rows = cols = 8192
+    kern = hip.LlirKernel(LLIR_SOFTMAX_4x8192, (1, 4, cols))
+    x = hip.DeviceBuffer.from_array(normal(3, (rows, cols), 2.0))
+    y = hip.DeviceBuffer(rows * cols * 4)
+    ptrs, shapes, grid = [x.ptr, y.ptr], [rows, cols, rows, cols], (rows // 4, 1, 1)
+    for _ in range(warmup):
+        kern(ptrs, shapes, grid)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        kern(ptrs, shapes, grid)
+    dt = (time.perf_counter() - t0) / steps
+    nbytes = 8.0 * rows * cols
+    res = summarise(name, nbytes, 1e9, "GB/s", dt * 1e3 * steps, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    x.close()
+    y.close()
+    kern.close()
+    return res
+
+
 # softmax<BM=4, BN=8192> (crates/sile/examples/softmax.rs:3-16) in the
 # printed Tile IR form (crates/sile-tile-ir/src/print.rs:5-354) after the
 # default passes, the text a Rust HipBackend hands to sile_hip_tile_ir_route
@@ -784,7 +889,8 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
-EXTRA = ["copy_calibration", "llir_vec_add", "tile_ir_softmax_f32_8192", "gemm_f32_exact_4096",
+EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "tile_ir_softmax_f32_8192",
+         "gemm_f32_exact_4096",
          "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
          # shapes off the headline configurations: 128 x 128 tiles, split K', the
          # transposed form (M x N x K)
@@ -835,6 +941,8 @@ def main():
             results[name] = bench_copy_calibration(name, args.steps, args.warmup)
         elif name == "llir_vec_add":
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
+        elif name == "llir_softmax_f32_8192":
+            results[name] = bench_llir_softmax(name, args.steps, args.warmup)
         elif name == "tile_ir_softmax_f32_8192":
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
         elif name == "reduce_rows_f32_8192":

@@ -201,9 +201,15 @@ int sile_hip_llir_compile(const char *llir_text, int64_t plan_output_param, int6
                           int64_t plan_cols, void **code_out, size_t *code_bytes,
                           char *kernel_name, size_t name_capacity);
 void sile_hip_llir_free_code(void *code);
-/* Launches a generated sile_kernel_<name>: grid[0]*grid[1]*grid[2] programs,
- * one per lane, 64 per workgroup (the CPU backend runs one program per
- * thread, crates/sile-backend/src/cpu/codegen.rs:517-551).  Arguments as
+/* Launches a generated sile_kernel_<name>: grid[0]*grid[1]*grid[2] programs.
+ * A function with a counted loop of at least 256 iterations that lanes can
+ * split (sums, max folds, stores one element per iteration) runs one program
+ * per workgroup of 1024 lanes with those loops spread over the lanes, as the
+ * Metal template runs one program per threadgroup
+ * (crates/sile-backend/src/metal/mod.rs:146-154); any other function runs
+ * one program per lane, 64 per workgroup (the CPU backend runs one program
+ * per thread, crates/sile-backend/src/cpu/codegen.rs:517-551).  The kernel's
+ * workgroup size tells the launch which.  Arguments as
  * sile_hip_launch_tiles.  Synchronous. */
 int sile_hip_launch_llir(sile_hip_function fn, void *const *buffers, int64_t num_buffers,
                          const int64_t *shapes, int64_t num_shapes, const uint32_t grid[3],

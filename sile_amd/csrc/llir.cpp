@@ -14,7 +14,8 @@
 //   * bin / cmp / select / load / store / cast / gep lower to the C operators
 //     (`&(base[i][j])` for a gep, plain assignment for a cast);
 //   * block ids are the program's tile coordinates (gid0, gid1, gid2), thread
-//     ids are 0 and barriers do nothing (one program = one thread);
+//     ids are 0 and barriers do nothing (the program's own code is one
+//     thread's, also where its long loops are spread over a workgroup);
 //   * exp is expf, atomic add is an atomic float add, vec.load / vec.reduce.add
 //     are 4-wide loads and ((v0 + v1) + v2) + v3.
 // Control flow is emitted as labels and gotos (the reference's structured
@@ -25,7 +26,8 @@
 // input here (the reference computes it with `infer_tile_plan`,
 // crates/sile-backend/src/emit.rs:241-296, which a HIP backend in that crate
 // calls before handing the text over).  Programs are laid out one per lane,
-// 64 per workgroup.
+// 64 per workgroup, or, when the function has long loops the lanes can split,
+// one per workgroup (cooperative mode, below).
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
@@ -33,8 +35,11 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <climits>
+#include <functional>
 #include <map>
 #include <memory>
+#include <set>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -688,9 +693,388 @@ std::string ident(const std::string& name) {
   return out;
 }
 
+// ---------------------------------------------------------------------------
+// One workgroup per program (cooperative mode)
+//
+// The CPU backend runs a program on one thread (crates/sile-backend/src/cpu/codegen.rs:517-551)
+// and the Metal template one thread per threadgroup
+// (crates/sile-backend/src/metal/mod.rs:146-154).  A program whose tile loops
+// are long (a softmax over 8192 columns) then runs each loop serially.  When
+// the function has such a loop in a form whose iterations can be spread over
+// lanes, the program runs on a workgroup of kCoopThreads lanes instead:
+//   * a spread loop is a counted loop: header H(iv, c...) holding only
+//     `icmp slt iv, bound` with constant start, bound and step and at least
+//     kCoopMinTrip iterations, one body block B that branches back with
+//     (iv + step, c'...), no atomics, barriers, calls or memcpy in B;
+//   * each carried value c is a fold the lanes can split: a sum
+//     c' = c + x (lane partials from -0.0, a workgroup tree, then
+//     init + total: within fp32 rounding of the sequential chain), or the
+//     max fold c' = x > c ? x : c (each lane keeps its first maximum and its
+//     iteration, partials merge by value then iteration, then
+//     total > init ? total : init: bit for bit the sequential fold, NaN and
+//     +0 / -0 included); c is used in B by its fold only;
+//   * B's stores go to addresses that differ between iterations (a gep whose
+//     last index is iv or iv + an invariant, the other indices invariant; a
+//     4-wide store at offset iv (+ invariant) with step >= 4), and B loads an
+//     object it stores only through the same pointer;
+//   * lane l runs iterations l, l + W, ...; after the loop every lane holds
+//     the folded values and the final iv, and a barrier orders the loop's
+//     stores before anything that follows;
+//   * everything outside spread loops runs on every lane with the same values
+//     (so its stores write identical values); an atomic there runs on lane 0
+//     only (its result must be unused); allocas become workgroup (LDS)
+//     arrays.
+// Functions without such a loop keep one program per lane.
+// ---------------------------------------------------------------------------
+constexpr int kCoopThreads = 1024;
+constexpr int64_t kCoopMinTrip = 256;
+constexpr int64_t kCoopLdsBytes = 144 * 1024;
+
+struct CoopFold {
+  std::string param;   // carried header parameter
+  int kind = 0;        // 0 unchanged, 1 sum, 2 max
+  std::string next;    // the back-edge value
+  std::string cond;    // max: the compare that selects the new value
+};
+struct CoopLoop {
+  std::string header, body, exit;
+  std::string iv;
+  int64_t start = 0, bound = 0, step = 1;
+  std::vector<CoopFold> folds;
+};
+struct CoopPlan {
+  bool on = false;
+  std::map<std::string, CoopLoop> loops;   // by header block
+  std::set<std::string> bodies;            // body blocks emitted inside their loop
+  std::set<std::string> private_allocas;   // tiles split over the lanes (per-lane slices)
+  std::string why;                         // why the function stays one program per lane
+};
+
+bool const_int(const Operand& o, int64_t& v) {
+  if (o.is_value || o.ck != Operand::kInt) return false;
+  try {
+    v = std::stoll(o.name);
+  } catch (...) {
+    return false;
+  }
+  return true;
+}
+
+CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types) {
+  CoopPlan plan;
+  // where each value is defined: block name (function parameters: "")
+  std::map<std::string, std::string> def_block;
+  std::map<std::string, const Inst*> def_inst;
+  for (const Block& b : fn.blocks) {
+    for (auto& p : b.params) def_block[p.first] = b.name;
+    for (const Inst& in : b.insts)
+      if (!in.result.empty()) {
+        def_block[in.result] = b.name;
+        def_inst[in.result] = &in;
+      }
+  }
+  auto block = [&](const std::string& n) -> const Block* {
+    for (const Block& b : fn.blocks)
+      if (b.name == n) return &b;
+    return nullptr;
+  };
+  // the object (buffer parameter or alloca) a pointer value points into
+  std::function<std::string(const std::string&)> root = [&](const std::string& v) -> std::string {
+    auto it = def_inst.find(v);
+    if (it == def_inst.end()) return v;  // a parameter
+    if (it->second->op == "gep" && it->second->args[0].is_value) return root(it->second->args[0].name);
+    return v;                            // an alloca (or an unknown pointer: itself)
+  };
+  int64_t alloca_bytes = 0;
+  for (const Block& b : fn.blocks)
+    for (const Inst& in : b.insts) {
+      if (in.op == "alloca") {
+        Type base;
+        std::vector<int64_t> dims;
+        array_shape(in.aux, base, dims);
+        int64_t n = 4;
+        for (int64_t d : dims) n *= d;
+        alloca_bytes += n;
+      }
+    }
+
+  for (const Block& h : fn.blocks) {
+    if (h.params.empty() || h.insts.size() != 1 || h.term.kind != "condbr") continue;
+    const Inst& cmp = h.insts[0];
+    if (cmp.op != "cmp" || cmp.sub != "slt" || !cmp.args[0].is_value ||
+        cmp.args[0].name != h.params[0].first || !h.term.cond.is_value ||
+        h.term.cond.name != cmp.result)
+      continue;
+    CoopLoop L;
+    L.header = h.name;
+    L.iv = h.params[0].first;
+    if (!const_int(cmp.args[1], L.bound)) continue;
+    const Block* body = block(h.term.t);
+    if (!body || !body->params.empty() || !h.term.targs.empty() || body->term.kind != "br" ||
+        body->term.t != h.name || body->term.targs.size() != h.params.size())
+      continue;
+    L.body = body->name;
+    L.exit = h.term.f;
+    // iv' = iv + step
+    const Operand& nx = body->term.targs[0];
+    auto ni = nx.is_value ? def_inst.find(nx.name) : def_inst.end();
+    if (ni == def_inst.end() || def_block[nx.name] != body->name || ni->second->op != "bin" ||
+        ni->second->sub != "add")
+      continue;
+    const auto& na = ni->second->args;
+    if (!((na[0].is_value && na[0].name == L.iv && const_int(na[1], L.step)) ||
+          (na[1].is_value && na[1].name == L.iv && const_int(na[0], L.step))) ||
+        L.step <= 0)
+      continue;
+    // the one entry edge from outside the loop gives a constant start
+    int entries = 0;
+    bool start_ok = true;
+    for (const Block& b : fn.blocks) {
+      if (b.name == body->name) continue;
+      auto edge = [&](const std::string& t, const std::vector<Operand>& args) {
+        if (t != h.name) return;
+        ++entries;
+        if (args.empty() || !const_int(args[0], L.start)) start_ok = false;
+      };
+      if (b.term.kind == "br") edge(b.term.t, b.term.targs);
+      if (b.term.kind == "condbr") {
+        edge(b.term.t, b.term.targs);
+        edge(b.term.f, b.term.fargs);
+      }
+    }
+    if (entries != 1 || !start_ok) continue;
+    const int64_t trip = L.bound > L.start ? (L.bound - L.start + L.step - 1) / L.step : 0;
+    if (trip < kCoopMinTrip) continue;
+
+    // uses of each value inside the body (instructions and the back edge)
+    std::map<std::string, int> uses;
+    for (const Inst& in : body->insts)
+      for (const Operand& a : in.args)
+        if (a.is_value) ++uses[a.name];
+    for (const Operand& a : body->term.targs)
+      if (a.is_value) ++uses[a.name];
+    bool ok = true;
+    // loop-invariant: defined outside the loop, or computed in the body by a
+    // pure operation of invariant operands (a row offset computed per iteration)
+    std::map<std::string, bool> inv_memo;
+    std::function<bool(const Operand&)> invariant = [&](const Operand& o) -> bool {
+      if (!o.is_value) return true;
+      auto it = def_block.find(o.name);
+      const std::string db = it == def_block.end() ? "" : it->second;
+      if (db == h.name) return false;
+      if (db != body->name) return true;
+      auto m = inv_memo.find(o.name);
+      if (m != inv_memo.end()) return m->second;
+      inv_memo[o.name] = false;
+      const Inst& d = *def_inst[o.name];
+      bool r = d.op == "bin" || d.op == "cmp" || d.op == "select" || d.op == "cast" || d.op == "gep";
+      for (const Operand& a : d.args) r = r && invariant(a);
+      inv_memo[o.name] = r;
+      return r;
+    };
+    auto in_body = [&](const std::string& v) {
+      auto it = def_block.find(v);
+      return it != def_block.end() && it->second == body->name;
+    };
+    // carried values: folds
+    for (size_t k = 1; k < h.params.size() && ok; ++k) {
+      CoopFold f;
+      f.param = h.params[k].first;
+      const Operand& back = body->term.targs[k];
+      f.next = back.is_value ? back.name : "";
+      if (back.is_value && back.name == f.param) {
+        f.kind = 0;
+        if (uses[f.param] != 1) ok = false;
+      } else if (!back.is_value || !in_body(back.name) || uses[back.name] != 1) {
+        ok = false;
+      } else {
+        const Inst& d = *def_inst[back.name];
+        const Type* t = nullptr;
+        auto ti = types.find(f.param);
+        if (ti != types.end()) t = &ti->second;
+        if (!t || t->k != TK::F32) {
+          ok = false;
+        } else if (d.op == "bin" && d.sub == "fadd" &&
+                   ((d.args[0].is_value && d.args[0].name == f.param) !=
+                    (d.args[1].is_value && d.args[1].name == f.param))) {
+          f.kind = 1;
+          if (uses[f.param] != 1) ok = false;
+        } else if (d.op == "select" && d.args[0].is_value && d.args[2].is_value &&
+                   d.args[2].name == f.param) {
+          auto ci = def_inst.find(d.args[0].name);
+          if (ci == def_inst.end() || !in_body(d.args[0].name) || ci->second->op != "cmp" ||
+              ci->second->sub != "ogt" || !ci->second->args[1].is_value ||
+              ci->second->args[1].name != f.param || !(ci->second->args[0].name == d.args[1].name &&
+                                                        ci->second->args[0].is_value == d.args[1].is_value) ||
+              uses[d.args[0].name] != 1 || uses[f.param] != 2) {
+            ok = false;
+          } else {
+            f.kind = 2;
+            f.cond = d.args[0].name;
+          }
+        } else {
+          ok = false;
+        }
+      }
+      L.folds.push_back(f);
+    }
+    if (!ok) continue;
+    // body instructions and memory
+    std::map<std::string, std::set<std::string>> stored;  // object -> store pointers / offsets
+    auto iter_index = [&](const Operand& o) {
+      // iv itself, or iv + invariant (either order)
+      if (!o.is_value) return false;
+      if (o.name == L.iv) return true;
+      auto it = def_inst.find(o.name);
+      if (it == def_inst.end() || !in_body(o.name)) return false;
+      const Inst& a = *it->second;
+      if (a.op != "bin" || a.sub != "add") return false;
+      return (a.args[0].is_value && a.args[0].name == L.iv && invariant(a.args[1])) ||
+             (a.args[1].is_value && a.args[1].name == L.iv && invariant(a.args[0]));
+    };
+    for (const Inst& in : body->insts) {
+      if (in.op == "atomic" || in.op == "memcpy" || in.op == "call" || in.op == "alloca" ||
+          (in.op == "intr" && in.sub == "barrier")) {
+        ok = false;
+        break;
+      }
+      if (in.op == "store" || (in.op == "intr" && in.sub == "vstore")) {
+        const bool vec = in.op != "store";
+        std::string obj, key;
+        if (vec) {
+          if (!in.args[0].is_value || !invariant(in.args[0]) || !iter_index(in.args[1]) ||
+              L.step < in.dim) {
+            ok = false;
+            break;
+          }
+          obj = root(in.args[0].name);
+          key = in.args[0].name + "+" + in.args[1].name;
+        } else {
+          const Operand& ptr = in.args[0];
+          auto gi = ptr.is_value ? def_inst.find(ptr.name) : def_inst.end();
+          if (gi == def_inst.end() || !in_body(ptr.name) || gi->second->op != "gep") {
+            ok = false;
+            break;
+          }
+          const Inst& g = *gi->second;
+          bool gok = invariant(g.args[0]) && iter_index(g.args.back());
+          for (size_t k = 1; k + 1 < g.args.size(); ++k) gok = gok && invariant(g.args[k]);
+          if (!gok) {
+            ok = false;
+            break;
+          }
+          obj = root(g.args[0].name);
+          key = ptr.name;
+        }
+        stored[obj].insert(key);
+      }
+    }
+    if (!ok) continue;
+    for (const Inst& in : body->insts) {
+      if (in.op == "load" && in.args[0].is_value) {
+        const std::string obj = root(in.args[0].name);
+        if (stored.count(obj) && !stored[obj].count(in.args[0].name)) ok = false;
+      } else if (in.op == "intr" && in.sub == "vload" && in.args[0].is_value) {
+        const std::string obj = root(in.args[0].name);
+        if (stored.count(obj) &&
+            !stored[obj].count(in.args[0].name + "+" + (in.args[1].is_value ? in.args[1].name : "")))
+          ok = false;
+      }
+    }
+    if (!ok) continue;
+    plan.loops[L.header] = L;
+    plan.bodies.insert(L.body);
+  }
+  if (plan.loops.empty()) {
+    plan.why = "no loop of at least " + std::to_string(kCoopMinTrip) + " iterations that lanes can split";
+    return plan;
+  }
+  // A tile that is only touched inside spread loops starting at 0 with step 1,
+  // at [.., iv] (last index the loop counter), is touched at element e only by
+  // lane e % W (iteration e runs on that lane in every such loop): each lane
+  // keeps its slice [.., e / W] in registers instead of the workgroup keeping
+  // the tile in LDS.
+  {
+    std::map<std::string, std::string> body_of_header;
+    for (auto& kv : plan.loops) body_of_header[kv.second.body] = kv.first;
+    for (const Block& b : fn.blocks)
+      for (const Inst& in : b.insts) {
+        if (in.op != "alloca") continue;
+        bool priv = true;
+        for (const Block& u : fn.blocks) {
+          auto lp = body_of_header.find(u.name);
+          const CoopLoop* L = lp == body_of_header.end() ? nullptr : &plan.loops[lp->second];
+          for (const Inst& x : u.insts) {
+            for (size_t k = 0; k < x.args.size(); ++k) {
+              if (!x.args[k].is_value || x.args[k].name != in.result) continue;
+              // only as the base of a gep in a spread loop with start 0, step 1,
+              // last index the loop counter
+              if (!(x.op == "gep" && k == 0 && L && L->start == 0 && L->step == 1 &&
+                    x.args.back().is_value && x.args.back().name == L->iv && x.args.size() >= 3))
+                priv = false;
+            }
+          }
+          for (const Operand& a : u.term.targs)
+            if (a.is_value && a.name == in.result) priv = false;
+          for (const Operand& a : u.term.fargs)
+            if (a.is_value && a.name == in.result) priv = false;
+        }
+        if (priv) {
+          plan.private_allocas.insert(in.result);
+          Type base;
+          std::vector<int64_t> dims;
+          array_shape(in.aux, base, dims);
+          int64_t n = 4;
+          for (int64_t d : dims) n *= d;
+          alloca_bytes -= n;
+        }
+      }
+  }
+  if (alloca_bytes > kCoopLdsBytes) {
+    plan.why = "allocas exceed the LDS budget";
+    plan.loops.clear();
+    plan.bodies.clear();
+    return plan;
+  }
+  // an atomic outside the spread loops runs once (lane 0): its result must be unused
+  for (const Block& b : fn.blocks)
+    for (const Inst& in : b.insts)
+      if (in.op == "atomic" && !in.result.empty()) {
+        for (const Block& u : fn.blocks) {
+          for (const Inst& x : u.insts)
+            for (const Operand& a : x.args)
+              if (a.is_value && a.name == in.result) plan.why = "an atomic's result is used";
+          for (const Operand& a : u.term.targs)
+            if (a.is_value && a.name == in.result) plan.why = "an atomic's result is used";
+          for (const Operand& a : u.term.fargs)
+            if (a.is_value && a.name == in.result) plan.why = "an atomic's result is used";
+        }
+      }
+  if (!plan.why.empty()) {
+    plan.loops.clear();
+    plan.bodies.clear();
+    return plan;
+  }
+  plan.on = true;
+  return plan;
+}
+
+// An array type with its last dimension cut to one lane's slice of kCoopThreads.
+Type slice_type(const Type& t) {
+  if (t.k != TK::Arr) return t;
+  Type out = t;
+  if (t.elem && t.elem->k == TK::Arr) {
+    out.elem = std::make_shared<Type>(slice_type(*t.elem));
+  } else {
+    out.len = (t.len + kCoopThreads - 1) / kCoopThreads;
+  }
+  return out;
+}
+
 struct Emitter {
   const Function& fn;
   const std::map<std::string, Type>& types;
+  const CoopPlan& coop;
   std::ostringstream o;
 
   std::string opnd(const Operand& x) {
@@ -727,13 +1111,24 @@ struct Emitter {
     const auto& a = in.args;
     if (in.op == "alloca") return;  // storage declared at the top
     if (in.op == "gep") {
+      // a per-lane slice of a tile: element e of the last dimension is the
+      // lane's e / W
+      const bool slice = coop.on && a[0].is_value && coop.private_allocas.count(a[0].name);
       o << "  " << r << " = &(" << opnd(a[0]);
-      for (size_t k = 1; k < a.size(); ++k) o << "[" << opnd(a[k]) << "]";
+      for (size_t k = 1; k < a.size(); ++k) {
+        if (slice && k + 1 == a.size())
+          o << "[(" << opnd(a[k]) << ") / " << kCoopThreads << "LL]";
+        else
+          o << "[" << opnd(a[k]) << "]";
+      }
       o << ");\n";
     } else if (in.op == "load") {
       o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
     } else if (in.op == "store") {
       o << "  *(" << opnd(a[0]) << ") = " << opnd(a[1]) << ";\n";
+    } else if (in.op == "atomic" && coop.on) {
+      // outside the spread loops every lane runs the program's code: add once
+      o << "  if (threadIdx.x == 0) atomicAdd(" << opnd(a[0]) << ", " << opnd(a[1]) << ");\n";
     } else if (in.op == "atomic") {
       o << "  " << (r.empty() ? "" : r + " = ") << "atomicAdd(" << opnd(a[0]) << ", " << opnd(a[1])
         << ");\n";
@@ -804,6 +1199,63 @@ struct Emitter {
 
   bool is_shapes(const Param& p) const { return p.name == "__sile_shapes"; }
 
+  // A spread loop at its header: lane l runs iterations l, l + W, ... of the
+  // body with the carried values replaced by the lane's partial folds, the
+  // partials are combined across the workgroup, the header's parameters get
+  // their final values, a barrier orders the loop's stores, and the header's
+  // exit branch follows.
+  void coop_loop(const Block& h, const CoopLoop& L) {
+    const Block* body = nullptr;
+    for (const Block& b : fn.blocks)
+      if (b.name == L.body) body = &b;
+    const std::string iv = ident(L.iv), st = std::to_string(L.step), bd = std::to_string(L.bound);
+    o << "  {\n    const long long coop_start = " << iv << ";\n";
+    for (size_t k = 0; k < L.folds.size(); ++k) {
+      const CoopFold& f = L.folds[k];
+      const std::string c = ident(f.param), ks = std::to_string(k);
+      o << "    const float coop_init" << ks << " = " << c << ";\n";
+      if (f.kind == 1) o << "    float coop_p" << ks << " = -0.0f;\n";
+      if (f.kind == 2)
+        o << "    float coop_p" << ks << " = -__builtin_inff(); long long coop_i" << ks
+          << " = LLONG_MAX;\n";
+    }
+    // unrolled, so a lane has several iterations' loads in flight
+    o << "#pragma unroll 8\n";
+    o << "    for (long long coop_it = coop_start + (long long)threadIdx.x * " << st
+      << "LL; coop_it < " << bd << "LL; coop_it += " << kCoopThreads << "LL * " << st << "LL) {\n";
+    o << "    " << iv << " = coop_it;\n";
+    for (size_t k = 0; k < L.folds.size(); ++k)
+      if (L.folds[k].kind != 0)
+        o << "    " << ident(L.folds[k].param) << " = coop_p" << k << ";\n";
+    for (const Inst& in : body->insts) inst(in);
+    for (size_t k = 0; k < L.folds.size(); ++k) {
+      const CoopFold& f = L.folds[k];
+      if (f.kind == 2) o << "    if (" << ident(f.cond) << ") coop_i" << k << " = coop_it;\n";
+      if (f.kind != 0) o << "    coop_p" << k << " = " << ident(f.next) << ";\n";
+    }
+    o << "    }\n";
+    for (size_t k = 0; k < L.folds.size(); ++k) {
+      const CoopFold& f = L.folds[k];
+      const std::string c = ident(f.param), ks = std::to_string(k);
+      if (f.kind == 0) {
+        o << "    " << c << " = coop_init" << ks << ";\n";
+      } else if (f.kind == 1) {
+        o << "    " << c << " = coop_init" << ks << " + coop_wg_sum(coop_p" << ks
+          << ", coop_red_v);\n";
+      } else {
+        o << "    coop_wg_first_max(coop_p" << ks << ", coop_i" << ks
+          << ", coop_red_v, coop_red_i);\n";
+        o << "    " << c << " = coop_p" << ks << " > coop_init" << ks << " ? coop_p" << ks
+          << " : coop_init" << ks << ";\n";
+      }
+    }
+    o << "    " << iv << " = " << bd << "LL > coop_start ? coop_start + ((" << bd
+      << "LL - coop_start + " << st << "LL - 1) / " << st << "LL) * " << st
+      << "LL : coop_start;\n  }\n";
+    o << "  __syncthreads();\n";
+    jump(h.term.f, h.term.fargs);
+  }
+
   void body() {
     o << "__device__ static void sile_llvm_ir_" << fn.name << "(";
     for (size_t k = 0; k < fn.params.size(); ++k) {
@@ -824,10 +1276,24 @@ struct Emitter {
           std::string d;
           for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
           if (dims.empty()) d = "[1]";
-          o << "  " << c_scalar(base) << " " << ident(in.result) << "_storage" << d << ";\n";
+          // one program per workgroup: the program's tiles live in LDS, or, when
+          // only spread loops touch them at [.., iv], as per-lane slices
+          const bool priv = coop.on && coop.private_allocas.count(in.result);
+          if (priv) {
+            d.clear();
+            for (size_t k = 0; k < dims.size(); ++k)
+              d += "[" + std::to_string(k + 1 == dims.size()
+                                             ? (dims[k] + kCoopThreads - 1) / kCoopThreads
+                                             : dims[k]) + "]";
+          }
+          o << "  " << (coop.on && !priv ? "__shared__ " : "") << c_scalar(base) << " "
+            << ident(in.result) << "_storage" << d << ";\n";
           if (dims.empty())
             o << "  " << c_scalar(base) << "* " << ident(in.result) << " = " << ident(in.result)
               << "_storage;\n";
+          else if (priv)
+            o << "  " << c_decl(ptr_to(slice_type(in.aux), in.ty.addr), ident(in.result))
+              << " = &" << ident(in.result) << "_storage;\n";
           else
             o << "  " << c_decl(in.ty, ident(in.result)) << " = &" << ident(in.result)
               << "_storage;\n";
@@ -836,8 +1302,15 @@ struct Emitter {
         }
       }
     }
+    if (coop.on) o << "  __shared__ float coop_red_v[32];\n  __shared__ long long coop_red_i[32];\n";
     for (const Block& b : fn.blocks) {
+      if (coop.bodies.count(b.name)) continue;  // emitted inside its spread loop
       o << "L_" << ident(b.name) << ":;\n";
+      auto lp = coop.loops.find(b.name);
+      if (lp != coop.loops.end()) {
+        coop_loop(b, lp->second);
+        continue;
+      }
       for (const Inst& in : b.insts) inst(in);
       term(b.term);
     }
@@ -860,9 +1333,13 @@ struct Emitter {
       if (!first_buf) first_buf = &p;
       last_buf = &p;
     }
-    o << "extern \"C\" __global__ __launch_bounds__(64) void sile_kernel_" << fn.name
+    const int threads = coop.on ? kCoopThreads : 64;
+    o << "extern \"C\" __global__ __launch_bounds__(" << threads << ") void sile_kernel_" << fn.name
       << "(void** buffers, long long num_programs, const long long* shapes, long long num_shapes) {\n";
-    o << "  const long long sile_pid = (long long)blockIdx.x * 64 + threadIdx.x;\n";
+    if (coop.on)
+      o << "  const long long sile_pid = (long long)blockIdx.x;  // one workgroup per program\n";
+    else
+      o << "  const long long sile_pid = (long long)blockIdx.x * 64 + threadIdx.x;\n";
     o << "  if (sile_pid >= num_programs) return;\n";
     o << "  (void)num_shapes;\n";
     // buffers in parameter order, each bound as its parameter's pointer type
@@ -927,6 +1404,28 @@ struct Emitter {
          "  p[off] = v.v[0]; p[off + 1] = v.v[1]; p[off + 2] = v.v[2]; p[off + 3] = v.v[3];\n}\n";
     o << "__device__ static inline float llir_vec_reduce_add(llir_float4 v) {\n"
          "  return v.v[0] + v.v[1] + v.v[2] + v.v[3];\n}\n\n";
+    if (coop.on) {
+      // workgroup folds of the lanes' partials; every lane returns the result
+      o << "#ifndef LLONG_MAX\n#define LLONG_MAX 9223372036854775807LL\n#endif\n"
+           "__device__ static float coop_wg_sum(float v, float* red) {\n"
+           "  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);\n"
+           "  __syncthreads();\n"
+           "  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;\n"
+           "  __syncthreads();\n"
+           "  float s = red[0];\n"
+           "  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) s += red[w];\n"
+           "  return s;\n}\n"
+           "__device__ static void coop_merge(float& v, long long& i, float ov, long long oi) {\n"
+           "  const bool take = ov > v || (ov == v && oi < i);\n"
+           "  v = take ? ov : v; i = take ? oi : i;\n}\n"
+           "__device__ static void coop_wg_first_max(float& v, long long& i, float* rv, long long* ri) {\n"
+           "  for (int m = 1; m < 64; m <<= 1) coop_merge(v, i, __shfl_xor(v, m, 64), __shfl_xor(i, m, 64));\n"
+           "  __syncthreads();\n"
+           "  if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = v; ri[threadIdx.x >> 6] = i; }\n"
+           "  __syncthreads();\n"
+           "  v = rv[0]; i = ri[0];\n"
+           "  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) coop_merge(v, i, rv[w], ri[w]);\n}\n\n";
+    }
     body();
     wrapper(plan_out, rows, cols);
     return o.str();
@@ -964,7 +1463,8 @@ int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::
     Parser p;
     p.parse(std::string(text));
     verify(p.fn);
-    Emitter e{p.fn, p.types, {}};
+    const CoopPlan coop = plan_coop(p.fn, p.types);
+    Emitter e{p.fn, p.types, coop, {}};
     src = e.emit(plan_out, rows, cols);
     name = "sile_kernel_" + p.fn.name;
   } catch (const ParseError& e) {

@@ -546,6 +546,18 @@ int sile_hip_launch_llir(sile_hip_function fn, void* const* buffers, int64_t num
   int rc = check_launch_args(fn, buffers, num_buffers, shapes, num_shapes, grid, &programs);
   if (rc != SILE_OK) return rc;
   if (programs == 0) return ok();
+  // a generated kernel takes one program per lane (64 lanes a workgroup) or,
+  // when its loops are spread over a workgroup, one program per workgroup;
+  // the generator sets the kernel's workgroup size to tell them apart
+  int max_threads = 64;
+  SILE_HIP_CHECK(hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                     static_cast<hipFunction_t>(fn)));
+  if (max_threads > 64) {
+    if (programs > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many programs");
+    return launch_with_tables(static_cast<hipFunction_t>(fn), buffers, num_buffers, shapes,
+                              num_shapes, programs, programs, max_threads,
+                              static_cast<hipStream_t>(stream));
+  }
   return launch_with_tables(static_cast<hipFunction_t>(fn), buffers, num_buffers, shapes,
                             num_shapes, programs, (programs + 63) / 64, 64,
                             static_cast<hipStream_t>(stream));

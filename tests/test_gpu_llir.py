@@ -98,3 +98,92 @@ def test_parallel_reduce(hip, kernels):
     out = _run(hip, kernels["parallel_reduce"], [x, np.zeros(1, np.float32)], (100, 1, 1))[1]
     parts = cpuref.parallel_reduce_partials(x, 100, 16)
     assert_close(out[0], parts.astype(np.float64).sum(), atol=1e-3, rtol=1e-5, what="llir reduce")
+
+
+# ---- one workgroup per program (loops of >= 256 iterations spread over lanes) ----
+
+from tests.helpers import assert_same_bits, max_fold_probe_rows  # noqa: E402
+from tests.test_llir import parallel_reduce_llir, softmax_llir, vec_add_llir  # noqa: E402
+
+# row_max<BN>: out[pid] = the fold from x[pid][0] over the row's BN columns
+# (reduce.rs:10-30), one row per program, written in the printed LLIR form
+ROW_MAX_LLIR = """\
+define void @row_max(ptr addrspace(1) %x, ptr addrspace(1) %out, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %x [rank=2, shape_offset=0, elem=f32]
+  ; sile.param %out [rank=1, shape_offset=2, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %__shape_x = getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0
+  %ldx_p = getelementptr i64, ptr addrspace(4) %__shape_x, i64 1
+  %ldx = load i64, ptr addrspace(4) %ldx_p
+  %pid = call i32 @llvm.nvvm.ctaid.x()
+  %xrow = mul %pid, %ldx
+  %x0p = getelementptr f32, ptr addrspace(1) %x, i64 %xrow
+  %x0 = load f32, ptr addrspace(1) %x0p
+  br label %rm_header ; args(1, %x0)
+rm_header:
+  ; args(%c: i64, %mx: f32)
+  %cond = icmp slt %c, BN
+  br i1 %cond, label %rm_body, label %rm_done
+rm_body:
+  %xi = add %xrow, %c
+  %xp = getelementptr f32, ptr addrspace(1) %x, i64 %xi
+  %xv = load f32, ptr addrspace(1) %xp
+  %gt = fcmp ogt %xv, %mx
+  %mx_next = select i1 %gt, f32 %xv, f32 %mx
+  %c_next = add %c, 1
+  br label %rm_header ; args(%c_next, %mx_next)
+rm_done:
+  %op = getelementptr f32, ptr addrspace(1) %out, i64 %pid
+  store f32 %mx, ptr addrspace(1) %op
+  ret void
+}
+"""
+
+
+@pytest.mark.parametrize("rows,bm,bn", [(64, 4, 8192), (10, 2, 300), (8, 1, 1000)])
+def test_spread_softmax(hip, rows, bm, bn):
+    """softmax<BM, BN> with its loops spread over a 1024-lane workgroup per
+    program: within 1e-7 + 1e-5 |r| of the oracle's tile semantics (the row
+    sum is a tree over lanes instead of one chain; the max is the fold)."""
+    say(f"llir spread softmax<{bm}, {bn}> over [{rows}, {bn}]")
+    kern = hip.LlirKernel(softmax_llir(bm, bn), (1, bm, bn))
+    x = rng(bm + bn).normal(scale=2.0, size=(rows, bn)).astype(np.float32)
+    grid = (rows // bm, 1, 1)
+    y = _run(hip, kern, [x, np.zeros_like(x)], grid)[1]
+    ref = np.zeros_like(x)
+    cpuref.kernel_softmax(x, ref, grid, bm, bn)
+    assert_close(y, ref, atol=1e-7, rtol=1e-5, what="llir spread softmax")
+    kern.close()
+
+
+@pytest.mark.parametrize("bn", [4096, 1000])
+def test_spread_max_fold_is_bit_exact(hip, bn):
+    """The spread max fold (lane partials with their first iteration, merged
+    by value then iteration, then against x0) equals the sequential fold bit
+    for bit on rows with NaN, -inf and +0 / -0 ties."""
+    x = max_fold_probe_rows(bn, bn + 7)
+    rows = x.shape[0]
+    say(f"llir spread row max over [{rows}, {bn}]")
+    kern = hip.LlirKernel(ROW_MAX_LLIR.replace("BN", str(bn)), (1, 1, 1))
+    out = _run(hip, kern, [x, np.full(rows, 5.0, np.float32)], (rows, 1, 1))[1]
+    assert_same_bits(out, cpuref.reduce_rows(x, cpuref.REDUCE_MAX), what="spread row max")
+    kern.close()
+
+
+def test_spread_reduce_and_vec_add(hip):
+    say("llir spread parallel_reduce<4096> and vec_add<4096>")
+    kern = hip.LlirKernel(parallel_reduce_llir(4096), None)
+    x = np.ones(1 << 20, np.float32)
+    out = _run(hip, kern, [x, np.zeros(1, np.float32)], (256, 1, 1))[1]
+    assert out[0] == float(1 << 20)   # one atomic add per program, sums of ones exact
+    x = rng(8).uniform(0, 1, size=1 << 16).astype(np.float32)
+    out = _run(hip, kern, [x, np.zeros(1, np.float32)], (16, 1, 1))[1]
+    assert_close(out[0], x.astype(np.float64).sum(), atol=1e-2, rtol=1e-5, what="spread reduce")
+    kern.close()
+    kern = hip.LlirKernel(vec_add_llir(4096), (2, 1, 4096))
+    a = rng(9).integers(-1000, 1000, 1 << 16).astype(np.float32)
+    b = rng(10).integers(-1000, 1000, 1 << 16).astype(np.float32)
+    c = _run(hip, kern, [a, b, np.zeros_like(a)], (16, 1, 1))[2]
+    np.testing.assert_array_equal(c, a + b)
+    kern.close()

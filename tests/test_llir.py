@@ -138,3 +138,79 @@ def test_thread_id_is_allowed_and_is_zero():
     src = _fn("entry:\n  %tid = call i32 @llvm.nvvm.tid.x()\n  ret void\n")
     out = hip.llir_to_hip(src)
     assert "v_tid = 0;" in out
+
+
+# ---- one workgroup per program: loops spread over the lanes ----
+
+def softmax_llir(bm, bn):
+    """The softmax fixture at BM rows and BN columns per program."""
+    t = text("softmax")
+    for old, new in [("[2 x [8 x f32]]", f"[{bm} x [{bn} x f32]]"), ("mul %m, 2", f"mul %m, {bm}"),
+                     ("icmp slt %r, 2", f"icmp slt %r, {bm}"), ("icmp slt %c, 8", f"icmp slt %c, {bn}"),
+                     ("icmp slt %e, 8", f"icmp slt %e, {bn}"), ("icmp slt %q, 8", f"icmp slt %q, {bn}")]:
+        assert old in t
+        t = t.replace(old, new)
+    return t
+
+
+def parallel_reduce_llir(tile):
+    t = text("parallel_reduce")
+    for old, new in [("mul %pid, 16", f"mul %pid, {tile}"), ("icmp slt %i, 16", f"icmp slt %i, {tile}")]:
+        assert old in t
+        t = t.replace(old, new)
+    return t
+
+
+def vec_add_llir(tile):
+    t = text("vec_add")
+    assert t.count(", 4") >= 2
+    return t.replace("mul %pid, 4", f"mul %pid, {tile}").replace("icmp slt %i, 4",
+                                                                  f"icmp slt %i, {tile}")
+
+
+def test_the_fixtures_keep_one_program_per_lane():
+    """Loops of fewer than 256 iterations are not spread: the five fixtures'
+    code is unchanged (64 programs a workgroup, no workgroup folds)."""
+    for name in PLANS:
+        src = hip.llir_to_hip(text(name), PLANS[name])
+        assert "__launch_bounds__(64)" in src and "coop_" not in src, name
+
+
+def test_long_loops_spread_over_the_workgroup():
+    src = hip.llir_to_hip(softmax_llir(4, 8192), (1, 4, 8192))
+    assert "__launch_bounds__(1024)" in src and "sile_pid = (long long)blockIdx.x;" in src
+    # the row loop (4 iterations, loops inside) stays on every lane; the max,
+    # exp + sum and divide loops are spread
+    assert src.count("for (long long coop_it = coop_start + (long long)threadIdx.x") == 3
+    assert src.count("#pragma unroll 8") == 3
+    assert "coop_wg_first_max(coop_p0, coop_i0" in src        # the max fold, from x0
+    assert "v_sum = coop_init1 + coop_wg_sum(coop_p1" in src or \
+           "v_sum = coop_init0 + coop_wg_sum(coop_p0" in src  # the sum of exp
+    # the tile is only touched at [r, e] by the spread loops: per-lane slices
+    assert "float v_tile_storage[4][8];" in src and "__shared__ float v_tile" not in src
+    assert "&(v_tile[(0LL)][v_r][(v_e) / 1024LL])" in src
+    assert src.count("__syncthreads();\n  {\n") + src.count("__syncthreads();\n  goto") >= 3
+    pr = hip.llir_to_hip(parallel_reduce_llir(4096), None)
+    assert "coop_wg_sum" in pr and "if (threadIdx.x == 0) atomicAdd(v_o, v_acc);" in pr
+    va = hip.llir_to_hip(vec_add_llir(4096), (2, 1, 4096))
+    assert "__launch_bounds__(1024)" in va
+    for t, plan in ((softmax_llir(4, 8192), (1, 4, 8192)), (parallel_reduce_llir(4096), None),
+                    (vec_add_llir(4096), (2, 1, 4096))):
+        image, _ = hip.llir_compile(t, plan)
+        assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+@pytest.mark.parametrize("name,old,new", [
+    # a store to the same element every iteration (not one per iteration)
+    ("vec_add", "%pc = getelementptr f32, ptr addrspace(1) %c, i64 %idx",
+     "%pc = getelementptr f32, ptr addrspace(1) %c, i64 %base"),
+    # a carried value that is not a sum or a max fold
+    ("parallel_reduce", "%acc_next = fadd %acc, %s", "%acc_next = fmul %acc, %s"),
+    # the loop's bound is not a constant
+    ("parallel_reduce", "icmp slt %i, 4096", "icmp slt %i, %base"),
+])
+def test_loops_that_cannot_be_spread_stay_serial(name, old, new):
+    t = vec_add_llir(4096) if name == "vec_add" else parallel_reduce_llir(4096)
+    assert old in t
+    src = hip.llir_to_hip(t.replace(old, new), (2, 1, 4096) if name == "vec_add" else None)
+    assert "__launch_bounds__(64)" in src and "coop_" not in src
