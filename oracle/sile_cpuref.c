@@ -28,9 +28,10 @@
  *                                 seeds + products; a 2^24 order probe that fails for a seed
  *                                 added last; signed-zero seeds with K' = 0)
  *   cpuref_softmax_rows           pinned (same program body as cpuref_kernel_softmax)
- *   cpuref_reduce_rows            pinned (max exact vs numpy; sequential sum vs a left fold;
- *                                 the vec4 loop's windows, tail and over-read by closed forms
- *                                 over ones and order probes)
+ *   cpuref_reduce_rows            pinned (max exact vs numpy on finite rows, and the fold's
+ *                                 NaN / -inf / signed-zero cases by closed forms; sequential
+ *                                 sum vs a left fold; the vec4 loop's windows, tail and
+ *                                 over-read by closed forms over ones and order probes)
  *   cpuref_attention_causal       pinned by closed forms and fp64 brute force only; the
  *                                 reference has no attention kernel (no mask/iota/transpose
  *                                 in its DSL), so there is no reference vector for it.

@@ -865,10 +865,6 @@ __device__ __forceinline__ void reduce_rows_rowblock_kernel(int op, const void* 
   extern "C" __global__ __launch_bounds__(512) void sile_reduce_rows_##TAG##_b512(            \
       int op, const void* x, float* out, int64_t rows, int64_t ldx) {                       \
     reduce_rows_rowblock_kernel<IN, 512>(op, x, out, rows, ldx);                            \
-  }                                                                                         \
-  extern "C" __global__ __launch_bounds__(1024) void sile_reduce_rows_##TAG##_b1024(          \
-      int op, const void* x, float* out, int64_t rows, int64_t ldx) {                       \
-    reduce_rows_rowblock_kernel<IN, 1024>(op, x, out, rows, ldx);                           \
   }
 SILE_REDUCE_SHAPES(f32, kF32)
 SILE_REDUCE_SHAPES(f16, kF16)
