@@ -283,7 +283,7 @@ def test_reduce_rows_fused_sum_order_probes(hip):
 @pytest.mark.parametrize("cols,pitch_pad", [
     (13, 0), (100, 0), (256, 0),   # kL lanes per row (f32 up to 128, 16-bit up to 256)
     (1000, 0), (6000, 0),          # a wave per row, 16-byte chunks
-    (2048, 0), (4096, 0), (8192, 0),  # a row per 256 / 512 / 1024-thread workgroup
+    (2048, 0), (4096, 0), (8192, 0),  # a row per 256- or 512-thread workgroup (2 chunks a thread)
     (1000, 1), (37, 1),            # a wave per row, element loads (pitch not 16-byte aligned)
     (16384, 0), (65537, 0),        # a 1024-thread workgroup per row
 ])

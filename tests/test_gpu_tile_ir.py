@@ -175,7 +175,9 @@ def test_row_max_route_follows_the_fold(hip, cols, bm):
 def test_attention_route_matches_the_oracle(hip, bm, bn, d, n_q, s_k, programs, passes):
     """The DSL attention loop (K transposed, no mask), routed and launched:
     within fp32 tolerance (|g - r| <= 1e-5 + 1e-4 |r|) of the oracle's
-    statement of the same program; rows no program owns stay untouched."""
+    statement of the same program and of the oracle's non-causal attention
+    over the keys the program reads (whole BN blocks, K = kt^T); rows no
+    program owns stay untouched."""
     say(f"tile ir attention BM={bm} BN={bn} D={d} n_q={n_q} S={s_k} programs={programs}")
     scale = 1 / np.sqrt(d)
     r = rng(bm + bn + d)
@@ -188,4 +190,12 @@ def test_attention_route_matches_the_oracle(hip, bm, bn, d, n_q, s_k, programs, 
     rows = programs * bm
     ref = cpuref.dsl_attention_f32(q, kt, v, bn, np.float32(scale), np.float32(-1e30), n_q=rows)
     assert_close(got[:rows], ref, atol=1e-5, rtol=1e-4, what="routed attention")
+    n_keys = (s_k // bn) * bn
+    assert rows <= n_keys
+    qq = np.zeros((n_keys, d), np.float32)
+    qq[:rows] = q[:rows]
+    fwd = cpuref.attention_fwd(qq, np.ascontiguousarray(kt[:, :n_keys].T),
+                               np.ascontiguousarray(v[:n_keys]), np.float32(scale), causal=False,
+                               q_end=rows)[:rows]
+    assert_close(got[:rows], fwd, atol=1e-5, rtol=1e-4, what="routed attention vs attention_fwd")
     np.testing.assert_array_equal(got[rows:], 11.0)
