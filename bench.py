@@ -666,6 +666,37 @@ def bench_reduce_rows(name, steps, warmup, stream):
     return res
 
 
+def bench_matvec(name, steps, warmup, stream, bk=32):
+    """The matvec program of crates/sile/examples/mlp.rs:26-44 over fp32
+    x [8192, 8192], y [8192] (BK = 32, bit-identical to the CPU backend):
+    sile_hip_matvec_f32, each launch reading x's 256 MiB from HBM (two inputs
+    rotate, 512 MiB, past the 256 MiB Infinity Cache).  Bytes per launch:
+    x, y and the output."""
+    rows = cols = 8192
+    log(f"[bench] {name}: generating inputs")
+    x = normal(11, (rows, cols), 1.0)
+    y = normal(12, (cols,), 1.0)
+    rotate = 2
+    xs = [hip.DeviceBuffer.from_array(x) for _ in range(rotate)]
+    del x
+    dy = hip.DeviceBuffer.from_array(y)
+    out = hip.DeviceBuffer(rows * 4)
+    nbytes = 4.0 * rows * cols + 4.0 * cols + 4.0 * rows
+
+    def launch(i):
+        hip.matvec_f32(rows, cols, bk, xs[i].ptr, cols, dy.ptr, out.ptr, 0.0, stream)
+
+    log(f"[bench] {name}: timing {steps} steps")
+    region = time_launches(launch, steps, warmup, stream, rotate=rotate)
+    res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS, None)
+    res["bytes_per_launch"] = nbytes
+    res["note"] = (f"matvec<BM, BK={bk}> (mlp.rs) over f32 x [{rows}, {cols}], y [{cols}], "
+                   "in the reference's order (bit-identical)")
+    for buf in xs + [dy, out]:
+        buf.close()
+    return res
+
+
 def bench_parallel_reduce(name, steps, warmup):
     """The reference's parallel_reduce (crates/sile/examples/parallel_reduce.rs: one atomic add of
     each program's fused vec4 tile sum into out[0]) over 64M fp32 elements,
@@ -892,6 +923,8 @@ ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_
 EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "tile_ir_softmax_f32_8192",
          "gemm_f32_exact_4096",
          "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
+         # the mlp example's matvec program (BK 32; _bk8: the example's BK)
+         "matvec_f32_8192", "matvec_f32_8192_bk8",
          # shapes off the headline configurations: 128 x 128 tiles, split K', the
          # transposed form (M x N x K)
          "gemm_bf16_2048x2048x2048", "gemm_bf16_128x8192x8192", "gemm_bf16_8192x64x8192",
@@ -949,6 +982,9 @@ def main():
             results[name] = bench_reduce_rows(name, args.steps, args.warmup, stream)
         elif name == "parallel_reduce_f32":
             results[name] = bench_parallel_reduce(name, args.steps, args.warmup)
+        elif name.startswith("matvec_f32_8192"):
+            bk = int(name.split("_bk")[-1]) if "_bk" in name else 32
+            results[name] = bench_matvec(name, args.steps, args.warmup, stream, bk=bk)
         elif name.startswith("gemm_f32_exact_"):
             size = int(name.split("_")[-1])
             results[name] = bench_gemm_f32_exact(name, size, args.steps, args.warmup, stream,

@@ -327,6 +327,18 @@ int sile_hip_mma_f32(int64_t m, int64_t n, int64_t k, const float *a, int64_t ld
                      int64_t ldb, sile_layout b_layout, const float *acc, int64_t ld_acc,
                      float acc_value, float *c, int64_t ldc, int64_t bk, sile_hip_stream stream);
 
+/* fp32 matrix-vector product in the order of the matvec DSL kernel
+ * (crates/sile/examples/mlp.rs:26-44): out[r] = ((seed + p_0) + p_1) + ...
+ * over the tiles t < k / bk of row r, p_t = x[r][t bk] y[t bk] + ... summed in
+ * order from the tile's first element (the fused map + reduce,
+ * crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:189-293),
+ * every product and sum rounded on its own.  x row-major [m, >= k] with row
+ * pitch ldx, y [>= (k / bk) bk], out [m]; seed is the accumulator's splat
+ * value (0.0f in the example).  Bit-identical to the CPU backend.  The
+ * router's matvec route calls it. */
+int sile_hip_matvec_f32(int64_t m, int64_t k, int64_t bk, const float *x, int64_t ldx,
+                        const float *y, float seed, float *out, sile_hip_stream stream);
+
 /* Row softmax of a [rows, cols] matrix: y = exp(x - max) / sum(exp(x - max))
  * per row with fp32 max/exp/sum (the softmax DSL kernel with BN = cols,
  * crates/sile/tests/backend_softmax.rs:3-15).  in/out dtypes: f16->f16,
@@ -425,8 +437,10 @@ typedef enum {
   SILE_ROUTE_SOFTMAX_TILES = 3, /* softmax chain, other tilings -> sile_hip_kernel_softmax */
   SILE_ROUTE_REDUCE_ROWS = 4,   /* load + reduce(axis 1) + store -> sile_hip_reduce_rows */
   SILE_ROUTE_ATOMIC_REDUCE = 5, /* load + sum + extract + atomic add -> sile_hip_kernel_parallel_reduce */
-  SILE_ROUTE_ATTENTION = 6      /* the DSL's online-softmax attention loop (K transposed)
+  SILE_ROUTE_ATTENTION = 6,     /* the DSL's online-softmax attention loop (K transposed)
                                    -> sile_hip_attention_f32_kt */
+  SILE_ROUTE_MATVEC = 7         /* the matvec loop (acc + reduce_sum(x tile * broadcast(y tile)))
+                                   -> sile_hip_matvec_f32 */
 } sile_route_kind;
 
 typedef struct {
@@ -438,15 +452,17 @@ typedef struct {
   int32_t rank[4];           /* rank of each operand (0: unused) */
   int32_t num_buffers;       /* buffer parameters of the kernel */
   int32_t seed_from_tile;    /* SILE_ROUTE_MATMUL: 1 = accumulator loaded from operand 3 */
-  float seed_value;          /* SILE_ROUTE_MATMUL: the accumulator's splat value otherwise */
+  float seed_value;          /* SILE_ROUTE_MATMUL / MATVEC: the accumulator's splat value
+                                (matmul: when seed_from_tile is 0) */
   float attn_scale;          /* SILE_ROUTE_ATTENTION: the score scale (1 without one) */
   float attn_m0;             /* SILE_ROUTE_ATTENTION: the running max's initial value */
   int64_t num_shapes;        /* shape values the route was made with */
   int64_t operand_shapes[8]; /* the operands' dims the route was made for */
   int64_t num_threadgroups;  /* the grid the route was made for */
   int64_t tile_m, tile_n, tile_k; /* BM, BN, BK (TILE in tile_n for the atomic reduce;
-                                      BM, BN, D for attention) */
-  int64_t rows, cols;        /* extents handed to the row kernels; attention: queries, keys */
+                                      BM, BN, D for attention; BM, -, BK for matvec) */
+  int64_t rows, cols;        /* extents handed to the row kernels; attention: queries, keys;
+                                matvec: rows, K */
   char reason[512];          /* SILE_ROUTE_NONE: why each detector declined */
 } sile_hip_route;
 

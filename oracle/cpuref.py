@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
         L.cpuref_dsl_attention_f32.argtypes = [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64,
                                                _I64, _I64, ctypes.c_float, ctypes.c_float,
                                                _I64, _I64]
+        L.cpuref_dsl_matvec_f32.argtypes = [_P, _I64, _P, _P, _I64, _I64, _I64, ctypes.c_float]
         L.cpuref_bf16_from_f32.argtypes = [_P, _P, _I64]
         L.cpuref_f32_from_bf16.argtypes = [_P, _P, _I64]
         L.cpuref_e4m3_encode.argtypes = [_P, _P, _I64, ctypes.c_float]
@@ -194,6 +195,18 @@ def attention_fwd(q, k, v, scale, causal=True, q_begin=0, q_end=None, out=None):
     lib().cpuref_attention_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s, d, float(scale),
                                1 if causal else 0, q_begin, q_end)
     return o
+
+
+def dsl_matvec_f32(x, y, bk, m=None, k=None, seed=0.0):
+    """The matvec program (crates/sile/examples/mlp.rs:26-44) over rows 0..m of
+    x [*, ldx] and y; k defaults to x's column count (the loop runs k / bk
+    whole tiles).  Returns out [m]."""
+    x, y = _f32(x), _f32(y)
+    m = x.shape[0] if m is None else m
+    k = x.shape[1] if k is None else k
+    out = np.zeros(m, dtype=np.float32)
+    lib().cpuref_dsl_matvec_f32(_ptr(x), x.shape[1], _ptr(y), _ptr(out), m, k, bk, float(seed))
+    return out
 
 
 def dsl_attention_f32(q, kt, v, bn, scale, m0, d=None, n_q=None, s_k=None):

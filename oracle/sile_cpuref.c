@@ -39,6 +39,11 @@
  *                                 scores), key truncation to whole BN blocks, the initial
  *                                 max's underflow closed form (m0 above every score: 0 / 0),
  *                                 and agreement with cpuref_attention_fwd (non-causal)
+ *   cpuref_dsl_matvec_f32         pinned by exact integer-valued rows, fp64 brute force, order
+ *                                 probes inside a tile ([2^24, 1, 1] gives 2^24, a tree gives
+ *                                 2^24 + 2) and across tiles (partials 2^24, 1, 1 in order),
+ *                                 K truncation to whole BK tiles, the seed, and -0.0 products
+ *                                 (+0.0 once added to the +0.0 seed)
  *   cpuref_e4m3_encode/decode     pinned (OCP e4m3fn table: 448 max, 2^-9 min subnormal,
  *                                 exhaustive decode/encode round trip of all 254 finite codes)
  *   cpuref_bf16_from_f32          pinned (RNE vs exhaustive cases and numpy bit tricks)
@@ -464,6 +469,38 @@ void cpuref_dsl_attention_f32(const float *q, int64_t ldq, const float *kt, int6
     }
     __builtin_free(acc);
     __builtin_free(sc);
+  }
+}
+
+/* The matvec program of crates/sile/examples/mlp.rs:26-44 (BM rows per
+ * program; the row order does not matter, every row is independent):
+ *   acc = constant(seed, [BM]); k_tiles = x.shape()[1] / BK;
+ *   for k < k_tiles: acc = acc + reduce_sum(x[rows, k-tile] * broadcast(y[k-tile]), 1)
+ * The product map feeds the reduce alone, so the reduce is the fused
+ * map + reduce (crates/sile-tile-ir/src/passes/lowering/block.rs:491-510,
+ * tile_compute/fused_reduce.rs:189-293): p = x0*y0, then p = p + xi*yi for
+ * i = 1 .. BK-1 in order, every product and sum rounded (no contraction);
+ * the carried add is the map addf of the [1, BM] accumulator and the
+ * [BM, 1] reduce, element r of both (lower.rs:643-691; the [BM, 1] tile's
+ * element (0, r) is its r-th element in row-major order).  Rows 0 .. m of
+ * x [*, ldx], y [*], out [m]; tiles = k / bk whole tiles of K. */
+void cpuref_dsl_matvec_f32(const float *x, int64_t ldx, const float *y, float *out, int64_t m,
+                           int64_t k, int64_t bk, float seed) {
+  const int64_t tiles = bk > 0 ? k / bk : 0;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < m; ++r) {
+    const float *xr = x + r * ldx;
+    float acc = seed;
+    for (int64_t t = 0; t < tiles; ++t) {
+      const float *xt = xr + t * bk, *yt = y + t * bk;
+      float p = xt[0] * yt[0];
+      for (int64_t i = 1; i < bk; ++i) {
+        const float prod = xt[i] * yt[i];
+        p = p + prod;
+      }
+      acc = acc + p;
+    }
+    out[r] = acc;
   }
 }
 

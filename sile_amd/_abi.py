@@ -64,10 +64,11 @@ class DeviceProps(ctypes.Structure):
 
 
 ROUTE_NONE, ROUTE_MATMUL, ROUTE_SOFTMAX_ROWS, ROUTE_SOFTMAX_TILES, ROUTE_REDUCE_ROWS, \
-    ROUTE_ATOMIC_REDUCE, ROUTE_ATTENTION = range(7)
+    ROUTE_ATOMIC_REDUCE, ROUTE_ATTENTION, ROUTE_MATVEC = range(8)
 ROUTE_NAMES = {ROUTE_NONE: "none", ROUTE_MATMUL: "matmul", ROUTE_SOFTMAX_ROWS: "softmax_rows",
                ROUTE_SOFTMAX_TILES: "softmax_tiles", ROUTE_REDUCE_ROWS: "reduce_rows",
-               ROUTE_ATOMIC_REDUCE: "atomic_reduce", ROUTE_ATTENTION: "attention"}
+               ROUTE_ATOMIC_REDUCE: "atomic_reduce", ROUTE_ATTENTION: "attention",
+               ROUTE_MATVEC: "matvec"}
 
 
 class Route(ctypes.Structure):
@@ -152,6 +153,7 @@ SIGNATURES = {
     "sile_hip_flash_attn_fwd": [_I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _I32, _P],
     "sile_hip_attention_f32_kt": [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _F32,
                                   _F32, _P],
+    "sile_hip_matvec_f32": [_I64, _I64, _I64, _P, _I64, _P, _F32, _P, _P],
     "sile_hip_tile_ir_route": [ctypes.c_char_p, _P, _I64, _I64, ctypes.POINTER(Route)],
     "sile_hip_tile_ir_launch": [ctypes.POINTER(Route), _P, _I64, _P, _I64, _I64, _P],
 }
@@ -491,6 +493,10 @@ def attention_f32_kt(n_q, n_k, head_dim, q, ldq, kt, ldkt, v, ldv, o, ldo, scale
                      stream=None):
     call("sile_hip_attention_f32_kt", n_q, n_k, head_dim, q, ldq, kt, ldkt, v, ldv, o, ldo, scale,
          m0, _sh(stream))
+
+
+def matvec_f32(m, k, bk, x, ldx, y, out, seed=0.0, stream=None):
+    call("sile_hip_matvec_f32", m, k, bk, x, ldx, y, seed, out, _sh(stream))
 
 
 def dtype_bytes(t: int) -> int:

@@ -189,6 +189,146 @@ extern "C" __global__ __launch_bounds__(64) void sile_dsl_parallel_reduce_f32(
   }
 }
 
+struct MatvecArgs {
+  int64_t m;      // rows of the output (programs x BM)
+  int64_t ldx;    // row pitch of x in elements (shape(x)[1])
+  int64_t tiles;  // whole BK tiles of K: shape(x)[1] / BK
+  int64_t bk;
+  float seed;     // the accumulator's splat value
+};
+
+// Matvec program (crates/sile/examples/mlp.rs:26-44):
+//   out[r] = ((seed + p_0) + p_1) + ... + p_{tiles-1},
+//   p_t = x[r][t BK] y[t BK] + x[r][t BK + 1] y[t BK + 1] + ... in order,
+// every product and every sum rounded on its own (the fused map + reduce,
+// crates/sile-tile-ir/src/passes/lowering/tile_compute/fused_reduce.rs:189-293,
+// then the carried add).  One wave per row, four rows per workgroup: lane l
+// computes the partials of tiles l, l + 64, ... of its row, and the wave adds
+// them to the accumulator in tile order (lane 0 first, through readlane), so
+// the result is the reference's, bit for bit.  kVec4: x rows, y and BK allow
+// 16-byte loads.
+template <bool kVec4>
+__device__ __forceinline__ void matvec_rows(const float* __restrict__ x, const float* __restrict__ y,
+                                            float* __restrict__ out, const MatvecArgs& a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.m) return;   // the whole wave
+  const float* xr = x + row * a.ldx;
+  float acc = a.seed;
+  for (int64_t base = 0; base < a.tiles; base += 64) {
+    const int64_t t = base + lane;
+    float p = 0.0f;
+    if (t < a.tiles) {
+      const float* xt = xr + t * a.bk;
+      const float* yt = y + t * a.bk;
+      if constexpr (kVec4) {
+        f32x4 xv = *reinterpret_cast<const f32x4*>(xt);
+        f32x4 yv = *reinterpret_cast<const f32x4*>(yt);
+        p = xv[0] * yv[0];
+        p = p + xv[1] * yv[1];
+        p = p + xv[2] * yv[2];
+        p = p + xv[3] * yv[3];
+        for (int64_t i = 4; i < a.bk; i += 4) {
+          xv = *reinterpret_cast<const f32x4*>(xt + i);
+          yv = *reinterpret_cast<const f32x4*>(yt + i);
+          p = p + xv[0] * yv[0];
+          p = p + xv[1] * yv[1];
+          p = p + xv[2] * yv[2];
+          p = p + xv[3] * yv[3];
+        }
+      } else {
+        p = xt[0] * yt[0];
+        for (int64_t i = 1; i < a.bk; ++i) p = p + xt[i] * yt[i];
+      }
+    }
+    const int n = (int)min<int64_t>(64, a.tiles - base);
+    for (int i = 0; i < n; ++i)
+      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), i));
+  }
+  if (lane == 0) out[row] = acc;
+}
+
+// BK = 4 L with L = 1, 2, 4, 8 or 16 lanes a tile, x rows, y and BK allowing
+// 16-byte loads: the wave reads the row 256 elements at a time with one
+// 16-byte load per lane (coalesced; four such spans in flight), lane j holding
+// elements 4 j .. 4 j + 3 of a span, so tile g of a span lives on lanes
+// g L .. g L + L - 1 of one 16-lane DPP row.  Its sequential sum is carried
+// from lane to lane in L steps (a DPP shift by one lane), each lane adding its
+// four products in order, so the tile's partial, on its last lane, is the
+// reference's chain; the partials are then added to the accumulator in tile
+// order as above.
+template <int kL>
+__device__ __forceinline__ void matvec_rows_chain(const float* __restrict__ x,
+                                                  const float* __restrict__ y,
+                                                  float* __restrict__ out, const MatvecArgs& a) {
+#pragma clang fp contract(off)
+  constexpr int kU = 4;              // spans in flight
+  const int lane = threadIdx.x & 63, s = lane % kL;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.m) return;   // the whole wave
+  const float* xr = x + row * a.ldx;
+  const int64_t n = a.tiles * 4 * kL;   // elements of the whole tiles
+  float acc = a.seed;
+  for (int64_t base = 0; base < n; base += 256 * kU) {
+    f32x4 xv[kU], yv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t e = base + 256 * u + 4 * lane;
+      xv[u] = yv[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (e < n) {
+        xv[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + e));
+        yv[u] = *reinterpret_cast<const f32x4*>(y + e);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t b = base + 256 * u;
+      if (b >= n) break;
+      const float p0 = xv[u][0] * yv[u][0], p1 = xv[u][1] * yv[u][1];
+      const float p2 = xv[u][2] * yv[u][2], p3 = xv[u][3] * yv[u][3];
+      float p = 0.0f, carry = 0.0f;
+#pragma unroll
+      for (int step = 0; step < kL; ++step) {
+        float c = step == 0 ? p0 : carry + p0;
+        c = c + p1;
+        c = c + p2;
+        c = c + p3;
+        p = s == step ? c : p;
+        if (step + 1 < kL) carry = dpp<0x111>(p);   // row_shr:1
+      }
+      const int g_n = (int)min<int64_t>(64 / kL, (n - b) / (4 * kL));
+      for (int g = 0; g < g_n; ++g)
+        acc = acc + __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), g * kL + kL - 1));
+    }
+  }
+  if (lane == 0) out[row] = acc;
+}
+
+#define SILE_MATVEC_CHAIN(L)                                                                   \
+  extern "C" __global__ __launch_bounds__(256) void sile_dsl_matvec_f32_l##L(                 \
+      const float* x, const float* y, float* out, MatvecArgs a) {                              \
+    matvec_rows_chain<L>(x, y, out, a);                                                        \
+  }
+SILE_MATVEC_CHAIN(1)
+SILE_MATVEC_CHAIN(2)
+SILE_MATVEC_CHAIN(4)
+SILE_MATVEC_CHAIN(8)
+SILE_MATVEC_CHAIN(16)
+
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_matvec_f32(const float* x,
+                                                                       const float* y, float* out,
+                                                                       MatvecArgs a) {
+  matvec_rows<false>(x, y, out, a);
+}
+extern "C" __global__ __launch_bounds__(256) void sile_dsl_matvec_f32_v4(const float* x,
+                                                                          const float* y,
+                                                                          float* out,
+                                                                          MatvecArgs a) {
+  matvec_rows<true>(x, y, out, a);
+}
+
 // vec_add of crates/sile/tests/backend_vec_add.rs:3-9 (outside the hot path),
 // written against the generic tile-launch convention of sile_hip_launch_tiles:
 // (buffers, num_programs, shapes, num_shapes) with buffers = {a, b, c} and

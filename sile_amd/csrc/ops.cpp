@@ -609,6 +609,34 @@ int sile_hip_mma_f32(int64_t m, int64_t n, int64_t k, const float* a, int64_t ld
   return rc == SILE_OK ? ok() : rc;
 }
 
+int sile_hip_matvec_f32(int64_t m, int64_t k, int64_t bk, const float* x, int64_t ldx,
+                        const float* y, float seed, float* out, sile_hip_stream stream) {
+  if (m < 0 || k < 0) return fail(SILE_ERR_SHAPE, "negative extent");
+  if (bk <= 0) return fail(SILE_ERR_SHAPE, "matvec tile BK must be positive (got %lld)", (long long)bk);
+  if (m == 0) return ok();
+  if (!x || !y || !out) return fail(SILE_ERR_SHAPE, "NULL operand");
+  if (ldx < k) return fail(SILE_ERR_SHAPE, "leading dimension smaller than K");
+  const int64_t blocks = (m + 3) / 4;
+  if (blocks > 0x7fffffffLL) return fail(SILE_ERR_SHAPE, "too many rows");
+  struct {
+    int64_t m, ldx, tiles, bk;
+    float seed;
+  } args{m, ldx, k / bk, bk, seed};
+  // 16-byte loads when every tile of every row starts on a 16-byte boundary;
+  // tiles of 1 .. 16 such chunks: coalesced spans with the chain carried
+  // across lanes, else a lane per tile
+  const bool vec4 = bk % 4 == 0 && ldx % 4 == 0 && aligned16(x) && aligned16(y);
+  char name[40];
+  if (vec4 && (bk == 4 || bk == 8 || bk == 16 || bk == 32 || bk == 64))
+    snprintf(name, sizeof name, "sile_dsl_matvec_f32_l%d", (int)(bk / 4));
+  else
+    snprintf(name, sizeof name, "%s", vec4 ? "sile_dsl_matvec_f32_v4" : "sile_dsl_matvec_f32");
+  void* params[] = {(void*)&x, (void*)&y, &out, &args};
+  int rc = launch(Module::kDsl, name, dim3((unsigned)blocks), dim3(256), params,
+                  static_cast<hipStream_t>(stream));
+  return rc == SILE_OK ? ok() : rc;
+}
+
 // ---------------------------------------------------------------------------
 // Row softmax / row reduce
 // ---------------------------------------------------------------------------

@@ -17,7 +17,9 @@
 //   * load + reduce + extract + atomic add -> the parallel-reduce kernel
 //     (crates/sile/examples/parallel_reduce.rs:3-9);
 //   * the online-softmax attention loop the DSL can write (K given
-//     transposed, no mask) -> the fp32 attention kernel.
+//     transposed, no mask) -> the fp32 attention kernel;
+//   * the matvec loop (crates/sile/examples/mlp.rs:26-44) -> the matvec
+//     kernel (bit-identical to the CPU backend).
 // A route is taken only where the routed kernel writes exactly the elements,
 // in exactly the tile decomposition, that the CPU backend's launch wrapper
 // writes for the same shapes and grid (crates/sile-backend/src/cpu/codegen.rs:409-555).
@@ -1347,6 +1349,142 @@ Match match_attention(const Function& fn) {
   return m;
 }
 
+// A tile load, whether the fusion pass folded it into a map (Expr::Load) or
+// left it standing (a value defined by load_ptr_tko in block b).
+struct TileLoad {
+  uint32_t buf = 0, row = 0, col = 0;
+  int64_t rows = 0, cols = 0, stride = 0;
+};
+bool tile_load_of(const Block& b, const ExprP& e, TileLoad& out) {
+  if (e->k == Expr::Load) {
+    out = TileLoad{e->buf, e->row, e->col, e->rows, e->cols, e->stride};
+    return true;
+  }
+  if (e->k != Expr::Value) return false;
+  const Inst* i = find_inst(b, e->v);
+  if (!i || i->op != Op::LoadTko) return false;
+  out = TileLoad{i->uses[0], i->uses[1], i->uses[2], i->rows, i->cols, i->stride};
+  return true;
+}
+
+// The matvec kernel of crates/sile/examples/mlp.rs:26-44:
+//   acc = constant(s, [BM]); k_tiles = x.shape()[1] / BK;
+//   for k in 0..k_tiles {
+//     acc = acc + reduce_sum(x.load_tile([BM, BK], [pid, k]) *
+//                            y.load_tile([BK], [k]).broadcast([BM, BK]), 1) }
+//   z.store(acc)
+// with x rank 2, y and z rank 1: the [1, BM] accumulator is stored at
+// [0, pid] (lower.rs:777-821).  Fused (the product and the broadcast load
+// folded into one map, pointwise_fusion.rs:5-235) and unfused forms alike.
+Match match_matvec(const Function& fn) {
+  const Block* entry = fn.block(fn.entry);
+  if (entry->term.k != Term::Br || entry->term.targs.size() != 2)
+    no_route("entry block does not jump into a loop with (k, acc)");
+  if (!is_const(*entry, entry->term.targs[0], 0)) no_route("loop counter does not start at constant 0");
+  const Inst* acc_seed = find_inst(*entry, entry->term.targs[1]);
+  if (!acc_seed || acc_seed->op != Op::Splat || acc_seed->ty.k != Ty::Tile || acc_seed->ty.rows != 1)
+    no_route("accumulator is not a [1, BM] splat");
+  const int64_t bm = acc_seed->ty.cols;
+
+  const Block* header = fn.block(entry->term.t);
+  if (header->params.size() != 2) no_route("loop header does not carry (k, acc)");
+  const uint32_t loop_k = header->params[0], loop_acc = header->params[1];
+  const Term& ht = header->term;
+  if (ht.k != Term::CondBr || ht.targs != std::vector<uint32_t>{loop_k, loop_acc} ||
+      ht.fargs != std::vector<uint32_t>{loop_acc})
+    no_route("loop header does not branch with (k, acc) / (acc)");
+  const Inst* cmp = find_inst(*header, ht.cond);
+  if (!cmp || cmp->op != Op::ICmp || cmp->sub != "lt" || cmp->uses[0] != loop_k)
+    no_route("loop condition is not k < bound");
+  auto def = [&](uint32_t v) {
+    const Inst* i = find_inst(*header, v);
+    return i ? i : find_inst(*entry, v);
+  };
+  const Inst* ktiles = def(cmp->uses[1]);
+  if (!ktiles || ktiles->op != Op::IBin || ktiles->sub != "divi") no_route("loop bound is not a division");
+  const Inst* bk_inst = def(ktiles->uses[1]);
+  if (!bk_inst || bk_inst->op != Op::ConstI64 || bk_inst->ival <= 0)
+    no_route("loop bound divisor is not a positive constant");
+  const int64_t bk = bk_inst->ival;
+  const Inst* sdim = def(ktiles->uses[0]);
+  if (!sdim || sdim->op != Op::ShapeDim || sdim->ival != 1) no_route("loop bound is not shape(x)[1] / BK");
+  const Param* sdesc = fn.param(sdim->uses[0]);
+  if (!sdesc || sdesc->kind != Param::Shape) no_route("shape_dim of a non-descriptor");
+  const uint32_t x_buf = sdesc->source;
+
+  const Block* body = fn.block(ht.t);
+  if (body->params.size() != 2) no_route("loop body does not take (k, acc)");
+  const uint32_t body_k = body->params[0], body_acc = body->params[1];
+  if (body->term.k != Term::Br || body->term.t != header->id || body->term.targs.size() != 2)
+    no_route("loop body does not jump back with (k', acc')");
+  const Inst* next_k = find_inst(*body, body->term.targs[0]);
+  if (!next_k || next_k->op != Op::IBin || next_k->sub != "addi") no_route("loop step is not an addition");
+  const uint32_t one = next_k->uses[0] == body_k ? next_k->uses[1]
+                       : next_k->uses[1] == body_k ? next_k->uses[0] : UINT32_MAX;
+  if (one == UINT32_MAX || !is_const(*body, one, 1)) no_route("loop step is not k + 1");
+
+  // acc' = acc + reduce_sum(..., 1), either operand order
+  const ExprP next = expand(*body, body->term.targs[1]);
+  if (next->k != Expr::Add || next->a.size() != 2) no_route("carried accumulator is not acc + partial");
+  uint32_t red_v;
+  if (is_val(next->a[0], body_acc) && next->a[1]->k == Expr::Value)
+    red_v = next->a[1]->v;
+  else if (is_val(next->a[1], body_acc) && next->a[0]->k == Expr::Value)
+    red_v = next->a[0]->v;
+  else
+    no_route("carried accumulator is not acc + partial");
+  const Inst* red = find_inst(*body, red_v);
+  if (!red || red->op != Op::Reduce || red->is_max || red->axis != 1 || red->rows != bm ||
+      red->cols != bk)
+    no_route("partial is not a row sum of a [BM, BK] tile");
+  // the reduced tile: x tile * broadcast(y tile), either order
+  const ExprP prod = expand(*body, red->uses[0]);
+  if (prod->k != Expr::Mul || prod->a.size() != 2) no_route("reduced tile is not a product");
+  TileLoad lx, ly;
+  ExprP other;
+  if (tile_load_of(*body, prod->a[0], lx)) {
+    other = prod->a[1];
+  } else if (tile_load_of(*body, prod->a[1], lx)) {
+    other = prod->a[0];
+  } else {
+    no_route("product has no tile load of x");
+  }
+  if (other->k != Expr::Bcast || other->rows != 1 || other->cols != bk || other->a.size() != 1 ||
+      !tile_load_of(*body, other->a[0], ly))
+    no_route("product's other factor is not a broadcast [1, BK] tile load");
+  if (lx.buf != x_buf || lx.rows != bm || lx.cols != bk || lx.stride != 1 || lx.col != body_k)
+    no_route("x tile is not x[pid, k] of [BM, BK]");
+  const uint32_t pid = lx.row;
+  if (launch_dim(fn, pid) != 0) no_route("x tile row is not launch index 0");
+  if (ly.rows != 1 || ly.cols != bk || ly.stride != 0 || ly.col != body_k || !is_const(*body, ly.row, 0))
+    no_route("y tile is not y[k] of [BK] (rank 1)");
+
+  const Block* exit = fn.block(ht.f);
+  if (exit->params.size() != 1 || exit->term.k != Term::Ret) no_route("loop exit does not take acc and return");
+  const Inst* st = nullptr;
+  for (const Inst& i : exit->insts) {
+    if (i.op == Op::ConstI64) continue;
+    if (st || i.op != Op::StoreTko) no_route("loop exit holds more than the store");
+    st = &i;
+  }
+  if (!st || st->uses[1] != exit->params[0] || st->stride != 0 || st->rows != 1 || st->cols != bm ||
+      !is_const(*exit, st->uses[2], 0) || st->uses[3] != pid)
+    no_route("loop exit does not store acc at [0, pid] of a rank-1 output");
+
+  Match m;
+  m.kind = SILE_ROUTE_MATVEC;
+  m.ops[0] = operand_of(fn, x_buf);
+  m.ops[1] = operand_of(fn, ly.buf);
+  m.ops[2] = operand_of(fn, st->uses[0]);
+  m.nops = 3;
+  if (m.ops[0].rank != 2 || m.ops[1].rank != 1 || m.ops[2].rank != 1)
+    no_route("operand ranks are not x 2, y 1, z 1");
+  m.tm = bm;
+  m.tk = bk;
+  m.seed_value = acc_seed->fval;
+  return m;
+}
+
 // Tries each detector; collects the reasons of the ones that did not fire.
 Match detect(const Function& fn, std::string& reasons) {
   struct TypesScope {
@@ -1360,6 +1498,7 @@ Match detect(const Function& fn, std::string& reasons) {
       {"row reduce", match_row_reduce},
       {"atomic reduce", match_atomic_reduce},
       {"attention", match_attention},
+      {"matvec", match_matvec},
   };
   for (const auto& d : detectors) {
     try {
@@ -1418,6 +1557,22 @@ void plan(const Match& m, const int64_t* shapes, int64_t programs, sile_hip_rout
       return decline("K^T / V do not cover the key tiles");
     r->rows = run * m.tm;
     r->cols = n_keys;
+  } else if (m.kind == SILE_ROUTE_MATVEC) {
+    // z rank 1: total = shape(z)[0] programs at most (codegen.rs:409-431);
+    // program pid writes z[pid BM .. pid BM + BM) from rows of x
+    const Operand &x = m.ops[0], &y = m.ops[1], &z = m.ops[2];
+    auto decline = [&](const char* why) {
+      r->kind = SILE_ROUTE_NONE;
+      set_reason(r, std::string("matvec: ") + why);
+    };
+    const int64_t run = std::max<int64_t>(0, std::min(programs, dim(shapes, z, 0)));
+    const int64_t rows = run * m.tm;
+    const int64_t k = dim(shapes, x, 1);
+    if (rows > dim(shapes, z, 0)) return decline("programs would write past the rank-1 output");
+    if (rows > dim(shapes, x, 0)) return decline("x does not cover the programs' rows");
+    if (dim(shapes, y, 0) < (k / m.tk) * m.tk) return decline("y does not cover the K tiles");
+    r->rows = rows;
+    r->cols = k;
   } else if (m.kind == SILE_ROUTE_SOFTMAX_TILES) {
     const Operand &x = m.ops[0], &y = m.ops[1];
     const int64_t tiles_n = m.tn > 0 ? dim(shapes, y, 1) / m.tn : 0;
@@ -1521,7 +1676,8 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
                 (long long)route->num_shapes);
   if (!buffers || (num_shapes > 0 && !shapes)) return fail(SILE_ERR_SHAPE, "NULL buffers / shapes");
   const int nops = route->kind == SILE_ROUTE_MATMUL ? (route->seed_from_tile ? 4 : 3)
-                   : route->kind == SILE_ROUTE_ATTENTION ? 4 : 2;
+                   : route->kind == SILE_ROUTE_ATTENTION ? 4
+                   : route->kind == SILE_ROUTE_MATVEC ? 3 : 2;
   void* bufs[4] = {nullptr, nullptr, nullptr, nullptr};
   int64_t shp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int64_t nshp = 0;
@@ -1562,6 +1718,13 @@ int sile_hip_tile_ir_launch(const sile_hip_route* route, void* const* buffers,
                                      static_cast<const float*>(bufs[2]), shp[5],
                                      static_cast<float*>(bufs[3]), shp[7], route->attn_scale,
                                      route->attn_m0, stream);
+      break;
+    case SILE_ROUTE_MATVEC:
+      // x [x0, x1] (row pitch x1 = K), y [y0], z [z0]
+      rc = sile_hip_matvec_f32(route->rows, route->cols, route->tile_k,
+                               static_cast<const float*>(bufs[0]), shp[1],
+                               static_cast<const float*>(bufs[1]), route->seed_value,
+                               static_cast<float*>(bufs[2]), stream);
       break;
     case SILE_ROUTE_SOFTMAX_ROWS:
       // x [x0, x1], y [y0, y1]: rows of BN elements at leading dimensions x1 / y1

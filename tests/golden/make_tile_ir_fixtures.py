@@ -1,6 +1,7 @@
 """Writes tests/golden/tile_ir/*.tir: the printed Tile IR of the DSL kernels
 with the constants of the reference's own end-to-end tests (matmul 2/2/2,
-softmax 2/8, parallel_reduce 1000, vec_add 4), derived as tests/tile_ir_text.py
+softmax 2/8, parallel_reduce 1000, vec_add 4, the mlp example's matvec
+32/8), derived as tests/tile_ir_text.py
 describes.  Run: python tests/golden/make_tile_ir_fixtures.py
 """
 import os
@@ -23,6 +24,8 @@ FIXTURES = {
     "attention_32x64x128.tir": T.attention(32, 64, 128, 0.08838834764831845),
     "attention_32x64x128_unfused.tir": T.attention(32, 64, 128, 0.08838834764831845,
                                                    passes=False),
+    "matvec_32x8.tir": T.matvec(32, 8),               # crates/sile/examples/mlp.rs:68-89
+    "matvec_32x8_unfused.tir": T.matvec(32, 8, passes=False),
 }
 
 

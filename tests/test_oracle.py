@@ -430,6 +430,58 @@ def test_dsl_attention_closed_forms():
                  rtol=1e-5, what="vs attention_fwd")
 
 
+
+# ---------------------------------------------------------------- matvec (mlp.rs)
+
+@pytest.mark.parametrize("m,k,bk", [(7, 64, 8), (33, 100, 3), (5, 1000, 32), (4, 9, 1)])
+def test_dsl_matvec_fp64(m, k, bk):
+    """The matvec program equals x[:, :K'] @ y[:K'] for K' = (k / bk) * bk,
+    within fp32 rounding of the sequential sums."""
+    r = rng(m + k + bk)
+    x = r.normal(size=(m, k)).astype(np.float32)
+    y = r.normal(size=k).astype(np.float32)
+    kp = (k // bk) * bk
+    want = x[:, :kp].astype(np.float64) @ y[:kp].astype(np.float64)
+    bound = 1e-6 * (np.abs(x[:, :kp]).astype(np.float64) @ np.abs(y[:kp]) + 1)
+    got = cpuref.dsl_matvec_f32(x, y, bk)
+    assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) / bound)
+
+
+def test_dsl_matvec_exact_and_order():
+    """Closed forms that pin the program's order of operations
+    (fused_reduce.rs:189-293 inside a tile, the carried add across tiles)."""
+    big = np.float32(2 ** 24)
+    # integer-valued rows: exact
+    r = rng(5)
+    x = r.integers(-8, 9, size=(6, 48)).astype(np.float32)
+    y = r.integers(-8, 9, size=48).astype(np.float32)
+    np.testing.assert_array_equal(cpuref.dsl_matvec_f32(x, y, 16), (x @ y).astype(np.float32))
+    ones = np.ones(4, np.float32)
+    row = np.array([[big, 1, 1, 1]], np.float32)
+    # one tile: sequential from element 0 gives 2^24 (each + 1 rounds back);
+    # a pairwise tree would give 2^24 + 2, the reverse order 2^24 + 4
+    assert cpuref.dsl_matvec_f32(row, ones, 4)[0] == big
+    # four tiles of one: the partials 2^24, 1, 1, 1 added to the seed in order
+    assert cpuref.dsl_matvec_f32(row, ones, 1)[0] == big
+    # the seed comes first: 2^24 + 1 + 1 = 2^24 (partials first would give 2^24 + 2)
+    assert cpuref.dsl_matvec_f32(np.ones((1, 2), np.float32), ones[:2], 1, seed=big)[0] == big
+    # products rounded on their own: (1 + 2^-12)^2 rounds to 1 + 2^-11, which
+    # cancels the first product exactly; a fused multiply-add would leave 2^-24
+    a = np.float32(1 + 2 ** -12)
+    x2 = np.array([[1.0, a]], np.float32)
+    y2 = np.array([-(1 + 2 ** -11), a], np.float32)
+    assert cpuref.dsl_matvec_f32(x2, y2, 2)[0] == 0.0
+    # K truncated to whole tiles: what lies past them never enters
+    x3 = np.array([[1, 2, 3, 4, 5, 6, np.nan, np.inf]], np.float32)
+    assert cpuref.dsl_matvec_f32(x3, np.ones(8, np.float32), 3, k=8)[0] == 21.0
+    # no whole tile: the seed
+    assert cpuref.dsl_matvec_f32(x3, np.ones(8, np.float32), 9, seed=2.5)[0] == 2.5
+    # -0.0 products: +0.0 once added to the +0.0 seed, -0.0 from a -0.0 seed
+    z = cpuref.dsl_matvec_f32(np.array([[-0.0]], np.float32), np.ones(1, np.float32), 1)
+    assert z[0] == 0.0 and not np.signbit(z[0])
+    z = cpuref.dsl_matvec_f32(np.array([[-0.0]], np.float32), np.ones(1, np.float32), 1, seed=-0.0)
+    assert np.signbit(z[0])
+
 # ---------------------------------------------------------------- number formats
 
 def _e4m3_table():

@@ -98,7 +98,7 @@ def test_vec_add_has_no_route(passes):
     r = _route(T.vec_add(4, passes), [8, 8, 8], 2)
     assert r.kind == hip.ROUTE_NONE
     why = r.reason.decode()
-    for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:", "attention:"):
+    for d in ("matmul:", "softmax:", "row reduce:", "atomic reduce:", "attention:", "matvec:"):
         assert d in why
     assert list(r.buffer) == [-1, -1, -1, -1]
 
@@ -316,3 +316,81 @@ def test_attention_detector_rejections(name):
     r = _route(text.replace(old, new), _attn_shapes(), 8)
     assert r.kind == hip.ROUTE_NONE, name
     assert b"attention:" in r.reason
+
+
+# ---------------------------------------------------------------- matvec (mlp.rs)
+
+def _mv_shapes(m=64, k=64, ky=None, mz=None):
+    """x [m, k], y [ky], z [mz]."""
+    return [m, k, ky if ky is not None else k, mz if mz is not None else m]
+
+
+@pytest.mark.parametrize("passes", [True, False])
+def test_matvec_routes(passes):
+    """The mlp example's matvec loop routes to the matvec kernel: rows =
+    programs * BM, K = shape(x)[1], BK and the seed from the text."""
+    r = _route(T.matvec(32, 8, passes=passes), _mv_shapes(), 2)
+    assert r.kind == hip.ROUTE_MATVEC, r.reason
+    assert (r.tile_m, r.tile_k, r.rows, r.cols) == (32, 8, 64, 64)
+    assert list(r.buffer[:3]) == [0, 1, 2] and list(r.shape_offset[:3]) == [0, 2, 3]
+    assert r.seed_value == 0.0
+    # fewer programs than row tiles; K not a multiple of BK; another seed
+    r = _route(T.matvec(16, 5, passes=passes, seed=1.5), _mv_shapes(m=100, k=23, ky=20, mz=96), 3)
+    assert r.kind == hip.ROUTE_MATVEC, r.reason
+    assert (r.rows, r.cols, r.tile_k, r.seed_value) == (48, 23, 5, 1.5)
+    # the factors in the other order (a program that loads y first)
+    t = T.matvec(32, 8, passes=passes)
+    if passes:
+        t = t.replace("map mulf(load_ptr_tko(%0, [%3, %13], shape=[32, 8], stride_dim=1), "
+                      "broadcast(load_ptr_tko(%1, [%17, %13], shape=[1, 8], stride_dim=0), "
+                      "src_shape=[1, 8]))",
+                      "map mulf(broadcast(load_ptr_tko(%1, [%17, %13], shape=[1, 8], "
+                      "stride_dim=0), src_shape=[1, 8]), load_ptr_tko(%0, [%3, %13], "
+                      "shape=[32, 8], stride_dim=1))")
+    else:
+        t = t.replace("%20 = mulf %15, %19", "%20 = mulf %19, %15")
+    t = t.replace("addf(%14, %21)", "addf(%21, %14)").replace("addf %14, %21", "addf %21, %14")
+    assert _route(t, _mv_shapes(), 2).kind == hip.ROUTE_MATVEC
+
+
+def test_matvec_route_declines_uncovered_shapes():
+    text = T.matvec(32, 8)
+    for shapes, grid, why in [(_mv_shapes(m=32, mz=64), 2, b"x does not cover"),
+                              (_mv_shapes(mz=48), 2, b"past the rank-1 output"),
+                              (_mv_shapes(ky=56), 2, b"y does not cover")]:
+        r = _route(text, shapes, grid)
+        assert r.kind == hip.ROUTE_NONE and why in r.reason, (shapes, r.reason)
+    # y may be longer than K; the grid may exceed z's tiles only within z
+    assert _route(text, _mv_shapes(ky=100), 2).kind == hip.ROUTE_MATVEC
+
+
+MATVEC_MUTATIONS = {
+    # each breaks one condition of the matvec program
+    "reduce max": ('combiner = "sum"', 'combiner = "max"'),
+    "reduce axis 0": ("axis = 1, combiner", "axis = 0, combiner"),
+    "acc times partial": ("map addf(%14, %21)", "map mulf(%14, %21)"),
+    "acc dropped": ("map addf(%14, %21)", "map addf(%21, %21)"),
+    "sum not product": ("%20 = map mulf(", "%20 = map addf("),
+    "x walked by (k, pid)": ("load_ptr_tko(%0, [%3, %13]", "load_ptr_tko(%0, [%13, %3]"),
+    "y not broadcast": ("broadcast(load_ptr_tko(%1, [%17, %13], shape=[1, 8], stride_dim=0), "
+                        "src_shape=[1, 8])",
+                        "load_ptr_tko(%1, [%17, %13], shape=[32, 8], stride_dim=0)"),
+    "y at row 1": ("%17 = constant <i64: 0>", "%17 = constant <i64: 1>"),
+    "bound BK differs": ("%7 = constant <i64: 8>", "%7 = constant <i64: 4>"),
+    "bound from y": ("%6 = sile.shape_dim %5 {dim = 1}", "%6 = sile.shape_dim %16 {dim = 1}"),
+    "step 2": ("%23 = constant <i64: 1>", "%23 = constant <i64: 2>"),
+    "seed not a splat": ("cf.br ^bb1(%11, %4)", "cf.br ^bb1(%11, %11)"),
+    "store at [pid, 0]": ("[%27, %3] {shape = [1, 32]", "[%3, %27] {shape = [1, 32]"),
+    "stored value not acc": ("store_ptr_tko %2, %25,", "store_ptr_tko %2, %27,"),
+    "counter from 1": ("%11 = constant <i64: 0>", "%11 = constant <i64: 1>"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MATVEC_MUTATIONS))
+def test_matvec_detector_rejections(name):
+    old, new = MATVEC_MUTATIONS[name]
+    text = T.matvec(32, 8)
+    assert old in text, name
+    r = _route(text.replace(old, new, 1), _mv_shapes(), 2)
+    assert r.kind == hip.ROUTE_NONE, name
+    assert b"matvec:" in r.reason

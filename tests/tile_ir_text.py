@@ -18,6 +18,7 @@ The kernels (DSL source as in crates/sile/examples/*.rs):
   matmul_acc<BM,BN,BK>  not in the reference: the matmul with its accumulator
                         loaded from a tile (`d.load_tile` or `c.load_tile`)
   gemm<BM,BN,BK>        crates/sile/examples/mlp.rs:6-23
+  matvec<BM,BK>         crates/sile/examples/mlp.rs:26-44
   softmax<BM,BN>        crates/sile/examples/softmax.rs:3-16
   parallel_reduce<TILE> crates/sile/examples/parallel_reduce.rs:3-9
   vec_add<TILE>         crates/sile/examples/vec_add.rs:3-14
@@ -154,7 +155,9 @@ def mlp_gemm(bm, bn, bk):
     before the loop, so the bound's division sits in the entry block and the
     reference's CanonicalMatmulPlan::detect (canonical_matmul.rs:511-534,
     which looks for it in the loop header) declines it; the general tile-MMA
-    lowering (LoopCarriedSplat seed 0.0) gives the same per-cell chain."""
+    lowering (LoopCarriedSplat seed 0.0) gives the same per-cell chain.  The
+    loop's block parameters take their value ids before the start constant
+    (lower.rs:266-283)."""
     acc = _tile(bm, bn)
     params = [_param_buf(0, "x", 2), _param_buf(1, "y", 2), _param_buf(2, "z", 2),
               _param_launch(3, 0), _param_launch(4, 1), _param_shape(6, 0, "x", 2),
@@ -164,11 +167,11 @@ def mlp_gemm(bm, bn, bk):
                   "%7 = sile.shape_dim %6 {dim = 1} : tile<i64>",
                   f"%8 = constant <i64: {bk}> : tile<i64>",
                   "%9 = divi %7, %8 : tile<i64>",
-                  "%10 = constant <i64: 0> : tile<i64>",
-                  "cf.br ^bb1(%10, %5)"]),
-        (f"^bb1(%11: tile<i64>, %12: {acc})",
-         ['%13 = cmpi "lt" %11, %9 : tile<i64>',
-          "cf.cond_br %13, ^bb2(%11, %12), ^bb3(%12)"]),
+                  "%12 = constant <i64: 0> : tile<i64>",
+                  "cf.br ^bb1(%12, %5)"]),
+        (f"^bb1(%10: tile<i64>, %11: {acc})",
+         ['%13 = cmpi "lt" %10, %9 : tile<i64>',
+          "cf.cond_br %13, ^bb2(%10, %11), ^bb3(%11)"]),
         (f"^bb2(%14: tile<i64>, %15: {acc})",
          [f"%16 = load_ptr_tko %0, [%3, %14] {{shape = [{bm}, {bk}], stride_dim = 1}} : "
           f"{_tile(bm, bk)}",
@@ -183,6 +186,71 @@ def mlp_gemm(bm, bn, bk):
           "return"]),
     ]
     return _module("gemm", params, blocks)
+
+
+def matvec(bm, bk, passes=True, seed=0.0):
+    """The matvec kernel of crates/sile/examples/mlp.rs:26-44:
+
+        let m_idx = tile::id().0;
+        let mut acc = sile::constant(SEED, [BM]);
+        let k_tiles = x.shape()[1] / BK;
+        for k_idx in 0..k_tiles {
+            let tile_x = x.load_tile([BM, BK], [m_idx, k_idx]);
+            let tile_y = y.load_tile([BK], [k_idx]).broadcast(&[BM, BK]);
+            let partial = sile::reduce_sum(tile_x * tile_y, 1);
+            acc = acc + partial;
+        }
+        z.store(acc);
+
+    x rank 2, y and z rank 1.  The [BM] constant is a [1, BM] tile and the
+    rank-1 loads are [1, BK] at [0, k] (lower.rs:514-546, 946-967); the loop
+    carries acc (find_loop_carried_vars keeps the names defined before the
+    loop, lower.rs:253-260, 448-465); y's shape descriptor is created at its
+    load in the body, z's at the store, which writes [1, BM] at [0, pid]
+    (lower.rs:777-821).  After the passes the product, the broadcast and both
+    single-use loads fold into one map (pointwise_fusion.rs:5-235; the loads
+    left standing and the broadcast map are dead, dce), and the carried add
+    becomes a map of two values."""
+    acc = _tile(1, bm)
+    params = [_param_buf(0, "x", 2), _param_buf(1, "y", 1), _param_buf(2, "z", 1),
+              _param_launch(3, 0), _param_shape(5, 0, "x", 2), _param_shape(16, 1, "y", 1),
+              _param_shape(26, 2, "z", 1)]
+    entry = [f"%4 = constant <f32: {_fmt_float(seed)}> : {acc}",
+             "%6 = sile.shape_dim %5 {dim = 1} : tile<i64>",
+             f"%7 = constant <i64: {bk}> : tile<i64>",
+             "%8 = divi %6, %7 : tile<i64>",
+             "%11 = constant <i64: 0> : tile<i64>",
+             "cf.br ^bb1(%11, %4)"]
+    header = (f"^bb1(%9: tile<i64>, %10: {acc})",
+              ['%12 = cmpi "lt" %9, %8 : tile<i64>',
+               "cf.cond_br %12, ^bb2(%9, %10), ^bb3(%10)"])
+    reduce = (f'%21 = reduce %20 {{axis = 1, combiner = "sum", input_shape = [{bm}, {bk}]}} : '
+              f"{_tile(bm, 1)}")
+    tail = ["%23 = constant <i64: 1> : tile<i64>", "%24 = addi %13, %23 : tile<i64>",
+            "cf.br ^bb1(%24, %22)"]
+    if passes:
+        body = ["%17 = constant <i64: 0> : tile<i64>",
+                f"%20 = map mulf(load_ptr_tko(%0, [%3, %13], shape=[{bm}, {bk}], stride_dim=1), "
+                f"broadcast(load_ptr_tko(%1, [%17, %13], shape=[1, {bk}], stride_dim=0), "
+                f"src_shape=[1, {bk}])) {{shape = [{bm}, {bk}]}} : {_tile(bm, bk)}",
+                reduce,
+                f"%22 = map addf(%14, %21) {{shape = [1, {bm}]}} : {acc}"] + tail
+    else:
+        body = [f"%15 = load_ptr_tko %0, [%3, %13] {{shape = [{bm}, {bk}], stride_dim = 1}} : "
+                f"{_tile(bm, bk)}",
+                "%17 = constant <i64: 0> : tile<i64>",
+                f"%18 = load_ptr_tko %1, [%17, %13] {{shape = [1, {bk}], stride_dim = 0}} : "
+                f"{_tile(1, bk)}",
+                f"%19 = broadcast %18 {{shape = [{bm}, {bk}]}} : {_tile(bm, bk)}",
+                f"%20 = mulf %15, %19 : {_tile(bm, bk)}",
+                reduce,
+                f"%22 = addf %14, %21 : {acc}"] + tail
+    exit_ = ["%27 = constant <i64: 0> : tile<i64>",
+             f"%28 = store_ptr_tko %2, %25, [%27, %3] {{shape = [1, {bm}], stride_dim = 0}} : none",
+             "return"]
+    return _module("matvec", params, [("^bb0", entry), header,
+                                      (f"^bb2(%13: tile<i64>, %14: {acc})", body),
+                                      (f"^bb3(%25: {acc})", exit_)])
 
 
 def softmax(bm, bn, passes=True):
