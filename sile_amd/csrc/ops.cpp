@@ -626,14 +626,20 @@ int sile_hip_matvec_f32(int64_t m, int64_t k, int64_t bk, const float* x, int64_
   // tiles of 1 .. 16 such chunks: coalesced spans with the chain carried
   // across lanes, else a lane per tile
   const bool vec4 = bk % 4 == 0 && ldx % 4 == 0 && aligned16(x) && aligned16(y);
+  // (BK 4 and 8: 8 rows a wave, so that one in-order add serves 8 rows)
   char name[40];
-  if (vec4 && (bk == 4 || bk == 8 || bk == 16 || bk == 32 || bk == 64))
+  int64_t rows_per_block = 4;
+  if (vec4 && (bk == 4 || bk == 8)) {
+    snprintf(name, sizeof name, "sile_dsl_matvec_f32_l%d_r8", (int)(bk / 4));
+    rows_per_block = 32;
+  } else if (vec4 && (bk == 16 || bk == 32 || bk == 64)) {
     snprintf(name, sizeof name, "sile_dsl_matvec_f32_l%d", (int)(bk / 4));
-  else
+  } else {
     snprintf(name, sizeof name, "%s", vec4 ? "sile_dsl_matvec_f32_v4" : "sile_dsl_matvec_f32");
+  }
   void* params[] = {(void*)&x, (void*)&y, &out, &args};
-  int rc = launch(Module::kDsl, name, dim3((unsigned)blocks), dim3(256), params,
-                  static_cast<hipStream_t>(stream));
+  int rc = launch(Module::kDsl, name, dim3((unsigned)((m + rows_per_block - 1) / rows_per_block)),
+                  dim3(256), params, static_cast<hipStream_t>(stream));
   return rc == SILE_OK ? ok() : rc;
 }
 

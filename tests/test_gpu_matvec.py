@@ -49,6 +49,9 @@ def _matvec(hip, x, y, bk, m=None, k=None, seed=0.0, x_off=0, y_off=0):
     (16, 1000, 16, 1000, 0),     # 62 tiles, K truncated to 992
     (16, 4096, 64, 4096, 0),     # 16 lanes a tile
     (8, 8200, 8, 8204, 0),       # pitch > K, 1025 tiles
+    # BK 4 and 8: eight rows a wave
+    (13, 1000, 8, 1000, 0),      # a wave with 5 rows past m
+    (37, 520, 4, 520, 0),        # 130 tiles, a partial last span
 ])
 def test_matvec_matches_the_oracle_bit_for_bit(hip, m, k, bk, ldx, x_off):
     say(f"matvec m={m} k={k} bk={bk} ldx={ldx} x_off={x_off}")
