@@ -666,7 +666,7 @@ def bench_reduce_rows(name, steps, warmup, stream):
     return res
 
 
-def bench_matvec(name, steps, warmup, stream, bk=32):
+def bench_matvec(name, steps, warmup, stream, traffic, bk=32):
     """The matvec program of crates/sile/examples/mlp.rs:26-44 over fp32
     x [8192, 8192], y [8192] (BK = 32, bit-identical to the CPU backend):
     sile_hip_matvec_f32, each launch reading x's 256 MiB from HBM (two inputs
@@ -688,7 +688,8 @@ def bench_matvec(name, steps, warmup, stream, bk=32):
 
     log(f"[bench] {name}: timing {steps} steps")
     region = time_launches(launch, steps, warmup, stream, rotate=rotate)
-    res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS, None)
+    res = summarise(name, nbytes, 1e9, "GB/s", region, steps, "hbm", PEAK_HBM_GBS,
+                    traffic.get(name))
     res["bytes_per_launch"] = nbytes
     res["note"] = (f"matvec<BM, BK={bk}> (mlp.rs) over f32 x [{rows}, {cols}], y [{cols}], "
                    "in the reference's order (bit-identical)")
@@ -916,7 +917,10 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
                    "sile_flash_attn", "gemm_f32_exact_4096": "sile_gemm_f32_exact",
                    "gemm_f32_exact_512": "sile_gemm_f32_exact",
                    "flash_attn_fwd_f16_s8000": "sile_flash_attn",
-                   "flash_attn_fwd_f16_s8192_d64": "sile_flash_attn"}
+                   "flash_attn_fwd_f16_s8192_d64": "sile_flash_attn",
+                   "matvec_f32_8192": "sile_dsl_matvec", "matvec_f32_8192_bk8": "sile_dsl_matvec",
+                   "llir_softmax_f32_8192": "sile_kernel_softmax",
+                   "tile_ir_softmax_f32_8192": "sile_softmax_rows"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
@@ -984,7 +988,7 @@ def main():
             results[name] = bench_parallel_reduce(name, args.steps, args.warmup)
         elif name.startswith("matvec_f32_8192"):
             bk = int(name.split("_bk")[-1]) if "_bk" in name else 32
-            results[name] = bench_matvec(name, args.steps, args.warmup, stream, bk=bk)
+            results[name] = bench_matvec(name, args.steps, args.warmup, stream, traffic, bk=bk)
         elif name.startswith("gemm_f32_exact_"):
             size = int(name.split("_")[-1])
             results[name] = bench_gemm_f32_exact(name, size, args.steps, args.warmup, stream,

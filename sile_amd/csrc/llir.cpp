@@ -655,17 +655,27 @@ void array_shape(const Type& t, Type& base, std::vector<int64_t>& dims) {
   base = *cur;
 }
 
+// The pointee qualifier of a pointer in LLIR address space `addr`.  Global
+// pointers (`ptr addrspace(1)`: the kernel's buffers and geps into them) keep
+// their address space, so the compiler issues global loads and stores: through
+// a generic pointer every access is a flat one, counted on the LDS counter as
+// well, and each workgroup barrier then waits for all of the lane's stores to
+// complete.  Other spaces stay generic (private and LDS tiles are declared as
+// arrays, whose space the compiler knows).
+std::string c_space(int addr) { return addr == 1 ? "__attribute__((address_space(1))) " : ""; }
+
 // declaration of `name` with type t
 std::string c_decl(const Type& t, const std::string& name) {
   if (t.k == TK::Ptr) {
-    if (!t.elem) return "float* " + name;  // untyped pointer: the CPU wrapper's float*
+    const std::string q = c_space(t.addr);
+    if (!t.elem) return q + "float* " + name;  // untyped pointer: the CPU wrapper's float*
     Type base;
     std::vector<int64_t> dims;
     array_shape(*t.elem, base, dims);
-    if (dims.empty()) return c_scalar(base) + "* " + name;
+    if (dims.empty()) return q + c_scalar(base) + "* " + name;
     std::string d;
     for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
-    return c_scalar(base) + " (*" + name + ")" + d;
+    return q + c_scalar(base) + " (*" + name + ")" + d;
   }
   return c_scalar(t) + " " + name;
 }
@@ -677,14 +687,15 @@ std::string c_decl(const Type& t, const std::string& name) {
 // element with the stores of another.
 std::string c_decl_buffer(const Type& t, const std::string& name) {
   if (t.k != TK::Ptr) return c_decl(t, name);
-  if (!t.elem) return "float* __restrict__ " + name;
+  const std::string q = c_space(t.addr);
+  if (!t.elem) return q + "float* __restrict__ " + name;
   Type base;
   std::vector<int64_t> dims;
   array_shape(*t.elem, base, dims);
-  if (dims.empty()) return c_scalar(base) + "* __restrict__ " + name;
+  if (dims.empty()) return q + c_scalar(base) + "* __restrict__ " + name;
   std::string d;
   for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
-  return c_scalar(base) + " (* __restrict__ " + name + ")" + d;
+  return q + c_scalar(base) + " (* __restrict__ " + name + ")" + d;
 }
 
 std::string ident(const std::string& name) {
@@ -736,19 +747,41 @@ struct CoopFold {
   std::string next;    // the back-edge value
   std::string cond;    // max: the compare that selects the new value
 };
+// A load of a read-only buffer at [inv + iv] in a spread loop, kept per lane:
+// the first loop (in block order) with the key (buffer, inv) stores what it
+// loads in the lane's slot; later loops take the slot when the key's inv and
+// the range of the loop that filled it match, and load otherwise.
+struct CoopCacheUse {
+  int cache = -1;
+  bool fill = false;
+};
+struct CoopCache {
+  std::string buf, inv;   // inv "" for an index of iv alone
+  int64_t slots = 0;
+  Type ty;                // the loaded value's type
+};
 struct CoopLoop {
   std::string header, body, exit;
   std::string iv;
   int64_t start = 0, bound = 0, step = 1;
   std::vector<CoopFold> folds;
+  // step 1 and at most kCoopMaxSlots iterations a lane: lane l runs iteration
+  // k W + l of slot k (k a compile-time index once unrolled)
+  int64_t slots = 0;
+  std::map<std::string, CoopCacheUse> cached;   // load result -> its cache
+  // a workgroup barrier after the loop: unless it stores only into per-lane
+  // slices and reads only those and memory the function never writes
+  bool barrier = true;
 };
 struct CoopPlan {
   bool on = false;
   std::map<std::string, CoopLoop> loops;   // by header block
   std::set<std::string> bodies;            // body blocks emitted inside their loop
   std::set<std::string> private_allocas;   // tiles split over the lanes (per-lane slices)
+  std::vector<CoopCache> caches;
   std::string why;                         // why the function stays one program per lane
 };
+constexpr int64_t kCoopMaxSlots = 16;
 
 bool const_int(const Operand& o, int64_t& v) {
   if (o.is_value || o.ck != Operand::kInt) return false;
@@ -989,11 +1022,76 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     plan.why = "no loop of at least " + std::to_string(kCoopMinTrip) + " iterations that lanes can split";
     return plan;
   }
-  // A tile that is only touched inside spread loops starting at 0 with step 1,
-  // at [.., iv] (last index the loop counter), is touched at element e only by
-  // lane e % W (iteration e runs on that lane in every such loop): each lane
-  // keeps its slice [.., e / W] in registers instead of the workgroup keeping
-  // the tile in LDS.
+  // Step-1 loops of at most kCoopMaxSlots iterations a lane take the slot
+  // form: iteration e runs on lane e % W whatever the loop's start, in slot
+  // e / W.
+  for (auto& kv : plan.loops) {
+    CoopLoop& L = kv.second;
+    if (L.step == 1 && L.bound > 0 && (L.bound + kCoopThreads - 1) / kCoopThreads <= kCoopMaxSlots)
+      L.slots = (L.bound + kCoopThreads - 1) / kCoopThreads;
+  }
+  // Loads of a buffer the function never writes, at [inv + iv] with inv
+  // defined outside the loop, in slot-form loops: the first such loop in
+  // block order fills a per-lane cache, later ones read it.
+  {
+    std::set<std::string> written;
+    for (const Block& b : fn.blocks)
+      for (const Inst& in : b.insts) {
+        if ((in.op == "store" || in.op == "atomic" || (in.op == "intr" && in.sub == "vstore")) &&
+            in.args[0].is_value)
+          written.insert(root(in.args[0].name));
+        if (in.op == "memcpy" && in.args[0].is_value) written.insert(root(in.args[0].name));
+      }
+    std::map<std::pair<std::string, std::string>, int> key_cache;
+    for (const Block& hb : fn.blocks) {
+      auto lp = plan.loops.find(hb.name);
+      if (lp == plan.loops.end() || lp->second.slots == 0) continue;
+      CoopLoop& L = lp->second;
+      const Block* body = block(L.body);
+      for (const Inst& in : body->insts) {
+        if (in.op != "load" || !in.args[0].is_value || in.result.empty()) continue;
+        auto gi = def_inst.find(in.args[0].name);
+        if (gi == def_inst.end() || def_block[in.args[0].name] != body->name) continue;
+        const Inst& g = *gi->second;
+        if (g.op != "gep" || g.args.size() != 2 || !g.args[0].is_value || !g.args[1].is_value) continue;
+        const std::string buf = g.args[0].name;
+        if (def_inst.count(buf) || written.count(buf)) continue;   // a parameter, never written
+        std::string inv;
+        const std::string idx = g.args[1].name;
+        if (idx != L.iv) {
+          auto ai = def_inst.find(idx);
+          if (ai == def_inst.end() || def_block[idx] != body->name || ai->second->op != "bin" ||
+              ai->second->sub != "add")
+            continue;
+          const auto& aa = ai->second->args;
+          const Operand* other = nullptr;
+          if (aa[0].is_value && aa[0].name == L.iv) other = &aa[1];
+          else if (aa[1].is_value && aa[1].name == L.iv) other = &aa[0];
+          if (!other || !other->is_value) continue;
+          auto od = def_block.find(other->name);
+          if (od == def_block.end() || od->second == body->name || od->second == L.header) continue;
+          inv = other->name;
+        }
+        const auto key = std::make_pair(buf, inv);
+        auto kc = key_cache.find(key);
+        if (kc == key_cache.end()) {
+          const int c = (int)plan.caches.size();
+          auto ti = types.find(in.result);
+          if (ti == types.end()) continue;
+          plan.caches.push_back(CoopCache{buf, inv, L.slots, ti->second});
+          key_cache[key] = c;
+          L.cached[in.result] = CoopCacheUse{c, true};
+        } else if (!L.cached.count(in.result)) {
+          L.cached[in.result] = CoopCacheUse{kc->second, false};
+        }
+      }
+    }
+  }
+  // A tile that is only touched inside step-1 spread loops (in the slot form,
+  // or starting at 0) at [.., iv] (last index the loop counter) is touched at
+  // element e only by lane e % W (iteration e runs on that lane in every such
+  // loop): each lane keeps its slice [.., e / W] in registers instead of the
+  // workgroup keeping the tile in LDS.
   {
     std::map<std::string, std::string> body_of_header;
     for (auto& kv : plan.loops) body_of_header[kv.second.body] = kv.first;
@@ -1009,7 +1107,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
               if (!x.args[k].is_value || x.args[k].name != in.result) continue;
               // only as the base of a gep in a spread loop with start 0, step 1,
               // last index the loop counter
-              if (!(x.op == "gep" && k == 0 && L && L->start == 0 && L->step == 1 &&
+              if (!(x.op == "gep" && k == 0 && L && L->step == 1 && (L->slots > 0 || L->start == 0) &&
                     x.args.back().is_value && x.args.back().name == L->iv && x.args.size() >= 3))
                 priv = false;
             }
@@ -1035,6 +1133,42 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     plan.loops.clear();
     plan.bodies.clear();
     return plan;
+  }
+  // A spread loop is followed by a workgroup barrier when another lane's later
+  // access may conflict with one of its accesses: a store outside the per-lane
+  // slices, or a read of memory the function writes anywhere (outside the
+  // slices).  Neither: what follows touches only memory nobody writes and the
+  // lane's own slice elements, ordered by the lane's program order.
+  {
+    std::set<std::string> written;
+    for (const Block& b : fn.blocks)
+      for (const Inst& in : b.insts) {
+        if ((in.op == "store" || in.op == "atomic" || in.op == "memcpy" ||
+             (in.op == "intr" && in.sub == "vstore")) && in.args[0].is_value)
+          written.insert(root(in.args[0].name));
+      }
+    for (auto& kv : plan.loops) {
+      CoopLoop& L = kv.second;
+      bool need = false;
+      for (const Inst& in : block(L.body)->insts) {
+        const bool st = in.op == "store" || in.op == "atomic" || in.op == "memcpy" ||
+                        (in.op == "intr" && in.sub == "vstore");
+        const bool ld = in.op == "load" || (in.op == "intr" && in.sub == "vload");
+        if (st) {
+          if (!in.args[0].is_value || !plan.private_allocas.count(root(in.args[0].name))) need = true;
+        }
+        const Operand* src = ld ? &in.args[0] : in.op == "memcpy" ? &in.args[1] : nullptr;
+        if (src) {
+          if (!src->is_value) {
+            need = true;
+          } else {
+            const std::string r = root(src->name);
+            if (!plan.private_allocas.count(r) && written.count(r)) need = true;
+          }
+        }
+      }
+      L.barrier = need;
+    }
   }
   // an atomic outside the spread loops runs once (lane 0): its result must be unused
   for (const Block& b : fn.blocks)
@@ -1076,6 +1210,7 @@ struct Emitter {
   const std::map<std::string, Type>& types;
   const CoopPlan& coop;
   std::ostringstream o;
+  const CoopLoop* cur = nullptr;   // the slot-form spread loop being emitted
 
   std::string opnd(const Operand& x) {
     if (x.is_value) return ident(x.name);
@@ -1116,13 +1251,28 @@ struct Emitter {
       const bool slice = coop.on && a[0].is_value && coop.private_allocas.count(a[0].name);
       o << "  " << r << " = &(" << opnd(a[0]);
       for (size_t k = 1; k < a.size(); ++k) {
-        if (slice && k + 1 == a.size())
+        if (slice && k + 1 == a.size() && cur && a[k].is_value && a[k].name == cur->iv)
+          o << "[coop_k]";   // the slot of this iteration
+        else if (slice && k + 1 == a.size())
           o << "[(" << opnd(a[k]) << ") / " << kCoopThreads << "LL]";
         else
           o << "[" << opnd(a[k]) << "]";
       }
       o << ");\n";
     } else if (in.op == "load") {
+      auto cu = cur ? cur->cached.find(in.result) : std::map<std::string, CoopCacheUse>::const_iterator();
+      if (cur && cu != cur->cached.end()) {
+        const std::string c = std::to_string(cu->second.cache);
+        if (cu->second.fill) {
+          o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
+          o << "  coop_cache" << c << "[coop_k] = " << r << ";\n";
+        } else {
+          o << "  if (coop_ok" << c << " && coop_it >= coop_lo" << c << " && coop_it < coop_hi" << c
+            << ") " << r << " = coop_cache" << c << "[coop_k]; else " << r << " = *(" << opnd(a[0])
+            << ");\n";
+        }
+        return;
+      }
       o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
     } else if (in.op == "store") {
       o << "  *(" << opnd(a[0]) << ") = " << opnd(a[1]) << ";\n";
@@ -1141,6 +1291,9 @@ struct Emitter {
     } else if (in.op == "cmp") {
       o << "  " << r << " = " << opnd(a[0]) << " " << cmp_sym(in.sub) << " " << opnd(a[1])
         << ";\n";
+    } else if (in.op == "cast" && in.ty.k == TK::Ptr) {
+      // a pointer bitcast may name another address space: convert explicitly
+      o << "  " << r << " = (" << c_decl(in.ty, "") << ")(" << opnd(a[0]) << ");\n";
     } else if (in.op == "cast") {
       o << "  " << r << " = " << opnd(a[0]) << ";\n";
     } else if (in.op == "select") {
@@ -1219,15 +1372,42 @@ struct Emitter {
         o << "    float coop_p" << ks << " = -__builtin_inff(); long long coop_i" << ks
           << " = LLONG_MAX;\n";
     }
-    // unrolled, so a lane has several iterations' loads in flight
-    o << "#pragma unroll 8\n";
-    o << "    for (long long coop_it = coop_start + (long long)threadIdx.x * " << st
-      << "LL; coop_it < " << bd << "LL; coop_it += " << kCoopThreads << "LL * " << st << "LL) {\n";
+    if (L.slots > 0) {
+      // slot form: iteration k W + l on lane l, fully unrolled (compile-time
+      // slots for the per-lane tiles and caches)
+      std::set<int> fills, uses;
+      for (auto& cu : L.cached) (cu.second.fill ? fills : uses).insert(cu.second.cache);
+      for (int c : fills) {
+        const CoopCache& cc = coop.caches[c];
+        const std::string cs = std::to_string(c);
+        o << "    coop_has" << cs << " = true; coop_tag" << cs << " = "
+          << (cc.inv.empty() ? std::string("0") : "(long long)" + ident(cc.inv)) << "; coop_lo" << cs
+          << " = coop_start; coop_hi" << cs << " = " << bd << "LL;\n";
+      }
+      for (int c : uses) {
+        const CoopCache& cc = coop.caches[c];
+        const std::string cs = std::to_string(c);
+        o << "    const bool coop_ok" << cs << " = coop_has" << cs << " && coop_tag" << cs << " == "
+          << (cc.inv.empty() ? std::string("0") : "(long long)" + ident(cc.inv)) << ";\n";
+      }
+      o << "#pragma unroll\n";
+      o << "    for (int coop_k = 0; coop_k < " << L.slots << "; ++coop_k) {\n";
+      o << "    const long long coop_it = (long long)coop_k * " << kCoopThreads
+        << "LL + (long long)threadIdx.x;\n";
+      o << "    if (coop_it < coop_start || coop_it >= " << bd << "LL) continue;\n";
+    } else {
+      // unrolled, so a lane has several iterations' loads in flight
+      o << "#pragma unroll 8\n";
+      o << "    for (long long coop_it = coop_start + (long long)threadIdx.x * " << st
+        << "LL; coop_it < " << bd << "LL; coop_it += " << kCoopThreads << "LL * " << st << "LL) {\n";
+    }
     o << "    " << iv << " = coop_it;\n";
     for (size_t k = 0; k < L.folds.size(); ++k)
       if (L.folds[k].kind != 0)
         o << "    " << ident(L.folds[k].param) << " = coop_p" << k << ";\n";
+    cur = L.slots > 0 ? &L : nullptr;
     for (const Inst& in : body->insts) inst(in);
+    cur = nullptr;
     for (size_t k = 0; k < L.folds.size(); ++k) {
       const CoopFold& f = L.folds[k];
       if (f.kind == 2) o << "    if (" << ident(f.cond) << ") coop_i" << k << " = coop_it;\n";
@@ -1241,10 +1421,10 @@ struct Emitter {
         o << "    " << c << " = coop_init" << ks << ";\n";
       } else if (f.kind == 1) {
         o << "    " << c << " = coop_init" << ks << " + coop_wg_sum(coop_p" << ks
-          << ", coop_red_v);\n";
+          << ", coop_red_v, coop_rb);\n";
       } else {
         o << "    coop_wg_first_max(coop_p" << ks << ", coop_i" << ks
-          << ", coop_red_v, coop_red_i);\n";
+          << ", coop_red_v, coop_red_i, coop_rb);\n";
         o << "    " << c << " = coop_p" << ks << " > coop_init" << ks << " ? coop_p" << ks
           << " : coop_init" << ks << ";\n";
       }
@@ -1252,7 +1432,7 @@ struct Emitter {
     o << "    " << iv << " = " << bd << "LL > coop_start ? coop_start + ((" << bd
       << "LL - coop_start + " << st << "LL - 1) / " << st << "LL) * " << st
       << "LL : coop_start;\n  }\n";
-    o << "  __syncthreads();\n";
+    if (L.barrier) o << "  __syncthreads();\n";
     jump(h.term.f, h.term.fargs);
   }
 
@@ -1302,7 +1482,16 @@ struct Emitter {
         }
       }
     }
-    if (coop.on) o << "  __shared__ float coop_red_v[32];\n  __shared__ long long coop_red_i[32];\n";
+    if (coop.on)
+      o << "  __shared__ float coop_red_v[2 * COOP_WAVES];\n"
+           "  __shared__ long long coop_red_i[2 * COOP_WAVES];\n"
+           "  int coop_rb = 0;\n";
+    for (size_t c = 0; c < coop.caches.size(); ++c) {
+      const std::string cs = std::to_string(c);
+      o << "  " << c_scalar(coop.caches[c].ty) << " coop_cache" << cs << "[" << coop.caches[c].slots
+        << "];\n  bool coop_has" << cs << " = false;\n  long long coop_tag" << cs << " = 0, coop_lo"
+        << cs << " = 0, coop_hi" << cs << " = 0;\n";
+    }
     for (const Block& b : fn.blocks) {
       if (coop.bodies.count(b.name)) continue;  // emitted inside its spread loop
       o << "L_" << ident(b.name) << ":;\n";
@@ -1405,26 +1594,63 @@ struct Emitter {
     o << "__device__ static inline float llir_vec_reduce_add(llir_float4 v) {\n"
          "  return v.v[0] + v.v[1] + v.v[2] + v.v[3];\n}\n\n";
     if (coop.on) {
-      // workgroup folds of the lanes' partials; every lane returns the result
+      // Workgroup folds of the lanes' partials; every lane returns the result.
+      // Within a wave: DPP steps lane ^ 1, lane ^ 2 (quad permutes), then the
+      // half-row and row mirrors, after which every lane holds its 16-lane
+      // row's fold; the four rows are combined from lanes 0, 16, 32, 48.  Across
+      // the waves: lane 0 of each wave writes its fold to LDS, one barrier, and
+      // every lane combines the waves' values in wave order.  The exchange
+      // alternates between two halves of the LDS arrays (`rb`, the same
+      // sequence on every lane): a fold writes the half the fold before last
+      // read, which every wave finished reading before it passed the last
+      // fold's barrier, so no barrier is needed before the write.
       o << "#ifndef LLONG_MAX\n#define LLONG_MAX 9223372036854775807LL\n#endif\n"
-           "__device__ static float coop_wg_sum(float v, float* red) {\n"
-           "  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);\n"
+        << "#define COOP_WAVES " << kCoopThreads / 64 << "\n"
+        << "template <int C> __device__ static inline float coop_dpp_f(float v) {\n"
+           "  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xF, 0xF, false));\n}\n"
+           "template <int C> __device__ static inline long long coop_dpp_i(long long v) {\n"
+           "  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)v, C, 0xF, 0xF, false);\n"
+           "  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)((unsigned long long)v >> 32), C, 0xF, 0xF, false);\n"
+           "  return (long long)(((unsigned long long)hi << 32) | lo);\n}\n"
+           "__device__ static inline float coop_lane_f(float v, int l) {\n"
+           "  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));\n}\n"
+           "__device__ static inline long long coop_lane_i(long long v, int l) {\n"
+           "  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);\n"
+           "  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)((unsigned long long)v >> 32), l);\n"
+           "  return (long long)(((unsigned long long)hi << 32) | lo);\n}\n"
+           "__device__ static float coop_wg_sum(float v, float* red, int& rb) {\n"
+           "  v += coop_dpp_f<0xB1>(v);\n"
+           "  v += coop_dpp_f<0x4E>(v);\n"
+           "  v += coop_dpp_f<0x141>(v);\n"
+           "  v += coop_dpp_f<0x140>(v);\n"
+           "  v = ((coop_lane_f(v, 0) + coop_lane_f(v, 16)) + coop_lane_f(v, 32)) + coop_lane_f(v, 48);\n"
+           "  float* r = red + rb * COOP_WAVES;\n"
+           "  rb ^= 1;\n"
+           "  if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;\n"
            "  __syncthreads();\n"
-           "  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;\n"
-           "  __syncthreads();\n"
-           "  float s = red[0];\n"
-           "  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) s += red[w];\n"
+           "  float s = r[0];\n"
+           "#pragma unroll\n"
+           "  for (int w = 1; w < COOP_WAVES; ++w) s += r[w];\n"
            "  return s;\n}\n"
            "__device__ static void coop_merge(float& v, long long& i, float ov, long long oi) {\n"
            "  const bool take = ov > v || (ov == v && oi < i);\n"
            "  v = take ? ov : v; i = take ? oi : i;\n}\n"
-           "__device__ static void coop_wg_first_max(float& v, long long& i, float* rv, long long* ri) {\n"
-           "  for (int m = 1; m < 64; m <<= 1) coop_merge(v, i, __shfl_xor(v, m, 64), __shfl_xor(i, m, 64));\n"
+           "__device__ static void coop_wg_first_max(float& v, long long& i, float* rv, long long* ri, int& rb) {\n"
+           "  coop_merge(v, i, coop_dpp_f<0xB1>(v), coop_dpp_i<0xB1>(i));\n"
+           "  coop_merge(v, i, coop_dpp_f<0x4E>(v), coop_dpp_i<0x4E>(i));\n"
+           "  coop_merge(v, i, coop_dpp_f<0x141>(v), coop_dpp_i<0x141>(i));\n"
+           "  coop_merge(v, i, coop_dpp_f<0x140>(v), coop_dpp_i<0x140>(i));\n"
+           "  float wv = coop_lane_f(v, 0);\n"
+           "  long long wi = coop_lane_i(i, 0);\n"
+           "  for (int l = 16; l < 64; l += 16) coop_merge(wv, wi, coop_lane_f(v, l), coop_lane_i(i, l));\n"
+           "  float* r = rv + rb * COOP_WAVES;\n"
+           "  long long* q = ri + rb * COOP_WAVES;\n"
+           "  rb ^= 1;\n"
+           "  if ((threadIdx.x & 63) == 0) { r[threadIdx.x >> 6] = wv; q[threadIdx.x >> 6] = wi; }\n"
            "  __syncthreads();\n"
-           "  if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = v; ri[threadIdx.x >> 6] = i; }\n"
-           "  __syncthreads();\n"
-           "  v = rv[0]; i = ri[0];\n"
-           "  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) coop_merge(v, i, rv[w], ri[w]);\n}\n\n";
+           "  v = r[0]; i = q[0];\n"
+           "#pragma unroll\n"
+           "  for (int w = 1; w < COOP_WAVES; ++w) coop_merge(v, i, r[w], q[w]);\n}\n\n";
     }
     body();
     wrapper(plan_out, rows, cols);

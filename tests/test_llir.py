@@ -180,20 +180,46 @@ def test_long_loops_spread_over_the_workgroup():
     src = hip.llir_to_hip(softmax_llir(4, 8192), (1, 4, 8192))
     assert "__launch_bounds__(1024)" in src and "sile_pid = (long long)blockIdx.x;" in src
     # the row loop (4 iterations, loops inside) stays on every lane; the max,
-    # exp + sum and divide loops are spread
-    assert src.count("for (long long coop_it = coop_start + (long long)threadIdx.x") == 3
-    assert src.count("#pragma unroll 8") == 3
+    # exp + sum and divide loops are spread, 8 iterations a lane: the slot
+    # form (iteration k W + l on lane l, fully unrolled)
+    assert src.count("for (int coop_k = 0; coop_k < 8; ++coop_k) {") == 3
+    assert src.count("const long long coop_it = (long long)coop_k * 1024LL + (long long)threadIdx.x;") == 3
     assert "coop_wg_first_max(coop_p0, coop_i0" in src        # the max fold, from x0
     assert "v_sum = coop_init1 + coop_wg_sum(coop_p1" in src or \
            "v_sum = coop_init0 + coop_wg_sum(coop_p0" in src  # the sum of exp
     # the tile is only touched at [r, e] by the spread loops: per-lane slices
     assert "float v_tile_storage[4][8];" in src and "__shared__ float v_tile" not in src
-    assert "&(v_tile[(0LL)][v_r][(v_e) / 1024LL])" in src
-    assert src.count("__syncthreads();\n  {\n") + src.count("__syncthreads();\n  goto") >= 3
+    assert "&(v_tile[(0LL)][v_r][coop_k])" in src
+    # x is never written: the max loop keeps each lane's x values, the exp
+    # loop takes them (its iteration 0, which the max loop starting at 1 did
+    # not run, loads)
+    assert "coop_cache0[coop_k] = v_xv;" in src
+    assert ("if (coop_ok0 && coop_it >= coop_lo0 && coop_it < coop_hi0) v_xev = coop_cache0[coop_k]; "
+            "else v_xev = *(v_xep);") in src
+    assert "coop_tag0 = (long long)v_xrow;" in src and "coop_tag0 == (long long)v_xrow;" in src
+    # past 16 iterations a lane: the strided form, tiles sliced by e / W, no cache
+    wide = hip.llir_to_hip(softmax_llir(1, 32768), (1, 1, 32768))
+    assert wide.count("for (long long coop_it = coop_start + (long long)threadIdx.x") == 3
+    assert wide.count("#pragma unroll 8") == 3 and "coop_cache" not in wide
+    assert "&(v_tile[(0LL)][v_r][(v_e) / 1024LL])" in wide
+    # a barrier after a spread loop only where another lane's later access may
+    # conflict: the divide loop stores y; the max loop reads x (never written)
+    # and the exp loop writes the lanes' own slices, so neither needs one
+    body = src[src.index("L_v_bb0:"):]
+    assert body.count("__syncthreads();") == 1 and "__syncthreads();\n  goto L_v_sm_row_latch;" in body
+    # one barrier a workgroup fold (its LDS exchange alternates halves)
+    assert src.count("__syncthreads();") == 3 and "int coop_rb = 0;" in src
     pr = hip.llir_to_hip(parallel_reduce_llir(4096), None)
     assert "coop_wg_sum" in pr and "if (threadIdx.x == 0) atomicAdd(v_o, v_acc);" in pr
+    # the reduce loop only reads x: the fold's own barrier, none after the loop
+    assert pr[pr.index("L_v_bb0:"):].count("__syncthreads();") == 0
     va = hip.llir_to_hip(vec_add_llir(4096), (2, 1, 4096))
     assert "__launch_bounds__(1024)" in va
+    # the add loop stores c: a barrier after it
+    assert va[va.index("L_v_bb0:"):].count("__syncthreads();") == 1
+    # buffers keep the global address space (global, not flat, loads and stores)
+    assert "__attribute__((address_space(1))) float* __restrict__ v_a" in va
+    assert "= (__attribute__((address_space(1))) float* )buffers[0];" in va
     for t, plan in ((softmax_llir(4, 8192), (1, 4, 8192)), (parallel_reduce_llir(4096), None),
                     (vec_add_llir(4096), (2, 1, 4096))):
         image, _ = hip.llir_compile(t, plan)
