@@ -515,7 +515,7 @@ sm_exp_body:
   %xev = load f32, ptr addrspace(1) %xep
   %d = fsub %xev, %mx
   %ex = call f32 @llvm.exp.f32(f32 %d)
-  %tp = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 0, i64 %r, i64 %e
+  %tp = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 %r, i64 %e
   store f32 %ex, ptr addrspace(5) %tp
   %sum_next = fadd %sum, %ex
   %e_next = add %e, 1
@@ -525,7 +525,7 @@ sm_div_header:
   %qc = icmp slt %q, 8192
   br i1 %qc, label %sm_div_body, label %sm_row_latch
 sm_div_body:
-  %tq = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 0, i64 %r, i64 %q
+  %tq = getelementptr [4 x [8192 x f32]], ptr addrspace(5) %tile, i64 %r, i64 %q
   %tv = load f32, ptr addrspace(5) %tq
   %yv = fdiv %tv, %sum
   %yrow = mul %row, %ldy
@@ -543,13 +543,14 @@ sm_exit:
 """
 
 
-def bench_llir_softmax(name, steps, warmup):
+def bench_llir_softmax(name, steps, warmup, text=None):
     """softmax<BM=4, BN=8192> over f32 [8192, 8192] generated from LLIR
-    (LLIR_SOFTMAX_4x8192), one workgroup per program, through the synchronous
-    sile_hip_launch_llir (table upload, launch, wait per call), rated by the
-    routed softmax's algorithmic bytes (8 per element: read x, write y)."""
+    (LLIR_SOFTMAX_4x8192, or `text`), one workgroup per program, through the
+    synchronous sile_hip_launch_llir (table upload, launch, wait per call),
+    rated by the routed softmax's algorithmic bytes (8 per element: read x,
+    write y)."""
     rows = cols = 8192
-    kern = hip.LlirKernel(LLIR_SOFTMAX_4x8192, (1, 4, cols))
+    kern = hip.LlirKernel(text or LLIR_SOFTMAX_4x8192, (1, 4, cols))
     x = hip.DeviceBuffer.from_array(normal(3, (rows, cols), 2.0))
     y = hip.DeviceBuffer(rows * cols * 4)
     ptrs, shapes, grid = [x.ptr, y.ptr], [rows, cols, rows, cols], (rows // 4, 1, 1)
@@ -920,11 +921,13 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
                    "flash_attn_fwd_f16_s8192_d64": "sile_flash_attn",
                    "matvec_f32_8192": "sile_dsl_matvec", "matvec_f32_8192_bk8": "sile_dsl_matvec",
                    "llir_softmax_f32_8192": "sile_kernel_softmax",
+                   "llir_softmax_ref_shapes_f32_8192": "sile_kernel_softmax",
                    "tile_ir_softmax_f32_8192": "sile_softmax_rows"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
-EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "tile_ir_softmax_f32_8192",
+EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "llir_softmax_ref_shapes_f32_8192",
+         "tile_ir_softmax_f32_8192",
          "gemm_f32_exact_4096",
          "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
          # the mlp example's matvec program (BK 32; _bk8: the example's BK)
@@ -980,6 +983,12 @@ def main():
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
         elif name == "llir_softmax_f32_8192":
             results[name] = bench_llir_softmax(name, args.steps, args.warmup)
+        elif name == "llir_softmax_ref_shapes_f32_8192":
+            # the same program in the reference's loop shapes: a loop nest and
+            # a private tile per op (tests/llir_shapes.py)
+            from tests import llir_shapes
+            results[name] = bench_llir_softmax(name, args.steps, args.warmup,
+                                               llir_shapes.softmax(4, 8192))
         elif name == "tile_ir_softmax_f32_8192":
             results[name] = bench_tile_ir_softmax(name, args.steps, args.warmup)
         elif name == "reduce_rows_f32_8192":

@@ -352,12 +352,21 @@ struct Parser {
         c.type();  // i64
         in.args.push_back(c.operand());
       }
-      // result: pointer to the source element type indexed by all but the
-      // first index (C array indexing), in the base's address space
+      // result: the backends' C indexing `&base[i][j]...` of a pointer whose
+      // array pointee is decayed (crates/sile-backend/src/emit.rs:164-176,
+      // cpu/codegen.rs:601-664): the indices address the array's dimensions
+      // in order (a tile [R x [C x f32]] takes [row, col]); a scalar pointee
+      // takes one index, pointer arithmetic.  In the base's address space.
       Type pointee = in.aux;
-      for (size_t k = 2; k < in.args.size(); ++k) {
-        if (pointee.k != TK::Arr) perr(line, "gep indexes past the array levels: " + raw);
-        pointee = *pointee.elem;
+      const size_t nidx = in.args.size() - 1;
+      if (nidx == 0) perr(line, "gep without an index: " + raw);
+      if (pointee.k == TK::Arr) {
+        for (size_t k = 0; k < nidx; ++k) {
+          if (pointee.k != TK::Arr) perr(line, "gep indexes past the array levels: " + raw);
+          pointee = *pointee.elem;
+        }
+      } else if (nidx != 1) {
+        perr(line, "gep on a scalar pointee takes one index: " + raw);
       }
       in.ty = ptr_to(pointee, bt.addr);
     } else if (op == "load") {
@@ -664,7 +673,10 @@ void array_shape(const Type& t, Type& base, std::vector<int64_t>& dims) {
 // arrays, whose space the compiler knows).
 std::string c_space(int addr) { return addr == 1 ? "__attribute__((address_space(1))) " : ""; }
 
-// declaration of `name` with type t
+// declaration of `name` with type t.  A pointer to an array is declared
+// decayed, as a pointer to the array's first element (the backends' C form,
+// crates/sile-backend/src/cpu/codegen.rs:625-664): `[R x [C x f32]]*` is
+// `float (*)[C]`, `[C x f32]*` is `float*`.
 std::string c_decl(const Type& t, const std::string& name) {
   if (t.k == TK::Ptr) {
     const std::string q = c_space(t.addr);
@@ -672,9 +684,9 @@ std::string c_decl(const Type& t, const std::string& name) {
     Type base;
     std::vector<int64_t> dims;
     array_shape(*t.elem, base, dims);
-    if (dims.empty()) return q + c_scalar(base) + "* " + name;
+    if (dims.size() <= 1) return q + c_scalar(base) + "* " + name;
     std::string d;
-    for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
+    for (size_t k = 1; k < dims.size(); ++k) d += "[" + std::to_string(dims[k]) + "]";
     return q + c_scalar(base) + " (*" + name + ")" + d;
   }
   return c_scalar(t) + " " + name;
@@ -692,9 +704,9 @@ std::string c_decl_buffer(const Type& t, const std::string& name) {
   Type base;
   std::vector<int64_t> dims;
   array_shape(*t.elem, base, dims);
-  if (dims.empty()) return q + c_scalar(base) + "* __restrict__ " + name;
+  if (dims.size() <= 1) return q + c_scalar(base) + "* __restrict__ " + name;
   std::string d;
-  for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
+  for (size_t k = 1; k < dims.size(); ++k) d += "[" + std::to_string(dims[k]) + "]";
   return q + c_scalar(base) + " (* __restrict__ " + name + ")" + d;
 }
 
@@ -772,12 +784,19 @@ struct CoopLoop {
   // a workgroup barrier after the loop: unless it stores only into per-lane
   // slices and reads only those and memory the function never writes
   bool barrier = true;
+  // a workgroup barrier before the loop: it writes LDS copies that code
+  // outside the spread loops reads, which every lane must have done first
+  bool pre_barrier = false;
 };
 struct CoopPlan {
   bool on = false;
   std::map<std::string, CoopLoop> loops;   // by header block
   std::set<std::string> bodies;            // body blocks emitted inside their loop
   std::set<std::string> private_allocas;   // tiles split over the lanes (per-lane slices)
+  // per-lane tiles whose elements at a constant last index c are read outside
+  // the spread loops: an LDS copy of those elements (the tile minus its last
+  // dimension) for each such c, written by the lane that stores the element
+  std::map<std::string, std::set<int64_t>> shadows;
   std::vector<CoopCache> caches;
   std::string why;                         // why the function stays one program per lane
 };
@@ -834,13 +853,18 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
   for (const Block& h : fn.blocks) {
     if (h.params.empty() || h.insts.size() != 1 || h.term.kind != "condbr") continue;
     const Inst& cmp = h.insts[0];
-    if (cmp.op != "cmp" || cmp.sub != "slt" || !cmp.args[0].is_value ||
-        cmp.args[0].name != h.params[0].first || !h.term.cond.is_value ||
+    if (cmp.op != "cmp" || cmp.sub != "slt" || !cmp.args[0].is_value || !h.term.cond.is_value ||
         h.term.cond.name != cmp.result)
       continue;
+    // the counter: the parameter the header compares (the reference's 2-D
+    // loops carry the row before the column, tile_loops/grid.rs)
+    size_t ivk = h.params.size();
+    for (size_t k = 0; k < h.params.size(); ++k)
+      if (h.params[k].first == cmp.args[0].name) ivk = k;
+    if (ivk == h.params.size()) continue;
     CoopLoop L;
     L.header = h.name;
-    L.iv = h.params[0].first;
+    L.iv = h.params[ivk].first;
     if (!const_int(cmp.args[1], L.bound)) continue;
     const Block* body = block(h.term.t);
     if (!body || !body->params.empty() || !h.term.targs.empty() || body->term.kind != "br" ||
@@ -849,7 +873,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     L.body = body->name;
     L.exit = h.term.f;
     // iv' = iv + step
-    const Operand& nx = body->term.targs[0];
+    const Operand& nx = body->term.targs[ivk];
     auto ni = nx.is_value ? def_inst.find(nx.name) : def_inst.end();
     if (ni == def_inst.end() || def_block[nx.name] != body->name || ni->second->op != "bin" ||
         ni->second->sub != "add")
@@ -867,7 +891,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
       auto edge = [&](const std::string& t, const std::vector<Operand>& args) {
         if (t != h.name) return;
         ++entries;
-        if (args.empty() || !const_int(args[0], L.start)) start_ok = false;
+        if (args.size() != h.params.size() || !const_int(args[ivk], L.start)) start_ok = false;
       };
       if (b.term.kind == "br") edge(b.term.t, b.term.targs);
       if (b.term.kind == "condbr") {
@@ -890,8 +914,14 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     // loop-invariant: defined outside the loop, or computed in the body by a
     // pure operation of invariant operands (a row offset computed per iteration)
     std::map<std::string, bool> inv_memo;
+    std::set<std::string> passthru;   // header parameters the back edge passes unchanged
+    for (size_t k = 0; k < h.params.size(); ++k) {
+      const Operand& back = body->term.targs[k];
+      if (k != ivk && back.is_value && back.name == h.params[k].first) passthru.insert(back.name);
+    }
     std::function<bool(const Operand&)> invariant = [&](const Operand& o) -> bool {
       if (!o.is_value) return true;
+      if (passthru.count(o.name)) return true;
       auto it = def_block.find(o.name);
       const std::string db = it == def_block.end() ? "" : it->second;
       if (db == h.name) return false;
@@ -909,15 +939,15 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
       auto it = def_block.find(v);
       return it != def_block.end() && it->second == body->name;
     };
-    // carried values: folds
-    for (size_t k = 1; k < h.params.size() && ok; ++k) {
+    // carried values: unchanged (loop-invariant, any use) or folds
+    for (size_t k = 0; k < h.params.size() && ok; ++k) {
+      if (k == ivk) continue;
       CoopFold f;
       f.param = h.params[k].first;
       const Operand& back = body->term.targs[k];
       f.next = back.is_value ? back.name : "";
       if (back.is_value && back.name == f.param) {
         f.kind = 0;
-        if (uses[f.param] != 1) ok = false;
       } else if (!back.is_value || !in_body(back.name) || uses[back.name] != 1) {
         ok = false;
       } else {
@@ -954,16 +984,18 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     if (!ok) continue;
     // body instructions and memory
     std::map<std::string, std::set<std::string>> stored;  // object -> store pointers / offsets
-    auto iter_index = [&](const Operand& o) {
-      // iv itself, or iv + invariant (either order)
+    // iv itself, or iv plus loop-invariant terms, added in any grouping (the
+    // reference's `tile_base + (row * cols + col)`, tile_memory.rs:232-275):
+    // a different address every iteration
+    std::function<bool(const Operand&)> iter_index = [&](const Operand& o) -> bool {
       if (!o.is_value) return false;
       if (o.name == L.iv) return true;
       auto it = def_inst.find(o.name);
       if (it == def_inst.end() || !in_body(o.name)) return false;
       const Inst& a = *it->second;
       if (a.op != "bin" || a.sub != "add") return false;
-      return (a.args[0].is_value && a.args[0].name == L.iv && invariant(a.args[1])) ||
-             (a.args[1].is_value && a.args[1].name == L.iv && invariant(a.args[0]));
+      return (iter_index(a.args[0]) && invariant(a.args[1])) ||
+             (iter_index(a.args[1]) && invariant(a.args[0]));
     };
     for (const Inst& in : body->insts) {
       if (in.op == "atomic" || in.op == "memcpy" || in.op == "call" || in.op == "alloca" ||
@@ -1099,17 +1131,50 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
       for (const Inst& in : b.insts) {
         if (in.op != "alloca") continue;
         bool priv = true;
+        Type abase;
+        std::vector<int64_t> adims;
+        array_shape(in.aux, abase, adims);
+        if (adims.empty()) priv = false;
+        std::set<int64_t> cols;   // constant last indices read outside the spread loops
+        // a value used only as the pointer of loads
+        auto only_loaded = [&](const std::string& v) {
+          for (const Block& u : fn.blocks) {
+            for (const Inst& y : u.insts)
+              for (size_t j = 0; j < y.args.size(); ++j)
+                if (y.args[j].is_value && y.args[j].name == v && !(y.op == "load" && j == 0))
+                  return false;
+            for (const Operand& a : u.term.targs)
+              if (a.is_value && a.name == v) return false;
+            for (const Operand& a : u.term.fargs)
+              if (a.is_value && a.name == v) return false;
+            if (u.term.cond.is_value && u.term.cond.name == v) return false;
+          }
+          return true;
+        };
         for (const Block& u : fn.blocks) {
           auto lp = body_of_header.find(u.name);
           const CoopLoop* L = lp == body_of_header.end() ? nullptr : &plan.loops[lp->second];
           for (const Inst& x : u.insts) {
             for (size_t k = 0; k < x.args.size(); ++k) {
               if (!x.args[k].is_value || x.args[k].name != in.result) continue;
-              // only as the base of a gep in a spread loop with start 0, step 1,
-              // last index the loop counter
-              if (!(x.op == "gep" && k == 0 && L && L->step == 1 && (L->slots > 0 || L->start == 0) &&
-                    x.args.back().is_value && x.args.back().name == L->iv && x.args.size() >= 3))
-                priv = false;
+              // as the base of a gep to an element (an index for each
+              // dimension) in a spread loop with start 0, step 1, last index
+              // the loop counter
+              if (x.op == "gep" && k == 0 && L && L->step == 1 && (L->slots > 0 || L->start == 0) &&
+                  x.args.back().is_value && x.args.back().name == L->iv &&
+                  x.args.size() == adims.size() + 1)
+                continue;
+              // outside the spread loops, a gep to an element at a constant
+              // last index that only loads use (the reference's reduce reads
+              // its first element, tile_compute/reduce.rs:325-335)
+              int64_t c = -1;
+              if (x.op == "gep" && k == 0 && !L && x.args.size() == adims.size() + 1 &&
+                  const_int(x.args.back(), c) && c >= 0 && c < adims.back() &&
+                  only_loaded(x.result)) {
+                cols.insert(c);
+                continue;
+              }
+              priv = false;
             }
           }
           for (const Operand& a : u.term.targs)
@@ -1119,6 +1184,12 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
         }
         if (priv) {
           plan.private_allocas.insert(in.result);
+          if (!cols.empty()) {
+            plan.shadows[in.result] = cols;
+            int64_t n = 4 * (int64_t)cols.size();
+            for (size_t k = 0; k + 1 < adims.size(); ++k) n *= adims[k];
+            alloca_bytes += n;   // the LDS copies
+          }
           Type base;
           std::vector<int64_t> dims;
           array_shape(in.aux, base, dims);
@@ -1155,7 +1226,12 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
                         (in.op == "intr" && in.sub == "vstore");
         const bool ld = in.op == "load" || (in.op == "intr" && in.sub == "vload");
         if (st) {
-          if (!in.args[0].is_value || !plan.private_allocas.count(root(in.args[0].name))) need = true;
+          if (!in.args[0].is_value || !plan.private_allocas.count(root(in.args[0].name))) {
+            need = true;
+          } else if (plan.shadows.count(root(in.args[0].name))) {
+            need = true;            // its LDS copies, read outside the loops
+            L.pre_barrier = true;
+          }
         }
         const Operand* src = ld ? &in.args[0] : in.op == "memcpy" ? &in.args[1] : nullptr;
         if (src) {
@@ -1211,6 +1287,22 @@ struct Emitter {
   const CoopPlan& coop;
   std::ostringstream o;
   const CoopLoop* cur = nullptr;   // the slot-form spread loop being emitted
+  const CoopLoop* in_loop = nullptr;   // the spread loop being emitted (any form)
+
+  const Inst* def_of(const std::string& v) const {
+    for (const Block& b : fn.blocks)
+      for (const Inst& in : b.insts)
+        if (in.result == v) return &in;
+    return nullptr;
+  }
+  // `A_sh<c>[i0]...[i(n-2)]`: the LDS copy of a shadowed tile's elements at
+  // last index c, indexed by a gep's other indices
+  std::string shadow_ref(const Inst& g, int64_t c) {
+    std::string r = ident(g.args[0].name) + "_sh" + std::to_string(c);
+    if (g.args.size() == 2) return r + "[0]";
+    for (size_t k = 1; k + 1 < g.args.size(); ++k) r += "[" + opnd(g.args[k]) + "]";
+    return r;
+  }
 
   std::string opnd(const Operand& x) {
     if (x.is_value) return ident(x.name);
@@ -1249,7 +1341,18 @@ struct Emitter {
       // a per-lane slice of a tile: element e of the last dimension is the
       // lane's e / W
       const bool slice = coop.on && a[0].is_value && coop.private_allocas.count(a[0].name);
-      o << "  " << r << " = &(" << opnd(a[0]);
+      if (slice && !in_loop) {
+        // outside the spread loops: the element's LDS copy
+        auto sh = coop.shadows.find(a[0].name);
+        int64_t c = -1;
+        if (sh == coop.shadows.end() || !const_int(a.back(), c) || !sh->second.count(c))
+          throw ParseError{"internal: per-lane tile %" + a[0].name + " addressed outside its loops"};
+        o << "  " << r << " = &(" << shadow_ref(in, c) << ");\n";
+        return;
+      }
+      // an element: its address; a sub-array: the sub-array, decayed
+      const bool sub = in.ty.elem && in.ty.elem->k == TK::Arr;
+      o << "  " << r << " = " << (sub ? "(" : "&(") << opnd(a[0]);
       for (size_t k = 1; k < a.size(); ++k) {
         if (slice && k + 1 == a.size() && cur && a[k].is_value && a[k].name == cur->iv)
           o << "[coop_k]";   // the slot of this iteration
@@ -1276,6 +1379,15 @@ struct Emitter {
       o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
     } else if (in.op == "store") {
       o << "  *(" << opnd(a[0]) << ") = " << opnd(a[1]) << ";\n";
+      // the lane storing a shadowed element also writes its LDS copy
+      const Inst* g = (coop.on && in_loop && a[0].is_value) ? def_of(a[0].name) : nullptr;
+      if (g && g->op == "gep" && g->args[0].is_value) {
+        auto sh = coop.shadows.find(g->args[0].name);
+        if (sh != coop.shadows.end())
+          for (int64_t c : sh->second)
+            o << "  if (coop_it == " << c << "LL) " << shadow_ref(*g, c) << " = " << opnd(a[1])
+              << ";\n";
+      }
     } else if (in.op == "atomic" && coop.on) {
       // outside the spread loops every lane runs the program's code: add once
       o << "  if (threadIdx.x == 0) atomicAdd(" << opnd(a[0]) << ", " << opnd(a[1]) << ");\n";
@@ -1362,10 +1474,12 @@ struct Emitter {
     for (const Block& b : fn.blocks)
       if (b.name == L.body) body = &b;
     const std::string iv = ident(L.iv), st = std::to_string(L.step), bd = std::to_string(L.bound);
+    if (L.pre_barrier) o << "  __syncthreads();\n";
     o << "  {\n    const long long coop_start = " << iv << ";\n";
     for (size_t k = 0; k < L.folds.size(); ++k) {
       const CoopFold& f = L.folds[k];
       const std::string c = ident(f.param), ks = std::to_string(k);
+      if (f.kind == 0) continue;  // unchanged by the loop
       o << "    const float coop_init" << ks << " = " << c << ";\n";
       if (f.kind == 1) o << "    float coop_p" << ks << " = -0.0f;\n";
       if (f.kind == 2)
@@ -1406,8 +1520,10 @@ struct Emitter {
       if (L.folds[k].kind != 0)
         o << "    " << ident(L.folds[k].param) << " = coop_p" << k << ";\n";
     cur = L.slots > 0 ? &L : nullptr;
+    in_loop = &L;
     for (const Inst& in : body->insts) inst(in);
     cur = nullptr;
+    in_loop = nullptr;
     for (size_t k = 0; k < L.folds.size(); ++k) {
       const CoopFold& f = L.folds[k];
       if (f.kind == 2) o << "    if (" << ident(f.cond) << ") coop_i" << k << " = coop_it;\n";
@@ -1418,7 +1534,7 @@ struct Emitter {
       const CoopFold& f = L.folds[k];
       const std::string c = ident(f.param), ks = std::to_string(k);
       if (f.kind == 0) {
-        o << "    " << c << " = coop_init" << ks << ";\n";
+        continue;
       } else if (f.kind == 1) {
         o << "    " << c << " = coop_init" << ks << " + coop_wg_sum(coop_p" << ks
           << ", coop_red_v, coop_rb);\n";
@@ -1468,14 +1584,23 @@ struct Emitter {
           }
           o << "  " << (coop.on && !priv ? "__shared__ " : "") << c_scalar(base) << " "
             << ident(in.result) << "_storage" << d << ";\n";
+          auto sh = priv ? coop.shadows.find(in.result) : coop.shadows.end();
+          if (sh != coop.shadows.end())
+            for (int64_t c : sh->second) {
+              std::string sd;
+              for (size_t k = 0; k + 1 < dims.size(); ++k) sd += "[" + std::to_string(dims[k]) + "]";
+              o << "  __shared__ " << c_scalar(base) << " " << ident(in.result) << "_sh" << c
+                << (sd.empty() ? "[1]" : sd) << ";\n";
+            }
+          // the pointer is the storage decayed to its first element
           if (dims.empty())
             o << "  " << c_scalar(base) << "* " << ident(in.result) << " = " << ident(in.result)
               << "_storage;\n";
           else if (priv)
             o << "  " << c_decl(ptr_to(slice_type(in.aux), in.ty.addr), ident(in.result))
-              << " = &" << ident(in.result) << "_storage;\n";
+              << " = " << ident(in.result) << "_storage;\n";
           else
-            o << "  " << c_decl(in.ty, ident(in.result)) << " = &" << ident(in.result)
+            o << "  " << c_decl(in.ty, ident(in.result)) << " = " << ident(in.result)
               << "_storage;\n";
         } else {
           o << "  " << c_decl(in.ty, ident(in.result)) << ";\n";
@@ -1679,6 +1804,61 @@ void verify(const Function& fn) {
   }
 }
 
+// A block entered by one edge only takes its arguments from that edge: its
+// parameters are replaced by the values the edge passes.  The reference's
+// loops pass the header's values on to the body block and the exit block
+// (crates/sile-tile-ir/src/passes/lowering/core/emit/tile_loops/*.rs,
+// tile_compute/reduce.rs), so after this the body of a loop uses the header's
+// values directly.  Safe for every use: the edge's source dominates the block
+// (it is its only way in), and a use of a block parameter lies in blocks the
+// block dominates, which control reaches from the source only through the
+// block.  The entry block and a block whose only edge is its own back edge
+// (unreachable) are left alone.
+void forward_block_args(Function& fn) {
+  for (bool changed = true; changed;) {
+    changed = false;
+    std::map<std::string, int> preds;
+    for (const Block& b : fn.blocks) {
+      if (b.term.kind == "br") ++preds[b.term.t];
+      if (b.term.kind == "condbr") {
+        ++preds[b.term.t];
+        ++preds[b.term.f];
+      }
+      if (b.term.kind == "switch") return;  // rejected by verify()
+    }
+    for (size_t bi = 1; bi < fn.blocks.size() && !changed; ++bi) {
+      Block& b = fn.blocks[bi];
+      if (b.params.empty() || preds[b.name] != 1) continue;
+      std::vector<Operand>* args = nullptr;
+      for (Block& src : fn.blocks) {
+        if (src.term.kind == "br" && src.term.t == b.name) args = &src.term.targs;
+        if (src.term.kind == "condbr" && src.term.t == b.name) args = &src.term.targs;
+        if (src.term.kind == "condbr" && src.term.f == b.name) args = &src.term.fargs;
+        if (args && &src == &b) args = nullptr;
+        if (args) break;
+      }
+      if (!args || args->size() != b.params.size()) continue;
+      std::map<std::string, Operand> sub;
+      for (size_t k = 0; k < b.params.size(); ++k) sub[b.params[k].first] = (*args)[k];
+      auto fix = [&](Operand& o) {
+        if (!o.is_value) return;
+        auto it = sub.find(o.name);
+        if (it != sub.end()) o = it->second;
+      };
+      args->clear();
+      b.params.clear();
+      for (Block& u : fn.blocks) {
+        for (Inst& in : u.insts)
+          for (Operand& a : in.args) fix(a);
+        fix(u.term.cond);
+        for (Operand& a : u.term.targs) fix(a);
+        for (Operand& a : u.term.fargs) fix(a);
+      }
+      changed = true;
+    }
+  }
+}
+
 // parse + emit; returns a status and fills `src` / the last error
 int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::string& src,
            std::string& name) {
@@ -1689,6 +1869,7 @@ int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::
     Parser p;
     p.parse(std::string(text));
     verify(p.fn);
+    forward_block_args(p.fn);
     const CoopPlan coop = plan_coop(p.fn, p.types);
     Emitter e{p.fn, p.types, coop, {}};
     src = e.emit(plan_out, rows, cols);

@@ -1,0 +1,318 @@
+"""LLIR in the loop shapes of the reference's Tile IR -> LLIR lowering, in its
+printed form (crates/sile-llvm-ir/src/print.rs), for tests of the generated
+code on those shapes.
+
+The shapes follow the reference's emitters, not this repository's
+hand-written fixtures:
+- a tile is a private alloca `[rows x [cols x f32]]`, addressed by
+  `getelementptr <tile type>, ptr addrspace(5) %t, i64 row, i64 col`
+  (core/emit/alloc.rs:8-32, insts/memory.rs:6-21);
+- a tile loop over rows x cols is `lower_nested_tile_loop`
+  (core/emit/tile_loops.rs:16-40): one column loop for rows == 1, one row loop
+  for cols == 1, else the 2-D nest of tile_loops/grid.rs:7-130 (row header,
+  column header carrying the row, body, row latch); every header passes its
+  values on to a body block with parameters of its own;
+- a reduction along the columns of more than 16 elements is a row loop whose
+  body reads the row's first element, then a reduce loop from index 1 with
+  the accumulator as a block parameter and an exit block receiving the final
+  value (tile_compute/reduce.rs:279-374, tile_loops/single_axis.rs:85-153);
+  the max combines with `fcmp ogt next, acc; select` (reduce.rs:10-30);
+- buffer elements are addressed `tile_origin + row * stride + col` from the
+  shape table (tile_memory.rs:150-318);
+- value names are a prefix and a counter, block names a prefix and a block
+  counter (core/block.rs:36-48, 101-122).
+
+Which fusions the reference's passes apply before lowering is not modelled:
+each tile op here is its own loop nest over its own tile.  The functions are
+test inputs (no reference output is reproduced byte for byte)."""
+
+
+class _Fn:
+    def __init__(self, name, params):
+        """params: (name, rank, shape_offset) of f32 buffers, in order."""
+        self.name = name
+        self.params = params
+        self.nv = 0
+        self.nb = 0
+        self.blocks = []          # [name, params, lines, term]
+        self.cur = self.new_block("entry", [])
+
+    def val(self, prefix="v"):
+        self.nv += 1
+        return f"%{prefix}{self.nv}"
+
+    def new_block(self, prefix, params):
+        name = f"{prefix}_{self.nb}"
+        self.nb += 1
+        ps = [(self.val(p), t) for p, t in params]
+        blk = [name, ps, [], None]
+        self.blocks.append(blk)
+        return blk
+
+    def emit(self, text, prefix="v"):
+        r = self.val(prefix)
+        self.cur[2].append(f"{r} = {text}")
+        return r
+
+    def stmt(self, text):
+        self.cur[2].append(text)
+
+    def term(self, text):
+        self.cur[3] = text
+
+    def switch(self, blk):
+        self.cur = blk
+
+    def text(self):
+        out = ["define void @%s(%s) {" % (self.name, ", ".join(
+            [f"ptr addrspace(1) %{n}" for n, _, _ in self.params] +
+            ["ptr addrspace(4) %__sile_shapes"]))]
+        for n, rank, off in self.params:
+            out.append(f"  ; sile.param %{n} [rank={rank}, shape_offset={off}, elem=f32]")
+        out.append("  ; sile.param %__sile_shapes [elem=i64]")
+        for name, ps, lines, term in self.blocks:
+            out.append(f"{name}:")
+            if ps:
+                out.append("  ; args(%s)" % ", ".join(f"{p}: {t}" for p, t in ps))
+            out += ["  " + x for x in lines]
+            out.append("  " + term)
+        out.append("}")
+        return "\n".join(out) + "\n"
+
+
+def _args(vals):
+    return ", ".join(str(v) for v in vals)
+
+
+def _tile_loop(f, prefix, rows, cols, body):
+    """lower_nested_tile_loop: body(row, col) appends the body's instructions."""
+    cont = None
+    if rows == 1 or cols == 1:
+        axis = "col" if rows == 1 else "row"
+        n = cols if rows == 1 else rows
+        header = f.new_block(f"{prefix}_{axis}_header", [(f"loop_{axis}", "i64")])
+        blk = f.new_block(f"{prefix}_body", [(f"loop_{axis}", "i64")])
+        cont = f.new_block(f"{prefix}_continue", [])
+        f.term(f"br label %{header[0]} ; args(0)")
+        f.switch(header)
+        i = header[1][0][0]
+        c = f.emit(f"icmp slt {i}, {n}")
+        f.term(f"br i1 {c}, label %{blk[0]}, label %{cont[0]} ; true_args({i})")
+        f.switch(blk)
+        bi = blk[1][0][0]
+        body(0, bi) if rows == 1 else body(bi, 0)
+        nx = f.emit(f"add {bi}, 1")
+        f.term(f"br label %{header[0]} ; args({nx})")
+        f.switch(cont)
+        return
+    rh = f.new_block(f"{prefix}_row_header", [("loop_row", "i64")])
+    ch = f.new_block(f"{prefix}_col_header", [("loop_row", "i64"), ("loop_col", "i64")])
+    blk = f.new_block(f"{prefix}_body", [("loop_row", "i64"), ("loop_col", "i64")])
+    latch = f.new_block(f"{prefix}_row_latch", [("loop_row", "i64")])
+    cont = f.new_block(f"{prefix}_continue", [])
+    f.term(f"br label %{rh[0]} ; args(0)")
+    f.switch(rh)
+    r = rh[1][0][0]
+    c = f.emit(f"icmp slt {r}, {rows}")
+    f.term(f"br i1 {c}, label %{ch[0]}, label %{cont[0]} ; true_args({r}, 0)")
+    f.switch(ch)
+    cr, cc = ch[1][0][0], ch[1][1][0]
+    c = f.emit(f"icmp slt {cc}, {cols}")
+    f.term(f"br i1 {c}, label %{blk[0]}, label %{latch[0]} ; true_args({cr}, {cc}) ; false_args({cr})")
+    f.switch(blk)
+    br, bc = blk[1][0][0], blk[1][1][0]
+    body(br, bc)
+    nx = f.emit(f"add {bc}, 1")
+    f.term(f"br label %{ch[0]} ; args({br}, {nx})")
+    f.switch(latch)
+    nr = f.emit(f"add {latch[1][0][0]}, 1")
+    f.term(f"br label %{rh[0]} ; args({nr})")
+    f.switch(cont)
+
+
+def _tile_gep(f, tile, rows, cols, r, c):
+    return f.emit(f"getelementptr [{rows} x [{cols} x f32]], ptr addrspace(5) {tile}, i64 {r}, i64 {c}")
+
+
+def _tile_load(f, tile, rows, cols, r, c):
+    p = _tile_gep(f, tile, rows, cols, r, c)
+    return f.emit(f"load f32, ptr addrspace(5) {p}")
+
+
+def _tile_store(f, tile, rows, cols, r, c, v):
+    p = _tile_gep(f, tile, rows, cols, r, c)
+    f.stmt(f"store f32 {v}, ptr addrspace(5) {p}")
+
+
+def _reduce_rows(f, prefix, src, rows, cols, dst, is_max):
+    """A reduction along axis 1 of a [rows x cols] tile into dst [rows x 1],
+    cols > 16: reduce.rs lower_single_row_reduce_loop + lower_reduce_extent_loop
+    (rows == 1 takes the single-column form with one column)."""
+    axis = "col" if rows == 1 else "row"
+    header = f.new_block(f"{prefix}_{axis}_header", [(f"loop_{axis}", "i64")])
+    blk = f.new_block(f"{prefix}_{axis}_body", [(f"loop_{axis}", "i64")])
+    cont = f.new_block(f"{prefix}_continue", [])
+    f.term(f"br label %{header[0]} ; args(0)")
+    f.switch(header)
+    i = header[1][0][0]
+    c = f.emit(f"icmp slt {i}, {1 if rows == 1 else rows}")
+    f.term(f"br i1 {c}, label %{blk[0]}, label %{cont[0]} ; true_args({i})")
+    f.switch(blk)
+    row = 0 if rows == 1 else blk[1][0][0]
+    col = blk[1][0][0] if rows == 1 else 0
+    init = _tile_load(f, src, rows, cols, row, 0)
+    rh = f.new_block(f"{prefix}_reduce_header", [("reduce_idx", "i64"), ("reduce_acc", "f32")])
+    rb = f.new_block(f"{prefix}_reduce_body", [("reduce_idx", "i64"), ("reduce_acc", "f32")])
+    rx = f.new_block(f"{prefix}_reduce_exit", [("final_acc", "f32")])
+    f.term(f"br label %{rh[0]} ; args(1, {init})")
+    f.switch(rh)
+    hi, ha = rh[1][0][0], rh[1][1][0]
+    c = f.emit(f"icmp slt {hi}, {cols}")
+    f.term(f"br i1 {c}, label %{rb[0]}, label %{rx[0]} ; true_args({hi}, {ha}) ; false_args({ha})")
+    f.switch(rb)
+    bi, ba = rb[1][0][0], rb[1][1][0]
+    nxt = _tile_load(f, src, rows, cols, row, bi)
+    if is_max:
+        gt = f.emit(f"fcmp ogt {nxt}, {ba}")
+        acc = f.emit(f"select i1 {gt}, f32 {nxt}, f32 {ba}")
+    else:
+        acc = f.emit(f"fadd {ba}, {nxt}")
+    ni = f.emit(f"add {bi}, 1")
+    f.term(f"br label %{rh[0]} ; args({ni}, {acc})")
+    f.switch(rx)
+    _tile_store(f, dst, rows, 1, row, col, rx[1][0][0])
+    nx = f.emit(f"add {blk[1][0][0]}, 1")
+    f.term(f"br label %{header[0]} ; args({nx})")
+    f.switch(cont)
+
+
+def softmax(bm, bn):
+    """softmax<BM, BN> over x, y [rows, BN·k] (crates/sile/tests/backend_softmax.rs:3-37):
+    per program the row tile [BM, BN] at (pid, 0): load, row max, exp(x - max),
+    row sum, divide, store, each its own loop nest over its own tile."""
+    f = _Fn("softmax", [("x", 2, 0), ("y", 2, 2)])
+    sx = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    sy = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2")
+    pid = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+
+    def origin(shape_desc):
+        rb = f.emit(f"mul {pid}, {bm}")
+        cb = f.emit(f"mul 0, {bn}")
+        sp = f.emit(f"getelementptr i64, ptr addrspace(4) {shape_desc}, i64 1")
+        stride = f.emit(f"load i64, ptr addrspace(4) {sp}")
+        ro = f.emit(f"mul {rb}, {stride}")
+        return f.emit(f"add {ro}, {cb}"), stride
+
+    tiles = {}
+    for t, cols in (("x", bn), ("m", 1), ("e", bn), ("s", 1), ("y", bn)):
+        tiles[t] = f.emit(f"alloca [{bm} x [{cols} x f32]], addrspace(5)")
+    xo, xs = origin(sx)
+
+    def load_body(r, c):
+        ro = f.emit(f"mul {r}, {xs}")
+        wr = f.emit(f"add {xo}, {ro}")
+        i = f.emit(f"add {wr}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %x, i64 {i}")
+        v = f.emit(f"load f32, ptr addrspace(1) {p}")
+        _tile_store(f, tiles["x"], bm, bn, r, c, v)
+    _tile_loop(f, "tile_load", bm, bn, load_body)
+    _reduce_rows(f, "tile_reduce_max", tiles["x"], bm, bn, tiles["m"], True)
+
+    def exp_body(r, c):
+        xv = _tile_load(f, tiles["x"], bm, bn, r, c)
+        mv = _tile_load(f, tiles["m"], bm, 1, r, 0)
+        d = f.emit(f"fsub {xv}, {mv}")
+        ex = f.emit(f"call f32 @llvm.exp.f32(f32 {d})")
+        _tile_store(f, tiles["e"], bm, bn, r, c, ex)
+    _tile_loop(f, "tile_map_exp", bm, bn, exp_body)
+    _reduce_rows(f, "tile_reduce_sum", tiles["e"], bm, bn, tiles["s"], False)
+
+    def div_body(r, c):
+        ev = _tile_load(f, tiles["e"], bm, bn, r, c)
+        sv = _tile_load(f, tiles["s"], bm, 1, r, 0)
+        q = f.emit(f"fdiv {ev}, {sv}")
+        _tile_store(f, tiles["y"], bm, bn, r, c, q)
+    _tile_loop(f, "tile_map_div", bm, bn, div_body)
+    yo, ys = origin(sy)
+
+    def store_body(r, c):
+        v = _tile_load(f, tiles["y"], bm, bn, r, c)
+        ro = f.emit(f"mul {r}, {ys}")
+        wr = f.emit(f"add {yo}, {ro}")
+        i = f.emit(f"add {wr}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %y, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {p}")
+    _tile_loop(f, "tile_store", bm, bn, store_body)
+    f.term("ret void")
+    return f.text()
+
+
+def vec_add(tile):
+    """vec_add<TILE> over rank-1 a, b, c (crates/sile/examples/vec_add.rs): the
+    tiles [1, TILE] at pid, loaded, added, stored (tile_memory.rs: rank-1
+    buffers take `pid * TILE + row * TILE + col`)."""
+    f = _Fn("vec_add", [("a", 1, 0), ("b", 1, 1), ("c", 1, 2)])
+    pid = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    ta = f.emit(f"alloca [1 x [{tile} x f32]], addrspace(5)")
+    tb = f.emit(f"alloca [1 x [{tile} x f32]], addrspace(5)")
+    tc = f.emit(f"alloca [1 x [{tile} x f32]], addrspace(5)")
+
+    def index(r, c):
+        base = f.emit(f"mul {pid}, {tile}")
+        ro = f.emit(f"mul {r}, {tile}")
+        eo = f.emit(f"add {ro}, {c}")
+        return f.emit(f"add {base}, {eo}")
+
+    for buf, t in (("a", ta), ("b", tb)):
+        def load_body(r, c, buf=buf, t=t):
+            p = f.emit(f"getelementptr f32, ptr addrspace(1) %{buf}, i64 {index(r, c)}")
+            v = f.emit(f"load f32, ptr addrspace(1) {p}")
+            _tile_store(f, t, 1, tile, r, c, v)
+        _tile_loop(f, "tile_load", 1, tile, load_body)
+
+    def add_body(r, c):
+        x = _tile_load(f, ta, 1, tile, r, c)
+        y = _tile_load(f, tb, 1, tile, r, c)
+        _tile_store(f, tc, 1, tile, r, c, f.emit(f"fadd {x}, {y}"))
+    _tile_loop(f, "tile_map", 1, tile, add_body)
+
+    def store_body(r, c):
+        v = _tile_load(f, tc, 1, tile, r, c)
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {index(r, c)}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {p}")
+    _tile_loop(f, "tile_store", 1, tile, store_body)
+    f.term("ret void")
+    return f.text()
+
+
+def row_max(bn):
+    """The row max of x [rows, BN] into out [rows] (the DSL's reduce_max along
+    axis 1 of a [1, BN] tile per program, reduce.rs:10-30): load, reduce
+    (single-column form: the output tile is [1 x 1]), store."""
+    f = _Fn("row_max", [("x", 2, 0), ("out", 1, 2)])
+    sx = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    pid = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    tx = f.emit(f"alloca [1 x [{bn} x f32]], addrspace(5)")
+    tm = f.emit("alloca [1 x [1 x f32]], addrspace(5)")
+    sp = f.emit(f"getelementptr i64, ptr addrspace(4) {sx}, i64 1")
+    stride = f.emit(f"load i64, ptr addrspace(4) {sp}")
+    ro = f.emit(f"mul {pid}, {stride}")
+
+    def load_body(r, c):
+        rs = f.emit(f"mul {r}, {stride}")
+        wr = f.emit(f"add {ro}, {rs}")
+        i = f.emit(f"add {wr}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %x, i64 {i}")
+        _tile_store(f, tx, 1, bn, r, c, f.emit(f"load f32, ptr addrspace(1) {p}"))
+    _tile_loop(f, "tile_load", 1, bn, load_body)
+    _reduce_rows(f, "tile_reduce_max", tx, 1, bn, tm, True)
+
+    def store_body(r, c):
+        v = _tile_load(f, tm, 1, 1, r, c)
+        base = f.emit(f"mul {pid}, 1")
+        i = f.emit(f"add {base}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %out, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {p}")
+    _tile_loop(f, "tile_store", 1, 1, store_body)
+    f.term("ret void")
+    return f.text()

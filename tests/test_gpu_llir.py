@@ -187,3 +187,50 @@ def test_spread_reduce_and_vec_add(hip):
     c = _run(hip, kern, [a, b, np.zeros_like(a)], (16, 1, 1))[2]
     np.testing.assert_array_equal(c, a + b)
     kern.close()
+
+
+# ---- LLIR in the reference's loop shapes (tests/llir_shapes.py) ----
+
+from tests import llir_shapes  # noqa: E402
+
+
+@pytest.mark.parametrize("rows,bm,bn", [(64, 4, 8192), (10, 2, 300), (8, 1, 1000), (6, 2, 8)])
+def test_reference_shaped_softmax(hip, rows, bm, bn):
+    """softmax<BM, BN> in the reference's loop shapes (a loop nest and a
+    private tile per op; reductions from element 0): spread over a
+    1024-lane workgroup per program (one program a lane at BN = 8), within
+    1e-7 + 1e-5 |r| of the oracle's tile semantics."""
+    say(f"llir reference-shaped softmax<{bm}, {bn}> over [{rows}, {bn}]")
+    kern = hip.LlirKernel(llir_shapes.softmax(bm, bn), (1, bm, bn))
+    x = rng(bm * bn + 3).normal(scale=2.0, size=(rows, bn)).astype(np.float32)
+    grid = (rows // bm, 1, 1)
+    y = _run(hip, kern, [x, np.zeros_like(x)], grid)[1]
+    ref = np.zeros_like(x)
+    cpuref.kernel_softmax(x, ref, grid, bm, bn)
+    assert_close(y, ref, atol=1e-7, rtol=1e-5, what="reference-shaped softmax")
+    kern.close()
+
+
+@pytest.mark.parametrize("bn", [4096, 1000])
+def test_reference_shaped_row_max_is_bit_exact(hip, bn):
+    """The row max in the reference's shapes (the reduction's element 0 read
+    from the LDS copy its lane wrote, the rest folded over the lanes) equals
+    the sequential fold bit for bit on rows with NaN, -inf and +0 / -0 ties."""
+    x = max_fold_probe_rows(bn, bn + 11)
+    rows = x.shape[0]
+    say(f"llir reference-shaped row max over [{rows}, {bn}]")
+    kern = hip.LlirKernel(llir_shapes.row_max(bn), (1, 1, 1))
+    out = _run(hip, kern, [x, np.full(rows, 5.0, np.float32)], (rows, 1, 1))[1]
+    assert_same_bits(out, cpuref.reduce_rows(x, cpuref.REDUCE_MAX), what="reference-shaped row max")
+    kern.close()
+
+
+def test_reference_shaped_vec_add(hip):
+    say("llir reference-shaped vec_add<4096> and <8>")
+    for tile, n in ((4096, 1 << 16), (8, 4096)):
+        kern = hip.LlirKernel(llir_shapes.vec_add(tile), (2, 1, tile))
+        a = rng(tile).integers(-1000, 1000, n).astype(np.float32)
+        b = rng(tile + 1).integers(-1000, 1000, n).astype(np.float32)
+        c = _run(hip, kern, [a, b, np.zeros_like(a)], (n // tile, 1, 1))[2]
+        np.testing.assert_array_equal(c, a + b)
+        kern.close()

@@ -50,7 +50,10 @@ def test_generated_source_follows_the_cpu_codegen():
     assert "v_prod = v_av * v_bv;" in src and "v_acc_next = v_acc + v_prod;" in src
     sm = hip.llir_to_hip(text("softmax"), PLANS["softmax"])
     assert "expf(v_d)" in sm and "(v_gt) ? (v_xv) : (v_mx)" in sm
-    assert "float v_tile_storage[2][8];" in sm and "&(v_tile[(0LL)][v_r][v_e])" in sm
+    # the tile's storage, its pointer decayed to a row pointer, an element gep
+    # indexing [row][col] (the backends' C form, cpu/codegen.rs:601-664)
+    assert "float v_tile_storage[2][8];" in sm and "float (*v_tile)[8] = v_tile_storage;" in sm
+    assert "&(v_tile[v_r][v_e])" in sm
     pr = hip.llir_to_hip(text("parallel_reduce"), None)
     assert "llir_vec_load_4(v_x, v_off)" in pr and "atomicAdd(v_o, v_acc)" in pr
     # no tile plan, rank-1 last buffer: total tiles = shape of the first buffer
@@ -189,7 +192,7 @@ def test_long_loops_spread_over_the_workgroup():
            "v_sum = coop_init0 + coop_wg_sum(coop_p0" in src  # the sum of exp
     # the tile is only touched at [r, e] by the spread loops: per-lane slices
     assert "float v_tile_storage[4][8];" in src and "__shared__ float v_tile" not in src
-    assert "&(v_tile[(0LL)][v_r][coop_k])" in src
+    assert "&(v_tile[v_r][coop_k])" in src
     # x is never written: the max loop keeps each lane's x values, the exp
     # loop takes them (its iteration 0, which the max loop starting at 1 did
     # not run, loads)
@@ -201,7 +204,7 @@ def test_long_loops_spread_over_the_workgroup():
     wide = hip.llir_to_hip(softmax_llir(1, 32768), (1, 1, 32768))
     assert wide.count("for (long long coop_it = coop_start + (long long)threadIdx.x") == 3
     assert wide.count("#pragma unroll 8") == 3 and "coop_cache" not in wide
-    assert "&(v_tile[(0LL)][v_r][(v_e) / 1024LL])" in wide
+    assert "&(v_tile[v_r][(v_e) / 1024LL])" in wide
     # a barrier after a spread loop only where another lane's later access may
     # conflict: the divide loop stores y; the max loop reads x (never written)
     # and the exp loop writes the lanes' own slices, so neither needs one
@@ -240,3 +243,78 @@ def test_loops_that_cannot_be_spread_stay_serial(name, old, new):
     assert old in t
     src = hip.llir_to_hip(t.replace(old, new), (2, 1, 4096) if name == "vec_add" else None)
     assert "__launch_bounds__(64)" in src and "coop_" not in src
+
+
+# ---- LLIR in the reference's loop shapes (tests/llir_shapes.py) ----
+
+from tests import llir_shapes  # noqa: E402
+
+
+def test_reference_loop_shapes_spread():
+    """The reference's lowering passes a loop header's values on to a body
+    block with parameters of its own, carries the row through the column
+    header of a 2-D nest, indexes tiles [row, col] and starts a reduction
+    from the row's element 0 read before its loop: those loops spread like
+    the hand-written form."""
+    src = hip.llir_to_hip(llir_shapes.softmax(4, 8192), (1, 4, 8192))
+    assert "__launch_bounds__(1024)" in src
+    # load, exp, divide and store column loops and the two reduce loops, in
+    # the slot form; the row loops stay on every lane
+    assert src.count("for (int coop_k = 0; coop_k < 8; ++coop_k) {") == 6
+    # body parameters were replaced by the header's values
+    assert "v_loop_row18" not in src and "v_reduce_acc39" not in src
+    # x, exp and y tiles are per-lane slices; the [4 x 1] max and sum tiles
+    # (read at [row, 0] outside the loops) live in LDS
+    for t in ("v_v4", "v_v6", "v_v8"):
+        assert f"float {t}_storage[4][8];" in src and f"float (*{t})[8] = {t}_storage;" in src
+    for t in ("v_v5", "v_v7"):
+        assert f"__shared__ float {t}_storage[4][1];" in src
+    # a reduction's element 0 comes from an LDS copy that the lane storing it
+    # writes, between barriers around the storing loop
+    assert "if (coop_it == 0LL) v_v4_sh0[v_loop_row16] = v_v27;" in src
+    assert "v_v34 = &(v_v4_sh0[v_loop_row31]);" in src
+    assert "__syncthreads();\n  {\n    const long long coop_start = v_loop_col17;" in src
+    # loops of 8 iterations: one program a lane, tiles in registers
+    small = hip.llir_to_hip(llir_shapes.softmax(2, 8), (1, 2, 8))
+    assert "__launch_bounds__(64)" in small and "coop_" not in small
+    assert "float (*v_v4)[8] = v_v4_storage;" in small
+    va = hip.llir_to_hip(llir_shapes.vec_add(4096), (2, 1, 4096))
+    assert "__launch_bounds__(1024)" in va and va.count("coop_k < 4;") == 4
+    rm = hip.llir_to_hip(llir_shapes.row_max(4096), (1, 1, 1))
+    assert "coop_wg_first_max" in rm and "v_v3_sh0" in rm
+    for t, plan in ((llir_shapes.softmax(4, 8192), (1, 4, 8192)), (llir_shapes.softmax(1, 1000), (1, 1, 1000)),
+                    (llir_shapes.vec_add(4096), (2, 1, 4096)), (llir_shapes.row_max(4096), (1, 1, 1))):
+        image, _ = hip.llir_compile(t, plan)
+        assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+def test_gep_indexes_the_tile_dimensions():
+    """A tile's gep takes an index for each dimension, [row][col], on the
+    storage decayed to a row pointer (crates/sile-backend/src/cpu/codegen.rs
+    gep_private_ptrs_do_not_materialize_fake_storage_bindings); a gep with
+    fewer indices gives the sub-array, decayed; more indices than dimensions
+    are rejected."""
+    t = """define void @g(ptr addrspace(1) %o, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %o [rank=1, shape_offset=0, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %tile = alloca [2 x [2 x f32]], addrspace(5)
+  %elt = getelementptr [2 x [2 x f32]], ptr addrspace(5) %tile, i64 0, i64 1
+  store f32 3.0, ptr addrspace(5) %elt
+  %row = getelementptr [2 x [2 x f32]], ptr addrspace(5) %tile, i64 0
+  %e2 = getelementptr [2 x f32], ptr addrspace(5) %row, i64 1
+  %v = load f32, ptr addrspace(5) %e2
+  %op = getelementptr f32, ptr addrspace(1) %o, i64 0
+  store f32 %v, ptr addrspace(1) %op
+  ret void
+}
+"""
+    src = hip.llir_to_hip(t, None)
+    assert "float v_tile_storage[2][2];" in src and "float (*v_tile)[2] = v_tile_storage;" in src
+    assert "v_elt = &(v_tile[(0LL)][(1LL)]);" in src
+    assert "v_row = (v_tile[(0LL)]);" in src and "v_e2 = &(v_row[(1LL)]);" in src
+    image, _ = hip.llir_compile(t, None)
+    assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    bad = t.replace("i64 0, i64 1\n", "i64 0, i64 0, i64 1\n")
+    with pytest.raises(hip.SileError, match="indexes past the array levels"):
+        hip.llir_to_hip(bad, None)
