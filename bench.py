@@ -569,6 +569,36 @@ def bench_llir_softmax(name, steps, warmup, text=None):
     return res
 
 
+def bench_llir_matmul(name, steps, warmup, size=2048, tile=64, bk=8):
+    """The canonical matmul's LLIR (canonical_matmul.rs:24-444, generated by
+    tests/llir_shapes.py) at M = N = K = size with tile x tile cells a
+    program: the row x column nest spread over a 1024-lane workgroup, each
+    cell's k loop serial on its lane (the reference's order, bit-exact),
+    through the synchronous sile_hip_launch_llir; 2 M N K flops per call,
+    against the VALU rate without FMA (the order forbids contraction)."""
+    from tests import llir_shapes
+    kern = hip.LlirKernel(llir_shapes.matmul(tile, tile, bk), (2, tile, tile))
+    a = hip.DeviceBuffer.from_array(normal(4, (size, size), 1.0))
+    b = hip.DeviceBuffer.from_array(normal(5, (size, size), 1.0))
+    c = hip.DeviceBuffer(size * size * 4)
+    ptrs, shapes = [a.ptr, b.ptr, c.ptr], [size] * 6
+    grid = ((size // tile) ** 2, 1, 1)
+    for _ in range(warmup):
+        kern(ptrs, shapes, grid)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        kern(ptrs, shapes, grid)
+    dt = (time.perf_counter() - t0) / steps
+    res = summarise(name, 2.0 * size ** 3, 1e12, "TFLOP/s", dt * 1e3 * steps, steps, "valu",
+                    PEAK_VALU_F32_TOPS, None)
+    res["note"] = (f"canonical matmul<{tile}, {tile}, {bk}> LLIR, f32, one 1024-lane workgroup "
+                   "a program, bit-identical to the reference's order")
+    for buf in (a, b, c):
+        buf.close()
+    kern.close()
+    return res
+
+
 # softmax<BM=4, BN=8192> (crates/sile/examples/softmax.rs:3-16) in the
 # printed Tile IR form (crates/sile-tile-ir/src/print.rs:5-354) after the
 # default passes, the text a Rust HipBackend hands to sile_hip_tile_ir_route
@@ -922,11 +952,13 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
                    "matvec_f32_8192": "sile_dsl_matvec", "matvec_f32_8192_bk8": "sile_dsl_matvec",
                    "llir_softmax_f32_8192": "sile_kernel_softmax",
                    "llir_softmax_ref_shapes_f32_8192": "sile_kernel_softmax",
+                   "llir_matmul_f32_2048": "sile_kernel_matmul",
                    "tile_ir_softmax_f32_8192": "sile_softmax_rows"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
 EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "llir_softmax_ref_shapes_f32_8192",
+         "llir_matmul_f32_2048",
          "tile_ir_softmax_f32_8192",
          "gemm_f32_exact_4096",
          "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
@@ -983,6 +1015,8 @@ def main():
             results[name] = bench_llir_vec_add(name, args.steps, args.warmup)
         elif name == "llir_softmax_f32_8192":
             results[name] = bench_llir_softmax(name, args.steps, args.warmup)
+        elif name == "llir_matmul_f32_2048":
+            results[name] = bench_llir_matmul(name, args.steps, args.warmup)
         elif name == "llir_softmax_ref_shapes_f32_8192":
             # the same program in the reference's loop shapes: a loop nest and
             # a private tile per op (tests/llir_shapes.py)

@@ -722,31 +722,37 @@ std::string ident(const std::string& name) {
 // The CPU backend runs a program on one thread (crates/sile-backend/src/cpu/codegen.rs:517-551)
 // and the Metal template one thread per threadgroup
 // (crates/sile-backend/src/metal/mod.rs:146-154).  A program whose tile loops
-// are long (a softmax over 8192 columns) then runs each loop serially.  When
-// the function has such a loop in a form whose iterations can be spread over
-// lanes, the program runs on a workgroup of kCoopThreads lanes instead:
-//   * a spread loop is a counted loop: header H(iv, c...) holding only
+// are long (a softmax over 8192 columns, a 64 x 64 matmul tile) then runs each
+// loop serially.  When the function has such a loop in a form whose
+// iterations can be spread over lanes, the program runs on a workgroup of
+// kCoopThreads lanes instead:
+//   * a spread loop is a counted loop: header H(.., iv, ..) holding only
 //     `icmp slt iv, bound` with constant start, bound and step and at least
 //     kCoopMinTrip iterations, one body block B that branches back with
-//     (iv + step, c'...), no atomics, barriers, calls or memcpy in B;
-//   * each carried value c is a fold the lanes can split: a sum
-//     c' = c + x (lane partials from -0.0, a workgroup tree, then
-//     init + total: within fp32 rounding of the sequential chain), or the
-//     max fold c' = x > c ? x : c (each lane keeps its first maximum and its
-//     iteration, partials merge by value then iteration, then
-//     total > init ? total : init: bit for bit the sequential fold, NaN and
-//     +0 / -0 included); c is used in B by its fold only;
+//     (.., iv + step, ..), no atomics, barriers, calls or memcpy in B;
+//   * each other carried value is passed back unchanged (loop-invariant) or
+//     is a fold the lanes can split: a sum c' = c + x (lane partials from
+//     -0.0, a workgroup tree, then init + total: within fp32 rounding of the
+//     sequential chain), or the max fold c' = x > c ? x : c (each lane keeps
+//     its first maximum and its iteration, partials merge by value then
+//     iteration, then total > init ? total : init: bit for bit the
+//     sequential fold, NaN and +0 / -0 included); a fold's value is used in
+//     B by its fold only;
 //   * B's stores go to addresses that differ between iterations (a gep whose
-//     last index is iv or iv + an invariant, the other indices invariant; a
-//     4-wide store at offset iv (+ invariant) with step >= 4), and B loads an
-//     object it stores only through the same pointer;
+//     last index is iv plus invariant terms, the other indices invariant; a
+//     4-wide store at such an offset with step >= 4), and B loads an object
+//     it stores only through the same pointer;
+//   * a 2-D nest (row loop around a column loop whose body is a region of
+//     blocks, e.g. the MMA's cell with its k loop) spreads its row x column
+//     iterations as one flat loop, the region serial on each lane;
 //   * lane l runs iterations l, l + W, ...; after the loop every lane holds
-//     the folded values and the final iv, and a barrier orders the loop's
-//     stores before anything that follows;
+//     the folded values and the final counter; a barrier follows when another
+//     lane's later access may conflict with the loop's;
 //   * everything outside spread loops runs on every lane with the same values
 //     (so its stores write identical values); an atomic there runs on lane 0
-//     only (its result must be unused); allocas become workgroup (LDS)
-//     arrays.
+//     only (its result must be unused); tiles touched only by spread loops at
+//     the iteration's element are split over the lanes' registers, others
+//     live in LDS.
 // Functions without such a loop keep one program per lane.
 // ---------------------------------------------------------------------------
 constexpr int kCoopThreads = 1024;
@@ -787,6 +793,16 @@ struct CoopLoop {
   // a workgroup barrier before the loop: it writes LDS copies that code
   // outside the spread loops reads, which every lane must have done first
   bool pre_barrier = false;
+  // A 2-D nest (rows > 0): `header` is the row header, `iv` the column and
+  // `row_iv` the row; iteration f = row * cols + col of [0, rows * cols) runs
+  // the region (the blocks between the column header and its back edges,
+  // `entry` first) with that row and column.  `guards`: strides that must be
+  // at least `cols` for the buffer stores of different iterations to differ
+  // (checked at run time; otherwise lane 0 runs the nest in order).
+  int64_t rows = 0, cols = 0;
+  std::string row_iv, col_header, row_latch, entry;
+  std::vector<std::string> region;
+  std::vector<std::string> guards;
 };
 struct CoopPlan {
   bool on = false;
@@ -797,6 +813,9 @@ struct CoopPlan {
   // the spread loops: an LDS copy of those elements (the tile minus its last
   // dimension) for each such c, written by the lane that stores the element
   std::map<std::string, std::set<int64_t>> shadows;
+  // tiles [rows x cols] touched only at [row, col] by slot-form nests of that
+  // shape: element f = row * cols + col is lane f % W's slot f / W
+  std::set<std::string> nest_private;
   std::vector<CoopCache> caches;
   std::string why;                         // why the function stays one program per lane
 };
@@ -1050,6 +1069,265 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     plan.loops[L.header] = L;
     plan.bodies.insert(L.body);
   }
+  // 2-D nests whose body is a region of blocks (the reference's tile loops
+  // and its MMA, tile_loops/grid.rs:7-130, tile_compute/mma.rs:25-260):
+  //   RH(r): icmp slt r, M; true -> CH(0), false -> X
+  //   CH(c): icmp slt c, N; true -> E, false -> RL
+  //   RL: r' = r + 1; br RH(r')
+  //   E ...: blocks entered only at E from CH and left only by br CH(c + 1)
+  // Iteration f = r N + c of [0, M N) runs the region with (r, c) on lane
+  // f % W; a loop inside the region stays serial on its lane (the MMA's k
+  // loop keeps its order).
+  for (const Block& rh : fn.blocks) {
+    int64_t M = 0, N = 0, z = -1, one = 0;
+    if (rh.params.size() != 1 || rh.insts.size() != 1 || rh.term.kind != "condbr") continue;
+    const std::string rv = rh.params[0].first;
+    const Inst& rc = rh.insts[0];
+    if (rc.op != "cmp" || rc.sub != "slt" || !rc.args[0].is_value || rc.args[0].name != rv ||
+        !const_int(rc.args[1], M) || !rh.term.cond.is_value || rh.term.cond.name != rc.result)
+      continue;
+    const Block* ch = block(rh.term.t);
+    if (!ch || ch == &rh || ch->params.size() != 1 || rh.term.targs.size() != 1 ||
+        !const_int(rh.term.targs[0], z) || z != 0 || ch->insts.size() != 1 ||
+        ch->term.kind != "condbr" || !ch->term.targs.empty() || !ch->term.fargs.empty())
+      continue;
+    const std::string cv = ch->params[0].first;
+    const Inst& cc = ch->insts[0];
+    if (cc.op != "cmp" || cc.sub != "slt" || !cc.args[0].is_value || cc.args[0].name != cv ||
+        !const_int(cc.args[1], N) || !ch->term.cond.is_value || ch->term.cond.name != cc.result)
+      continue;
+    const Block* rl = block(ch->term.f);
+    const Block* entry = block(ch->term.t);
+    if (!rl || !entry || rl == entry || rl == &rh || entry == &rh || !entry->params.empty() ||
+        rl->insts.size() != 1 || rl->term.kind != "br" || rl->term.t != rh.name ||
+        rl->term.targs.size() != 1)
+      continue;
+    {
+      const Inst& a = rl->insts[0];
+      if (a.op != "bin" || a.sub != "add" || !a.args[0].is_value || a.args[0].name != rv ||
+          !const_int(a.args[1], one) || one != 1 || !rl->term.targs[0].is_value ||
+          rl->term.targs[0].name != a.result)
+        continue;
+    }
+    if (M <= 0 || N <= 0 || M * N < kCoopMinTrip) continue;
+    // the region: what E reaches without passing CH
+    std::set<std::string> region;
+    bool ok = true;
+    std::vector<std::string> work{entry->name};
+    while (!work.empty() && ok) {
+      const std::string n = work.back();
+      work.pop_back();
+      if (region.count(n)) continue;
+      if (n == rh.name || n == rl->name) {
+        ok = false;
+        break;
+      }
+      const Block* b = block(n);
+      if (!b || b->term.kind == "ret" || b->term.kind == "switch") {
+        ok = false;
+        break;
+      }
+      region.insert(n);
+      for (const std::string& t : {b->term.t, b->term.f})
+        if (!t.empty() && t != ch->name) work.push_back(t);
+    }
+    if (!ok) continue;
+    if (region.size() == 1 && N >= kCoopMinTrip) continue;   // the column loop spreads by itself
+    // entered only at E from CH; CH reached only from RH (with 0) and from the
+    // region with c + 1; RH reached from one place outside (with 0) and RL
+    int rh_entries = 0;
+    for (const Block& b : fn.blocks) {
+      auto edge = [&](const std::string& t, const std::vector<Operand>& args) {
+        if (t.empty()) return;
+        if (region.count(t) && !region.count(b.name) && !(b.name == ch->name && t == entry->name))
+          ok = false;
+        if (t == ch->name && b.name != rh.name) {
+          if (!region.count(b.name) || args.size() != 1 || !args[0].is_value) {
+            ok = false;
+            return;
+          }
+          auto d = def_inst.find(args[0].name);
+          int64_t inc = 0;
+          if (d == def_inst.end() || d->second->op != "bin" || d->second->sub != "add" ||
+              !d->second->args[0].is_value || d->second->args[0].name != cv ||
+              !const_int(d->second->args[1], inc) || inc != 1)
+            ok = false;
+        }
+        if (t == rh.name && b.name != rl->name) {
+          int64_t s0 = -1;
+          ++rh_entries;
+          if (args.size() != 1 || !const_int(args[0], s0) || s0 != 0) ok = false;
+        }
+      };
+      if (b.term.kind == "br") edge(b.term.t, b.term.targs);
+      if (b.term.kind == "condbr") {
+        edge(b.term.t, b.term.targs);
+        edge(b.term.f, b.term.fargs);
+      }
+    }
+    if (!ok || rh_entries != 1) continue;
+    auto in_region = [&](const std::string& v) {
+      auto it = def_block.find(v);
+      return it != def_block.end() && region.count(it->second);
+    };
+    // invariant over the nest: defined before it, or a pure operation of
+    // invariant operands in the region
+    std::map<std::string, bool> memo;
+    std::function<bool(const Operand&)> invariant = [&](const Operand& o) -> bool {
+      if (!o.is_value) return true;
+      if (o.name == rv || o.name == cv) return false;
+      auto it = def_block.find(o.name);
+      const std::string db = it == def_block.end() ? "" : it->second;
+      if (db == rh.name || db == ch->name || db == rl->name) return false;
+      if (!region.count(db)) return true;
+      auto m = memo.find(o.name);
+      if (m != memo.end()) return m->second;
+      memo[o.name] = false;
+      auto di = def_inst.find(o.name);
+      if (di == def_inst.end()) return false;        // a region block's parameter
+      const Inst& d = *di->second;
+      bool r = d.op == "bin" || d.op == "cmp" || d.op == "select" || d.op == "cast" || d.op == "gep";
+      for (const Operand& a : d.args) r = r && invariant(a);
+      memo[o.name] = r;
+      return r;
+    };
+    // a buffer index `invariants + r * S + c` (any grouping): the stride S
+    std::vector<std::string> guards;
+    auto row_col_index = [&](const Operand& idx) -> bool {
+      int cols_seen = 0, rows_seen = 0;
+      bool good = true;
+      std::function<void(const Operand&)> walk = [&](const Operand& o) {
+        if (!good) return;
+        if (invariant(o)) return;
+        if (o.is_value && o.name == cv) {
+          ++cols_seen;
+          return;
+        }
+        auto di = o.is_value ? def_inst.find(o.name) : def_inst.end();
+        if (di == def_inst.end() || !in_region(o.name)) {
+          good = false;
+          return;
+        }
+        const Inst& d = *di->second;
+        if (d.op == "bin" && d.sub == "add") {
+          walk(d.args[0]);
+          walk(d.args[1]);
+          return;
+        }
+        if (d.op == "bin" && d.sub == "mul") {
+          const Operand* st = nullptr;
+          if (d.args[0].is_value && d.args[0].name == rv) st = &d.args[1];
+          else if (d.args[1].is_value && d.args[1].name == rv) st = &d.args[0];
+          if (!st || !invariant(*st)) {
+            good = false;
+            return;
+          }
+          ++rows_seen;
+          int64_t sv = 0;
+          if (const_int(*st, sv)) {
+            if (sv < N) good = false;
+          } else if (st->is_value) {
+            guards.push_back(st->name);
+          } else {
+            good = false;
+          }
+          return;
+        }
+        good = false;
+      };
+      walk(idx);
+      return good && cols_seen == 1 && (rows_seen == 1 || (rows_seen == 0 && M == 1));
+    };
+    auto row_col_gep = [&](const Inst& g) {
+      return g.args.size() == 3 && g.args[1].is_value && g.args[1].name == rv && g.args[2].is_value &&
+             g.args[2].name == cv;
+    };
+    std::vector<std::string> order;
+    for (const Block& b : fn.blocks)
+      if (region.count(b.name)) order.push_back(b.name);
+    std::set<std::string> stored;      // objects the region stores
+    std::set<std::string> store_ptrs;  // pointers it stores through
+    bool any_store = false;
+    for (const std::string& bn : order) {
+      for (const Inst& in : block(bn)->insts) {
+        if (in.op == "atomic" || in.op == "memcpy" || in.op == "call" || in.op == "alloca" ||
+            (in.op == "intr" && (in.sub == "barrier" || in.sub == "vload" || in.sub == "vstore"))) {
+          ok = false;
+          break;
+        }
+        if (in.op != "store") continue;
+        any_store = true;
+        auto gi = in.args[0].is_value ? def_inst.find(in.args[0].name) : def_inst.end();
+        if (gi == def_inst.end() || !in_region(in.args[0].name) || gi->second->op != "gep" ||
+            !gi->second->args[0].is_value || !invariant(gi->second->args[0])) {
+          ok = false;
+          break;
+        }
+        const Inst& g = *gi->second;
+        const std::string obj = root(g.args[0].name);
+        const bool is_param = !def_inst.count(obj) && !def_block.count(obj);
+        if (!(row_col_gep(g) || (is_param && g.args.size() == 2 && row_col_index(g.args[1])))) {
+          ok = false;
+          break;
+        }
+        stored.insert(obj);
+        store_ptrs.insert(in.args[0].name);
+      }
+      if (!ok) break;
+    }
+    if (!ok) continue;
+    // loads of what the region stores (or through a pointer of unknown
+    // origin while it stores): only the iteration's own element
+    for (const std::string& bn : order) {
+      for (const Inst& in : block(bn)->insts) {
+        if (in.op != "load" || !in.args[0].is_value) continue;
+        const std::string obj = root(in.args[0].name);
+        const bool known = !def_block.count(obj) || (def_inst.count(obj) && def_inst[obj]->op == "alloca");
+        if (!stored.count(obj) && (known || !any_store)) continue;
+        if (store_ptrs.count(in.args[0].name)) continue;
+        auto gi = def_inst.find(in.args[0].name);
+        if (gi == def_inst.end() || gi->second->op != "gep" || !row_col_gep(*gi->second)) ok = false;
+      }
+    }
+    if (!ok) continue;
+    CoopLoop L;
+    L.header = rh.name;
+    L.exit = rh.term.f;
+    L.iv = cv;
+    L.row_iv = rv;
+    L.rows = M;
+    L.cols = N;
+    L.bound = M * N;
+    L.col_header = ch->name;
+    L.row_latch = rl->name;
+    L.entry = entry->name;
+    L.region = order;
+    L.guards = guards;
+    const int64_t slots = (M * N + kCoopThreads - 1) / kCoopThreads;
+    if (guards.empty() && slots <= kCoopMaxSlots) L.slots = slots;
+    plan.loops[L.header] = L;
+  }
+  // a nest inside another nest's region, or a loop inside one, stays serial
+  {
+    std::set<std::string> inner;
+    for (auto& kv : plan.loops)
+      if (kv.second.rows > 0)
+        for (const std::string& b : kv.second.region) inner.insert(b);
+    for (auto it = plan.loops.begin(); it != plan.loops.end();) {
+      if (inner.count(it->first)) {
+        plan.bodies.erase(it->second.body);
+        it = plan.loops.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    for (auto& kv : plan.loops)
+      if (kv.second.rows > 0) {
+        plan.bodies.insert(kv.second.col_header);
+        plan.bodies.insert(kv.second.row_latch);
+        for (const std::string& b : kv.second.region) plan.bodies.insert(b);
+      }
+  }
   if (plan.loops.empty()) {
     plan.why = "no loop of at least " + std::to_string(kCoopMinTrip) + " iterations that lanes can split";
     return plan;
@@ -1059,7 +1337,8 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
   // e / W.
   for (auto& kv : plan.loops) {
     CoopLoop& L = kv.second;
-    if (L.step == 1 && L.bound > 0 && (L.bound + kCoopThreads - 1) / kCoopThreads <= kCoopMaxSlots)
+    if (L.rows == 0 && L.step == 1 && L.bound > 0 &&
+        (L.bound + kCoopThreads - 1) / kCoopThreads <= kCoopMaxSlots)
       L.slots = (L.bound + kCoopThreads - 1) / kCoopThreads;
   }
   // Loads of a buffer the function never writes, at [inv + iv] with inv
@@ -1077,7 +1356,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     std::map<std::pair<std::string, std::string>, int> key_cache;
     for (const Block& hb : fn.blocks) {
       auto lp = plan.loops.find(hb.name);
-      if (lp == plan.loops.end() || lp->second.slots == 0) continue;
+      if (lp == plan.loops.end() || lp->second.slots == 0 || lp->second.rows > 0) continue;
       CoopLoop& L = lp->second;
       const Block* body = block(L.body);
       for (const Inst& in : body->insts) {
@@ -1126,11 +1405,15 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
   // workgroup keeping the tile in LDS.
   {
     std::map<std::string, std::string> body_of_header;
-    for (auto& kv : plan.loops) body_of_header[kv.second.body] = kv.first;
+    for (auto& kv : plan.loops) {
+      if (kv.second.rows == 0) body_of_header[kv.second.body] = kv.first;
+      for (const std::string& r : kv.second.region) body_of_header[r] = kv.first;
+    }
     for (const Block& b : fn.blocks)
       for (const Inst& in : b.insts) {
         if (in.op != "alloca") continue;
         bool priv = true;
+        bool in_nest = false, in_1d = false;   // touched by a nest / by a 1-D loop
         Type abase;
         std::vector<int64_t> adims;
         array_shape(in.aux, abase, adims);
@@ -1157,13 +1440,27 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
           for (const Inst& x : u.insts) {
             for (size_t k = 0; k < x.args.size(); ++k) {
               if (!x.args[k].is_value || x.args[k].name != in.result) continue;
+              // in a slot-form nest of the tile's shape, at [row, col]
+              if (L && L->rows > 0) {
+                if (x.op == "gep" && k == 0 && L->slots > 0 && adims.size() == 2 &&
+                    adims[0] == L->rows && adims[1] == L->cols && x.args.size() == 3 &&
+                    x.args[1].is_value && x.args[1].name == L->row_iv && x.args[2].is_value &&
+                    x.args[2].name == L->iv) {
+                  in_nest = true;
+                  continue;
+                }
+                priv = false;
+                continue;
+              }
               // as the base of a gep to an element (an index for each
               // dimension) in a spread loop with start 0, step 1, last index
               // the loop counter
               if (x.op == "gep" && k == 0 && L && L->step == 1 && (L->slots > 0 || L->start == 0) &&
                   x.args.back().is_value && x.args.back().name == L->iv &&
-                  x.args.size() == adims.size() + 1)
+                  x.args.size() == adims.size() + 1) {
+                in_1d = true;
                 continue;
+              }
               // outside the spread loops, a gep to an element at a constant
               // last index that only loads use (the reference's reduce reads
               // its first element, tile_compute/reduce.rs:325-335)
@@ -1182,7 +1479,11 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
           for (const Operand& a : u.term.fargs)
             if (a.is_value && a.name == in.result) priv = false;
         }
-        if (priv) {
+        if (priv && in_nest && (in_1d || !cols.empty())) priv = false;
+        if (priv && in_nest) {
+          plan.nest_private.insert(in.result);
+          alloca_bytes -= 4 * adims[0] * adims[1];
+        } else if (priv) {
           plan.private_allocas.insert(in.result);
           if (!cols.empty()) {
             plan.shadows[in.result] = cols;
@@ -1218,31 +1519,41 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
              (in.op == "intr" && in.sub == "vstore")) && in.args[0].is_value)
           written.insert(root(in.args[0].name));
       }
+    auto sliced = [&](const std::string& r) {
+      return plan.private_allocas.count(r) || plan.nest_private.count(r);
+    };
+    // a buffer parameter or an alloca (else a pointer of unknown origin)
+    auto known = [&](const std::string& r) {
+      return !def_block.count(r) || (def_inst.count(r) && def_inst.at(r)->op == "alloca");
+    };
     for (auto& kv : plan.loops) {
       CoopLoop& L = kv.second;
       bool need = false;
-      for (const Inst& in : block(L.body)->insts) {
-        const bool st = in.op == "store" || in.op == "atomic" || in.op == "memcpy" ||
-                        (in.op == "intr" && in.sub == "vstore");
-        const bool ld = in.op == "load" || (in.op == "intr" && in.sub == "vload");
-        if (st) {
-          if (!in.args[0].is_value || !plan.private_allocas.count(root(in.args[0].name))) {
-            need = true;
-          } else if (plan.shadows.count(root(in.args[0].name))) {
-            need = true;            // its LDS copies, read outside the loops
-            L.pre_barrier = true;
+      std::vector<std::string> blocks = L.region;
+      if (L.rows == 0) blocks.push_back(L.body);
+      for (const std::string& bn : blocks)
+        for (const Inst& in : block(bn)->insts) {
+          const bool st = in.op == "store" || in.op == "atomic" || in.op == "memcpy" ||
+                          (in.op == "intr" && in.sub == "vstore");
+          const bool ld = in.op == "load" || (in.op == "intr" && in.sub == "vload");
+          if (st) {
+            if (!in.args[0].is_value || !sliced(root(in.args[0].name))) {
+              need = true;
+            } else if (plan.shadows.count(root(in.args[0].name))) {
+              need = true;            // its LDS copies, read outside the loops
+              L.pre_barrier = true;
+            }
+          }
+          const Operand* src = ld ? &in.args[0] : in.op == "memcpy" ? &in.args[1] : nullptr;
+          if (src) {
+            if (!src->is_value) {
+              need = true;
+            } else {
+              const std::string r = root(src->name);
+              if (!known(r) || (!sliced(r) && written.count(r))) need = true;
+            }
           }
         }
-        const Operand* src = ld ? &in.args[0] : in.op == "memcpy" ? &in.args[1] : nullptr;
-        if (src) {
-          if (!src->is_value) {
-            need = true;
-          } else {
-            const std::string r = root(src->name);
-            if (!plan.private_allocas.count(r) && written.count(r)) need = true;
-          }
-        }
-      }
       L.barrier = need;
     }
   }
@@ -1288,6 +1599,8 @@ struct Emitter {
   std::ostringstream o;
   const CoopLoop* cur = nullptr;   // the slot-form spread loop being emitted
   const CoopLoop* in_loop = nullptr;   // the spread loop being emitted (any form)
+  std::map<std::string, std::string> relabel;   // block -> label inside a nest being emitted
+  int nests = 0;
 
   const Inst* def_of(const std::string& v) const {
     for (const Block& b : fn.blocks)
@@ -1340,6 +1653,11 @@ struct Emitter {
     if (in.op == "gep") {
       // a per-lane slice of a tile: element e of the last dimension is the
       // lane's e / W
+      if (coop.on && a[0].is_value && coop.nest_private.count(a[0].name)) {
+        // [row, col] in a slot-form nest: this lane's slot
+        o << "  " << r << " = &(" << opnd(a[0]) << "[coop_k]);\n";
+        return;
+      }
       const bool slice = coop.on && a[0].is_value && coop.private_allocas.count(a[0].name);
       if (slice && !in_loop) {
         // outside the spread loops: the element's LDS copy
@@ -1428,7 +1746,8 @@ struct Emitter {
   }
 
   // parallel assignment of branch arguments, then the jump
-  void jump(const std::string& target, const std::vector<Operand>& args) {
+  // parallel assignment of branch arguments to the target's parameters
+  void assign(const std::string& target, const std::vector<Operand>& args) {
     const Block* b = nullptr;
     for (const Block& x : fn.blocks)
       if (x.name == target) b = &x;
@@ -1445,7 +1764,12 @@ struct Emitter {
         o << "    " << ident(b->params[k].first) << " = t" << k << ";\n";
       o << "  }\n";
     }
-    o << "  goto L_" << ident(target) << ";\n";
+  }
+
+  void jump(const std::string& target, const std::vector<Operand>& args) {
+    assign(target, args);
+    auto rl = relabel.find(target);
+    o << "  goto " << (rl != relabel.end() ? rl->second : "L_" + ident(target)) << ";\n";
   }
 
   void term(const Term& t) {
@@ -1463,6 +1787,95 @@ struct Emitter {
   }
 
   bool is_shapes(const Param& p) const { return p.name == "__sile_shapes"; }
+
+  // A loop whose header holds only its compare and whose body is one block,
+  // entered only from the header and branching back to it: the body is
+  // emitted inside a C loop at the header (the compiler may unroll it and
+  // keep several iterations' loads in flight; each iteration still runs its
+  // instructions in order).
+  std::set<std::string> c_loop_bodies;
+  const Block* c_loop_body(const Block& h) const {
+    if (h.term.kind != "condbr" || h.insts.size() != 1 || h.insts[0].op != "cmp" ||
+        !h.term.targs.empty() || !h.term.cond.is_value || h.term.cond.name != h.insts[0].result)
+      return nullptr;
+    const Block* b = nullptr;
+    int preds = 0;
+    for (const Block& x : fn.blocks) {
+      if (x.name == h.term.t) b = &x;
+      if (x.term.t == h.term.t) ++preds;
+      if (x.term.kind == "condbr" && x.term.f == h.term.t) ++preds;
+    }
+    if (!b || b == &h || preds != 1 || !b->params.empty() || b->term.kind != "br" ||
+        b->term.t != h.name || h.term.f == b->name)
+      return nullptr;
+    return b;
+  }
+  void block_code(const Block& b, const std::string& label) {
+    o << label << ":;\n";
+    if (const Block* body = c_loop_body(b)) {
+      o << "#pragma unroll 4\n  for (;;) {\n";
+      inst(b.insts[0]);
+      o << "  if (!(" << opnd(b.term.cond) << ")) break;\n";
+      for (const Inst& in : body->insts) inst(in);
+      assign(b.name, body->term.targs);
+      o << "  }\n";
+      jump(b.term.f, b.term.fargs);
+      return;
+    }
+    for (const Inst& in : b.insts) inst(in);
+    term(b.term);
+  }
+
+  // A 2-D nest at its row header: iteration f = row * cols + col runs the
+  // region with that row and column, on lane f % W (slot f / W, unrolled) or,
+  // with stride guards, lane l runs f = l, l + W, ... when every guarded
+  // stride is at least cols and lane 0 runs all of them in order otherwise;
+  // the region's back edges go to the next iteration.  Then the counters
+  // take their final values, a barrier (when needed) and the row header's
+  // exit branch.
+  void coop_nest(const Block& rh, const CoopLoop& L) {
+    const std::string id = std::to_string(nests++);
+    const std::string r = ident(L.row_iv), c = ident(L.iv);
+    const std::string mn = std::to_string(L.rows * L.cols) + "LL", n = std::to_string(L.cols) + "LL";
+    if (L.pre_barrier) o << "  __syncthreads();\n";
+    o << "  {\n";
+    if (L.slots > 0) {
+      o << "#pragma unroll\n";
+      o << "    for (int coop_k = 0; coop_k < " << L.slots << "; ++coop_k) {\n";
+      o << "    const long long coop_it = (long long)coop_k * " << kCoopThreads
+        << "LL + (long long)threadIdx.x;\n";
+      o << "    if (coop_it >= " << mn << ") continue;\n";
+    } else {
+      o << "    const bool coop_par = true";
+      for (const std::string& g : L.guards) o << " && " << ident(g) << " >= " << n;
+      o << ";\n";
+      o << "    const long long coop_end = (coop_par || threadIdx.x == 0) ? " << mn << " : 0LL;\n";
+      o << "    for (long long coop_it = coop_par ? (long long)threadIdx.x : 0LL; coop_it < coop_end; "
+           "coop_it += coop_par ? "
+        << kCoopThreads << "LL : 1LL) {\n";
+    }
+    o << "    " << r << " = coop_it / " << n << "; " << c << " = coop_it % " << n << ";\n";
+    for (const std::string& b : L.region) relabel[b] = "L_" + ident(b) + "_n" + id;
+    relabel[L.col_header] = "coop_next" + id;
+    o << "  goto " << relabel[L.entry] << ";\n";
+    cur = L.slots > 0 ? &L : nullptr;
+    in_loop = &L;
+    for (const std::string& bn : L.region) {
+      if (c_loop_bodies.count(bn)) continue;   // inside its header's C loop
+      const Block* b = nullptr;
+      for (const Block& x : fn.blocks)
+        if (x.name == bn) b = &x;
+      block_code(*b, relabel[bn]);
+    }
+    cur = nullptr;
+    in_loop = nullptr;
+    for (const std::string& b : L.region) relabel.erase(b);
+    relabel.erase(L.col_header);
+    o << "    coop_next" << id << ":;\n    }\n";
+    o << "    " << r << " = " << L.rows << "LL; " << c << " = " << n << ";\n  }\n";
+    if (L.barrier) o << "  __syncthreads();\n";
+    jump(rh.term.f, rh.term.fargs);
+  }
 
   // A spread loop at its header: lane l runs iterations l, l + W, ... of the
   // body with the carried values replaced by the lane's partial folds, the
@@ -1572,6 +1985,16 @@ struct Emitter {
           std::string d;
           for (int64_t n : dims) d += "[" + std::to_string(n) + "]";
           if (dims.empty()) d = "[1]";
+          if (coop.on && coop.nest_private.count(in.result)) {
+            // element f = row * cols + col of the tile is this lane's slot f / W
+            int64_t n = 1;
+            for (int64_t x : dims) n *= x;
+            o << "  " << c_scalar(base) << " " << ident(in.result) << "_storage["
+              << (n + kCoopThreads - 1) / kCoopThreads << "];\n";
+            o << "  " << c_scalar(base) << "* " << ident(in.result) << " = " << ident(in.result)
+              << "_storage;\n";
+            continue;
+          }
           // one program per workgroup: the program's tiles live in LDS, or, when
           // only spread loops touch them at [.., iv], as per-lane slices
           const bool priv = coop.on && coop.private_allocas.count(in.result);
@@ -1617,16 +2040,26 @@ struct Emitter {
         << "];\n  bool coop_has" << cs << " = false;\n  long long coop_tag" << cs << " = 0, coop_lo"
         << cs << " = 0, coop_hi" << cs << " = 0;\n";
     }
+    std::set<std::string> spread_headers;   // spread loops' and nests' own headers
+    for (auto& kv : coop.loops) {
+      spread_headers.insert(kv.first);
+      if (kv.second.rows > 0) spread_headers.insert(kv.second.col_header);
+    }
+    for (const Block& b : fn.blocks)
+      if (!spread_headers.count(b.name))
+        if (const Block* cb = c_loop_body(b)) c_loop_bodies.insert(cb->name);
     for (const Block& b : fn.blocks) {
-      if (coop.bodies.count(b.name)) continue;  // emitted inside its spread loop
-      o << "L_" << ident(b.name) << ":;\n";
+      if (coop.bodies.count(b.name) || c_loop_bodies.count(b.name)) continue;  // emitted in their loop
       auto lp = coop.loops.find(b.name);
       if (lp != coop.loops.end()) {
-        coop_loop(b, lp->second);
+        o << "L_" << ident(b.name) << ":;\n";
+        if (lp->second.rows > 0)
+          coop_nest(b, lp->second);
+        else
+          coop_loop(b, lp->second);
         continue;
       }
-      for (const Inst& in : b.insts) inst(in);
-      term(b.term);
+      block_code(b, "L_" + ident(b.name));
     }
     o << "}\n\n";
   }
@@ -1859,6 +2292,63 @@ void forward_block_args(Function& fn) {
   }
 }
 
+// A block parameter that every edge into the block passes the same value
+// (or itself, around a loop) is that value: it is replaced by it and dropped
+// from the edges.  The value dominates the block (it reaches the block on
+// every edge), so it is available wherever the parameter was.  The
+// reference's MMA loop carries the row and column through its k loop this way
+// (tile_compute/mma.rs:58-75, 190-192).
+bool drop_trivial_params(Function& fn) {
+  bool any = false;
+  for (size_t bi = 1; bi < fn.blocks.size(); ++bi) {
+    Block& b = fn.blocks[bi];
+    for (size_t k = 0; k < b.params.size();) {
+      const std::string p = b.params[k].first;
+      std::vector<std::vector<Operand>*> edges;
+      for (Block& src : fn.blocks) {
+        if (src.term.kind == "br" && src.term.t == b.name) edges.push_back(&src.term.targs);
+        if (src.term.kind == "condbr" && src.term.t == b.name) edges.push_back(&src.term.targs);
+        if (src.term.kind == "condbr" && src.term.f == b.name) edges.push_back(&src.term.fargs);
+      }
+      const Operand* same = nullptr;
+      bool trivial = !edges.empty();
+      for (auto* e : edges) {
+        if (e->size() != b.params.size()) {
+          trivial = false;
+          break;
+        }
+        const Operand& a = (*e)[k];
+        if (a.is_value && a.name == p) continue;
+        if (!same) {
+          same = &a;
+        } else if (same->is_value != a.is_value || same->name != a.name || same->ck != a.ck) {
+          trivial = false;
+          break;
+        }
+      }
+      if (!trivial || !same) {
+        ++k;
+        continue;
+      }
+      const Operand v = *same;
+      for (auto* e : edges) e->erase(e->begin() + (long)k);
+      b.params.erase(b.params.begin() + (long)k);
+      for (Block& u : fn.blocks) {
+        auto fix = [&](Operand& o) {
+          if (o.is_value && o.name == p) o = v;
+        };
+        for (Inst& in : u.insts)
+          for (Operand& a : in.args) fix(a);
+        fix(u.term.cond);
+        for (Operand& a : u.term.targs) fix(a);
+        for (Operand& a : u.term.fargs) fix(a);
+      }
+      any = true;
+    }
+  }
+  return any;
+}
+
 // parse + emit; returns a status and fills `src` / the last error
 int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::string& src,
            std::string& name) {
@@ -1869,7 +2359,8 @@ int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::
     Parser p;
     p.parse(std::string(text));
     verify(p.fn);
-    forward_block_args(p.fn);
+    do forward_block_args(p.fn);
+    while (drop_trivial_params(p.fn));
     const CoopPlan coop = plan_coop(p.fn, p.types);
     Emitter e{p.fn, p.types, coop, {}};
     src = e.emit(plan_out, rows, cols);

@@ -316,3 +316,185 @@ def row_max(bn):
     _tile_loop(f, "tile_store", 1, 1, store_body)
     f.term("ret void")
     return f.text()
+
+
+def matmul(bm, bn, bk):
+    """The canonical matmul's LLIR (crates/sile-tile-ir/src/passes/lowering/
+    canonical_matmul.rs:24-444): c[tile] = a[rows] @ b[:, cols] over
+    k < (lda / BK) * BK for program (m, n): a row x column nest of
+    BM x BN cells, each a k loop carrying (k, sum, a_index, b_index) from
+    (0, 0.0, a_tile_base + row * lda, col_tile_origin + col), then the store
+    at c_tile_base + row * ldc + col."""
+    f = _Fn("matmul", [("a", 2, 0), ("b", 2, 2), ("c", 2, 4)])
+    sa = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    sb = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2")
+    sc = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 4")
+    m = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    n = f.emit("call i32 @llvm.nvvm.ctaid.y()")
+
+    def dim1(desc):
+        p = f.emit(f"getelementptr i64, ptr addrspace(4) {desc}, i64 1")
+        return f.emit(f"load i64, ptr addrspace(4) {p}")
+    lda, ldb, ldc = dim1(sa), dim1(sb), dim1(sc)
+    kt = f.emit(f"sdiv {lda}, {bk}")
+    klim = f.emit(f"mul {kt}, {bk}")
+    row0 = f.emit(f"mul {m}, {bm}")
+    col0 = f.emit(f"mul {n}, {bn}")
+    abase = f.emit(f"mul {row0}, {lda}")
+    crow = f.emit(f"mul {row0}, {ldc}")
+    cbase = f.emit(f"add {crow}, {col0}")
+    rh = f.new_block("matmul_row_header", [("loop_row", "i64")])
+    ch = f.new_block("matmul_col_header", [("loop_row", "i64"), ("loop_col", "i64")])
+    ci = f.new_block("matmul_cell_init", [("loop_row", "i64"), ("loop_col", "i64")])
+    kp = [("loop_row", "i64"), ("loop_col", "i64"), ("loop_k", "i64"), ("loop_sum", "f32"),
+          ("loop_a_index", "i64"), ("loop_b_index", "i64")]
+    kh = f.new_block("matmul_k_header", kp)
+    kb = f.new_block("matmul_k_body", kp)
+    st = f.new_block("matmul_store", [("loop_row", "i64"), ("loop_col", "i64"), ("loop_sum", "f32")])
+    rl = f.new_block("matmul_row_latch", [("loop_row", "i64")])
+    cont = f.new_block("matmul_continue", [])
+    f.term(f"br label %{rh[0]} ; args(0)")
+    f.switch(rh)
+    r = rh[1][0][0]
+    c = f.emit(f"icmp slt {r}, {bm}")
+    f.term(f"br i1 {c}, label %{ch[0]}, label %{cont[0]} ; true_args({r}, 0)")
+    f.switch(ch)
+    cr, cc = ch[1][0][0], ch[1][1][0]
+    c = f.emit(f"icmp slt {cc}, {bn}")
+    f.term(f"br i1 {c}, label %{ci[0]}, label %{rl[0]} ; true_args({cr}, {cc}) ; false_args({cr})")
+    f.switch(ci)
+    ir, ic = ci[1][0][0], ci[1][1][0]
+    aro = f.emit(f"mul {ir}, {lda}")
+    a0 = f.emit(f"add {abase}, {aro}")
+    b0 = f.emit(f"add {col0}, {ic}")
+    f.term(f"br label %{kh[0]} ; args({ir}, {ic}, 0, 0.0, {a0}, {b0})")
+    f.switch(kh)
+    hr, hc, hk, hs, ha, hb = (p for p, _ in kh[1])
+    c = f.emit(f"icmp slt {hk}, {klim}")
+    f.term(f"br i1 {c}, label %{kb[0]}, label %{st[0]} ; true_args({hr}, {hc}, {hk}, {hs}, {ha}, {hb})"
+           f" ; false_args({hr}, {hc}, {hs})")
+    f.switch(kb)
+    br_, bc, bkk, bs, ba, bb = (p for p, _ in kb[1])
+    ap = f.emit(f"getelementptr f32, ptr addrspace(1) %a, i64 {ba}")
+    av = f.emit(f"load f32, ptr addrspace(1) {ap}")
+    bp = f.emit(f"getelementptr f32, ptr addrspace(1) %b, i64 {bb}")
+    bv = f.emit(f"load f32, ptr addrspace(1) {bp}")
+    prod = f.emit(f"fmul {av}, {bv}")
+    ns = f.emit(f"fadd {bs}, {prod}")
+    nk = f.emit(f"add {bkk}, 1")
+    na = f.emit(f"add {ba}, 1")
+    nb = f.emit(f"add {bb}, {ldb}")
+    f.term(f"br label %{kh[0]} ; args({br_}, {bc}, {nk}, {ns}, {na}, {nb})")
+    f.switch(st)
+    sr, scol, ssum = (p for p, _ in st[1])
+    cro = f.emit(f"mul {sr}, {ldc}")
+    crb = f.emit(f"add {cbase}, {cro}")
+    cix = f.emit(f"add {crb}, {scol}")
+    cp = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {cix}")
+    f.stmt(f"store f32 {ssum}, ptr addrspace(1) {cp}")
+    nc = f.emit(f"add {scol}, 1")
+    f.term(f"br label %{ch[0]} ; args({sr}, {nc})")
+    f.switch(rl)
+    nr = f.emit(f"add {rl[1][0][0]}, 1")
+    f.term(f"br label %{rh[0]} ; args({nr})")
+    f.switch(cont)
+    f.term("ret void")
+    return f.text()
+
+
+def mma_program(bm, bn, bk):
+    """c[tile (m, n)] = a[rows of m, :BK] @ b[:BK, cols of n] through tiles:
+    loads of a [BM x BK] and b [BK x BN] (2-D tile loops), a zero
+    accumulator (tile_memory.rs:22-47 fill loop), the MMA nest of
+    tile_compute/mma.rs:25-260 (per cell: sum from acc[row][col], k loop over
+    BK of a[row][k] * b[k][col], store into the result tile), then the
+    store loop into c."""
+    f = _Fn("mma", [("a", 2, 0), ("b", 2, 2), ("c", 2, 4)])
+    sa = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    sb = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2")
+    sc = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 4")
+    m = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    n = f.emit("call i32 @llvm.nvvm.ctaid.y()")
+    ta = f.emit(f"alloca [{bm} x [{bk} x f32]], addrspace(5)")
+    tb = f.emit(f"alloca [{bk} x [{bn} x f32]], addrspace(5)")
+    tacc = f.emit(f"alloca [{bm} x [{bn} x f32]], addrspace(5)")
+    tdst = f.emit(f"alloca [{bm} x [{bn} x f32]], addrspace(5)")
+
+    def origin(desc, rt, ct, rows, cols):
+        rb = f.emit(f"mul {rt}, {rows}")
+        cb = f.emit(f"mul {ct}, {cols}")
+        p = f.emit(f"getelementptr i64, ptr addrspace(4) {desc}, i64 1")
+        stride = f.emit(f"load i64, ptr addrspace(4) {p}")
+        ro = f.emit(f"mul {rb}, {stride}")
+        return f.emit(f"add {ro}, {cb}"), stride
+
+    def load(buf, desc, tile, rows, cols, rt, ct):
+        o, stride = origin(desc, rt, ct, rows, cols)
+
+        def body(r, c):
+            ro = f.emit(f"mul {r}, {stride}")
+            wr = f.emit(f"add {o}, {ro}")
+            i = f.emit(f"add {wr}, {c}")
+            p = f.emit(f"getelementptr f32, ptr addrspace(1) %{buf}, i64 {i}")
+            _tile_store(f, tile, rows, cols, r, c, f.emit(f"load f32, ptr addrspace(1) {p}"))
+        _tile_loop(f, "tile_load", rows, cols, body)
+    load("a", sa, ta, bm, bk, m, 0)
+    load("b", sb, tb, bk, bn, 0, n)
+    _tile_loop(f, "tile_fill", bm, bn, lambda r, c: _tile_store(f, tacc, bm, bn, r, c, "0.0"))
+    # the MMA nest (mma.rs:25-260)
+    rh = f.new_block("tile_mma_row_header", [("loop_row", "i64")])
+    ch = f.new_block("tile_mma_col_header", [("loop_row", "i64"), ("loop_col", "i64")])
+    ib = f.new_block("tile_mma_init", [("loop_row", "i64"), ("loop_col", "i64")])
+    kp = [("loop_row", "i64"), ("loop_col", "i64"), ("loop_k", "i64"), ("loop_sum", "f32")]
+    kh = f.new_block("tile_mma_k_header", kp)
+    kb = f.new_block("tile_mma_k_body", kp)
+    st = f.new_block("tile_mma_store", [("loop_row", "i64"), ("loop_col", "i64"), ("loop_sum", "f32")])
+    rl = f.new_block("tile_mma_row_latch", [("loop_row", "i64")])
+    cont = f.new_block("tile_mma_continue", [])
+    f.term(f"br label %{rh[0]} ; args(0)")
+    f.switch(rh)
+    r = rh[1][0][0]
+    c = f.emit(f"icmp slt {r}, {bm}")
+    f.term(f"br i1 {c}, label %{ch[0]}, label %{cont[0]} ; true_args({r}, 0)")
+    f.switch(ch)
+    cr, cc = ch[1][0][0], ch[1][1][0]
+    c = f.emit(f"icmp slt {cc}, {bn}")
+    f.term(f"br i1 {c}, label %{ib[0]}, label %{rl[0]} ; true_args({cr}, {cc}) ; false_args({cr})")
+    f.switch(ib)
+    ir, ic = ib[1][0][0], ib[1][1][0]
+    s0 = _tile_load(f, tacc, bm, bn, ir, ic)
+    f.term(f"br label %{kh[0]} ; args({ir}, {ic}, 0, {s0})")
+    f.switch(kh)
+    hr, hc, hk, hs = (p for p, _ in kh[1])
+    c = f.emit(f"icmp slt {hk}, {bk}")
+    f.term(f"br i1 {c}, label %{kb[0]}, label %{st[0]} ; true_args({hr}, {hc}, {hk}, {hs})"
+           f" ; false_args({hr}, {hc}, {hs})")
+    f.switch(kb)
+    br_, bc, bkk, bs = (p for p, _ in kb[1])
+    lhs = _tile_load(f, ta, bm, bk, br_, bkk)
+    rhs = _tile_load(f, tb, bk, bn, bkk, bc)
+    prod = f.emit(f"fmul {lhs}, {rhs}")
+    ns = f.emit(f"fadd {bs}, {prod}")
+    nk = f.emit(f"add {bkk}, 1")
+    f.term(f"br label %{kh[0]} ; args({br_}, {bc}, {nk}, {ns})")
+    f.switch(st)
+    sr, scol, ssum = (p for p, _ in st[1])
+    _tile_store(f, tdst, bm, bn, sr, scol, ssum)
+    nc = f.emit(f"add {scol}, 1")
+    f.term(f"br label %{ch[0]} ; args({sr}, {nc})")
+    f.switch(rl)
+    nr = f.emit(f"add {rl[1][0][0]}, 1")
+    f.term(f"br label %{rh[0]} ; args({nr})")
+    f.switch(cont)
+    o, stride = origin(sc, m, n, bm, bn)
+
+    def store_body(r, c):
+        v = _tile_load(f, tdst, bm, bn, r, c)
+        ro = f.emit(f"mul {r}, {stride}")
+        wr = f.emit(f"add {o}, {ro}")
+        i = f.emit(f"add {wr}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {p}")
+    _tile_loop(f, "tile_store", bm, bn, store_body)
+    f.term("ret void")
+    return f.text()

@@ -234,3 +234,65 @@ def test_reference_shaped_vec_add(hip):
         c = _run(hip, kern, [a, b, np.zeros_like(a)], (n // tile, 1, 1))[2]
         np.testing.assert_array_equal(c, a + b)
         kern.close()
+
+
+@pytest.mark.parametrize("bm,bn,bk,m,n,k", [
+    (64, 64, 8, 128, 192, 72),    # 4096 cells a program, nine k tiles
+    (64, 64, 8, 64, 64, 75),      # K truncated to 72 (whole BK tiles)
+    (32, 32, 8, 64, 64, 64),      # the mlp example's gemm tiles
+    (16, 32, 4, 48, 96, 20),      # 512 cells a program
+])
+def test_canonical_matmul_nest(hip, bm, bn, bk, m, n, k):
+    """The canonical matmul's LLIR with its row x column nest spread over the
+    lanes (each cell's k loop serial on one lane): bit for bit the oracle's
+    canonical order."""
+    say(f"llir canonical matmul<{bm}, {bn}, {bk}> {m}x{n}x{k}")
+    kern = hip.LlirKernel(llir_shapes.matmul(bm, bn, bk), (2, bm, bn))
+    r = rng(m + n + k)
+    a = r.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    grid = (m // bm, n // bn, 1)
+    c = _run(hip, kern, [a, b, np.zeros((m, n), np.float32)], (grid[0] * grid[1], 1, 1))[2]
+    want = np.zeros((m, n), np.float32)
+    cpuref.kernel_matmul(a, b, want, grid, bm, bn, bk)
+    assert_same_bits(c, want, what="llir canonical matmul")
+    kern.close()
+
+
+def test_canonical_matmul_nest_in_order_when_rows_overlap(hip):
+    """With ldc < BN the rows of the C tile overlap: the nest then runs in
+    order on lane 0, so the last write of each element is the sequential
+    one (one program, planned on a; numpy restatement of the loops)."""
+    say("llir canonical matmul<32, 32, 8>, ldc 16: the in-order path")
+    kern = hip.LlirKernel(llir_shapes.matmul(32, 32, 8), (0, 32, 16))
+    r = rng(77)
+    a = r.integers(-4, 5, size=(32, 16)).astype(np.float32)
+    b = r.integers(-4, 5, size=(16, 32)).astype(np.float32)
+    c = _run(hip, kern, [a, b, np.zeros((40, 16), np.float32)], (1, 1, 1))[2]
+    want = np.zeros((40, 16), np.float32).ravel()
+    for row in range(32):
+        for col in range(32):
+            s = np.float32(0.0)
+            for kk in range(16):
+                s = np.float32(s + np.float32(a[row, kk] * b[kk, col]))
+            want[row * 16 + col] = s
+    np.testing.assert_array_equal(c.ravel(), want)
+    kern.close()
+
+
+@pytest.mark.parametrize("bm,bn,bk,grid", [(32, 32, 16, (2, 3)), (64, 64, 8, (1, 2)), (16, 16, 32, (3, 2))])
+def test_tile_mma_nest(hip, bm, bn, bk, grid):
+    """Tiles loaded, a zero accumulator, the tile MMA nest (mma.rs) and the
+    store, every nest spread over the lanes: bit for bit the canonical order
+    (sum from 0.0, products rounded, k in order)."""
+    m, n = grid[0] * bm, grid[1] * bn
+    say(f"llir tile mma<{bm}, {bn}, {bk}> {m}x{n}x{bk}")
+    kern = hip.LlirKernel(llir_shapes.mma_program(bm, bn, bk), (2, bm, bn))
+    r = rng(bm * bn + bk)
+    a = r.uniform(-1, 1, size=(m, bk)).astype(np.float32)
+    b = r.uniform(-1, 1, size=(bk, n)).astype(np.float32)
+    c = _run(hip, kern, [a, b, np.zeros((m, n), np.float32)], (grid[0] * grid[1], 1, 1))[2]
+    want = np.zeros((m, n), np.float32)
+    cpuref.kernel_matmul(a, b, want, (*grid, 1), bm, bn, bk)
+    assert_same_bits(c, want, what="llir tile mma")
+    kern.close()

@@ -80,7 +80,10 @@ done:
   ret void
 }
 """, None)
-    body = src[src.index("L_v_body:"):src.index("L_v_done:")]
+    # the body, entered only from its header, runs inside a C loop there
+    body = src[src.index("L_v_loop:"):src.index("L_v_done:")]
+    assert "#pragma unroll 4\n  for (;;) {" in body and "if (!(v_c)) break;" in body
+    assert "L_v_body:" not in src
     # every new value is read before any loop variable is written
     assert "float t1 = v_y;" in body and "float t2 = v_x;" in body
     assert body.index("float t2 = v_x;") < body.index("v_x = t1;") < body.index("v_y = t2;")
@@ -261,8 +264,10 @@ def test_reference_loop_shapes_spread():
     # load, exp, divide and store column loops and the two reduce loops, in
     # the slot form; the row loops stay on every lane
     assert src.count("for (int coop_k = 0; coop_k < 8; ++coop_k) {") == 6
-    # body parameters were replaced by the header's values
+    # body parameters were replaced by the header's values, and the column
+    # header's row (passed the row header's row or itself) by that row
     assert "v_loop_row18" not in src and "v_reduce_acc39" not in src
+    assert "v_loop_row16" not in src
     # x, exp and y tiles are per-lane slices; the [4 x 1] max and sum tiles
     # (read at [row, 0] outside the loops) live in LDS
     for t in ("v_v4", "v_v6", "v_v8"):
@@ -271,7 +276,7 @@ def test_reference_loop_shapes_spread():
         assert f"__shared__ float {t}_storage[4][1];" in src
     # a reduction's element 0 comes from an LDS copy that the lane storing it
     # writes, between barriers around the storing loop
-    assert "if (coop_it == 0LL) v_v4_sh0[v_loop_row16] = v_v27;" in src
+    assert "if (coop_it == 0LL) v_v4_sh0[v_loop_row15] = v_v27;" in src
     assert "v_v34 = &(v_v4_sh0[v_loop_row31]);" in src
     assert "__syncthreads();\n  {\n    const long long coop_start = v_loop_col17;" in src
     # loops of 8 iterations: one program a lane, tiles in registers
@@ -318,3 +323,36 @@ bb0:
     bad = t.replace("i64 0, i64 1\n", "i64 0, i64 0, i64 1\n")
     with pytest.raises(hip.SileError, match="indexes past the array levels"):
         hip.llir_to_hip(bad, None)
+
+
+def test_two_dimensional_nests_spread():
+    """The canonical matmul's row x column nest (canonical_matmul.rs:24-444)
+    and the tile MMA's (tile_compute/mma.rs:25-260) have a region of blocks
+    for a body (cell init, the k loop, the store): iteration row * BN + col
+    runs the region on one lane, the k loop stays serial on it.  A buffer
+    store at `row * ldc + col` spreads when ldc >= BN at run time (lane 0
+    runs the nest in order otherwise); tile-only nests take the slot form,
+    and a tile touched only at [row, col] by nests of its shape is split
+    over the lanes."""
+    mm = hip.llir_to_hip(llir_shapes.matmul(64, 64, 8), (2, 64, 64))
+    assert "__launch_bounds__(1024)" in mm
+    assert "const bool coop_par = true && v_v11 >= 64LL;" in mm
+    assert "v_loop_row19 = coop_it / 64LL; v_loop_col21 = coop_it % 64LL;" in mm
+    assert "goto coop_next0;" in mm and "L_v_matmul_k_header_4_n0:;" in mm
+    # the k loop's carried row and column were the nest's own
+    assert "v_loop_row22" not in mm and "v_loop_col23" not in mm
+    small = hip.llir_to_hip(llir_shapes.matmul(8, 8, 8), (2, 8, 8))   # 64 cells: a lane each
+    assert "__launch_bounds__(64)" in small and "coop_" not in small
+    mma = hip.llir_to_hip(llir_shapes.mma_program(32, 32, 16), (2, 32, 32))
+    assert "__launch_bounds__(1024)" in mma
+    # the accumulator (filled and read at [row, col] by slot-form nests): one
+    # slot a lane; a and b (read at [row, k] / [k, col]) and the result
+    # (read by the guarded store nest) in LDS
+    assert "float v_v8_storage[1];" in mma and "v_v8 = v_v8_storage;" in mma
+    assert "__shared__ float v_v6_storage[32][16];" in mma
+    assert "__shared__ float v_v9_storage[32][32];" in mma
+    assert mma.count("for (int coop_k = 0; coop_k < 1; ++coop_k) {") == 4
+    for t, plan in ((llir_shapes.matmul(64, 64, 8), (2, 64, 64)),
+                    (llir_shapes.mma_program(32, 32, 16), (2, 32, 32))):
+        image, _ = hip.llir_compile(t, plan)
+        assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
