@@ -1069,40 +1069,55 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     plan.loops[L.header] = L;
     plan.bodies.insert(L.body);
   }
-  // 2-D nests whose body is a region of blocks (the reference's tile loops
-  // and its MMA, tile_loops/grid.rs:7-130, tile_compute/mma.rs:25-260):
+  // Nests whose body is a region of blocks (the reference's tile loops and
+  // its MMA, tile_loops/grid.rs:7-130, tile_compute/mma.rs:25-260, and its
+  // column reductions, tile_compute/reduce.rs:160-277):
   //   RH(r): icmp slt r, M; true -> CH(0), false -> X
   //   CH(c): icmp slt c, N; true -> E, false -> RL
   //   RL: r' = r + 1; br RH(r')
   //   E ...: blocks entered only at E from CH and left only by br CH(c + 1)
-  // Iteration f = r N + c of [0, M N) runs the region with (r, c) on lane
-  // f % W; a loop inside the region stays serial on its lane (the MMA's k
-  // loop keeps its order).
-  for (const Block& rh : fn.blocks) {
-    int64_t M = 0, N = 0, z = -1, one = 0;
-    if (rh.params.size() != 1 || rh.insts.size() != 1 || rh.term.kind != "condbr") continue;
-    const std::string rv = rh.params[0].first;
-    const Inst& rc = rh.insts[0];
-    if (rc.op != "cmp" || rc.sub != "slt" || !rc.args[0].is_value || rc.args[0].name != rv ||
-        !const_int(rc.args[1], M) || !rh.term.cond.is_value || rh.term.cond.name != rc.result)
-      continue;
-    const Block* ch = block(rh.term.t);
-    if (!ch || ch == &rh || ch->params.size() != 1 || rh.term.targs.size() != 1 ||
-        !const_int(rh.term.targs[0], z) || z != 0 || ch->insts.size() != 1 ||
-        ch->term.kind != "condbr" || !ch->term.targs.empty() || !ch->term.fargs.empty())
+  // or a column loop alone (M = 1: CH's false edge is the exit).  Iteration
+  // f = r N + c of [0, M N) runs the region with (r, c) on lane f % W; a loop
+  // inside the region stays serial on its lane (the MMA's k loop keeps its
+  // order).  2-D nests first, then lone column loops.
+  for (int pass = 0; pass < 2; ++pass)
+  for (const Block& h : fn.blocks) {
+    int64_t M = 1, N = 0, z = -1, one = 0;
+    const Block* rh = pass == 0 ? &h : nullptr;
+    const Block* ch = pass == 0 ? block(h.term.t) : &h;
+    const Block* rl = nullptr;
+    std::string rv;
+    if (pass == 1) {
+      bool taken = plan.loops.count(h.name) > 0;
+      for (auto& kv : plan.loops)
+        if (kv.second.rows > 0 && kv.second.col_header == h.name) taken = true;
+      if (taken) continue;
+    }
+    if (rh) {
+      if (rh->params.size() != 1 || rh->insts.size() != 1 || rh->term.kind != "condbr") continue;
+      rv = rh->params[0].first;
+      const Inst& rc = rh->insts[0];
+      if (rc.op != "cmp" || rc.sub != "slt" || !rc.args[0].is_value || rc.args[0].name != rv ||
+          !const_int(rc.args[1], M) || !rh->term.cond.is_value || rh->term.cond.name != rc.result)
+        continue;
+      if (!ch || ch == rh || rh->term.targs.size() != 1 || !const_int(rh->term.targs[0], z) || z != 0)
+        continue;
+    }
+    if (!ch || ch->params.size() != 1 || ch->insts.size() != 1 || ch->term.kind != "condbr" ||
+        !ch->term.targs.empty() || (rh && !ch->term.fargs.empty()))
       continue;
     const std::string cv = ch->params[0].first;
     const Inst& cc = ch->insts[0];
     if (cc.op != "cmp" || cc.sub != "slt" || !cc.args[0].is_value || cc.args[0].name != cv ||
         !const_int(cc.args[1], N) || !ch->term.cond.is_value || ch->term.cond.name != cc.result)
       continue;
-    const Block* rl = block(ch->term.f);
     const Block* entry = block(ch->term.t);
-    if (!rl || !entry || rl == entry || rl == &rh || entry == &rh || !entry->params.empty() ||
-        rl->insts.size() != 1 || rl->term.kind != "br" || rl->term.t != rh.name ||
-        rl->term.targs.size() != 1)
-      continue;
-    {
+    if (!entry || !entry->params.empty() || entry == ch || entry == rh) continue;
+    if (rh) {
+      rl = block(ch->term.f);
+      if (!rl || rl == entry || rl == rh || rl->insts.size() != 1 || rl->term.kind != "br" ||
+          rl->term.t != rh->name || rl->term.targs.size() != 1)
+        continue;
       const Inst& a = rl->insts[0];
       if (a.op != "bin" || a.sub != "add" || !a.args[0].is_value || a.args[0].name != rv ||
           !const_int(a.args[1], one) || one != 1 || !rl->term.targs[0].is_value ||
@@ -1110,6 +1125,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
         continue;
     }
     if (M <= 0 || N <= 0 || M * N < kCoopMinTrip) continue;
+    const std::string rh_name = rh ? rh->name : "", rl_name = rl ? rl->name : "";
     // the region: what E reaches without passing CH
     std::set<std::string> region;
     bool ok = true;
@@ -1118,7 +1134,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
       const std::string n = work.back();
       work.pop_back();
       if (region.count(n)) continue;
-      if (n == rh.name || n == rl->name) {
+      if (n == rh_name || n == rl_name || n == ch->name) {
         ok = false;
         break;
       }
@@ -1133,6 +1149,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     }
     if (!ok) continue;
     if (region.size() == 1 && N >= kCoopMinTrip) continue;   // the column loop spreads by itself
+    if (!rh && region.size() == 1) continue;
     // entered only at E from CH; CH reached only from RH (with 0) and from the
     // region with c + 1; RH reached from one place outside (with 0) and RL
     int rh_entries = 0;
@@ -1141,8 +1158,18 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
         if (t.empty()) return;
         if (region.count(t) && !region.count(b.name) && !(b.name == ch->name && t == entry->name))
           ok = false;
-        if (t == ch->name && b.name != rh.name) {
-          if (!region.count(b.name) || args.size() != 1 || !args[0].is_value) {
+        if (t == ch->name && (!rh || b.name != rh_name)) {
+          if (!region.count(b.name)) {
+            if (rh) {
+              ok = false;
+              return;
+            }
+            int64_t s0 = -1;   // a lone column loop: one entry from outside, with 0
+            ++rh_entries;
+            if (args.size() != 1 || !const_int(args[0], s0) || s0 != 0) ok = false;
+            return;
+          }
+          if (args.size() != 1 || !args[0].is_value) {
             ok = false;
             return;
           }
@@ -1153,7 +1180,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
               !const_int(d->second->args[1], inc) || inc != 1)
             ok = false;
         }
-        if (t == rh.name && b.name != rl->name) {
+        if (rh && t == rh_name && b.name != rl_name) {
           int64_t s0 = -1;
           ++rh_entries;
           if (args.size() != 1 || !const_int(args[0], s0) || s0 != 0) ok = false;
@@ -1175,10 +1202,10 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     std::map<std::string, bool> memo;
     std::function<bool(const Operand&)> invariant = [&](const Operand& o) -> bool {
       if (!o.is_value) return true;
-      if (o.name == rv || o.name == cv) return false;
+      if ((!rv.empty() && o.name == rv) || o.name == cv) return false;
       auto it = def_block.find(o.name);
       const std::string db = it == def_block.end() ? "" : it->second;
-      if (db == rh.name || db == ch->name || db == rl->name) return false;
+      if ((rh && db == rh_name) || db == ch->name || (rl && db == rl_name)) return false;
       if (!region.count(db)) return true;
       auto m = memo.find(o.name);
       if (m != memo.end()) return m->second;
@@ -1216,8 +1243,8 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
         }
         if (d.op == "bin" && d.sub == "mul") {
           const Operand* st = nullptr;
-          if (d.args[0].is_value && d.args[0].name == rv) st = &d.args[1];
-          else if (d.args[1].is_value && d.args[1].name == rv) st = &d.args[0];
+          if (!rv.empty() && d.args[0].is_value && d.args[0].name == rv) st = &d.args[1];
+          else if (!rv.empty() && d.args[1].is_value && d.args[1].name == rv) st = &d.args[0];
           if (!st || !invariant(*st)) {
             good = false;
             return;
@@ -1238,9 +1265,12 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
       walk(idx);
       return good && cols_seen == 1 && (rows_seen == 1 || (rows_seen == 0 && M == 1));
     };
+    // a gep to the iteration's element: [r, c], or [0, c] of a lone column loop
     auto row_col_gep = [&](const Inst& g) {
-      return g.args.size() == 3 && g.args[1].is_value && g.args[1].name == rv && g.args[2].is_value &&
-             g.args[2].name == cv;
+      int64_t z0 = -1;
+      const bool row_ok = rv.empty() ? (const_int(g.args[1], z0) && z0 == 0)
+                                     : (g.args[1].is_value && g.args[1].name == rv);
+      return g.args.size() == 3 && row_ok && g.args[2].is_value && g.args[2].name == cv;
     };
     std::vector<std::string> order;
     for (const Block& b : fn.blocks)
@@ -1291,15 +1321,15 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     }
     if (!ok) continue;
     CoopLoop L;
-    L.header = rh.name;
-    L.exit = rh.term.f;
+    L.header = rh ? rh_name : ch->name;
+    L.exit = rh ? rh->term.f : ch->term.f;
     L.iv = cv;
     L.row_iv = rv;
     L.rows = M;
     L.cols = N;
     L.bound = M * N;
     L.col_header = ch->name;
-    L.row_latch = rl->name;
+    L.row_latch = rl_name;
     L.entry = entry->name;
     L.region = order;
     L.guards = guards;
@@ -1323,8 +1353,10 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     }
     for (auto& kv : plan.loops)
       if (kv.second.rows > 0) {
-        plan.bodies.insert(kv.second.col_header);
-        plan.bodies.insert(kv.second.row_latch);
+        if (!kv.second.row_iv.empty()) {   // a 2-D nest (a lone column loop is its own header)
+          plan.bodies.insert(kv.second.col_header);
+          plan.bodies.insert(kv.second.row_latch);
+        }
         for (const std::string& b : kv.second.region) plan.bodies.insert(b);
       }
   }
@@ -1440,11 +1472,26 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
           for (const Inst& x : u.insts) {
             for (size_t k = 0; k < x.args.size(); ++k) {
               if (!x.args[k].is_value || x.args[k].name != in.result) continue;
+              // in a slot-form lone column loop, at [.., col]: column col is
+              // lane col % W's in every such loop and in 1-D spread loops
+              if (L && L->rows > 0 && L->row_iv.empty()) {
+                if (x.op == "gep" && k == 0 && L->slots > 0 && x.args.back().is_value &&
+                    x.args.back().name == L->iv && x.args.size() == adims.size() + 1) {
+                  in_1d = true;
+                  continue;
+                }
+                priv = false;
+                continue;
+              }
               // in a slot-form nest of the tile's shape, at [row, col]
               if (L && L->rows > 0) {
+                int64_t z0 = -1;
+                const bool row_ok = L->row_iv.empty()
+                                        ? (x.args.size() == 3 && const_int(x.args[1], z0) && z0 == 0)
+                                        : (x.args.size() == 3 && x.args[1].is_value &&
+                                           x.args[1].name == L->row_iv);
                 if (x.op == "gep" && k == 0 && L->slots > 0 && adims.size() == 2 &&
-                    adims[0] == L->rows && adims[1] == L->cols && x.args.size() == 3 &&
-                    x.args[1].is_value && x.args[1].name == L->row_iv && x.args[2].is_value &&
+                    adims[0] == L->rows && adims[1] == L->cols && row_ok && x.args[2].is_value &&
                     x.args[2].name == L->iv) {
                   in_nest = true;
                   continue;
@@ -1854,7 +1901,10 @@ struct Emitter {
            "coop_it += coop_par ? "
         << kCoopThreads << "LL : 1LL) {\n";
     }
-    o << "    " << r << " = coop_it / " << n << "; " << c << " = coop_it % " << n << ";\n";
+    if (L.row_iv.empty())
+      o << "    " << c << " = coop_it;\n";
+    else
+      o << "    " << r << " = coop_it / " << n << "; " << c << " = coop_it % " << n << ";\n";
     for (const std::string& b : L.region) relabel[b] = "L_" + ident(b) + "_n" + id;
     relabel[L.col_header] = "coop_next" + id;
     o << "  goto " << relabel[L.entry] << ";\n";
@@ -1872,7 +1922,8 @@ struct Emitter {
     for (const std::string& b : L.region) relabel.erase(b);
     relabel.erase(L.col_header);
     o << "    coop_next" << id << ":;\n    }\n";
-    o << "    " << r << " = " << L.rows << "LL; " << c << " = " << n << ";\n  }\n";
+    if (!L.row_iv.empty()) o << "    " << r << " = " << L.rows << "LL;";
+    o << "    " << c << " = " << n << ";\n  }\n";
     if (L.barrier) o << "  __syncthreads();\n";
     jump(rh.term.f, rh.term.fargs);
   }

@@ -498,3 +498,76 @@ def mma_program(bm, bn, bk):
     _tile_loop(f, "tile_store", bm, bn, store_body)
     f.term("ret void")
     return f.text()
+
+
+def col_reduce(bm, bn, is_max):
+    """out[pid * BN + c] = the reduction over the BM rows of column c of the
+    tile x[0:BM, pid * BN : (pid + 1) * BN] (reduce_max / reduce_sum along
+    axis 0, tile_compute/reduce.rs:160-277: a column loop whose body reads
+    row 0, then a reduce loop over rows 1.., then stores), out rank 1."""
+    f = _Fn("col_reduce", [("x", 2, 0), ("out", 1, 2)])
+    sx = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    pid = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    tx = f.emit(f"alloca [{bm} x [{bn} x f32]], addrspace(5)")
+    tr = f.emit(f"alloca [1 x [{bn} x f32]], addrspace(5)")
+    rb = f.emit(f"mul 0, {bm}")
+    cb = f.emit(f"mul {pid}, {bn}")
+    sp = f.emit(f"getelementptr i64, ptr addrspace(4) {sx}, i64 1")
+    stride = f.emit(f"load i64, ptr addrspace(4) {sp}")
+    ro = f.emit(f"mul {rb}, {stride}")
+    origin = f.emit(f"add {ro}, {cb}")
+
+    def load_body(r, c):
+        rs = f.emit(f"mul {r}, {stride}")
+        wr = f.emit(f"add {origin}, {rs}")
+        i = f.emit(f"add {wr}, {c}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %x, i64 {i}")
+        _tile_store(f, tx, bm, bn, r, c, f.emit(f"load f32, ptr addrspace(1) {p}"))
+    _tile_loop(f, "tile_load", bm, bn, load_body)
+    prefix = "tile_reduce"
+    header = f.new_block(f"{prefix}_col_header", [("loop_col", "i64")])
+    blk = f.new_block(f"{prefix}_col_body", [("loop_col", "i64")])
+    cont = f.new_block(f"{prefix}_continue", [])
+    f.term(f"br label %{header[0]} ; args(0)")
+    f.switch(header)
+    i = header[1][0][0]
+    c = f.emit(f"icmp slt {i}, {bn}")
+    f.term(f"br i1 {c}, label %{blk[0]}, label %{cont[0]} ; true_args({i})")
+    f.switch(blk)
+    col = blk[1][0][0]
+    init = _tile_load(f, tx, bm, bn, 0, col)
+    rh = f.new_block(f"{prefix}_reduce_header", [("reduce_idx", "i64"), ("reduce_acc", "f32")])
+    rbk = f.new_block(f"{prefix}_reduce_body", [("reduce_idx", "i64"), ("reduce_acc", "f32")])
+    rx = f.new_block(f"{prefix}_reduce_exit", [("final_acc", "f32")])
+    f.term(f"br label %{rh[0]} ; args(1, {init})")
+    f.switch(rh)
+    hi, ha = rh[1][0][0], rh[1][1][0]
+    c = f.emit(f"icmp slt {hi}, {bm}")
+    f.term(f"br i1 {c}, label %{rbk[0]}, label %{rx[0]} ; true_args({hi}, {ha}) ; false_args({ha})")
+    f.switch(rbk)
+    bi, ba = rbk[1][0][0], rbk[1][1][0]
+    nxt = _tile_load(f, tx, bm, bn, bi, col)
+    if is_max:
+        gt = f.emit(f"fcmp ogt {nxt}, {ba}")
+        acc = f.emit(f"select i1 {gt}, f32 {nxt}, f32 {ba}")
+    else:
+        acc = f.emit(f"fadd {ba}, {nxt}")
+    ni = f.emit(f"add {bi}, 1")
+    f.term(f"br label %{rh[0]} ; args({ni}, {acc})")
+    f.switch(rx)
+    _tile_store(f, tr, 1, bn, 0, col, rx[1][0][0])
+    nx = f.emit(f"add {col}, 1")
+    f.term(f"br label %{header[0]} ; args({nx})")
+    f.switch(cont)
+
+    def store_body(r, c):
+        v = _tile_load(f, tr, 1, bn, r, c)
+        base = f.emit(f"mul {pid}, {bn}")
+        ro2 = f.emit(f"mul {r}, {bn}")
+        eo = f.emit(f"add {ro2}, {c}")
+        i = f.emit(f"add {base}, {eo}")
+        p = f.emit(f"getelementptr f32, ptr addrspace(1) %out, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {p}")
+    _tile_loop(f, "tile_store", 1, bn, store_body)
+    f.term("ret void")
+    return f.text()

@@ -296,3 +296,25 @@ def test_tile_mma_nest(hip, bm, bn, bk, grid):
     cpuref.kernel_matmul(a, b, want, (*grid, 1), bm, bn, bk)
     assert_same_bits(c, want, what="llir tile mma")
     kern.close()
+
+
+@pytest.mark.parametrize("bm,bn,is_max", [(64, 1024, True), (64, 1024, False), (20, 300, True),
+                                          (33, 512, False)])
+def test_reference_shaped_column_reduce(hip, bm, bn, is_max):
+    """Reductions along axis 0 in the reference's shape (a column a lane,
+    rows folded in order from row 0): bit for bit the left fold, with NaN,
+    -inf and +0 / -0 columns for the max."""
+    say(f"llir column {'max' if is_max else 'sum'} over [{bm}, {bn}] tiles")
+    progs = 3
+    x = rng(bm + bn).normal(size=(bm, bn * progs)).astype(np.float32)
+    if is_max:
+        probe = max_fold_probe_rows(bm, bm + 5)        # rows become columns
+        k = min(probe.shape[0], bn * progs)
+        x[:, :k] = probe[:k].T
+    kern = hip.LlirKernel(llir_shapes.col_reduce(bm, bn, is_max), (1, 1, bn))
+    out = _run(hip, kern, [x, np.full(bn * progs, 7.0, np.float32)], (progs, 1, 1))[1]
+    acc = x[0].copy()
+    for i in range(1, bm):
+        acc = np.where(x[i] > acc, x[i], acc) if is_max else (acc + x[i]).astype(np.float32)
+    assert_same_bits(out, acc.astype(np.float32), what="reference-shaped column reduce")
+    kern.close()

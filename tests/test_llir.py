@@ -356,3 +356,17 @@ def test_two_dimensional_nests_spread():
                     (llir_shapes.mma_program(32, 32, 16), (2, 32, 32))):
         image, _ = hip.llir_compile(t, plan)
         assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+def test_lone_column_loops_with_a_region_spread():
+    """A reduction along axis 0 is a column loop whose body holds a reduce
+    loop over the rows (tile_compute/reduce.rs:160-277): each column runs on
+    one lane (its reduce loop serial, in order); the tile read at [row, col]
+    stays the lane's column slice."""
+    src = hip.llir_to_hip(llir_shapes.col_reduce(64, 1024, True), (1, 1, 1024))
+    assert "__launch_bounds__(1024)" in src
+    assert "    v_loop_col27 = coop_it;\n  goto L_v_tile_reduce_col_body_7_n0;" in src
+    assert "v_v38 = &(v_v3[v_reduce_idx32][coop_k]);" in src
+    assert "float v_v3_storage[64][1];" in src
+    image, _ = hip.llir_compile(llir_shapes.col_reduce(20, 300, False), (1, 1, 300))
+    assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
