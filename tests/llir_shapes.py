@@ -571,3 +571,27 @@ def col_reduce(bm, bn, is_max):
     _tile_loop(f, "tile_store", 1, bn, store_body)
     f.term("ret void")
     return f.text()
+
+
+def vec_add_fused(tile):
+    """vec_add<TILE> as the reference lowers it after fusion (no tile allocas,
+    crates/sile/tests/llvm_ir_lowering.rs:58-78): one column loop loading
+    a and b at pid * TILE + col, adding, storing c."""
+    f = _Fn("vec_add", [("a", 1, 0), ("b", 1, 1), ("c", 1, 2)])
+    pid = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    base = f.emit(f"mul {pid}, {tile}")
+
+    def body(r, c):
+        ro = f.emit(f"mul {r}, {tile}")
+        eo = f.emit(f"add {ro}, {c}")
+        i = f.emit(f"add {base}, {eo}")
+        pa = f.emit(f"getelementptr f32, ptr addrspace(1) %a, i64 {i}")
+        va = f.emit(f"load f32, ptr addrspace(1) {pa}")
+        pb = f.emit(f"getelementptr f32, ptr addrspace(1) %b, i64 {i}")
+        vb = f.emit(f"load f32, ptr addrspace(1) {pb}")
+        s = f.emit(f"fadd {va}, {vb}")
+        pc = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {i}")
+        f.stmt(f"store f32 {s}, ptr addrspace(1) {pc}")
+    _tile_loop(f, "tile_map", 1, tile, body)
+    f.term("ret void")
+    return f.text()

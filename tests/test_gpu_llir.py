@@ -225,10 +225,12 @@ def test_reference_shaped_row_max_is_bit_exact(hip, bn):
     kern.close()
 
 
-def test_reference_shaped_vec_add(hip):
-    say("llir reference-shaped vec_add<4096> and <8>")
+@pytest.mark.parametrize("fused", [False, True])
+def test_reference_shaped_vec_add(hip, fused):
+    say(f"llir reference-shaped vec_add<4096> and <8>, fused={fused}")
+    gen = llir_shapes.vec_add_fused if fused else llir_shapes.vec_add
     for tile, n in ((4096, 1 << 16), (8, 4096)):
-        kern = hip.LlirKernel(llir_shapes.vec_add(tile), (2, 1, tile))
+        kern = hip.LlirKernel(gen(tile), (2, 1, tile))
         a = rng(tile).integers(-1000, 1000, n).astype(np.float32)
         b = rng(tile + 1).integers(-1000, 1000, n).astype(np.float32)
         c = _run(hip, kern, [a, b, np.zeros_like(a)], (n // tile, 1, 1))[2]

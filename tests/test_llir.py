@@ -285,6 +285,8 @@ def test_reference_loop_shapes_spread():
     assert "float (*v_v4)[8] = v_v4_storage;" in small
     va = hip.llir_to_hip(llir_shapes.vec_add(4096), (2, 1, 4096))
     assert "__launch_bounds__(1024)" in va and va.count("coop_k < 4;") == 4
+    fused = hip.llir_to_hip(llir_shapes.vec_add_fused(4096), (2, 1, 4096))
+    assert "__launch_bounds__(1024)" in fused and fused.count("coop_k < 4;") == 1
     rm = hip.llir_to_hip(llir_shapes.row_max(4096), (1, 1, 1))
     assert "coop_wg_first_max" in rm and "v_v3_sh0" in rm
     for t, plan in ((llir_shapes.softmax(4, 8192), (1, 4, 8192)), (llir_shapes.softmax(1, 1000), (1, 1, 1000)),
