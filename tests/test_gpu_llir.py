@@ -282,7 +282,8 @@ def test_canonical_matmul_nest_in_order_when_rows_overlap(hip):
     kern.close()
 
 
-@pytest.mark.parametrize("bm,bn,bk,grid", [(32, 32, 16, (2, 3)), (64, 64, 8, (1, 2)), (16, 16, 32, (3, 2))])
+@pytest.mark.parametrize("bm,bn,bk,grid", [(32, 32, 16, (2, 3)), (64, 64, 8, (1, 2)), (16, 16, 32, (3, 2)),
+                                          (48, 32, 8, (2, 2))])   # 1536 cells: a partial second slot
 def test_tile_mma_nest(hip, bm, bn, bk, grid):
     """Tiles loaded, a zero accumulator, the tile MMA nest (mma.rs) and the
     store, every nest spread over the lanes: bit for bit the canonical order
