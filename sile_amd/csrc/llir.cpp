@@ -777,6 +777,7 @@ struct CoopCache {
   std::string buf, inv;   // inv "" for an index of iv alone
   int64_t slots = 0;
   Type ty;                // the loaded value's type
+  int64_t lo = 0, hi = 0; // the iterations the filling loop runs (constants)
 };
 struct CoopLoop {
   std::string header, body, exit;
@@ -1421,7 +1422,7 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
           const int c = (int)plan.caches.size();
           auto ti = types.find(in.result);
           if (ti == types.end()) continue;
-          plan.caches.push_back(CoopCache{buf, inv, L.slots, ti->second});
+          plan.caches.push_back(CoopCache{buf, inv, L.slots, ti->second, L.start, L.bound});
           key_cache[key] = c;
           L.cached[in.result] = CoopCacheUse{c, true};
         } else if (!L.cached.count(in.result)) {
@@ -1735,7 +1736,8 @@ struct Emitter {
           o << "  " << r << " = *(" << opnd(a[0]) << ");\n";
           o << "  coop_cache" << c << "[coop_k] = " << r << ";\n";
         } else {
-          o << "  if (coop_ok" << c << " && coop_it >= coop_lo" << c << " && coop_it < coop_hi" << c
+          const CoopCache& cc = coop.caches[cu->second.cache];
+          o << "  if (coop_ok" << c << " && coop_it >= " << cc.lo << " && coop_it < " << cc.hi
             << ") " << r << " = coop_cache" << c << "[coop_k]; else " << r << " = *(" << opnd(a[0])
             << ");\n";
         }
@@ -1946,9 +1948,10 @@ struct Emitter {
       if (f.kind == 0) continue;  // unchanged by the loop
       o << "    const float coop_init" << ks << " = " << c << ";\n";
       if (f.kind == 1) o << "    float coop_p" << ks << " = -0.0f;\n";
-      if (f.kind == 2)
-        o << "    float coop_p" << ks << " = -__builtin_inff(); long long coop_i" << ks
-          << " = LLONG_MAX;\n";
+      if (f.kind == 2)   // the partial's first iteration: 32-bit in the slot form
+        o << "    float coop_p" << ks << " = -__builtin_inff(); "
+          << (L.slots > 0 ? "int coop_i" + ks + " = INT_MAX;\n"
+                          : "long long coop_i" + ks + " = LLONG_MAX;\n");
     }
     if (L.slots > 0) {
       // slot form: iteration k W + l on lane l, fully unrolled (compile-time
@@ -1959,8 +1962,7 @@ struct Emitter {
         const CoopCache& cc = coop.caches[c];
         const std::string cs = std::to_string(c);
         o << "    coop_has" << cs << " = true; coop_tag" << cs << " = "
-          << (cc.inv.empty() ? std::string("0") : "(long long)" + ident(cc.inv)) << "; coop_lo" << cs
-          << " = coop_start; coop_hi" << cs << " = " << bd << "LL;\n";
+          << (cc.inv.empty() ? std::string("0") : "(long long)" + ident(cc.inv)) << ";\n";
       }
       for (int c : uses) {
         const CoopCache& cc = coop.caches[c];
@@ -1968,11 +1970,17 @@ struct Emitter {
         o << "    const bool coop_ok" << cs << " = coop_has" << cs << " && coop_tag" << cs << " == "
           << (cc.inv.empty() ? std::string("0") : "(long long)" + ident(cc.inv)) << ";\n";
       }
+      // the iteration, checked against the loop's constant start and bound
+      // only where a slot can cross them
       o << "#pragma unroll\n";
       o << "    for (int coop_k = 0; coop_k < " << L.slots << "; ++coop_k) {\n";
       o << "    const long long coop_it = (long long)coop_k * " << kCoopThreads
         << "LL + (long long)threadIdx.x;\n";
-      o << "    if (coop_it < coop_start || coop_it >= " << bd << "LL) continue;\n";
+      std::string skip;
+      if (L.start > 0) skip = "coop_it < " + std::to_string(L.start) + "LL";
+      if (L.slots * kCoopThreads > L.bound)
+        skip += (skip.empty() ? "" : " || ") + std::string("coop_it >= ") + bd + "LL";
+      if (!skip.empty()) o << "    if (" << skip << ") continue;\n";
     } else {
       // unrolled, so a lane has several iterations' loads in flight
       o << "#pragma unroll 8\n";
@@ -1990,7 +1998,9 @@ struct Emitter {
     in_loop = nullptr;
     for (size_t k = 0; k < L.folds.size(); ++k) {
       const CoopFold& f = L.folds[k];
-      if (f.kind == 2) o << "    if (" << ident(f.cond) << ") coop_i" << k << " = coop_it;\n";
+      if (f.kind == 2)
+        o << "    if (" << ident(f.cond) << ") coop_i" << k << " = "
+          << (L.slots > 0 ? "(int)coop_it" : "coop_it") << ";\n";
       if (f.kind != 0) o << "    coop_p" << k << " = " << ident(f.next) << ";\n";
     }
     o << "    }\n";
@@ -2003,8 +2013,8 @@ struct Emitter {
         o << "    " << c << " = coop_init" << ks << " + coop_wg_sum(coop_p" << ks
           << ", coop_red_v, coop_rb);\n";
       } else {
-        o << "    coop_wg_first_max(coop_p" << ks << ", coop_i" << ks
-          << ", coop_red_v, coop_red_i, coop_rb);\n";
+        o << "    coop_wg_first_max(coop_p" << ks << ", coop_i" << ks << ", coop_red_v, "
+          << (L.slots > 0 ? "coop_red_j" : "coop_red_i") << ", coop_rb);\n";
         o << "    " << c << " = coop_p" << ks << " > coop_init" << ks << " ? coop_p" << ks
           << " : coop_init" << ks << ";\n";
       }
@@ -2084,12 +2094,12 @@ struct Emitter {
     if (coop.on)
       o << "  __shared__ float coop_red_v[2 * COOP_WAVES];\n"
            "  __shared__ long long coop_red_i[2 * COOP_WAVES];\n"
+           "  __shared__ int coop_red_j[2 * COOP_WAVES];\n"
            "  int coop_rb = 0;\n";
     for (size_t c = 0; c < coop.caches.size(); ++c) {
       const std::string cs = std::to_string(c);
       o << "  " << c_scalar(coop.caches[c].ty) << " coop_cache" << cs << "[" << coop.caches[c].slots
-        << "];\n  bool coop_has" << cs << " = false;\n  long long coop_tag" << cs << " = 0, coop_lo"
-        << cs << " = 0, coop_hi" << cs << " = 0;\n";
+        << "];\n  bool coop_has" << cs << " = false;\n  long long coop_tag" << cs << " = 0;\n";
     }
     std::set<std::string> spread_headers;   // spread loops' and nests' own headers
     for (auto& kv : coop.loops) {
@@ -2132,7 +2142,11 @@ struct Emitter {
       last_buf = &p;
     }
     const int threads = coop.on ? kCoopThreads : 64;
-    o << "extern \"C\" __global__ __launch_bounds__(" << threads << ") void sile_kernel_" << fn.name
+    // one program per workgroup: ask for two workgroups per CU (8 waves per
+    // SIMD, every wave slot: at most 64 VGPRs), so one program's loads overlap
+    // the other's folds and barriers
+    o << "extern \"C\" __global__ __launch_bounds__(" << threads << ") "
+      << (coop.on ? "__attribute__((amdgpu_waves_per_eu(8))) " : "") << "void sile_kernel_" << fn.name
       << "(void** buffers, long long num_programs, const long long* shapes, long long num_shapes) {\n";
     if (coop.on)
       o << "  const long long sile_pid = (long long)blockIdx.x;  // one workgroup per program\n";
@@ -2214,15 +2228,20 @@ struct Emitter {
       // read, which every wave finished reading before it passed the last
       // fold's barrier, so no barrier is needed before the write.
       o << "#ifndef LLONG_MAX\n#define LLONG_MAX 9223372036854775807LL\n#endif\n"
+           "#ifndef INT_MAX\n#define INT_MAX 2147483647\n#endif\n"
         << "#define COOP_WAVES " << kCoopThreads / 64 << "\n"
         << "template <int C> __device__ static inline float coop_dpp_f(float v) {\n"
            "  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xF, 0xF, false));\n}\n"
+           "template <int C> __device__ static inline int coop_dpp_i(int v) {\n"
+           "  return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false);\n}\n"
            "template <int C> __device__ static inline long long coop_dpp_i(long long v) {\n"
            "  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)v, C, 0xF, 0xF, false);\n"
            "  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)((unsigned long long)v >> 32), C, 0xF, 0xF, false);\n"
            "  return (long long)(((unsigned long long)hi << 32) | lo);\n}\n"
            "__device__ static inline float coop_lane_f(float v, int l) {\n"
            "  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));\n}\n"
+           "__device__ static inline int coop_lane_i(int v, int l) {\n"
+           "  return __builtin_amdgcn_readlane(v, l);\n}\n"
            "__device__ static inline long long coop_lane_i(long long v, int l) {\n"
            "  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);\n"
            "  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)((unsigned long long)v >> 32), l);\n"
@@ -2241,19 +2260,19 @@ struct Emitter {
            "#pragma unroll\n"
            "  for (int w = 1; w < COOP_WAVES; ++w) s += r[w];\n"
            "  return s;\n}\n"
-           "__device__ static void coop_merge(float& v, long long& i, float ov, long long oi) {\n"
+           "template <class I> __device__ static void coop_merge(float& v, I& i, float ov, I oi) {\n"
            "  const bool take = ov > v || (ov == v && oi < i);\n"
            "  v = take ? ov : v; i = take ? oi : i;\n}\n"
-           "__device__ static void coop_wg_first_max(float& v, long long& i, float* rv, long long* ri, int& rb) {\n"
+           "template <class I> __device__ static void coop_wg_first_max(float& v, I& i, float* rv, I* ri, int& rb) {\n"
            "  coop_merge(v, i, coop_dpp_f<0xB1>(v), coop_dpp_i<0xB1>(i));\n"
            "  coop_merge(v, i, coop_dpp_f<0x4E>(v), coop_dpp_i<0x4E>(i));\n"
            "  coop_merge(v, i, coop_dpp_f<0x141>(v), coop_dpp_i<0x141>(i));\n"
            "  coop_merge(v, i, coop_dpp_f<0x140>(v), coop_dpp_i<0x140>(i));\n"
            "  float wv = coop_lane_f(v, 0);\n"
-           "  long long wi = coop_lane_i(i, 0);\n"
+           "  I wi = coop_lane_i(i, 0);\n"
            "  for (int l = 16; l < 64; l += 16) coop_merge(wv, wi, coop_lane_f(v, l), coop_lane_i(i, l));\n"
            "  float* r = rv + rb * COOP_WAVES;\n"
-           "  long long* q = ri + rb * COOP_WAVES;\n"
+           "  I* q = ri + rb * COOP_WAVES;\n"
            "  rb ^= 1;\n"
            "  if ((threadIdx.x & 63) == 0) { r[threadIdx.x >> 6] = wv; q[threadIdx.x >> 6] = wi; }\n"
            "  __syncthreads();\n"

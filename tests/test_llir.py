@@ -190,6 +190,9 @@ def test_long_loops_spread_over_the_workgroup():
     # form (iteration k W + l on lane l, fully unrolled)
     assert src.count("for (int coop_k = 0; coop_k < 8; ++coop_k) {") == 3
     assert src.count("const long long coop_it = (long long)coop_k * 1024LL + (long long)threadIdx.x;") == 3
+    # bounds checked only where a slot can cross them: the max loop starts at 1
+    assert src.count("if (coop_it < 1LL) continue;") == 1 and "coop_it >= 8192" not in src
+    assert "int coop_i0 = INT_MAX;" in src and "coop_red_j, coop_rb);" in src
     assert "coop_wg_first_max(coop_p0, coop_i0" in src        # the max fold, from x0
     assert "v_sum = coop_init1 + coop_wg_sum(coop_p1" in src or \
            "v_sum = coop_init0 + coop_wg_sum(coop_p0" in src  # the sum of exp
@@ -200,7 +203,8 @@ def test_long_loops_spread_over_the_workgroup():
     # loop takes them (its iteration 0, which the max loop starting at 1 did
     # not run, loads)
     assert "coop_cache0[coop_k] = v_xv;" in src
-    assert ("if (coop_ok0 && coop_it >= coop_lo0 && coop_it < coop_hi0) v_xev = coop_cache0[coop_k]; "
+    # (the max loop ran iterations 1 .. 8191: constants the unrolled slots fold)
+    assert ("if (coop_ok0 && coop_it >= 1 && coop_it < 8192) v_xev = coop_cache0[coop_k]; "
             "else v_xev = *(v_xep);") in src
     assert "coop_tag0 = (long long)v_xrow;" in src and "coop_tag0 == (long long)v_xrow;" in src
     # past 16 iterations a lane: the strided form, tiles sliced by e / W, no cache
