@@ -80,13 +80,8 @@ class _Fn:
         return "\n".join(out) + "\n"
 
 
-def _args(vals):
-    return ", ".join(str(v) for v in vals)
-
-
 def _tile_loop(f, prefix, rows, cols, body):
     """lower_nested_tile_loop: body(row, col) appends the body's instructions."""
-    cont = None
     if rows == 1 or cols == 1:
         axis = "col" if rows == 1 else "row"
         n = cols if rows == 1 else rows
