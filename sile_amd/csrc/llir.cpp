@@ -2419,6 +2419,49 @@ bool drop_trivial_params(Function& fn) {
   return any;
 }
 
+// The printed form gives a pointer block parameter no pointee (`ptr
+// addrspace(5)`), but the reference's lowering passes tiles between blocks
+// that way (a tile carried through a loop).  A gep on the parameter names
+// the tile type; the parameter takes it, so it is declared as the tile
+// pointer the backends' C form uses (`float (*)[C]`) and its geps index the
+// tile's dimensions.
+// A parameter also takes the pointee of a value an edge passes it (the
+// alloca a loop starts from).
+void type_pointer_params(Function& fn, std::map<std::string, Type>& types) {
+  std::map<std::string, Type> pointee;
+  for (const Block& b : fn.blocks)
+    for (const Inst& in : b.insts)
+      if (in.op == "gep" && in.args[0].is_value && in.aux.k == TK::Arr)
+        pointee.emplace(in.args[0].name, in.aux);
+  for (bool changed = true; changed;) {
+    changed = false;
+    for (Block& b : fn.blocks)
+      for (size_t k = 0; k < b.params.size(); ++k) {
+        auto& p = b.params[k];
+        if (p.second.k != TK::Ptr || p.second.elem) continue;
+        std::shared_ptr<Type> e;
+        auto it = pointee.find(p.first);
+        if (it != pointee.end()) e = std::make_shared<Type>(it->second);
+        for (const Block& src : fn.blocks) {
+          auto from = [&](const std::string& t, const std::vector<Operand>& args) {
+            if (e || t != b.name || k >= args.size() || !args[k].is_value) return;
+            auto ti = types.find(args[k].name);
+            if (ti != types.end() && ti->second.k == TK::Ptr && ti->second.elem) e = ti->second.elem;
+          };
+          if (src.term.kind == "br") from(src.term.t, src.term.targs);
+          if (src.term.kind == "condbr") {
+            from(src.term.t, src.term.targs);
+            from(src.term.f, src.term.fargs);
+          }
+        }
+        if (!e) continue;
+        p.second.elem = e;
+        types[p.first] = p.second;
+        changed = true;
+      }
+  }
+}
+
 // parse + emit; returns a status and fills `src` / the last error
 int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::string& src,
            std::string& name) {
@@ -2431,6 +2474,7 @@ int to_hip(const char* text, int64_t plan_out, int64_t rows, int64_t cols, std::
     verify(p.fn);
     do forward_block_args(p.fn);
     while (drop_trivial_params(p.fn));
+    type_pointer_params(p.fn, p.types);
     const CoopPlan coop = plan_coop(p.fn, p.types);
     Emitter e{p.fn, p.types, coop, {}};
     src = e.emit(plan_out, rows, cols);

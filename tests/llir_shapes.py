@@ -590,3 +590,248 @@ def vec_add_fused(tile):
     _tile_loop(f, "tile_map", 1, tile, body)
     f.term("ret void")
     return f.text()
+
+
+def fused_mma_loop(bm, bn, bk):
+    """c[tile (m, n)] = sum over K tiles of a[rows, k tile] @ b[k tile, cols],
+    with the accumulator tile carried through the K-tile loop as a block
+    parameter (a pointer) and the MMA fused with its loads
+    (tile_compute/mma.rs:262-739: per cell, the first K tile starts from the
+    splat 0.0, later ones from the accumulator; the k loop reads a and b from
+    their buffers; the cell's sum goes back into the accumulator), then the
+    store loop into c.  K = lda, whole BK tiles."""
+    f = _Fn("fused_mma", [("a", 2, 0), ("b", 2, 2), ("c", 2, 4)])
+    sa = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    sb = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2")
+    sc = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 4")
+    m = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    n = f.emit("call i32 @llvm.nvvm.ctaid.y()")
+
+    def dim1(desc):
+        p = f.emit(f"getelementptr i64, ptr addrspace(4) {desc}, i64 1")
+        return f.emit(f"load i64, ptr addrspace(4) {p}")
+    lda, ldb, ldc = dim1(sa), dim1(sb), dim1(sc)
+    ktiles = f.emit(f"sdiv {lda}, {bk}")
+    acc0 = f.emit(f"alloca [{bm} x [{bn} x f32]], addrspace(5)")
+    tty = f"[{bm} x [{bn} x f32]]"
+    lh = f.new_block("loop_header", [("kt", "i64"), ("acc", "ptr addrspace(5)")])
+    lb = f.new_block("loop_body", [("kt", "i64"), ("acc", "ptr addrspace(5)")])
+    lx = f.new_block("loop_exit", [("acc", "ptr addrspace(5)")])
+    f.term(f"br label %{lh[0]} ; args(0, {acc0})")
+    f.switch(lh)
+    kt, acc = lh[1][0][0], lh[1][1][0]
+    c = f.emit(f"icmp slt {kt}, {ktiles}")
+    f.term(f"br i1 {c}, label %{lb[0]}, label %{lx[0]} ; true_args({kt}, {acc}) ; false_args({acc})")
+    f.switch(lb)
+    bkt, bacc = lb[1][0][0], lb[1][1][0]
+    # tile origins (compute_rank2_tile_origin, mma.rs:741-784)
+    arb = f.emit(f"mul {m}, {bm}")
+    acb = f.emit(f"mul {bkt}, {bk}")
+    aro = f.emit(f"mul {arb}, {lda}")
+    aorg = f.emit(f"add {aro}, {acb}")
+    brb = f.emit(f"mul {bkt}, {bk}")
+    bcb = f.emit(f"mul {n}, {bn}")
+    bro = f.emit(f"mul {brb}, {ldb}")
+    borg = f.emit(f"add {bro}, {bcb}")
+    rh = f.new_block("tile_mma_row_header", [("loop_row", "i64")])
+    ch = f.new_block("tile_mma_col_header", [("loop_row", "i64"), ("loop_col", "i64")])
+    ib = f.new_block("tile_mma_init", [("loop_row", "i64"), ("loop_col", "i64")])
+    zp = [("loop_row", "i64"), ("loop_col", "i64"), ("loop_a_index", "i64"), ("loop_b_index", "i64")]
+    zb = f.new_block("tile_mma_init_zero", zp)
+    ldb_ = f.new_block("tile_mma_init_load", zp)
+    kp = [("loop_row", "i64"), ("loop_col", "i64"), ("loop_k", "i64"), ("loop_sum", "f32"),
+          ("loop_a_index", "i64"), ("loop_b_index", "i64")]
+    kh = f.new_block("tile_mma_k_header", kp)
+    kb = f.new_block("tile_mma_k_body", kp)
+    st = f.new_block("tile_mma_store", [("loop_row", "i64"), ("loop_col", "i64"), ("loop_sum", "f32")])
+    rl = f.new_block("tile_mma_row_latch", [("loop_row", "i64")])
+    cont = f.new_block("tile_mma_continue", [])
+    f.term(f"br label %{rh[0]} ; args(0)")
+    f.switch(rh)
+    r = rh[1][0][0]
+    c = f.emit(f"icmp slt {r}, {bm}")
+    f.term(f"br i1 {c}, label %{ch[0]}, label %{cont[0]} ; true_args({r}, 0)")
+    f.switch(ch)
+    cr, cc = ch[1][0][0], ch[1][1][0]
+    c = f.emit(f"icmp slt {cc}, {bn}")
+    f.term(f"br i1 {c}, label %{ib[0]}, label %{rl[0]} ; true_args({cr}, {cc}) ; false_args({cr})")
+    f.switch(ib)
+    ir, ic = ib[1][0][0], ib[1][1][0]
+    aro2 = f.emit(f"mul {ir}, {lda}")
+    a0 = f.emit(f"add {aorg}, {aro2}")
+    b0 = f.emit(f"add {borg}, {ic}")
+    first = f.emit(f"icmp eq {bkt}, 0")
+    f.term(f"br i1 {first}, label %{zb[0]}, label %{ldb_[0]} ; true_args({ir}, {ic}, {a0}, {b0})"
+           f" ; false_args({ir}, {ic}, {a0}, {b0})")
+    f.switch(zb)
+    zr, zc, za, zbi = (p for p, _ in zb[1])
+    f.term(f"br label %{kh[0]} ; args({zr}, {zc}, 0, 0.0, {za}, {zbi})")
+    f.switch(ldb_)
+    lr, lc, la, lbi = (p for p, _ in ldb_[1])
+    gp = f.emit(f"getelementptr {tty}, ptr addrspace(5) {bacc}, i64 {lr}, i64 {lc}")
+    s0 = f.emit(f"load f32, ptr addrspace(5) {gp}")
+    f.term(f"br label %{kh[0]} ; args({lr}, {lc}, 0, {s0}, {la}, {lbi})")
+    f.switch(kh)
+    hr, hc, hk, hs, ha, hb = (p for p, _ in kh[1])
+    c = f.emit(f"icmp slt {hk}, {bk}")
+    f.term(f"br i1 {c}, label %{kb[0]}, label %{st[0]} ; true_args({hr}, {hc}, {hk}, {hs}, {ha}, {hb})"
+           f" ; false_args({hr}, {hc}, {hs})")
+    f.switch(kb)
+    br_, bc, bkk, bs, ba, bb = (p for p, _ in kb[1])
+    ap = f.emit(f"getelementptr f32, ptr addrspace(1) %a, i64 {ba}")
+    av = f.emit(f"load f32, ptr addrspace(1) {ap}")
+    bp = f.emit(f"getelementptr f32, ptr addrspace(1) %b, i64 {bb}")
+    bv = f.emit(f"load f32, ptr addrspace(1) {bp}")
+    prod = f.emit(f"fmul {av}, {bv}")
+    ns = f.emit(f"fadd {bs}, {prod}")
+    nk = f.emit(f"add {bkk}, 1")
+    na = f.emit(f"add {ba}, 1")
+    nb = f.emit(f"add {bb}, {ldb}")
+    f.term(f"br label %{kh[0]} ; args({br_}, {bc}, {nk}, {ns}, {na}, {nb})")
+    f.switch(st)
+    sr, scol, ssum = (p for p, _ in st[1])
+    dp = f.emit(f"getelementptr {tty}, ptr addrspace(5) {bacc}, i64 {sr}, i64 {scol}")
+    f.stmt(f"store f32 {ssum}, ptr addrspace(5) {dp}")
+    nc = f.emit(f"add {scol}, 1")
+    f.term(f"br label %{ch[0]} ; args({sr}, {nc})")
+    f.switch(rl)
+    nr = f.emit(f"add {rl[1][0][0]}, 1")
+    f.term(f"br label %{rh[0]} ; args({nr})")
+    f.switch(cont)
+    nkt = f.emit(f"add {bkt}, 1")
+    f.term(f"br label %{lh[0]} ; args({nkt}, {bacc})")
+    f.switch(lx)
+    xacc = lx[1][0][0]
+    crb = f.emit(f"mul {m}, {bm}")
+    ccb = f.emit(f"mul {n}, {bn}")
+    cro = f.emit(f"mul {crb}, {ldc}")
+    corg = f.emit(f"add {cro}, {ccb}")
+
+    def store_body(r, c):
+        p = f.emit(f"getelementptr {tty}, ptr addrspace(5) {xacc}, i64 {r}, i64 {c}")
+        v = f.emit(f"load f32, ptr addrspace(5) {p}")
+        ro = f.emit(f"mul {r}, {ldc}")
+        wr = f.emit(f"add {corg}, {ro}")
+        i = f.emit(f"add {wr}, {c}")
+        q = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {q}")
+    _tile_loop(f, "tile_store", bm, bn, store_body)
+    f.term("ret void")
+    return f.text()
+
+
+def mma_k_loop(bm, bn, bk):
+    """The unfused form of a K-tile loop: the accumulator tile is a block
+    parameter (a pointer) that starts at a zero-filled tile and is then the
+    MMA's result tile: each iteration loads a [BM x BK] and b [BK x BN] tiles
+    (2-D tile loops), runs the MMA nest of mma.rs:25-260 from acc into the
+    result tile, and carries the result; the exit stores it into c."""
+    f = _Fn("mma_k_loop", [("a", 2, 0), ("b", 2, 2), ("c", 2, 4)])
+    sa = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 0")
+    sb = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 2")
+    sc = f.emit("getelementptr i64, ptr addrspace(4) %__sile_shapes, i64 4")
+    m = f.emit("call i32 @llvm.nvvm.ctaid.x()")
+    n = f.emit("call i32 @llvm.nvvm.ctaid.y()")
+
+    def dim1(desc):
+        p = f.emit(f"getelementptr i64, ptr addrspace(4) {desc}, i64 1")
+        return f.emit(f"load i64, ptr addrspace(4) {p}")
+    lda, ldb, ldc = dim1(sa), dim1(sb), dim1(sc)
+    ktiles = f.emit(f"sdiv {lda}, {bk}")
+    tty = f"[{bm} x [{bn} x f32]]"
+    ta = f.emit(f"alloca [{bm} x [{bk} x f32]], addrspace(5)")
+    tb = f.emit(f"alloca [{bk} x [{bn} x f32]], addrspace(5)")
+    t0 = f.emit(f"alloca {tty}, addrspace(5)")
+    td = f.emit(f"alloca {tty}, addrspace(5)")
+    _tile_loop(f, "tile_fill", bm, bn, lambda r, c: _tile_store(f, t0, bm, bn, r, c, "0.0"))
+    lh = f.new_block("loop_header", [("kt", "i64"), ("acc", "ptr addrspace(5)")])
+    lb = f.new_block("loop_body", [("kt", "i64"), ("acc", "ptr addrspace(5)")])
+    lx = f.new_block("loop_exit", [("acc", "ptr addrspace(5)")])
+    f.term(f"br label %{lh[0]} ; args(0, {t0})")
+    f.switch(lh)
+    kt, acc = lh[1][0][0], lh[1][1][0]
+    c = f.emit(f"icmp slt {kt}, {ktiles}")
+    f.term(f"br i1 {c}, label %{lb[0]}, label %{lx[0]} ; true_args({kt}, {acc}) ; false_args({acc})")
+    f.switch(lb)
+    bkt, bacc = lb[1][0][0], lb[1][1][0]
+
+    def load(buf, tile, rows, cols, rt, ct, stride):
+        rb = f.emit(f"mul {rt}, {rows}")
+        cb = f.emit(f"mul {ct}, {cols}")
+        ro = f.emit(f"mul {rb}, {stride}")
+        o = f.emit(f"add {ro}, {cb}")
+
+        def body(r, c):
+            rs = f.emit(f"mul {r}, {stride}")
+            wr = f.emit(f"add {o}, {rs}")
+            i = f.emit(f"add {wr}, {c}")
+            p = f.emit(f"getelementptr f32, ptr addrspace(1) %{buf}, i64 {i}")
+            _tile_store(f, tile, rows, cols, r, c, f.emit(f"load f32, ptr addrspace(1) {p}"))
+        _tile_loop(f, "tile_load", rows, cols, body)
+    load("a", ta, bm, bk, m, bkt, lda)
+    load("b", tb, bk, bn, bkt, n, ldb)
+    rh = f.new_block("tile_mma_row_header", [("loop_row", "i64")])
+    ch = f.new_block("tile_mma_col_header", [("loop_row", "i64"), ("loop_col", "i64")])
+    ib = f.new_block("tile_mma_init", [("loop_row", "i64"), ("loop_col", "i64")])
+    kp = [("loop_row", "i64"), ("loop_col", "i64"), ("loop_k", "i64"), ("loop_sum", "f32")]
+    kh = f.new_block("tile_mma_k_header", kp)
+    kb = f.new_block("tile_mma_k_body", kp)
+    st = f.new_block("tile_mma_store", [("loop_row", "i64"), ("loop_col", "i64"), ("loop_sum", "f32")])
+    rl = f.new_block("tile_mma_row_latch", [("loop_row", "i64")])
+    cont = f.new_block("tile_mma_continue", [])
+    f.term(f"br label %{rh[0]} ; args(0)")
+    f.switch(rh)
+    r = rh[1][0][0]
+    c = f.emit(f"icmp slt {r}, {bm}")
+    f.term(f"br i1 {c}, label %{ch[0]}, label %{cont[0]} ; true_args({r}, 0)")
+    f.switch(ch)
+    cr, cc = ch[1][0][0], ch[1][1][0]
+    c = f.emit(f"icmp slt {cc}, {bn}")
+    f.term(f"br i1 {c}, label %{ib[0]}, label %{rl[0]} ; true_args({cr}, {cc}) ; false_args({cr})")
+    f.switch(ib)
+    ir, ic = ib[1][0][0], ib[1][1][0]
+    gp = f.emit(f"getelementptr {tty}, ptr addrspace(5) {bacc}, i64 {ir}, i64 {ic}")
+    s0 = f.emit(f"load f32, ptr addrspace(5) {gp}")
+    f.term(f"br label %{kh[0]} ; args({ir}, {ic}, 0, {s0})")
+    f.switch(kh)
+    hr, hc, hk, hs = (p for p, _ in kh[1])
+    c = f.emit(f"icmp slt {hk}, {bk}")
+    f.term(f"br i1 {c}, label %{kb[0]}, label %{st[0]} ; true_args({hr}, {hc}, {hk}, {hs})"
+           f" ; false_args({hr}, {hc}, {hs})")
+    f.switch(kb)
+    br_, bc, bkk, bs = (p for p, _ in kb[1])
+    lhs = _tile_load(f, ta, bm, bk, br_, bkk)
+    rhs = _tile_load(f, tb, bk, bn, bkk, bc)
+    prod = f.emit(f"fmul {lhs}, {rhs}")
+    ns = f.emit(f"fadd {bs}, {prod}")
+    nk = f.emit(f"add {bkk}, 1")
+    f.term(f"br label %{kh[0]} ; args({br_}, {bc}, {nk}, {ns})")
+    f.switch(st)
+    sr, scol, ssum = (p for p, _ in st[1])
+    _tile_store(f, td, bm, bn, sr, scol, ssum)
+    nc = f.emit(f"add {scol}, 1")
+    f.term(f"br label %{ch[0]} ; args({sr}, {nc})")
+    f.switch(rl)
+    nr = f.emit(f"add {rl[1][0][0]}, 1")
+    f.term(f"br label %{rh[0]} ; args({nr})")
+    f.switch(cont)
+    nkt = f.emit(f"add {bkt}, 1")
+    f.term(f"br label %{lh[0]} ; args({nkt}, {td})")
+    f.switch(lx)
+    xacc = lx[1][0][0]
+    crb = f.emit(f"mul {m}, {bm}")
+    ccb = f.emit(f"mul {n}, {bn}")
+    cro = f.emit(f"mul {crb}, {ldc}")
+    corg = f.emit(f"add {cro}, {ccb}")
+
+    def store_body(r, c):
+        p = f.emit(f"getelementptr {tty}, ptr addrspace(5) {xacc}, i64 {r}, i64 {c}")
+        v = f.emit(f"load f32, ptr addrspace(5) {p}")
+        ro = f.emit(f"mul {r}, {ldc}")
+        wr = f.emit(f"add {corg}, {ro}")
+        i = f.emit(f"add {wr}, {c}")
+        q = f.emit(f"getelementptr f32, ptr addrspace(1) %c, i64 {i}")
+        f.stmt(f"store f32 {v}, ptr addrspace(1) {q}")
+    _tile_loop(f, "tile_store", bm, bn, store_body)
+    f.term("ret void")
+    return f.text()

@@ -321,3 +321,24 @@ def test_reference_shaped_column_reduce(hip, bm, bn, is_max):
         acc = np.where(x[i] > acc, x[i], acc) if is_max else (acc + x[i]).astype(np.float32)
     assert_same_bits(out, acc.astype(np.float32), what="reference-shaped column reduce")
     kern.close()
+
+
+@pytest.mark.parametrize("gen", ["fused_mma_loop", "mma_k_loop"])
+@pytest.mark.parametrize("bm,bn,bk,m,n,k", [(32, 32, 8, 64, 96, 64), (64, 64, 16, 128, 64, 48),
+                                            (4, 4, 2, 8, 8, 6)])
+def test_k_tile_loop_with_a_carried_accumulator(hip, gen, bm, bn, bk, m, n, k):
+    """K-tile loops carrying the accumulator tile (fused: the MMA reads a and
+    b from their buffers and updates the tile in place, starting from the
+    splat; unfused: loaded tiles, the MMA into a result tile that is carried
+    on): bit for bit the canonical order (one sequential sum over all k)."""
+    say(f"llir {gen}<{bm}, {bn}, {bk}> {m}x{n}x{k}")
+    kern = hip.LlirKernel(getattr(llir_shapes, gen)(bm, bn, bk), (2, bm, bn))
+    r = rng(m * n + k)
+    a = r.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    grid = (m // bm, n // bn, 1)
+    c = _run(hip, kern, [a, b, np.zeros((m, n), np.float32)], (grid[0] * grid[1], 1, 1))[2]
+    want = np.zeros((m, n), np.float32)
+    cpuref.kernel_matmul(a, b, want, grid, bm, bn, bk)
+    assert_same_bits(c, want, what=f"llir {gen}")
+    kern.close()

@@ -376,3 +376,21 @@ def test_lone_column_loops_with_a_region_spread():
     assert "float v_v3_storage[64][1];" in src
     image, _ = hip.llir_compile(llir_shapes.col_reduce(20, 300, False), (1, 1, 300))
     assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+def test_tiles_carried_through_a_loop():
+    """A tile carried through the K-tile loop is a pointer block parameter
+    (`ptr addrspace(5)`, no pointee in the printed form): it takes the tile
+    type from its geps or from the alloca passed to it, and is declared as
+    the backends' tile pointer.  The fused MMA passes the same tile back (the
+    parameter is that alloca); the unfused one passes its result tile."""
+    fused = hip.llir_to_hip(llir_shapes.fused_mma_loop(32, 32, 8), (2, 32, 32))
+    assert "__launch_bounds__(1024)" in fused and "v_acc" not in fused
+    unfused = hip.llir_to_hip(llir_shapes.mma_k_loop(32, 32, 8), (2, 32, 32))
+    assert "float (*v_acc29)[32];" in unfused
+    assert "v_v93 = &(v_acc29[v_loop_row74][v_loop_col76]);" in unfused
+    for t, plan in ((llir_shapes.fused_mma_loop(32, 32, 8), (2, 32, 32)),
+                    (llir_shapes.mma_k_loop(32, 32, 8), (2, 32, 32)),
+                    (llir_shapes.mma_k_loop(4, 4, 2), (2, 4, 4))):
+        image, _ = hip.llir_compile(t, plan)
+        assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
