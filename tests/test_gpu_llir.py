@@ -342,3 +342,30 @@ def test_k_tile_loop_with_a_carried_accumulator(hip, gen, bm, bn, bk, m, n, k):
     cpuref.kernel_matmul(a, b, want, grid, bm, bn, bk)
     assert_same_bits(c, want, what=f"llir {gen}")
     kern.close()
+
+
+def test_memcpy_round_trip(hip):
+    """Each program copies its 4 elements of x into a private tile and from
+    there into y (memcpy both ways): y equals x bit for bit."""
+    from tests.test_llir import MEMCPY_LLIR
+    say("llir memcpy buffer -> tile -> buffer")
+    kern = hip.LlirKernel(MEMCPY_LLIR, None)
+    x = rng(5).normal(size=4096).astype(np.float32)
+    x[7] = -0.0
+    x[9] = np.nan
+    y = _run(hip, kern, [x, np.zeros_like(x)], (1024, 1, 1))[1]
+    assert_same_bits(y, x, what="memcpy round trip")
+    kern.close()
+
+
+def test_every_operation_runs(hip):
+    """Each binary op, compare predicate, cast and select of the printed form
+    on a = 7.75, b = -2.5 gives the C targets' value (casts convert, `sdiv`
+    truncates toward zero, `and` / `or` are bitwise, booleans widen to 0/1)."""
+    from tests.test_llir import OPS_EXPECTED, ops_llir
+    say("llir every operation")
+    kern = hip.LlirKernel(ops_llir(), None)
+    x = np.array([7.75, -2.5], np.float32)
+    out = _run(hip, kern, [x, np.full(20, 99.0, np.float32)], (1, 1, 1))[1]
+    assert_same_bits(out, np.array(OPS_EXPECTED, np.float32), what="llir operations")
+    kern.close()

@@ -394,3 +394,107 @@ def test_tiles_carried_through_a_loop():
                     (llir_shapes.mma_k_loop(4, 4, 2), (2, 4, 4))):
         image, _ = hip.llir_compile(t, plan)
         assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+MEMCPY_LLIR = """define void @cp(ptr addrspace(1) %x, ptr addrspace(1) %y, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %x [rank=1, shape_offset=0, elem=f32]
+  ; sile.param %y [rank=1, shape_offset=1, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %pid = call i32 @llvm.nvvm.ctaid.x()
+  %t = alloca [1 x [4 x f32]], addrspace(5)
+  %off = mul %pid, 4
+  %src = getelementptr f32, ptr addrspace(1) %x, i64 %off
+  %dst = getelementptr [1 x [4 x f32]], ptr addrspace(5) %t, i64 0, i64 0
+  call void @llvm.memcpy.inline(ptr addrspace(5) %dst, ptr addrspace(1) %src, i64 16, i1 false)
+  %d2 = getelementptr f32, ptr addrspace(1) %y, i64 %off
+  call void @llvm.memcpy.inline(ptr addrspace(1) %d2, ptr addrspace(5) %dst, i64 16, i1 false)
+  ret void
+}
+"""
+
+
+def test_memcpy_between_buffers_and_tiles():
+    """`llvm.memcpy.inline` as the reference prints it (print.rs:209-216: dst,
+    src, a byte count, and a volatile flag the C targets ignore) between a
+    global buffer and a private tile: `__builtin_memcpy`, compiled."""
+    src = hip.llir_to_hip(MEMCPY_LLIR, None)
+    assert "__builtin_memcpy(v_dst, v_src, (16LL));" in src
+    assert "__builtin_memcpy(v_d2, v_dst, (16LL));" in src
+    image, _ = hip.llir_compile(MEMCPY_LLIR, None)
+    assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
+# every binary op, compare predicate, cast and select the printed form has
+# (crates/sile-llvm-ir/src/print.rs:217-247), on a = 7.75, b = -2.5; the C
+# targets' semantics (emit.rs:112-177): casts are C conversions, `sdiv`
+# truncates, `and` / `or` are bitwise
+OPS_LLIR = """define void @ops(ptr addrspace(1) %x, ptr addrspace(1) %o, ptr addrspace(4) %__sile_shapes) {
+  ; sile.param %x [rank=1, shape_offset=0, elem=f32]
+  ; sile.param %o [rank=1, shape_offset=1, elem=f32]
+  ; sile.param %__sile_shapes [elem=i64]
+bb0:
+  %pa = getelementptr f32, ptr addrspace(1) %x, i64 0
+  %a = load f32, ptr addrspace(1) %pa
+  %pb = getelementptr f32, ptr addrspace(1) %x, i64 1
+  %b = load f32, ptr addrspace(1) %pb
+  %fs = fsub %a, %b
+  %fm = fmul %a, %b
+  %fd = fdiv %a, %b
+  %ia = fptosi %a to i64
+  %ib = fptosi %b to i64
+  %q = sdiv %ia, %ib
+  %d = sub %ia, %ib
+  %m = mul %ia, %ib
+  %an = and %ia, %ib
+  %or = or %ia, %ib
+  %c1 = icmp slt %ib, %ia
+  %c2 = icmp sle %ia, %ia
+  %c3 = icmp sgt %ib, %ia
+  %c4 = icmp sge %ia, %ib
+  %c5 = icmp eq %q, -3
+  %c6 = icmp ne %q, -3
+  %f1 = fcmp olt %b, %a
+  %f2 = fcmp ole %a, %a
+  %f3 = fcmp oge %b, %a
+  %cc = and %c1, %c3
+  %co = or %c1, %c3
+  %sel = select i1 %c3, f32 %a, f32 %b
+  br label %out ; args(%fs, %fm, %fd, %q, %d, %m, %an, %or, %c1, %c2, %c3, %c4, %c5, %c6, %f1, %f2, %f3, %cc, %co, %sel)
+out:
+  ; args(%v0: f32, %v1: f32, %v2: f32, %v3: i64, %v4: i64, %v5: i64, %v6: i64, %v7: i64, %v8: i1, %v9: i1, %v10: i1, %v11: i1, %v12: i1, %v13: i1, %v14: i1, %v15: i1, %v16: i1, %v17: i1, %v18: i1, %v19: f32)
+OUT_STORES
+  ret void
+}
+"""
+
+
+def ops_llir():
+    lines = []
+    for k in range(20):
+        v = f"%v{k}"
+        if 3 <= k <= 7:
+            lines.append(f"  %w{k} = sitofp {v} to f32")
+            v = f"%w{k}"
+        elif 8 <= k <= 18:
+            lines.append(f"  %z{k} = zext {v} to i64")
+            lines.append(f"  %w{k} = sitofp %z{k} to f32")
+            v = f"%w{k}"
+        lines.append(f"  %p{k} = getelementptr f32, ptr addrspace(1) %o, i64 {k}")
+        lines.append(f"  store f32 {v}, ptr addrspace(1) %p{k}")
+    return OPS_LLIR.replace("OUT_STORES\n", "\n".join(lines) + "\n")
+
+
+OPS_EXPECTED = [10.25, 7.75 * -2.5, 7.75 / -2.5, -3, 9, -14, 7 & -2, 7 | -2,
+                1, 1, 0, 1, 1, 0, 1, 1, 0, 0, 1, -2.5]
+
+
+def test_every_operation_translates():
+    src = hip.llir_to_hip(ops_llir(), None)
+    for line in ("v_q = v_ia / v_ib;", "v_an = v_ia & v_ib;", "v_or = v_ia | v_ib;",
+                 "v_c2 = v_ia <= v_ia;", "v_c4 = v_ia >= v_ib;", "v_c5 = v_q == (-3LL);",
+                 "v_c6 = v_q != (-3LL);", "v_f3 = v_b >= v_a;", "v_ia = v_a;",
+                 "v_sel = (v_c3) ? (v_a) : (v_b);"):
+        assert line in src, line
+    image, _ = hip.llir_compile(ops_llir(), None)
+    assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
