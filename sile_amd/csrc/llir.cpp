@@ -744,7 +744,10 @@ std::string ident(const std::string& name) {
 //     it stores only through the same pointer;
 //   * a 2-D nest (row loop around a column loop whose body is a region of
 //     blocks, e.g. the MMA's cell with its k loop) spreads its row x column
-//     iterations as one flat loop, the region serial on each lane;
+//     iterations as one flat loop, the region serial on each lane; with
+//     every lane's slots full and the region's branches alike for all of a
+//     lane's cells, a lane runs up to kCoopJam cells through one pass of the
+//     region (the values that differ between them held per cell);
 //   * lane l runs iterations l, l + W, ...; after the loop every lane holds
 //     the folded values and the final counter; a barrier follows when another
 //     lane's later access may conflict with the loop's;
@@ -804,6 +807,13 @@ struct CoopLoop {
   std::string row_iv, col_header, row_latch, entry;
   std::vector<std::string> region;
   std::vector<std::string> guards;
+  // Jammed in groups of `jam` slots (every lane's slots full, every branch in
+  // the region taken alike by all of a lane's cells): the region runs once a
+  // group with each value that differs between a lane's cells (jam_nu) held
+  // per slot, so the cells' loads and arithmetic interleave and what they
+  // share (an inner loop's counter, its compare) is computed once.
+  int jam = 0;
+  std::set<std::string> jam_nu;
 };
 struct CoopPlan {
   bool on = false;
@@ -821,6 +831,7 @@ struct CoopPlan {
   std::string why;                         // why the function stays one program per lane
 };
 constexpr int64_t kCoopMaxSlots = 16;
+constexpr int kCoopJam = 4;   // slots a jammed nest interleaves
 
 bool const_int(const Operand& o, int64_t& v) {
   if (o.is_value || o.ck != Operand::kInt) return false;
@@ -1335,7 +1346,55 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
     L.region = order;
     L.guards = guards;
     const int64_t slots = (M * N + kCoopThreads - 1) / kCoopThreads;
-    if (guards.empty() && slots <= kCoopMaxSlots) L.slots = slots;
+    if (slots <= kCoopMaxSlots) L.slots = slots;   // with guards: the spread branch
+    // values that differ between a lane's cells: the row, the column unless
+    // the column count divides the workgroup (then cell f + W keeps f's
+    // column), and what depends on them (block parameters through their
+    // edges' values)
+    if (L.slots >= 2 && (M * N) % kCoopThreads == 0) {
+      std::set<std::string> nu;
+      if (kCoopThreads % N != 0) nu.insert(cv);
+      if (!rv.empty()) nu.insert(rv);
+      for (bool grew = true; grew;) {
+        grew = false;
+        for (const std::string& bn : order) {
+          const Block* b = block(bn);
+          for (const Inst& in : b->insts) {
+            if (in.result.empty() || nu.count(in.result)) continue;
+            for (const Operand& a : in.args)
+              if (a.is_value && nu.count(a.name)) {
+                nu.insert(in.result);
+                grew = true;
+                break;
+              }
+          }
+          auto edge = [&](const std::string& t, const std::vector<Operand>& args) {
+            const Block* tb = block(t);
+            if (!tb || !region.count(t)) return;
+            for (size_t k = 0; k < args.size() && k < tb->params.size(); ++k)
+              if (args[k].is_value && nu.count(args[k].name) && !nu.count(tb->params[k].first)) {
+                nu.insert(tb->params[k].first);
+                grew = true;
+              }
+          };
+          if (b->term.kind == "br") edge(b->term.t, b->term.targs);
+          if (b->term.kind == "condbr") {
+            edge(b->term.t, b->term.targs);
+            edge(b->term.f, b->term.fargs);
+          }
+        }
+      }
+      bool uniform = true;
+      for (const std::string& bn : order) {
+        const Block* b = block(bn);
+        if (b->term.kind == "condbr" && b->term.cond.is_value && nu.count(b->term.cond.name))
+          uniform = false;
+      }
+      // groups of at most kCoopJam slots keep a group's values in registers
+      for (int g = kCoopJam; g >= 2 && uniform && !L.jam; --g)
+        if (L.slots % g == 0) L.jam = g;
+      if (L.jam) L.jam_nu = nu;
+    }
     plan.loops[L.header] = L;
   }
   // a nest inside another nest's region, or a loop inside one, stays serial
@@ -1476,8 +1535,9 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
               // in a slot-form lone column loop, at [.., col]: column col is
               // lane col % W's in every such loop and in 1-D spread loops
               if (L && L->rows > 0 && L->row_iv.empty()) {
-                if (x.op == "gep" && k == 0 && L->slots > 0 && x.args.back().is_value &&
-                    x.args.back().name == L->iv && x.args.size() == adims.size() + 1) {
+                if (x.op == "gep" && k == 0 && L->slots > 0 && L->guards.empty() &&
+                    x.args.back().is_value && x.args.back().name == L->iv &&
+                    x.args.size() == adims.size() + 1) {
                   in_1d = true;
                   continue;
                 }
@@ -1491,9 +1551,9 @@ CoopPlan plan_coop(const Function& fn, const std::map<std::string, Type>& types)
                                         ? (x.args.size() == 3 && const_int(x.args[1], z0) && z0 == 0)
                                         : (x.args.size() == 3 && x.args[1].is_value &&
                                            x.args[1].name == L->row_iv);
-                if (x.op == "gep" && k == 0 && L->slots > 0 && adims.size() == 2 &&
-                    adims[0] == L->rows && adims[1] == L->cols && row_ok && x.args[2].is_value &&
-                    x.args[2].name == L->iv) {
+                if (x.op == "gep" && k == 0 && L->slots > 0 && L->guards.empty() &&
+                    adims.size() == 2 && adims[0] == L->rows && adims[1] == L->cols && row_ok &&
+                    x.args[2].is_value && x.args[2].name == L->iv) {
                   in_nest = true;
                   continue;
                 }
@@ -1649,6 +1709,29 @@ struct Emitter {
   const CoopLoop* in_loop = nullptr;   // the spread loop being emitted (any form)
   std::map<std::string, std::string> relabel;   // block -> label inside a nest being emitted
   int nests = 0;
+  // a jammed nest being emitted: values of its jam_nu set are written per
+  // slot of the group (`v__s<k>`), the rest once
+  const CoopLoop* jam = nullptr;
+  int jam_k = -1;                  // the slot being written, -1 outside a replica
+  std::string kslot = "coop_k";    // the C expressions of this slot and its iteration
+  std::string itslot = "coop_it";
+
+  bool per_slot(const std::string& v) const { return jam && jam->jam_nu.count(v); }
+  std::string vname(const std::string& v) const {
+    if (!per_slot(v)) return ident(v);
+    if (jam_k < 0) throw ParseError{"internal: per-slot value %" + v + " read outside a slot"};
+    return ident(v) + "__s" + std::to_string(jam_k);
+  }
+  void enter_slot(int k) {
+    jam_k = k;
+    kslot = "(coop_g * " + std::to_string(jam->jam) + " + " + std::to_string(k) + ")";
+    itslot = "coop_it__s" + std::to_string(k);
+  }
+  void leave_slot() {
+    jam_k = -1;
+    kslot = "coop_k";
+    itslot = "coop_it";
+  }
 
   const Inst* def_of(const std::string& v) const {
     for (const Block& b : fn.blocks)
@@ -1666,7 +1749,7 @@ struct Emitter {
   }
 
   std::string opnd(const Operand& x) {
-    if (x.is_value) return ident(x.name);
+    if (x.is_value) return vname(x.name);
     if (x.ck == Operand::kBool) return x.name;
     if (x.ck == Operand::kFloat) {
       if (x.name == "inf") return "__builtin_inff()";
@@ -1695,7 +1778,21 @@ struct Emitter {
   }
 
   void inst(const Inst& in) {
-    const std::string r = in.result.empty() ? "" : ident(in.result);
+    if (jam && jam_k < 0) {
+      // in a jammed nest: an instruction that reads or defines a per-slot
+      // value runs once a slot
+      bool rep = per_slot(in.result);
+      for (const Operand& x : in.args) rep = rep || (x.is_value && per_slot(x.name));
+      if (rep) {
+        for (int k = 0; k < jam->jam; ++k) {
+          enter_slot(k);
+          inst(in);
+        }
+        leave_slot();
+        return;
+      }
+    }
+    const std::string r = in.result.empty() ? "" : vname(in.result);
     const auto& a = in.args;
     if (in.op == "alloca") return;  // storage declared at the top
     if (in.op == "gep") {
@@ -1703,7 +1800,7 @@ struct Emitter {
       // lane's e / W
       if (coop.on && a[0].is_value && coop.nest_private.count(a[0].name)) {
         // [row, col] in a slot-form nest: this lane's slot
-        o << "  " << r << " = &(" << opnd(a[0]) << "[coop_k]);\n";
+        o << "  " << r << " = &(" << opnd(a[0]) << "[" << kslot << "]);\n";
         return;
       }
       const bool slice = coop.on && a[0].is_value && coop.private_allocas.count(a[0].name);
@@ -1721,7 +1818,7 @@ struct Emitter {
       o << "  " << r << " = " << (sub ? "(" : "&(") << opnd(a[0]);
       for (size_t k = 1; k < a.size(); ++k) {
         if (slice && k + 1 == a.size() && cur && a[k].is_value && a[k].name == cur->iv)
-          o << "[coop_k]";   // the slot of this iteration
+          o << "[" << kslot << "]";   // the slot of this iteration
         else if (slice && k + 1 == a.size())
           o << "[(" << opnd(a[k]) << ") / " << kCoopThreads << "LL]";
         else
@@ -1752,8 +1849,8 @@ struct Emitter {
         auto sh = coop.shadows.find(g->args[0].name);
         if (sh != coop.shadows.end())
           for (int64_t c : sh->second)
-            o << "  if (coop_it == " << c << "LL) " << shadow_ref(*g, c) << " = " << opnd(a[1])
-              << ";\n";
+            o << "  if (" << itslot << " == " << c << "LL) " << shadow_ref(*g, c) << " = "
+              << opnd(a[1]) << ";\n";
       }
     } else if (in.op == "atomic" && coop.on) {
       // outside the spread loops every lane runs the program's code: add once
@@ -1804,19 +1901,34 @@ struct Emitter {
     if (args.size() != b->params.size())
       throw ParseError{"branch to %" + target + " passes " + std::to_string(args.size()) +
                        " arguments for " + std::to_string(b->params.size()) + " parameters"};
-    if (!args.empty()) {
-      o << "  {\n";
-      for (size_t k = 0; k < args.size(); ++k)
-        o << "    " << c_decl(b->params[k].second, "t" + std::to_string(k)) << " = "
-          << opnd(args[k]) << ";\n";
-      for (size_t k = 0; k < args.size(); ++k)
-        o << "    " << ident(b->params[k].first) << " = t" << k << ";\n";
-      o << "  }\n";
+    if (args.empty()) return;
+    // in a jammed nest a per-slot parameter takes each slot's value
+    const bool outer = jam && jam_k < 0;
+    o << "  {\n";
+    for (size_t k = 0; k < args.size(); ++k) {
+      const int reps = outer && per_slot(b->params[k].first) ? jam->jam : 0;
+      for (int s = 0; s < std::max(reps, 1); ++s) {
+        if (reps) enter_slot(s);
+        o << "    " << c_decl(b->params[k].second, "t" + std::to_string(k) + (reps ? "_" + std::to_string(s) : ""))
+          << " = " << opnd(args[k]) << ";\n";
+      }
+      if (reps) leave_slot();
     }
+    for (size_t k = 0; k < args.size(); ++k) {
+      const int reps = outer && per_slot(b->params[k].first) ? jam->jam : 0;
+      for (int s = 0; s < std::max(reps, 1); ++s) {
+        if (reps) enter_slot(s);
+        o << "    " << vname(b->params[k].first) << " = t" << k << (reps ? "_" + std::to_string(s) : "")
+          << ";\n";
+      }
+      if (reps) leave_slot();
+    }
+    o << "  }\n";
   }
 
   void jump(const std::string& target, const std::vector<Operand>& args) {
-    assign(target, args);
+    // a jammed nest's back edge: the next group sets the row and column itself
+    if (!(jam && target == jam->col_header)) assign(target, args);
     auto rl = relabel.find(target);
     o << "  goto " << (rl != relabel.end() ? rl->second : "L_" + ident(target)) << ";\n";
   }
@@ -1876,41 +1988,82 @@ struct Emitter {
   }
 
   // A 2-D nest at its row header: iteration f = row * cols + col runs the
-  // region with that row and column, on lane f % W (slot f / W, unrolled) or,
-  // with stride guards, lane l runs f = l, l + W, ... when every guarded
-  // stride is at least cols and lane 0 runs all of them in order otherwise;
-  // the region's back edges go to the next iteration.  Then the counters
-  // take their final values, a barrier (when needed) and the row header's
-  // exit branch.
+  // region with that row and column on lane f % W, in slot f / W (slots
+  // unrolled, or jammed a group at a time), or lane l runs f = l, l + W, ...
+  // when the slots are too many.  With stride guards that spread runs when
+  // every guarded stride is at least cols, and lane 0 runs all iterations in
+  // order otherwise.  The region's back edges go to the next iteration.  Then
+  // the counters take their final values, a barrier (when needed) and the row
+  // header's exit branch.
   void coop_nest(const Block& rh, const CoopLoop& L) {
     const std::string id = std::to_string(nests++);
-    const std::string r = ident(L.row_iv), c = ident(L.iv);
-    const std::string mn = std::to_string(L.rows * L.cols) + "LL", n = std::to_string(L.cols) + "LL";
+    const std::string n = std::to_string(L.cols) + "LL";
     if (L.pre_barrier) o << "  __syncthreads();\n";
     o << "  {\n";
-    if (L.slots > 0) {
-      o << "#pragma unroll\n";
-      o << "    for (int coop_k = 0; coop_k < " << L.slots << "; ++coop_k) {\n";
-      o << "    const long long coop_it = (long long)coop_k * " << kCoopThreads
-        << "LL + (long long)threadIdx.x;\n";
-      o << "    if (coop_it >= " << mn << ") continue;\n";
+    if (L.guards.empty()) {
+      nest_copy(L, id, true);
     } else {
       o << "    const bool coop_par = true";
       for (const std::string& g : L.guards) o << " && " << ident(g) << " >= " << n;
-      o << ";\n";
-      o << "    const long long coop_end = (coop_par || threadIdx.x == 0) ? " << mn << " : 0LL;\n";
-      o << "    for (long long coop_it = coop_par ? (long long)threadIdx.x : 0LL; coop_it < coop_end; "
-           "coop_it += coop_par ? "
-        << kCoopThreads << "LL : 1LL) {\n";
+      o << ";\n    if (coop_par) {\n";
+      nest_copy(L, id + "p", true);
+      o << "    } else if (threadIdx.x == 0) {\n";
+      nest_copy(L, id + "s", false);
+      o << "    }\n";
     }
-    if (L.row_iv.empty())
-      o << "    " << c << " = coop_it;\n";
-    else
-      o << "    " << r << " = coop_it / " << n << "; " << c << " = coop_it % " << n << ";\n";
+    if (!L.row_iv.empty()) o << "    " << ident(L.row_iv) << " = " << L.rows << "LL;";
+    o << "    " << ident(L.iv) << " = " << n << ";\n  }\n";
+    if (L.barrier) o << "  __syncthreads();\n";
+    jump(rh.term.f, rh.term.fargs);
+  }
+
+  // One copy of a nest's iterations: spread over the lanes (par) or all of
+  // them in order.
+  void nest_copy(const CoopLoop& L, const std::string& id, bool par) {
+    const std::string mn = std::to_string(L.rows * L.cols) + "LL", n = std::to_string(L.cols) + "LL";
+    auto cell = [&](const std::string& it, const std::string& sfx) {
+      if (L.row_iv.empty())
+        o << "    " << ident(L.iv) << sfx << " = " << it << ";\n";
+      else
+        o << "    " << ident(L.row_iv) << sfx << " = " << it << " / " << n << "; " << ident(L.iv)
+          << sfx << " = " << it << " % " << n << ";\n";
+    };
+    if (par && L.jam) {
+      const std::string g = std::to_string(L.jam);
+      o << "#pragma unroll\n";
+      o << "    for (int coop_g = 0; coop_g < " << L.slots / L.jam << "; ++coop_g) {\n";
+      for (int k = 0; k < L.jam; ++k) {
+        const std::string s = "__s" + std::to_string(k), it = "coop_it" + s;
+        o << "    const long long " << it << " = (long long)(coop_g * " << g << " + " << k << ") * "
+          << kCoopThreads << "LL + (long long)threadIdx.x;\n";
+        if (L.jam_nu.count(L.iv)) {
+          cell(it, s);
+          continue;
+        }
+        // the column is the lane's in every slot
+        if (k == 0) o << "    " << ident(L.iv) << " = " << it << " % " << n << ";\n";
+        if (!L.row_iv.empty()) o << "    " << ident(L.row_iv) << s << " = " << it << " / " << n << ";\n";
+      }
+    } else {
+      if (par && L.slots > 0) {
+        o << "#pragma unroll\n";
+        o << "    for (int coop_k = 0; coop_k < " << L.slots << "; ++coop_k) {\n";
+        o << "    const long long coop_it = (long long)coop_k * " << kCoopThreads
+          << "LL + (long long)threadIdx.x;\n";
+        o << "    if (coop_it >= " << mn << ") continue;\n";
+      } else if (par) {
+        o << "    for (long long coop_it = (long long)threadIdx.x; coop_it < " << mn
+          << "; coop_it += " << kCoopThreads << "LL) {\n";
+      } else {
+        o << "    for (long long coop_it = 0; coop_it < " << mn << "; ++coop_it) {\n";
+      }
+      cell("coop_it", "");
+    }
     for (const std::string& b : L.region) relabel[b] = "L_" + ident(b) + "_n" + id;
     relabel[L.col_header] = "coop_next" + id;
     o << "  goto " << relabel[L.entry] << ";\n";
-    cur = L.slots > 0 ? &L : nullptr;
+    cur = par && L.slots > 0 ? &L : nullptr;
+    jam = par && L.jam ? &L : nullptr;
     in_loop = &L;
     for (const std::string& bn : L.region) {
       if (c_loop_bodies.count(bn)) continue;   // inside its header's C loop
@@ -1920,14 +2073,11 @@ struct Emitter {
       block_code(*b, relabel[bn]);
     }
     cur = nullptr;
+    jam = nullptr;
     in_loop = nullptr;
     for (const std::string& b : L.region) relabel.erase(b);
     relabel.erase(L.col_header);
     o << "    coop_next" << id << ":;\n    }\n";
-    if (!L.row_iv.empty()) o << "    " << r << " = " << L.rows << "LL;";
-    o << "    " << c << " = " << n << ";\n  }\n";
-    if (L.barrier) o << "  __syncthreads();\n";
-    jump(rh.term.f, rh.term.fargs);
   }
 
   // A spread loop at its header: lane l runs iterations l, l + W, ... of the
@@ -2034,9 +2184,21 @@ struct Emitter {
     }
     o << ", long long sile_gid_0, long long sile_gid_1, long long sile_gid_2) {\n";
     o << "  (void)sile_gid_0; (void)sile_gid_1; (void)sile_gid_2;\n";
-    // declarations: block parameters, instruction results, alloca storage
+    // declarations: block parameters, instruction results, alloca storage,
+    // and the per-slot copies of jammed nests' values
+    std::map<std::string, int> copies;
+    for (auto& kv : coop.loops)
+      for (const std::string& v : kv.second.jam_nu) copies[v] = std::max(copies[v], kv.second.jam);
+    auto slot_copies = [&](const Type& t, const std::string& v) {
+      auto cp = copies.find(v);
+      for (int k = 0; cp != copies.end() && k < cp->second; ++k)
+        o << "  " << c_decl(t, ident(v) + "__s" + std::to_string(k)) << ";\n";
+    };
     for (const Block& b : fn.blocks) {
-      for (auto& p : b.params) o << "  " << c_decl(p.second, ident(p.first)) << ";\n";
+      for (auto& p : b.params) {
+        o << "  " << c_decl(p.second, ident(p.first)) << ";\n";
+        slot_copies(p.second, p.first);
+      }
       for (const Inst& in : b.insts) {
         if (in.result.empty()) continue;
         if (in.op == "alloca") {
@@ -2088,6 +2250,7 @@ struct Emitter {
               << "_storage;\n";
         } else {
           o << "  " << c_decl(in.ty, ident(in.result)) << ";\n";
+          slot_copies(in.ty, in.result);
         }
       }
     }

@@ -243,6 +243,9 @@ def test_reference_shaped_vec_add(hip, fused):
     (64, 64, 8, 64, 64, 75),      # K truncated to 72 (whole BK tiles)
     (32, 32, 8, 64, 64, 64),      # the mlp example's gemm tiles
     (16, 32, 4, 48, 96, 20),      # 512 cells a program
+    (128, 64, 8, 256, 128, 40),   # 8192 cells: two jammed groups of four a lane
+    (96, 32, 8, 96, 64, 24),      # 3072 cells: one group of three
+    (32, 96, 8, 64, 192, 16),     # the same, the column per cell (96 does not divide 1024)
 ])
 def test_canonical_matmul_nest(hip, bm, bn, bk, m, n, k):
     """The canonical matmul's LLIR with its row x column nest spread over the
@@ -283,7 +286,8 @@ def test_canonical_matmul_nest_in_order_when_rows_overlap(hip):
 
 
 @pytest.mark.parametrize("bm,bn,bk,grid", [(32, 32, 16, (2, 3)), (64, 64, 8, (1, 2)), (16, 16, 32, (3, 2)),
-                                          (48, 32, 8, (2, 2))])   # 1536 cells: a partial second slot
+                                          (48, 32, 8, (2, 2)),    # 1536 cells: a partial second slot
+                                          (128, 128, 4, (1, 2))])  # 16 accumulator slots a lane, jammed
 def test_tile_mma_nest(hip, bm, bn, bk, grid):
     """Tiles loaded, a zero accumulator, the tile MMA nest (mma.rs) and the
     store, every nest spread over the lanes: bit for bit the canonical order

@@ -337,28 +337,62 @@ def test_two_dimensional_nests_spread():
     for a body (cell init, the k loop, the store): iteration row * BN + col
     runs the region on one lane, the k loop stays serial on it.  A buffer
     store at `row * ldc + col` spreads when ldc >= BN at run time (lane 0
-    runs the nest in order otherwise); tile-only nests take the slot form,
-    and a tile touched only at [row, col] by nests of its shape is split
-    over the lanes."""
+    runs the nest in order otherwise); nests take the slot form, and a tile
+    touched only at [row, col] by unguarded nests of its shape is split over
+    the lanes.  With every slot of every lane full and the region's branches
+    alike for all of a lane's cells, a lane's cells run jammed, four at a
+    time: what depends on the row or column per slot, the rest once."""
     mm = hip.llir_to_hip(llir_shapes.matmul(64, 64, 8), (2, 64, 64))
     assert "__launch_bounds__(1024)" in mm
-    assert "const bool coop_par = true && v_v11 >= 64LL;" in mm
-    assert "v_loop_row19 = coop_it / 64LL; v_loop_col21 = coop_it % 64LL;" in mm
-    assert "goto coop_next0;" in mm and "L_v_matmul_k_header_4_n0:;" in mm
+    assert "const bool coop_par = true && v_v11 >= 64LL;\n    if (coop_par) {" in mm
+    # spread: 4 cells a lane, jammed; 64 columns divide the workgroup, so a
+    # lane's cells share their column (and the b element of each k)
+    assert "for (int coop_g = 0; coop_g < 1; ++coop_g) {" in mm
+    assert ("const long long coop_it__s0 = (long long)(coop_g * 4 + 0) * 1024LL + "
+            "(long long)threadIdx.x;\n"
+            "    v_loop_col21 = coop_it__s0 % 64LL;\n"
+            "    v_loop_row19__s0 = coop_it__s0 / 64LL;\n") in mm
+    assert ("const long long coop_it__s3 = (long long)(coop_g * 4 + 3) * 1024LL + "
+            "(long long)threadIdx.x;\n"
+            "    v_loop_row19__s3 = coop_it__s3 / 64LL;\n") in mm
+    assert "v_v51__s3 = v_loop_sum27__s3 + v_v50__s3;" in mm   # a sum per cell
+    assert "v_v50__s3 = v_v47__s3 * v_v49;" in mm              # one b element
+    assert "v_v54 = v_loop_b_index29 + v_v9;" in mm and "v_v54__s" not in mm
+    assert mm.count("v_v52 = v_loop_k26 + (1LL);") == 2         # the k counter once a copy
+    assert "goto coop_next0p;" in mm and "L_v_matmul_k_header_4_n0p:;" in mm
+    # in order on lane 0 when ldc < BN
+    assert ("} else if (threadIdx.x == 0) {\n"
+            "    for (long long coop_it = 0; coop_it < 4096LL; ++coop_it) {\n"
+            "    v_loop_row19 = coop_it / 64LL; v_loop_col21 = coop_it % 64LL;\n"
+            "  goto L_v_matmul_cell_init_3_n0s;") in mm
+    assert "goto coop_next0s;" in mm and "L_v_matmul_k_header_4_n0s:;" in mm
     # the k loop's carried row and column were the nest's own
     assert "v_loop_row22" not in mm and "v_loop_col23" not in mm
     small = hip.llir_to_hip(llir_shapes.matmul(8, 8, 8), (2, 8, 8))   # 64 cells: a lane each
     assert "__launch_bounds__(64)" in small and "coop_" not in small
+    # 96 columns do not divide the workgroup: the column per slot as well
+    odd = hip.llir_to_hip(llir_shapes.matmul(32, 96, 8), (2, 32, 96))
+    assert "for (int coop_g = 0; coop_g < 1; ++coop_g) {" in odd
+    assert "__s2 = coop_it__s2 / 96LL; v_loop_col21__s2 = coop_it__s2 % 96LL;" in odd
+    # a partial slot (1536 cells): the slot form with its bound check, no jam
+    part = hip.llir_to_hip(llir_shapes.matmul(48, 32, 8), (2, 48, 32))
+    assert "for (int coop_k = 0; coop_k < 2; ++coop_k) {" in part
+    assert "if (coop_it >= 1536LL) continue;" in part and "coop_g" not in part
+    mma64 = hip.llir_to_hip(llir_shapes.mma_program(64, 64, 16), (2, 64, 64))
+    assert "float v_v8_storage[4];" in mma64
+    assert "v_v62__s2 = &(v_v8[(coop_g * 4 + 2)]);" in mma64   # slot coop_g * 4 + k
     mma = hip.llir_to_hip(llir_shapes.mma_program(32, 32, 16), (2, 32, 32))
     assert "__launch_bounds__(1024)" in mma
-    # the accumulator (filled and read at [row, col] by slot-form nests): one
-    # slot a lane; a and b (read at [row, k] / [k, col]) and the result
-    # (read by the guarded store nest) in LDS
+    # the accumulator (filled and read at [row, col] by unguarded slot-form
+    # nests): one slot a lane; a and b (read at [row, k] / [k, col]) and the
+    # result (read by the guarded store nest) in LDS
     assert "float v_v8_storage[1];" in mma and "v_v8 = v_v8_storage;" in mma
     assert "__shared__ float v_v6_storage[32][16];" in mma
     assert "__shared__ float v_v9_storage[32][32];" in mma
-    assert mma.count("for (int coop_k = 0; coop_k < 1; ++coop_k) {") == 4
+    assert mma.count("for (int coop_k = 0; coop_k < 1; ++coop_k) {") == 5
     for t, plan in ((llir_shapes.matmul(64, 64, 8), (2, 64, 64)),
+                    (llir_shapes.matmul(48, 32, 8), (2, 48, 32)),
+                    (llir_shapes.mma_program(64, 64, 16), (2, 64, 64)),
                     (llir_shapes.mma_program(32, 32, 16), (2, 32, 32))):
         image, _ = hip.llir_compile(t, plan)
         assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
