@@ -2021,12 +2021,21 @@ struct Emitter {
   // them in order.
   void nest_copy(const CoopLoop& L, const std::string& id, bool par) {
     const std::string mn = std::to_string(L.rows * L.cols) + "LL", n = std::to_string(L.cols) + "LL";
+    // spread, a wave's 64 iterations start at a multiple of 64: with a column
+    // count that 64 divides they share their row, which then goes to a scalar
+    // register (and what the row alone addresses can come through the scalar
+    // cache)
+    auto row = [&](const std::string& it) {
+      if (par && L.cols % 64 == 0 && L.rows < (int64_t(1) << 31))
+        return "(long long)__builtin_amdgcn_readfirstlane((int)(" + it + " / " + n + "))";
+      return it + " / " + n;
+    };
     auto cell = [&](const std::string& it, const std::string& sfx) {
       if (L.row_iv.empty())
         o << "    " << ident(L.iv) << sfx << " = " << it << ";\n";
       else
-        o << "    " << ident(L.row_iv) << sfx << " = " << it << " / " << n << "; " << ident(L.iv)
-          << sfx << " = " << it << " % " << n << ";\n";
+        o << "    " << ident(L.row_iv) << sfx << " = " << row(it) << "; " << ident(L.iv) << sfx
+          << " = " << it << " % " << n << ";\n";
     };
     if (par && L.jam) {
       const std::string g = std::to_string(L.jam);
@@ -2042,7 +2051,7 @@ struct Emitter {
         }
         // the column is the lane's in every slot
         if (k == 0) o << "    " << ident(L.iv) << " = " << it << " % " << n << ";\n";
-        if (!L.row_iv.empty()) o << "    " << ident(L.row_iv) << s << " = " << it << " / " << n << ";\n";
+        if (!L.row_iv.empty()) o << "    " << ident(L.row_iv) << s << " = " << row(it) << ";\n";
       }
     } else {
       if (par && L.slots > 0) {

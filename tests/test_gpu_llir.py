@@ -246,6 +246,8 @@ def test_reference_shaped_vec_add(hip, fused):
     (128, 64, 8, 256, 128, 40),   # 8192 cells: two jammed groups of four a lane
     (96, 32, 8, 96, 64, 24),      # 3072 cells: one group of three
     (32, 96, 8, 64, 192, 16),     # the same, the column per cell (96 does not divide 1024)
+    (24, 64, 8, 48, 128, 16),     # 1536 cells: slot form, a partial slot, rows in scalar registers
+    (256, 128, 4, 256, 256, 8),   # 32768 cells: the strided form, rows in scalar registers
 ])
 def test_canonical_matmul_nest(hip, bm, bn, bk, m, n, k):
     """The canonical matmul's LLIR with its row x column nest spread over the

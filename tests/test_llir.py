@@ -346,15 +346,16 @@ def test_two_dimensional_nests_spread():
     assert "__launch_bounds__(1024)" in mm
     assert "const bool coop_par = true && v_v11 >= 64LL;\n    if (coop_par) {" in mm
     # spread: 4 cells a lane, jammed; 64 columns divide the workgroup, so a
-    # lane's cells share their column (and the b element of each k)
+    # lane's cells share their column (and the b element of each k); a
+    # wave's 64 cells share their row, read as the wave's first lane's
     assert "for (int coop_g = 0; coop_g < 1; ++coop_g) {" in mm
     assert ("const long long coop_it__s0 = (long long)(coop_g * 4 + 0) * 1024LL + "
             "(long long)threadIdx.x;\n"
             "    v_loop_col21 = coop_it__s0 % 64LL;\n"
-            "    v_loop_row19__s0 = coop_it__s0 / 64LL;\n") in mm
+            "    v_loop_row19__s0 = (long long)__builtin_amdgcn_readfirstlane((int)(coop_it__s0 / 64LL));\n") in mm
     assert ("const long long coop_it__s3 = (long long)(coop_g * 4 + 3) * 1024LL + "
             "(long long)threadIdx.x;\n"
-            "    v_loop_row19__s3 = coop_it__s3 / 64LL;\n") in mm
+            "    v_loop_row19__s3 = (long long)__builtin_amdgcn_readfirstlane((int)(coop_it__s3 / 64LL));\n") in mm
     assert "v_v51__s3 = v_loop_sum27__s3 + v_v50__s3;" in mm   # a sum per cell
     assert "v_v50__s3 = v_v47__s3 * v_v49;" in mm              # one b element
     assert "v_v54 = v_loop_b_index29 + v_v9;" in mm and "v_v54__s" not in mm
