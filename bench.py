@@ -569,17 +569,26 @@ def bench_llir_softmax(name, steps, warmup, text=None):
     return res
 
 
-def bench_llir_matmul(name, steps, warmup, size=2048, tile=64, bk=8):
-    """The canonical matmul's LLIR (canonical_matmul.rs:24-444, generated by
-    tests/llir_shapes.py) at M = N = K = size with tile x tile cells a
-    program: the row x column nest spread over a 1024-lane workgroup, each
-    cell's k loop serial on its lane (the reference's order, bit-exact),
-    through the synchronous sile_hip_launch_llir; 2 M N K flops per call,
-    against the VALU rate without FMA (the order forbids contraction)."""
+def llir_matmul_inputs(size):
+    """The generated matmul lines' A and B: seeded N(0, 1) f32 [size, size]."""
+    return normal(4, (size, size), 1.0), normal(5, (size, size), 1.0)
+
+
+def bench_llir_matmul(name, steps, warmup, size=2048, tile=64, bk=8, gen="matmul"):
+    """A matmul program's LLIR (tests/llir_shapes.py) at M = N = K = size
+    with tile x tile cells a program: `matmul` is the canonical matmul
+    (canonical_matmul.rs:24-444), the row x column nest with each cell's k
+    loop; `mma_k_loop` the K-tile loop of tile loads and the tile MMA nest
+    (mma.rs:25-260) carrying its accumulator tile.  The nests spread over a
+    1024-lane workgroup, each cell's sum serial on its lane (the reference's
+    order, bit-exact), through the synchronous sile_hip_launch_llir; 2 M N K
+    flops per call, against the VALU rate without FMA (the order forbids
+    contraction)."""
     from tests import llir_shapes
-    kern = hip.LlirKernel(llir_shapes.matmul(tile, tile, bk), (2, tile, tile))
-    a = hip.DeviceBuffer.from_array(normal(4, (size, size), 1.0))
-    b = hip.DeviceBuffer.from_array(normal(5, (size, size), 1.0))
+    kern = hip.LlirKernel(getattr(llir_shapes, gen)(tile, tile, bk), (2, tile, tile))
+    ha, hb = llir_matmul_inputs(size)
+    a = hip.DeviceBuffer.from_array(ha)
+    b = hip.DeviceBuffer.from_array(hb)
     c = hip.DeviceBuffer(size * size * 4)
     ptrs, shapes = [a.ptr, b.ptr, c.ptr], [size] * 6
     grid = ((size // tile) ** 2, 1, 1)
@@ -591,7 +600,8 @@ def bench_llir_matmul(name, steps, warmup, size=2048, tile=64, bk=8):
     dt = (time.perf_counter() - t0) / steps
     res = summarise(name, 2.0 * size ** 3, 1e12, "TFLOP/s", dt * 1e3 * steps, steps, "valu",
                     PEAK_VALU_F32_TOPS, None)
-    res["note"] = (f"canonical matmul<{tile}, {tile}, {bk}> LLIR, f32, one 1024-lane workgroup "
+    form = "canonical matmul" if gen == "matmul" else "K-tile MMA loop"
+    res["note"] = (f"{form}<{tile}, {tile}, {bk}> LLIR, f32, one 1024-lane workgroup "
                    "a program, bit-identical to the reference's order")
     for buf in (a, b, c):
         buf.close()
@@ -953,12 +963,13 @@ WORKLOAD_KERNEL = {"softmax_f16_8192": "sile_softmax_rows", "gemm_bf16_8192": "s
                    "llir_softmax_f32_8192": "sile_kernel_softmax",
                    "llir_softmax_ref_shapes_f32_8192": "sile_kernel_softmax",
                    "llir_matmul_f32_2048": "sile_kernel_matmul",
+                   "llir_mma_k_loop_f32_2048": "sile_kernel_mma_k_loop",
                    "tile_ir_softmax_f32_8192": "sile_softmax_rows"}
 
 ALL = ["gemm_bf16_8192", "gemm_bf16_4096", "gemm_fp8_8192", "flash_attn_fwd_f16_s8192",
        "flash_attn_fwd_f16_s4096", "softmax_f16_8192"]
 EXTRA = ["copy_calibration", "llir_vec_add", "llir_softmax_f32_8192", "llir_softmax_ref_shapes_f32_8192",
-         "llir_matmul_f32_2048",
+         "llir_matmul_f32_2048", "llir_mma_k_loop_f32_2048",
          "tile_ir_softmax_f32_8192",
          "gemm_f32_exact_4096",
          "gemm_f32_exact_512", "reduce_rows_f32_8192", "parallel_reduce_f32",
@@ -1017,6 +1028,8 @@ def main():
             results[name] = bench_llir_softmax(name, args.steps, args.warmup)
         elif name == "llir_matmul_f32_2048":
             results[name] = bench_llir_matmul(name, args.steps, args.warmup)
+        elif name == "llir_mma_k_loop_f32_2048":
+            results[name] = bench_llir_matmul(name, args.steps, args.warmup, bk=16, gen="mma_k_loop")
         elif name == "llir_softmax_ref_shapes_f32_8192":
             # the same program in the reference's loop shapes: a loop nest and
             # a private tile per op (tests/llir_shapes.py)

@@ -10,7 +10,9 @@ with the CPU oracle:
     inputs;
   * causal flash attention B=4 H=32 D=128 at S = 4096 and 8192: three
     (batch, head) pairs, the first, the last and every 16th 128-query block;
-  * row softmax [8192, 8192] fp16: every 64th row.
+  * row softmax [8192, 8192] fp16: every 64th row;
+  * the matmuls generated from LLIR, f32 2048^3 (canonical and K-tile MMA
+    forms): three rows of programs, bit for bit.
 Bound for 16-bit and fp8 outputs: |g - r| <= 2e-2 + 1e-2 |r| (the north
 star's 2e-2 absolute / 1e-2 relative), and every output element finite.
 """
@@ -19,7 +21,7 @@ import pytest
 
 import bench
 from oracle import cpuref
-from tests.helpers import assert_close, say
+from tests.helpers import assert_close, assert_same_bits, say
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +106,30 @@ def test_softmax_at_bench_shape(hip):
     ref = cpuref.softmax_rows(x[sample].astype(np.float32))
     # every softmax output here is far below 2e-2: the bound is relative
     assert_close(got[sample].astype(np.float32), ref, atol=1e-6, rtol=RTOL, what="softmax")
+
+
+@pytest.mark.parametrize("gen,bk", [("matmul", 8), ("mma_k_loop", 16)])
+def test_generated_matmul_at_bench_shape(hip, gen, bk):
+    """The generated LLIR matmul lines (bench.py llir_matmul_f32_2048 and
+    llir_mma_k_loop_f32_2048): f32 2048^3 on the bench's inputs, 64 x 64
+    cells a program; the first, a middle and the last row of programs are
+    bit for bit the oracle's canonical order (each cell one sequential sum
+    over k of rounded products)."""
+    from tests import llir_shapes
+    size, tile = 2048, 64
+    say(f"bench-shape generated {gen}<{tile}, {tile}, {bk}> {size}^3")
+    a, b = bench.llir_matmul_inputs(size)
+    kern = hip.LlirKernel(getattr(llir_shapes, gen)(tile, tile, bk), (2, tile, tile))
+    da, db = hip.DeviceBuffer.from_array(a), hip.DeviceBuffer.from_array(b)
+    dc = hip.DeviceBuffer(size * size * 4)
+    dc.fill_bytes(0xFF)
+    kern([da.ptr, db.ptr, dc.ptr], [size] * 6, ((size // tile) ** 2, 1, 1))
+    got = dc.download(np.float32, (size, size))
+    for buf in (da, db, dc):
+        buf.close()
+    kern.close()
+    for tr in (0, 15, size // tile - 1):
+        rows = slice(tr * tile, (tr + 1) * tile)
+        want = np.zeros((tile, size), np.float32)
+        cpuref.kernel_matmul(np.ascontiguousarray(a[rows]), b, want, (1, size // tile, 1), tile, tile, bk)
+        assert_same_bits(got[rows], want, what=f"generated {gen}, row tile {tr}")
