@@ -266,19 +266,49 @@ def test_canonical_matmul_nest(hip, bm, bn, bk, m, n, k):
     kern.close()
 
 
-def test_canonical_matmul_nest_in_order_when_rows_overlap(hip):
+@pytest.mark.parametrize("by", ["row", "col"])
+def test_nest_with_a_trip_count_per_cell(hip, by):
+    """The canonical matmul with its k loop bounded by the cell's row or
+    column (tests/test_llir.py triangular_matmul): bounded by the column the
+    lane's cells still run jammed, bounded by the row one slot at a time;
+    both bit for bit a numpy restatement of the loops (each cell a
+    sequential sum of rounded products over k < its bound)."""
+    from tests.test_llir import triangular_matmul
+    say(f"llir canonical matmul<64, 64, 8> with k < {by}")
+    kern = hip.LlirKernel(triangular_matmul(64, 64, 8, by), (2, 64, 64))
+    m, n, k = 128, 128, 72
+    r = rng(91 if by == "row" else 92)
+    a = r.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, size=(k, n)).astype(np.float32)
+    c = _run(hip, kern, [a, b, np.zeros((m, n), np.float32)], (4, 1, 1))[2]
+    kern.close()
+    want = np.zeros((m, n), np.float32)
+    for row in range(m):
+        for col0 in range(0, n, 64):
+            s = np.zeros(64, np.float32)
+            for kk in range(k):
+                # the bound is the cell's row / column inside its 64 x 64 tile
+                live = (np.full(64, row % 64) if by == "row" else np.arange(64)) > kk
+                s = np.where(live, s + a[row, kk] * b[kk, col0:col0 + 64], s).astype(np.float32)
+            want[row, col0:col0 + 64] = s
+    assert_same_bits(c, want, what=f"llir k < {by}")
+
+
+@pytest.mark.parametrize("t", [32, 64])   # 64: the nest whose spread copy is jammed
+def test_canonical_matmul_nest_in_order_when_rows_overlap(hip, t):
     """With ldc < BN the rows of the C tile overlap: the nest then runs in
     order on lane 0, so the last write of each element is the sequential
     one (one program, planned on a; numpy restatement of the loops)."""
-    say("llir canonical matmul<32, 32, 8>, ldc 16: the in-order path")
-    kern = hip.LlirKernel(llir_shapes.matmul(32, 32, 8), (0, 32, 16))
-    r = rng(77)
-    a = r.integers(-4, 5, size=(32, 16)).astype(np.float32)
-    b = r.integers(-4, 5, size=(16, 32)).astype(np.float32)
-    c = _run(hip, kern, [a, b, np.zeros((40, 16), np.float32)], (1, 1, 1))[2]
-    want = np.zeros((40, 16), np.float32).ravel()
-    for row in range(32):
-        for col in range(32):
+    say(f"llir canonical matmul<{t}, {t}, 8>, ldc 16: the in-order path")
+    kern = hip.LlirKernel(llir_shapes.matmul(t, t, 8), (0, t, 16))
+    r = rng(77 + t)
+    a = r.integers(-4, 5, size=(t, 16)).astype(np.float32)
+    b = r.integers(-4, 5, size=(16, t)).astype(np.float32)
+    crows = (t - 1) + (t - 1) // 16 + 2     # holds element (t - 1) * 16 + t - 1
+    c = _run(hip, kern, [a, b, np.zeros((crows, 16), np.float32)], (1, 1, 1))[2]
+    want = np.zeros((crows, 16), np.float32).ravel()
+    for row in range(t):
+        for col in range(t):
             s = np.float32(0.0)
             for kk in range(16):
                 s = np.float32(s + np.float32(a[row, kk] * b[kk, col]))

@@ -331,6 +331,30 @@ bb0:
         hip.llir_to_hip(bad, None)
 
 
+def triangular_matmul(bm, bn, bk, by):
+    """The canonical matmul's LLIR with the k loop's bound replaced by the
+    cell's row or column (`k < row` / `k < col`): a trip count that differs
+    between cells."""
+    t = llir_shapes.matmul(bm, bn, bk)
+    old = "%v45 = icmp slt %loop_k26, %v13"
+    assert t.count(old) == 1
+    return t.replace(old, "%v45 = icmp slt %loop_k26, " + ("%loop_row24" if by == "row" else "%loop_col25"))
+
+
+def test_jam_needs_branches_alike_for_a_lanes_cells():
+    """Mutations of the jam's rule: a lane's four cells of a 64 x 64 nest
+    share their column (64 divides 1024) but not their row, so a k loop
+    bounded by the column still runs them jammed, and one bounded by the row
+    (each cell's own trip count) runs them one slot at a time."""
+    by_col = hip.llir_to_hip(triangular_matmul(64, 64, 8, "col"), (2, 64, 64))
+    assert "for (int coop_g = 0; coop_g < 1; ++coop_g) {" in by_col
+    assert "v_v45 = v_loop_k26 < v_loop_col21;" in by_col
+    by_row = hip.llir_to_hip(triangular_matmul(64, 64, 8, "row"), (2, 64, 64))
+    assert "coop_g" not in by_row and "__s0" not in by_row
+    assert "for (int coop_k = 0; coop_k < 4; ++coop_k) {" in by_row
+    assert "v_v45 = v_loop_k26 < v_loop_row19;" in by_row
+
+
 def test_two_dimensional_nests_spread():
     """The canonical matmul's row x column nest (canonical_matmul.rs:24-444)
     and the tile MMA's (tile_compute/mma.rs:25-260) have a region of blocks
