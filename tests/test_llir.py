@@ -384,6 +384,8 @@ def test_two_dimensional_nests_spread():
     assert "v_v50__s3 = v_v47__s3 * v_v49;" in mm              # one b element
     assert "v_v54 = v_loop_b_index29 + v_v9;" in mm and "v_v54__s" not in mm
     assert mm.count("v_v52 = v_loop_k26 + (1LL);") == 2         # the k counter once a copy
+    # a cell's k loop, in both copies, unrolled 16 times (loads in flight)
+    assert mm.count("#pragma unroll 16\n  for (;;) {") == 2 and "#pragma unroll 4\n" not in mm
     assert "goto coop_next0p;" in mm and "L_v_matmul_k_header_4_n0p:;" in mm
     # in order on lane 0 when ldc < BN
     assert ("} else if (threadIdx.x == 0) {\n"
