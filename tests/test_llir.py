@@ -355,6 +355,29 @@ def test_jam_needs_branches_alike_for_a_lanes_cells():
     assert "v_v45 = v_loop_k26 < v_loop_row19;" in by_row
 
 
+@pytest.mark.parametrize("bm,bn", [(16, 64), (32, 32), (64, 64), (128, 64), (64, 128), (32, 96),
+                                   (96, 32), (24, 64), (128, 128), (256, 64), (48, 32), (8, 8)])
+def test_nest_shapes_translate(bm, bn):
+    """Every nest generator of tests/llir_shapes.py translates at tile shapes
+    that take each form (one program a lane, slot form with and without a
+    partial slot, jammed groups of two to four with the column shared or per
+    slot, the strided form), and the canonical and MMA-loop forms compile.
+    (The MMA forms keep one program a lane where their tiles pass the LDS
+    budget: 256 x 64 accumulator and result tiles.)"""
+    for gen in ("matmul", "mma_program", "fused_mma_loop", "mma_k_loop"):
+        for bk in (4, 16):
+            src = hip.llir_to_hip(getattr(llir_shapes, gen)(bm, bn, bk), (2, bm, bn))
+            if gen != "matmul":
+                continue
+            cells = bm * bn
+            assert ("__launch_bounds__(1024)" in src) == (cells >= 256), (bm, bn, bk)
+            jammed = cells % 1024 == 0 and 2 <= cells // 1024 <= 16
+            assert ("coop_g" in src) == jammed, (bm, bn, bk)
+    for gen in ("matmul", "mma_k_loop"):
+        image, _ = hip.llir_compile(getattr(llir_shapes, gen)(bm, bn, 8), (2, bm, bn))
+        assert image[:4] == b"\x7fELF" or image.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+
+
 def test_two_dimensional_nests_spread():
     """The canonical matmul's row x column nest (canonical_matmul.rs:24-444)
     and the tile MMA's (tile_compute/mma.rs:25-260) have a region of blocks
